@@ -1,0 +1,218 @@
+#ifndef QWASAR_GPU_H
+#define QWASAR_GPU_H
+
+/* qwasar_gpu.h -- the GPU op boundary for qwasar's Flash-Next MoE layer, as
+ * implemented for one AMD Instinct MI355X (gfx950) by qwasar_hip.c.
+ *
+ * This is the subset of the reference's own qwasar_gpu.h that the MoE path
+ * crosses (reference qwasar_gpu.h:13-82 runtime, :102-118 and :180-192
+ * quantised/dense products, :316-317 swiglu, :384 add, :559-616 MoE ops).
+ * Every declaration keeps the reference's name, argument order, argument
+ * meaning and error convention, so the reference's callers
+ * (qwasar_flash_graph.c:531-632 encode_moe, tests/test_sparse.c,
+ * tools/bench/gmmbench.c) link against this backend unchanged.  The last
+ * section lists additions that have no counterpart in the reference.
+ *
+ * Conventions (as in the reference):
+ *   - void ops return without encoding anything when `c` is NULL;
+ *   - an unsupported shape prints one line to stderr and encodes nothing;
+ *   - bool ops return false, encoding nothing, when the shape does not apply;
+ *   - device errors are reported by qw_cmd_error after qw_cmd_wait.
+ *
+ * Buffers are host-visible: qw_buf_contents returns host memory that mirrors
+ * the device copy.  Write a buffer through the pointer returned by a fresh
+ * qw_buf_contents call; the next op that touches the buffer uploads it.  After
+ * qw_cmd_wait, every buffer an op wrote and whose contents were ever taken is
+ * copied back, so pointers held across the wait see the results. */
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- device (reference qwasar_gpu.h:16-28) ---------------------------------- */
+
+typedef struct qw_buf_s *qw_buf;
+
+/* Brings up the first HIP device and the backend's stream.  Returns false and
+ * fills `err` when there is no usable gfx950 device. */
+bool qw_gpu_init(char *err, size_t errcap);
+void qw_gpu_shutdown(void);
+const char *qw_gpu_name(void);
+uint64_t qw_gpu_working_set_limit(void);   /* free device memory at init */
+uint64_t qw_gpu_max_buffer_length(void);   /* total device memory */
+
+/* ---- buffers (reference qwasar_gpu.h:30-37) --------------------------------- */
+
+/* Copies `len` bytes at `ptr` to a new device buffer once; `ptr` must stay
+ * valid for the buffer's lifetime and is what qw_buf_contents returns. */
+qw_buf qw_buf_wrap(void *ptr, size_t len);
+/* A device buffer with a pinned host mirror, zero-filled. */
+qw_buf qw_buf_alloc(size_t len);
+void   qw_buf_free(qw_buf b);
+void  *qw_buf_contents(qw_buf b);
+size_t qw_buf_length(qw_buf b);
+
+/* ---- dispatch (reference qwasar_gpu.h:39-69) -------------------------------- */
+
+typedef struct { qw_buf buf; size_t off; } qw_ref;
+
+static inline qw_ref qw_ref_at(qw_buf b, size_t off) { qw_ref r = { b, off }; return r; }
+static inline qw_ref qw_ref_offset(qw_ref r, size_t off) { r.off += off; return r; }
+
+typedef struct qw_cmd_s *qw_cmd;
+
+/* Ops are launched on the backend's one in-order HIP stream as they are
+ * encoded; commit and flush therefore only mark submission points. */
+qw_cmd qw_cmd_begin(void);
+void   qw_cmd_commit(qw_cmd c);
+void   qw_cmd_wait(qw_cmd c);
+void   qw_cmd_flush(qw_cmd c);
+/* Regions whose ops the caller vouches are independent.  Accepted and
+ * ignored: the in-order stream is always a correct schedule. */
+void   qw_cmd_parallel(qw_cmd c, bool on);
+void   qw_cmd_free(qw_cmd c);
+const char *qw_cmd_error(qw_cmd c);
+
+/* ---- residency (reference qwasar_gpu.h:71-75) ------------------------------- */
+
+/* Device buffers never page out on this backend; always NULL. */
+typedef void *qw_residency;
+qw_residency qw_residency_new(qw_buf *bufs, int32_t n);
+void         qw_residency_free(qw_residency r);
+
+/* ---- profiling (reference qwasar_gpu.h:77-82) ------------------------------- */
+
+/* QWASAR_PROFILE=1: qw_cmd_mark records a HIP event on the stream and charges
+ * the device time since the previous mark (or since qw_cmd_begin) to `label`;
+ * totals are gathered at qw_cmd_wait. */
+bool qw_prof_enabled(void);
+void qw_cmd_mark(qw_cmd c, const char *label);
+void qw_prof_report(FILE *out, long tokens);
+void qw_prof_reset(void);
+
+/* ---- quantised and dense products (reference qwasar_gpu.h:84-192) ---------- */
+
+/* y[r][n] = sum_k dequant(w)[n][k] * x[r][k]; w U32 [n, k/8] MLX affine 4-bit,
+ * scales/biases BF16 [n, k/group], x F32 [rows, k], y F32 [rows, n]. */
+void qw_op_qmat_q4(qw_cmd c, qw_ref y, qw_ref x,
+                   qw_ref w, qw_ref scales, qw_ref biases,
+                   int32_t k, int32_t n, int32_t rows, int32_t group);
+
+/* Up to four one-token matvecs sharing x [1, k] and group, in one launch.
+ * False, nothing encoded, for count outside 1..4. */
+typedef struct { qw_ref y, w, scales, biases; int32_t n; } qw_qmv_part;
+bool qw_op_qmv_q4_multi(qw_cmd c, qw_ref x, int32_t k, int32_t group,
+                        int32_t count, const qw_qmv_part *parts);
+
+void qw_op_qmv_q4(qw_cmd c, qw_ref y, qw_ref x,
+                  qw_ref w, qw_ref scales, qw_ref biases,
+                  int32_t k, int32_t n, int32_t rows, int32_t group);
+void qw_op_qmm_q4(qw_cmd c, qw_ref y, qw_ref x,
+                  qw_ref w, qw_ref scales, qw_ref biases,
+                  int32_t k, int32_t n, int32_t rows, int32_t group);
+void qw_op_qmvb_q4(qw_cmd c, qw_ref y, qw_ref x,
+                   qw_ref w, qw_ref scales, qw_ref biases,
+                   int32_t k, int32_t n, int32_t rows, int32_t group);
+
+/* y = x * w^T, w BF16 [n, k], x F32 [rows, k], y F32 [rows, n].  Summed in
+ * order R (64-element fmaf chains added left to right), the order routing's
+ * bit-exactness is defined in. */
+void qw_op_dmat_bf16(qw_cmd c, qw_ref y, qw_ref x, qw_ref w,
+                     int32_t k, int32_t n, int32_t rows);
+
+/* ---- elementwise (reference qwasar_gpu.h:316-317, :384) --------------------- */
+
+void qw_op_swiglu(qw_cmd c, qw_ref y, qw_ref gate, qw_ref up, int32_t n);
+void qw_op_add_inplace(qw_cmd c, qw_ref y, qw_ref x, int32_t n);
+
+/* ---- the MoE block (reference qwasar_gpu.h:559-616) ------------------------- */
+
+/* out[r] = sum_k w[r,k] y[r*K+k] + sigmoid(g[r]) sh[r]. */
+void qw_op_moe_combine_shared(qw_cmd c, qw_ref out, qw_ref y, qw_ref w, qw_ref sh, qw_ref g,
+                              int32_t rows, int32_t K, int32_t H);
+/* Softmax over E in fp32, top-K (ties to the lower index), renormalised when
+ * `norm`.  idx I32 [rows, K], w F32 [rows, K].  Refuses K > 32 or E > 1024. */
+void qw_op_moe_route(qw_cmd c, qw_ref idx, qw_ref w, qw_ref logits,
+                     int32_t rows, int32_t E, int32_t K, bool norm);
+/* y[p] = bank[idx[p]] . x[x_by_pair ? p : p / K] for `pairs` pairs. */
+void qw_op_qmv_q4_bank(qw_cmd c, qw_ref y, qw_ref x, qw_ref idx,
+                       qw_ref w, qw_ref scales, qw_ref biases,
+                       int32_t k, int32_t n, int32_t pairs, int32_t K, bool x_by_pair,
+                       int32_t group);
+/* Two banks of one shape against x (p / K), y [2, pairs, n].  False, nothing
+ * encoded, for k < 2048, as in the reference. */
+bool qw_op_qmv_q4_bank2(qw_cmd c, qw_ref y, qw_ref x, qw_ref idx,
+                        qw_ref w, qw_ref scales, qw_ref biases,
+                        qw_ref w2, qw_ref scales2, qw_ref biases2,
+                        int32_t k, int32_t n, int32_t pairs, int32_t K, int32_t group);
+/* y[p] = W . (silu(gate[p]) * up[p]), rows p at p * stride; W is expert
+ * idx[p] of a bank, or the one matrix when idx.buf is NULL. */
+void qw_op_qmv_q4_swiglu(qw_cmd c, qw_ref y, qw_ref gate, qw_ref up, int32_t stride, qw_ref idx,
+                         qw_ref w, qw_ref scales, qw_ref biases,
+                         int32_t k, int32_t n, int32_t rows, int32_t group);
+/* Prefill's grouped experts.  qw_op_moe_group sorts the pairs by expert --
+ * stably: ascending pair index within an expert, so perm is deterministic --
+ * into tiles [1 + 3 * qw_moe_max_tiles] = (count, (expert, start, len)...);
+ * qw_op_qmm_q4_gather runs one tiled product per tile.  cursor [E] is
+ * accepted for the reference's signature and not used. */
+int32_t qw_moe_max_tiles(int32_t pairs, int32_t E);
+void qw_op_moe_group(qw_cmd c, qw_ref perm, qw_ref tiles, qw_ref cursor, qw_ref idx,
+                     int32_t pairs, int32_t E);
+void qw_op_qmm_q4_gather(qw_cmd c, qw_ref y, qw_ref x, qw_ref perm, qw_ref tiles,
+                         qw_ref w, qw_ref scales, qw_ref biases,
+                         int32_t k, int32_t n, int32_t pairs, int32_t E, int32_t K,
+                         bool x_by_pair, int32_t group);
+/* act[p, i] = silu(gu[p, i]) * gu[p, I+i]. */
+void qw_op_swiglu_split(qw_cmd c, qw_ref act, qw_ref gu, int32_t pairs, int32_t I);
+/* out[r] = sum_k w[r, k] * y[r*K + k]. */
+void qw_op_moe_combine(qw_cmd c, qw_ref out, qw_ref y, qw_ref w, int32_t rows, int32_t K, int32_t H);
+/* y[r, :] *= sigmoid(g[r]). */
+void qw_op_scale_rows_sigmoid(qw_cmd c, qw_ref y, qw_ref g, int32_t rows, int32_t dim);
+
+/* ---- additions without a reference counterpart ------------------------------ */
+
+/* The tile height the grouping and the grouped product agree on for a
+ * given (pairs, E): 16, 32 or 64 rows. */
+int32_t qw_moe_tile_rows(int32_t pairs, int32_t E);
+
+/* One quantised matrix or bank. */
+typedef struct { qw_ref w, scales, biases; int32_t group; } qw_q4_ref;
+
+/* The MoE block's tensors, as the reference's qw_moe (qwasar_model.h:137-153). */
+typedef struct {
+    int32_t H, E, K, I, SI;
+    bool norm;                   /* norm_topk_prob */
+    bool split;                  /* gate/up banks [E, I, H]; else gate_up [E, 2I, H] */
+    qw_ref router;               /* BF16 [E, H] */
+    qw_q4_ref gate_up, gate, up; /* banks */
+    qw_q4_ref down;              /* bank [E, H, I] */
+    qw_q4_ref sh_gate, sh_up;    /* [SI, H] */
+    qw_q4_ref sh_down;           /* [H, SI] */
+    qw_ref sh_gate_w;            /* BF16 [1, H] */
+} qw_moe_layer;
+
+/* The whole MoE block -- router, routing, routed experts, gated shared
+ * expert, combine -- for `rows` tokens, in the fewest launches this backend
+ * has: out F32 [rows, H]; idx I32 [rows, K] and w F32 [rows, K] receive the
+ * routing.  Decode (rows < 8) is a fused path over only the selected
+ * experts; prefill is the grouped path.  Scratch is owned by the backend.
+ * False, nothing encoded, for shapes outside what the kernels take. */
+bool qw_op_moe_layer(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,
+                     const qw_moe_layer *M, int32_t rows);
+
+/* Profiling for harnesses: force profiling on or off (overrides
+ * QWASAR_PROFILE), and read one label's accumulated device milliseconds and
+ * mark count. */
+void   qw_prof_set_enabled(bool on);
+double qw_prof_ms(const char *label, int64_t *count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWASAR_GPU_H */

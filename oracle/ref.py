@@ -1,0 +1,156 @@
+"""ctypes access to the CPU oracle (libmoe_ref.so) and to the reference's own
+scalar twins compiled from /root/reference/qwasar_cpu.c (_ref/libqwasar_cpu.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the product package.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmoe_ref.so")
+REF_PATH = os.path.join(HERE, "_ref", "libqwasar_cpu.so")
+
+_P = C.c_void_p
+_I = C.c_int32
+
+
+def build() -> None:
+    """Compile the oracle (and _ref where the reference tree is present)."""
+    subprocess.run(["make", "-B", "-s", "-C", HERE], check=True)
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+class _Q4(C.Structure):
+    _fields_ = [("w", _P), ("s", _P), ("b", _P), ("group", _I)]
+
+
+class _Moe(C.Structure):
+    _fields_ = [("H", _I), ("E", _I), ("K", _I), ("I", _I), ("SI", _I),
+                ("norm", _I), ("split", _I), ("router", _P),
+                ("gate_up", _Q4), ("gate", _Q4), ("up", _Q4), ("down", _Q4),
+                ("sh_gate", _Q4), ("sh_up", _Q4), ("sh_down", _Q4),
+                ("sh_gate_w", _P)]
+
+
+_lib = None
+_ref = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        L.qr_bf16_to_f32.restype = C.c_float
+        L.qr_bf16_to_f32.argtypes = [C.c_uint16]
+        L.qr_exp.restype = C.c_float
+        L.qr_exp.argtypes = [C.c_float]
+        L.qr_dot_bf16.restype = C.c_float
+        L.qr_dot_bf16.argtypes = [_P, _P, _I]
+        L.qr_dequant_row.argtypes = [_P, _P, _P, _P, _I, _I, _I]
+        L.qr_qmv_q4.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I]
+        L.qr_dmat_bf16.argtypes = [_P, _P, _P, _I, _I, _I]
+        L.qr_route.argtypes = [_P, _P, _P, _I, _I, _I, _I]
+        L.qr_route_literal.argtypes = [_P, _P, _P, _I, _I, _I, _I]
+        L.qr_max_tiles.restype = _I
+        L.qr_max_tiles.argtypes = [_I, _I, _I]
+        L.qr_moe_group.restype = _I
+        L.qr_moe_group.argtypes = [_P, _P, _P, _I, _I, _I, _I]
+        L.qr_silu.restype = C.c_float
+        L.qr_silu.argtypes = [C.c_float]
+        L.qr_moe_forward.argtypes = [_P, _P, _P, _P, _I, C.POINTER(_Moe)]
+        L.qr_rms_norm.argtypes = [_P, _P, _I, _I, C.c_float]
+        _lib = L
+    return _lib
+
+
+def reflib():
+    """The reference's qwasar_cpu.c, or None where it was never built."""
+    global _ref
+    if _ref is None and os.path.exists(REF_PATH):
+        R = C.CDLL(REF_PATH)
+        R.qw_cpu_qmv_q4.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I]
+        R.qw_cpu_dequant_row.argtypes = [_P, _P, _P, _P, _I, _I, _I]
+        R.qw_cpu_dmv_bf16.argtypes = [_P, _P, _P, _I, _I, _I]
+        R.qw_cpu_swiglu.argtypes = [_P, _P, _P, _I]
+        R.qw_bf16_to_f32_c.restype = C.c_float
+        R.qw_bf16_to_f32_c.argtypes = [C.c_uint16]
+        _ref = R
+    return _ref
+
+
+# ---- numpy-level helpers -----------------------------------------------------
+
+def exp_vec(x: np.ndarray) -> np.ndarray:
+    L = lib()
+    return np.array([L.qr_exp(float(v)) for v in np.asarray(x, np.float32).ravel()],
+                    dtype=np.float32).reshape(np.shape(x))
+
+
+def qmv_q4(x, w, s, b, k, n, rows, group):
+    y = np.zeros((rows, n), np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    lib().qr_qmv_q4(_ptr(y), _ptr(x), _ptr(w), _ptr(s), _ptr(b), k, n, rows, group)
+    return y
+
+
+def dmat_bf16(x, w, k, n, rows):
+    y = np.zeros((rows, n), np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    lib().qr_dmat_bf16(_ptr(y), _ptr(x), _ptr(w), k, n, rows)
+    return y
+
+
+def route(logits, rows, E, K, norm=True, literal=False):
+    idx = np.zeros((rows, K), np.int32)
+    w = np.zeros((rows, K), np.float32)
+    lg = np.ascontiguousarray(logits, np.float32)
+    fn = lib().qr_route_literal if literal else lib().qr_route
+    fn(_ptr(idx), _ptr(w), _ptr(lg), rows, E, K, 1 if norm else 0)
+    return idx, w
+
+
+def max_tiles(pairs, E, bm):
+    return lib().qr_max_tiles(pairs, E, bm)
+
+
+def moe_group(idx, E, bm):
+    idx = np.ascontiguousarray(idx, np.int32).ravel()
+    pairs = idx.size
+    mt = max_tiles(pairs, E, bm)
+    perm = np.zeros(max(pairs, 1), np.int32)
+    tiles = np.zeros(1 + 3 * max(mt, 1), np.int32)
+    lib().qr_moe_group(_ptr(perm), _ptr(tiles), _ptr(idx), pairs, E, bm, mt)
+    return perm[:pairs], tiles
+
+
+def _q4(t):
+    if t is None:
+        return _Q4(None, None, None, 0)
+    return _Q4(t.w.ctypes.data, t.s.ctypes.data, t.b.ctypes.data, t.group)
+
+
+def moe_forward(layer, x, rows=None):
+    """The whole MoE block on the CPU.  `layer` is a qwasar_amd.synth.MoeLayer."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows = x.shape[0] if rows is None else rows
+    L = layer
+    m = _Moe(L.H, L.E, L.K, L.I, L.SI, 1 if L.norm else 0, 1 if L.split else 0,
+             L.router.ctypes.data, _q4(L.gate_up), _q4(L.gate), _q4(L.up), _q4(L.down),
+             _q4(L.sh_gate), _q4(L.sh_up), _q4(L.sh_down), L.sh_gate_w.ctypes.data)
+    out = np.zeros((rows, L.H), np.float32)
+    idx = np.zeros((rows, L.K), np.int32)
+    w = np.zeros((rows, L.K), np.float32)
+    lib().qr_moe_forward(_ptr(out), _ptr(idx), _ptr(w), _ptr(x), rows, C.byref(m))
+    return out, idx, w

@@ -1,0 +1,89 @@
+// qw_elem.hip -- the MoE block's elementwise steps: SwiGLU (split halves and
+// interleaved per pair), the weighted combine with and without the gated
+// shared expert, the shared expert's row scale, and an in-place add.
+#include "qw_device.h"
+#include "qw_kernels.h"
+
+#define QW_EW_THREADS 256
+
+static dim3 ew_grid(int64_t n) { return dim3((unsigned)((n + QW_EW_THREADS - 1) / QW_EW_THREADS)); }
+
+__global__ void k_swiglu(float *__restrict__ y, const float *__restrict__ g,
+                         const float *__restrict__ u, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * QW_EW_THREADS + threadIdx.x;
+    if (i < n) y[i] = qw_silu(g[i]) * u[i];
+}
+
+// act[p, i] = silu(gu[p, i]) * gu[p, I + i]
+__global__ void k_swiglu_split(float *__restrict__ act, const float *__restrict__ gu, int pairs, int I)
+{
+    const int64_t t = (int64_t)blockIdx.x * QW_EW_THREADS + threadIdx.x;
+    if (t >= (int64_t)pairs * I) return;
+    const int64_t p = t / I, i = t % I;
+    act[t] = qw_silu(gu[p * 2 * I + i]) * gu[p * 2 * I + I + i];
+}
+
+// out[r, i] = [sh[r, i] * sigmoid(g[r])] + sum_k w[r, k] * y[r*K + k, i], an fma
+// chain in slot order starting from the shared term (or from 0 without one).
+__global__ void k_moe_combine(float *__restrict__ out, const float *__restrict__ y,
+                              const float *__restrict__ w, const float *__restrict__ sh,
+                              const float *__restrict__ g, int rows, int K, int H)
+{
+    const int64_t t = (int64_t)blockIdx.x * QW_EW_THREADS + threadIdx.x;
+    if (t >= (int64_t)rows * H) return;
+    const int64_t r = t / H, i = t % H;
+    float acc = sh ? sh[t] * qw_sigmoid(g[r]) : 0.0f;
+    for (int k = 0; k < K; k++) acc = __builtin_fmaf(w[r * K + k], y[(r * K + k) * H + i], acc);
+    out[t] = acc;
+}
+
+__global__ void k_scale_rows_sigmoid(float *__restrict__ y, const float *__restrict__ g, int rows, int dim)
+{
+    const int64_t t = (int64_t)blockIdx.x * QW_EW_THREADS + threadIdx.x;
+    if (t < (int64_t)rows * dim) y[t] *= qw_sigmoid(g[t / dim]);
+}
+
+__global__ void k_add_inplace(float *__restrict__ y, const float *__restrict__ x, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * QW_EW_THREADS + threadIdx.x;
+    if (i < n) y[i] += x[i];
+}
+
+extern "C" int qwk_swiglu(hipStream_t s, float *y, const float *gate, const float *up, int64_t n)
+{
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_swiglu, ew_grid(n), dim3(QW_EW_THREADS), 0, s, y, gate, up, n);
+    return (int)hipGetLastError();
+}
+
+extern "C" int qwk_swiglu_split(hipStream_t s, float *act, const float *gu, int pairs, int I)
+{
+    if ((int64_t)pairs * I <= 0) return 0;
+    hipLaunchKernelGGL(k_swiglu_split, ew_grid((int64_t)pairs * I), dim3(QW_EW_THREADS), 0, s, act, gu, pairs, I);
+    return (int)hipGetLastError();
+}
+
+extern "C" int qwk_moe_combine(hipStream_t s, float *out, const float *y, const float *w,
+                               const float *sh, const float *g, int rows, int K, int H)
+{
+    if ((int64_t)rows * H <= 0) return 0;
+    hipLaunchKernelGGL(k_moe_combine, ew_grid((int64_t)rows * H), dim3(QW_EW_THREADS), 0, s,
+                       out, y, w, sh, g, rows, K, H);
+    return (int)hipGetLastError();
+}
+
+extern "C" int qwk_scale_rows_sigmoid(hipStream_t s, float *y, const float *g, int rows, int dim)
+{
+    if ((int64_t)rows * dim <= 0) return 0;
+    hipLaunchKernelGGL(k_scale_rows_sigmoid, ew_grid((int64_t)rows * dim), dim3(QW_EW_THREADS), 0, s,
+                       y, g, rows, dim);
+    return (int)hipGetLastError();
+}
+
+extern "C" int qwk_add_inplace(hipStream_t s, float *y, const float *x, int64_t n)
+{
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_add_inplace, ew_grid(n), dim3(QW_EW_THREADS), 0, s, y, x, n);
+    return (int)hipGetLastError();
+}

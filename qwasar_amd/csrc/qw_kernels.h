@@ -1,0 +1,90 @@
+/* qw_kernels.h -- the thin C ABI between the C backend (qwasar_hip.c) and the
+ * gfx950 kernels.  Plain device pointers, sizes and a HIP stream; every
+ * function launches asynchronously on `s` and returns a hipError_t as int
+ * (0 = launched).  Shapes are validated here, before any launch, so a shape
+ * a kernel does not support is refused rather than run. */
+#ifndef QW_KERNELS_H
+#define QW_KERNELS_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QWK_DMAT_MAX_K   16384
+#define QWK_ROUTE_MAX_E  1024
+#define QWK_ROUTE_MAX_K  32
+#define QWK_GROUP_MAX_E  1024
+
+/* One MLX affine 4-bit matrix, or the base of a bank of them. */
+typedef struct { const uint32_t *w; const uint16_t *s; const uint16_t *b; } qwk_q4;
+
+/* Router logits / dense bf16 matvec in order R: y[rows, n] = x[rows, k] . w[n, k]^T. */
+int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint16_t *w,
+                  int k, int n, int rows);
+
+/* Softmax, top-K, renormalise: idx/w [rows, K]. */
+int qwk_route(hipStream_t s, int32_t *idx, float *w, const float *logits,
+              int rows, int E, int K, int norm);
+
+/* Stable sort of pairs by expert; tiles = [count, (expert, start, len)...]. */
+int qwk_moe_group(hipStream_t s, int32_t *perm, int32_t *tiles, const int32_t *idx,
+                  int pairs, int E, int bm, int max_tiles);
+
+/* Quantised matvec over (token, slot) pairs.
+ *   y[z][p, 0:n] = W_z(e_p) . in(p)
+ * with e_p = idx[p] (idx NULL: the single matrix), W_z the z-th of `nmat`
+ * matrices (bank2: gate and up), and in(p) either x row (x_by_pair ? p : p/K)
+ * at stride `xstride`, or, with `up` non-NULL, silu(x[p*xstride + i]) *
+ * up[p*xstride + i].  y[z] = y + z * pairs * n. */
+int qwk_q4mv(hipStream_t s, float *y, const float *x, const float *up, int xstride,
+             const int32_t *idx, const qwk_q4 *mats, int nmat,
+             int k, int n, int pairs, int K, int x_by_pair, int group);
+
+/* Up to 4 one-token matvecs sharing x [1, k]: y_i = W_i . x. */
+int qwk_q4mv_multi(hipStream_t s, const float *x, int k, int group, int count,
+                   const qwk_q4 *mats, float *const *ys, const int *ns);
+
+/* The grouped (prefill) product: per tile of pairs routed to one expert,
+ * y[perm[j], :] = W_e . in(perm[j]), in(p) = x row (x_by_pair ? p : p/K).
+ * Tiles were cut at `bm` rows by qwk_moe_group; `max_tiles` bounds the grid. */
+int qwk_gather_gemm(hipStream_t s, float *y, const float *x, const int32_t *perm,
+                    const int32_t *tiles, qwk_q4 m, int k, int n, int K, int x_by_pair,
+                    int group, int bm, int max_tiles);
+
+/* Dense prefill product y[rows, n] = x[rows, k] . W^T (the shared expert). */
+int qwk_qmm(hipStream_t s, float *y, const float *x, qwk_q4 m, int k, int n, int rows, int group);
+
+/* Elementwise. */
+int qwk_swiglu(hipStream_t s, float *y, const float *gate, const float *up, int64_t n);
+int qwk_swiglu_split(hipStream_t s, float *act, const float *gu, int pairs, int I);
+int qwk_moe_combine(hipStream_t s, float *out, const float *y, const float *w,
+                    const float *sh, const float *g, int rows, int K, int H);
+int qwk_scale_rows_sigmoid(hipStream_t s, float *y, const float *g, int rows, int dim);
+int qwk_add_inplace(hipStream_t s, float *y, const float *x, int64_t n);
+
+/* ---- the fused MoE layer -------------------------------------------------- */
+
+typedef struct {
+    int H, E, K, I, SI, group, norm, split;
+    const uint16_t *router;          /* bf16 [E, H] */
+    qwk_q4 gate, up;                 /* banks [E, I, H] (split) */
+    qwk_q4 gate_up;                  /* bank [E, 2I, H] (fused: gate rows first) */
+    qwk_q4 down;                     /* bank [E, H, I] */
+    qwk_q4 sh_gate, sh_up, sh_down;  /* [SI, H], [SI, H], [H, SI] */
+    const uint16_t *sh_gate_w;       /* bf16 [H] */
+} qwk_moe;
+
+/* Bytes of device scratch the decode path needs for `rows` tokens. */
+size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows);
+/* Decode (rows <= QWK_DECODE_MAX_ROWS): out [rows, H], idx/w [rows, K]. */
+#define QWK_DECODE_MAX_ROWS 8
+int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
+                   const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

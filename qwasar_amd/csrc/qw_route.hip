@@ -1,0 +1,289 @@
+// qw_route.hip -- router logits, softmax/top-k routing and the dispatch
+// permutation, for gfx950.
+//
+// Routing must agree bit for bit with the host's restatement, so the router
+// dot product and the softmax follow specified orders:
+//
+//   order R   dot(w, x) = p_0 + p_1 + ... (left to right), where p_c is the
+//             fmaf chain, from 0, over the 64 consecutive elements of chunk c
+//   softmax   m = max; e_i = qw_exp_spec(l_i - m); lane l of a wave sums
+//             e_l, e_{l+64}, ... serially; the 64 lane sums meet in an xor
+//             butterfly (offsets 32..1); p_i = e_i / sum (correctly rounded)
+//   top-k     K rounds of arg-max, ties to the lower expert index, a pick
+//             struck to -1 (the order a serial scan with '>' picks in)
+//   renorm    wsum = w_0 + w_1 + ... in pick order; w_k / wsum
+#include "qw_device.h"
+#include "qw_kernels.h"
+
+#define QW_DMAT_WAVES 4
+#define QW_DMAT_RB 8                       // token rows per block
+#define QW_DMAT_MAXCH (QWK_DMAT_MAX_K / 64)
+
+// y[r, o] = order-R dot of bf16 row w[o] with fp32 row x[r].  A wave owns one
+// output and up to QW_DMAT_RB token rows; lane l computes the partials of
+// chunks l, l+64, ...; partials meet in LDS and lane r adds row r's chunk
+// partials left to right.
+template <bool VEC>
+__global__ __launch_bounds__(QW_DMAT_WAVES * 64) void k_dmat_bf16(
+    float *__restrict__ y, const float *__restrict__ x, const uint16_t *__restrict__ w,
+    int k, int n, int rows)
+{
+    __shared__ float part[QW_DMAT_WAVES][QW_DMAT_MAXCH][QW_DMAT_RB];
+    const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+    const int o = blockIdx.x * QW_DMAT_WAVES + wave;
+    const int r0 = blockIdx.y * QW_DMAT_RB;
+    const int nr = min(QW_DMAT_RB, rows - r0);
+    const int nch = (k + 63) / 64;
+    if (o < n) {
+        const uint16_t *wr = w + (size_t)o * k;
+        for (int c = lane; c < nch; c += 64) {
+            float p[QW_DMAT_RB];
+#pragma unroll
+            for (int r = 0; r < QW_DMAT_RB; r++) p[r] = 0.0f;
+            const int i0 = c * 64, len = min(64, k - i0);
+            if (VEC && len == 64) {
+                const uint4 *wv = reinterpret_cast<const uint4 *>(wr + i0);
+#pragma unroll 2
+                for (int q = 0; q < 8; q++) {
+                    const uint4 ww = wv[q];
+                    const uint32_t wd[4] = {ww.x, ww.y, ww.z, ww.w};
+                    float wf[8];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        wf[2 * j] = __uint_as_float(wd[j] << 16);
+                        wf[2 * j + 1] = __uint_as_float(wd[j] & 0xFFFF0000u);
+                    }
+#pragma unroll
+                    for (int r = 0; r < QW_DMAT_RB; r++) {
+                        if (r < nr) {
+                            const float4 *xv = reinterpret_cast<const float4 *>(
+                                x + (size_t)(r0 + r) * k + i0 + q * 8);
+                            const float4 a = xv[0], b = xv[1];
+                            float t = p[r];
+                            t = __builtin_fmaf(wf[0], a.x, t);
+                            t = __builtin_fmaf(wf[1], a.y, t);
+                            t = __builtin_fmaf(wf[2], a.z, t);
+                            t = __builtin_fmaf(wf[3], a.w, t);
+                            t = __builtin_fmaf(wf[4], b.x, t);
+                            t = __builtin_fmaf(wf[5], b.y, t);
+                            t = __builtin_fmaf(wf[6], b.z, t);
+                            t = __builtin_fmaf(wf[7], b.w, t);
+                            p[r] = t;
+                        }
+                    }
+                }
+            } else {
+                for (int i = 0; i < len; i++) {
+                    const float wf = qw_bf16(wr[i0 + i]);
+#pragma unroll
+                    for (int r = 0; r < QW_DMAT_RB; r++)
+                        if (r < nr) p[r] = __builtin_fmaf(wf, x[(size_t)(r0 + r) * k + i0 + i], p[r]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < QW_DMAT_RB; r++) part[wave][c][r] = p[r];
+        }
+    }
+    __syncthreads();
+    if (o < n && lane < nr) {
+        float total = part[wave][0][lane];
+        for (int c = 1; c < nch; c++) total = total + part[wave][c][lane];
+        y[(size_t)(r0 + lane) * n + o] = total;
+    }
+}
+
+extern "C" int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint16_t *w,
+                             int k, int n, int rows)
+{
+    if (k < 1 || k > QWK_DMAT_MAX_K || n < 1 || rows < 1) return (int)hipErrorInvalidValue;
+    dim3 grid((n + QW_DMAT_WAVES - 1) / QW_DMAT_WAVES, (rows + QW_DMAT_RB - 1) / QW_DMAT_RB);
+    const bool vec = k % 8 == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)x % 16) == 0;
+    if (vec) hipLaunchKernelGGL(k_dmat_bf16<true>, grid, dim3(QW_DMAT_WAVES * 64), 0, s, y, x, w, k, n, rows);
+    else hipLaunchKernelGGL(k_dmat_bf16<false>, grid, dim3(QW_DMAT_WAVES * 64), 0, s, y, x, w, k, n, rows);
+    return (int)hipGetLastError();
+}
+
+// ---- route -------------------------------------------------------------------
+
+#define QW_ROUTE_PER_LANE (QWK_ROUTE_MAX_E / 64)
+
+// The whole route of one token in one wave; every lane ends holding the same
+// picks, so the K rounds need no LDS and no barriers.
+__device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E, int K, int norm,
+                                              int lane, int *pick_i, float *pick_w)
+{
+    float v[QW_ROUTE_PER_LANE];
+    float m = -__builtin_huge_valf();
+#pragma unroll
+    for (int j = 0; j < QW_ROUTE_PER_LANE; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? l[e] : -__builtin_huge_valf();
+        m = fmaxf(m, v[j]);
+    }
+    m = qw_wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < QW_ROUTE_PER_LANE; j++) {
+        const int e = lane + 64 * j;
+        if (e < E) { v[j] = qw_exp_spec(v[j] - m); s = s + v[j]; }
+    }
+    s = qw_xor_sum<64>(s);
+#pragma unroll
+    for (int j = 0; j < QW_ROUTE_PER_LANE; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? v[j] / s : -2.0f;
+    }
+    float mine_w = 0.0f;
+    int mine_i = 0;
+    for (int n = 0; n < K; n++) {
+        float bv = -2.0f;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < QW_ROUTE_PER_LANE; j++)
+            if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
+        qw_wave_argmax(bv, bi);
+#pragma unroll
+        for (int j = 0; j < QW_ROUTE_PER_LANE; j++)
+            if (lane + 64 * j == bi) v[j] = -1.0f;
+        if (lane == n) { mine_w = bv; mine_i = bi; }
+    }
+    float wsum = 0.0f;
+    for (int n = 0; n < K; n++) wsum = wsum + __shfl(mine_w, n, 64);
+    *pick_i = mine_i;
+    *pick_w = norm ? mine_w / wsum : mine_w;
+}
+
+__global__ __launch_bounds__(64) void k_route(int *__restrict__ idx, float *__restrict__ w,
+                                              const float *__restrict__ logits, int rows,
+                                              int E, int K, int norm)
+{
+    const int r = blockIdx.x, lane = threadIdx.x;
+    int pi;
+    float pw;
+    qw_route_wave(logits + (size_t)r * E, E, K, norm, lane, &pi, &pw);
+    if (lane < K) { idx[(size_t)r * K + lane] = pi; w[(size_t)r * K + lane] = pw; }
+}
+
+extern "C" int qwk_route(hipStream_t s, int32_t *idx, float *w, const float *logits,
+                         int rows, int E, int K, int norm)
+{
+    if (rows < 1 || E < 1 || E > QWK_ROUTE_MAX_E || K < 1 || K > QWK_ROUTE_MAX_K || K > E)
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_route, dim3(rows), dim3(64), 0, s, idx, w, logits, rows, E, K, norm);
+    return (int)hipGetLastError();
+}
+
+// ---- the dispatch permutation ------------------------------------------------
+//
+// Pairs sorted by expert, stably: within an expert, ascending pair index.
+// Eight waves each own a contiguous run of pairs.  Counts per (wave, expert)
+// are order-free (LDS atomics); an exclusive scan over experts and then over
+// waves gives every (wave, expert) its first slot; each wave then walks its
+// run 64 pairs at a time, ranking a lane among the lower lanes that share
+// its expert with ballots over the expert id's bits.
+
+#define QW_GROUP_WAVES 8
+#define QW_GROUP_THREADS (QW_GROUP_WAVES * 64)
+
+// Exclusive scan of v over the block (QW_GROUP_THREADS values); returns the
+// prefix and writes the total to *total.
+__device__ int qw_block_excl_scan(int v, int *tmp, int *total)
+{
+    const int t = threadIdx.x;
+    tmp[t] = v;
+    __syncthreads();
+    for (int off = 1; off < QW_GROUP_THREADS; off <<= 1) {
+        const int add = t >= off ? tmp[t - off] : 0;
+        __syncthreads();
+        tmp[t] += add;
+        __syncthreads();
+    }
+    const int incl = tmp[t];
+    *total = tmp[QW_GROUP_THREADS - 1];
+    __syncthreads();
+    return incl - v;
+}
+
+__global__ __launch_bounds__(QW_GROUP_THREADS) void k_moe_group(
+    int *__restrict__ perm, int *__restrict__ tiles, const int *__restrict__ idx,
+    int pairs, int E, int bm, int max_tiles)
+{
+    __shared__ int cnt[QW_GROUP_WAVES][QWK_GROUP_MAX_E];
+    __shared__ int tmp[QW_GROUP_THREADS];
+    const int t = threadIdx.x, wave = t / 64, lane = t % 64;
+    const int per = (pairs + QW_GROUP_WAVES - 1) / QW_GROUP_WAVES;
+    const int p0 = min(pairs, wave * per), p1 = min(pairs, p0 + per);
+
+    for (int i = t; i < QW_GROUP_WAVES * QWK_GROUP_MAX_E; i += QW_GROUP_THREADS)
+        (&cnt[0][0])[i] = 0;
+    __syncthreads();
+    for (int p = p0 + lane; p < p1; p += 64) atomicAdd(&cnt[wave][idx[p]], 1);
+    __syncthreads();
+
+    // Each thread owns experts [e0, e0 + per_t): their totals, scanned.
+    const int per_t = (E + QW_GROUP_THREADS - 1) / QW_GROUP_THREADS;
+    const int e0 = min(E, t * per_t), e1 = min(E, e0 + per_t);
+    int mytot = 0, mytiles = 0;
+    for (int e = e0; e < e1; e++) {
+        int c = 0;
+        for (int wv = 0; wv < QW_GROUP_WAVES; wv++) c += cnt[wv][e];
+        mytot += c;
+        mytiles += (c + bm - 1) / bm;
+    }
+    int total_pairs, total_tiles;
+    int base = qw_block_excl_scan(mytot, tmp, &total_pairs);
+    int tbase = qw_block_excl_scan(mytiles, tmp, &total_tiles);
+    for (int e = e0; e < e1; e++) {
+        int run = base, c = 0;
+        for (int wv = 0; wv < QW_GROUP_WAVES; wv++) {
+            const int x = cnt[wv][e];
+            cnt[wv][e] = run;
+            run += x;
+            c += x;
+        }
+        for (int s = 0; s < c; s += bm, tbase++) {
+            if (tbase < max_tiles) {
+                tiles[1 + 3 * tbase + 0] = e;
+                tiles[1 + 3 * tbase + 1] = base + s;
+                tiles[1 + 3 * tbase + 2] = min(bm, c - s);
+            }
+        }
+        base += c;
+    }
+    if (t == 0) tiles[0] = min(total_tiles, max_tiles);
+    __syncthreads();
+
+    int nbits = 1;
+    while ((1 << nbits) < E) nbits++;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    for (int pb = p0; pb < p1; pb += 64) {
+        const int p = pb + lane;
+        const bool valid = p < p1;
+        const int e = valid ? idx[p] : 0;
+        unsigned long long same = __ballot(valid);
+        for (int b = 0; b < nbits; b++) {
+            const bool bit = (e >> b) & 1;
+            const unsigned long long bb = __ballot(valid && bit);
+            same &= bit ? bb : ~bb;
+        }
+        if (valid) {
+            const int rank = __popcll(same & below);
+            perm[cnt[wave][e] + rank] = p;
+        }
+        __builtin_amdgcn_wave_barrier();
+        // The highest lane of each run of equal experts advances the cursor.
+        if (valid && (same >> lane) == 1ull) cnt[wave][e] += __popcll(same);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+extern "C" int qwk_moe_group(hipStream_t s, int32_t *perm, int32_t *tiles, const int32_t *idx,
+                             int pairs, int E, int bm, int max_tiles)
+{
+    if (pairs < 0 || E < 1 || E > QWK_GROUP_MAX_E || bm < 1 || max_tiles < 0)
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(QW_GROUP_THREADS), 0, s, perm, tiles, idx,
+                       pairs, E, bm, max_tiles);
+    return (int)hipGetLastError();
+}

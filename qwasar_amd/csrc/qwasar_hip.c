@@ -1,0 +1,648 @@
+/* qwasar_hip.c -- the HIP backend behind qwasar_gpu.h for one MI355X.
+ *
+ * The reference's backend is qwasar_metal.m: Metal buffers in unified
+ * memory, command buffers that run at commit, and a pipeline per kernel.  On
+ * an MI355X the weights must sit in HBM and the host cannot cheaply read
+ * device memory, so this backend differs in mechanism while keeping the
+ * reference's contract:
+ *
+ *   qw_buf   a device allocation plus a host mirror (pinned, or the caller's
+ *            memory for qw_buf_wrap).  Two flags say which side is stale.
+ *            qw_buf_contents hands out the mirror and marks the device copy
+ *            stale; an op that touches a stale buffer uploads it first.  An
+ *            op that writes a buffer marks the mirror stale; qw_cmd_wait
+ *            copies written buffers back if their mirror was ever handed out.
+ *   qw_cmd   the backend's single in-order HIP stream plus this command's
+ *            first error, its written buffers and its profiling events.  Ops
+ *            launch as they are encoded (reference qwasar_metal.m:1606-1611
+ *            encodes and runs at commit; both give encode-order execution).
+ *   ops      each qw_op_* validates its shape, launches through the C ABI in
+ *            qw_kernels.h, and records a launch failure as the command's
+ *            error, reported by qw_cmd_error after qw_cmd_wait.
+ *
+ * Host code only: built with gcc against the HIP runtime's C API. */
+
+#include "qwasar_gpu.h"
+#include "qw_kernels.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <stdarg.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* The MoE layer runs its experts grouped above QWK_DECODE_MAX_ROWS rows and
+ * through the fused decode path at or below it (the reference switches at
+ * 8 rows, qwasar_flash_graph.c:28; here a verify batch of 8 stays on the
+ * decode path, which dedups expert reads across its tokens). */
+/* Rows at or above which qw_op_qmat_q4 takes the MFMA product. */
+#define QW_QMM_MIN_ROWS 8
+
+struct qw_buf_s {
+    void *host;
+    void *dev;
+    size_t len;
+    int owns_host;   /* host mirror allocated here (pinned) */
+    int host_stale;  /* device holds newer data */
+    int dev_stale;   /* host mirror may hold newer data */
+    int exposed;     /* qw_buf_contents was called (or the memory is the caller's) */
+};
+
+typedef struct { const char *label; hipEvent_t a, b; } qw_mark;
+
+struct qw_cmd_s {
+    hipError_t err;
+    char msg[256];
+    qw_buf *written;
+    int nwritten, capwritten;
+    qw_mark *marks;
+    int nmarks, capmarks;
+    hipEvent_t last;
+    struct qw_cmd_s *next;   /* live commands, for qw_buf_free */
+};
+
+static struct {
+    int ready;
+    int device;
+    hipStream_t stream;
+    char name[320];
+    uint64_t free0, total;
+    int prof;
+    qw_cmd live;
+    void *scratch;
+    size_t scratch_len;
+} G;
+
+/* ---- profiling table ---------------------------------------------------- */
+
+#define QW_PROF_MAX 64
+static struct { const char *label; double ms; int64_t count; } P[QW_PROF_MAX];
+static int NP;
+
+static void prof_add(const char *label, double ms) {
+    for (int i = 0; i < NP; i++)
+        if (P[i].label == label || !strcmp(P[i].label, label)) { P[i].ms += ms; P[i].count++; return; }
+    if (NP < QW_PROF_MAX) { P[NP].label = label; P[NP].ms = ms; P[NP].count = 1; NP++; }
+}
+
+bool qw_prof_enabled(void) { return G.prof != 0; }
+void qw_prof_set_enabled(bool on) { G.prof = on ? 1 : 0; }
+void qw_prof_reset(void) { NP = 0; }
+
+double qw_prof_ms(const char *label, int64_t *count) {
+    for (int i = 0; i < NP; i++)
+        if (!strcmp(P[i].label, label)) { if (count) *count = P[i].count; return P[i].ms; }
+    if (count) *count = 0;
+    return 0.0;
+}
+
+void qw_prof_report(FILE *out, long tokens) {
+    double total = 0.0;
+    for (int i = 0; i < NP; i++) total += P[i].ms;
+    if (!out || total <= 0.0) return;
+    fprintf(out, "qwasar profile (%s, %ld tokens):\n", G.name, tokens);
+    for (int i = 0; i < NP; i++)
+        fprintf(out, "  %-28s %9.4f ms/token %5.1f%%  (%lld marks)\n", P[i].label,
+                tokens > 0 ? P[i].ms / (double)tokens : P[i].ms, 100.0 * P[i].ms / total,
+                (long long)P[i].count);
+}
+
+/* ---- device --------------------------------------------------------------- */
+
+bool qw_gpu_init(char *err, size_t errcap) {
+    if (G.ready) return true;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
+        if (err && errcap) snprintf(err, errcap, "no HIP device");
+        return false;
+    }
+    hipDeviceProp_t prop;
+    if (hipSetDevice(0) != hipSuccess || hipGetDeviceProperties(&prop, 0) != hipSuccess) {
+        if (err && errcap) snprintf(err, errcap, "cannot open HIP device 0");
+        return false;
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        if (err && errcap) snprintf(err, errcap, "device is %s; kernels are built for gfx950", prop.gcnArchName);
+        return false;
+    }
+    if (hipStreamCreateWithFlags(&G.stream, hipStreamNonBlocking) != hipSuccess) {
+        if (err && errcap) snprintf(err, errcap, "cannot create a HIP stream");
+        return false;
+    }
+    size_t fr = 0, tot = 0;
+    (void)hipMemGetInfo(&fr, &tot);
+    G.free0 = fr;
+    G.total = tot;
+    snprintf(G.name, sizeof G.name, "%s (%s)", prop.name, prop.gcnArchName);
+    const char *pe = getenv("QWASAR_PROFILE");
+    G.prof = pe && *pe && strcmp(pe, "0") != 0;
+    G.device = 0;
+    G.ready = 1;
+    return true;
+}
+
+static int ensure_init(void) {
+    if (G.ready) return 1;
+    char e[128];
+    if (!qw_gpu_init(e, sizeof e)) { fprintf(stderr, "qwasar: %s\n", e); return 0; }
+    return 1;
+}
+
+void qw_gpu_shutdown(void) {
+    if (!G.ready) return;
+    hipStreamSynchronize(G.stream);
+    if (G.scratch) hipFree(G.scratch);
+    G.scratch = NULL;
+    G.scratch_len = 0;
+    hipStreamDestroy(G.stream);
+    G.ready = 0;
+}
+
+const char *qw_gpu_name(void) { return G.ready ? G.name : "none"; }
+uint64_t qw_gpu_working_set_limit(void) { return G.free0; }
+uint64_t qw_gpu_max_buffer_length(void) { return G.total; }
+
+/* ---- buffers --------------------------------------------------------------- */
+
+qw_buf qw_buf_alloc(size_t len) {
+    if (!ensure_init()) return NULL;
+    qw_buf b = calloc(1, sizeof *b);
+    if (!b) return NULL;
+    const size_t n = len ? len : 1;
+    if (hipMalloc(&b->dev, n) != hipSuccess) { free(b); return NULL; }
+    if (hipHostMalloc(&b->host, n, hipHostMallocDefault) != hipSuccess) {
+        hipFree(b->dev);
+        free(b);
+        return NULL;
+    }
+    memset(b->host, 0, n);
+    hipMemsetAsync(b->dev, 0, n, G.stream);
+    hipStreamSynchronize(G.stream);
+    b->len = len;
+    b->owns_host = 1;
+    return b;
+}
+
+qw_buf qw_buf_wrap(void *ptr, size_t len) {
+    if (!ensure_init() || !ptr) return NULL;
+    qw_buf b = calloc(1, sizeof *b);
+    if (!b) return NULL;
+    if (hipMalloc(&b->dev, len ? len : 1) != hipSuccess) { free(b); return NULL; }
+    if (len && hipMemcpy(b->dev, ptr, len, hipMemcpyHostToDevice) != hipSuccess) {
+        hipFree(b->dev);
+        free(b);
+        return NULL;
+    }
+    b->host = ptr;
+    b->len = len;
+    b->exposed = 1;
+    return b;
+}
+
+void qw_buf_free(qw_buf b) {
+    if (!b) return;
+    for (qw_cmd c = G.live; c; c = c->next)
+        for (int i = 0; i < c->nwritten; i++)
+            if (c->written[i] == b) c->written[i] = c->written[--c->nwritten];
+    hipStreamSynchronize(G.stream);
+    hipFree(b->dev);
+    if (b->owns_host) hipHostFree(b->host);
+    free(b);
+}
+
+void *qw_buf_contents(qw_buf b) {
+    if (!b) return NULL;
+    if (b->host_stale) {
+        hipStreamSynchronize(G.stream);
+        hipMemcpy(b->host, b->dev, b->len, hipMemcpyDeviceToHost);
+        b->host_stale = 0;
+    }
+    b->dev_stale = 1;
+    b->exposed = 1;
+    return b->host;
+}
+
+size_t qw_buf_length(qw_buf b) { return b ? b->len : 0; }
+
+/* ---- commands ---------------------------------------------------------------- */
+
+qw_cmd qw_cmd_begin(void) {
+    if (!ensure_init()) return NULL;
+    qw_cmd c = calloc(1, sizeof *c);
+    if (!c) return NULL;
+    if (G.prof) {
+        hipEventCreate(&c->last);
+        hipEventRecord(c->last, G.stream);
+    }
+    c->next = G.live;
+    G.live = c;
+    return c;
+}
+
+static void cmd_fail(qw_cmd c, hipError_t e, const char *fmt, ...) {
+    if (!c || c->err != hipSuccess) return;
+    c->err = e == hipSuccess ? hipErrorUnknown : e;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(c->msg, sizeof c->msg, fmt, ap);
+    va_end(ap);
+}
+
+/* Makes the device copy of r's buffer current; notes it as written. */
+static void touch(qw_cmd c, qw_ref r, int writes) {
+    qw_buf b = r.buf;
+    if (!b) return;
+    if (b->dev_stale) {
+        hipMemcpyAsync(b->dev, b->host, b->len, hipMemcpyHostToDevice, G.stream);
+        hipStreamSynchronize(G.stream);
+        b->dev_stale = 0;
+    }
+    if (!writes) return;
+    b->host_stale = 1;
+    for (int i = 0; i < c->nwritten; i++) if (c->written[i] == b) return;
+    if (c->nwritten == c->capwritten) {
+        c->capwritten = c->capwritten ? 2 * c->capwritten : 16;
+        c->written = realloc(c->written, (size_t)c->capwritten * sizeof *c->written);
+    }
+    c->written[c->nwritten++] = b;
+}
+
+static void *dp(qw_ref r) { return r.buf ? (char *)r.buf->dev + r.off : NULL; }
+
+/* Launch result of one op: a refusal (invalid shape) is printed, as the
+ * reference prints unsupported shapes; either kind becomes the error. */
+static void launched(qw_cmd c, const char *op, int rc) {
+    if (rc == 0) return;
+    if (rc == (int)hipErrorInvalidValue) fprintf(stderr, "qwasar: %s: shape or alignment unsupported\n", op);
+    cmd_fail(c, (hipError_t)rc, "%s: %s", op, hipGetErrorString((hipError_t)rc));
+}
+
+void qw_cmd_commit(qw_cmd c) { (void)c; }
+void qw_cmd_flush(qw_cmd c) { (void)c; }
+void qw_cmd_parallel(qw_cmd c, bool on) { (void)c; (void)on; }
+
+void qw_cmd_mark(qw_cmd c, const char *label) {
+    if (!c || !G.prof) return;
+    hipEvent_t e;
+    hipEventCreate(&e);
+    hipEventRecord(e, G.stream);
+    if (c->nmarks == c->capmarks) {
+        c->capmarks = c->capmarks ? 2 * c->capmarks : 16;
+        c->marks = realloc(c->marks, (size_t)c->capmarks * sizeof *c->marks);
+    }
+    c->marks[c->nmarks].label = label;
+    c->marks[c->nmarks].a = c->last;
+    c->marks[c->nmarks].b = e;
+    c->nmarks++;
+    c->last = e;
+}
+
+void qw_cmd_wait(qw_cmd c) {
+    if (!c) return;
+    hipError_t e = hipStreamSynchronize(G.stream);
+    if (e != hipSuccess) cmd_fail(c, e, "device: %s", hipGetErrorString(e));
+    for (int i = 0; i < c->nwritten; i++) {
+        qw_buf b = c->written[i];
+        if (b->exposed && b->host_stale) {
+            hipMemcpy(b->host, b->dev, b->len, hipMemcpyDeviceToHost);
+            b->host_stale = 0;
+        }
+    }
+    c->nwritten = 0;
+    for (int i = 0; i < c->nmarks; i++) {
+        float ms = 0.0f;
+        if (c->marks[i].a && hipEventElapsedTime(&ms, c->marks[i].a, c->marks[i].b) == hipSuccess)
+            prof_add(c->marks[i].label, ms);
+        if (c->marks[i].a && (i == 0 || c->marks[i].a != c->marks[i - 1].b)) hipEventDestroy(c->marks[i].a);
+    }
+    if (c->nmarks) {
+        c->last = c->marks[c->nmarks - 1].b;
+        for (int i = 0; i + 1 < c->nmarks; i++) hipEventDestroy(c->marks[i].b);
+    }
+    c->nmarks = 0;
+}
+
+const char *qw_cmd_error(qw_cmd c) { return c && c->err != hipSuccess ? c->msg : NULL; }
+
+void qw_cmd_free(qw_cmd c) {
+    if (!c) return;
+    for (qw_cmd *pp = &G.live; *pp; pp = &(*pp)->next)
+        if (*pp == c) { *pp = c->next; break; }
+    for (int i = 0; i < c->nmarks; i++) {
+        if (c->marks[i].a && (i == 0 || c->marks[i].a != c->marks[i - 1].b)) hipEventDestroy(c->marks[i].a);
+        hipEventDestroy(c->marks[i].b);
+    }
+    if (!c->nmarks && c->last) hipEventDestroy(c->last);
+    free(c->marks);
+    free(c->written);
+    free(c);
+}
+
+qw_residency qw_residency_new(qw_buf *bufs, int32_t n) { (void)bufs; (void)n; return NULL; }
+void qw_residency_free(qw_residency r) { (void)r; }
+
+/* ---- ops ------------------------------------------------------------------- */
+
+#define QW_OP(c) if (!(c)) return
+
+static qwk_q4 q4(qw_ref w, qw_ref s, qw_ref b) {
+    qwk_q4 m = { (const uint32_t *)dp(w), (const uint16_t *)dp(s), (const uint16_t *)dp(b) };
+    return m;
+}
+
+void qw_op_qmv_q4(qw_cmd c, qw_ref y, qw_ref x, qw_ref w, qw_ref scales, qw_ref biases,
+                  int32_t k, int32_t n, int32_t rows, int32_t group) {
+    QW_OP(c);
+    touch(c, x, 0); touch(c, w, 0); touch(c, scales, 0); touch(c, biases, 0); touch(c, y, 1);
+    const qwk_q4 m = q4(w, scales, biases);
+    launched(c, "qmv_q4", qwk_q4mv(G.stream, dp(y), dp(x), NULL, k, NULL, &m, 1, k, n, rows, 1, 1, group));
+}
+
+void qw_op_qmvb_q4(qw_cmd c, qw_ref y, qw_ref x, qw_ref w, qw_ref scales, qw_ref biases,
+                   int32_t k, int32_t n, int32_t rows, int32_t group) {
+    qw_op_qmv_q4(c, y, x, w, scales, biases, k, n, rows, group);
+}
+
+void qw_op_qmm_q4(qw_cmd c, qw_ref y, qw_ref x, qw_ref w, qw_ref scales, qw_ref biases,
+                  int32_t k, int32_t n, int32_t rows, int32_t group) {
+    QW_OP(c);
+    touch(c, x, 0); touch(c, w, 0); touch(c, scales, 0); touch(c, biases, 0); touch(c, y, 1);
+    launched(c, "qmm_q4", qwk_qmm(G.stream, dp(y), dp(x), q4(w, scales, biases), k, n, rows, group));
+}
+
+void qw_op_qmat_q4(qw_cmd c, qw_ref y, qw_ref x, qw_ref w, qw_ref scales, qw_ref biases,
+                   int32_t k, int32_t n, int32_t rows, int32_t group) {
+    if (rows >= QW_QMM_MIN_ROWS && k % 32 == 0)
+        qw_op_qmm_q4(c, y, x, w, scales, biases, k, n, rows, group);
+    else
+        qw_op_qmv_q4(c, y, x, w, scales, biases, k, n, rows, group);
+}
+
+bool qw_op_qmv_q4_multi(qw_cmd c, qw_ref x, int32_t k, int32_t group, int32_t count,
+                        const qw_qmv_part *parts) {
+    if (count < 1 || count > 4) return false;
+    if (!c) return true;
+    qwk_q4 m[4];
+    float *ys[4];
+    int ns[4];
+    touch(c, x, 0);
+    for (int32_t i = 0; i < count; i++) {
+        touch(c, parts[i].w, 0); touch(c, parts[i].scales, 0); touch(c, parts[i].biases, 0);
+        touch(c, parts[i].y, 1);
+        m[i] = q4(parts[i].w, parts[i].scales, parts[i].biases);
+        ys[i] = dp(parts[i].y);
+        ns[i] = parts[i].n;
+    }
+    launched(c, "qmv_q4_multi", qwk_q4mv_multi(G.stream, dp(x), k, group, count, m, ys, ns));
+    return true;
+}
+
+void qw_op_dmat_bf16(qw_cmd c, qw_ref y, qw_ref x, qw_ref w, int32_t k, int32_t n, int32_t rows) {
+    QW_OP(c);
+    touch(c, x, 0); touch(c, w, 0); touch(c, y, 1);
+    launched(c, "dmat_bf16", qwk_dmat_bf16(G.stream, dp(y), dp(x), dp(w), k, n, rows));
+}
+
+void qw_op_swiglu(qw_cmd c, qw_ref y, qw_ref gate, qw_ref up, int32_t n) {
+    QW_OP(c);
+    touch(c, gate, 0); touch(c, up, 0); touch(c, y, 1);
+    launched(c, "swiglu", qwk_swiglu(G.stream, dp(y), dp(gate), dp(up), n));
+}
+
+void qw_op_add_inplace(qw_cmd c, qw_ref y, qw_ref x, int32_t n) {
+    QW_OP(c);
+    touch(c, x, 0); touch(c, y, 1);
+    launched(c, "add_inplace", qwk_add_inplace(G.stream, dp(y), dp(x), n));
+}
+
+void qw_op_moe_combine_shared(qw_cmd c, qw_ref out, qw_ref y, qw_ref w, qw_ref sh, qw_ref g,
+                              int32_t rows, int32_t K, int32_t H) {
+    QW_OP(c);
+    touch(c, y, 0); touch(c, w, 0); touch(c, sh, 0); touch(c, g, 0); touch(c, out, 1);
+    launched(c, "moe_combine_shared", qwk_moe_combine(G.stream, dp(out), dp(y), dp(w), dp(sh), dp(g), rows, K, H));
+}
+
+void qw_op_moe_combine(qw_cmd c, qw_ref out, qw_ref y, qw_ref w, int32_t rows, int32_t K, int32_t H) {
+    QW_OP(c);
+    touch(c, y, 0); touch(c, w, 0); touch(c, out, 1);
+    launched(c, "moe_combine", qwk_moe_combine(G.stream, dp(out), dp(y), dp(w), NULL, NULL, rows, K, H));
+}
+
+void qw_op_scale_rows_sigmoid(qw_cmd c, qw_ref y, qw_ref g, int32_t rows, int32_t dim) {
+    QW_OP(c);
+    touch(c, g, 0); touch(c, y, 1);
+    launched(c, "scale_rows_sigmoid", qwk_scale_rows_sigmoid(G.stream, dp(y), dp(g), rows, dim));
+}
+
+void qw_op_swiglu_split(qw_cmd c, qw_ref act, qw_ref gu, int32_t pairs, int32_t I) {
+    QW_OP(c);
+    touch(c, gu, 0); touch(c, act, 1);
+    launched(c, "swiglu_split", qwk_swiglu_split(G.stream, dp(act), dp(gu), pairs, I));
+}
+
+void qw_op_moe_route(qw_cmd c, qw_ref idx, qw_ref w, qw_ref logits, int32_t rows, int32_t E,
+                     int32_t K, bool norm) {
+    if (K > QWK_ROUTE_MAX_K || E > QWK_ROUTE_MAX_E) {
+        fprintf(stderr, "qwasar: moe top-%d of %d unsupported (max top-%d of %d)\n", K, E,
+                QWK_ROUTE_MAX_K, QWK_ROUTE_MAX_E);
+        return;
+    }
+    QW_OP(c);
+    touch(c, logits, 0); touch(c, idx, 1); touch(c, w, 1);
+    launched(c, "moe_route", qwk_route(G.stream, dp(idx), dp(w), dp(logits), rows, E, K, norm ? 1 : 0));
+}
+
+void qw_op_qmv_q4_bank(qw_cmd c, qw_ref y, qw_ref x, qw_ref idx, qw_ref w, qw_ref scales,
+                       qw_ref biases, int32_t k, int32_t n, int32_t pairs, int32_t K,
+                       bool x_by_pair, int32_t group) {
+    QW_OP(c);
+    touch(c, x, 0); touch(c, idx, 0); touch(c, w, 0); touch(c, scales, 0); touch(c, biases, 0);
+    touch(c, y, 1);
+    const qwk_q4 m = q4(w, scales, biases);
+    launched(c, "qmv_q4_bank", qwk_q4mv(G.stream, dp(y), dp(x), NULL, k, dp(idx), &m, 1, k, n, pairs, K,
+                                        x_by_pair ? 1 : 0, group));
+}
+
+bool qw_op_qmv_q4_bank2(qw_cmd c, qw_ref y, qw_ref x, qw_ref idx, qw_ref w, qw_ref scales,
+                        qw_ref biases, qw_ref w2, qw_ref scales2, qw_ref biases2, int32_t k,
+                        int32_t n, int32_t pairs, int32_t K, int32_t group) {
+    /* The reference declines inputs too short to split (k < 2048,
+     * qwasar_metal.m:516,1700) and its caller falls back to two banks. */
+    if (k < 2048) return false;
+    if (!c) return true;
+    touch(c, x, 0); touch(c, idx, 0);
+    touch(c, w, 0); touch(c, scales, 0); touch(c, biases, 0);
+    touch(c, w2, 0); touch(c, scales2, 0); touch(c, biases2, 0);
+    touch(c, y, 1);
+    const qwk_q4 m[2] = { q4(w, scales, biases), q4(w2, scales2, biases2) };
+    launched(c, "qmv_q4_bank2", qwk_q4mv(G.stream, dp(y), dp(x), NULL, k, dp(idx), m, 2, k, n, pairs, K, 0, group));
+    return true;
+}
+
+void qw_op_qmv_q4_swiglu(qw_cmd c, qw_ref y, qw_ref gate, qw_ref up, int32_t stride, qw_ref idx,
+                         qw_ref w, qw_ref scales, qw_ref biases, int32_t k, int32_t n, int32_t rows,
+                         int32_t group) {
+    QW_OP(c);
+    touch(c, gate, 0); touch(c, up, 0); touch(c, idx, 0);
+    touch(c, w, 0); touch(c, scales, 0); touch(c, biases, 0); touch(c, y, 1);
+    const qwk_q4 m = q4(w, scales, biases);
+    launched(c, "qmv_q4_swiglu", qwk_q4mv(G.stream, dp(y), dp(gate), dp(up), stride, dp(idx), &m, 1, k, n,
+                                          rows, 1, 1, group));
+}
+
+static int32_t tiles_for(int32_t pairs, int32_t E, int32_t bm) {
+    return (pairs < E ? pairs : E) + (pairs + bm - 1) / bm;
+}
+
+int32_t qw_moe_max_tiles(int32_t pairs, int32_t E) { return tiles_for(pairs, E, 16); }
+
+int32_t qw_moe_tile_rows(int32_t pairs, int32_t E) {
+    /* Expected pairs per expert decide the tile height: a tile pads its
+     * pairs up to the height with idle MFMA rows, and a taller tile reads
+     * each expert's weights fewer times. */
+    const int64_t avg4 = E > 0 ? (int64_t)4 * pairs / E : 0;   /* 4 x average */
+    if (avg4 >= 4 * 24) return 64;
+    if (avg4 >= 4 * 12) return 32;
+    return 16;
+}
+
+void qw_op_moe_group(qw_cmd c, qw_ref perm, qw_ref tiles, qw_ref cursor, qw_ref idx,
+                     int32_t pairs, int32_t E) {
+    (void)cursor;
+    QW_OP(c);
+    if (E > QWK_GROUP_MAX_E) {
+        fprintf(stderr, "qwasar: moe grouping of %d experts unsupported (max %d)\n", E, QWK_GROUP_MAX_E);
+        return;
+    }
+    touch(c, idx, 0); touch(c, perm, 1); touch(c, tiles, 1);
+    const int32_t bm = qw_moe_tile_rows(pairs, E);
+    launched(c, "moe_group", qwk_moe_group(G.stream, dp(perm), dp(tiles), dp(idx), pairs, E, bm,
+                                           tiles_for(pairs, E, bm)));
+}
+
+void qw_op_qmm_q4_gather(qw_cmd c, qw_ref y, qw_ref x, qw_ref perm, qw_ref tiles, qw_ref w,
+                         qw_ref scales, qw_ref biases, int32_t k, int32_t n, int32_t pairs,
+                         int32_t E, int32_t K, bool x_by_pair, int32_t group) {
+    QW_OP(c);
+    if (k % 32 != 0) {
+        fprintf(stderr, "qwasar: grouped qmm needs k divisible by 32, got %d\n", k);
+        return;
+    }
+    touch(c, x, 0); touch(c, perm, 0); touch(c, tiles, 0);
+    touch(c, w, 0); touch(c, scales, 0); touch(c, biases, 0); touch(c, y, 1);
+    const int32_t bm = qw_moe_tile_rows(pairs, E);
+    launched(c, "qmm_q4_gather", qwk_gather_gemm(G.stream, dp(y), dp(x), dp(perm), dp(tiles),
+                                                 q4(w, scales, biases), k, n, K, x_by_pair ? 1 : 0,
+                                                 group, bm, tiles_for(pairs, E, bm)));
+}
+
+/* ---- the whole MoE layer ------------------------------------------------------ */
+
+static void *scratch(size_t bytes) {
+    if (bytes <= G.scratch_len) return G.scratch;
+    hipStreamSynchronize(G.stream);
+    if (G.scratch) hipFree(G.scratch);
+    G.scratch = NULL;
+    G.scratch_len = 0;
+    if (hipMalloc(&G.scratch, bytes) != hipSuccess) return NULL;
+    /* The decode kernels' arrival counters start at zero and are reset by
+     * the workgroup that completes them. */
+    hipMemset(G.scratch, 0, bytes);
+    G.scratch_len = bytes;
+    return G.scratch;
+}
+
+static qwk_q4 q4r(const qw_q4_ref *r) { return q4(r->w, r->scales, r->biases); }
+
+static void touch_q4(qw_cmd c, const qw_q4_ref *r) {
+    touch(c, r->w, 0); touch(c, r->scales, 0); touch(c, r->biases, 0);
+}
+
+static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+/* Prefill: the grouped path, op by op on the one stream. */
+static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const float *x,
+                        const qw_moe_layer *M, int32_t rows) {
+    const int32_t H = M->H, E = M->E, K = M->K, I = M->I, SI = M->SI, pairs = rows * K;
+    const int32_t bm = qw_moe_tile_rows(pairs, E), mt = tiles_for(pairs, E, bm);
+    const int32_t grp = M->split ? M->gate.group : M->gate_up.group;
+    size_t off = 0;
+    const size_t o_logits = off; off += al256((size_t)rows * E * 4);
+    const size_t o_perm = off;   off += al256((size_t)pairs * 4);
+    const size_t o_tiles = off;  off += al256((size_t)(1 + 3 * mt) * 4);
+    const size_t o_gu = off;     off += al256((size_t)pairs * 2 * I * 4);
+    const size_t o_act = off;    off += al256((size_t)pairs * I * 4);
+    const size_t o_ey = off;     off += al256((size_t)pairs * H * 4);
+    const size_t o_sg = off;     off += al256((size_t)rows * SI * 4);
+    const size_t o_su = off;     off += al256((size_t)rows * SI * 4);
+    const size_t o_sh = off;     off += al256((size_t)rows * H * 4);
+    const size_t o_g1 = off;     off += al256((size_t)rows * 4);
+    char *S = scratch(off);
+    if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", off); return false; }
+    float *logits = (float *)(S + o_logits), *gu = (float *)(S + o_gu), *act = (float *)(S + o_act);
+    float *ey = (float *)(S + o_ey), *sg = (float *)(S + o_sg), *su = (float *)(S + o_su);
+    float *sh = (float *)(S + o_sh), *g1 = (float *)(S + o_g1);
+    int32_t *perm = (int32_t *)(S + o_perm), *tiles = (int32_t *)(S + o_tiles);
+    hipStream_t s = G.stream;
+    int rc = qwk_dmat_bf16(s, logits, x, dp(M->router), H, E, rows);
+    if (!rc) rc = qwk_route(s, idx, w, logits, rows, E, K, M->norm ? 1 : 0);
+    if (!rc) rc = qwk_moe_group(s, perm, tiles, idx, pairs, E, bm, mt);
+    if (M->split) {
+        if (!rc) rc = qwk_gather_gemm(s, gu, x, perm, tiles, q4r(&M->gate), H, I, K, 0, M->gate.group, bm, mt);
+        if (!rc) rc = qwk_gather_gemm(s, gu + (size_t)pairs * I, x, perm, tiles, q4r(&M->up), H, I, K, 0,
+                                      M->up.group, bm, mt);
+        if (!rc) rc = qwk_swiglu(s, act, gu, gu + (size_t)pairs * I, (int64_t)pairs * I);
+    } else {
+        if (!rc) rc = qwk_gather_gemm(s, gu, x, perm, tiles, q4r(&M->gate_up), H, 2 * I, K, 0, grp, bm, mt);
+        if (!rc) rc = qwk_swiglu_split(s, act, gu, pairs, I);
+    }
+    if (!rc) rc = qwk_gather_gemm(s, ey, act, perm, tiles, q4r(&M->down), I, H, K, 1, M->down.group, bm, mt);
+    if (!rc) rc = qwk_qmm(s, sg, x, q4r(&M->sh_gate), H, SI, rows, M->sh_gate.group);
+    if (!rc) rc = qwk_qmm(s, su, x, q4r(&M->sh_up), H, SI, rows, M->sh_up.group);
+    if (!rc) rc = qwk_swiglu(s, sg, sg, su, (int64_t)rows * SI);
+    if (!rc) rc = qwk_qmm(s, sh, sg, q4r(&M->sh_down), SI, H, rows, M->sh_down.group);
+    if (!rc) rc = qwk_dmat_bf16(s, g1, x, dp(M->sh_gate_w), H, 1, rows);
+    if (!rc) rc = qwk_moe_combine(s, out, ey, w, sh, g1, rows, K, H);
+    launched(c, "moe_layer (prefill)", rc);
+    return rc == 0;
+}
+
+/* Decode: the fused launches over only the selected experts. */
+static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float *x,
+                       const qw_moe_layer *M, int32_t rows) {
+    qwk_moe m;
+    m.H = M->H; m.E = M->E; m.K = M->K; m.I = M->I; m.SI = M->SI;
+    m.group = M->split ? M->gate.group : M->gate_up.group;
+    m.norm = M->norm ? 1 : 0;
+    m.split = M->split ? 1 : 0;
+    m.router = dp(M->router);
+    m.gate = q4r(&M->gate); m.up = q4r(&M->up); m.gate_up = q4r(&M->gate_up);
+    m.down = q4r(&M->down);
+    m.sh_gate = q4r(&M->sh_gate); m.sh_up = q4r(&M->sh_up); m.sh_down = q4r(&M->sh_down);
+    m.sh_gate_w = dp(M->sh_gate_w);
+    const size_t need = qwk_moe_decode_scratch(&m, rows);
+    void *S = scratch(need);
+    if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", need); return false; }
+    const int rc = qwk_moe_decode(G.stream, out, idx, w, x, &m, rows, S, need);
+    launched(c, "moe_layer (decode)", rc);
+    return rc == 0;
+}
+
+bool qw_op_moe_layer(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,
+                     const qw_moe_layer *M, int32_t rows) {
+    if (!M || rows < 1 || M->K > QWK_ROUTE_MAX_K || M->E > QWK_ROUTE_MAX_E || M->K > M->E ||
+        M->H % 64 || M->I % 64 || M->SI % 64 || M->H > QWK_DMAT_MAX_K)
+        return false;
+    const int32_t grp = M->split ? M->gate.group : M->gate_up.group;
+    if (M->down.group != grp || M->sh_gate.group != grp || M->sh_up.group != grp ||
+        M->sh_down.group != grp || (M->split && M->up.group != grp))
+        return false;
+    if (!c) return true;
+    touch(c, x, 0); touch(c, M->router, 0); touch(c, M->sh_gate_w, 0);
+    if (M->split) { touch_q4(c, &M->gate); touch_q4(c, &M->up); } else touch_q4(c, &M->gate_up);
+    touch_q4(c, &M->down); touch_q4(c, &M->sh_gate); touch_q4(c, &M->sh_up); touch_q4(c, &M->sh_down);
+    touch(c, out, 1); touch(c, idx, 1); touch(c, w, 1);
+    if (rows > QWK_DECODE_MAX_ROWS)
+        return moe_prefill(c, dp(out), dp(idx), dp(w), dp(x), M, rows);
+    return moe_decode(c, dp(out), dp(idx), dp(w), dp(x), M, rows);
+}

@@ -1,0 +1,145 @@
+"""Writes the golden fixtures under tests/golden/.  Run in the build container:
+
+    python tests/golden/make_fixtures.py
+
+1. tiny_q4_layer0.npz, tiny_mlx_layer0.npz -- layer 0's MoE tensors from the
+   reference's own toy checkpoints (tests/fixtures/flashnext-tiny-q4: fused
+   gate_up bank, group 64, bf16 router; flashnext-tiny-mlx: split switch_mlp
+   banks, group 32, 8-bit router and shared gate).  Safetensors are parsed
+   here as a JSON header plus raw little-endian bytes; nothing is executed.
+   The 8-bit matrices are dequantised to bf16 as the reference's loader does
+   (qwasar.c:1426-1461: w = scale * q + bias per group, rounded to bf16).
+2. c0_golden.npz -- BASELINE config 0 (seeded synthetic tensors) with the
+   oracle's routing and output for one token, and the tiny-q4 layer on
+   seeded inputs with the oracle's routing and outputs: regression vectors.
+"""
+from __future__ import annotations
+
+import json
+import os
+import struct
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+REF = "/root/reference/tests/fixtures"
+DT = {"BF16": np.uint16, "U32": np.uint32, "I32": np.int32, "F32": np.float32, "I64": np.int64,
+      "F16": np.float16, "U8": np.uint8, "I8": np.int8}
+
+
+def read_safetensors(path):
+    with open(path, "rb") as f:
+        raw = f.read()
+    n = struct.unpack("<Q", raw[:8])[0]
+    hdr = json.loads(raw[8:8 + n])
+    base = 8 + n
+    out = {}
+    for k, v in hdr.items():
+        if k == "__metadata__":
+            continue
+        a, b = v["data_offsets"]
+        out[k] = np.frombuffer(raw[base + a:base + b], dtype=DT[v["dtype"]]).reshape(v["shape"]).copy()
+    return out
+
+
+def load_dir(d):
+    t = {}
+    for f in sorted(os.listdir(d)):
+        if f.endswith(".safetensors"):
+            t.update(read_safetensors(os.path.join(d, f)))
+    return t
+
+
+def f32_to_bf16(a):
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(b):
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def dequant_small(w, s, b, cols):
+    """8- or 4-bit affine matrix -> bf16 [rows, cols] (qwasar.c:1444-1458)."""
+    rows, words = w.shape
+    bits = words * 32 // cols
+    per = 32 // bits
+    groups = s.shape[1]
+    group = cols // groups
+    j = np.arange(cols)
+    q = (w[:, j // per] >> (bits * (j % per)).astype(np.uint32)) & ((1 << bits) - 1)
+    v = bf16_to_f32(s)[:, j // group] * q.astype(np.float32) + bf16_to_f32(b)[:, j // group]
+    return f32_to_bf16(v.astype(np.float32))
+
+
+def tiny_q4():
+    d = os.path.join(REF, "flashnext-tiny-q4")
+    cfg = json.load(open(os.path.join(d, "config.json")))
+    t = load_dir(d)
+    p = "language_model.model.layers.0.mlp."
+    H, E = cfg["hidden_size"], cfg["num_experts"]
+    I, SI = cfg["moe_intermediate_size"], cfg["shared_expert_intermediate_size"]
+    out = dict(H=H, E=E, K=cfg["num_experts_per_tok"], I=I, SI=SI, group=64, split=0,
+               norm=int(cfg["norm_topk_prob"]),
+               router=t[p + "gate.weight"],
+               sh_gate_w=t[p + "shared_expert_gate.weight"].reshape(H))
+    for name, key, rows in (("gate_up", "experts.gate_up_proj", E * 2 * I), ("down", "experts.down_proj", E * H),
+                            ("sh_gate", "shared_expert.gate_proj", SI), ("sh_up", "shared_expert.up_proj", SI),
+                            ("sh_down", "shared_expert.down_proj", H)):
+        out[name + "_w"] = t[p + key + ".weight"].view(np.uint32).reshape(rows, -1)
+        out[name + "_s"] = t[p + key + ".scales"].reshape(rows, -1)
+        out[name + "_b"] = t[p + key + ".biases"].reshape(rows, -1)
+    return out
+
+
+def tiny_mlx():
+    d = os.path.join(REF, "flashnext-tiny-mlx")
+    cfg = json.load(open(os.path.join(d, "config.json")))
+    tc = cfg.get("text_config", cfg)
+    t = load_dir(d)
+    p = "language_model.model.layers.0.mlp."
+    H, E = tc["hidden_size"], tc["num_experts"]
+    I, SI = tc["moe_intermediate_size"], tc["shared_expert_intermediate_size"]
+    out = dict(H=H, E=E, K=tc["num_experts_per_tok"], I=I, SI=SI, group=32, split=1,
+               norm=int(tc["norm_topk_prob"]),
+               router=dequant_small(t[p + "gate.weight"], t[p + "gate.scales"], t[p + "gate.biases"], H),
+               sh_gate_w=dequant_small(t[p + "shared_expert_gate.weight"], t[p + "shared_expert_gate.scales"],
+                                       t[p + "shared_expert_gate.biases"], H).reshape(H))
+    for name, key, rows in (("gate", "switch_mlp.gate_proj", E * I), ("up", "switch_mlp.up_proj", E * I),
+                            ("down", "switch_mlp.down_proj", E * H),
+                            ("sh_gate", "shared_expert.gate_proj", SI), ("sh_up", "shared_expert.up_proj", SI),
+                            ("sh_down", "shared_expert.down_proj", H)):
+        out[name + "_w"] = t[p + key + ".weight"].view(np.uint32).reshape(rows, -1)
+        out[name + "_s"] = t[p + key + ".scales"].reshape(rows, -1)
+        out[name + "_b"] = t[p + key + ".biases"].reshape(rows, -1)
+    return out
+
+
+def main():
+    from qwasar_amd import synth
+    from oracle import ref
+    from tests.fixture_layers import layer_from_npz
+
+    q4 = tiny_q4()
+    np.savez_compressed(os.path.join(HERE, "tiny_q4_layer0.npz"), **q4)
+    mlx = tiny_mlx()
+    np.savez_compressed(os.path.join(HERE, "tiny_mlx_layer0.npz"), **mlx)
+
+    L, x = synth.make_config(0)
+    out, idx, w = ref.moe_forward(L, x)
+    gold = dict(c0_x=x, c0_out=out, c0_idx=idx, c0_w=w)
+    for tag, path in (("q4", "tiny_q4_layer0.npz"), ("mlx", "tiny_mlx_layer0.npz")):
+        TL = layer_from_npz(os.path.join(HERE, path))
+        tx = synth.make_x(77, 5, TL.H, name=f"tiny_{tag}.x")
+        o, i, ww = ref.moe_forward(TL, tx)
+        gold.update({f"{tag}_x": tx, f"{tag}_out": o, f"{tag}_idx": i, f"{tag}_w": ww})
+    np.savez_compressed(os.path.join(HERE, "c0_golden.npz"), **gold)
+    print("wrote", sorted(os.listdir(HERE)))
+
+
+if __name__ == "__main__":
+    main()

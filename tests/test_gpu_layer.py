@@ -1,0 +1,132 @@
+"""The whole MoE block through qw_op_moe_layer on the GPU against the CPU
+oracle: routing ids and weights bit-exact, outputs within the stated
+tolerance (max-abs 2e-2 and rel-L2 1e-3 is the bar; the fp32 decode path
+is held tighter)."""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import ref
+from qwasar_amd import synth
+from tests.fixture_layers import layer_from_npz
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return np.sqrt(((a - b) ** 2).sum() / (b * b).sum())
+
+
+def run_layer(gpu, lb, x):
+    rows = x.shape[0]
+    L = lb.L
+    B = gpu.Buf
+    xb, ob = B.of(x), B(rows * L.H * 4)
+    ib, wb = B(rows * L.K * 4), B(rows * L.K * 4)
+    c = gpu.qw_cmd_begin()
+    assert gpu.qw_op_moe_layer(c, ob.ref(), ib.ref(), wb.ref(), xb.ref(), lb.desc, rows)
+    gpu.run(c, f"moe_layer rows={rows}")
+    return (ob.read(np.float32, (rows, L.H)), ib.read(np.int32, (rows, L.K)),
+            wb.read(np.float32, (rows, L.K)))
+
+
+def check(got, want, tol_rel, tol_abs=2e-2):
+    out, idx, w = got
+    wout, widx, ww = want
+    assert np.array_equal(idx, widx), f"routing ids differ:\n{idx}\n{widx}"
+    assert np.array_equal(w.view(np.uint32), ww.view(np.uint32)), "routing weights not bit-exact"
+    e = rel_l2(out, wout)
+    m = np.abs(out - wout).max()
+    assert e < tol_rel and m < tol_abs, f"rel-L2 {e:.3g} max-abs {m:.3g}"
+    return e
+
+
+@pytest.mark.parametrize("name", ["tiny_q4_layer0.npz", "tiny_mlx_layer0.npz"])
+def test_reference_fixture_banks(gpu, name):
+    """Layer 0 of the reference's toy checkpoints (fused group 64; MLX split
+    group 32), on the committed golden inputs and oracle outputs."""
+    L = layer_from_npz(os.path.join(GOLD, name))
+    tag = "q4" if "q4" in name else "mlx"
+    g = np.load(os.path.join(GOLD, "c0_golden.npz"))
+    lb = gpu.LayerBufs(L)
+    got = run_layer(gpu, lb, g[f"{tag}_x"])
+    check(got, (g[f"{tag}_out"], g[f"{tag}_idx"], g[f"{tag}_w"]), 1e-5)
+    lb.free()
+
+
+def test_config0_golden(gpu):
+    L, x = synth.make_config(0)
+    g = np.load(os.path.join(GOLD, "c0_golden.npz"))
+    assert np.array_equal(x, g["c0_x"])
+    lb = gpu.LayerBufs(L)
+    check(run_layer(gpu, lb, x), (g["c0_out"], g["c0_idx"], g["c0_w"]), 1e-5)
+    lb.free()
+
+
+@pytest.mark.parametrize("rows", [1, 2, 5, 8, 9, 24])
+@pytest.mark.parametrize("split", [True, False])
+def test_config0_rows(gpu, rows, split):
+    """Decode (rows <= 8, fused) and grouped (rows > 8) on config 0's shape."""
+    L, x = synth.make_config(0, split=split, rows=rows, seed=100 + rows)
+    lb = gpu.LayerBufs(L)
+    got = run_layer(gpu, lb, x)
+    want = ref.moe_forward(L, x)
+    check(got, want, 1e-5 if rows <= 8 else 1e-3)
+    lb.free()
+
+
+@pytest.fixture(scope="module")
+def c1(gpu):
+    L, x = synth.make_config(1)
+    lb = gpu.LayerBufs(L)
+    yield L, lb
+    lb.free()
+
+
+def test_config1_decode(gpu, c1):
+    L, lb = c1
+    for t in range(3):
+        x = synth.make_x(500 + t, 1, L.H)
+        check(run_layer(gpu, lb, x), ref.moe_forward(L, x), 1e-5)
+
+
+def test_config2_decode_batch8_shared_experts(gpu, c1):
+    """Eight tokens that all pick experts 7, 200, 411 (a +8 logit bias through
+    column 0): the union dedups their weight reads."""
+    L0, lb0 = c1
+    L, x = synth.make_config(2)
+    lb = gpu.LayerBufs(L)
+    got = run_layer(gpu, lb, x)
+    want = ref.moe_forward(L, x)
+    check(got, want, 1e-5)
+    for r in range(8):
+        assert set(synth.C2_HOT) <= set(got[1][r].tolist())
+    lb.free()
+
+
+def test_config3_prefill_sample(gpu):
+    """512-token prefill with Zipf-skewed routing: every token's routing
+    bit-exact; outputs of a sample of tokens against the oracle."""
+    L, x = synth.make_config(3)
+    lb = gpu.LayerBufs(L)
+    out, idx, w = run_layer(gpu, lb, x)
+    logits = ref.dmat_bf16(x, L.router, L.H, L.E, x.shape[0])
+    widx, ww = ref.route(logits, x.shape[0], L.E, L.K, norm=True)
+    assert np.array_equal(idx, widx)
+    assert np.array_equal(w.view(np.uint32), ww.view(np.uint32))
+    sel = np.arange(0, 512, 37)
+    wout, _, _ = ref.moe_forward(L, np.ascontiguousarray(x[sel]))
+    e = rel_l2(out[sel], wout)
+    assert e < 1e-3 and np.abs(out[sel] - wout).max() < 2e-2, f"rel-L2 {e:.3g}"
+    # the skew: the hottest expert takes many tokens
+    counts = np.bincount(idx.ravel(), minlength=L.E)
+    assert counts.max() > 100
+    # deterministic: a second run is bit-identical
+    out2, _, _ = run_layer(gpu, lb, x)
+    assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
+    lb.free()
