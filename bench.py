@@ -1,0 +1,286 @@
+#!/usr/bin/env python3
+"""Benchmark of the Flash-Next MoE layer on one MI355X.
+
+Headline (the JSON line's `value`): BASELINE config 1 -- one MoE layer of
+Flash-Next shape (H 3072, 512 experts, top-10, I 512, shared SI 512, MLX
+4-bit group 64) decoding one token -- in microseconds per token, with all
+expert weights resident in HBM, timed with HIP events on the backend's
+stream over K back-to-back steps.  A step is one qw_op_moe_layer call on one
+token (router, routing, the ten selected experts, the gated shared expert,
+the combine).
+
+Steps cycle through a pool of 64 tokens chosen (by the GPU's own routing) so
+that any 12 consecutive tokens select pairwise disjoint experts: every step
+reads its routed experts from HBM, not from the 256 MB Infinity Cache.
+
+Also reported: the per-kernel decode breakdown, HBM bandwidth on the routed
+("selected-expert") bytes and on all bytes, config 3 (512-token prefill with
+Zipf-skewed routing) and a 2048-token prefill chunk (config 4's per-layer
+step) in tokens/s and bf16-MFMA utilisation, and the CPU oracle's time on a
+bounded sample of the same decode workload (single-threaded scalar C, the
+reference's own CPU path restated; see oracle/).
+
+    python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, AMD spec
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, AMD spec
+POOL = 64
+COLD_WINDOW = 12
+
+
+def q4_bytes(rows, cols, group):
+    return rows * cols // 2 + (rows * cols // group) * 4
+
+
+def decode_bytes(c):
+    """Algorithmic bytes of one decode token, per kernel and in total."""
+    H, E, K, I, SI, G = c["H"], c["E"], c["K"], c["I"], c["SI"], c["group"]
+    expert_gu = 2 * q4_bytes(I, H, G)
+    expert_down = q4_bytes(H, I, G)
+    shared_gu = 2 * q4_bytes(SI, H, G)
+    shared_down = q4_bytes(H, SI, G)
+    router = 2 * E * H + 2 * H
+    return {
+        "routed": K * (expert_gu + expert_down),
+        "all": K * (expert_gu + expert_down) + shared_gu + shared_down + router,
+        "front": router + shared_gu,
+        "experts": K * expert_gu + shared_down,
+        "down": K * expert_down,
+    }
+
+
+def prefill_flops(c, rows):
+    H, E, K, I, SI = c["H"], c["E"], c["K"], c["I"], c["SI"]
+    return rows * (2 * K * 3 * I * H + 2 * 3 * SI * H + 2 * E * H)
+
+
+def select_cold_pool(gpu, lb, cand_x, K):
+    """Route candidates on the GPU; keep a cycle of POOL tokens in which any
+    COLD_WINDOW consecutive ones select disjoint experts."""
+    L = lb.L
+    n = cand_x.shape[0]
+    B = gpu.Buf
+    xb, lg = B.of(cand_x), B(n * L.E * 4)
+    ib, wb = B(n * K * 4), B(n * K * 4)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_op_dmat_bf16(c, lg.ref(), xb.ref(), lb.router.ref(), L.H, L.E, n)
+    gpu.qw_op_moe_route(c, ib.ref(), wb.ref(), lg.ref(), n, L.E, K, True)
+    gpu.run(c, "route candidates")
+    ids = ib.read(np.int32, (n, K))
+    chosen, used = [], set(range(n))
+    for _ in range(POOL):
+        recent = set()
+        for j in chosen[-(COLD_WINDOW - 1):]:
+            recent.update(ids[j].tolist())
+        if len(chosen) >= POOL - COLD_WINDOW + 1:
+            for j in chosen[:COLD_WINDOW - (POOL - len(chosen))]:
+                recent.update(ids[j].tolist())
+        pick = next((i for i in sorted(used) if not recent.intersection(ids[i].tolist())), None)
+        if pick is None:
+            raise RuntimeError("could not build a cold token pool; raise the candidate count")
+        chosen.append(pick)
+        used.discard(pick)
+    return np.ascontiguousarray(cand_x[chosen]), ids[chosen]
+
+
+def time_decode(gpu, lb, xpool, steps, warmup, profile):
+    """Returns ms for `steps` decode steps, bracketed by HIP events (marks)."""
+    L = lb.L
+    B = gpu.Buf
+    xb = B.of(xpool)
+    ob, ib, wb = B(L.H * 4), B(L.K * 4), B(L.K * 4)
+    row = L.H * 4
+    c = gpu.qw_cmd_begin()
+    for s in range(warmup):
+        gpu.qw_op_moe_layer(c, ob.ref(), ib.ref(), wb.ref(), xb.ref((s % POOL) * row), lb.desc, 1)
+    gpu.qw_cmd_wait(c)
+    gpu.qw_prof_reset()
+    gpu.qw_prof_set_enabled(True)
+    gpu.qw_cmd_free(c)
+    c = gpu.qw_cmd_begin()                       # records the region's start event
+    if not profile:
+        gpu.qw_prof_set_enabled(False)           # no per-kernel events inside the region
+    for s in range(steps):
+        gpu.qw_op_moe_layer(c, ob.ref(), ib.ref(), wb.ref(), xb.ref(((warmup + s) % POOL) * row), lb.desc, 1)
+    gpu.qw_prof_set_enabled(True)
+    gpu.qw_cmd_mark(c, b"decode region")
+    gpu.run(c, "decode")
+    gpu.qw_prof_set_enabled(False)
+    res = {"region": gpu.qw_prof_ms(b"decode region", None)}
+    for k in ("front", "experts", "down"):
+        res[k] = gpu.qw_prof_ms(f"moe decode {k}".encode(), None)
+    gpu.qw_prof_reset()
+    return res
+
+
+def time_prefill(gpu, lb, x, reps):
+    L = lb.L
+    rows = x.shape[0]
+    B = gpu.Buf
+    xb, ob = B.of(x), B(rows * L.H * 4)
+    ib, wb = B(rows * L.K * 4), B(rows * L.K * 4)
+    c = gpu.qw_cmd_begin()
+    for _ in range(2):
+        gpu.qw_op_moe_layer(c, ob.ref(), ib.ref(), wb.ref(), xb.ref(), lb.desc, rows)
+    gpu.run(c, "prefill warmup")
+    gpu.qw_prof_reset()
+    gpu.qw_prof_set_enabled(True)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_prof_set_enabled(False)
+    for _ in range(reps):
+        gpu.qw_op_moe_layer(c, ob.ref(), ib.ref(), wb.ref(), xb.ref(), lb.desc, rows)
+    gpu.qw_prof_set_enabled(True)
+    gpu.qw_cmd_mark(c, b"prefill region")
+    gpu.run(c, "prefill")
+    gpu.qw_prof_set_enabled(False)
+    ms = gpu.qw_prof_ms(b"prefill region", None) / reps
+    gpu.qw_prof_reset()
+    counts = np.bincount(ib.read(np.int32, (rows, L.K)).ravel(), minlength=L.E)
+    return ms, int(counts.max()), int((counts > 0).sum())
+
+
+def cpu_baseline(L, xpool, seconds):
+    """The oracle (the reference's scalar moe_step restated in C, one thread)
+    on the same decode tokens, for a bounded time."""
+    from oracle import ref
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds and n < xpool.shape[0]:
+        ref.moe_forward(L, xpool[n:n + 1])
+        n += 1
+    dt = time.perf_counter() - t0
+    return dt / n * 1e6, n
+
+
+def calib_copy(nbytes):
+    """A plain device copy of known size, for scaling rocprofv3's FETCH_SIZE /
+    WRITE_SIZE counters to bytes."""
+    import torch
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"calib_copy_bytes": nbytes}))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--calib-copy", type=int, default=0, help="bytes: run only the copy calibration")
+    ap.add_argument("--decode-only-steps", type=int, default=0,
+                    help="profiling aid: only run this many decode steps after setup")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.calib_copy:
+        calib_copy(args.calib_copy)
+        return
+
+    from qwasar_amd import gpu, synth
+    gpu.init()
+    cfg = dict(synth.CONFIGS[1])
+    seed = 1234
+    L = synth.make_layer(seed, **{k: cfg[k] for k in ("H", "E", "K", "I", "SI", "group")})
+    lb = gpu.LayerBufs(L)
+    cand = synth.make_x(seed, 2048, L.H, name="bench.candidates")
+    xpool, pool_ids = select_cold_pool(gpu, lb, cand, L.K)
+
+    if args.decode_only_steps:
+        time_decode(gpu, lb, xpool, args.decode_only_steps, 0, False)
+        return
+
+    nb = decode_bytes(cfg)
+    dec = time_decode(gpu, lb, xpool, args.steps, args.warmup, profile=False)
+    us_tok = dec["region"] * 1000.0 / args.steps
+    brk = time_decode(gpu, lb, xpool, args.steps, 0, profile=True)
+    per_k = {k: brk[k] * 1000.0 / args.steps for k in ("front", "experts", "down")}
+    dom = max(per_k, key=per_k.get)
+    roof_gbs = nb[dom] / (per_k[dom] * 1e-6) / 1e9
+
+    out = {
+        "metric": "moe_layer_decode_us_per_token",
+        "value": round(us_tok, 3),
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_tok / 1000.0, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4xf32",
+        "data": "synthetic (seeded MLX-affine 4-bit weights, N(0,1) bf16 tokens)",
+        "config": {"workload": "BASELINE config 1: Flash-Next-shaped MoE layer decode, batch 1",
+                   "H": cfg["H"], "E": cfg["E"], "K": cfg["K"], "I": cfg["I"], "SI": cfg["SI"],
+                   "group": cfg["group"], "tokens_per_step": 1, "token_pool": POOL,
+                   "cold_window": COLD_WINDOW},
+        "decode": {
+            "us_per_token": round(us_tok, 3),
+            "routed_bytes": nb["routed"], "all_bytes": nb["all"],
+            "routed_hbm_gbs": round(nb["routed"] / (us_tok * 1e-6) / 1e9, 1),
+            "routed_hbm_frac": round(nb["routed"] / (us_tok * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "all_hbm_gbs": round(nb["all"] / (us_tok * 1e-6) / 1e9, 1),
+            "kernels_us": {k: round(v, 3) for k, v in per_k.items()},
+            "kernels_bytes": {k: nb[k] for k in ("front", "experts", "down")},
+            "kernels_gbs": {k: round(nb[k] / (per_k[k] * 1e-6) / 1e9, 1) for k in per_k},
+            "breakdown_us_total": round(brk["region"] * 1000.0 / args.steps, 3),
+        },
+        "roofline": {"bound": "hbm", "kernel": f"k_decode_{dom}", "achieved": round(roof_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(roof_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None},
+    }
+
+    if not args.no_prefill:
+        pf = {}
+        zb = synth.zipf_bias(seed, L.E)
+        r3 = synth.make_router(seed, L.E, L.H, zb)
+        rb3 = gpu.Buf(wrap=r3)
+        d3 = gpu.qw_moe_layer.from_buffer_copy(lb.desc)
+        d3.router = rb3.ref()
+
+        class _LB3:
+            pass
+        lb3 = _LB3()
+        lb3.L, lb3.desc = L, d3
+        for name, rows, lbx, const0 in (("config3_zipf_512", 512, lb3, True),
+                                        ("chunk_2048_uniform", 2048, lb, False)):
+            x = synth.make_x(seed + rows, rows, L.H, name=f"bench.prefill{rows}", const_col0=const0)
+            ms, hot, touched = time_prefill(gpu, lbx, x, reps=5)
+            fl = prefill_flops(cfg, rows)
+            pf[name] = {"rows": rows, "ms": round(ms, 3), "tokens_per_s": round(rows / (ms * 1e-3), 1),
+                        "useful_tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+                        "mfma_util": round(fl / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                        "weight_read_floor_ms": round(L.weight_bytes() / HBM_PEAK_GBS / 1e6, 3),
+                        "hottest_expert_pairs": hot, "experts_touched": touched}
+        out["prefill"] = pf
+
+    if not args.no_cpu:
+        us, n = cpu_baseline(L, xpool, args.cpu_seconds)
+        out["cpu_baseline"] = {"value": round(us, 1), "unit": "us/token", "cores": 1, "kind": "port",
+                               "sample": f"{n} decode tokens of config 1 through oracle/moe_ref.c "
+                                         "(scalar C, -O2, one thread), same weights and tokens"}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

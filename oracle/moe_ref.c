@@ -54,6 +54,10 @@ float qr_exp(float x) {
     return ldexpf(p, (int)kf);
 }
 
+void qr_exp_vec(float *out, const float *in, int64_t n) {
+    for (int64_t i = 0; i < n; i++) out[i] = qr_exp(in[i]);
+}
+
 void qr_dequant_row(float *out, const uint32_t *w, const uint16_t *scales,
                     const uint16_t *biases, int32_t k, int32_t row, int32_t group) {
     /* MLX affine: element i at bit 4*(i%8) of word i/8; w = scale*nib + bias

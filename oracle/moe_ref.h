@@ -53,6 +53,7 @@ extern "C" {
 float qr_bf16_to_f32(uint16_t v);
 uint16_t qr_f32_to_bf16(float f);
 float qr_exp(float x);
+void qr_exp_vec(float *out, const float *in, int64_t n);
 
 /* Dequantised row `row` of an MLX affine 4-bit matrix (qwasar_cpu.c:21-38). */
 void qr_dequant_row(float *out, const uint32_t *w, const uint16_t *scales,

@@ -56,6 +56,7 @@ def lib():
         L.qr_bf16_to_f32.argtypes = [C.c_uint16]
         L.qr_exp.restype = C.c_float
         L.qr_exp.argtypes = [C.c_float]
+        L.qr_exp_vec.argtypes = [_P, _P, C.c_int64]
         L.qr_dot_bf16.restype = C.c_float
         L.qr_dot_bf16.argtypes = [_P, _P, _I]
         L.qr_dequant_row.argtypes = [_P, _P, _P, _P, _I, _I, _I]
@@ -93,9 +94,10 @@ def reflib():
 # ---- numpy-level helpers -----------------------------------------------------
 
 def exp_vec(x: np.ndarray) -> np.ndarray:
-    L = lib()
-    return np.array([L.qr_exp(float(v)) for v in np.asarray(x, np.float32).ravel()],
-                    dtype=np.float32).reshape(np.shape(x))
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().qr_exp_vec(_ptr(out), _ptr(x), x.size)
+    return out
 
 
 def qmv_q4(x, w, s, b, k, n, rows, group):

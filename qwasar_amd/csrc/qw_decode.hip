@@ -27,7 +27,7 @@
 #define QD_MAXU (QWK_DECODE_MAX_ROWS * QWK_ROUTE_MAX_K)
 
 struct QdLayout {
-    size_t ctr, logits, g1, shgu, shout, uinfo, gu, ey, total;
+    size_t logits, g1, shgu, shout, uinfo, gu, ey, total;
     int nrb;        // down row blocks
 };
 
@@ -49,7 +49,6 @@ static QdLayout qd_layout(const qwk_moe *M, int rows)
     const int umax = rows * M->K < M->E ? rows * M->K : M->E;
     L.nrb = (M->H + qd_rows_per_wg(M->I) - 1) / qd_rows_per_wg(M->I);
     size_t o = 0;
-    L.ctr = o;    o += al((size_t)(4 + L.nrb) * 4);
     L.logits = o; o += al((size_t)rows * M->E * 4);
     L.g1 = o;     o += al((size_t)rows * 4);
     L.shgu = o;   o += al((size_t)rows * 2 * M->SI * 4);
@@ -366,8 +365,9 @@ __global__ __launch_bounds__(QD_THREADS) void k_decode_experts(QdArgs a)
     const int ngu = a.umax * a.n_gu_wg_per_u;
     if (b < ngu) {
         const int u = b / a.n_gu_wg_per_u, rb = b % a.n_gu_wg_per_u;
-        if (u >= a.uinfo[0]) return;
-        const int e = qd_uexp(a)[u], nt = qd_ucnt(a)[u];
+        if (u >= min(a.uinfo[0], a.umax)) return;
+        const int e = qd_uexp(a)[u], nt = min(qd_ucnt(a)[u], a.rows);
+        if (e < 0 || e >= a.m.E || nt < 1) return;
         // Split banks: z = gate / up, each I rows; fused: one bank of 2I rows.
         const int nz = a.m.split ? 2 : 1, nrow = a.m.split ? I : 2 * I;
         const int per_z = a.n_gu_wg_per_u / nz;
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(QD_THREADS) void k_decode_experts(QdArgs a)
         const int row0 = ((rb % per_z) * QD_WAVES + wave) * (qd_rows_per_wg(H) / QD_WAVES);
         if (threadIdx.x < QD_MAXT) {
             const int t = threadIdx.x;
-            const int p = qd_upair(a)[u * a.rows + min(t, nt - 1)];
+            const int p = min(max(qd_upair(a)[u * a.rows + min(t, nt - 1)], 0), a.rows * K - 1);
             xp[t] = a.x + (size_t)(p / K) * H;
             yp[t] = a.gu + (size_t)p * 2 * I + z * I;
         }
@@ -410,21 +410,22 @@ __global__ __launch_bounds__(QD_THREADS) void k_decode_down(QdArgs a)
     const int wave = threadIdx.x >> 6, b = blockIdx.x;
     const int H = a.m.H, I = a.m.I, K = a.m.K;
     const int u = b / a.nrb, rb = b % a.nrb;
-    const int U = a.uinfo[0];
+    const int U = min(a.uinfo[0], a.umax);
     if (u >= U) return;
-    const int e = qd_uexp(a)[u], nt = qd_ucnt(a)[u];
+    const int e = qd_uexp(a)[u], nt = min(qd_ucnt(a)[u], a.rows);
+    const bool ok = e >= 0 && e < a.m.E && nt >= 1;
     const int rpw = qd_rows_per_wg(I);
     const int row0 = rb * rpw + wave * (rpw / QD_WAVES);
     if (threadIdx.x < QD_MAXT) {
         const int t = threadIdx.x;
-        const int p = qd_upair(a)[u * a.rows + min(t, nt - 1)];
+        const int p = ok ? min(max(qd_upair(a)[u * a.rows + min(t, nt - 1)], 0), a.rows * K - 1) : 0;
         xp[t] = a.gu + (size_t)p * 2 * I;
         upp[t] = a.gu + (size_t)p * 2 * I + I;
         yp[t] = a.ey + (size_t)p * H;
     }
     __syncthreads();
     const size_t words = I / 8, groups = I / G;
-    if (row0 < H)
+    if (ok && row0 < H)
         qd_rows_k<G, true>(I, a.m.down.w + (size_t)e * H * words, a.m.down.s + (size_t)e * H * groups,
                            a.m.down.b + (size_t)e * H * groups, H, row0, nt, xp, upp, yp);
     if (qd_last_arrival(a.ctr + 4 + rb, U)) {
@@ -446,18 +447,28 @@ extern "C" size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows)
     return qd_layout(M, rows).total;
 }
 
+extern "C" int qwk_moe_decode_counters(const qwk_moe *M)
+{
+    return 4 + qd_layout(M, 1).nrb;
+}
+
 template <int G>
-static int qd_launch(hipStream_t s, QdArgs &a)
+static int qd_launch(hipStream_t s, QdArgs &a, hipEvent_t *ev)
 {
     const dim3 blk(QD_THREADS);
+    if (ev) (void)hipEventRecord(ev[0], s);
     hipLaunchKernelGGL(k_decode_front<G>, dim3(a.n_router_wg + a.n_shared_wg), blk, 0, s, a);
+    if (ev) (void)hipEventRecord(ev[1], s);
     hipLaunchKernelGGL(k_decode_experts<G>, dim3(a.umax * a.n_gu_wg_per_u + a.n_shdown_wg), blk, 0, s, a);
+    if (ev) (void)hipEventRecord(ev[2], s);
     hipLaunchKernelGGL(k_decode_down<G>, dim3(a.umax * a.nrb), blk, 0, s, a);
+    if (ev) (void)hipEventRecord(ev[3], s);
     return (int)hipGetLastError();
 }
 
 extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
-                              const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes)
+                              const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes,
+                              int *counters, int ncounters, hipEvent_t *ev)
 {
     if (rows < 1 || rows > QWK_DECODE_MAX_ROWS || M->K < 1 || M->K > QWK_ROUTE_MAX_K ||
         M->E < M->K || M->E > QWK_ROUTE_MAX_E || M->H % 64 || M->I % 32 || M->SI % 32 ||
@@ -465,7 +476,8 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
         M->H % M->group || M->I % M->group || M->SI % M->group)
         return (int)hipErrorInvalidValue;
     const QdLayout L = qd_layout(M, rows);
-    if (scratch_bytes < L.total || ((uintptr_t)x & 15u)) return (int)hipErrorInvalidValue;
+    if (scratch_bytes < L.total || ((uintptr_t)x & 15u) || ncounters < 4 + L.nrb)
+        return (int)hipErrorInvalidValue;
     char *S = (char *)scratch;
     QdArgs a;
     a.m = *M;
@@ -479,7 +491,7 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     a.n_gu_wg_per_u = nz * ((nrow + rpw_h - 1) / rpw_h);
     const int rpw_si = qd_rows_per_wg(M->SI);
     a.n_shdown_wg = (M->H + rpw_si - 1) / rpw_si;
-    a.ctr = (int *)(S + L.ctr);
+    a.ctr = counters;
     a.logits = (float *)(S + L.logits);
     a.g1 = (float *)(S + L.g1);
     a.shgu = (float *)(S + L.shgu);
@@ -488,8 +500,8 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     a.gu = (float *)(S + L.gu);
     a.ey = (float *)(S + L.ey);
     switch (M->group) {
-    case 32: return qd_launch<32>(s, a);
-    case 64: return qd_launch<64>(s, a);
-    default: return qd_launch<128>(s, a);
+    case 32: return qd_launch<32>(s, a, ev);
+    case 64: return qd_launch<64>(s, a, ev);
+    default: return qd_launch<128>(s, a, ev);
     }
 }

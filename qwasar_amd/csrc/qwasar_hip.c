@@ -57,7 +57,9 @@ struct qw_cmd_s {
     int nwritten, capwritten;
     qw_mark *marks;
     int nmarks, capmarks;
-    hipEvent_t last;
+    hipEvent_t *evs;         /* every event this command created */
+    int nevs, capevs;
+    hipEvent_t last;         /* where the next mark starts */
     struct qw_cmd_s *next;   /* live commands, for qw_buf_free */
 };
 
@@ -71,6 +73,8 @@ static struct {
     qw_cmd live;
     void *scratch;
     size_t scratch_len;
+    int *counters;       /* the decode path's arrival counters, zero between calls */
+    int ncounters;
 } G;
 
 /* ---- profiling table ---------------------------------------------------- */
@@ -133,7 +137,7 @@ bool qw_gpu_init(char *err, size_t errcap) {
     (void)hipMemGetInfo(&fr, &tot);
     G.free0 = fr;
     G.total = tot;
-    snprintf(G.name, sizeof G.name, "%s (%s)", prop.name, prop.gcnArchName);
+    snprintf(G.name, sizeof G.name, "%.200s (%.64s)", prop.name, prop.gcnArchName);
     const char *pe = getenv("QWASAR_PROFILE");
     G.prof = pe && *pe && strcmp(pe, "0") != 0;
     G.device = 0;
@@ -154,6 +158,9 @@ void qw_gpu_shutdown(void) {
     if (G.scratch) hipFree(G.scratch);
     G.scratch = NULL;
     G.scratch_len = 0;
+    if (G.counters) hipFree(G.counters);
+    G.counters = NULL;
+    G.ncounters = 0;
     hipStreamDestroy(G.stream);
     G.ready = 0;
 }
@@ -226,16 +233,38 @@ size_t qw_buf_length(qw_buf b) { return b ? b->len : 0; }
 
 /* ---- commands ---------------------------------------------------------------- */
 
+/* A new event owned by the command, optionally recorded on the stream now. */
+static hipEvent_t cmd_event(qw_cmd c, int record) {
+    hipEvent_t e = NULL;
+    if (hipEventCreate(&e) != hipSuccess) return NULL;
+    if (c->nevs == c->capevs) {
+        c->capevs = c->capevs ? 2 * c->capevs : 16;
+        c->evs = realloc(c->evs, (size_t)c->capevs * sizeof *c->evs);
+    }
+    c->evs[c->nevs++] = e;
+    if (record) hipEventRecord(e, G.stream);
+    return e;
+}
+
+static void cmd_add_mark(qw_cmd c, const char *label, hipEvent_t a, hipEvent_t b) {
+    if (!a || !b) return;
+    if (c->nmarks == c->capmarks) {
+        c->capmarks = c->capmarks ? 2 * c->capmarks : 16;
+        c->marks = realloc(c->marks, (size_t)c->capmarks * sizeof *c->marks);
+    }
+    c->marks[c->nmarks].label = label;
+    c->marks[c->nmarks].a = a;
+    c->marks[c->nmarks].b = b;
+    c->nmarks++;
+}
+
 qw_cmd qw_cmd_begin(void) {
     if (!ensure_init()) return NULL;
     qw_cmd c = calloc(1, sizeof *c);
     if (!c) return NULL;
-    if (G.prof) {
-        hipEventCreate(&c->last);
-        hipEventRecord(c->last, G.stream);
-    }
     c->next = G.live;
     G.live = c;
+    if (G.prof) c->last = cmd_event(c, 1);
     return c;
 }
 
@@ -283,17 +312,8 @@ void qw_cmd_parallel(qw_cmd c, bool on) { (void)c; (void)on; }
 
 void qw_cmd_mark(qw_cmd c, const char *label) {
     if (!c || !G.prof) return;
-    hipEvent_t e;
-    hipEventCreate(&e);
-    hipEventRecord(e, G.stream);
-    if (c->nmarks == c->capmarks) {
-        c->capmarks = c->capmarks ? 2 * c->capmarks : 16;
-        c->marks = realloc(c->marks, (size_t)c->capmarks * sizeof *c->marks);
-    }
-    c->marks[c->nmarks].label = label;
-    c->marks[c->nmarks].a = c->last;
-    c->marks[c->nmarks].b = e;
-    c->nmarks++;
+    hipEvent_t e = cmd_event(c, 1);
+    if (c->last) cmd_add_mark(c, label, c->last, e);
     c->last = e;
 }
 
@@ -311,15 +331,17 @@ void qw_cmd_wait(qw_cmd c) {
     c->nwritten = 0;
     for (int i = 0; i < c->nmarks; i++) {
         float ms = 0.0f;
-        if (c->marks[i].a && hipEventElapsedTime(&ms, c->marks[i].a, c->marks[i].b) == hipSuccess)
+        if (hipEventElapsedTime(&ms, c->marks[i].a, c->marks[i].b) == hipSuccess)
             prof_add(c->marks[i].label, ms);
-        if (c->marks[i].a && (i == 0 || c->marks[i].a != c->marks[i - 1].b)) hipEventDestroy(c->marks[i].a);
-    }
-    if (c->nmarks) {
-        c->last = c->marks[c->nmarks - 1].b;
-        for (int i = 0; i + 1 < c->nmarks; i++) hipEventDestroy(c->marks[i].b);
     }
     c->nmarks = 0;
+    /* Keep only the event the next mark starts from. */
+    int kept = 0;
+    for (int i = 0; i < c->nevs; i++) {
+        if (c->evs[i] == c->last) c->evs[kept++] = c->evs[i];
+        else hipEventDestroy(c->evs[i]);
+    }
+    c->nevs = kept;
 }
 
 const char *qw_cmd_error(qw_cmd c) { return c && c->err != hipSuccess ? c->msg : NULL; }
@@ -328,11 +350,8 @@ void qw_cmd_free(qw_cmd c) {
     if (!c) return;
     for (qw_cmd *pp = &G.live; *pp; pp = &(*pp)->next)
         if (*pp == c) { *pp = c->next; break; }
-    for (int i = 0; i < c->nmarks; i++) {
-        if (c->marks[i].a && (i == 0 || c->marks[i].a != c->marks[i - 1].b)) hipEventDestroy(c->marks[i].a);
-        hipEventDestroy(c->marks[i].b);
-    }
-    if (!c->nmarks && c->last) hipEventDestroy(c->last);
+    for (int i = 0; i < c->nevs; i++) hipEventDestroy(c->evs[i]);
+    free(c->evs);
     free(c->marks);
     free(c->written);
     free(c);
@@ -545,9 +564,6 @@ static void *scratch(size_t bytes) {
     G.scratch = NULL;
     G.scratch_len = 0;
     if (hipMalloc(&G.scratch, bytes) != hipSuccess) return NULL;
-    /* The decode kernels' arrival counters start at zero and are reset by
-     * the workgroup that completes them. */
-    hipMemset(G.scratch, 0, bytes);
     G.scratch_len = bytes;
     return G.scratch;
 }
@@ -623,7 +639,32 @@ static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float
     const size_t need = qwk_moe_decode_scratch(&m, rows);
     void *S = scratch(need);
     if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", need); return false; }
-    const int rc = qwk_moe_decode(G.stream, out, idx, w, x, &m, rows, S, need);
+    /* Arrival counters live apart from the scratch, which the prefill path
+     * overwrites: zeroed once when (re)allocated, left zero by each call. */
+    const int nctr = qwk_moe_decode_counters(&m);
+    if (nctr > G.ncounters) {
+        hipStreamSynchronize(G.stream);
+        if (G.counters) hipFree(G.counters);
+        G.counters = NULL;
+        G.ncounters = 0;
+        if (hipMalloc((void **)&G.counters, (size_t)nctr * sizeof(int)) != hipSuccess) {
+            cmd_fail(c, hipErrorOutOfMemory, "moe_layer: counters");
+            return false;
+        }
+        hipMemset(G.counters, 0, (size_t)nctr * sizeof(int));
+        G.ncounters = nctr;
+    }
+    /* Profiling charges each of the three launches to its own label. */
+    hipEvent_t ev[4] = { NULL, NULL, NULL, NULL };
+    int per_kernel = G.prof != 0;
+    for (int i = 0; per_kernel && i < 4; i++)
+        if (!(ev[i] = cmd_event(c, 0))) per_kernel = 0;
+    const int rc = qwk_moe_decode(G.stream, out, idx, w, x, &m, rows, S, need, G.counters, G.ncounters,
+                                  per_kernel ? ev : NULL);
+    if (per_kernel) {
+        static const char *labels[3] = { "moe decode front", "moe decode experts", "moe decode down" };
+        for (int i = 0; i < 3; i++) cmd_add_mark(c, labels[i], ev[i], ev[i + 1]);
+    }
     launched(c, "moe_layer (decode)", rc);
     return rc == 0;
 }

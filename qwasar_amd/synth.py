@@ -133,14 +133,20 @@ class MoeLayer:
         return per // 2 + (per // self.group) * 4
 
 
+def make_router(seed: int, E: int, H: int, logit_bias: Optional[np.ndarray] = None,
+                tag: str = "") -> np.ndarray:
+    """bf16 [E, H] router, N(0, 0.02); column 0 holds the logit bias if given."""
+    router = normal(seed, f"{tag}moe.router", E * H, 0.02).astype(np.float32).reshape(E, H)
+    if logit_bias is not None:
+        router[:, 0] = np.asarray(logit_bias, np.float32)
+    return to_bf16(router)
+
+
 def make_layer(seed: int, H: int, E: int, K: int, I: int, SI: int, group: int = 64,
                norm: bool = True, split: bool = True,
                logit_bias: Optional[np.ndarray] = None, tag: str = "") -> MoeLayer:
     p = f"{tag}moe."
-    router = normal(seed, p + "router", E * H, 0.02).astype(np.float32).reshape(E, H)
-    if logit_bias is not None:
-        router[:, 0] = np.asarray(logit_bias, np.float32)
-    router = to_bf16(router)
+    router = make_router(seed, E, H, logit_bias, tag)
     if split:
         gate = make_q4(seed, p + "gate", E * I, H, group)
         up = make_q4(seed, p + "up", E * I, H, group)

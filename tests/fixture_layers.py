@@ -21,4 +21,4 @@ def layer_from_npz(path: str) -> MoeLayer:
                     np.ascontiguousarray(d["router"]),
                     q("gate_up", E * 2 * I, H), q("gate", E * I, H), q("up", E * I, H),
                     q("down", E * H, I), q("sh_gate", SI, H), q("sh_up", SI, H), q("sh_down", H, SI),
-                    np.ascontiguousarray(d["sh_gate_w"]))
+                    np.ascontiguousarray(d["sh_gate_vec"]))

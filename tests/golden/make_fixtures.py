@@ -86,7 +86,7 @@ def tiny_q4():
     out = dict(H=H, E=E, K=cfg["num_experts_per_tok"], I=I, SI=SI, group=64, split=0,
                norm=int(cfg["norm_topk_prob"]),
                router=t[p + "gate.weight"],
-               sh_gate_w=t[p + "shared_expert_gate.weight"].reshape(H))
+               sh_gate_vec=t[p + "shared_expert_gate.weight"].reshape(H))
     for name, key, rows in (("gate_up", "experts.gate_up_proj", E * 2 * I), ("down", "experts.down_proj", E * H),
                             ("sh_gate", "shared_expert.gate_proj", SI), ("sh_up", "shared_expert.up_proj", SI),
                             ("sh_down", "shared_expert.down_proj", H)):
@@ -107,7 +107,7 @@ def tiny_mlx():
     out = dict(H=H, E=E, K=tc["num_experts_per_tok"], I=I, SI=SI, group=32, split=1,
                norm=int(tc["norm_topk_prob"]),
                router=dequant_small(t[p + "gate.weight"], t[p + "gate.scales"], t[p + "gate.biases"], H),
-               sh_gate_w=dequant_small(t[p + "shared_expert_gate.weight"], t[p + "shared_expert_gate.scales"],
+               sh_gate_vec=dequant_small(t[p + "shared_expert_gate.weight"], t[p + "shared_expert_gate.scales"],
                                        t[p + "shared_expert_gate.biases"], H).reshape(H))
     for name, key, rows in (("gate", "switch_mlp.gate_proj", E * I), ("up", "switch_mlp.up_proj", E * I),
                             ("down", "switch_mlp.down_proj", E * H),

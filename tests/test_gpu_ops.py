@@ -61,7 +61,7 @@ def test_route_bit_exact(gpu, E, K, rows):
     got_w = wb.read(np.float32, (rows, K))
     assert np.array_equal(got_i, idx), "route ids differ from the oracle"
     assert np.array_equal(got_w.view(np.uint32), w.view(np.uint32)), "route weights not bit-exact"
-    assert list(got_i[0, :3]) == [3, 5, 7]
+    assert list(got_i[0, :3]) == [3, 5, 7][:min(K, 3)]
     assert list(got_i[1 % rows, :K]) == list(range(K))
 
 
@@ -233,7 +233,7 @@ def skewed_idx(pairs, E, seed):
     (tests/test_sparse.c:996-1003)."""
     r = synth.raw64(seed, "skew", pairs)
     a = (r >> np.uint64(16)) % np.uint64(5)
-    b = (r >> np.uint64(8)) % np.uint64(E - 16)
+    b = (r >> np.uint64(8)) % np.uint64(max(E - 16, 1))
     return np.where(a < 2, 0, b).astype(np.int32)
 
 

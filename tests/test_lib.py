@@ -1,0 +1,71 @@
+"""The C-ABI library without a GPU: it loads, exports every function that
+include/qwasar_gpu.h declares, and honours the reference's host-side
+conventions (NULL command -> nothing encoded; bool ops' shape answers)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qwasar_gpu.h")
+
+
+def declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    names = set()
+    for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b(qw_\w+)\s*\(", src, flags=re.M):
+        line = src[m.start():src.index("\n", m.start())]
+        if "static inline" in line or line.lstrip().startswith("typedef"):
+            continue
+        names.add(m.group(1))
+    return sorted(names)
+
+
+def test_header_declares_the_moe_boundary():
+    names = declared()
+    for n in ("qw_gpu_init", "qw_buf_alloc", "qw_cmd_begin", "qw_op_moe_route", "qw_op_qmv_q4_bank",
+              "qw_op_qmv_q4_bank2", "qw_op_qmv_q4_swiglu", "qw_op_moe_group", "qw_op_qmm_q4_gather",
+              "qw_op_moe_combine_shared", "qw_op_dmat_bf16", "qw_op_qmat_q4", "qw_op_moe_layer"):
+        assert n in names
+
+
+def test_library_exports_every_declared_function():
+    from qwasar_amd import gpu
+    lib = C.CDLL(gpu.LIB_PATH)
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_null_command_encodes_nothing():
+    from qwasar_amd import gpu
+    r = gpu.NULL_REF
+    # void ops return at once with no command (reference QW_BEGIN, qwasar_metal.m:1606-1611)
+    gpu.qw_op_swiglu(None, r, r, r, 10)
+    gpu.qw_op_qmv_q4_bank(None, r, r, r, r, r, r, 64, 8, 1, 1, False, 64)
+    gpu.qw_op_moe_group(None, r, r, r, r, 4, 4)
+    # bool ops still answer whether the shape applies
+    assert not gpu.qw_op_qmv_q4_bank2(None, r, r, r, r, r, r, r, r, r, 1024, 8, 1, 1, 64)
+    assert gpu.qw_op_qmv_q4_bank2(None, r, r, r, r, r, r, r, r, r, 2048, 8, 1, 1, 64)
+    assert not gpu.qw_op_qmv_q4_multi(None, r, 2048, 64, 5, None)
+    assert gpu.qw_op_qmv_q4_multi(None, r, 2048, 64, 2, None)
+
+
+def test_tile_bounds():
+    from qwasar_amd import gpu
+    from oracle import ref
+    for pairs, E in ((5120, 512), (20480, 512), (10, 16), (80, 512)):
+        bm = gpu.qw_moe_tile_rows(pairs, E)
+        assert bm in (16, 32, 64)
+        assert ref.max_tiles(pairs, E, bm) <= gpu.qw_moe_max_tiles(pairs, E)
+    assert gpu.qw_moe_tile_rows(20480, 512) == 64
+    assert gpu.qw_moe_tile_rows(5120, 512) == 16
+
+
+def test_init_reports_a_missing_gpu():
+    from qwasar_amd import gpu
+    err = C.create_string_buffer(256)
+    if gpu.qw_gpu_init(err, 256):
+        pytest.skip("a gfx950 GPU is present")
+    assert err.value
