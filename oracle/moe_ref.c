@@ -116,7 +116,8 @@ void qr_dmat_bf16(float *y, const float *x, const uint16_t *w, int32_t k, int32_
 }
 
 /* The tree sum of the softmax: 64 lane sums, serial within a lane over
- * e = l, l+64, ..., then an xor butterfly over the lanes. */
+ * e = l, l+64, ..., then an xor butterfly over the lanes with ascending
+ * offsets 1, 2, 4, 8, 16, 32 (adjacent pairs first). */
 static float tree_sum(const float *v, int32_t n) {
     float lane[QR_SUM_LANES];
     for (int32_t l = 0; l < QR_SUM_LANES; l++) {
@@ -124,7 +125,7 @@ static float tree_sum(const float *v, int32_t n) {
         for (int32_t e = l; e < n; e += QR_SUM_LANES) s = s + v[e];
         lane[l] = s;
     }
-    for (int32_t off = QR_SUM_LANES / 2; off >= 1; off >>= 1) {
+    for (int32_t off = 1; off < QR_SUM_LANES; off <<= 1) {
         float nxt[QR_SUM_LANES];
         for (int32_t l = 0; l < QR_SUM_LANES; l++) nxt[l] = lane[l] + lane[l ^ off];
         memcpy(lane, nxt, sizeof lane);

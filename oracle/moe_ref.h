@@ -47,7 +47,8 @@ extern "C" {
  * fmaf-chain partials of consecutive 64-element chunks. */
 #define QR_ROUTER_CHUNK 64
 /* Lanes of the softmax sum's tree: lane l sums e = l, l+64, ... serially,
- * then the 64 lane sums meet in an xor butterfly (offsets 32 .. 1). */
+ * then the 64 lane sums meet in an xor butterfly with ascending offsets
+ * 1, 2, 4, 8, 16, 32. */
 #define QR_SUM_LANES 64
 
 float qr_bf16_to_f32(uint16_t v);

@@ -1,37 +1,30 @@
-// qw_decode.hip -- the MoE block at decode (1..8 tokens) in three launches.
+// qw_decode.hip -- the MoE block at decode (1..8 tokens) in three launches,
+// with no communication between workgroups inside a launch.
 //
-//   front   router logits (order R) for every expert, the shared expert's
-//           gate and up rows, and its gate logit; the last workgroup to
-//           finish routes every token (softmax, top-K, renormalise), writes
-//           idx/w, and lists the union of the selected experts with the
-//           (token, slot) pairs that use each one
-//   experts gate and up rows of each selected expert -- each weight byte read
-//           once and applied to every token routed to that expert -- and
-//           the shared expert's down projection, SwiGLU on load
-//   down    each selected expert's down projection, SwiGLU on load, into
-//           per-pair rows; the last workgroup to finish a block of output
-//           rows combines it: shared * sigmoid(gate) + sum_k w_k * y_k,
-//           an fma chain in slot order (deterministic whatever the arrival
-//           order)
+//   front    router logits (order R) for every expert and the shared
+//            expert's gate logit; the shared expert's gate and up rows, a
+//            wave taking the same rows of both, and its SwiGLU activation
+//   experts  every workgroup first routes every token itself from the
+//            logits (softmax, top-K, renormalise: cheap, and it saves a
+//            launch and any cross-workgroup handoff) and lists the union of
+//            the selected experts; then the gate and up rows of one selected
+//            expert for every token routed to it -- each weight byte read
+//            once -- and their SwiGLU activation; workgroup 0 writes idx / w
+//   down     per (block of output rows, token): the down rows of the shared
+//            expert and of each of the token's K experts, and the combine in
+//            registers: sigmoid(g) * shared + sum_k w_k * y_k, an fma chain
+//            in slot order
 //
-// "Last to finish" is an agent-scope acq_rel atomic on a counter that the
-// finishing workgroup resets, so the counters are zero between calls.
+// A lane issues all its weight loads for a matrix (or a batch of matrices)
+// before its first multiply, so each wave keeps those reads in flight at once.
 #include "qw_device.h"
 #include "qw_kernels.h"
 
-#define QD_WAVES 4
-#define QD_THREADS (QD_WAVES * 64)
-#define QD_RIT 4
 #define QD_MAXT QWK_DECODE_MAX_ROWS
-#define QD_MAXCH (QWK_DMAT_MAX_K / 64)
 #define QD_MAXU (QWK_DECODE_MAX_ROWS * QWK_ROUTE_MAX_K)
-
-struct QdLayout {
-    size_t logits, g1, shgu, shout, uinfo, gu, ey, total;
-    int nrb;        // down row blocks
-};
-
-static __host__ __device__ size_t al(size_t n) { return (n + 255) & ~(size_t)255; }
+#define QD_MAXCH (QWK_DMAT_MAX_K / 64)
+#define QD_WAVES 4
+#define QD_DOWN_WAVES 2
 
 static __host__ __device__ int qd_lpr(int k)
 {
@@ -41,21 +34,24 @@ static __host__ __device__ int qd_lpr(int k)
     return l;
 }
 
-static __host__ __device__ int qd_rows_per_wg(int k) { return QD_WAVES * (64 / qd_lpr(k)) * QD_RIT; }
+static int qd_splmax(int spl) { return spl <= 4 ? spl : 8; }
+// Row slots a lane carries per matrix: fewer as segments per lane grow.
+static __host__ __device__ constexpr int qd_rit(int splmax) { return splmax <= 2 ? 2 : 1; }
+
+struct QdLayout {
+    size_t logits, g1, shact, act, total;
+};
+
+static size_t al(size_t n) { return (n + 255) & ~(size_t)255; }
 
 static QdLayout qd_layout(const qwk_moe *M, int rows)
 {
     QdLayout L;
-    const int umax = rows * M->K < M->E ? rows * M->K : M->E;
-    L.nrb = (M->H + qd_rows_per_wg(M->I) - 1) / qd_rows_per_wg(M->I);
     size_t o = 0;
     L.logits = o; o += al((size_t)rows * M->E * 4);
     L.g1 = o;     o += al((size_t)rows * 4);
-    L.shgu = o;   o += al((size_t)rows * 2 * M->SI * 4);
-    L.shout = o;  o += al((size_t)rows * M->H * 4);
-    L.uinfo = o;  o += al((size_t)(1 + 2 * umax + umax * rows) * 4);
-    L.gu = o;     o += al((size_t)rows * M->K * 2 * M->I * 4);
-    L.ey = o;     o += al((size_t)rows * M->K * M->H * 4);
+    L.shact = o;  o += al((size_t)rows * M->SI * 4);
+    L.act = o;    o += al((size_t)rows * M->K * M->I * 4);
     L.total = o;
     return L;
 }
@@ -66,57 +62,59 @@ struct QdArgs {
     float *out;
     int32_t *idx;
     float *w;
-    int rows, umax, nrb;
-    int n_router_wg, n_shared_wg;       // front
-    int n_gu_wg_per_u, n_shdown_wg;     // experts
-    int *ctr;
-    float *logits, *g1, *shgu, *shout, *gu, *ey;
-    int *uinfo;                          // [0] = U, [1..umax] experts, then counts, then pair lists
+    int rows, umax, lgG;
+    int n_router_wg, n_shared_wg;   // front
+    int gu_wg_per_u;                // experts
+    int down_rows_per_wg, n_down_rb;
+    float *logits, *g1, *shact, *act;
 };
 
-__device__ __forceinline__ int *qd_uexp(const QdArgs &a) { return a.uinfo + 1; }
-__device__ __forceinline__ int *qd_ucnt(const QdArgs &a) { return a.uinfo + 1 + a.umax; }
-__device__ __forceinline__ int *qd_upair(const QdArgs &a) { return a.uinfo + 1 + 2 * a.umax; }
-
-// Rows [row0, row0 + slots*RIT) of a quantised matrix (one wave) against up to
-// QD_MAXT input vectors: y_t[row] = W[row] . in_t, in_t = x_t or
-// silu(x_t) * u_t.  Weights are loaded once per segment and reused for every
-// token.
-template <int G, int LPR, bool SWIGLU>
-__device__ __forceinline__ void qd_rows(const uint32_t *__restrict__ wm, const uint16_t *__restrict__ sm,
-                                        const uint16_t *__restrict__ bm, int n, int k, int row0, int nt,
-                                        const float *const *xp, const float *const *up, float *const *yp)
+// ---- gate and up rows with SwiGLU -----------------------------------------------
+//
+// Rows row0 + slot + SLOTS*i (i < RIT) of a gate matrix and the same rows of
+// an up matrix (k inputs, LPR lanes to a row) against up to QD_MAXT inputs
+// xp[t]: yp[t][row] = silu(gate . x_t) * (up . x_t).  A row's k/32 segments of
+// 16 bytes go to its lanes round-robin; segment s lies in group (32 s) >> lgG.
+template <int LPR, int SPLMAX, int RIT>
+__device__ __forceinline__ void qd_glu_rows(const qwk_q4 gm, const qwk_q4 um, int n, int k, int lgG, int row0,
+                                            int nt, const float *const *xp, float *const *yp)
 {
     constexpr int SLOTS = 64 / LPR;
     const int lane = threadIdx.x & 63, slot = lane / LPR, lr = lane % LPR;
-    const int words = k / 8, groups = k / G;
-    float acc[QD_MAXT][QD_RIT];
-#pragma unroll
-    for (int t = 0; t < QD_MAXT; t++)
-#pragma unroll
-        for (int i = 0; i < QD_RIT; i++) acc[t][i] = 0.0f;
-
+    const int words = k / 8, groups = k >> lgG;
     const int spl = (k / 32) / LPR;
-    for (int j = 0; j < spl; j++) {
-        const int seg = j * LPR + lr, g = seg * 32 / G;
-        uint4 wv[QD_RIT];
-        float sc[QD_RIT], bi[QD_RIT];
+    uint4 wv[2][SPLMAX][RIT];
+    float sc[2][SPLMAX][RIT], bi[2][SPLMAX][RIT];
 #pragma unroll
-        for (int i = 0; i < QD_RIT; i++) {
-            const int row = row0 + slot + SLOTS * i;
-            if (row < n) {
-                wv[i] = *reinterpret_cast<const uint4 *>(wm + (size_t)row * words + seg * 4);
-                sc[i] = qw_bf16(sm[(size_t)row * groups + g]);
-                bi[i] = qw_bf16(bm[(size_t)row * groups + g]);
-            } else {
-                wv[i] = make_uint4(0, 0, 0, 0);
-                sc[i] = 0.0f;
-                bi[i] = 0.0f;
+    for (int z = 0; z < 2; z++) {
+        const qwk_q4 q = z ? um : gm;
+#pragma unroll
+        for (int j = 0; j < SPLMAX; j++) {
+            const int seg = j * LPR + lr, g = (seg * 32) >> lgG;
+#pragma unroll
+            for (int i = 0; i < RIT; i++) {
+                const int row = row0 + slot + SLOTS * i;
+                if (j < spl && row < n) {
+                    wv[z][j][i] = *reinterpret_cast<const uint4 *>(q.w + (size_t)row * words + seg * 4);
+                    sc[z][j][i] = qw_bf16(q.s[(size_t)row * groups + g]);
+                    bi[z][j][i] = qw_bf16(q.b[(size_t)row * groups + g]);
+                } else {
+                    wv[z][j][i] = make_uint4(0, 0, 0, 0);
+                    sc[z][j][i] = 0.0f;
+                    bi[z][j][i] = 0.0f;
+                }
             }
         }
+    }
+#pragma unroll 1
+    for (int t = 0; t < nt; t++) {
+        float acc[2][RIT];
 #pragma unroll
-        for (int t = 0; t < QD_MAXT; t++) {
-            if (t < nt) {
+        for (int i = 0; i < RIT; i++) acc[0][i] = acc[1][i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < SPLMAX; j++) {
+            if (j < spl) {
+                const int seg = j * LPR + lr;
                 float xs[32];
                 const float4 *xv = reinterpret_cast<const float4 *>(xp[t] + seg * 32);
 #pragma unroll
@@ -124,323 +122,316 @@ __device__ __forceinline__ void qd_rows(const uint32_t *__restrict__ wm, const u
                     const float4 v = xv[q];
                     xs[4 * q] = v.x; xs[4 * q + 1] = v.y; xs[4 * q + 2] = v.z; xs[4 * q + 3] = v.w;
                 }
-                if (SWIGLU) {
-                    const float4 *uv = reinterpret_cast<const float4 *>(up[t] + seg * 32);
-#pragma unroll
-                    for (int q = 0; q < 8; q++) {
-                        const float4 v = uv[q];
-                        xs[4 * q] = qw_silu(xs[4 * q]) * v.x;
-                        xs[4 * q + 1] = qw_silu(xs[4 * q + 1]) * v.y;
-                        xs[4 * q + 2] = qw_silu(xs[4 * q + 2]) * v.z;
-                        xs[4 * q + 3] = qw_silu(xs[4 * q + 3]) * v.w;
-                    }
-                }
                 float xsum = 0.0f;
 #pragma unroll
                 for (int q = 0; q < 32; q++) xsum += xs[q];
 #pragma unroll
-                for (int i = 0; i < QD_RIT; i++) {
-                    float d = qw_dot8_q(wv[i].x, xs, 0.0f);
-                    d = qw_dot8_q(wv[i].y, xs + 8, d);
-                    d = qw_dot8_q(wv[i].z, xs + 16, d);
-                    d = qw_dot8_q(wv[i].w, xs + 24, d);
-                    acc[t][i] = __builtin_fmaf(sc[i], d, acc[t][i]);
-                    acc[t][i] = __builtin_fmaf(bi[i], xsum, acc[t][i]);
+                for (int z = 0; z < 2; z++) {
+#pragma unroll
+                    for (int i = 0; i < RIT; i++) {
+                        float d = qw_dot8_q(wv[z][j][i].x, xs, 0.0f);
+                        d = qw_dot8_q(wv[z][j][i].y, xs + 8, d);
+                        d = qw_dot8_q(wv[z][j][i].z, xs + 16, d);
+                        d = qw_dot8_q(wv[z][j][i].w, xs + 24, d);
+                        acc[z][i] = __builtin_fmaf(sc[z][j][i], d, acc[z][i]);
+                        acc[z][i] = __builtin_fmaf(bi[z][j][i], xsum, acc[z][i]);
+                    }
                 }
             }
         }
-    }
 #pragma unroll
-    for (int t = 0; t < QD_MAXT; t++) {
-#pragma unroll
-        for (int i = 0; i < QD_RIT; i++) {
-            const float v = qw_xor_sum<LPR>(acc[t][i]);
+        for (int i = 0; i < RIT; i++) {
+            const float g = qw_xor_sum<LPR>(acc[0][i]);
+            const float u = qw_xor_sum<LPR>(acc[1][i]);
             const int row = row0 + slot + SLOTS * i;
-            if (t < nt && lr == 0 && row < n) yp[t][row] = v;
+            if (lr == 0 && row < n) yp[t][row] = qw_silu(g) * u;
         }
     }
 }
 
-template <int G, bool SWIGLU>
-__device__ __forceinline__ void qd_rows_k(int k, const uint32_t *wm, const uint16_t *sm, const uint16_t *bm,
-                                          int n, int row0, int nt, const float *const *xp,
-                                          const float *const *up, float *const *yp)
-{
-    switch (qd_lpr(k)) {
-    case 64: qd_rows<G, 64, SWIGLU>(wm, sm, bm, n, k, row0, nt, xp, up, yp); break;
-    case 32: qd_rows<G, 32, SWIGLU>(wm, sm, bm, n, k, row0, nt, xp, up, yp); break;
-    case 16: qd_rows<G, 16, SWIGLU>(wm, sm, bm, n, k, row0, nt, xp, up, yp); break;
-    case 8:  qd_rows<G, 8, SWIGLU>(wm, sm, bm, n, k, row0, nt, xp, up, yp); break;
-    case 4:  qd_rows<G, 4, SWIGLU>(wm, sm, bm, n, k, row0, nt, xp, up, yp); break;
-    case 2:  qd_rows<G, 2, SWIGLU>(wm, sm, bm, n, k, row0, nt, xp, up, yp); break;
-    default: qd_rows<G, 1, SWIGLU>(wm, sm, bm, n, k, row0, nt, xp, up, yp); break;
-    }
-}
+// ---- front: router logits and the shared expert's gate / up ----------------------
 
-// Order-R dot of one bf16 row with up to `nt` token rows; one wave.  Chunk
-// partials meet in `part` (this wave's slice) and lane t adds token t's.
+// Order-R dot of one bf16 row with nt token rows (one wave): lane l computes
+// the fmaf chains of chunks l, l+64, ...; the chunk partials are then added
+// left to right, read lane by lane with readlane, so every lane holds the
+// total.
 __device__ __forceinline__ void qd_router_row(const uint16_t *__restrict__ wr, const float *__restrict__ x,
-                                              int k, int nt, float (*part)[QD_MAXT], float *y, int ystride)
+                                              int k, int nt, float *y, int ystride)
 {
+    constexpr int CPL = QD_MAXCH / 64;      // chunks per lane at most
     const int lane = threadIdx.x & 63, nch = k / 64;
-    for (int c = lane; c < nch; c += 64) {
-        float p[QD_MAXT];
+#pragma unroll 1
+    for (int t = 0; t < nt; t++) {
+        float p[CPL];
 #pragma unroll
-        for (int t = 0; t < QD_MAXT; t++) p[t] = 0.0f;
-        const uint4 *wv = reinterpret_cast<const uint4 *>(wr + c * 64);
-        for (int q = 0; q < 8; q++) {
-            const uint4 ww = wv[q];
-            const uint32_t wd[4] = {ww.x, ww.y, ww.z, ww.w};
-            float wf[8];
+        for (int j = 0; j < CPL; j++) {
+            const int c = lane + 64 * j;
+            float s = 0.0f;
+            if (c < nch) {
+                const uint4 *wp = reinterpret_cast<const uint4 *>(wr + c * 64);
+                const float4 *xv = reinterpret_cast<const float4 *>(x + (size_t)t * k + c * 64);
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                wf[2 * j] = __uint_as_float(wd[j] << 16);
-                wf[2 * j + 1] = __uint_as_float(wd[j] & 0xFFFF0000u);
-            }
-#pragma unroll
-            for (int t = 0; t < QD_MAXT; t++) {
-                if (t < nt) {
-                    const float4 *xv = reinterpret_cast<const float4 *>(x + (size_t)t * k + c * 64 + q * 8);
-                    const float4 a = xv[0], b = xv[1];
-                    float s = p[t];
-                    s = __builtin_fmaf(wf[0], a.x, s);
-                    s = __builtin_fmaf(wf[1], a.y, s);
-                    s = __builtin_fmaf(wf[2], a.z, s);
-                    s = __builtin_fmaf(wf[3], a.w, s);
-                    s = __builtin_fmaf(wf[4], b.x, s);
-                    s = __builtin_fmaf(wf[5], b.y, s);
-                    s = __builtin_fmaf(wf[6], b.z, s);
-                    s = __builtin_fmaf(wf[7], b.w, s);
-                    p[t] = s;
+                for (int q = 0; q < 8; q++) {
+                    const uint4 w = wp[q];
+                    const float4 a = xv[2 * q], b = xv[2 * q + 1];
+                    s = __builtin_fmaf(__uint_as_float(w.x << 16), a.x, s);
+                    s = __builtin_fmaf(__uint_as_float(w.x & 0xFFFF0000u), a.y, s);
+                    s = __builtin_fmaf(__uint_as_float(w.y << 16), a.z, s);
+                    s = __builtin_fmaf(__uint_as_float(w.y & 0xFFFF0000u), a.w, s);
+                    s = __builtin_fmaf(__uint_as_float(w.z << 16), b.x, s);
+                    s = __builtin_fmaf(__uint_as_float(w.z & 0xFFFF0000u), b.y, s);
+                    s = __builtin_fmaf(__uint_as_float(w.w << 16), b.z, s);
+                    s = __builtin_fmaf(__uint_as_float(w.w & 0xFFFF0000u), b.w, s);
                 }
             }
+            p[j] = s;
         }
+        float total = qw_lane(p[0], 0);
 #pragma unroll
-        for (int t = 0; t < QD_MAXT; t++) part[c][t] = p[t];
+        for (int j = 0; j < CPL; j++)
+            for (int l = j == 0 ? 1 : 0; l < 64 && 64 * j + l < nch; l++) total = total + qw_lane(p[j], l);
+        if (lane == 0) y[(size_t)t * ystride] = total;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    if (lane < nt) {
-        float total = part[0][lane];
-        for (int c = 1; c < nch; c++) total = total + part[c][lane];
-        y[(size_t)lane * ystride] = total;
-    }
-    __builtin_amdgcn_wave_barrier();
 }
 
-// Returns true in every thread of the workgroup that arrived last at *ctr
-// (of `expect`); that workgroup also resets the counter.
-__device__ __forceinline__ bool qd_last_arrival(int *ctr, int expect)
+template <int LPR, int SPLMAX>
+__global__ __launch_bounds__(QD_WAVES * 64) void k_decode_front(QdArgs a)
 {
-    __shared__ int last;
-    // Every wave publishes its own stores at agent scope before the count.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int old = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last = old == expect - 1;
-        if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    return last;
-}
-
-// Route every token (one wave per token), then list the union of selected
-// experts, ascending, and for each the pairs t*K + k that use it, in pair
-// order.
-__device__ void qd_route_all(const QdArgs &a)
-{
-    __shared__ int picks[QD_MAXU];
-    __shared__ int mark[QWK_ROUTE_MAX_E];
-    __shared__ int upos[QWK_ROUTE_MAX_E];
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    const int E = a.m.E, K = a.m.K;
-    for (int e = t; e < E; e += QD_THREADS) mark[e] = 0;
-    for (int r = wave; r < a.rows; r += QD_WAVES) {
-        // The same wave routine as the standalone route kernel.
-        float v[QWK_ROUTE_MAX_E / 64];
-        const float *l = a.logits + (size_t)r * E;
-        float m = -__builtin_huge_valf();
-#pragma unroll
-        for (int j = 0; j < QWK_ROUTE_MAX_E / 64; j++) {
-            const int e = lane + 64 * j;
-            v[j] = e < E ? l[e] : -__builtin_huge_valf();
-            m = fmaxf(m, v[j]);
-        }
-        m = qw_wave_max(m);
-        float s = 0.0f;
-#pragma unroll
-        for (int j = 0; j < QWK_ROUTE_MAX_E / 64; j++) {
-            const int e = lane + 64 * j;
-            if (e < E) { v[j] = qw_exp_spec(v[j] - m); s = s + v[j]; }
-        }
-        s = qw_xor_sum<64>(s);
-#pragma unroll
-        for (int j = 0; j < QWK_ROUTE_MAX_E / 64; j++) {
-            const int e = lane + 64 * j;
-            v[j] = e < E ? v[j] / s : -2.0f;
-        }
-        float mine_w = 0.0f;
-        int mine_i = 0;
-        for (int n = 0; n < K; n++) {
-            float bv = -2.0f;
-            int bi = 0x7fffffff;
-#pragma unroll
-            for (int j = 0; j < QWK_ROUTE_MAX_E / 64; j++)
-                if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
-            qw_wave_argmax(bv, bi);
-#pragma unroll
-            for (int j = 0; j < QWK_ROUTE_MAX_E / 64; j++)
-                if (lane + 64 * j == bi) v[j] = -1.0f;
-            if (lane == n) { mine_w = bv; mine_i = bi; }
-        }
-        float wsum = 0.0f;
-        for (int n = 0; n < K; n++) wsum = wsum + __shfl(mine_w, n, 64);
-        if (lane < K) {
-            a.idx[(size_t)r * K + lane] = mine_i;
-            a.w[(size_t)r * K + lane] = a.m.norm ? mine_w / wsum : mine_w;
-            picks[r * K + lane] = mine_i;
-        }
-    }
-    __syncthreads();
-    const int npk = a.rows * K;
-    for (int p = t; p < npk; p += QD_THREADS) mark[picks[p]] = 1;
-    __syncthreads();
-    if (t == 0) {
-        int u = 0;
-        for (int e = 0; e < E; e++) {
-            if (mark[e]) { upos[e] = u; qd_uexp(a)[u] = e; qd_ucnt(a)[u] = 0; u++; }
-        }
-        for (int p = 0; p < npk; p++) {
-            const int uu = upos[picks[p]];
-            qd_upair(a)[uu * a.rows + qd_ucnt(a)[uu]++] = p;
-        }
-        a.uinfo[0] = u;
-    }
-    __syncthreads();
-}
-
-template <int G>
-__global__ __launch_bounds__(QD_THREADS) void k_decode_front(QdArgs a)
-{
-    __shared__ float part[QD_WAVES][QD_MAXCH][QD_MAXT];
     __shared__ const float *xp[QD_MAXT];
     __shared__ float *yp[QD_MAXT];
     const int wave = threadIdx.x >> 6, b = blockIdx.x;
     const int H = a.m.H, E = a.m.E, SI = a.m.SI;
     if (b < a.n_router_wg) {
-        // Router rows, plus the shared gate logit as row E.
         const int o = b * QD_WAVES + wave;
         if (o < E)
-            qd_router_row(a.m.router + (size_t)o * H, a.x, H, a.rows, part[wave], a.logits + o, E);
+            qd_router_row(a.m.router + (size_t)o * H, a.x, H, a.rows, a.logits + o, E);
         else if (o == E)
-            qd_router_row(a.m.sh_gate_w, a.x, H, a.rows, part[wave], a.g1, 1);
-    } else {
-        // Shared gate (z = 0) and up (z = 1) rows.
-        const int sb = b - a.n_router_wg;
-        const int half = a.n_shared_wg / 2;
-        const int z = sb >= half ? 1 : 0;
-        const int row0 = ((sb - z * half) * QD_WAVES + wave) * (qd_rows_per_wg(H) / QD_WAVES);
-        if (threadIdx.x < QD_MAXT) {
-            const int t = threadIdx.x;
-            xp[t] = a.x + (size_t)min(t, a.rows - 1) * H;
-            yp[t] = a.shgu + ((size_t)min(t, a.rows - 1) * 2 + z) * SI;
-        }
-        __syncthreads();
-        const qwk_q4 q = z ? a.m.sh_up : a.m.sh_gate;
-        if (row0 < SI) qd_rows_k<G, false>(H, q.w, q.s, q.b, SI, row0, a.rows, xp, nullptr, yp);
+            qd_router_row(a.m.sh_gate_w, a.x, H, a.rows, a.g1, 1);
+        return;
     }
-    if (qd_last_arrival(a.ctr, gridDim.x)) qd_route_all(a);
+    constexpr int RIT = qd_rit(SPLMAX);
+    constexpr int RPW = (64 / LPR) * RIT;
+    const int row0 = ((b - a.n_router_wg) * QD_WAVES + wave) * RPW;
+    if (threadIdx.x < QD_MAXT) {
+        const int t = min((int)threadIdx.x, a.rows - 1);
+        xp[threadIdx.x] = a.x + (size_t)t * H;
+        yp[threadIdx.x] = a.shact + (size_t)t * SI;
+    }
+    __syncthreads();
+    if (row0 < SI)
+        qd_glu_rows<LPR, SPLMAX, RIT>(a.m.sh_gate, a.m.sh_up, SI, H, a.lgG, row0, a.rows, xp, yp);
 }
 
-template <int G>
-__global__ __launch_bounds__(QD_THREADS) void k_decode_experts(QdArgs a)
+// ---- experts: routing in the prologue, then gate / up of one selected expert ----
+
+struct QdRoute {
+    int U;
+    int picks[QD_MAXU];
+    float pw[QD_MAXU];
+    int uexp[QD_MAXU];
+    int ucnt[QD_MAXU];
+    int ustart[QD_MAXU];
+    int upair[QD_MAXU];       // pairs grouped by unique expert, ascending pair index
+    int mark[QWK_ROUTE_MAX_E];
+};
+
+// Routes every token (a wave per token) with the arithmetic of the
+// standalone route kernel, then builds the union of selected experts with,
+// for each, its pairs in ascending order.  One token's picks are distinct, so
+// for one token the union is the picks themselves, in pick order.
+template <int PL>
+__device__ void qd_route_all(const QdArgs &a, QdRoute &R)
 {
-    __shared__ const float *xp[QD_MAXT];
-    __shared__ const float *upp[QD_MAXT];
-    __shared__ float *yp[QD_MAXT];
-    const int wave = threadIdx.x >> 6, b = blockIdx.x;
-    const int H = a.m.H, I = a.m.I, SI = a.m.SI, K = a.m.K;
-    const int ngu = a.umax * a.n_gu_wg_per_u;
-    if (b < ngu) {
-        const int u = b / a.n_gu_wg_per_u, rb = b % a.n_gu_wg_per_u;
-        if (u >= min(a.uinfo[0], a.umax)) return;
-        const int e = qd_uexp(a)[u], nt = min(qd_ucnt(a)[u], a.rows);
-        if (e < 0 || e >= a.m.E || nt < 1) return;
-        // Split banks: z = gate / up, each I rows; fused: one bank of 2I rows.
-        const int nz = a.m.split ? 2 : 1, nrow = a.m.split ? I : 2 * I;
-        const int per_z = a.n_gu_wg_per_u / nz;
-        const int z = rb / per_z;
-        const int row0 = ((rb % per_z) * QD_WAVES + wave) * (qd_rows_per_wg(H) / QD_WAVES);
-        if (threadIdx.x < QD_MAXT) {
-            const int t = threadIdx.x;
-            const int p = min(max(qd_upair(a)[u * a.rows + min(t, nt - 1)], 0), a.rows * K - 1);
-            xp[t] = a.x + (size_t)(p / K) * H;
-            yp[t] = a.gu + (size_t)p * 2 * I + z * I;
+    const int t = threadIdx.x, nthr = blockDim.x, wave = t >> 6, lane = t & 63, nw = nthr >> 6;
+    const int E = a.m.E, K = a.m.K;
+    for (int r = wave; r < a.rows; r += nw) {
+        int pi;
+        float pw;
+        qw_route_wave<PL>(a.logits + (size_t)r * E, E, K, a.m.norm, lane, &pi, &pw);
+        if (lane < K) {
+            R.picks[r * K + lane] = pi;
+            R.pw[r * K + lane] = pw;
         }
-        __syncthreads();
-        const qwk_q4 q = a.m.split ? (z ? a.m.up : a.m.gate) : a.m.gate_up;
-        const size_t words = H / 8, groups = H / G;
-        if (row0 < nrow)
-            qd_rows_k<G, false>(H, q.w + (size_t)e * nrow * words, q.s + (size_t)e * nrow * groups,
-                                q.b + (size_t)e * nrow * groups, nrow, row0, nt, xp, nullptr, yp);
-    } else {
-        // The shared expert's down projection, SwiGLU on load.
-        const int rb = b - ngu;
-        const int row0 = (rb * QD_WAVES + wave) * (qd_rows_per_wg(SI) / QD_WAVES);
-        if (threadIdx.x < QD_MAXT) {
-            const int t = min((int)threadIdx.x, a.rows - 1);
-            xp[threadIdx.x] = a.shgu + (size_t)t * 2 * SI;
-            upp[threadIdx.x] = a.shgu + (size_t)t * 2 * SI + SI;
-            yp[threadIdx.x] = a.shout + (size_t)t * H;
-        }
-        __syncthreads();
-        if (row0 < H)
-            qd_rows_k<G, true>(SI, a.m.sh_down.w, a.m.sh_down.s, a.m.sh_down.b, H, row0, a.rows, xp, upp, yp);
     }
+    __syncthreads();
+    if (a.rows == 1) {
+        if (t < K) {
+            R.uexp[t] = R.picks[t];
+            R.ucnt[t] = 1;
+            R.ustart[t] = t;
+            R.upair[t] = t;
+        }
+        if (t == 0) R.U = K;
+        __syncthreads();
+        return;
+    }
+    for (int e = t; e < E; e += nthr) R.mark[e] = 0;
+    __syncthreads();
+    const int npk = a.rows * K;
+    for (int p = t; p < npk; p += nthr) R.mark[R.picks[p]] = 1;
+    __syncthreads();
+    // Compact the marked experts in ascending order, 64 at a time with ballots.
+    if (wave == 0) {
+        int base = 0;
+        for (int e0 = 0; e0 < E; e0 += 64) {
+            const int e = e0 + lane;
+            const bool on = e < E && R.mark[e];
+            const unsigned long long bal = __ballot(on);
+            if (on) R.uexp[base + __popcll(bal & ((1ull << lane) - 1ull))] = e;
+            base += __popcll(bal);
+        }
+        if (lane == 0) R.U = base;
+    }
+    __syncthreads();
+    for (int u = t; u < R.U; u += nthr) {
+        const int e = R.uexp[u];
+        int c = 0;
+        for (int p = 0; p < npk; p++) c += R.picks[p] == e;
+        R.ucnt[u] = c;
+    }
+    __syncthreads();
+    if (t == 0) {
+        int s = 0;
+        for (int u = 0; u < R.U; u++) { R.ustart[u] = s; s += R.ucnt[u]; }
+    }
+    __syncthreads();
+    for (int u = t; u < R.U; u += nthr) {
+        const int e = R.uexp[u];
+        int c = R.ustart[u];
+        for (int p = 0; p < npk; p++)
+            if (R.picks[p] == e) R.upair[c++] = p;
+    }
+    __syncthreads();
 }
 
-template <int G>
-__global__ __launch_bounds__(QD_THREADS) void k_decode_down(QdArgs a)
+template <int LPR, int SPLMAX, int PL>
+__global__ __launch_bounds__(QD_WAVES * 64) void k_decode_experts(QdArgs a)
 {
+    __shared__ QdRoute R;
     __shared__ const float *xp[QD_MAXT];
-    __shared__ const float *upp[QD_MAXT];
     __shared__ float *yp[QD_MAXT];
     const int wave = threadIdx.x >> 6, b = blockIdx.x;
     const int H = a.m.H, I = a.m.I, K = a.m.K;
-    const int u = b / a.nrb, rb = b % a.nrb;
-    const int U = min(a.uinfo[0], a.umax);
-    if (u >= U) return;
-    const int e = qd_uexp(a)[u], nt = min(qd_ucnt(a)[u], a.rows);
-    const bool ok = e >= 0 && e < a.m.E && nt >= 1;
-    const int rpw = qd_rows_per_wg(I);
-    const int row0 = rb * rpw + wave * (rpw / QD_WAVES);
+    const int u = b / a.gu_wg_per_u, rb = b % a.gu_wg_per_u;
+    qd_route_all<PL>(a, R);
+    if (b == 0)
+        for (int p = threadIdx.x; p < a.rows * K; p += blockDim.x) {
+            a.idx[p] = R.picks[p];
+            a.w[p] = R.pw[p];
+        }
+    if (u >= R.U) return;
+    const int e = R.uexp[u], nt = R.ucnt[u], p0 = R.ustart[u];
+    constexpr int RIT = qd_rit(SPLMAX);
+    constexpr int RPW = (64 / LPR) * RIT;
+    const int row0 = (rb * QD_WAVES + wave) * RPW;
     if (threadIdx.x < QD_MAXT) {
         const int t = threadIdx.x;
-        const int p = ok ? min(max(qd_upair(a)[u * a.rows + min(t, nt - 1)], 0), a.rows * K - 1) : 0;
-        xp[t] = a.gu + (size_t)p * 2 * I;
-        upp[t] = a.gu + (size_t)p * 2 * I + I;
-        yp[t] = a.ey + (size_t)p * H;
+        const int p = R.upair[p0 + min(t, nt - 1)];
+        xp[t] = a.x + (size_t)(p / K) * H;
+        yp[t] = a.act + (size_t)p * I;
     }
     __syncthreads();
-    const size_t words = I / 8, groups = I / G;
-    if (ok && row0 < H)
-        qd_rows_k<G, true>(I, a.m.down.w + (size_t)e * H * words, a.m.down.s + (size_t)e * H * groups,
-                           a.m.down.b + (size_t)e * H * groups, H, row0, nt, xp, upp, yp);
-    if (qd_last_arrival(a.ctr + 4 + rb, U)) {
-        // Combine this block of output rows for every token.
-        const int h0 = rb * rpw, h1 = min(H, h0 + rpw);
-        const int span = h1 - h0;
-        for (int i = threadIdx.x; i < a.rows * span; i += QD_THREADS) {
-            const int t = i / span, h = h0 + i % span;
-            float acc = a.shout[(size_t)t * H + h] * qw_sigmoid(a.g1[t]);
-            for (int k = 0; k < K; k++)
-                acc = __builtin_fmaf(a.w[(size_t)t * K + k], a.ey[((size_t)t * K + k) * H + h], acc);
-            a.out[(size_t)t * H + h] = acc;
+    // Split banks: gate and up [E, I, H]; fused: gate_up [E, 2I, H], gate rows
+    // first, so up row r of expert e is row I + r of its slice.
+    const size_t words = H / 8, groups = H >> a.lgG;
+    qwk_q4 gm, um;
+    if (a.m.split) {
+        const size_t off = (size_t)e * I;
+        gm = {a.m.gate.w + off * words, a.m.gate.s + off * groups, a.m.gate.b + off * groups};
+        um = {a.m.up.w + off * words, a.m.up.s + off * groups, a.m.up.b + off * groups};
+    } else {
+        const size_t off = (size_t)e * 2 * I;
+        gm = {a.m.gate_up.w + off * words, a.m.gate_up.s + off * groups, a.m.gate_up.b + off * groups};
+        um = {gm.w + (size_t)I * words, gm.s + (size_t)I * groups, gm.b + (size_t)I * groups};
+    }
+    if (row0 < I) qd_glu_rows<LPR, SPLMAX, RIT>(gm, um, I, H, a.lgG, row0, nt, xp, yp);
+}
+
+// ---- down: the shared expert and every expert of a token, and the combine -------
+
+template <int LPR, int SPLMAX>
+__global__ __launch_bounds__(QD_DOWN_WAVES * 64) void k_decode_down(QdArgs a)
+{
+    const int H = a.m.H, I = a.m.I, SI = a.m.SI, K = a.m.K;
+    const int rb = blockIdx.x % a.n_down_rb, t = blockIdx.x / a.n_down_rb;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int SLOTS = 64 / LPR;
+    const int slot = lane / LPR, lr = lane % LPR;
+    const int row = rb * a.down_rows_per_wg + wave * SLOTS + slot;
+    const int lgG = a.lgG;
+    float acc = 0.0f;
+    // The shared expert first (the combine starts from its gated term), then
+    // the routed experts in slot order; NB matrices' weights are loaded per
+    // round before any of them is used.
+    constexpr int NB = SPLMAX >= 8 ? 1 : 8 / SPLMAX;
+    for (int k0 = -1; k0 < K; k0 += NB) {
+        uint4 wv[NB][SPLMAX];
+        float sc[NB][SPLMAX], bi[NB][SPLMAX];
+#pragma unroll
+        for (int kb = 0; kb < NB; kb++) {
+            const int k = k0 + kb;
+            const int kin = k < 0 ? SI : I;
+            const int words = kin / 8, groups = kin >> lgG, spl = (kin / 32) / LPR;
+            const uint32_t *wm = a.m.sh_down.w;
+            const uint16_t *sm = a.m.sh_down.s, *bm = a.m.sh_down.b;
+            if (k >= 0 && k < K) {
+                const size_t e = (size_t)a.idx[t * K + k];
+                wm = a.m.down.w + e * H * words;
+                sm = a.m.down.s + e * H * groups;
+                bm = a.m.down.b + e * H * groups;
+            }
+#pragma unroll
+            for (int j = 0; j < SPLMAX; j++) {
+                const int seg = j * LPR + lr, g = (seg * 32) >> lgG;
+                if (k < K && j < spl && row < H) {
+                    wv[kb][j] = *reinterpret_cast<const uint4 *>(wm + (size_t)row * words + seg * 4);
+                    sc[kb][j] = qw_bf16(sm[(size_t)row * groups + g]);
+                    bi[kb][j] = qw_bf16(bm[(size_t)row * groups + g]);
+                } else {
+                    wv[kb][j] = make_uint4(0, 0, 0, 0);
+                    sc[kb][j] = 0.0f;
+                    bi[kb][j] = 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int kb = 0; kb < NB; kb++) {
+            const int k = k0 + kb;
+            if (k >= K) break;
+            const int kin = k < 0 ? SI : I, spl = (kin / 32) / LPR;
+            const float *av = k < 0 ? a.shact + (size_t)t * SI : a.act + ((size_t)t * K + k) * I;
+            float y = 0.0f;
+#pragma unroll
+            for (int j = 0; j < SPLMAX; j++) {
+                if (j < spl) {
+                    const int seg = j * LPR + lr;
+                    float xs[32];
+                    const float4 *xv = reinterpret_cast<const float4 *>(av + seg * 32);
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {
+                        const float4 v = xv[q];
+                        xs[4 * q] = v.x; xs[4 * q + 1] = v.y; xs[4 * q + 2] = v.z; xs[4 * q + 3] = v.w;
+                    }
+                    float xsum = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 32; q++) xsum += xs[q];
+                    float d = qw_dot8_q(wv[kb][j].x, xs, 0.0f);
+                    d = qw_dot8_q(wv[kb][j].y, xs + 8, d);
+                    d = qw_dot8_q(wv[kb][j].z, xs + 16, d);
+                    d = qw_dot8_q(wv[kb][j].w, xs + 24, d);
+                    y = __builtin_fmaf(sc[kb][j], d, y);
+                    y = __builtin_fmaf(bi[kb][j], xsum, y);
+                }
+            }
+            y = qw_xor_sum<LPR>(y);
+            if (k < 0) acc = y * qw_sigmoid(a.g1[t]);
+            else acc = __builtin_fmaf(a.w[t * K + k], y, acc);
         }
     }
+    if (lr == 0 && row < H) a.out[(size_t)t * H + row] = acc;
 }
+
+// ---- host side -------------------------------------------------------------------
 
 extern "C" size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows)
 {
@@ -449,59 +440,117 @@ extern "C" size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows)
 
 extern "C" int qwk_moe_decode_counters(const qwk_moe *M)
 {
-    return 4 + qd_layout(M, 1).nrb;
+    (void)M;
+    return 0;
 }
 
-template <int G>
-static int qd_launch(hipStream_t s, QdArgs &a, hipEvent_t *ev)
+template <int LPR, int SPLMAX>
+static void launch_fe(hipStream_t s, QdArgs &a, hipEvent_t *ev)
 {
-    const dim3 blk(QD_THREADS);
     if (ev) (void)hipEventRecord(ev[0], s);
-    hipLaunchKernelGGL(k_decode_front<G>, dim3(a.n_router_wg + a.n_shared_wg), blk, 0, s, a);
+    hipLaunchKernelGGL((k_decode_front<LPR, SPLMAX>), dim3(a.n_router_wg + a.n_shared_wg),
+                       dim3(QD_WAVES * 64), 0, s, a);
     if (ev) (void)hipEventRecord(ev[1], s);
-    hipLaunchKernelGGL(k_decode_experts<G>, dim3(a.umax * a.n_gu_wg_per_u + a.n_shdown_wg), blk, 0, s, a);
+    const dim3 grid(a.umax * a.gu_wg_per_u), blk(QD_WAVES * 64);
+    if (a.m.E <= 256) hipLaunchKernelGGL((k_decode_experts<LPR, SPLMAX, 4>), grid, blk, 0, s, a);
+    else if (a.m.E <= 512) hipLaunchKernelGGL((k_decode_experts<LPR, SPLMAX, 8>), grid, blk, 0, s, a);
+    else hipLaunchKernelGGL((k_decode_experts<LPR, SPLMAX, 16>), grid, blk, 0, s, a);
     if (ev) (void)hipEventRecord(ev[2], s);
-    hipLaunchKernelGGL(k_decode_down<G>, dim3(a.umax * a.nrb), blk, 0, s, a);
-    if (ev) (void)hipEventRecord(ev[3], s);
-    return (int)hipGetLastError();
+}
+
+template <int LPR>
+static bool launch_fe_spl(int splmax, hipStream_t s, QdArgs &a, hipEvent_t *ev)
+{
+    switch (splmax) {
+    case 1: launch_fe<LPR, 1>(s, a, ev); return true;
+    case 2: launch_fe<LPR, 2>(s, a, ev); return true;
+    case 3: launch_fe<LPR, 3>(s, a, ev); return true;
+    case 4: launch_fe<LPR, 4>(s, a, ev); return true;
+    case 8: launch_fe<LPR, 8>(s, a, ev); return true;
+    default: return false;
+    }
+}
+
+template <int LPR, int SPLMAX>
+static void launch_down(hipStream_t s, QdArgs &a)
+{
+    hipLaunchKernelGGL((k_decode_down<LPR, SPLMAX>), dim3(a.rows * a.n_down_rb), dim3(QD_DOWN_WAVES * 64), 0, s, a);
+}
+
+template <int LPR>
+static bool launch_down_spl(int splmax, hipStream_t s, QdArgs &a)
+{
+    switch (splmax) {
+    case 1: launch_down<LPR, 1>(s, a); return true;
+    case 2: launch_down<LPR, 2>(s, a); return true;
+    case 3: launch_down<LPR, 3>(s, a); return true;
+    case 4: launch_down<LPR, 4>(s, a); return true;
+    case 8: launch_down<LPR, 8>(s, a); return true;
+    default: return false;
+    }
 }
 
 extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
                               const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes,
                               int *counters, int ncounters, hipEvent_t *ev)
 {
+    (void)counters; (void)ncounters;
+    const int G = M->group;
     if (rows < 1 || rows > QWK_DECODE_MAX_ROWS || M->K < 1 || M->K > QWK_ROUTE_MAX_K ||
         M->E < M->K || M->E > QWK_ROUTE_MAX_E || M->H % 64 || M->I % 32 || M->SI % 32 ||
-        M->H > QWK_DMAT_MAX_K || (M->group != 32 && M->group != 64 && M->group != 128) ||
-        M->H % M->group || M->I % M->group || M->SI % M->group)
+        M->H > QWK_DMAT_MAX_K || (G != 32 && G != 64 && G != 128) ||
+        M->H % G || M->I % G || M->SI % G || ((uintptr_t)x & 15u))
         return (int)hipErrorInvalidValue;
     const QdLayout L = qd_layout(M, rows);
-    if (scratch_bytes < L.total || ((uintptr_t)x & 15u) || ncounters < 4 + L.nrb)
+    if (scratch_bytes < L.total) return (int)hipErrorInvalidValue;
+    // Lanes per row: k = H for the front and expert launches; for down one
+    // width that divides the segment counts of both I and SI.
+    const int lpr_h = qd_lpr(M->H);
+    int lpr_d = qd_lpr(M->I);
+    const int lpr_si = qd_lpr(M->SI);
+    if (lpr_si < lpr_d) lpr_d = lpr_si;
+    const int kmax_d = M->I > M->SI ? M->I : M->SI;
+    if ((M->H / 32) / lpr_h > 8 || (kmax_d / 32) / lpr_d > 8 || lpr_h < 2 || lpr_d < 2)
         return (int)hipErrorInvalidValue;
+    const int spl_h = qd_splmax((M->H / 32) / lpr_h);
+    const int spl_d = qd_splmax((kmax_d / 32) / lpr_d);
+
     char *S = (char *)scratch;
     QdArgs a;
     a.m = *M;
     a.x = x; a.out = out; a.idx = idx; a.w = w; a.rows = rows;
     a.umax = rows * M->K < M->E ? rows * M->K : M->E;
-    a.nrb = L.nrb;
+    a.lgG = G == 32 ? 5 : G == 64 ? 6 : 7;
     a.n_router_wg = (M->E + 1 + QD_WAVES - 1) / QD_WAVES;
-    const int rpw_h = qd_rows_per_wg(M->H);
-    a.n_shared_wg = 2 * ((M->SI + rpw_h - 1) / rpw_h);
-    const int nz = M->split ? 2 : 1, nrow = M->split ? M->I : 2 * M->I;
-    a.n_gu_wg_per_u = nz * ((nrow + rpw_h - 1) / rpw_h);
-    const int rpw_si = qd_rows_per_wg(M->SI);
-    a.n_shdown_wg = (M->H + rpw_si - 1) / rpw_si;
-    a.ctr = counters;
+    const int rpg_h = QD_WAVES * (64 / lpr_h) * qd_rit(spl_h);
+    a.n_shared_wg = (M->SI + rpg_h - 1) / rpg_h;
+    a.gu_wg_per_u = (M->I + rpg_h - 1) / rpg_h;
+    a.down_rows_per_wg = QD_DOWN_WAVES * (64 / lpr_d);
+    a.n_down_rb = (M->H + a.down_rows_per_wg - 1) / a.down_rows_per_wg;
     a.logits = (float *)(S + L.logits);
     a.g1 = (float *)(S + L.g1);
-    a.shgu = (float *)(S + L.shgu);
-    a.shout = (float *)(S + L.shout);
-    a.uinfo = (int *)(S + L.uinfo);
-    a.gu = (float *)(S + L.gu);
-    a.ey = (float *)(S + L.ey);
-    switch (M->group) {
-    case 32: return qd_launch<32>(s, a, ev);
-    case 64: return qd_launch<64>(s, a, ev);
-    default: return qd_launch<128>(s, a, ev);
+    a.shact = (float *)(S + L.shact);
+    a.act = (float *)(S + L.act);
+
+    bool ok;
+    switch (lpr_h) {
+    case 2: ok = launch_fe_spl<2>(spl_h, s, a, ev); break;
+    case 4: ok = launch_fe_spl<4>(spl_h, s, a, ev); break;
+    case 8: ok = launch_fe_spl<8>(spl_h, s, a, ev); break;
+    case 16: ok = launch_fe_spl<16>(spl_h, s, a, ev); break;
+    case 32: ok = launch_fe_spl<32>(spl_h, s, a, ev); break;
+    default: ok = launch_fe_spl<64>(spl_h, s, a, ev); break;
     }
+    if (!ok) return (int)hipErrorInvalidValue;
+    switch (lpr_d) {
+    case 2: ok = launch_down_spl<2>(spl_d, s, a); break;
+    case 4: ok = launch_down_spl<4>(spl_d, s, a); break;
+    case 8: ok = launch_down_spl<8>(spl_d, s, a); break;
+    case 16: ok = launch_down_spl<16>(spl_d, s, a); break;
+    case 32: ok = launch_down_spl<32>(spl_d, s, a); break;
+    default: ok = launch_down_spl<64>(spl_d, s, a); break;
+    }
+    if (ev) (void)hipEventRecord(ev[3], s);
+    if (!ok) return (int)hipErrorInvalidValue;
+    return (int)hipGetLastError();
 }

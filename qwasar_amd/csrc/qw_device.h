@@ -40,35 +40,94 @@ __device__ __forceinline__ float qw_exp_spec(float x) {
 __device__ __forceinline__ float qw_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 __device__ __forceinline__ float qw_silu(float x) { return x * qw_sigmoid(x); }
 
-// Sum over a power-of-two run of `width` lanes with an xor butterfly; every
-// lane of the run ends with the same bits (fp32 add commutes).
+// ---- cross-lane steps ----------------------------------------------------------
+//
+// DPP moves run in the VALU at register latency; a shuffle (ds_bpermute)
+// round-trips through the LDS unit.  Reductions below use DPP within a row of
+// 16 lanes and readlane across the four rows.
+//
+// A butterfly step with offset 2^s pairs each lane with one in the partner
+// half of its 2^(s+1)-lane block.  After the steps below 2^s every lane of a
+// 2^s block holds the same value, so any such pairing gives the same bits as
+// the xor pairing: quad_perm for offsets 1 and 2, row_half_mirror (i <-> 7-i)
+// for 4, row_mirror (i <-> 15-i) for 8.
+
+template <int CTRL>
+__device__ __forceinline__ float qw_dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int qw_dpp_i(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+#define QW_DPP_XOR1 0xB1     // quad_perm [1,0,3,2]
+#define QW_DPP_XOR2 0x4E     // quad_perm [2,3,0,1]
+#define QW_DPP_HMIRROR 0x141 // row_half_mirror
+#define QW_DPP_MIRROR 0x140  // row_mirror
+
+__device__ __forceinline__ float qw_lane(float v, int l)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Sum over each aligned run of `width` lanes (a power of two); every lane of
+// a run ends with its run's sum.  For width 64 the tree is the xor butterfly
+// with ascending offsets 1, 2, 4, 8, 16, 32 -- the order routing is specified
+// in -- and every lane gets the same bits.
 template <int width>
-__device__ __forceinline__ float qw_xor_sum(float v) {
-#pragma unroll
-    for (int off = width / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, QW_WAVE);
+__device__ __forceinline__ float qw_xor_sum(float v)
+{
+    if (width >= 2) v = v + qw_dpp<QW_DPP_XOR1>(v);
+    if (width >= 4) v = v + qw_dpp<QW_DPP_XOR2>(v);
+    if (width >= 8) v = v + qw_dpp<QW_DPP_HMIRROR>(v);
+    if (width >= 16) v = v + qw_dpp<QW_DPP_MIRROR>(v);
+    if (width == 32) v = v + __shfl_xor(v, 16, 64);
+    if (width == 64) {
+        const float a = qw_lane(v, 0) + qw_lane(v, 16);
+        const float b = qw_lane(v, 32) + qw_lane(v, 48);
+        v = a + b;
+    }
     return v;
 }
 
-__device__ __forceinline__ float qw_wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, QW_WAVE));
-    return v;
+__device__ __forceinline__ float qw_wave_max(float v)
+{
+    v = fmaxf(v, qw_dpp<QW_DPP_XOR1>(v));
+    v = fmaxf(v, qw_dpp<QW_DPP_XOR2>(v));
+    v = fmaxf(v, qw_dpp<QW_DPP_HMIRROR>(v));
+    v = fmaxf(v, qw_dpp<QW_DPP_MIRROR>(v));
+    return fmaxf(fmaxf(qw_lane(v, 0), qw_lane(v, 16)), fmaxf(qw_lane(v, 32), qw_lane(v, 48)));
 }
 
 // Arg-max over the wave: highest value, ties to the lowest index.  The same
 // (value, index) lands in every lane.
-__device__ __forceinline__ void qw_wave_argmax(float &v, int &i) {
+__device__ __forceinline__ void qw_argmax_step(float &v, int &i, float ov, int oi)
+{
+    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+
+__device__ __forceinline__ void qw_wave_argmax(float &v, int &i)
+{
+    qw_argmax_step(v, i, qw_dpp<QW_DPP_XOR1>(v), qw_dpp_i<QW_DPP_XOR1>(i));
+    qw_argmax_step(v, i, qw_dpp<QW_DPP_XOR2>(v), qw_dpp_i<QW_DPP_XOR2>(i));
+    qw_argmax_step(v, i, qw_dpp<QW_DPP_HMIRROR>(v), qw_dpp_i<QW_DPP_HMIRROR>(i));
+    qw_argmax_step(v, i, qw_dpp<QW_DPP_MIRROR>(v), qw_dpp_i<QW_DPP_MIRROR>(i));
+    float bv = qw_lane(v, 0);
+    int bi = __builtin_amdgcn_readlane(i, 0);
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(v, off, QW_WAVE);
-        const int oi = __shfl_xor(i, off, QW_WAVE);
-        if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
-    }
+    for (int r = 1; r < 4; r++) qw_argmax_step(bv, bi, qw_lane(v, 16 * r), __builtin_amdgcn_readlane(i, 16 * r));
+    v = bv;
+    i = bi;
 }
 
 // Eight nibbles of one packed word against eight activations.  Returns
 // sum_j q_j * x_j; the group's scale and bias are applied by the caller.
 __device__ __forceinline__ float qw_dot8_q(uint32_t w, const float *x, float acc) {
+    // Keeps the compiler from converting every preloaded word up front (which
+    // holds 8 floats per word in registers): the conversions start here.
+    asm volatile("" : "+v"(w));
     const uint32_t lo = w & 0x0F0F0F0Fu;          // nibbles 0, 2, 4, 6
     const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // nibbles 1, 3, 5, 7
     // (float)(byte j of v) compiles to one v_cvt_f32_ubyte<j>.
@@ -81,4 +140,54 @@ __device__ __forceinline__ float qw_dot8_q(uint32_t w, const float *x, float acc
     acc = __builtin_fmaf((float)(lo >> 24), x[6], acc);
     acc = __builtin_fmaf((float)(hi >> 24), x[7], acc);
     return acc;
+}
+
+// ---- routing of one token ----------------------------------------------------------
+
+// The whole route of one token in one wave; every lane ends holding the same
+// picks, so the K rounds need no LDS and no barriers.  A lane holds experts
+// lane, lane + 64, ... (QW_ROUTE_PER_LANE of them, so E <= 64 * that).
+template <int QW_ROUTE_PER_LANE>
+__device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E, int K, int norm,
+                                              int lane, int *pick_i, float *pick_w)
+{
+    float v[QW_ROUTE_PER_LANE];
+    float m = -__builtin_huge_valf();
+#pragma unroll
+    for (int j = 0; j < QW_ROUTE_PER_LANE; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? l[e] : -__builtin_huge_valf();
+        m = fmaxf(m, v[j]);
+    }
+    m = qw_wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < QW_ROUTE_PER_LANE; j++) {
+        const int e = lane + 64 * j;
+        if (e < E) { v[j] = qw_exp_spec(v[j] - m); s = s + v[j]; }
+    }
+    s = qw_xor_sum<64>(s);
+#pragma unroll
+    for (int j = 0; j < QW_ROUTE_PER_LANE; j++) {
+        const int e = lane + 64 * j;
+        v[j] = e < E ? v[j] / s : -2.0f;
+    }
+    float mine_w = 0.0f;
+    int mine_i = 0;
+    for (int n = 0; n < K; n++) {
+        float bv = -2.0f;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < QW_ROUTE_PER_LANE; j++)
+            if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
+        qw_wave_argmax(bv, bi);
+#pragma unroll
+        for (int j = 0; j < QW_ROUTE_PER_LANE; j++)
+            if (lane + 64 * j == bi) v[j] = -1.0f;
+        if (lane == n) { mine_w = bv; mine_i = bi; }
+    }
+    float wsum = 0.0f;
+    for (int n = 0; n < K; n++) wsum = wsum + qw_lane(mine_w, n);
+    *pick_i = mine_i;
+    *pick_w = norm ? mine_w / wsum : mine_w;
 }

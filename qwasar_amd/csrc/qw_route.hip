@@ -8,7 +8,8 @@
 //             fmaf chain, from 0, over the 64 consecutive elements of chunk c
 //   softmax   m = max; e_i = qw_exp_spec(l_i - m); lane l of a wave sums
 //             e_l, e_{l+64}, ... serially; the 64 lane sums meet in an xor
-//             butterfly (offsets 32..1); p_i = e_i / sum (correctly rounded)
+//             butterfly with ascending offsets 1..32; p_i = e_i / sum
+//             (correctly rounded)
 //   top-k     K rounds of arg-max, ties to the lower expert index, a pick
 //             struck to -1 (the order a serial scan with '>' picks in)
 //   renorm    wsum = w_0 + w_1 + ... in pick order; w_k / wsum
@@ -105,54 +106,6 @@ extern "C" int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint
 
 // ---- route -------------------------------------------------------------------
 
-#define QW_ROUTE_PER_LANE (QWK_ROUTE_MAX_E / 64)
-
-// The whole route of one token in one wave; every lane ends holding the same
-// picks, so the K rounds need no LDS and no barriers.
-__device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E, int K, int norm,
-                                              int lane, int *pick_i, float *pick_w)
-{
-    float v[QW_ROUTE_PER_LANE];
-    float m = -__builtin_huge_valf();
-#pragma unroll
-    for (int j = 0; j < QW_ROUTE_PER_LANE; j++) {
-        const int e = lane + 64 * j;
-        v[j] = e < E ? l[e] : -__builtin_huge_valf();
-        m = fmaxf(m, v[j]);
-    }
-    m = qw_wave_max(m);
-    float s = 0.0f;
-#pragma unroll
-    for (int j = 0; j < QW_ROUTE_PER_LANE; j++) {
-        const int e = lane + 64 * j;
-        if (e < E) { v[j] = qw_exp_spec(v[j] - m); s = s + v[j]; }
-    }
-    s = qw_xor_sum<64>(s);
-#pragma unroll
-    for (int j = 0; j < QW_ROUTE_PER_LANE; j++) {
-        const int e = lane + 64 * j;
-        v[j] = e < E ? v[j] / s : -2.0f;
-    }
-    float mine_w = 0.0f;
-    int mine_i = 0;
-    for (int n = 0; n < K; n++) {
-        float bv = -2.0f;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < QW_ROUTE_PER_LANE; j++)
-            if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
-        qw_wave_argmax(bv, bi);
-#pragma unroll
-        for (int j = 0; j < QW_ROUTE_PER_LANE; j++)
-            if (lane + 64 * j == bi) v[j] = -1.0f;
-        if (lane == n) { mine_w = bv; mine_i = bi; }
-    }
-    float wsum = 0.0f;
-    for (int n = 0; n < K; n++) wsum = wsum + __shfl(mine_w, n, 64);
-    *pick_i = mine_i;
-    *pick_w = norm ? mine_w / wsum : mine_w;
-}
-
 __global__ __launch_bounds__(64) void k_route(int *__restrict__ idx, float *__restrict__ w,
                                               const float *__restrict__ logits, int rows,
                                               int E, int K, int norm)
@@ -160,7 +113,10 @@ __global__ __launch_bounds__(64) void k_route(int *__restrict__ idx, float *__re
     const int r = blockIdx.x, lane = threadIdx.x;
     int pi;
     float pw;
-    qw_route_wave(logits + (size_t)r * E, E, K, norm, lane, &pi, &pw);
+    const float *l = logits + (size_t)r * E;
+    if (E <= 256) qw_route_wave<4>(l, E, K, norm, lane, &pi, &pw);
+    else if (E <= 512) qw_route_wave<8>(l, E, K, norm, lane, &pi, &pw);
+    else qw_route_wave<16>(l, E, K, norm, lane, &pi, &pw);
     if (lane < K) { idx[(size_t)r * K + lane] = pi; w[(size_t)r * K + lane] = pw; }
 }
 

@@ -13,7 +13,7 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libqwasar_hip.so")
+LIB_PATH = os.environ.get("QWASAR_HIP_LIB") or os.path.join(HERE, "lib", "libqwasar_hip.so")
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() "
