@@ -24,7 +24,6 @@
 #define QD_MAXU (QWK_DECODE_MAX_ROWS * QWK_ROUTE_MAX_K)
 #define QD_MAXCH (QWK_DMAT_MAX_K / 64)
 #define QD_WAVES 4
-#define QD_DOWN_WAVES 2
 
 static __host__ __device__ int qd_lpr(int k)
 {
@@ -233,6 +232,7 @@ struct QdRoute {
     int ustart[QD_MAXU];
     int upair[QD_MAXU];       // pairs grouped by unique expert, ascending pair index
     int mark[QWK_ROUTE_MAX_E];
+    int scratch[QD_WAVES][4 * QWK_ROUTE_MAX_K];
 };
 
 // Routes every token (a wave per token) with the arithmetic of the
@@ -247,7 +247,7 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
     for (int r = wave; r < a.rows; r += nw) {
         int pi;
         float pw;
-        qw_route_wave<PL>(a.logits + (size_t)r * E, E, K, a.m.norm, lane, &pi, &pw);
+        qw_route_wave<PL>(a.logits + (size_t)r * E, E, K, a.m.norm, lane, &pi, &pw, R.scratch[wave]);
         if (lane < K) {
             R.picks[r * K + lane] = pi;
             R.pw[r * K + lane] = pw;
@@ -348,87 +348,101 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_decode_experts(QdArgs a)
 }
 
 // ---- down: the shared expert and every expert of a token, and the combine -------
+//
+// A workgroup owns RIT * 64/LPR output rows of one token; wave w computes those
+// rows of matrix w, w + nw, ... (matrix 0 = the shared expert, matrix 1 + k =
+// the token's k-th expert), so each wave has one round of loads in flight.
+// The per-matrix rows meet in LDS and the combine runs in slot order.
+#define QD_DOWN_MAXW 16
+static __host__ __device__ constexpr int qd_down_rit(int splmax) { return splmax <= 2 ? 4 : splmax <= 4 ? 2 : 1; }
 
 template <int LPR, int SPLMAX>
-__global__ __launch_bounds__(QD_DOWN_WAVES * 64) void k_decode_down(QdArgs a)
+__global__ __launch_bounds__(QD_DOWN_MAXW * 64) void k_decode_down(QdArgs a)
 {
+    constexpr int RIT = qd_down_rit(SPLMAX);
+    constexpr int SLOTS = 64 / LPR, RPG = SLOTS * RIT;
+    __shared__ float ys[QWK_ROUTE_MAX_K + 1][RPG];
     const int H = a.m.H, I = a.m.I, SI = a.m.SI, K = a.m.K;
     const int rb = blockIdx.x % a.n_down_rb, t = blockIdx.x / a.n_down_rb;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    constexpr int SLOTS = 64 / LPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int slot = lane / LPR, lr = lane % LPR;
-    const int row = rb * a.down_rows_per_wg + wave * SLOTS + slot;
+    const int row0 = rb * RPG;
     const int lgG = a.lgG;
-    float acc = 0.0f;
-    // The shared expert first (the combine starts from its gated term), then
-    // the routed experts in slot order; NB matrices' weights are loaded per
-    // round before any of them is used.
-    constexpr int NB = SPLMAX >= 8 ? 1 : 8 / SPLMAX;
-    for (int k0 = -1; k0 < K; k0 += NB) {
-        uint4 wv[NB][SPLMAX];
-        float sc[NB][SPLMAX], bi[NB][SPLMAX];
+    for (int m = wave; m <= K; m += nw) {
+        const int kin = m == 0 ? SI : I;
+        const int words = kin / 8, groups = kin >> lgG, spl = (kin / 32) / LPR;
+        const uint32_t *wm = a.m.sh_down.w;
+        const uint16_t *sm = a.m.sh_down.s, *bm = a.m.sh_down.b;
+        const float *av = a.shact + (size_t)t * SI;
+        if (m > 0) {
+            const size_t e = (size_t)a.idx[t * K + m - 1];
+            wm = a.m.down.w + e * H * words;
+            sm = a.m.down.s + e * H * groups;
+            bm = a.m.down.b + e * H * groups;
+            av = a.act + ((size_t)t * K + m - 1) * I;
+        }
+        uint4 wv[SPLMAX][RIT];
+        float sc[SPLMAX][RIT], bi[SPLMAX][RIT];
 #pragma unroll
-        for (int kb = 0; kb < NB; kb++) {
-            const int k = k0 + kb;
-            const int kin = k < 0 ? SI : I;
-            const int words = kin / 8, groups = kin >> lgG, spl = (kin / 32) / LPR;
-            const uint32_t *wm = a.m.sh_down.w;
-            const uint16_t *sm = a.m.sh_down.s, *bm = a.m.sh_down.b;
-            if (k >= 0 && k < K) {
-                const size_t e = (size_t)a.idx[t * K + k];
-                wm = a.m.down.w + e * H * words;
-                sm = a.m.down.s + e * H * groups;
-                bm = a.m.down.b + e * H * groups;
-            }
+        for (int j = 0; j < SPLMAX; j++) {
+            const int seg = j * LPR + lr, g = (seg * 32) >> lgG;
 #pragma unroll
-            for (int j = 0; j < SPLMAX; j++) {
-                const int seg = j * LPR + lr, g = (seg * 32) >> lgG;
-                if (k < K && j < spl && row < H) {
-                    wv[kb][j] = *reinterpret_cast<const uint4 *>(wm + (size_t)row * words + seg * 4);
-                    sc[kb][j] = qw_bf16(sm[(size_t)row * groups + g]);
-                    bi[kb][j] = qw_bf16(bm[(size_t)row * groups + g]);
+            for (int i = 0; i < RIT; i++) {
+                const int row = row0 + slot + SLOTS * i;
+                if (j < spl && row < H) {
+                    wv[j][i] = *reinterpret_cast<const uint4 *>(wm + (size_t)row * words + seg * 4);
+                    sc[j][i] = qw_bf16(sm[(size_t)row * groups + g]);
+                    bi[j][i] = qw_bf16(bm[(size_t)row * groups + g]);
                 } else {
-                    wv[kb][j] = make_uint4(0, 0, 0, 0);
-                    sc[kb][j] = 0.0f;
-                    bi[kb][j] = 0.0f;
+                    wv[j][i] = make_uint4(0, 0, 0, 0);
+                    sc[j][i] = 0.0f;
+                    bi[j][i] = 0.0f;
+                }
+            }
+        }
+        float y[RIT];
+#pragma unroll
+        for (int i = 0; i < RIT; i++) y[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < SPLMAX; j++) {
+            if (j < spl) {
+                const int seg = j * LPR + lr;
+                float xs[32];
+                const float4 *xv = reinterpret_cast<const float4 *>(av + seg * 32);
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const float4 v = xv[q];
+                    xs[4 * q] = v.x; xs[4 * q + 1] = v.y; xs[4 * q + 2] = v.z; xs[4 * q + 3] = v.w;
+                }
+                float xsum = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 32; q++) xsum += xs[q];
+#pragma unroll
+                for (int i = 0; i < RIT; i++) {
+                    float d = qw_dot8_q(wv[j][i].x, xs, 0.0f);
+                    d = qw_dot8_q(wv[j][i].y, xs + 8, d);
+                    d = qw_dot8_q(wv[j][i].z, xs + 16, d);
+                    d = qw_dot8_q(wv[j][i].w, xs + 24, d);
+                    y[i] = __builtin_fmaf(sc[j][i], d, y[i]);
+                    y[i] = __builtin_fmaf(bi[j][i], xsum, y[i]);
                 }
             }
         }
 #pragma unroll
-        for (int kb = 0; kb < NB; kb++) {
-            const int k = k0 + kb;
-            if (k >= K) break;
-            const int kin = k < 0 ? SI : I, spl = (kin / 32) / LPR;
-            const float *av = k < 0 ? a.shact + (size_t)t * SI : a.act + ((size_t)t * K + k) * I;
-            float y = 0.0f;
-#pragma unroll
-            for (int j = 0; j < SPLMAX; j++) {
-                if (j < spl) {
-                    const int seg = j * LPR + lr;
-                    float xs[32];
-                    const float4 *xv = reinterpret_cast<const float4 *>(av + seg * 32);
-#pragma unroll
-                    for (int q = 0; q < 8; q++) {
-                        const float4 v = xv[q];
-                        xs[4 * q] = v.x; xs[4 * q + 1] = v.y; xs[4 * q + 2] = v.z; xs[4 * q + 3] = v.w;
-                    }
-                    float xsum = 0.0f;
-#pragma unroll
-                    for (int q = 0; q < 32; q++) xsum += xs[q];
-                    float d = qw_dot8_q(wv[kb][j].x, xs, 0.0f);
-                    d = qw_dot8_q(wv[kb][j].y, xs + 8, d);
-                    d = qw_dot8_q(wv[kb][j].z, xs + 16, d);
-                    d = qw_dot8_q(wv[kb][j].w, xs + 24, d);
-                    y = __builtin_fmaf(sc[kb][j], d, y);
-                    y = __builtin_fmaf(bi[kb][j], xsum, y);
-                }
-            }
-            y = qw_xor_sum<LPR>(y);
-            if (k < 0) acc = y * qw_sigmoid(a.g1[t]);
-            else acc = __builtin_fmaf(a.w[t * K + k], y, acc);
+        for (int i = 0; i < RIT; i++) {
+            const float v = qw_xor_sum<LPR>(y[i]);
+            if (lr == 0) ys[m][slot + SLOTS * i] = v;
         }
     }
-    if (lr == 0 && row < H) a.out[(size_t)t * H + row] = acc;
+    __syncthreads();
+    // The combine: the shared term first, then an fma per slot, in order.
+    for (int r = threadIdx.x; r < RPG; r += blockDim.x) {
+        const int row = row0 + r;
+        if (row >= H) continue;
+        float acc = ys[0][r] * qw_sigmoid(a.g1[t]);
+        for (int k = 0; k < K; k++) acc = __builtin_fmaf(a.w[t * K + k], ys[1 + k][r], acc);
+        a.out[(size_t)t * H + row] = acc;
+    }
 }
 
 // ---- host side -------------------------------------------------------------------
@@ -474,7 +488,8 @@ static bool launch_fe_spl(int splmax, hipStream_t s, QdArgs &a, hipEvent_t *ev)
 template <int LPR, int SPLMAX>
 static void launch_down(hipStream_t s, QdArgs &a)
 {
-    hipLaunchKernelGGL((k_decode_down<LPR, SPLMAX>), dim3(a.rows * a.n_down_rb), dim3(QD_DOWN_WAVES * 64), 0, s, a);
+    const int nw = a.m.K + 1 < QD_DOWN_MAXW ? a.m.K + 1 : QD_DOWN_MAXW;
+    hipLaunchKernelGGL((k_decode_down<LPR, SPLMAX>), dim3(a.rows * a.n_down_rb), dim3(nw * 64), 0, s, a);
 }
 
 template <int LPR>
@@ -525,7 +540,7 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     const int rpg_h = QD_WAVES * (64 / lpr_h) * qd_rit(spl_h);
     a.n_shared_wg = (M->SI + rpg_h - 1) / rpg_h;
     a.gu_wg_per_u = (M->I + rpg_h - 1) / rpg_h;
-    a.down_rows_per_wg = QD_DOWN_WAVES * (64 / lpr_d);
+    a.down_rows_per_wg = qd_down_rit(spl_d) * (64 / lpr_d);
     a.n_down_rb = (M->H + a.down_rows_per_wg - 1) / a.down_rows_per_wg;
     a.logits = (float *)(S + L.logits);
     a.g1 = (float *)(S + L.g1);

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "qw_kernels.h"
+
 #define QW_WAVE 64
 
 __device__ __forceinline__ float qw_bf16(uint16_t v) {
@@ -143,18 +145,31 @@ __device__ __forceinline__ float qw_dot8_q(uint32_t w, const float *x, float acc
 }
 
 // ---- routing of one token ----------------------------------------------------------
-
-// The whole route of one token in one wave; every lane ends holding the same
-// picks, so the K rounds need no LDS and no barriers.  A lane holds experts
-// lane, lane + 64, ... (QW_ROUTE_PER_LANE of them, so E <= 64 * that).
-template <int QW_ROUTE_PER_LANE>
+//
+// Softmax over E logits and the K picks of a serial scan with strict '>'
+// from e = 0 -- the K largest probabilities, ties to the lower expert, in
+// descending (p, then ascending index) order -- by one wave, exactly:
+//
+//   1. key_e = bits(p_e) + 1 for every expert (p >= 0, so the bits order as
+//      the values; 0 marks a lane slot past E).
+//   2. Radix select: the K-th largest key T, one bit at a time from the top,
+//      counting keys >= candidate with ballots (no cross-lane data moves).
+//   3. Select every key > T and, of the keys == T, the lowest-indexed
+//      K - #(> T).
+//   4. The K selected entries are compacted into LDS, and each of K lanes
+//      counts the entries ahead of its own: its output position.
+//
+// Lane l holds experts l, l + 64, ..., so expert order is slot-major.
+// `lds` is this wave's scratch of 4 * QWK_ROUTE_MAX_K ints.  Every lane ends
+// holding pick `lane` (lane < K) in *pick_i / *pick_w.
+template <int PL>
 __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E, int K, int norm,
-                                              int lane, int *pick_i, float *pick_w)
+                                              int lane, int *pick_i, float *pick_w, int *lds)
 {
-    float v[QW_ROUTE_PER_LANE];
+    float v[PL];
     float m = -__builtin_huge_valf();
 #pragma unroll
-    for (int j = 0; j < QW_ROUTE_PER_LANE; j++) {
+    for (int j = 0; j < PL; j++) {
         const int e = lane + 64 * j;
         v[j] = e < E ? l[e] : -__builtin_huge_valf();
         m = fmaxf(m, v[j]);
@@ -162,30 +177,67 @@ __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E
     m = qw_wave_max(m);
     float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < QW_ROUTE_PER_LANE; j++) {
+    for (int j = 0; j < PL; j++) {
         const int e = lane + 64 * j;
         if (e < E) { v[j] = qw_exp_spec(v[j] - m); s = s + v[j]; }
     }
     s = qw_xor_sum<64>(s);
+    uint32_t key[PL];
 #pragma unroll
-    for (int j = 0; j < QW_ROUTE_PER_LANE; j++) {
+    for (int j = 0; j < PL; j++) {
         const int e = lane + 64 * j;
-        v[j] = e < E ? v[j] / s : -2.0f;
+        key[j] = e < E ? __float_as_uint(v[j] / s) + 1u : 0u;
     }
-    float mine_w = 0.0f;
-    int mine_i = 0;
+    // 2. the K-th largest key
+    uint32_t T = 0;
+    for (int b = 30; b >= 0; b--) {
+        const uint32_t cand = T | (1u << b);
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < PL; j++) cnt += __popcll(__ballot(key[j] >= cand));
+        if (cnt >= K) T = cand;
+    }
+    // 3. the selection
+    int gt = 0;
+#pragma unroll
+    for (int j = 0; j < PL; j++) gt += __popcll(__ballot(key[j] > T));
+    const int need = K - gt;
+    const unsigned long long below = (1ull << lane) - 1ull;
+    int eq_before = 0, sel_before = 0;
+    int *ek = lds, *ei = lds + QWK_ROUTE_MAX_K;
+#pragma unroll
+    for (int j = 0; j < PL; j++) {
+        const unsigned long long eq = __ballot(key[j] == T);
+        const bool is_eq = key[j] == T;
+        const int r = eq_before + __popcll(eq & below);
+        const bool sel = key[j] > T || (is_eq && r < need);
+        const unsigned long long sm = __ballot(sel);
+        if (sel) {
+            const int pos = sel_before + __popcll(sm & below);
+            ek[pos] = (int)key[j];
+            ei[pos] = lane + 64 * j;
+        }
+        eq_before += __popcll(eq);
+        sel_before += __popcll(sm);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    // 4. positions: entries ahead = larger key, or equal key and lower index
+    const uint32_t mk = lane < K ? (uint32_t)ek[lane] : 0u;
+    const int mi = lane < K ? ei[lane] : 0;
+    int rank = 0;
     for (int n = 0; n < K; n++) {
-        float bv = -2.0f;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < QW_ROUTE_PER_LANE; j++)
-            if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
-        qw_wave_argmax(bv, bi);
-#pragma unroll
-        for (int j = 0; j < QW_ROUTE_PER_LANE; j++)
-            if (lane + 64 * j == bi) v[j] = -1.0f;
-        if (lane == n) { mine_w = bv; mine_i = bi; }
+        const uint32_t kn = (uint32_t)__builtin_amdgcn_readlane((int)mk, n);
+        const int in = __builtin_amdgcn_readlane(mi, n);
+        rank += (kn > mk || (kn == mk && in < mi)) ? 1 : 0;
     }
+    int *ok = lds + 2 * QWK_ROUTE_MAX_K, *oi = lds + 3 * QWK_ROUTE_MAX_K;
+    __builtin_amdgcn_wave_barrier();
+    if (lane < K) { ok[rank] = (int)mk; oi[rank] = mi; }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    const float mine_w = lane < K ? __uint_as_float((uint32_t)ok[lane] - 1u) : 0.0f;
+    const int mine_i = lane < K ? oi[lane] : 0;
     float wsum = 0.0f;
     for (int n = 0; n < K; n++) wsum = wsum + qw_lane(mine_w, n);
     *pick_i = mine_i;

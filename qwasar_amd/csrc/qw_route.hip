@@ -10,8 +10,9 @@
 //             e_l, e_{l+64}, ... serially; the 64 lane sums meet in an xor
 //             butterfly with ascending offsets 1..32; p_i = e_i / sum
 //             (correctly rounded)
-//   top-k     K rounds of arg-max, ties to the lower expert index, a pick
-//             struck to -1 (the order a serial scan with '>' picks in)
+//   top-k     the K largest probabilities, ties to the lower expert index,
+//             in descending order (what K rounds of a serial scan with '>'
+//             pick), found exactly by a radix select on the fp32 bits
 //   renorm    wsum = w_0 + w_1 + ... in pick order; w_k / wsum
 #include "qw_device.h"
 #include "qw_kernels.h"
@@ -110,13 +111,14 @@ __global__ __launch_bounds__(64) void k_route(int *__restrict__ idx, float *__re
                                               const float *__restrict__ logits, int rows,
                                               int E, int K, int norm)
 {
+    __shared__ int lds[4 * QWK_ROUTE_MAX_K];
     const int r = blockIdx.x, lane = threadIdx.x;
     int pi;
     float pw;
     const float *l = logits + (size_t)r * E;
-    if (E <= 256) qw_route_wave<4>(l, E, K, norm, lane, &pi, &pw);
-    else if (E <= 512) qw_route_wave<8>(l, E, K, norm, lane, &pi, &pw);
-    else qw_route_wave<16>(l, E, K, norm, lane, &pi, &pw);
+    if (E <= 256) qw_route_wave<4>(l, E, K, norm, lane, &pi, &pw, lds);
+    else if (E <= 512) qw_route_wave<8>(l, E, K, norm, lane, &pi, &pw, lds);
+    else qw_route_wave<16>(l, E, K, norm, lane, &pi, &pw, lds);
     if (lane < K) { idx[(size_t)r * K + lane] = pi; w[(size_t)r * K + lane] = pw; }
 }
 
