@@ -1,44 +1,46 @@
 // qw_decode.hip -- the MoE block at decode (1..8 tokens) in three launches,
 // with no communication between workgroups inside a launch.
 //
-//   front    router logits (order R) for every expert and the shared
-//            expert's gate logit; the shared expert's gate and up rows, a
-//            wave taking the same rows of both, and its SwiGLU activation
-//   experts  every workgroup first routes every token itself from the
-//            logits (softmax, top-K, renormalise: cheap, and it saves a
-//            launch and any cross-workgroup handoff) and lists the union of
-//            the selected experts; then the gate and up rows of one selected
-//            expert for every token routed to it -- each weight byte read
-//            once -- and their SwiGLU activation; workgroup 0 writes idx / w
+//   front    router logits (order R, fp32) for every expert and the shared
+//            expert's gate logit; the input rows staged as q16 units
+//   experts  the shared expert's gate / up rows (no routing needed), and, in
+//            the other workgroups, routing of every token (softmax, top-K,
+//            renormalise: cheap, and it saves a launch and any
+//            cross-workgroup handoff) followed by the gate / up rows of one
+//            selected expert for every token routed to it -- each weight
+//            byte read once; the SwiGLU activations leave staged as q16
+//            units; workgroup 0 writes idx / w
 //   down     per (block of output rows, token): the down rows of the shared
 //            expert and of each of the token's K experts, and the combine in
 //            registers: sigmoid(g) * shared + sum_k w_k * y_k, an fma chain
 //            in slot order
 //
-// A lane issues all its weight loads for a matrix (or a batch of matrices)
-// before its first multiply, so each wave keeps those reads in flight at once.
+// The 4-bit products use the q16 dot (qw_unit_dot): staged activations are
+// loaded straight into registers next to the weights, and a lane issues all
+// its loads before its first multiply.
 #include "qw_device.h"
 #include "qw_kernels.h"
 
 #define QD_MAXT QWK_DECODE_MAX_ROWS
 #define QD_MAXU (QWK_DECODE_MAX_ROWS * QWK_ROUTE_MAX_K)
 #define QD_MAXCH (QWK_DMAT_MAX_K / 64)
-#define QD_WAVES 4
+#define QD_FRONT_WAVES 4
+#define QD_GU_WAVES 16       // experts workgroup: 16 waves
+#define QD_GU_MAXRPB (QD_GU_WAVES * 4)
+#define QD_GU_LDS (48 * 1024)  // LDS for staged input vectors
+#define QD_DOWN_MAXW 16
+#define QD_DOWN_RIT 2        // down rows per lane slot
 
-static __host__ __device__ int qd_lpr(int k)
+// Lanes per row for a row of `units` q16 units, and units per lane.
+static __host__ __device__ constexpr int qd_lpr(int units) { return units >= 128 ? 64 : units >= 64 ? 32 : 16; }
+static int qd_nul(int units, int lpr)
 {
-    const int S = k / 32;
-    int l = 1;
-    while (l < 64 && S % (2 * l) == 0) l *= 2;
-    return l;
+    const int n = (units + lpr - 1) / lpr;
+    return n <= 4 ? n : n <= 8 ? 8 : -1;
 }
 
-static int qd_splmax(int spl) { return spl <= 4 ? spl : 8; }
-// Row slots a lane carries per matrix: fewer as segments per lane grow.
-static __host__ __device__ constexpr int qd_rit(int splmax) { return splmax <= 2 ? 2 : 1; }
-
 struct QdLayout {
-    size_t logits, g1, shact, act, total;
+    size_t logits, g1, qx, qsh, qact, total;
 };
 
 static size_t al(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -49,8 +51,9 @@ static QdLayout qd_layout(const qwk_moe *M, int rows)
     size_t o = 0;
     L.logits = o; o += al((size_t)rows * M->E * 4);
     L.g1 = o;     o += al((size_t)rows * 4);
-    L.shact = o;  o += al((size_t)rows * M->SI * 4);
-    L.act = o;    o += al((size_t)rows * M->K * M->I * 4);
+    L.qx = o;     o += al((size_t)rows * (M->H / 16) * QW_Q16_BYTES);
+    L.qsh = o;    o += al((size_t)rows * (M->SI / 16) * QW_Q16_BYTES);
+    L.qact = o;   o += al((size_t)rows * M->K * (M->I / 16) * QW_Q16_BYTES);
     L.total = o;
     return L;
 }
@@ -62,93 +65,15 @@ struct QdArgs {
     int32_t *idx;
     float *w;
     int rows, umax, lgG;
-    int n_router_wg, n_shared_wg;   // front
-    int gu_wg_per_u;                // experts
-    int down_rows_per_wg, n_down_rb;
-    float *logits, *g1, *shact, *act;
+    int n_router_wg;                // front
+    int n_shared_wg, gu_wg_per_u;   // experts
+    int tch;                        // input vectors per LDS pass
+    int n_down_rb;                  // down
+    float *logits, *g1;
+    uint4 *qx, *qsh, *qact;         // q16 units: [vector][units][3]
 };
 
-// ---- gate and up rows with SwiGLU -----------------------------------------------
-//
-// Rows row0 + slot + SLOTS*i (i < RIT) of a gate matrix and the same rows of
-// an up matrix (k inputs, LPR lanes to a row) against up to QD_MAXT inputs
-// xp[t]: yp[t][row] = silu(gate . x_t) * (up . x_t).  A row's k/32 segments of
-// 16 bytes go to its lanes round-robin; segment s lies in group (32 s) >> lgG.
-template <int LPR, int SPLMAX, int RIT>
-__device__ __forceinline__ void qd_glu_rows(const qwk_q4 gm, const qwk_q4 um, int n, int k, int lgG, int row0,
-                                            int nt, const float *const *xp, float *const *yp)
-{
-    constexpr int SLOTS = 64 / LPR;
-    const int lane = threadIdx.x & 63, slot = lane / LPR, lr = lane % LPR;
-    const int words = k / 8, groups = k >> lgG;
-    const int spl = (k / 32) / LPR;
-    uint4 wv[2][SPLMAX][RIT];
-    float sc[2][SPLMAX][RIT], bi[2][SPLMAX][RIT];
-#pragma unroll
-    for (int z = 0; z < 2; z++) {
-        const qwk_q4 q = z ? um : gm;
-#pragma unroll
-        for (int j = 0; j < SPLMAX; j++) {
-            const int seg = j * LPR + lr, g = (seg * 32) >> lgG;
-#pragma unroll
-            for (int i = 0; i < RIT; i++) {
-                const int row = row0 + slot + SLOTS * i;
-                if (j < spl && row < n) {
-                    wv[z][j][i] = *reinterpret_cast<const uint4 *>(q.w + (size_t)row * words + seg * 4);
-                    sc[z][j][i] = qw_bf16(q.s[(size_t)row * groups + g]);
-                    bi[z][j][i] = qw_bf16(q.b[(size_t)row * groups + g]);
-                } else {
-                    wv[z][j][i] = make_uint4(0, 0, 0, 0);
-                    sc[z][j][i] = 0.0f;
-                    bi[z][j][i] = 0.0f;
-                }
-            }
-        }
-    }
-#pragma unroll 1
-    for (int t = 0; t < nt; t++) {
-        float acc[2][RIT];
-#pragma unroll
-        for (int i = 0; i < RIT; i++) acc[0][i] = acc[1][i] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < SPLMAX; j++) {
-            if (j < spl) {
-                const int seg = j * LPR + lr;
-                float xs[32];
-                const float4 *xv = reinterpret_cast<const float4 *>(xp[t] + seg * 32);
-#pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    const float4 v = xv[q];
-                    xs[4 * q] = v.x; xs[4 * q + 1] = v.y; xs[4 * q + 2] = v.z; xs[4 * q + 3] = v.w;
-                }
-                float xsum = 0.0f;
-#pragma unroll
-                for (int q = 0; q < 32; q++) xsum += xs[q];
-#pragma unroll
-                for (int z = 0; z < 2; z++) {
-#pragma unroll
-                    for (int i = 0; i < RIT; i++) {
-                        float d = qw_dot8_q(wv[z][j][i].x, xs, 0.0f);
-                        d = qw_dot8_q(wv[z][j][i].y, xs + 8, d);
-                        d = qw_dot8_q(wv[z][j][i].z, xs + 16, d);
-                        d = qw_dot8_q(wv[z][j][i].w, xs + 24, d);
-                        acc[z][i] = __builtin_fmaf(sc[z][j][i], d, acc[z][i]);
-                        acc[z][i] = __builtin_fmaf(bi[z][j][i], xsum, acc[z][i]);
-                    }
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < RIT; i++) {
-            const float g = qw_xor_sum<LPR>(acc[0][i]);
-            const float u = qw_xor_sum<LPR>(acc[1][i]);
-            const int row = row0 + slot + SLOTS * i;
-            if (lr == 0 && row < n) yp[t][row] = qw_silu(g) * u;
-        }
-    }
-}
-
-// ---- front: router logits and the shared expert's gate / up ----------------------
+// ---- front: router logits and the staged input ----------------------------------
 
 // Order-R dot of one bf16 row with nt token rows (one wave): lane l computes
 // the fmaf chains of chunks l, l+64, ...; the chunk partials are then added
@@ -193,35 +118,124 @@ __device__ __forceinline__ void qd_router_row(const uint16_t *__restrict__ wr, c
     }
 }
 
-template <int LPR, int SPLMAX>
-__global__ __launch_bounds__(QD_WAVES * 64) void k_decode_front(QdArgs a)
+__global__ __launch_bounds__(QD_FRONT_WAVES * 64) void k_decode_front(QdArgs a)
 {
-    __shared__ const float *xp[QD_MAXT];
-    __shared__ float *yp[QD_MAXT];
     const int wave = threadIdx.x >> 6, b = blockIdx.x;
-    const int H = a.m.H, E = a.m.E, SI = a.m.SI;
+    const int H = a.m.H, E = a.m.E;
     if (b < a.n_router_wg) {
-        const int o = b * QD_WAVES + wave;
+        const int o = b * QD_FRONT_WAVES + wave;
         if (o < E)
             qd_router_row(a.m.router + (size_t)o * H, a.x, H, a.rows, a.logits + o, E);
         else if (o == E)
             qd_router_row(a.m.sh_gate_w, a.x, H, a.rows, a.g1, 1);
         return;
     }
-    constexpr int RIT = qd_rit(SPLMAX);
-    constexpr int RPW = (64 / LPR) * RIT;
-    const int row0 = ((b - a.n_router_wg) * QD_WAVES + wave) * RPW;
-    if (threadIdx.x < QD_MAXT) {
-        const int t = min((int)threadIdx.x, a.rows - 1);
-        xp[threadIdx.x] = a.x + (size_t)t * H;
-        yp[threadIdx.x] = a.shact + (size_t)t * SI;
+    // one workgroup per token: a unit per thread
+    const int t = b - a.n_router_wg, units = H / 16;
+    for (int u = threadIdx.x; u < units; u += blockDim.x) {
+        const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)t * H + 16 * u);
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 f = src[q];
+            v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+        }
+        qw_q16_stage(v, a.qx + ((size_t)t * units + u) * 3);
     }
-    __syncthreads();
-    if (row0 < SI)
-        qd_glu_rows<LPR, SPLMAX, RIT>(a.m.sh_gate, a.m.sh_up, SI, H, a.lgG, row0, a.rows, xp, yp);
 }
 
-// ---- experts: routing in the prologue, then gate / up of one selected expert ----
+// ---- experts: gate / up rows with SwiGLU --------------------------------------------
+//
+// A workgroup owns RPB = QD_GU_WAVES * 64/LPR consecutive rows of one gate / up
+// pair (the shared expert's, or one routed expert's) for nt input vectors.
+// Lane (slot, lr) of wave w takes row row0 + w * 64/LPR + slot and its units
+// lr, lr + LPR, ... (NUL of them), in both matrices; its weights stay in
+// registers while the input vectors pass through LDS, up to `tch` at a time.
+// The per-row results meet in LDS and leave as q16 units of the activation
+// vectors.
+
+// Copies staged vectors vin[t] (t < n; vector t when vin is NULL) of src,
+// `units` units each, into LDS, with threads tid0.. of the workgroup.
+__device__ __forceinline__ void qd_copy_vecs(uint4 *xs, const uint4 *src, const int *vin, int n, int units,
+                                             int tid0, int nthr)
+{
+    const int per = units * 3;
+    for (int i = threadIdx.x - tid0; i < n * per; i += nthr) {
+        const int t = i / per, o = i % per;
+        xs[i] = src[(size_t)(vin ? vin[t] : t) * per + o];
+    }
+}
+
+template <int LPR, int NUL>
+__device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, int n, int k, int lgG, int row0,
+                                             int nt, int tch, bool staged, uint4 *xs, const uint4 *src,
+                                             const int *vin, const int *vout, uint4 *dst,
+                                             float (*ys)[QD_GU_MAXRPB])
+{
+    constexpr int SL = 64 / LPR, RPB = QD_GU_WAVES * SL;
+    static_assert(RPB % 16 == 0 && RPB <= QD_GU_MAXRPB, "rows per block");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, slot = lane / LPR, lr = lane % LPR;
+    const int units = k / 16, words = k / 8, groups = k >> lgG;
+    const int rl = wave * SL + slot, row = row0 + rl;
+    uint2 wv[2][NUL];
+    float sc[2][NUL], bi[2][NUL];
+#pragma unroll
+    for (int z = 0; z < 2; z++) {
+        const qwk_q4 q = z ? um : gm;
+#pragma unroll
+        for (int j = 0; j < NUL; j++) {
+            const int c = j * LPR + lr;
+            if (row < n && c < units) {
+                wv[z][j] = *reinterpret_cast<const uint2 *>(q.w + (size_t)row * words + 2 * c);
+                sc[z][j] = qw_bf16(q.s[(size_t)row * groups + ((16 * c) >> lgG)]);
+                bi[z][j] = qw_bf16(q.b[(size_t)row * groups + ((16 * c) >> lgG)]);
+            } else {
+                wv[z][j] = make_uint2(0, 0);
+                sc[z][j] = bi[z][j] = 0.0f;
+            }
+        }
+    }
+    for (int t0 = 0; t0 < nt; t0 += tch) {
+        const int tn = min(tch, nt - t0);
+        if (!staged) {
+            __syncthreads();
+            qd_copy_vecs(xs, src, vin + t0, tn, units, 0, blockDim.x);
+        }
+        __syncthreads();
+#pragma unroll 1
+        for (int t = 0; t < tn; t++) {
+            const uint4 *xt = xs + (size_t)t * units * 3;
+            float acc[2] = {0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < NUL; j++) {
+                const int c = j * LPR + lr;
+                if (c < units) {
+                    const uint4 p0 = xt[3 * c], p1 = xt[3 * c + 1];
+                    const uint4 rr = xt[3 * c + 2];
+                    const float4 r = *reinterpret_cast<const float4 *>(&rr);
+#pragma unroll
+                    for (int z = 0; z < 2; z++)
+                        acc[z] = qw_unit_dot(wv[z][j], p0, p1, r, sc[z][j], bi[z][j], acc[z]);
+                }
+            }
+            const float g = qw_xor_sum<LPR>(acc[0]);
+            const float u = qw_xor_sum<LPR>(acc[1]);
+            if (lr == 0) ys[t0 + t][rl] = qw_silu(g) * u;
+        }
+    }
+    __syncthreads();
+    // one thread per (vector, unit) of this block's rows
+    constexpr int upb = RPB / 16;
+    const int outunits = n / 16;
+    for (int i = threadIdx.x; i < nt * upb; i += blockDim.x) {
+        const int t = i / upb, uu = i % upb;
+        if (row0 + 16 * uu >= n) continue;
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 16; q++) v[q] = ys[t][16 * uu + q];
+        qw_q16_stage(v, dst + ((size_t)vout[t] * outunits + row0 / 16 + uu) * 3);
+    }
+}
 
 struct QdRoute {
     int U;
@@ -232,7 +246,6 @@ struct QdRoute {
     int ustart[QD_MAXU];
     int upair[QD_MAXU];       // pairs grouped by unique expert, ascending pair index
     int mark[QWK_ROUTE_MAX_E];
-    int scratch[QD_WAVES][4 * QWK_ROUTE_MAX_K];
 };
 
 // Routes every token (a wave per token) with the arithmetic of the
@@ -247,7 +260,7 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
     for (int r = wave; r < a.rows; r += nw) {
         int pi;
         float pw;
-        qw_route_wave<PL>(a.logits + (size_t)r * E, E, K, a.m.norm, lane, &pi, &pw, R.scratch[wave]);
+        qw_route_wave<PL>(a.logits + (size_t)r * E, E, K, a.m.norm, lane, &pi, &pw);
         if (lane < K) {
             R.picks[r * K + lane] = pi;
             R.pw[r * K + lane] = pw;
@@ -304,31 +317,41 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
     __syncthreads();
 }
 
-template <int LPR, int SPLMAX, int PL>
-__global__ __launch_bounds__(QD_WAVES * 64) void k_decode_experts(QdArgs a)
+template <int LPR, int NUL, int PL>
+__global__ __launch_bounds__(QD_GU_WAVES * 64) void k_decode_experts(QdArgs a)
 {
+    extern __shared__ uint4 xs[];     // [tch][units][3]
     __shared__ QdRoute R;
-    __shared__ const float *xp[QD_MAXT];
-    __shared__ float *yp[QD_MAXT];
-    const int wave = threadIdx.x >> 6, b = blockIdx.x;
-    const int H = a.m.H, I = a.m.I, K = a.m.K;
-    const int u = b / a.gu_wg_per_u, rb = b % a.gu_wg_per_u;
+    __shared__ int vin[QD_MAXT], vout[QD_MAXT];
+    __shared__ float ys[QD_MAXT][QD_GU_MAXRPB];
+    constexpr int RPB = QD_GU_WAVES * (64 / LPR);
+    const int b = blockIdx.x;
+    const int H = a.m.H, I = a.m.I, K = a.m.K, SI = a.m.SI;
+    const int xunits = H / 16;
+    if (b < a.n_shared_wg) {
+        if (threadIdx.x < QD_MAXT) vin[threadIdx.x] = vout[threadIdx.x] = threadIdx.x;
+        __syncthreads();
+        qd_glu_block<LPR, NUL>(a.m.sh_gate, a.m.sh_up, SI, H, a.lgG, b * RPB, a.rows, a.tch, false,
+                               xs, a.qx, vin, vout, a.qsh, ys);
+        return;
+    }
+    const int bb = b - a.n_shared_wg;
+    const int u = bb / a.gu_wg_per_u, rb = bb % a.gu_wg_per_u;
+    // One token: its input goes to LDS (waves 1..) while wave 0 routes.
+    const bool one = a.rows == 1;
+    if (one && threadIdx.x >= 64) qd_copy_vecs(xs, a.qx, nullptr, 1, xunits, 64, blockDim.x - 64);
     qd_route_all<PL>(a, R);
-    if (b == 0)
+    if (bb == 0)
         for (int p = threadIdx.x; p < a.rows * K; p += blockDim.x) {
             a.idx[p] = R.picks[p];
             a.w[p] = R.pw[p];
         }
     if (u >= R.U) return;
     const int e = R.uexp[u], nt = R.ucnt[u], p0 = R.ustart[u];
-    constexpr int RIT = qd_rit(SPLMAX);
-    constexpr int RPW = (64 / LPR) * RIT;
-    const int row0 = (rb * QD_WAVES + wave) * RPW;
-    if (threadIdx.x < QD_MAXT) {
-        const int t = threadIdx.x;
-        const int p = R.upair[p0 + min(t, nt - 1)];
-        xp[t] = a.x + (size_t)(p / K) * H;
-        yp[t] = a.act + (size_t)p * I;
+    if (threadIdx.x < nt) {
+        const int p = R.upair[p0 + threadIdx.x];
+        vin[threadIdx.x] = p / K;
+        vout[threadIdx.x] = p;
     }
     __syncthreads();
     // Split banks: gate and up [E, I, H]; fused: gate_up [E, 2I, H], gate rows
@@ -344,23 +367,20 @@ __global__ __launch_bounds__(QD_WAVES * 64) void k_decode_experts(QdArgs a)
         gm = {a.m.gate_up.w + off * words, a.m.gate_up.s + off * groups, a.m.gate_up.b + off * groups};
         um = {gm.w + (size_t)I * words, gm.s + (size_t)I * groups, gm.b + (size_t)I * groups};
     }
-    if (row0 < I) qd_glu_rows<LPR, SPLMAX, RIT>(gm, um, I, H, a.lgG, row0, nt, xp, yp);
+    qd_glu_block<LPR, NUL>(gm, um, I, H, a.lgG, rb * RPB, nt, a.tch, one, xs, a.qx, vin, vout, a.qact, ys);
 }
 
 // ---- down: the shared expert and every expert of a token, and the combine -------
 //
-// A workgroup owns RIT * 64/LPR output rows of one token; wave w computes those
-// rows of matrix w, w + nw, ... (matrix 0 = the shared expert, matrix 1 + k =
-// the token's k-th expert), so each wave has one round of loads in flight.
-// The per-matrix rows meet in LDS and the combine runs in slot order.
-#define QD_DOWN_MAXW 16
-static __host__ __device__ constexpr int qd_down_rit(int splmax) { return splmax <= 2 ? 4 : splmax <= 4 ? 2 : 1; }
-
-template <int LPR, int SPLMAX>
+// A workgroup owns RPG = QD_DOWN_RIT * 64/LPR output rows of one token; wave m
+// computes those rows of matrix m (0 = the shared expert, 1 + k = the token's
+// k-th expert) against that matrix's staged input, so each wave has one round
+// of loads in flight.  The per-matrix rows meet in LDS and the combine runs in
+// slot order.
+template <int LPR, int NUL>
 __global__ __launch_bounds__(QD_DOWN_MAXW * 64) void k_decode_down(QdArgs a)
 {
-    constexpr int RIT = qd_down_rit(SPLMAX);
-    constexpr int SLOTS = 64 / LPR, RPG = SLOTS * RIT;
+    constexpr int RPP = 64 / LPR, RPG = RPP * QD_DOWN_RIT;
     __shared__ float ys[QWK_ROUTE_MAX_K + 1][RPG];
     const int H = a.m.H, I = a.m.I, SI = a.m.SI, K = a.m.K;
     const int rb = blockIdx.x % a.n_down_rb, t = blockIdx.x / a.n_down_rb;
@@ -370,68 +390,57 @@ __global__ __launch_bounds__(QD_DOWN_MAXW * 64) void k_decode_down(QdArgs a)
     const int lgG = a.lgG;
     for (int m = wave; m <= K; m += nw) {
         const int kin = m == 0 ? SI : I;
-        const int words = kin / 8, groups = kin >> lgG, spl = (kin / 32) / LPR;
+        const int units = kin / 16, words = kin / 8, groups = kin >> lgG;
         const uint32_t *wm = a.m.sh_down.w;
         const uint16_t *sm = a.m.sh_down.s, *bm = a.m.sh_down.b;
-        const float *av = a.shact + (size_t)t * SI;
+        const uint4 *xv = a.qsh + (size_t)t * (SI / 16) * 3;
         if (m > 0) {
             const size_t e = (size_t)a.idx[t * K + m - 1];
             wm = a.m.down.w + e * H * words;
             sm = a.m.down.s + e * H * groups;
             bm = a.m.down.b + e * H * groups;
-            av = a.act + ((size_t)t * K + m - 1) * I;
+            xv = a.qact + ((size_t)t * K + m - 1) * (I / 16) * 3;
         }
-        uint4 wv[SPLMAX][RIT];
-        float sc[SPLMAX][RIT], bi[SPLMAX][RIT];
+        uint2 wv[NUL][QD_DOWN_RIT];
+        float sc[NUL][QD_DOWN_RIT], bi[NUL][QD_DOWN_RIT];
+        uint4 xp[NUL][3];
 #pragma unroll
-        for (int j = 0; j < SPLMAX; j++) {
-            const int seg = j * LPR + lr, g = (seg * 32) >> lgG;
+        for (int j = 0; j < NUL; j++) {
+            const int c = j * LPR + lr;
+            const int g = (16 * c) >> lgG;
 #pragma unroll
-            for (int i = 0; i < RIT; i++) {
-                const int row = row0 + slot + SLOTS * i;
-                if (j < spl && row < H) {
-                    wv[j][i] = *reinterpret_cast<const uint4 *>(wm + (size_t)row * words + seg * 4);
+            for (int i = 0; i < QD_DOWN_RIT; i++) {
+                const int row = row0 + slot + RPP * i;
+                if (c < units && row < H) {
+                    wv[j][i] = *reinterpret_cast<const uint2 *>(wm + (size_t)row * words + 2 * c);
                     sc[j][i] = qw_bf16(sm[(size_t)row * groups + g]);
                     bi[j][i] = qw_bf16(bm[(size_t)row * groups + g]);
                 } else {
-                    wv[j][i] = make_uint4(0, 0, 0, 0);
-                    sc[j][i] = 0.0f;
-                    bi[j][i] = 0.0f;
+                    wv[j][i] = make_uint2(0, 0);
+                    sc[j][i] = bi[j][i] = 0.0f;
                 }
             }
-        }
-        float y[RIT];
-#pragma unroll
-        for (int i = 0; i < RIT; i++) y[i] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < SPLMAX; j++) {
-            if (j < spl) {
-                const int seg = j * LPR + lr;
-                float xs[32];
-                const float4 *xv = reinterpret_cast<const float4 *>(av + seg * 32);
-#pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    const float4 v = xv[q];
-                    xs[4 * q] = v.x; xs[4 * q + 1] = v.y; xs[4 * q + 2] = v.z; xs[4 * q + 3] = v.w;
-                }
-                float xsum = 0.0f;
-#pragma unroll
-                for (int q = 0; q < 32; q++) xsum += xs[q];
-#pragma unroll
-                for (int i = 0; i < RIT; i++) {
-                    float d = qw_dot8_q(wv[j][i].x, xs, 0.0f);
-                    d = qw_dot8_q(wv[j][i].y, xs + 8, d);
-                    d = qw_dot8_q(wv[j][i].z, xs + 16, d);
-                    d = qw_dot8_q(wv[j][i].w, xs + 24, d);
-                    y[i] = __builtin_fmaf(sc[j][i], d, y[i]);
-                    y[i] = __builtin_fmaf(bi[j][i], xsum, y[i]);
-                }
+            if (c < units) {
+                const uint4 *src = xv + (size_t)c * 3;
+                xp[j][0] = src[0]; xp[j][1] = src[1]; xp[j][2] = src[2];
+            } else {
+                xp[j][0] = xp[j][1] = xp[j][2] = make_uint4(0, 0, 0, 0);
             }
         }
+        float y[QD_DOWN_RIT];
 #pragma unroll
-        for (int i = 0; i < RIT; i++) {
+        for (int i = 0; i < QD_DOWN_RIT; i++) y[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NUL; j++) {
+            const float4 r = *reinterpret_cast<const float4 *>(&xp[j][2]);
+#pragma unroll
+            for (int i = 0; i < QD_DOWN_RIT; i++)
+                y[i] = qw_unit_dot(wv[j][i], xp[j][0], xp[j][1], r, sc[j][i], bi[j][i], y[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < QD_DOWN_RIT; i++) {
             const float v = qw_xor_sum<LPR>(y[i]);
-            if (lr == 0) ys[m][slot + SLOTS * i] = v;
+            if (lr == 0) ys[m][slot + RPP * i] = v;
         }
     }
     __syncthreads();
@@ -452,83 +461,85 @@ extern "C" size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows)
     return qd_layout(M, rows).total;
 }
 
-extern "C" int qwk_moe_decode_counters(const qwk_moe *M)
+template <int LPR, int NUL>
+static void launch_experts(hipStream_t s, QdArgs &a)
 {
-    (void)M;
-    return 0;
+    const dim3 grid(a.n_shared_wg + a.umax * a.gu_wg_per_u), blk(QD_GU_WAVES * 64);
+    const size_t lds = (size_t)a.tch * (a.m.H / 16) * QW_Q16_BYTES;
+    if (a.m.E <= 256) hipLaunchKernelGGL((k_decode_experts<LPR, NUL, 4>), grid, blk, lds, s, a);
+    else if (a.m.E <= 512) hipLaunchKernelGGL((k_decode_experts<LPR, NUL, 8>), grid, blk, lds, s, a);
+    else hipLaunchKernelGGL((k_decode_experts<LPR, NUL, 16>), grid, blk, lds, s, a);
 }
 
-template <int LPR, int SPLMAX>
-static void launch_fe(hipStream_t s, QdArgs &a, hipEvent_t *ev)
-{
-    if (ev) (void)hipEventRecord(ev[0], s);
-    hipLaunchKernelGGL((k_decode_front<LPR, SPLMAX>), dim3(a.n_router_wg + a.n_shared_wg),
-                       dim3(QD_WAVES * 64), 0, s, a);
-    if (ev) (void)hipEventRecord(ev[1], s);
-    const dim3 grid(a.umax * a.gu_wg_per_u), blk(QD_WAVES * 64);
-    if (a.m.E <= 256) hipLaunchKernelGGL((k_decode_experts<LPR, SPLMAX, 4>), grid, blk, 0, s, a);
-    else if (a.m.E <= 512) hipLaunchKernelGGL((k_decode_experts<LPR, SPLMAX, 8>), grid, blk, 0, s, a);
-    else hipLaunchKernelGGL((k_decode_experts<LPR, SPLMAX, 16>), grid, blk, 0, s, a);
-    if (ev) (void)hipEventRecord(ev[2], s);
-}
-
-template <int LPR>
-static bool launch_fe_spl(int splmax, hipStream_t s, QdArgs &a, hipEvent_t *ev)
-{
-    switch (splmax) {
-    case 1: launch_fe<LPR, 1>(s, a, ev); return true;
-    case 2: launch_fe<LPR, 2>(s, a, ev); return true;
-    case 3: launch_fe<LPR, 3>(s, a, ev); return true;
-    case 4: launch_fe<LPR, 4>(s, a, ev); return true;
-    case 8: launch_fe<LPR, 8>(s, a, ev); return true;
-    default: return false;
-    }
-}
-
-template <int LPR, int SPLMAX>
+template <int LPR, int NUL>
 static void launch_down(hipStream_t s, QdArgs &a)
 {
     const int nw = a.m.K + 1 < QD_DOWN_MAXW ? a.m.K + 1 : QD_DOWN_MAXW;
-    hipLaunchKernelGGL((k_decode_down<LPR, SPLMAX>), dim3(a.rows * a.n_down_rb), dim3(nw * 64), 0, s, a);
+    hipLaunchKernelGGL((k_decode_down<LPR, NUL>), dim3(a.rows * a.n_down_rb), dim3(nw * 64), 0, s, a);
 }
 
-template <int LPR>
-static bool launch_down_spl(int splmax, hipStream_t s, QdArgs &a)
+// Instantiates F<LPR, NUL> for the supported (LPR, NUL) pairs.
+#define QD_DISPATCH_GU(F, lpr, nul, ...)                                               \
+    do {                                                                               \
+        ok = true;                                                                     \
+        switch ((lpr) * 16 + (nul)) {                                                  \
+        case 16 * 16 + 1: F<16, 1>(__VA_ARGS__); break;                                \
+        case 16 * 16 + 2: F<16, 2>(__VA_ARGS__); break;                                \
+        case 16 * 16 + 3: F<16, 3>(__VA_ARGS__); break;                                \
+        case 16 * 16 + 4: F<16, 4>(__VA_ARGS__); break;                                \
+        case 32 * 16 + 2: F<32, 2>(__VA_ARGS__); break;                                \
+        case 32 * 16 + 3: F<32, 3>(__VA_ARGS__); break;                                \
+        case 32 * 16 + 4: F<32, 4>(__VA_ARGS__); break;                                \
+        case 64 * 16 + 2: F<64, 2>(__VA_ARGS__); break;                                \
+        case 64 * 16 + 3: F<64, 3>(__VA_ARGS__); break;                                \
+        case 64 * 16 + 4: F<64, 4>(__VA_ARGS__); break;                                \
+        default: ok = false;                                                           \
+        }                                                                              \
+    } while (0)
+#define QD_DISPATCH_DOWN(F, nul, ...)                                                  \
+    do {                                                                               \
+        ok = true;                                                                     \
+        switch (nul) {                                                                 \
+        case 1: F<16, 1>(__VA_ARGS__); break;                                          \
+        case 2: F<16, 2>(__VA_ARGS__); break;                                          \
+        case 3: F<16, 3>(__VA_ARGS__); break;                                          \
+        case 4: F<16, 4>(__VA_ARGS__); break;                                          \
+        default: ok = false;                                                           \
+        }                                                                              \
+    } while (0)
+
+// Lane layouts: gate / up rows have k = H; down rows k = I (routed) or SI
+// (shared), one layout covering the larger.  Units per lane at most 4.
+static bool qd_shapes(const qwk_moe *M, int *lpr_h, int *nul_h, int *nul_d)
 {
-    switch (splmax) {
-    case 1: launch_down<LPR, 1>(s, a); return true;
-    case 2: launch_down<LPR, 2>(s, a); return true;
-    case 3: launch_down<LPR, 3>(s, a); return true;
-    case 4: launch_down<LPR, 4>(s, a); return true;
-    case 8: launch_down<LPR, 8>(s, a); return true;
-    default: return false;
-    }
+    const int uh = M->H / 16, ud = (M->I > M->SI ? M->I : M->SI) / 16;
+    *lpr_h = qd_lpr(uh);
+    *nul_h = qd_nul(uh, *lpr_h);
+    *nul_d = qd_nul(ud, 16);
+    return *nul_h > 0 && *nul_h <= 4 && *nul_d > 0 && *nul_d <= 4;
+}
+
+extern "C" int qwk_moe_decode_supported(const qwk_moe *M, int rows)
+{
+    int a, b, c;
+    const int G = M->group;
+    return rows >= 1 && rows <= QWK_DECODE_MAX_ROWS && M->K >= 1 && M->K <= QWK_ROUTE_MAX_K &&
+           M->E >= M->K && M->E <= QWK_ROUTE_MAX_E && M->H % 64 == 0 && M->I % 16 == 0 &&
+           M->SI % 16 == 0 && M->H <= QWK_DMAT_MAX_K && (G == 32 || G == 64 || G == 128) &&
+           M->H % G == 0 && M->I % G == 0 && M->SI % G == 0 && qd_shapes(M, &a, &b, &c);
 }
 
 extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
                               const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes,
-                              int *counters, int ncounters, hipEvent_t *ev)
+                              hipEvent_t *ev)
 {
-    (void)counters; (void)ncounters;
     const int G = M->group;
-    if (rows < 1 || rows > QWK_DECODE_MAX_ROWS || M->K < 1 || M->K > QWK_ROUTE_MAX_K ||
-        M->E < M->K || M->E > QWK_ROUTE_MAX_E || M->H % 64 || M->I % 32 || M->SI % 32 ||
-        M->H > QWK_DMAT_MAX_K || (G != 32 && G != 64 && G != 128) ||
-        M->H % G || M->I % G || M->SI % G || ((uintptr_t)x & 15u))
-        return (int)hipErrorInvalidValue;
+    if (!qwk_moe_decode_supported(M, rows) || ((uintptr_t)x & 15u)) return (int)hipErrorInvalidValue;
     const QdLayout L = qd_layout(M, rows);
     if (scratch_bytes < L.total) return (int)hipErrorInvalidValue;
-    // Lanes per row: k = H for the front and expert launches; for down one
-    // width that divides the segment counts of both I and SI.
-    const int lpr_h = qd_lpr(M->H);
-    int lpr_d = qd_lpr(M->I);
-    const int lpr_si = qd_lpr(M->SI);
-    if (lpr_si < lpr_d) lpr_d = lpr_si;
-    const int kmax_d = M->I > M->SI ? M->I : M->SI;
-    if ((M->H / 32) / lpr_h > 8 || (kmax_d / 32) / lpr_d > 8 || lpr_h < 2 || lpr_d < 2)
-        return (int)hipErrorInvalidValue;
-    const int spl_h = qd_splmax((M->H / 32) / lpr_h);
-    const int spl_d = qd_splmax((kmax_d / 32) / lpr_d);
+    int lpr_h, nul_h, nul_d;
+    qd_shapes(M, &lpr_h, &nul_h, &nul_d);
+    const int lpr_d = 16;
 
     char *S = (char *)scratch;
     QdArgs a;
@@ -536,36 +547,28 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     a.x = x; a.out = out; a.idx = idx; a.w = w; a.rows = rows;
     a.umax = rows * M->K < M->E ? rows * M->K : M->E;
     a.lgG = G == 32 ? 5 : G == 64 ? 6 : 7;
-    a.n_router_wg = (M->E + 1 + QD_WAVES - 1) / QD_WAVES;
-    const int rpg_h = QD_WAVES * (64 / lpr_h) * qd_rit(spl_h);
-    a.n_shared_wg = (M->SI + rpg_h - 1) / rpg_h;
-    a.gu_wg_per_u = (M->I + rpg_h - 1) / rpg_h;
-    a.down_rows_per_wg = qd_down_rit(spl_d) * (64 / lpr_d);
-    a.n_down_rb = (M->H + a.down_rows_per_wg - 1) / a.down_rows_per_wg;
+    a.n_router_wg = (M->E + 1 + QD_FRONT_WAVES - 1) / QD_FRONT_WAVES;
+    const int rpb = QD_GU_WAVES * (64 / lpr_h);
+    const int vbytes = (M->H / 16) * QW_Q16_BYTES;
+    a.tch = QD_GU_LDS / vbytes < rows ? QD_GU_LDS / vbytes : rows;
+    a.n_shared_wg = (M->SI + rpb - 1) / rpb;
+    a.gu_wg_per_u = (M->I + rpb - 1) / rpb;
+    a.n_down_rb = (M->H + QD_DOWN_RIT * (64 / lpr_d) - 1) / (QD_DOWN_RIT * (64 / lpr_d));
     a.logits = (float *)(S + L.logits);
     a.g1 = (float *)(S + L.g1);
-    a.shact = (float *)(S + L.shact);
-    a.act = (float *)(S + L.act);
+    a.qx = (uint4 *)(S + L.qx);
+    a.qsh = (uint4 *)(S + L.qsh);
+    a.qact = (uint4 *)(S + L.qact);
 
     bool ok;
-    switch (lpr_h) {
-    case 2: ok = launch_fe_spl<2>(spl_h, s, a, ev); break;
-    case 4: ok = launch_fe_spl<4>(spl_h, s, a, ev); break;
-    case 8: ok = launch_fe_spl<8>(spl_h, s, a, ev); break;
-    case 16: ok = launch_fe_spl<16>(spl_h, s, a, ev); break;
-    case 32: ok = launch_fe_spl<32>(spl_h, s, a, ev); break;
-    default: ok = launch_fe_spl<64>(spl_h, s, a, ev); break;
-    }
+    if (ev) (void)hipEventRecord(ev[0], s);
+    hipLaunchKernelGGL(k_decode_front, dim3(a.n_router_wg + rows), dim3(QD_FRONT_WAVES * 64), 0, s, a);
+    if (ev) (void)hipEventRecord(ev[1], s);
+    QD_DISPATCH_GU(launch_experts, lpr_h, nul_h, s, a);
     if (!ok) return (int)hipErrorInvalidValue;
-    switch (lpr_d) {
-    case 2: ok = launch_down_spl<2>(spl_d, s, a); break;
-    case 4: ok = launch_down_spl<4>(spl_d, s, a); break;
-    case 8: ok = launch_down_spl<8>(spl_d, s, a); break;
-    case 16: ok = launch_down_spl<16>(spl_d, s, a); break;
-    case 32: ok = launch_down_spl<32>(spl_d, s, a); break;
-    default: ok = launch_down_spl<64>(spl_d, s, a); break;
-    }
+    if (ev) (void)hipEventRecord(ev[2], s);
+    QD_DISPATCH_DOWN(launch_down, nul_d, s, a);
+    if (!ok) return (int)hipErrorInvalidValue;
     if (ev) (void)hipEventRecord(ev[3], s);
-    if (!ok) return (int)hipErrorInvalidValue;
     return (int)hipGetLastError();
 }

@@ -144,27 +144,135 @@ __device__ __forceinline__ float qw_dot8_q(uint32_t w, const float *x, float acc
     return acc;
 }
 
+// ---- q16: activations staged for the 4-bit dot ----------------------------------
+//
+// An activation vector is staged in units of 16 elements, 48 bytes each:
+//
+//   pairs[2]  uint4 per 8-element word: f16 pairs (h0,h4) (h2,h6) (h1,h5) (h3,h7)
+//   rec       float4 { X = sum of the unit's values as staged, unscaled,
+//                      Y = 1024 * (sum of even positions) + 64 * (sum of odd),
+//                      f = 2^-sh, 0 }
+//
+// where h = f16(x * 2^sh) with sh chosen per unit so that the unit's largest
+// magnitude lands in [2^14, 2^15): no f16 overflow, full f16 precision.
+//
+// A packed word w holds nibbles q0..q7 (q_i at bit 4i).  Inserting the
+// nibbles into the f16 pattern 0x6400 (1024.0) gives exact f16 values:
+//   bfi(0x000F000F, w)      -> (1024 + q0, 1024 + q4)
+//   bfi(0x00F000F0, w)      -> (1024 + 16 q1, 1024 + 16 q5)
+//   bfi(0x000F000F, w >> 8) -> (1024 + q2, 1024 + q6)
+//   bfi(0x00F000F0, w >> 8) -> (1024 + 16 q3, 1024 + 16 q7)
+// so two fp32 dot2 chains give d = sum_even (1024 + q) h and
+// d2 = sum_odd (1024 + 16 q) h, and sum_i q_i h_i = d + d2/16 - Y exactly up
+// to fp32 rounding.  A unit against one row of a group with scale s, bias b:
+//   s * sum q x + b * sum x = (s f) (d + d2/16 - Y) + b X.
+#define QW_Q16_BYTES 48
+
+typedef _Float16 qw_h2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t qw_bfi(uint32_t mask, uint32_t w, uint32_t base)
+{
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(w), "v"(base));
+    return r;
+}
+
+__device__ __forceinline__ float qw_dot2(uint32_t a, uint32_t b, float c)
+{
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(qw_h2, a), __builtin_bit_cast(qw_h2, b), c, false);
+}
+
+// One packed word against its four staged pairs: d += even terms, d2 += odd.
+__device__ __forceinline__ void qw_word_dot(uint32_t w, uint4 xp, uint32_t magic, float &d, float &d2)
+{
+    const uint32_t w8 = w >> 8;
+    d = qw_dot2(qw_bfi(0x000F000Fu, w, magic), xp.x, d);
+    d2 = qw_dot2(qw_bfi(0x00F000F0u, w, magic), xp.z, d2);
+    d = qw_dot2(qw_bfi(0x000F000Fu, w8, magic), xp.y, d);
+    d2 = qw_dot2(qw_bfi(0x00F000F0u, w8, magic), xp.w, d2);
+}
+
+// One staged unit x (p0, p1, r) against 16 nibbles (w0, w1) of a row with
+// group scale s and bias b: acc += s * sum q x + b * sum x.
+__device__ __forceinline__ float qw_unit_dot(uint2 w, uint4 p0, uint4 p1, float4 r, float s, float b, float acc)
+{
+    const uint32_t magic = 0x64006400u;
+    // Keeps the dequantised halves (8 registers a word) from being built
+    // ahead of their use -- across units or out of a token loop: each unit's
+    // are rebuilt right before its dot products.
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" : "+v"(w.x), "+v"(w.y));
+    float d = 0.0f, d2 = 0.0f;
+    qw_word_dot(w.x, p0, magic, d, d2);
+    qw_word_dot(w.y, p1, magic, d, d2);
+    const float t = __builtin_fmaf(d2, 0.0625f, d) - r.y;
+    acc = __builtin_fmaf(b, r.x, acc);
+    return __builtin_fmaf(s * r.z, t, acc);
+}
+
+__device__ __forceinline__ uint32_t qw_pack_h2(float a, float b)
+{
+    qw_h2 h = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
+// Stages 16 values into one unit at dst (three uint4 stores).
+__device__ __forceinline__ void qw_q16_stage(const float v[16], uint4 *dst)
+{
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[i]));
+    int sh = 0;
+    if (m > 0.0f && m <= 3.40282346638528859812e+38f) {
+        sh = 15 - __builtin_amdgcn_frexp_expf(m);
+        sh = sh < -126 ? -126 : sh > 126 ? 126 : sh;
+    }
+    float h[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) h[i] = (float)(_Float16)__builtin_ldexpf(v[i], sh);
+    float xa = 0.0f, xb = 0.0f;
+#pragma unroll
+    for (int wd = 0; wd < 2; wd++) {
+        const float *q = h + 8 * wd;
+        dst[wd] = make_uint4(qw_pack_h2(q[0], q[4]), qw_pack_h2(q[2], q[6]),
+                             qw_pack_h2(q[1], q[5]), qw_pack_h2(q[3], q[7]));
+        xa += (q[0] + q[4]) + (q[2] + q[6]);
+        xb += (q[1] + q[5]) + (q[3] + q[7]);
+    }
+    const float f = __builtin_ldexpf(1.0f, -sh);
+    const float4 r = make_float4((xa + xb) * f, __builtin_fmaf(1024.0f, xa, 64.0f * xb), f, 0.0f);
+    dst[2] = *reinterpret_cast<const uint4 *>(&r);
+}
+
 // ---- routing of one token ----------------------------------------------------------
 //
 // Softmax over E logits and the K picks of a serial scan with strict '>'
 // from e = 0 -- the K largest probabilities, ties to the lower expert, in
-// descending (p, then ascending index) order -- by one wave, exactly:
+// descending (p, then ascending index) order -- by one wave, exactly, as a
+// K-round tournament:
 //
-//   1. key_e = bits(p_e) + 1 for every expert (p >= 0, so the bits order as
-//      the values; 0 marks a lane slot past E).
-//   2. Radix select: the K-th largest key T, one bit at a time from the top,
-//      counting keys >= candidate with ballots (no cross-lane data moves).
-//   3. Select every key > T and, of the keys == T, the lowest-indexed
-//      K - #(> T).
-//   4. The K selected entries are compacted into LDS, and each of K lanes
-//      counts the entries ahead of its own: its output position.
+//   each lane keeps the best of its own experts (lane, lane + 64, ...: the
+//   first of equal values, so the lowest index); a round takes the wave's
+//   largest value V, and of the lanes holding V the lowest candidate index
+//   (one ballot bit in the common case, a min-reduction otherwise); the
+//   owning lane retires that expert (p = -1, below every probability) and
+//   rescans its slots.
 //
-// Lane l holds experts l, l + 64, ..., so expert order is slot-major.
-// `lds` is this wave's scratch of 4 * QWK_ROUTE_MAX_K ints.  Every lane ends
-// holding pick `lane` (lane < K) in *pick_i / *pick_w.
+// The renormalising sum adds the picks in pick order, as the serial scan
+// does.  Every lane ends holding pick `lane` (lane < K) in *pick_i / *pick_w.
+__device__ __forceinline__ int qw_wave_min_i(int v)
+{
+    v = min(v, qw_dpp_i<QW_DPP_XOR1>(v));
+    v = min(v, qw_dpp_i<QW_DPP_XOR2>(v));
+    v = min(v, qw_dpp_i<QW_DPP_HMIRROR>(v));
+    v = min(v, qw_dpp_i<QW_DPP_MIRROR>(v));
+    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
 template <int PL>
 __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E, int K, int norm,
-                                              int lane, int *pick_i, float *pick_w, int *lds)
+                                              int lane, int *pick_i, float *pick_w)
 {
     float v[PL];
     float m = -__builtin_huge_valf();
@@ -182,64 +290,40 @@ __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E
         if (e < E) { v[j] = qw_exp_spec(v[j] - m); s = s + v[j]; }
     }
     s = qw_xor_sum<64>(s);
-    uint32_t key[PL];
+    // probabilities; -2 marks a slot past E (below a retired -1)
 #pragma unroll
-    for (int j = 0; j < PL; j++) {
-        const int e = lane + 64 * j;
-        key[j] = e < E ? __float_as_uint(v[j] / s) + 1u : 0u;
-    }
-    // 2. the K-th largest key
-    uint32_t T = 0;
-    for (int b = 30; b >= 0; b--) {
-        const uint32_t cand = T | (1u << b);
-        int cnt = 0;
+    for (int j = 0; j < PL; j++) v[j] = lane + 64 * j < E ? v[j] / s : -2.0f;
+    float bv = v[0];
+    int bj = 0;
 #pragma unroll
-        for (int j = 0; j < PL; j++) cnt += __popcll(__ballot(key[j] >= cand));
-        if (cnt >= K) T = cand;
-    }
-    // 3. the selection
-    int gt = 0;
-#pragma unroll
-    for (int j = 0; j < PL; j++) gt += __popcll(__ballot(key[j] > T));
-    const int need = K - gt;
-    const unsigned long long below = (1ull << lane) - 1ull;
-    int eq_before = 0, sel_before = 0;
-    int *ek = lds, *ei = lds + QWK_ROUTE_MAX_K;
-#pragma unroll
-    for (int j = 0; j < PL; j++) {
-        const unsigned long long eq = __ballot(key[j] == T);
-        const bool is_eq = key[j] == T;
-        const int r = eq_before + __popcll(eq & below);
-        const bool sel = key[j] > T || (is_eq && r < need);
-        const unsigned long long sm = __ballot(sel);
-        if (sel) {
-            const int pos = sel_before + __popcll(sm & below);
-            ek[pos] = (int)key[j];
-            ei[pos] = lane + 64 * j;
-        }
-        eq_before += __popcll(eq);
-        sel_before += __popcll(sm);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    // 4. positions: entries ahead = larger key, or equal key and lower index
-    const uint32_t mk = lane < K ? (uint32_t)ek[lane] : 0u;
-    const int mi = lane < K ? ei[lane] : 0;
-    int rank = 0;
+    for (int j = 1; j < PL; j++)
+        if (v[j] > bv) { bv = v[j]; bj = j; }
+    float wsum = 0.0f, mine_w = 0.0f;
+    int mine_i = 0;
     for (int n = 0; n < K; n++) {
-        const uint32_t kn = (uint32_t)__builtin_amdgcn_readlane((int)mk, n);
-        const int in = __builtin_amdgcn_readlane(mi, n);
-        rank += (kn > mk || (kn == mk && in < mi)) ? 1 : 0;
+        const float V = qw_wave_max(bv);
+        const unsigned long long at = __ballot(bv == V);
+        int I;
+        if ((at & (at - 1)) == 0) {
+            const int owner = __builtin_ctzll(at);
+            I = owner + 64 * __builtin_amdgcn_readlane(bj, owner);
+        } else {
+            I = qw_wave_min_i(bv == V ? lane + 64 * bj : 0x7FFFFFFF);
+        }
+        wsum = wsum + V;
+        if (lane == n) { mine_i = I; mine_w = V; }
+        if (lane == (I & 63)) {
+            const int jr = I >> 6;
+#pragma unroll
+            for (int j = 0; j < PL; j++)
+                if (j == jr) v[j] = -1.0f;
+            bv = v[0];
+            bj = 0;
+#pragma unroll
+            for (int j = 1; j < PL; j++)
+                if (v[j] > bv) { bv = v[j]; bj = j; }
+        }
     }
-    int *ok = lds + 2 * QWK_ROUTE_MAX_K, *oi = lds + 3 * QWK_ROUTE_MAX_K;
-    __builtin_amdgcn_wave_barrier();
-    if (lane < K) { ok[rank] = (int)mk; oi[rank] = mi; }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    const float mine_w = lane < K ? __uint_as_float((uint32_t)ok[lane] - 1u) : 0.0f;
-    const int mine_i = lane < K ? oi[lane] : 0;
-    float wsum = 0.0f;
-    for (int n = 0; n < K; n++) wsum = wsum + qw_lane(mine_w, n);
     *pick_i = mine_i;
     *pick_w = norm ? mine_w / wsum : mine_w;
 }

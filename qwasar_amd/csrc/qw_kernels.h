@@ -77,19 +77,18 @@ typedef struct {
     const uint16_t *sh_gate_w;       /* bf16 [H] */
 } qwk_moe;
 
-/* Bytes of device scratch the decode path needs for `rows` tokens, and the
- * number of int arrival counters it needs.  The counters must be zero before
- * the first call and are left zero by every call that completes; they must
- * not share memory with anything else. */
+/* Bytes of device scratch the decode path needs for `rows` tokens.  Nothing
+ * in it needs to be initialised. */
 size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows);
-int qwk_moe_decode_counters(const qwk_moe *M);
+/* Non-zero when the decode path takes this layer shape and token count. */
+int qwk_moe_decode_supported(const qwk_moe *M, int rows);
 /* Decode (rows <= QWK_DECODE_MAX_ROWS): out [rows, H], idx/w [rows, K]. */
 #define QWK_DECODE_MAX_ROWS 8
 /* `ev`, when not NULL, holds 4 events recorded on `s` before the first
  * launch and after each of the three (front, experts, down). */
 int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
                    const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes,
-                   int *counters, int ncounters, hipEvent_t *ev);
+                   hipEvent_t *ev);
 
 #ifdef __cplusplus
 }

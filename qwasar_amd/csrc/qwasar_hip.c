@@ -73,8 +73,6 @@ static struct {
     qw_cmd live;
     void *scratch;
     size_t scratch_len;
-    int *counters;       /* the decode path's arrival counters, zero between calls */
-    int ncounters;
 } G;
 
 /* ---- profiling table ---------------------------------------------------- */
@@ -158,9 +156,6 @@ void qw_gpu_shutdown(void) {
     if (G.scratch) hipFree(G.scratch);
     G.scratch = NULL;
     G.scratch_len = 0;
-    if (G.counters) hipFree(G.counters);
-    G.counters = NULL;
-    G.ncounters = 0;
     hipStreamDestroy(G.stream);
     G.ready = 0;
 }
@@ -623,9 +618,7 @@ static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const floa
     return rc == 0;
 }
 
-/* Decode: the fused launches over only the selected experts. */
-static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float *x,
-                       const qw_moe_layer *M, int32_t rows) {
+static void moe_desc(qwk_moe *mp, const qw_moe_layer *M) {
     qwk_moe m;
     m.H = M->H; m.E = M->E; m.K = M->K; m.I = M->I; m.SI = M->SI;
     m.group = M->split ? M->gate.group : M->gate_up.group;
@@ -636,30 +629,22 @@ static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float
     m.down = q4r(&M->down);
     m.sh_gate = q4r(&M->sh_gate); m.sh_up = q4r(&M->sh_up); m.sh_down = q4r(&M->sh_down);
     m.sh_gate_w = dp(M->sh_gate_w);
+    *mp = m;
+}
+
+/* Decode: the fused launches over only the selected experts. */
+static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float *x,
+                       const qwk_moe *mp, int32_t rows) {
+    const qwk_moe m = *mp;
     const size_t need = qwk_moe_decode_scratch(&m, rows);
     void *S = scratch(need);
     if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", need); return false; }
-    /* Arrival counters live apart from the scratch, which the prefill path
-     * overwrites: zeroed once when (re)allocated, left zero by each call. */
-    const int nctr = qwk_moe_decode_counters(&m);
-    if (nctr > G.ncounters) {
-        hipStreamSynchronize(G.stream);
-        if (G.counters) hipFree(G.counters);
-        G.counters = NULL;
-        G.ncounters = 0;
-        if (hipMalloc((void **)&G.counters, (size_t)nctr * sizeof(int)) != hipSuccess) {
-            cmd_fail(c, hipErrorOutOfMemory, "moe_layer: counters");
-            return false;
-        }
-        hipMemset(G.counters, 0, (size_t)nctr * sizeof(int));
-        G.ncounters = nctr;
-    }
     /* Profiling charges each of the three launches to its own label. */
     hipEvent_t ev[4] = { NULL, NULL, NULL, NULL };
     int per_kernel = G.prof != 0;
     for (int i = 0; per_kernel && i < 4; i++)
         if (!(ev[i] = cmd_event(c, 0))) per_kernel = 0;
-    const int rc = qwk_moe_decode(G.stream, out, idx, w, x, &m, rows, S, need, G.counters, G.ncounters,
+    const int rc = qwk_moe_decode(G.stream, out, idx, w, x, &m, rows, S, need,
                                   per_kernel ? ev : NULL);
     if (per_kernel) {
         static const char *labels[3] = { "moe decode front", "moe decode experts", "moe decode down" };
@@ -683,7 +668,9 @@ bool qw_op_moe_layer(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,
     if (M->split) { touch_q4(c, &M->gate); touch_q4(c, &M->up); } else touch_q4(c, &M->gate_up);
     touch_q4(c, &M->down); touch_q4(c, &M->sh_gate); touch_q4(c, &M->sh_up); touch_q4(c, &M->sh_down);
     touch(c, out, 1); touch(c, idx, 1); touch(c, w, 1);
-    if (rows > QWK_DECODE_MAX_ROWS)
+    qwk_moe m;
+    moe_desc(&m, M);
+    if (rows > QWK_DECODE_MAX_ROWS || !qwk_moe_decode_supported(&m, rows))
         return moe_prefill(c, dp(out), dp(idx), dp(w), dp(x), M, rows);
-    return moe_decode(c, dp(out), dp(idx), dp(w), dp(x), M, rows);
+    return moe_decode(c, dp(out), dp(idx), dp(w), dp(x), &m, rows);
 }

@@ -1,7 +1,12 @@
 """The whole MoE block through qw_op_moe_layer on the GPU against the CPU
 oracle: routing ids and weights bit-exact, outputs within the stated
-tolerance (max-abs 2e-2 and rel-L2 1e-3 is the bar; the fp32 decode path
-is held tighter)."""
+tolerance (max-abs 2e-2 and rel-L2 1e-3 is the bar).
+
+The decode path (<= 8 rows) feeds the 4-bit products with activations staged
+as f16 (each 16-element unit scaled by a power of two, fp32 accumulation):
+its rel-L2 against the fp32 oracle measures about 2.5e-4 on every case here,
+so it is held to DECODE_REL = 5e-4, inside the bar with room to catch a
+regression."""
 import os
 
 import numpy as np
@@ -35,6 +40,9 @@ def run_layer(gpu, lb, x):
             wb.read(np.float32, (rows, L.K)))
 
 
+DECODE_REL = 5e-4
+
+
 def check(got, want, tol_rel, tol_abs=2e-2):
     out, idx, w = got
     wout, widx, ww = want
@@ -55,7 +63,7 @@ def test_reference_fixture_banks(gpu, name):
     g = np.load(os.path.join(GOLD, "c0_golden.npz"))
     lb = gpu.LayerBufs(L)
     got = run_layer(gpu, lb, g[f"{tag}_x"])
-    check(got, (g[f"{tag}_out"], g[f"{tag}_idx"], g[f"{tag}_w"]), 1e-5)
+    check(got, (g[f"{tag}_out"], g[f"{tag}_idx"], g[f"{tag}_w"]), DECODE_REL)
     lb.free()
 
 
@@ -64,7 +72,7 @@ def test_config0_golden(gpu):
     g = np.load(os.path.join(GOLD, "c0_golden.npz"))
     assert np.array_equal(x, g["c0_x"])
     lb = gpu.LayerBufs(L)
-    check(run_layer(gpu, lb, x), (g["c0_out"], g["c0_idx"], g["c0_w"]), 1e-5)
+    check(run_layer(gpu, lb, x), (g["c0_out"], g["c0_idx"], g["c0_w"]), DECODE_REL)
     lb.free()
 
 
@@ -76,7 +84,22 @@ def test_config0_rows(gpu, rows, split):
     lb = gpu.LayerBufs(L)
     got = run_layer(gpu, lb, x)
     want = ref.moe_forward(L, x)
-    check(got, want, 1e-5 if rows <= 8 else 1e-3)
+    check(got, want, DECODE_REL if rows <= 8 else 1e-3)
+    lb.free()
+
+
+@pytest.mark.parametrize("mag", [1e5, 1e-5])
+def test_decode_input_magnitude(gpu, mag):
+    """Inputs far outside f16's range (1e5 * N(0,1) overflows it, 1e-5 * N(0,1)
+    is mostly subnormal) must still match: the staging scales each 16-element
+    unit by a power of two.  A few units hold one large outlier (1e4 times the
+    rest), which sets the unit's scale."""
+    L, x = synth.make_config(0, rows=3, seed=77)
+    x = (x * mag).astype(np.float32)
+    x[1, 5] *= 1e4
+    x[2, 40] = 0.0
+    lb = gpu.LayerBufs(L)
+    check(run_layer(gpu, lb, x), ref.moe_forward(L, x), DECODE_REL, tol_abs=np.inf)
     lb.free()
 
 
@@ -92,7 +115,7 @@ def test_config1_decode(gpu, c1):
     L, lb = c1
     for t in range(3):
         x = synth.make_x(500 + t, 1, L.H)
-        check(run_layer(gpu, lb, x), ref.moe_forward(L, x), 1e-5)
+        check(run_layer(gpu, lb, x), ref.moe_forward(L, x), DECODE_REL)
 
 
 def test_config2_decode_batch8_shared_experts(gpu, c1):
@@ -103,7 +126,7 @@ def test_config2_decode_batch8_shared_experts(gpu, c1):
     lb = gpu.LayerBufs(L)
     got = run_layer(gpu, lb, x)
     want = ref.moe_forward(L, x)
-    check(got, want, 1e-5)
+    check(got, want, DECODE_REL)
     for r in range(8):
         assert set(synth.C2_HOT) <= set(got[1][r].tolist())
     lb.free()

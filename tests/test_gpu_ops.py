@@ -51,6 +51,10 @@ def test_route_bit_exact(gpu, E, K, rows):
     # constructed ties: equal logits must go to the lower expert first
     lg[0, 3] = lg[0, 5] = lg[0, 7] = lg[0].max() + 1.0
     lg[1 % rows, :] = 0.25
+    if E >= 192 and rows > 2:
+        # equal values in one lane's slots (5, 69, 133 share a wave lane) and
+        # one more in another lane (131): ascending index order is required
+        lg[2, [133, 69, 5, 131]] = lg[2].max() + 2.0
     B = gpu.Buf
     lgb, ib, wb = B.of(lg), B(rows * K * 4), B(rows * K * 4)
     c = gpu.qw_cmd_begin()
@@ -63,6 +67,8 @@ def test_route_bit_exact(gpu, E, K, rows):
     assert np.array_equal(got_w.view(np.uint32), w.view(np.uint32)), "route weights not bit-exact"
     assert list(got_i[0, :3]) == [3, 5, 7][:min(K, 3)]
     assert list(got_i[1 % rows, :K]) == list(range(K))
+    if E >= 192 and rows > 2:
+        assert list(got_i[2, :4]) == [5, 69, 131, 133][:K]
 
 
 def test_route_refuses_oversize(gpu, capfd):
