@@ -317,8 +317,10 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
     __syncthreads();
 }
 
+// 8 waves per SIMD: two 16-wave workgroups per CU, which takes at most 64
+// VGPRs and 78 SGPRs a wave (at 80 SGPRs a CU holds one).
 template <int LPR, int NUL, int PL>
-__global__ __launch_bounds__(QD_GU_WAVES * 64) void k_decode_experts(QdArgs a)
+__global__ __launch_bounds__(QD_GU_WAVES * 64, 8) void k_decode_experts(QdArgs a)
 {
     extern __shared__ uint4 xs[];     // [tch][units][3]
     __shared__ QdRoute R;

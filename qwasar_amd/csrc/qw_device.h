@@ -20,9 +20,8 @@ __device__ __forceinline__ float qw_bf16(uint16_t v) {
 // polynomial in Horner form, then one ldexp.  Operations and order are fixed
 // so that the host restatement of the same method gives identical bits.
 __device__ __forceinline__ float qw_exp_spec(float x) {
-    if (x != x) return x;
-    if (x > 88.72283935546875f) return __builtin_huge_valf();
-    if (x < -103.972084045410f) return 0.0f;
+    // Branch-free: the polynomial runs on every input and the special cases
+    // are selected afterwards (their operands may overflow; they are dropped).
     const float kf = __builtin_rintf(__fmul_rn(x, 1.44269502162933349609375f));
     float r = __builtin_fmaf(kf, -0.693145751953125f, x);
     r = __builtin_fmaf(kf, -1.428606765330187045e-06f, r);
@@ -34,7 +33,11 @@ __device__ __forceinline__ float qw_exp_spec(float x) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return __builtin_ldexpf(p, (int)kf);
+    const int ki = (int)__builtin_fmaxf(__builtin_fminf(kf, 200.0f), -200.0f);
+    float y = __builtin_ldexpf(p, ki);
+    y = x < -103.972084045410f ? 0.0f : y;
+    y = x > 88.72283935546875f ? __builtin_huge_valf() : y;
+    return x != x ? x : y;
 }
 
 // Activation numerics: sigmoid(x) = 1 / (1 + e^-x), silu(x) = x * sigmoid(x),
@@ -101,27 +104,6 @@ __device__ __forceinline__ float qw_wave_max(float v)
     v = fmaxf(v, qw_dpp<QW_DPP_HMIRROR>(v));
     v = fmaxf(v, qw_dpp<QW_DPP_MIRROR>(v));
     return fmaxf(fmaxf(qw_lane(v, 0), qw_lane(v, 16)), fmaxf(qw_lane(v, 32), qw_lane(v, 48)));
-}
-
-// Arg-max over the wave: highest value, ties to the lowest index.  The same
-// (value, index) lands in every lane.
-__device__ __forceinline__ void qw_argmax_step(float &v, int &i, float ov, int oi)
-{
-    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
-}
-
-__device__ __forceinline__ void qw_wave_argmax(float &v, int &i)
-{
-    qw_argmax_step(v, i, qw_dpp<QW_DPP_XOR1>(v), qw_dpp_i<QW_DPP_XOR1>(i));
-    qw_argmax_step(v, i, qw_dpp<QW_DPP_XOR2>(v), qw_dpp_i<QW_DPP_XOR2>(i));
-    qw_argmax_step(v, i, qw_dpp<QW_DPP_HMIRROR>(v), qw_dpp_i<QW_DPP_HMIRROR>(i));
-    qw_argmax_step(v, i, qw_dpp<QW_DPP_MIRROR>(v), qw_dpp_i<QW_DPP_MIRROR>(i));
-    float bv = qw_lane(v, 0);
-    int bi = __builtin_amdgcn_readlane(i, 0);
-#pragma unroll
-    for (int r = 1; r < 4; r++) qw_argmax_step(bv, bi, qw_lane(v, 16 * r), __builtin_amdgcn_readlane(i, 16 * r));
-    v = bv;
-    i = bi;
 }
 
 // Eight nibbles of one packed word against eight activations.  Returns
@@ -270,6 +252,18 @@ __device__ __forceinline__ int qw_wave_min_i(int v)
                min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 
+// Wave maximum of ints (probability bits, which order as the values for
+// p >= 0, or negative sentinels below every probability).
+__device__ __forceinline__ int qw_wave_max_i(int v)
+{
+    v = max(v, qw_dpp_i<QW_DPP_XOR1>(v));
+    v = max(v, qw_dpp_i<QW_DPP_XOR2>(v));
+    v = max(v, qw_dpp_i<QW_DPP_HMIRROR>(v));
+    v = max(v, qw_dpp_i<QW_DPP_MIRROR>(v));
+    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
 template <int PL>
 __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E, int K, int norm,
                                               int lane, int *pick_i, float *pick_w)
@@ -279,29 +273,72 @@ __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E
 #pragma unroll
     for (int j = 0; j < PL; j++) {
         const int e = lane + 64 * j;
-        v[j] = e < E ? l[e] : -__builtin_huge_valf();
+        const float x = l[e < E ? e : E - 1];
+        v[j] = e < E ? x : -__builtin_huge_valf();
         m = fmaxf(m, v[j]);
     }
     m = qw_wave_max(m);
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < PL; j++) {
-        const int e = lane + 64 * j;
-        if (e < E) { v[j] = qw_exp_spec(v[j] - m); s = s + v[j]; }
+        const float ex = qw_exp_spec(v[j] - m);
+        v[j] = lane + 64 * j < E ? ex : 0.0f;
+        s = s + v[j];
     }
     s = qw_xor_sum<64>(s);
-    // probabilities; -2 marks a slot past E (below a retired -1)
+    // p = v / s, correctly rounded: with y = 1/s correctly rounded and
+    // q = v*y, q + (v - s q) y rounds to v/s (Markstein) for results in the
+    // normal range; s >= 1 (the largest term is e^0), so only v below 2^-100
+    // can leave it and those take the division itself.
+    const float y = 1.0f / s;
+    int pb[PL];
+    bool tiny = false;
 #pragma unroll
-    for (int j = 0; j < PL; j++) v[j] = lane + 64 * j < E ? v[j] / s : -2.0f;
-    float bv = v[0];
-    int bj = 0;
+    for (int j = 0; j < PL; j++) {
+        const float q = __fmul_rn(v[j], y);
+        const float p = __builtin_fmaf(__builtin_fmaf(-s, q, v[j]), y, q);
+        pb[j] = __float_as_int(p);
+        tiny |= v[j] != 0.0f && v[j] < 7.888609052210118e-31f;
+    }
+    if (__ballot(tiny)) {
 #pragma unroll
-    for (int j = 1; j < PL; j++)
-        if (v[j] > bv) { bv = v[j]; bj = j; }
+        for (int j = 0; j < PL; j++)
+            if (lane + 64 * j < E) pb[j] = __float_as_int(v[j] / s);
+    }
+    // A lane's slots in groups of four, each group sorted once by the key
+    // (bits(p) + 2) << 2 | (3 - slot % 4): p < 2 has bits below 2^30, so the
+    // key orders by p and then by the lower slot.  A slot past E has key < 4,
+    // an emptied one 0, both below every probability (keys >= 8).
+    constexpr int NG = PL / 4;
+    uint32_t g[NG][4];
+#pragma unroll
+    for (int k = 0; k < NG; k++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int j = 4 * k + i;
+            const int bits = lane + 64 * j < E ? pb[j] : -2;
+            g[k][i] = ((uint32_t)(bits + 2) << 2) | (uint32_t)(3 - i);
+        }
+        // sort descending: (0,1) (2,3) (0,2) (1,3) (1,2)
+#define QW_CE(x, y) { const uint32_t hi = max(g[k][x], g[k][y]), lo = min(g[k][x], g[k][y]); g[k][x] = hi; g[k][y] = lo; }
+        QW_CE(0, 1) QW_CE(2, 3) QW_CE(0, 2) QW_CE(1, 3) QW_CE(1, 2)
+#undef QW_CE
+    }
     float wsum = 0.0f, mine_w = 0.0f;
     int mine_i = 0;
     for (int n = 0; n < K; n++) {
-        const float V = qw_wave_max(bv);
+        // the lane's best: the best group head, ties to the lower group
+        uint32_t hk = g[0][0];
+        int hg = 0;
+#pragma unroll
+        for (int k = 1; k < NG; k++) {
+            const bool gt = (g[k][0] >> 2) > (hk >> 2);
+            hk = gt ? g[k][0] : hk;
+            hg = gt ? k : hg;
+        }
+        const int bv = (int)(hk >> 2) - 2;
+        const int bj = 4 * hg + 3 - (int)(hk & 3u);
+        const int V = qw_wave_max_i(bv);
         const unsigned long long at = __ballot(bv == V);
         int I;
         if ((at & (at - 1)) == 0) {
@@ -310,18 +347,20 @@ __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E
         } else {
             I = qw_wave_min_i(bv == V ? lane + 64 * bj : 0x7FFFFFFF);
         }
-        wsum = wsum + V;
-        if (lane == n) { mine_i = I; mine_w = V; }
-        if (lane == (I & 63)) {
-            const int jr = I >> 6;
+        I = __builtin_amdgcn_readfirstlane(I);
+        const float Vf = __int_as_float(V);
+        wsum = wsum + Vf;
+        mine_i = lane == n ? I : mine_i;
+        mine_w = lane == n ? Vf : mine_w;
+        // the owner pops its best group's head
+        const bool own = lane == (I & 63);
 #pragma unroll
-            for (int j = 0; j < PL; j++)
-                if (j == jr) v[j] = -1.0f;
-            bv = v[0];
-            bj = 0;
-#pragma unroll
-            for (int j = 1; j < PL; j++)
-                if (v[j] > bv) { bv = v[j]; bj = j; }
+        for (int k = 0; k < NG; k++) {
+            const bool pop = own && hg == k;
+            g[k][0] = pop ? g[k][1] : g[k][0];
+            g[k][1] = pop ? g[k][2] : g[k][1];
+            g[k][2] = pop ? g[k][3] : g[k][2];
+            g[k][3] = pop ? 0u : g[k][3];
         }
     }
     *pick_i = mine_i;
