@@ -56,10 +56,21 @@ def decode_bytes(c):
     return {
         "routed": K * (expert_gu + expert_down),
         "all": K * (expert_gu + expert_down) + shared_gu + shared_down + router,
-        "front": router + shared_gu,
-        "experts": K * expert_gu + shared_down,
-        "down": K * expert_down,
+        "front": router,
+        "experts": K * expert_gu + shared_gu,
+        "down": K * expert_down + shared_down,
     }
+
+
+def measured_traffic(kernel):
+    """HBM bytes per dispatch of `kernel` (fetch + write) from the committed
+    rocprofv3 counter passes, or None when no summary covers it."""
+    path = os.path.join(ROOT, "profiles", "decode_config1_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["bytes_per_dispatch"].get(kernel)
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def prefill_flops(c, rows):
@@ -243,11 +254,11 @@ def main():
             "kernels_us": {k: round(v, 3) for k, v in per_k.items()},
             "kernels_bytes": {k: nb[k] for k in ("front", "experts", "down")},
             "kernels_gbs": {k: round(nb[k] / (per_k[k] * 1e-6) / 1e9, 1) for k in per_k},
-            "breakdown_us_total": round(brk["region"] * 1000.0 / args.steps, 3),
         },
         "roofline": {"bound": "hbm", "kernel": f"k_decode_{dom}", "achieved": round(roof_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(roof_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic(f"k_decode_{dom}"),
+                     "algorithmic_bytes": nb[dom]},
     }
 
     if not args.no_prefill:

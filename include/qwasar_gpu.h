@@ -199,7 +199,7 @@ typedef struct {
 /* The whole MoE block -- router, routing, routed experts, gated shared
  * expert, combine -- for `rows` tokens, in the fewest launches this backend
  * has: out F32 [rows, H]; idx I32 [rows, K] and w F32 [rows, K] receive the
- * routing.  Decode (rows < 8) is a fused path over only the selected
+ * routing.  Decode (rows <= 8) is a fused path over only the selected
  * experts; prefill is the grouped path.  Scratch is owned by the backend.
  * False, nothing encoded, for shapes outside what the kernels take. */
 bool qw_op_moe_layer(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,

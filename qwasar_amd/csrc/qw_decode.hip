@@ -18,6 +18,8 @@
 // The 4-bit products use the q16 dot (qw_unit_dot): staged activations are
 // loaded straight into registers next to the weights, and a lane issues all
 // its loads before its first multiply.
+#include <hip/hip_ext.h>
+
 #include "qw_device.h"
 #include "qw_kernels.h"
 
@@ -463,21 +465,30 @@ extern "C" size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows)
     return qd_layout(M, rows).total;
 }
 
-template <int LPR, int NUL>
-static void launch_experts(hipStream_t s, QdArgs &a)
+// A launch, with its own start / end stamps when e0 / e1 are given.
+template <typename F>
+static void qd_launch(F kern, dim3 grid, dim3 blk, size_t lds, hipStream_t s, hipEvent_t e0, hipEvent_t e1,
+                      const QdArgs &a)
 {
-    const dim3 grid(a.n_shared_wg + a.umax * a.gu_wg_per_u), blk(QD_GU_WAVES * 64);
-    const size_t lds = (size_t)a.tch * (a.m.H / 16) * QW_Q16_BYTES;
-    if (a.m.E <= 256) hipLaunchKernelGGL((k_decode_experts<LPR, NUL, 4>), grid, blk, lds, s, a);
-    else if (a.m.E <= 512) hipLaunchKernelGGL((k_decode_experts<LPR, NUL, 8>), grid, blk, lds, s, a);
-    else hipLaunchKernelGGL((k_decode_experts<LPR, NUL, 16>), grid, blk, lds, s, a);
+    if (e0) hipExtLaunchKernelGGL(kern, grid, blk, (uint32_t)lds, s, e0, e1, 0, a);
+    else hipLaunchKernelGGL(kern, grid, blk, lds, s, a);
 }
 
 template <int LPR, int NUL>
-static void launch_down(hipStream_t s, QdArgs &a)
+static void launch_experts(hipStream_t s, QdArgs &a, hipEvent_t e0, hipEvent_t e1)
+{
+    const dim3 grid(a.n_shared_wg + a.umax * a.gu_wg_per_u), blk(QD_GU_WAVES * 64);
+    const size_t lds = (size_t)a.tch * (a.m.H / 16) * QW_Q16_BYTES;
+    if (a.m.E <= 256) qd_launch(k_decode_experts<LPR, NUL, 4>, grid, blk, lds, s, e0, e1, a);
+    else if (a.m.E <= 512) qd_launch(k_decode_experts<LPR, NUL, 8>, grid, blk, lds, s, e0, e1, a);
+    else qd_launch(k_decode_experts<LPR, NUL, 16>, grid, blk, lds, s, e0, e1, a);
+}
+
+template <int LPR, int NUL>
+static void launch_down(hipStream_t s, QdArgs &a, hipEvent_t e0, hipEvent_t e1)
 {
     const int nw = a.m.K + 1 < QD_DOWN_MAXW ? a.m.K + 1 : QD_DOWN_MAXW;
-    hipLaunchKernelGGL((k_decode_down<LPR, NUL>), dim3(a.rows * a.n_down_rb), dim3(nw * 64), 0, s, a);
+    qd_launch(k_decode_down<LPR, NUL>, dim3(a.rows * a.n_down_rb), dim3(nw * 64), 0, s, e0, e1, a);
 }
 
 // Instantiates F<LPR, NUL> for the supported (LPR, NUL) pairs.
@@ -563,14 +574,12 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     a.qact = (uint4 *)(S + L.qact);
 
     bool ok;
-    if (ev) (void)hipEventRecord(ev[0], s);
-    hipLaunchKernelGGL(k_decode_front, dim3(a.n_router_wg + rows), dim3(QD_FRONT_WAVES * 64), 0, s, a);
-    if (ev) (void)hipEventRecord(ev[1], s);
-    QD_DISPATCH_GU(launch_experts, lpr_h, nul_h, s, a);
+    hipEvent_t no[6] = {0, 0, 0, 0, 0, 0};
+    hipEvent_t *e = ev ? ev : no;
+    qd_launch(k_decode_front, dim3(a.n_router_wg + rows), dim3(QD_FRONT_WAVES * 64), 0, s, e[0], e[1], a);
+    QD_DISPATCH_GU(launch_experts, lpr_h, nul_h, s, a, e[2], e[3]);
     if (!ok) return (int)hipErrorInvalidValue;
-    if (ev) (void)hipEventRecord(ev[2], s);
-    QD_DISPATCH_DOWN(launch_down, nul_d, s, a);
+    QD_DISPATCH_DOWN(launch_down, nul_d, s, a, e[4], e[5]);
     if (!ok) return (int)hipErrorInvalidValue;
-    if (ev) (void)hipEventRecord(ev[3], s);
     return (int)hipGetLastError();
 }

@@ -84,8 +84,8 @@ size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows);
 int qwk_moe_decode_supported(const qwk_moe *M, int rows);
 /* Decode (rows <= QWK_DECODE_MAX_ROWS): out [rows, H], idx/w [rows, K]. */
 #define QWK_DECODE_MAX_ROWS 8
-/* `ev`, when not NULL, holds 4 events recorded on `s` before the first
- * launch and after each of the three (front, experts, down). */
+/* `ev`, when not NULL, holds 6 events: the start and end of each of the three
+ * launches (front, experts, down), stamped by the dispatches themselves. */
 int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
                    const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes,
                    hipEvent_t *ev);

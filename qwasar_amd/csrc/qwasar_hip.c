@@ -640,15 +640,15 @@ static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float
     void *S = scratch(need);
     if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", need); return false; }
     /* Profiling charges each of the three launches to its own label. */
-    hipEvent_t ev[4] = { NULL, NULL, NULL, NULL };
+    hipEvent_t ev[6] = { NULL, NULL, NULL, NULL, NULL, NULL };
     int per_kernel = G.prof != 0;
-    for (int i = 0; per_kernel && i < 4; i++)
+    for (int i = 0; per_kernel && i < 6; i++)
         if (!(ev[i] = cmd_event(c, 0))) per_kernel = 0;
     const int rc = qwk_moe_decode(G.stream, out, idx, w, x, &m, rows, S, need,
                                   per_kernel ? ev : NULL);
     if (per_kernel) {
         static const char *labels[3] = { "moe decode front", "moe decode experts", "moe decode down" };
-        for (int i = 0; i < 3; i++) cmd_add_mark(c, labels[i], ev[i], ev[i + 1]);
+        for (int i = 0; i < 3; i++) cmd_add_mark(c, labels[i], ev[2 * i], ev[2 * i + 1]);
     }
     launched(c, "moe_layer (decode)", rc);
     return rc == 0;
