@@ -12,7 +12,7 @@
 //             (correctly rounded)
 //   top-k     the K largest probabilities, ties to the lower expert index,
 //             in descending order (what K rounds of a serial scan with '>'
-//             pick), found exactly by a radix select on the fp32 bits
+//             pick), found exactly by a K-round wave tournament
 //   renorm    wsum = w_0 + w_1 + ... in pick order; w_k / wsum
 #include "qw_device.h"
 #include "qw_kernels.h"
@@ -94,12 +94,100 @@ __global__ __launch_bounds__(QW_DMAT_WAVES * 64) void k_dmat_bf16(
     }
 }
 
+// The same order-R logits for many token rows, register-tiled: one wave owns
+// a 32 x 32 block of (token row, output); lane (ty, tx) keeps 4 x 4 of them.
+// Chunk c of 64 inputs is staged in LDS transposed (x as [k][row], w as
+// [k][out] in fp32), and every output runs its own fmaf chain over the chunk
+// in index order from 0, then joins the running total (total = p_0, then
+// total + p_c) -- the order above, element for element.  The next chunk is
+// loaded into registers while the current one is consumed.  k % 64 == 0.
+#define QW_DT 32
+__global__ __launch_bounds__(64) void k_dmat_tiled(float *__restrict__ y, const float *__restrict__ x,
+                                                   const uint16_t *__restrict__ w, int k, int n, int rows)
+{
+    __shared__ float4 xs[64][QW_DT / 4];      // [k][row / 4]
+    __shared__ float4 ws[64][QW_DT / 4];      // [k][out / 4]
+    const int lane = threadIdx.x, ty = lane / 8, tx = lane % 8;
+    const int r0 = blockIdx.y * QW_DT, o0 = blockIdx.x * QW_DT;
+    // staging: x rows r0 + lane / 2 (32 rows, two lanes a row, 32 inputs each);
+    // w rows o0 + lane / 2 likewise (bf16, 32 inputs = 4 uint4)
+    const int sr = lane / 2, sh = (lane % 2) * 32;
+    const bool xok = r0 + sr < rows, wok = o0 + sr < n;
+    const float4 *xg = reinterpret_cast<const float4 *>(x + (size_t)(xok ? r0 + sr : 0) * k + sh);
+    const uint4 *wg = reinterpret_cast<const uint4 *>(w + (size_t)(wok ? o0 + sr : 0) * k + sh);
+    float4 xr[8];
+    uint4 wr[4];
+    auto fetch = [&](int c) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) xr[i] = xok ? xg[c * 16 + i] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < 4; i++) wr[i] = wok ? wg[c * 8 + i] : make_uint4(0, 0, 0, 0);
+    };
+    float tot[4][4], p[4][4];
+    const int nch = k / 64;
+    fetch(0);
+    for (int c = 0; c < nch; c++) {
+        __syncthreads();
+        // transpose into LDS: element (row sr, input sh + 4i + j)
+        float *xsf = reinterpret_cast<float *>(xs), *wsf = reinterpret_cast<float *>(ws);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float v[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) xsf[(sh + 4 * i + j) * QW_DT + sr] = v[j];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t v[4] = {wr[i].x, wr[i].y, wr[i].z, wr[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                wsf[(sh + 8 * i + 2 * j) * QW_DT + sr] = __uint_as_float(v[j] << 16);
+                wsf[(sh + 8 * i + 2 * j + 1) * QW_DT + sr] = __uint_as_float(v[j] & 0xFFFF0000u);
+            }
+        }
+        __syncthreads();
+        if (c + 1 < nch) fetch(c + 1);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) p[i][j] = 0.0f;
+#pragma unroll 8
+        for (int kk = 0; kk < 64; kk++) {
+            const float4 a = xs[kk][ty], b = ws[kk][tx];
+            const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) p[i][j] = __builtin_fmaf(bv[j], av[i], p[i][j]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) tot[i][j] = c == 0 ? p[i][j] : tot[i][j] + p[i][j];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = r0 + 4 * ty + i;
+        if (r >= rows) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int o = o0 + 4 * tx + j;
+            if (o < n) y[(size_t)r * n + o] = tot[i][j];
+        }
+    }
+}
+
 extern "C" int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint16_t *w,
                              int k, int n, int rows)
 {
     if (k < 1 || k > QWK_DMAT_MAX_K || n < 1 || rows < 1) return (int)hipErrorInvalidValue;
-    dim3 grid((n + QW_DMAT_WAVES - 1) / QW_DMAT_WAVES, (rows + QW_DMAT_RB - 1) / QW_DMAT_RB);
     const bool vec = k % 8 == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)x % 16) == 0;
+    if (vec && k % 64 == 0 && rows >= QW_DT) {
+        hipLaunchKernelGGL(k_dmat_tiled, dim3((n + QW_DT - 1) / QW_DT, (rows + QW_DT - 1) / QW_DT), dim3(64), 0, s,
+                           y, x, w, k, n, rows);
+        return (int)hipGetLastError();
+    }
+    dim3 grid((n + QW_DMAT_WAVES - 1) / QW_DMAT_WAVES, (rows + QW_DMAT_RB - 1) / QW_DMAT_RB);
     if (vec) hipLaunchKernelGGL(k_dmat_bf16<true>, grid, dim3(QW_DMAT_WAVES * 64), 0, s, y, x, w, k, n, rows);
     else hipLaunchKernelGGL(k_dmat_bf16<false>, grid, dim3(QW_DMAT_WAVES * 64), 0, s, y, x, w, k, n, rows);
     return (int)hipGetLastError();

@@ -82,10 +82,17 @@ def test_route_refuses_oversize(gpu, capfd):
     assert err.count("unsupported") == 2
 
 
-@pytest.mark.parametrize("k,n,rows", [(3072, 512, 1), (3072, 512, 8), (3072, 64, 20), (256, 16, 3), (100, 7, 2)])
+@pytest.mark.parametrize("k,n,rows", [(3072, 512, 1), (3072, 512, 8), (3072, 64, 20), (256, 16, 3), (100, 7, 2),
+                                      (3072, 512, 70), (2560, 100, 33), (256, 16, 64), (192, 40, 97)])
 def test_dmat_bf16_order_r_bit_exact(gpu, k, n, rows):
+    """Small row counts take one wave per output; from 32 rows on (k % 64 == 0)
+    the register-tiled kernel, including ragged row and output blocks."""
     w = synth.to_bf16(rnd((n, k), 5 + k, 0.02))
     x = synth.bf16_round(rnd((rows, k), 6 + n))
+    if rows >= 32:
+        x = rnd((rows, k), 9 + n).astype(np.float32)   # full fp32 inputs
+        x[rows // 2] = 0.0                             # a zero row: signed zeros must match
+        x[rows // 3, : k // 2] *= -1e-30               # tiny products
     B = gpu.Buf
     wb, xb, yb = B.of(w), B.of(x), B(rows * n * 4)
     c = gpu.qw_cmd_begin()
