@@ -13,7 +13,7 @@ Steps cycle through a pool of 64 tokens chosen (by the GPU's own routing) so
 that any 12 consecutive tokens select pairwise disjoint experts: every step
 reads its routed experts from HBM, not from the 256 MB Infinity Cache.
 
-Also reported: the per-kernel decode breakdown, HBM bandwidth on the routed
+Also reported: the decode launch's own duration, HBM bandwidth on the routed
 ("selected-expert") bytes and on all bytes, config 3 (512-token prefill with
 Zipf-skewed routing) and a 2048-token prefill chunk (config 4's per-layer
 step) in tokens/s and bf16-MFMA utilisation, and the CPU oracle's time on a
@@ -56,9 +56,6 @@ def decode_bytes(c):
     return {
         "routed": K * (expert_gu + expert_down),
         "all": K * (expert_gu + expert_down) + shared_gu + shared_down + router,
-        "front": router,
-        "experts": K * expert_gu + shared_gu,
-        "down": K * expert_down + shared_down,
     }
 
 
@@ -130,9 +127,8 @@ def time_decode(gpu, lb, xpool, steps, warmup, profile):
     gpu.qw_cmd_mark(c, b"decode region")
     gpu.run(c, "decode")
     gpu.qw_prof_set_enabled(False)
-    res = {"region": gpu.qw_prof_ms(b"decode region", None)}
-    for k in ("front", "experts", "down"):
-        res[k] = gpu.qw_prof_ms(f"moe decode {k}".encode(), None)
+    res = {"region": gpu.qw_prof_ms(b"decode region", None),
+           "fused": gpu.qw_prof_ms(b"moe decode", None)}
     gpu.qw_prof_reset()
     return res
 
@@ -223,10 +219,10 @@ def main():
     nb = decode_bytes(cfg)
     dec = time_decode(gpu, lb, xpool, args.steps, args.warmup, profile=False)
     us_tok = dec["region"] * 1000.0 / args.steps
+    # the one decode launch, timed by its own dispatch stamps
     brk = time_decode(gpu, lb, xpool, args.steps, 0, profile=True)
-    per_k = {k: brk[k] * 1000.0 / args.steps for k in ("front", "experts", "down")}
-    dom = max(per_k, key=per_k.get)
-    roof_gbs = nb[dom] / (per_k[dom] * 1e-6) / 1e9
+    k_us = brk["fused"] * 1000.0 / args.steps
+    roof_gbs = nb["all"] / (k_us * 1e-6) / 1e9
 
     out = {
         "metric": "moe_layer_decode_us_per_token",
@@ -251,14 +247,12 @@ def main():
             "routed_hbm_gbs": round(nb["routed"] / (us_tok * 1e-6) / 1e9, 1),
             "routed_hbm_frac": round(nb["routed"] / (us_tok * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "all_hbm_gbs": round(nb["all"] / (us_tok * 1e-6) / 1e9, 1),
-            "kernels_us": {k: round(v, 3) for k, v in per_k.items()},
-            "kernels_bytes": {k: nb[k] for k in ("front", "experts", "down")},
-            "kernels_gbs": {k: round(nb[k] / (per_k[k] * 1e-6) / 1e9, 1) for k in per_k},
+            "kernel_us": round(k_us, 3),
         },
-        "roofline": {"bound": "hbm", "kernel": f"k_decode_{dom}", "achieved": round(roof_gbs, 1),
+        "roofline": {"bound": "hbm", "kernel": "k_decode_fused", "achieved": round(roof_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(roof_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(f"k_decode_{dom}"),
-                     "algorithmic_bytes": nb[dom]},
+                     "traffic": measured_traffic("k_decode_fused"),
+                     "algorithmic_bytes": nb["all"]},
     }
 
     if not args.no_prefill:

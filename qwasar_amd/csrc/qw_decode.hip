@@ -1,44 +1,159 @@
-// qw_decode.hip -- the MoE block at decode (1..8 tokens) in three launches,
-// with no communication between workgroups inside a launch.
+// qw_decode.hip -- the MoE block at decode (1..8 tokens) in ONE launch.
 //
-//   front    router logits (order R, fp32) for every expert and the shared
-//            expert's gate logit; the input rows staged as q16 units
-//   experts  the shared expert's gate / up rows (no routing needed), and, in
-//            the other workgroups, routing of every token (softmax, top-K,
-//            renormalise: cheap, and it saves a launch and any
-//            cross-workgroup handoff) followed by the gate / up rows of one
-//            selected expert for every token routed to it -- each weight
-//            byte read once; the SwiGLU activations leave staged as q16
-//            units; workgroup 0 writes idx / w
-//   down     per (block of output rows, token): the down rows of the shared
-//            expert and of each of the token's K experts, and the combine in
-//            registers: sigmoid(g) * shared + sum_k w_k * y_k, an fma chain
-//            in slot order
+// The launch's workgroups take four roles, in block-index order:
+//
+//   router   one wave per router row (E rows, plus the shared expert's gate
+//            vector): the order-R logits of every token
+//   shared   the shared expert's gate / up rows and SwiGLU (needs only x)
+//   experts  per (selected expert, 16-row block): route every token, then
+//            the gate / up rows of that expert for every token routed to it
+//            -- each weight byte read once; SwiGLU fused; the activations
+//            leave staged as q16 units
+//   down     per (token, block of output rows): route, load the down rows of
+//            the shared expert and of each of the token's K experts into
+//            registers, then wait for the activations and finish with the
+//            combine: sigmoid(g) * shared + sum_k w_k * y_k, an fma chain in
+//            slot order
+//
+// Hand-offs between roles go through device memory past the per-XCD L2: the
+// producer writes with device-coherent (sc1) stores, waits for them, and
+// bumps a counter; the last arriver of a counter resets it to zero and
+// publishes the launch's epoch in the counter's flag.  A consumer polls the
+// flag with device-coherent loads and reads the data the same way.  So the
+// down rows' weight fetch overlaps the gate / up fetch, and no launch
+// boundary sits between router, routing, experts and down.
+//
+// Progress: a workgroup only waits on workgroups with smaller block indices,
+// which the dispatcher has already placed (workgroups are dispatched in index
+// order), so every wait ends.  Each wait is also bounded: past a spin limit
+// it raises the error word, every later wait gives up at once, and the host
+// reports the error; no wave is left spinning.
 //
 // The 4-bit products use the q16 dot (qw_unit_dot): staged activations are
-// loaded straight into registers next to the weights, and a lane issues all
-// its loads before its first multiply.
+// loaded straight into registers next to the weights.
 #include <hip/hip_ext.h>
 
 #include "qw_device.h"
 #include "qw_kernels.h"
 
+// Built with -DQD_TRACE, every workgroup stamps the device wall clock
+// (100 MHz) at its phases into qd_trace[block][slot], for timelines.
+#ifdef QD_TRACE
+__device__ unsigned long long qd_trace[8192 * 8];
+#define QD_TS(slot) do { if (threadIdx.x == 0) qd_trace[blockIdx.x * 8 + (slot)] = wall_clock64(); } while (0)
+extern "C" int qd_trace_read(unsigned long long *dst)
+{
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(qd_trace), sizeof(qd_trace));
+}
+#else
+#define QD_TS(slot) do { } while (0)
+#endif
+
 #define QD_MAXT QWK_DECODE_MAX_ROWS
-#define QD_MAXU (QWK_DECODE_MAX_ROWS * QWK_ROUTE_MAX_K)
-#define QD_MAXCH (QWK_DMAT_MAX_K / 64)
-#define QD_FRONT_WAVES 4
-#define QD_GU_WAVES 16       // experts workgroup: 16 waves
-#define QD_GU_MAXRPB (QD_GU_WAVES * 4)
-#define QD_GU_LDS (48 * 1024)  // LDS for staged input vectors
-#define QD_DOWN_MAXW 16
-#define QD_DOWN_RIT 2        // down rows per lane slot
+#define QD_MAXU (QWK_DECODE_MAX_ROWS * QWK_DECODE_MAX_K)
+#define QD_WAVES 16                 // every role: 16 waves
+#define QD_THREADS (QD_WAVES * 64)
+#define QD_GU_MAXRPB (QD_WAVES * 4)
+#define QD_LDS (48 * 1024)          // dynamic LDS: staged inputs, or router partials
+#define QD_DOWN_LPR 16
+#define QD_DOWN_RIT 4               // down rows per lane slot
+#define QD_DOWN_RPG ((64 / QD_DOWN_LPR) * QD_DOWN_RIT)
+#define QD_SPIN_LIMIT (1 << 16)     // polls (each a memory round trip plus a sleep)
+
+static_assert((64 * 68 + 4 * 64) * 4 <= QD_LDS, "router: a padded token row and partials fit the dynamic LDS");
+static_assert(QWK_DECODE_MAX_K + 1 <= QD_WAVES, "down: one wave per matrix");
+// down: the K + 1 activation vectors (at most 64 units each) in LDS
+static_assert((QWK_DECODE_MAX_K + 1) * 64 * QW_Q16_BYTES <= QD_LDS, "down activations fit the dynamic LDS");
 
 // Lanes per row for a row of `units` q16 units, and units per lane.
 static __host__ __device__ constexpr int qd_lpr(int units) { return units >= 128 ? 64 : units >= 64 ? 32 : 16; }
 static int qd_nul(int units, int lpr)
 {
     const int n = (units + lpr - 1) / lpr;
-    return n <= 4 ? n : n <= 8 ? 8 : -1;
+    return n <= 4 ? n : -1;
+}
+
+// ---- hand-off state (zeroed once by the host) -------------------------------------
+//
+// Producers (router, shared, experts workgroups) come in families: all router
+// workgroups, all shared ones, the experts workgroups of one selected expert.
+// A family is cut into groups of QD_GROUP consecutive workgroups; each group
+// has a counter and a flag.  A producer makes its device-coherent stores
+// visible, bumps its group's counter, and the group's last arriver resets the
+// counter and publishes the launch's epoch in the group's flag.  A consumer
+// polls the few flags of the groups it needs (one a lane, in one batch).
+
+#define QD_GROUP 16
+#define QD_NSYNC 2048
+#define QD_FL_RT 0           // router groups
+#define QD_FL_SH 64          // shared-expert groups
+#define QD_FL_EX 128         // experts: slot u, group h at QD_FL_EX + u * ngu + h
+
+struct QdSync {
+    uint32_t cnt[QD_NSYNC];
+    uint32_t flag[QD_NSYNC];
+    uint32_t err;
+};
+
+__device__ __forceinline__ void qd_stf(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// One q16 uint4 written device-coherently, as two 64-bit halves.
+__device__ __forceinline__ void qd_st4(uint4 *p, uint4 v)
+{
+    unsigned long long *q = reinterpret_cast<unsigned long long *>(p);
+    __hip_atomic_store(q, (unsigned long long)v.x | ((unsigned long long)v.y << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 1, (unsigned long long)v.z | ((unsigned long long)v.w << 32), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A flag read for polling: volatile, so it is issued on every pass; the
+// caller waits for a batch of them at once.
+__device__ __forceinline__ uint32_t qd_poll_ld(const uint32_t *p)
+{
+    uint32_t v;
+    asm volatile("global_load_dword %0, %1, off sc1" : "=v"(v) : "v"(p));
+    return v;
+}
+
+// Member i of a producer family of n workgroups whose groups' counters and
+// flags start at `base`: the workgroup's device-coherent stores are done;
+// count it, and publish the epoch if it completes its group.
+__device__ __forceinline__ void qd_signal(QdSync *S, int base, int i, int n, uint32_t epoch)
+{
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int g = i / QD_GROUP, members = min(QD_GROUP, n - g * QD_GROUP);
+        uint32_t *c = &S->cnt[base + g];
+        const uint32_t old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old + 1u == (uint32_t)members) {
+            __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&S->flag[base + g], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// Wave 0 only: waits until flag[idx] holds the epoch in every lane that has a
+// flag (has = true), bounded; each pass reads all the flags and the error
+// word in one batch.  Returns false (and raises the error word) when the wait
+// gave up or another wait already had.
+__device__ __forceinline__ bool qd_wait_flags(QdSync *S, bool has, int idx, uint32_t epoch)
+{
+    const uint32_t *f = &S->flag[has ? idx : 0];
+    for (int spins = 0;; spins++) {
+        uint32_t v = qd_poll_ld(f), e = qd_poll_ld(&S->err);
+        asm volatile("s_waitcnt vmcnt(0)" : "+v"(v), "+v"(e)::"memory");
+        if (__ballot(has && v != epoch) == 0ull) return true;
+        if (spins >= QD_SPIN_LIMIT || __ballot(e != 0u) != 0ull) {
+            if ((threadIdx.x & 63) == 0)
+                __hip_atomic_fetch_or(&S->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
 }
 
 struct QdLayout {
@@ -67,141 +182,186 @@ struct QdArgs {
     int32_t *idx;
     float *w;
     int rows, umax, lgG;
-    int n_router_wg;                // front
-    int n_shared_wg, gu_wg_per_u;   // experts
+    int n_rt, n_sh, gu_wg_per_u, ngu, n_ex, n_down_rb;
     int tch;                        // input vectors per LDS pass
-    int n_down_rb;                  // down
+    char *scr;                      // the scratch base (device-coherent loads are offsets from it)
     float *logits, *g1;
     uint4 *qx, *qsh, *qact;         // q16 units: [vector][units][3]
+    QdSync *sync;
+    uint32_t epoch;
 };
 
-// ---- front: router logits and the staged input ----------------------------------
+// ---- router ---------------------------------------------------------------------
+//
+// QD_RT_ROWS router rows per workgroup, one wave each; the token rows pass
+// through LDS one at a time, chunk c of 64 inputs at c * QD_XPAD floats (the
+// pad makes the per-lane chunk reads conflict-free).
 
-// Order-R dot of one bf16 row with nt token rows (one wave): lane l computes
-// the fmaf chains of chunks l, l+64, ...; the chunk partials are then added
-// left to right, read lane by lane with readlane, so every lane holds the
-// total.
-__device__ __forceinline__ void qd_router_row(const uint16_t *__restrict__ wr, const float *__restrict__ x,
-                                              int k, int nt, float *y, int ystride)
+#define QD_RT_ROWS 4
+#define QD_XPAD 68
+
+// Order-R dot of one bf16 row with one token row xl (LDS, padded chunks):
+// lane l computes the fmaf chain of chunk l (k <= 64 * 64); the chunk
+// partials go to LDS and lane 0 adds them left to right, from -0 (so the
+// first addition is exact).
+__device__ __forceinline__ void qd_router_row(const uint4 (&w)[8], const float *xl, int nch, float *y,
+                                              float *part)
 {
-    constexpr int CPL = QD_MAXCH / 64;      // chunks per lane at most
-    const int lane = threadIdx.x & 63, nch = k / 64;
-#pragma unroll 1
-    for (int t = 0; t < nt; t++) {
-        float p[CPL];
+    const int lane = threadIdx.x & 63;
+    if (lane < nch) {
+        const float4 *xv = reinterpret_cast<const float4 *>(xl + lane * QD_XPAD);
+        float s = 0.0f;
 #pragma unroll
-        for (int j = 0; j < CPL; j++) {
-            const int c = lane + 64 * j;
-            float s = 0.0f;
-            if (c < nch) {
-                const uint4 *wp = reinterpret_cast<const uint4 *>(wr + c * 64);
-                const float4 *xv = reinterpret_cast<const float4 *>(x + (size_t)t * k + c * 64);
-#pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    const uint4 w = wp[q];
-                    const float4 a = xv[2 * q], b = xv[2 * q + 1];
-                    s = __builtin_fmaf(__uint_as_float(w.x << 16), a.x, s);
-                    s = __builtin_fmaf(__uint_as_float(w.x & 0xFFFF0000u), a.y, s);
-                    s = __builtin_fmaf(__uint_as_float(w.y << 16), a.z, s);
-                    s = __builtin_fmaf(__uint_as_float(w.y & 0xFFFF0000u), a.w, s);
-                    s = __builtin_fmaf(__uint_as_float(w.z << 16), b.x, s);
-                    s = __builtin_fmaf(__uint_as_float(w.z & 0xFFFF0000u), b.y, s);
-                    s = __builtin_fmaf(__uint_as_float(w.w << 16), b.z, s);
-                    s = __builtin_fmaf(__uint_as_float(w.w & 0xFFFF0000u), b.w, s);
-                }
-            }
-            p[j] = s;
+        for (int q = 0; q < 8; q++) {
+            uint4 wq = w[q];
+            // converted here, not all 64 values up front
+            asm volatile("" : "+v"(wq.x), "+v"(wq.y), "+v"(wq.z), "+v"(wq.w));
+            const float4 a = xv[2 * q], b = xv[2 * q + 1];
+            s = __builtin_fmaf(__uint_as_float(wq.x << 16), a.x, s);
+            s = __builtin_fmaf(__uint_as_float(wq.x & 0xFFFF0000u), a.y, s);
+            s = __builtin_fmaf(__uint_as_float(wq.y << 16), a.z, s);
+            s = __builtin_fmaf(__uint_as_float(wq.y & 0xFFFF0000u), a.w, s);
+            s = __builtin_fmaf(__uint_as_float(wq.z << 16), b.x, s);
+            s = __builtin_fmaf(__uint_as_float(wq.z & 0xFFFF0000u), b.y, s);
+            s = __builtin_fmaf(__uint_as_float(wq.w << 16), b.z, s);
+            s = __builtin_fmaf(__uint_as_float(wq.w & 0xFFFF0000u), b.w, s);
         }
-        float total = qw_lane(p[0], 0);
-#pragma unroll
-        for (int j = 0; j < CPL; j++)
-            for (int l = j == 0 ? 1 : 0; l < 64 && 64 * j + l < nch; l++) total = total + qw_lane(p[j], l);
-        if (lane == 0) y[(size_t)t * ystride] = total;
+        part[lane] = s;
+    }
+    // A wave's LDS accesses run in order: lane 0 reads what the wave wrote.
+    if (lane == 0) {
+        float total = -0.0f;
+        int c = 0;
+        for (; c + 4 <= nch; c += 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(part + c);
+            total = total + v.x;
+            total = total + v.y;
+            total = total + v.z;
+            total = total + v.w;
+        }
+        for (; c < nch; c++) total = total + part[c];
+        qd_stf(y, total);
     }
 }
 
-__global__ __launch_bounds__(QD_FRONT_WAVES * 64) void k_decode_front(QdArgs a)
+__device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *lds)
 {
-    const int wave = threadIdx.x >> 6, b = blockIdx.x;
-    const int H = a.m.H, E = a.m.E;
-    if (b < a.n_router_wg) {
-        const int o = b * QD_FRONT_WAVES + wave;
-        if (o < E)
-            qd_router_row(a.m.router + (size_t)o * H, a.x, H, a.rows, a.logits + o, E);
-        else if (o == E)
-            qd_router_row(a.m.sh_gate_w, a.x, H, a.rows, a.g1, 1);
-        return;
-    }
-    // one workgroup per token: a unit per thread
-    const int t = b - a.n_router_wg, units = H / 16;
-    for (int u = threadIdx.x; u < units; u += blockDim.x) {
-        const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)t * H + 16 * u);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int H = a.m.H, E = a.m.E, nch = H / 64;
+    const int o = b * QD_RT_ROWS + wave;
+    float *xl = lds, *part = lds + nch * QD_XPAD + wave * 64;
+    // the token rows, staged as q16 units for the gate / up roles
+    const int units = H / 16;
+    for (int i = b * QD_THREADS + threadIdx.x; i < a.rows * units; i += a.n_rt * QD_THREADS) {
+        const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)i * 16);
         float v[16];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const float4 f = src[q];
             v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
         }
-        qw_q16_stage(v, a.qx + ((size_t)t * units + u) * 3);
+        uint4 u[3];
+        qw_q16_make(v, u);
+        qd_st4(a.qx + (size_t)i * 3, u[0]);
+        qd_st4(a.qx + (size_t)i * 3 + 1, u[1]);
+        qd_st4(a.qx + (size_t)i * 3 + 2, u[2]);
     }
+    QD_TS(1);
+    // this wave's row in registers: lane c holds chunk c
+    const bool row = wave < QD_RT_ROWS && o <= E;
+    const uint16_t *wr = o < E ? a.m.router + (size_t)o * H : a.m.sh_gate_w;
+    uint4 w[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++)
+        w[q] = row && lane < nch ? reinterpret_cast<const uint4 *>(wr + lane * 64)[q] : make_uint4(0, 0, 0, 0);
+    for (int t = 0; t < a.rows; t++) {
+        if (t) __syncthreads();
+        for (int i = threadIdx.x; i < H / 4; i += blockDim.x) {
+            const float4 v = reinterpret_cast<const float4 *>(a.x + (size_t)t * H)[i];
+            *reinterpret_cast<float4 *>(xl + (i / 16) * QD_XPAD + (i % 16) * 4) = v;
+        }
+        __syncthreads();
+        if (row) qd_router_row(w, xl, nch, o < E ? a.logits + (size_t)t * E + o : a.g1 + t, part);
+    }
+    QD_TS(2);
+    qd_signal(a.sync, QD_FL_RT, b, a.n_rt, a.epoch);
+    QD_TS(5);
 }
 
-// ---- experts: gate / up rows with SwiGLU --------------------------------------------
+// ---- gate / up rows with SwiGLU ----------------------------------------------------
 //
-// A workgroup owns RPB = QD_GU_WAVES * 64/LPR consecutive rows of one gate / up
+// A workgroup owns RPB = QD_WAVES * 64/LPR consecutive rows of one gate / up
 // pair (the shared expert's, or one routed expert's) for nt input vectors.
 // Lane (slot, lr) of wave w takes row row0 + w * 64/LPR + slot and its units
 // lr, lr + LPR, ... (NUL of them), in both matrices; its weights stay in
 // registers while the input vectors pass through LDS, up to `tch` at a time.
 // The per-row results meet in LDS and leave as q16 units of the activation
-// vectors.
+// vectors, written device-coherently.  Unless `staged` (the inputs already
+// in LDS), the inputs are copied from the router role's staged rows.
 
-// Copies staged vectors vin[t] (t < n; vector t when vin is NULL) of src,
-// `units` units each, into LDS, with threads tid0.. of the workgroup.
-__device__ __forceinline__ void qd_copy_vecs(uint4 *xs, const uint4 *src, const int *vin, int n, int units,
-                                             int tid0, int nthr)
+// Stages token rows x[vin[t]] (t < n; token t when vin is NULL) into LDS as
+// q16 units, with threads tid0.. of the workgroup.
+__device__ __forceinline__ void qd_stage_x(uint4 *xs, const float *x, const int *vin, int n, int H, int tid0,
+                                           int nthr)
 {
-    const int per = units * 3;
-    for (int i = threadIdx.x - tid0; i < n * per; i += nthr) {
-        const int t = i / per, o = i % per;
-        xs[i] = src[(size_t)(vin ? vin[t] : t) * per + o];
+    const int units = H / 16;
+    for (int i = threadIdx.x - tid0; i < n * units; i += nthr) {
+        const int t = i / units, u = i % units;
+        const float4 *src = reinterpret_cast<const float4 *>(x + (size_t)(vin ? vin[t] : t) * H + 16 * u);
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 f = src[q];
+            v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+        }
+        qw_q16_stage(v, xs + (size_t)i * 3);
     }
 }
 
 template <int LPR, int NUL>
-__device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, int n, int k, int lgG, int row0,
-                                             int nt, int tch, bool staged, uint4 *xs, const uint4 *src,
-                                             const int *vin, const int *vout, uint4 *dst,
-                                             float (*ys)[QD_GU_MAXRPB])
+__device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, int n, const QdArgs &a,
+                                             int row0, int nt, bool staged, uint4 *xs, const int *vin,
+                                             const int *vout, uint4 *dst, float (*ys)[QD_GU_MAXRPB])
 {
-    constexpr int SL = 64 / LPR, RPB = QD_GU_WAVES * SL;
+    constexpr int SL = 64 / LPR, RPB = QD_WAVES * SL;
     static_assert(RPB % 16 == 0 && RPB <= QD_GU_MAXRPB, "rows per block");
+    const int k = a.m.H, lgG = a.lgG;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, slot = lane / LPR, lr = lane % LPR;
     const int units = k / 16, words = k / 8, groups = k >> lgG;
     const int rl = wave * SL + slot, row = row0 + rl;
+    // Every load is issued (at a clamped, valid address) before any is used;
+    // out-of-range lanes are zeroed afterwards.
     uint2 wv[2][NUL];
-    float sc[2][NUL], bi[2][NUL];
+    uint32_t sv[2][NUL], bv[2][NUL];
+    const int rowc = min(row, n - 1);
 #pragma unroll
     for (int z = 0; z < 2; z++) {
         const qwk_q4 q = z ? um : gm;
 #pragma unroll
         for (int j = 0; j < NUL; j++) {
-            const int c = j * LPR + lr;
-            if (row < n && c < units) {
-                wv[z][j] = *reinterpret_cast<const uint2 *>(q.w + (size_t)row * words + 2 * c);
-                sc[z][j] = qw_bf16(q.s[(size_t)row * groups + ((16 * c) >> lgG)]);
-                bi[z][j] = qw_bf16(q.b[(size_t)row * groups + ((16 * c) >> lgG)]);
-            } else {
-                wv[z][j] = make_uint2(0, 0);
-                sc[z][j] = bi[z][j] = 0.0f;
-            }
+            const int c = min(j * LPR + lr, units - 1);
+            wv[z][j] = *reinterpret_cast<const uint2 *>(q.w + (size_t)rowc * words + 2 * c);
+            const size_t gi = (size_t)rowc * groups + ((16 * c) >> lgG);
+            sv[z][j] = q.s[gi];
+            bv[z][j] = q.b[gi];
         }
     }
-    for (int t0 = 0; t0 < nt; t0 += tch) {
-        const int tn = min(tch, nt - t0);
+    uint32_t sb[2][NUL];          // bf16 scale (low half) and bias (high half)
+#pragma unroll
+    for (int z = 0; z < 2; z++)
+#pragma unroll
+        for (int j = 0; j < NUL; j++) {
+            const bool ok = row < n && j * LPR + lr < units;
+            wv[z][j] = ok ? wv[z][j] : make_uint2(0, 0);
+            sb[z][j] = ok ? sv[z][j] | (bv[z][j] << 16) : 0u;
+        }
+    for (int t0 = 0; t0 < nt; t0 += a.tch) {
+        const int tn = min(a.tch, nt - t0);
         if (!staged) {
             __syncthreads();
-            qd_copy_vecs(xs, src, vin + t0, tn, units, 0, blockDim.x);
+            const int per = units * 3;
+            for (int i = threadIdx.x; i < tn * per; i += blockDim.x)
+                xs[i] = qw_ld4_coh(a.qx, (uint32_t)((vin[t0 + i / per] * per + i % per) * 16));
         }
         __syncthreads();
 #pragma unroll 1
@@ -217,9 +377,14 @@ __device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, i
                     const float4 r = *reinterpret_cast<const float4 *>(&rr);
 #pragma unroll
                     for (int z = 0; z < 2; z++)
-                        acc[z] = qw_unit_dot(wv[z][j], p0, p1, r, sc[z][j], bi[z][j], acc[z]);
+                        acc[z] = qw_unit_dot(wv[z][j], p0, p1, r, __uint_as_float(sb[z][j] << 16),
+                                             __uint_as_float(sb[z][j] & 0xFFFF0000u), acc[z]);
                 }
             }
+#ifdef QD_TRACE
+            if (t0 + t == 0 && threadIdx.x == 0)
+                qd_trace[blockIdx.x * 8 + 3] = __builtin_amdgcn_readfirstlane(__float_as_int(acc[0] + acc[1])) == 12345 ? 0 : wall_clock64();
+#endif
             const float g = qw_xor_sum<LPR>(acc[0]);
             const float u = qw_xor_sum<LPR>(acc[1]);
             if (lr == 0) ys[t0 + t][rl] = qw_silu(g) * u;
@@ -235,9 +400,16 @@ __device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, i
         float v[16];
 #pragma unroll
         for (int q = 0; q < 16; q++) v[q] = ys[t][16 * uu + q];
-        qw_q16_stage(v, dst + ((size_t)vout[t] * outunits + row0 / 16 + uu) * 3);
+        uint4 s[3];
+        qw_q16_make(v, s);
+        uint4 *d = dst + ((size_t)vout[t] * outunits + row0 / 16 + uu) * 3;
+        qd_st4(d, s[0]);
+        qd_st4(d + 1, s[1]);
+        qd_st4(d + 2, s[2]);
     }
 }
+
+// ---- routing inside a workgroup -----------------------------------------------------
 
 struct QdRoute {
     int U;
@@ -247,13 +419,14 @@ struct QdRoute {
     int ucnt[QD_MAXU];
     int ustart[QD_MAXU];
     int upair[QD_MAXU];       // pairs grouped by unique expert, ascending pair index
-    int mark[QWK_ROUTE_MAX_E];
+    int mark[QWK_ROUTE_MAX_E];// after routing: the unique-expert slot of each selected expert
 };
 
 // Routes every token (a wave per token) with the arithmetic of the
-// standalone route kernel, then builds the union of selected experts with,
-// for each, its pairs in ascending order.  One token's picks are distinct, so
-// for one token the union is the picks themselves, in pick order.
+// standalone route kernel, then builds the union of selected experts
+// (ascending) with, for each, its pairs in ascending order, and mark[e] = the
+// union slot of expert e.  One token's picks are distinct, so for one token
+// the union is the picks themselves, in pick order.
 template <int PL>
 __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
 {
@@ -262,7 +435,7 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
     for (int r = wave; r < a.rows; r += nw) {
         int pi;
         float pw;
-        qw_route_wave<PL>(a.logits + (size_t)r * E, E, K, a.m.norm, lane, &pi, &pw);
+        qw_route_wave<PL, true>(a.logits + (size_t)r * E, E, K, a.m.norm, lane, &pi, &pw);
         if (lane < K) {
             R.picks[r * K + lane] = pi;
             R.pw[r * K + lane] = pw;
@@ -275,6 +448,7 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
             R.ucnt[t] = 1;
             R.ustart[t] = t;
             R.upair[t] = t;
+            R.mark[R.picks[t]] = t;
         }
         if (t == 0) R.U = K;
         __syncthreads();
@@ -303,6 +477,7 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
         int c = 0;
         for (int p = 0; p < npk; p++) c += R.picks[p] == e;
         R.ucnt[u] = c;
+        R.mark[e] = u;
     }
     __syncthreads();
     if (t == 0) {
@@ -319,32 +494,30 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
     __syncthreads();
 }
 
-// 8 waves per SIMD: two 16-wave workgroups per CU, which takes at most 64
-// VGPRs and 78 SGPRs a wave (at 80 SGPRs a CU holds one).
-template <int LPR, int NUL, int PL>
-__global__ __launch_bounds__(QD_GU_WAVES * 64, 8) void k_decode_experts(QdArgs a)
+// Waits, with the whole workgroup, until the router workgroups are done.
+__device__ __forceinline__ void qd_wait_router(const QdArgs &a)
 {
-    extern __shared__ uint4 xs[];     // [tch][units][3]
-    __shared__ QdRoute R;
-    __shared__ int vin[QD_MAXT], vout[QD_MAXT];
-    __shared__ float ys[QD_MAXT][QD_GU_MAXRPB];
-    constexpr int RPB = QD_GU_WAVES * (64 / LPR);
-    const int b = blockIdx.x;
-    const int H = a.m.H, I = a.m.I, K = a.m.K, SI = a.m.SI;
-    const int xunits = H / 16;
-    if (b < a.n_shared_wg) {
-        if (threadIdx.x < QD_MAXT) vin[threadIdx.x] = vout[threadIdx.x] = threadIdx.x;
-        __syncthreads();
-        qd_glu_block<LPR, NUL>(a.m.sh_gate, a.m.sh_up, SI, H, a.lgG, b * RPB, a.rows, a.tch, false,
-                               xs, a.qx, vin, vout, a.qsh, ys);
-        return;
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        qd_wait_flags(a.sync, lane < (a.n_rt + QD_GROUP - 1) / QD_GROUP, QD_FL_RT + lane, a.epoch);
     }
-    const int bb = b - a.n_shared_wg;
+    __syncthreads();
+}
+
+template <int LPR, int NUL, int PL>
+__device__ __forceinline__ void qd_role_experts(const QdArgs &a, int bb, uint4 *xs, QdRoute &R, int *vin,
+                                                int *vout, float (*ys)[QD_GU_MAXRPB])
+{
+    constexpr int RPB = QD_WAVES * (64 / LPR);
+    const int H = a.m.H, I = a.m.I, K = a.m.K;
     const int u = bb / a.gu_wg_per_u, rb = bb % a.gu_wg_per_u;
-    // One token: its input goes to LDS (waves 1..) while wave 0 routes.
+    // One token: its input is staged into LDS while the router runs.
     const bool one = a.rows == 1;
-    if (one && threadIdx.x >= 64) qd_copy_vecs(xs, a.qx, nullptr, 1, xunits, 64, blockDim.x - 64);
+    if (one) qd_stage_x(xs, a.x, nullptr, 1, H, 0, blockDim.x);
+    qd_wait_router(a);
+    QD_TS(1);
     qd_route_all<PL>(a, R);
+    QD_TS(2);
     if (bb == 0)
         for (int p = threadIdx.x; p < a.rows * K; p += blockDim.x) {
             a.idx[p] = R.picks[p];
@@ -371,78 +544,113 @@ __global__ __launch_bounds__(QD_GU_WAVES * 64, 8) void k_decode_experts(QdArgs a
         gm = {a.m.gate_up.w + off * words, a.m.gate_up.s + off * groups, a.m.gate_up.b + off * groups};
         um = {gm.w + (size_t)I * words, gm.s + (size_t)I * groups, gm.b + (size_t)I * groups};
     }
-    qd_glu_block<LPR, NUL>(gm, um, I, H, a.lgG, rb * RPB, nt, a.tch, one, xs, a.qx, vin, vout, a.qact, ys);
+    qd_glu_block<LPR, NUL>(gm, um, I, a, rb * RPB, nt, one, xs, vin, vout, a.qact, ys);
+    QD_TS(4);
+    qd_signal(a.sync, QD_FL_EX + u * a.ngu, rb, a.gu_wg_per_u, a.epoch);
+    QD_TS(5);
 }
 
 // ---- down: the shared expert and every expert of a token, and the combine -------
 //
-// A workgroup owns RPG = QD_DOWN_RIT * 64/LPR output rows of one token; wave m
-// computes those rows of matrix m (0 = the shared expert, 1 + k = the token's
-// k-th expert) against that matrix's staged input, so each wave has one round
-// of loads in flight.  The per-matrix rows meet in LDS and the combine runs in
-// slot order.
-template <int LPR, int NUL>
-__global__ __launch_bounds__(QD_DOWN_MAXW * 64) void k_decode_down(QdArgs a)
+// A workgroup owns QD_DOWN_RPG output rows of one token; wave m holds those
+// rows of matrix m (0 = the shared expert, 1 + k = the token's k-th expert)
+// in registers from the moment routing is known, then waits for the
+// activations.  The per-matrix rows meet in LDS and the combine runs in slot
+// order.
+template <int NUL, int PL>
+__device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R, uint4 *xa,
+                                             float (*ys)[QD_DOWN_RPG])
 {
-    constexpr int RPP = 64 / LPR, RPG = RPP * QD_DOWN_RIT;
-    __shared__ float ys[QWK_ROUTE_MAX_K + 1][RPG];
+    constexpr int LPR = QD_DOWN_LPR, RPP = 64 / LPR, RIT = QD_DOWN_RIT, RPG = QD_DOWN_RPG;
     const int H = a.m.H, I = a.m.I, SI = a.m.SI, K = a.m.K;
-    const int rb = blockIdx.x % a.n_down_rb, t = blockIdx.x / a.n_down_rb;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int rb = bd % a.n_down_rb, t = bd / a.n_down_rb;
+    const int lane = threadIdx.x & 63, m = threadIdx.x >> 6;
     const int slot = lane / LPR, lr = lane % LPR;
     const int row0 = rb * RPG;
     const int lgG = a.lgG;
-    for (int m = wave; m <= K; m += nw) {
-        const int kin = m == 0 ? SI : I;
-        const int units = kin / 16, words = kin / 8, groups = kin >> lgG;
-        const uint32_t *wm = a.m.sh_down.w;
-        const uint16_t *sm = a.m.sh_down.s, *bm = a.m.sh_down.b;
-        const uint4 *xv = a.qsh + (size_t)t * (SI / 16) * 3;
-        if (m > 0) {
-            const size_t e = (size_t)a.idx[t * K + m - 1];
-            wm = a.m.down.w + e * H * words;
-            sm = a.m.down.s + e * H * groups;
-            bm = a.m.down.b + e * H * groups;
-            xv = a.qact + ((size_t)t * K + m - 1) * (I / 16) * 3;
+    qd_wait_router(a);
+    QD_TS(1);
+    qd_route_all<PL>(a, R);
+    QD_TS(2);
+    const float gate = qw_sigmoid(qw_ldf_coh(a.g1, (uint32_t)t * 4u));
+
+    const bool busy = m <= K;
+    const int kin = m == 0 ? SI : I;
+    const int units = kin / 16, words = kin / 8, groups = kin >> lgG;
+    const uint32_t *wm = a.m.sh_down.w;
+    const uint16_t *sm = a.m.sh_down.s, *bm = a.m.sh_down.b;
+    if (busy && m > 0) {
+        const size_t e = (size_t)R.picks[t * K + m - 1];
+        wm = a.m.down.w + e * H * words;
+        sm = a.m.down.s + e * H * groups;
+        bm = a.m.down.b + e * H * groups;
+    }
+    // Every load is issued (at a clamped, valid address) before any is used;
+    // out-of-range lanes are zeroed afterwards.
+    uint2 wv[NUL][RIT];
+    uint32_t sv[NUL][RIT], bv[NUL][RIT];
+#pragma unroll
+    for (int j = 0; j < NUL; j++) {
+        const int c = min(j * LPR + lr, units - 1);
+        const int g = (16 * c) >> lgG;
+#pragma unroll
+        for (int i = 0; i < RIT; i++) {
+            const int row = min(row0 + slot + RPP * i, H - 1);
+            wv[j][i] = qw_ld2(wm, (uint32_t)(row * words + 2 * c) * 4u);
+            sv[j][i] = qw_ldu16(sm, (uint32_t)(row * groups + g) * 2u);
+            bv[j][i] = qw_ldu16(bm, (uint32_t)(row * groups + g) * 2u);
         }
-        uint2 wv[NUL][QD_DOWN_RIT];
-        float sc[NUL][QD_DOWN_RIT], bi[NUL][QD_DOWN_RIT];
-        uint4 xp[NUL][3];
+    }
+    uint32_t sb[NUL][RIT];        // bf16 scale (low half) and bias (high half)
+#pragma unroll
+    for (int j = 0; j < NUL; j++)
+#pragma unroll
+        for (int i = 0; i < RIT; i++) {
+            const bool ok = busy && j * LPR + lr < units && row0 + slot + RPP * i < H;
+            wv[j][i] = ok ? wv[j][i] : make_uint2(0, 0);
+            sb[j][i] = ok ? sv[j][i] | (bv[j][i] << 16) : 0u;
+        }
+    // the activations: the shared expert's and this token's K experts', into
+    // LDS (vector m at xa + base(m)), device-coherently
+    if (threadIdx.x < 64) {
+        // lanes [0, gsh): the shared groups; then K * ngu lanes, the groups of
+        // each of the token's experts
+        const int lane = threadIdx.x, gsh = (a.n_sh + QD_GROUP - 1) / QD_GROUP;
+        int idx = QD_FL_SH + lane;
+        if (lane >= gsh) {
+            const int q = lane - gsh, k = q / a.ngu;
+            idx = k < K ? QD_FL_EX + R.mark[R.picks[t * K + k]] * a.ngu + q % a.ngu : 0;
+        }
+        qd_wait_flags(a.sync, lane < gsh + K * a.ngu, idx, a.epoch);
+    }
+    __syncthreads();
+    QD_TS(3);
+    const int ush = (SI / 16) * 3, uex = (I / 16) * 3;
+    for (int i = threadIdx.x; i < ush + K * uex; i += blockDim.x) {
+        const uint4 *src = i < ush ? a.qsh + (size_t)t * ush + i : a.qact + (size_t)t * K * uex + (i - ush);
+        xa[i] = qw_ld4_coh(a.scr, (uint32_t)(reinterpret_cast<const char *>(src) - a.scr));
+    }
+    __syncthreads();
+    QD_TS(4);
+    if (busy) {
+        const uint4 *xm = xa + (m == 0 ? 0 : ush + (m - 1) * uex);
+        float y[RIT];
+#pragma unroll
+        for (int i = 0; i < RIT; i++) y[i] = 0.0f;
 #pragma unroll
         for (int j = 0; j < NUL; j++) {
             const int c = j * LPR + lr;
-            const int g = (16 * c) >> lgG;
-#pragma unroll
-            for (int i = 0; i < QD_DOWN_RIT; i++) {
-                const int row = row0 + slot + RPP * i;
-                if (c < units && row < H) {
-                    wv[j][i] = *reinterpret_cast<const uint2 *>(wm + (size_t)row * words + 2 * c);
-                    sc[j][i] = qw_bf16(sm[(size_t)row * groups + g]);
-                    bi[j][i] = qw_bf16(bm[(size_t)row * groups + g]);
-                } else {
-                    wv[j][i] = make_uint2(0, 0);
-                    sc[j][i] = bi[j][i] = 0.0f;
-                }
-            }
             if (c < units) {
-                const uint4 *src = xv + (size_t)c * 3;
-                xp[j][0] = src[0]; xp[j][1] = src[1]; xp[j][2] = src[2];
-            } else {
-                xp[j][0] = xp[j][1] = xp[j][2] = make_uint4(0, 0, 0, 0);
+                const uint4 p0 = xm[3 * c], p1 = xm[3 * c + 1], rr = xm[3 * c + 2];
+                const float4 r = *reinterpret_cast<const float4 *>(&rr);
+#pragma unroll
+                for (int i = 0; i < RIT; i++)
+                    y[i] = qw_unit_dot(wv[j][i], p0, p1, r, __uint_as_float(sb[j][i] << 16),
+                                       __uint_as_float(sb[j][i] & 0xFFFF0000u), y[i]);
             }
         }
-        float y[QD_DOWN_RIT];
 #pragma unroll
-        for (int i = 0; i < QD_DOWN_RIT; i++) y[i] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NUL; j++) {
-            const float4 r = *reinterpret_cast<const float4 *>(&xp[j][2]);
-#pragma unroll
-            for (int i = 0; i < QD_DOWN_RIT; i++)
-                y[i] = qw_unit_dot(wv[j][i], xp[j][0], xp[j][1], r, sc[j][i], bi[j][i], y[i]);
-        }
-#pragma unroll
-        for (int i = 0; i < QD_DOWN_RIT; i++) {
+        for (int i = 0; i < RIT; i++) {
             const float v = qw_xor_sum<LPR>(y[i]);
             if (lr == 0) ys[m][slot + RPP * i] = v;
         }
@@ -452,10 +660,55 @@ __global__ __launch_bounds__(QD_DOWN_MAXW * 64) void k_decode_down(QdArgs a)
     for (int r = threadIdx.x; r < RPG; r += blockDim.x) {
         const int row = row0 + r;
         if (row >= H) continue;
-        float acc = ys[0][r] * qw_sigmoid(a.g1[t]);
-        for (int k = 0; k < K; k++) acc = __builtin_fmaf(a.w[t * K + k], ys[1 + k][r], acc);
+        float acc = ys[0][r] * gate;
+        for (int k = 0; k < K; k++) acc = __builtin_fmaf(R.pw[t * K + k], ys[1 + k][r], acc);
         a.out[(size_t)t * H + row] = acc;
     }
+    QD_TS(5);
+}
+
+// ---- the kernel --------------------------------------------------------------------
+
+// 8 waves per SIMD: two 16-wave workgroups per CU, which takes at most 64
+// VGPRs and 78 SGPRs a wave (at 80 SGPRs a CU holds one).
+template <int LPR, int NUL, int NULD, int PL>
+__global__ __launch_bounds__(QD_THREADS, 8) void k_decode_fused(QdArgs a)
+{
+    extern __shared__ uint4 xs[];     // [tch][units][3], or the router's partials
+    __shared__ QdRoute R;
+    __shared__ int vin[QD_MAXT], vout[QD_MAXT];
+    __shared__ float ys[QD_MAXT][QD_GU_MAXRPB];
+    static_assert(QD_MAXT * QD_GU_MAXRPB >= (QWK_DECODE_MAX_K + 1) * QD_DOWN_RPG, "down shares ys");
+    constexpr int RPB = QD_WAVES * (64 / LPR);
+    QD_TS(0);
+    int b = blockIdx.x;
+    if (b < a.n_rt) {
+        qd_role_router(a, b, reinterpret_cast<float *>(xs));
+        return;
+    }
+    b -= a.n_rt;
+    if (b < a.n_sh) {
+        // All token rows fit one LDS pass: stage them here, no wait.
+        // Otherwise copy them, pass by pass, from the router role's staging.
+        const bool own = a.rows <= a.tch;
+        if (threadIdx.x < QD_MAXT) vin[threadIdx.x] = vout[threadIdx.x] = threadIdx.x;
+        if (own) qd_stage_x(xs, a.x, nullptr, a.rows, a.m.H, 0, blockDim.x);
+        else qd_wait_router(a);
+        __syncthreads();
+        qd_glu_block<LPR, NUL>(a.m.sh_gate, a.m.sh_up, a.m.SI, a, b * RPB, a.rows, own, xs, vin, vout, a.qsh,
+                               ys);
+        QD_TS(4);
+        qd_signal(a.sync, QD_FL_SH, b, a.n_sh, a.epoch);
+        QD_TS(5);
+        return;
+    }
+    b -= a.n_sh;
+    if (b < a.n_ex) {
+        qd_role_experts<LPR, NUL, PL>(a, b, xs, R, vin, vout, ys);
+        return;
+    }
+    b -= a.n_ex;
+    qd_role_down<NULD, PL>(a, b, R, xs, reinterpret_cast<float (*)[QD_DOWN_RPG]>(&ys[0][0]));
 }
 
 // ---- host side -------------------------------------------------------------------
@@ -465,94 +718,61 @@ extern "C" size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows)
     return qd_layout(M, rows).total;
 }
 
-// A launch, with its own start / end stamps when e0 / e1 are given.
-template <typename F>
-static void qd_launch(F kern, dim3 grid, dim3 blk, size_t lds, hipStream_t s, hipEvent_t e0, hipEvent_t e1,
-                      const QdArgs &a)
+extern "C" size_t qwk_moe_decode_sync_bytes(void) { return sizeof(QdSync); }
+
+extern "C" int qwk_moe_decode_sync_error(const void *sync, uint32_t *err)
 {
-    if (e0) hipExtLaunchKernelGGL(kern, grid, blk, (uint32_t)lds, s, e0, e1, 0, a);
-    else hipLaunchKernelGGL(kern, grid, blk, lds, s, a);
+    return (int)hipMemcpy(err, &static_cast<const QdSync *>(sync)->err, sizeof *err, hipMemcpyDeviceToHost);
 }
 
-template <int LPR, int NUL>
-static void launch_experts(hipStream_t s, QdArgs &a, hipEvent_t e0, hipEvent_t e1)
+template <int LPR, int NUL, int NULD, int PL>
+static void qd_launch(hipStream_t s, const QdArgs &a, int grid, hipEvent_t e0, hipEvent_t e1)
 {
-    const dim3 grid(a.n_shared_wg + a.umax * a.gu_wg_per_u), blk(QD_GU_WAVES * 64);
-    const size_t lds = (size_t)a.tch * (a.m.H / 16) * QW_Q16_BYTES;
-    if (a.m.E <= 256) qd_launch(k_decode_experts<LPR, NUL, 4>, grid, blk, lds, s, e0, e1, a);
-    else if (a.m.E <= 512) qd_launch(k_decode_experts<LPR, NUL, 8>, grid, blk, lds, s, e0, e1, a);
-    else qd_launch(k_decode_experts<LPR, NUL, 16>, grid, blk, lds, s, e0, e1, a);
+    auto kern = k_decode_fused<LPR, NUL, NULD, PL>;
+    if (e0) hipExtLaunchKernelGGL(kern, dim3(grid), dim3(QD_THREADS), QD_LDS, s, e0, e1, 0, a);
+    else hipLaunchKernelGGL(kern, dim3(grid), dim3(QD_THREADS), QD_LDS, s, a);
 }
 
-template <int LPR, int NUL>
-static void launch_down(hipStream_t s, QdArgs &a, hipEvent_t e0, hipEvent_t e1)
-{
-    const int nw = a.m.K + 1 < QD_DOWN_MAXW ? a.m.K + 1 : QD_DOWN_MAXW;
-    qd_launch(k_decode_down<LPR, NUL>, dim3(a.rows * a.n_down_rb), dim3(nw * 64), 0, s, e0, e1, a);
-}
+// The instantiated shapes: (LPR, NUL) of the gate / up rows (k = H), NULD of
+// the down rows (k = max(I, SI), 16 lanes a row), PL logits per lane (E).
+#define QD_SHAPES(X)                                                                   \
+    X(16, 1, 1, 4) X(16, 1, 2, 4) X(16, 2, 1, 4) X(16, 2, 2, 4)                         \
+    X(32, 2, 2, 8) X(64, 2, 2, 8) X(64, 3, 2, 8) X(64, 4, 2, 8)
 
-// Instantiates F<LPR, NUL> for the supported (LPR, NUL) pairs.
-#define QD_DISPATCH_GU(F, lpr, nul, ...)                                               \
-    do {                                                                               \
-        ok = true;                                                                     \
-        switch ((lpr) * 16 + (nul)) {                                                  \
-        case 16 * 16 + 1: F<16, 1>(__VA_ARGS__); break;                                \
-        case 16 * 16 + 2: F<16, 2>(__VA_ARGS__); break;                                \
-        case 16 * 16 + 3: F<16, 3>(__VA_ARGS__); break;                                \
-        case 16 * 16 + 4: F<16, 4>(__VA_ARGS__); break;                                \
-        case 32 * 16 + 2: F<32, 2>(__VA_ARGS__); break;                                \
-        case 32 * 16 + 3: F<32, 3>(__VA_ARGS__); break;                                \
-        case 32 * 16 + 4: F<32, 4>(__VA_ARGS__); break;                                \
-        case 64 * 16 + 2: F<64, 2>(__VA_ARGS__); break;                                \
-        case 64 * 16 + 3: F<64, 3>(__VA_ARGS__); break;                                \
-        case 64 * 16 + 4: F<64, 4>(__VA_ARGS__); break;                                \
-        default: ok = false;                                                           \
-        }                                                                              \
-    } while (0)
-#define QD_DISPATCH_DOWN(F, nul, ...)                                                  \
-    do {                                                                               \
-        ok = true;                                                                     \
-        switch (nul) {                                                                 \
-        case 1: F<16, 1>(__VA_ARGS__); break;                                          \
-        case 2: F<16, 2>(__VA_ARGS__); break;                                          \
-        case 3: F<16, 3>(__VA_ARGS__); break;                                          \
-        case 4: F<16, 4>(__VA_ARGS__); break;                                          \
-        default: ok = false;                                                           \
-        }                                                                              \
-    } while (0)
-
-// Lane layouts: gate / up rows have k = H; down rows k = I (routed) or SI
-// (shared), one layout covering the larger.  Units per lane at most 4.
-static bool qd_shapes(const qwk_moe *M, int *lpr_h, int *nul_h, int *nul_d)
+static bool qd_shapes(const qwk_moe *M, int *lpr_h, int *nul_h, int *nul_d, int *pl)
 {
     const int uh = M->H / 16, ud = (M->I > M->SI ? M->I : M->SI) / 16;
     *lpr_h = qd_lpr(uh);
     *nul_h = qd_nul(uh, *lpr_h);
-    *nul_d = qd_nul(ud, 16);
-    return *nul_h > 0 && *nul_h <= 4 && *nul_d > 0 && *nul_d <= 4;
+    *nul_d = qd_nul(ud, QD_DOWN_LPR);
+    *pl = M->E <= 256 ? 4 : M->E <= 512 ? 8 : 16;
+#define QD_HAS(L, N, D, P) if (*lpr_h == L && *nul_h == N && *nul_d == D && *pl == P) return true;
+    QD_SHAPES(QD_HAS)
+#undef QD_HAS
+    return false;
 }
 
 extern "C" int qwk_moe_decode_supported(const qwk_moe *M, int rows)
 {
-    int a, b, c;
+    int a, b, c, d;
     const int G = M->group;
-    return rows >= 1 && rows <= QWK_DECODE_MAX_ROWS && M->K >= 1 && M->K <= QWK_ROUTE_MAX_K &&
+    return rows >= 1 && rows <= QWK_DECODE_MAX_ROWS && M->K >= 1 && M->K <= QWK_DECODE_MAX_K &&
            M->E >= M->K && M->E <= QWK_ROUTE_MAX_E && M->H % 64 == 0 && M->I % 16 == 0 &&
-           M->SI % 16 == 0 && M->H <= QWK_DMAT_MAX_K && (G == 32 || G == 64 || G == 128) &&
-           M->H % G == 0 && M->I % G == 0 && M->SI % G == 0 && qd_shapes(M, &a, &b, &c);
+           M->SI % 16 == 0 && M->H <= 4096 && (G == 32 || G == 64 || G == 128) &&
+           M->H % G == 0 && M->I % G == 0 && M->SI % G == 0 && qd_shapes(M, &a, &b, &c, &d);
 }
 
 extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
                               const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes,
-                              hipEvent_t *ev)
+                              void *sync, uint32_t epoch, hipEvent_t *ev)
 {
     const int G = M->group;
-    if (!qwk_moe_decode_supported(M, rows) || ((uintptr_t)x & 15u)) return (int)hipErrorInvalidValue;
+    if (!qwk_moe_decode_supported(M, rows) || ((uintptr_t)x & 15u) || !sync || epoch == 0u)
+        return (int)hipErrorInvalidValue;
     const QdLayout L = qd_layout(M, rows);
     if (scratch_bytes < L.total) return (int)hipErrorInvalidValue;
-    int lpr_h, nul_h, nul_d;
-    qd_shapes(M, &lpr_h, &nul_h, &nul_d);
-    const int lpr_d = 16;
+    int lpr_h, nul_h, nul_d, pl;
+    qd_shapes(M, &lpr_h, &nul_h, &nul_d, &pl);
 
     char *S = (char *)scratch;
     QdArgs a;
@@ -560,26 +780,34 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     a.x = x; a.out = out; a.idx = idx; a.w = w; a.rows = rows;
     a.umax = rows * M->K < M->E ? rows * M->K : M->E;
     a.lgG = G == 32 ? 5 : G == 64 ? 6 : 7;
-    a.n_router_wg = (M->E + 1 + QD_FRONT_WAVES - 1) / QD_FRONT_WAVES;
-    const int rpb = QD_GU_WAVES * (64 / lpr_h);
+    const int rpb = QD_WAVES * (64 / lpr_h);
     const int vbytes = (M->H / 16) * QW_Q16_BYTES;
-    a.tch = QD_GU_LDS / vbytes < rows ? QD_GU_LDS / vbytes : rows;
-    a.n_shared_wg = (M->SI + rpb - 1) / rpb;
+    a.tch = QD_LDS / vbytes < rows ? QD_LDS / vbytes : rows;
+    a.n_rt = (M->E + 1 + QD_RT_ROWS - 1) / QD_RT_ROWS;
+    a.n_sh = (M->SI + rpb - 1) / rpb;
     a.gu_wg_per_u = (M->I + rpb - 1) / rpb;
-    a.n_down_rb = (M->H + QD_DOWN_RIT * (64 / lpr_d) - 1) / (QD_DOWN_RIT * (64 / lpr_d));
+    a.ngu = (a.gu_wg_per_u + QD_GROUP - 1) / QD_GROUP;
+    a.n_ex = a.umax * a.gu_wg_per_u;
+    a.n_down_rb = (M->H + QD_DOWN_RPG - 1) / QD_DOWN_RPG;
+    a.scr = S;
     a.logits = (float *)(S + L.logits);
     a.g1 = (float *)(S + L.g1);
     a.qx = (uint4 *)(S + L.qx);
     a.qsh = (uint4 *)(S + L.qsh);
     a.qact = (uint4 *)(S + L.qact);
+    a.sync = (QdSync *)sync;
+    a.epoch = epoch;
+    const int gsh = (a.n_sh + QD_GROUP - 1) / QD_GROUP, grt = (a.n_rt + QD_GROUP - 1) / QD_GROUP;
+    if (a.tch < 1 || a.umax > QD_MAXU || grt > QD_FL_SH - QD_FL_RT || gsh > QD_FL_EX - QD_FL_SH ||
+        QD_FL_EX + a.umax * a.ngu > QD_NSYNC || gsh + M->K * a.ngu > 64 || grt > 64)
+        return (int)hipErrorInvalidValue;
+    const int grid = a.n_rt + a.n_sh + a.n_ex + rows * a.n_down_rb;
 
-    bool ok;
-    hipEvent_t no[6] = {0, 0, 0, 0, 0, 0};
-    hipEvent_t *e = ev ? ev : no;
-    qd_launch(k_decode_front, dim3(a.n_router_wg + rows), dim3(QD_FRONT_WAVES * 64), 0, s, e[0], e[1], a);
-    QD_DISPATCH_GU(launch_experts, lpr_h, nul_h, s, a, e[2], e[3]);
-    if (!ok) return (int)hipErrorInvalidValue;
-    QD_DISPATCH_DOWN(launch_down, nul_d, s, a, e[4], e[5]);
-    if (!ok) return (int)hipErrorInvalidValue;
+    hipEvent_t e0 = ev ? ev[0] : 0, e1 = ev ? ev[1] : 0;
+#define QD_GO(L_, N_, D_, P_) \
+    if (lpr_h == L_ && nul_h == N_ && nul_d == D_ && pl == P_) qd_launch<L_, N_, D_, P_>(s, a, grid, e0, e1); else
+    QD_SHAPES(QD_GO)
+#undef QD_GO
+    return (int)hipErrorInvalidValue;
     return (int)hipGetLastError();
 }

@@ -198,8 +198,8 @@ __device__ __forceinline__ uint32_t qw_pack_h2(float a, float b)
     return __builtin_bit_cast(uint32_t, h);
 }
 
-// Stages 16 values into one unit at dst (three uint4 stores).
-__device__ __forceinline__ void qw_q16_stage(const float v[16], uint4 *dst)
+// Stages 16 values into one unit: the three uint4 of the unit in u[].
+__device__ __forceinline__ void qw_q16_make(const float v[16], uint4 u[3])
 {
     float m = 0.0f;
 #pragma unroll
@@ -216,14 +216,24 @@ __device__ __forceinline__ void qw_q16_stage(const float v[16], uint4 *dst)
 #pragma unroll
     for (int wd = 0; wd < 2; wd++) {
         const float *q = h + 8 * wd;
-        dst[wd] = make_uint4(qw_pack_h2(q[0], q[4]), qw_pack_h2(q[2], q[6]),
-                             qw_pack_h2(q[1], q[5]), qw_pack_h2(q[3], q[7]));
+        u[wd] = make_uint4(qw_pack_h2(q[0], q[4]), qw_pack_h2(q[2], q[6]),
+                           qw_pack_h2(q[1], q[5]), qw_pack_h2(q[3], q[7]));
         xa += (q[0] + q[4]) + (q[2] + q[6]);
         xb += (q[1] + q[5]) + (q[3] + q[7]);
     }
     const float f = __builtin_ldexpf(1.0f, -sh);
     const float4 r = make_float4((xa + xb) * f, __builtin_fmaf(1024.0f, xa, 64.0f * xb), f, 0.0f);
-    dst[2] = *reinterpret_cast<const uint4 *>(&r);
+    u[2] = *reinterpret_cast<const uint4 *>(&r);
+}
+
+// Stages 16 values into one unit at dst (three uint4 stores).
+__device__ __forceinline__ void qw_q16_stage(const float v[16], uint4 *dst)
+{
+    uint4 u[3];
+    qw_q16_make(v, u);
+    dst[0] = u[0];
+    dst[1] = u[1];
+    dst[2] = u[2];
 }
 
 // ---- routing of one token ----------------------------------------------------------
@@ -264,7 +274,43 @@ __device__ __forceinline__ int qw_wave_max_i(int v)
                max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 
-template <int PL>
+// Device-coherent loads (cache policy sc1: served past this XCD's L2, so
+// they see other XCDs' sc1 stores), as buffer loads the compiler batches
+// like ordinary ones.  `base` must be wave-uniform; `off` is in bytes.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t qw_rsrc(const void *base)
+{
+    // the compiler cannot see that `base` is wave-uniform; say so
+    const uint64_t p = reinterpret_cast<uint64_t>(base);
+    // (readfirstlane returns int: widen through uint32_t, not by sign extension)
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)p);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+    const uint64_t u = (uint64_t)lo | ((uint64_t)hi << 32);
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void *>(u), (short)0, 0x7FFFFFFF, 0x00020000);
+}
+#define QW_CPOL_SC1 16
+__device__ __forceinline__ float qw_ldf_coh(const float *base, uint32_t off)
+{
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(qw_rsrc(base), off, 0, QW_CPOL_SC1));
+}
+__device__ __forceinline__ uint4 qw_ld4_coh(const void *base, uint32_t off)
+{
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(qw_rsrc(base), off, 0, QW_CPOL_SC1));
+}
+
+// Plain (cached) buffer loads from a wave-uniform base: 32-bit offsets in
+// place of 64-bit per-lane addresses.
+__device__ __forceinline__ uint2 qw_ld2(const void *base, uint32_t off)
+{
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(qw_rsrc(base), off, 0, 0));
+}
+__device__ __forceinline__ uint32_t qw_ldu16(const void *base, uint32_t off)
+{
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(qw_rsrc(base), off, 0, 0);
+}
+
+// COH: the logits were written by other workgroups of the same launch and are
+// read with device-coherent loads (past this XCD's L2).
+template <int PL, bool COH = false>
 __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E, int K, int norm,
                                               int lane, int *pick_i, float *pick_w)
 {
@@ -273,7 +319,8 @@ __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E
 #pragma unroll
     for (int j = 0; j < PL; j++) {
         const int e = lane + 64 * j;
-        const float x = l[e < E ? e : E - 1];
+        const int ec = e < E ? e : E - 1;
+        const float x = COH ? qw_ldf_coh(l, (uint32_t)ec * 4u) : l[ec];
         v[j] = e < E ? x : -__builtin_huge_valf();
         m = fmaxf(m, v[j]);
     }

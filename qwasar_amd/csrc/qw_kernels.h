@@ -80,15 +80,23 @@ typedef struct {
 /* Bytes of device scratch the decode path needs for `rows` tokens.  Nothing
  * in it needs to be initialised. */
 size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows);
+/* Bytes of the decode path's hand-off state.  It must be zeroed once before
+ * first use (and again after an error); each launch then needs an epoch one
+ * greater than the last (never 0), and launches on one state run in order. */
+size_t qwk_moe_decode_sync_bytes(void);
+/* Reads the state's error word (non-zero: a launch's bounded wait gave up;
+ * its outputs are garbage and the state must be zeroed).  Synchronous. */
+int qwk_moe_decode_sync_error(const void *sync, uint32_t *err);
 /* Non-zero when the decode path takes this layer shape and token count. */
 int qwk_moe_decode_supported(const qwk_moe *M, int rows);
-/* Decode (rows <= QWK_DECODE_MAX_ROWS): out [rows, H], idx/w [rows, K]. */
+/* Decode (rows <= QWK_DECODE_MAX_ROWS, K <= QWK_DECODE_MAX_K), one launch:
+ * out [rows, H], idx/w [rows, K].  `ev`, when not NULL, holds 2 events, the
+ * launch's start and end, stamped by the dispatch itself. */
 #define QWK_DECODE_MAX_ROWS 8
-/* `ev`, when not NULL, holds 6 events: the start and end of each of the three
- * launches (front, experts, down), stamped by the dispatches themselves. */
+#define QWK_DECODE_MAX_K 15
 int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
                    const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes,
-                   hipEvent_t *ev);
+                   void *sync, uint32_t epoch, hipEvent_t *ev);
 
 #ifdef __cplusplus
 }

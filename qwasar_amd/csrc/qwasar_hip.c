@@ -60,6 +60,7 @@ struct qw_cmd_s {
     hipEvent_t *evs;         /* every event this command created */
     int nevs, capevs;
     hipEvent_t last;         /* where the next mark starts */
+    int decoded;             /* launched the decode path since the last wait */
     struct qw_cmd_s *next;   /* live commands, for qw_buf_free */
 };
 
@@ -73,6 +74,8 @@ static struct {
     qw_cmd live;
     void *scratch;
     size_t scratch_len;
+    void *dsync;          /* the decode launch's hand-off state (zeroed) */
+    uint32_t depoch;      /* epoch of the last decode launch */
 } G;
 
 /* ---- profiling table ---------------------------------------------------- */
@@ -156,6 +159,8 @@ void qw_gpu_shutdown(void) {
     if (G.scratch) hipFree(G.scratch);
     G.scratch = NULL;
     G.scratch_len = 0;
+    if (G.dsync) hipFree(G.dsync);
+    G.dsync = NULL;
     hipStreamDestroy(G.stream);
     G.ready = 0;
 }
@@ -293,6 +298,19 @@ static void touch(qw_cmd c, qw_ref r, int writes) {
 
 static void *dp(qw_ref r) { return r.buf ? (char *)r.buf->dev + r.off : NULL; }
 
+/* The decode launch's hand-off state: allocated and zeroed on first use,
+ * zeroed again (epoch restarting) after a launch reported an error. */
+static int dsync_reset(void) {
+    hipStreamSynchronize(G.stream);
+    if (!G.dsync && hipMalloc(&G.dsync, qwk_moe_decode_sync_bytes()) != hipSuccess) {
+        G.dsync = NULL;
+        return 0;
+    }
+    if (hipMemset(G.dsync, 0, qwk_moe_decode_sync_bytes()) != hipSuccess) return 0;
+    G.depoch = 0;
+    return 1;
+}
+
 /* Launch result of one op: a refusal (invalid shape) is printed, as the
  * reference prints unsupported shapes; either kind becomes the error. */
 static void launched(qw_cmd c, const char *op, int rc) {
@@ -316,6 +334,14 @@ void qw_cmd_wait(qw_cmd c) {
     if (!c) return;
     hipError_t e = hipStreamSynchronize(G.stream);
     if (e != hipSuccess) cmd_fail(c, e, "device: %s", hipGetErrorString(e));
+    if (c->decoded) {
+        c->decoded = 0;
+        uint32_t derr = 0;
+        if (qwk_moe_decode_sync_error(G.dsync, &derr) != 0 || derr != 0) {
+            cmd_fail(c, hipErrorLaunchFailure, "moe_layer (decode): a hand-off wait gave up");
+            dsync_reset();
+        }
+    }
     for (int i = 0; i < c->nwritten; i++) {
         qw_buf b = c->written[i];
         if (b->exposed && b->host_stale) {
@@ -632,24 +658,24 @@ static void moe_desc(qwk_moe *mp, const qw_moe_layer *M) {
     *mp = m;
 }
 
-/* Decode: the fused launches over only the selected experts. */
+/* Decode: one launch over only the selected experts. */
 static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float *x,
                        const qwk_moe *mp, int32_t rows) {
     const qwk_moe m = *mp;
     const size_t need = qwk_moe_decode_scratch(&m, rows);
     void *S = scratch(need);
     if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", need); return false; }
-    /* Profiling charges each of the three launches to its own label. */
-    hipEvent_t ev[6] = { NULL, NULL, NULL, NULL, NULL, NULL };
-    int per_kernel = G.prof != 0;
-    for (int i = 0; per_kernel && i < 6; i++)
-        if (!(ev[i] = cmd_event(c, 0))) per_kernel = 0;
-    const int rc = qwk_moe_decode(G.stream, out, idx, w, x, &m, rows, S, need,
-                                  per_kernel ? ev : NULL);
-    if (per_kernel) {
-        static const char *labels[3] = { "moe decode front", "moe decode experts", "moe decode down" };
-        for (int i = 0; i < 3; i++) cmd_add_mark(c, labels[i], ev[2 * i], ev[2 * i + 1]);
+    if (!G.dsync && !dsync_reset()) {
+        cmd_fail(c, hipErrorOutOfMemory, "moe_layer: decode hand-off state");
+        return false;
     }
+    if (++G.depoch == 0u) G.depoch = 1u;   /* flags hold past epochs; 0 is "never" */
+    hipEvent_t ev[2] = { NULL, NULL };
+    const int per_kernel = G.prof && (ev[0] = cmd_event(c, 0)) && (ev[1] = cmd_event(c, 0));
+    const int rc = qwk_moe_decode(G.stream, out, idx, w, x, &m, rows, S, need, G.dsync, G.depoch,
+                                  per_kernel ? ev : NULL);
+    if (per_kernel) cmd_add_mark(c, "moe decode", ev[0], ev[1]);
+    c->decoded = 1;
     launched(c, "moe_layer (decode)", rc);
     return rc == 0;
 }

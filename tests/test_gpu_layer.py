@@ -153,3 +153,28 @@ def test_config3_prefill_sample(gpu):
     out2, _, _ = run_layer(gpu, lb, x)
     assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
     lb.free()
+
+
+@pytest.mark.parametrize("rows", [1, 3])
+def test_decode_back_to_back(gpu, c1, rows):
+    """Sixteen decode launches queued in one command, each on its own tokens
+    and into its own outputs: every launch hands its router logits and
+    activations between workgroups through device memory, and none may see
+    a neighbour's.  Each result against the oracle."""
+    L, lb = c1
+    n = 16
+    x = synth.make_x(900 + rows, n * rows, L.H)
+    B = gpu.Buf
+    xb, ob = B.of(x), B(n * rows * L.H * 4)
+    ib, wb = B(n * rows * L.K * 4), B(n * rows * L.K * 4)
+    c = gpu.qw_cmd_begin()
+    for s in range(n):
+        assert gpu.qw_op_moe_layer(c, ob.ref(s * rows * L.H * 4), ib.ref(s * rows * L.K * 4),
+                                   wb.ref(s * rows * L.K * 4), xb.ref(s * rows * L.H * 4), lb.desc, rows)
+    gpu.run(c, f"moe_layer x{n} rows={rows}")
+    out = ob.read(np.float32, (n, rows, L.H))
+    idx = ib.read(np.int32, (n, rows, L.K))
+    w = wb.read(np.float32, (n, rows, L.K))
+    for s in range(n):
+        want = ref.moe_forward(L, np.ascontiguousarray(x[s * rows:(s + 1) * rows]))
+        check((out[s], idx[s], w[s]), want, DECODE_REL)
