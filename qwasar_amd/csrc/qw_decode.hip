@@ -33,6 +33,10 @@
 // loaded straight into registers next to the weights.
 #include <hip/hip_ext.h>
 
+#ifdef QD_TRACE
+extern __device__ unsigned long long qd_trace[8192 * 8];
+#define QW_STAMP(slot) do { if (threadIdx.x == 0) qd_trace[blockIdx.x * 8 + (slot)] = wall_clock64(); } while (0)
+#endif
 #include "qw_device.h"
 #include "qw_kernels.h"
 
@@ -58,12 +62,14 @@ extern "C" int qd_trace_read(unsigned long long *dst)
 #define QD_DOWN_LPR 16
 #define QD_DOWN_RIT 4               // down rows per lane slot
 #define QD_DOWN_RPG ((64 / QD_DOWN_LPR) * QD_DOWN_RIT)
+#define QD_DOWN_XA 3                // activation uint4 a thread: (K + 1) * 64 units * 3 <= 3 * QD_THREADS
 #define QD_SPIN_LIMIT (1 << 16)     // polls (each a memory round trip plus a sleep)
 
 static_assert((64 * 68 + 4 * 64) * 4 <= QD_LDS, "router: a padded token row and partials fit the dynamic LDS");
 static_assert(QWK_DECODE_MAX_K + 1 <= QD_WAVES, "down: one wave per matrix");
 // down: the K + 1 activation vectors (at most 64 units each) in LDS
 static_assert((QWK_DECODE_MAX_K + 1) * 64 * QW_Q16_BYTES <= QD_LDS, "down activations fit the dynamic LDS");
+static_assert((QWK_DECODE_MAX_K + 1) * 64 * 3 <= QD_DOWN_XA * QD_THREADS, "down activations: one pass");
 
 // Lanes per row for a row of `units` q16 units, and units per lane.
 static __host__ __device__ constexpr int qd_lpr(int units) { return units >= 128 ? 64 : units >= 64 ? 32 : 16; }
@@ -360,8 +366,19 @@ __device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, i
         if (!staged) {
             __syncthreads();
             const int per = units * 3;
-            for (int i = threadIdx.x; i < tn * per; i += blockDim.x)
-                xs[i] = qw_ld4_coh(a.qx, (uint32_t)((vin[t0 + i / per] * per + i % per) * 16));
+            for (int i0 = 0; i0 < tn * per; i0 += 4 * QD_THREADS) {
+                uint4 v[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int i = min(i0 + (int)threadIdx.x + r * QD_THREADS, tn * per - 1);
+                    v[r] = qw_ld4_coh(a.qx, (uint32_t)((vin[t0 + i / per] * per + i % per) * 16));
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) asm volatile("" : "+v"(v[r].x), "+v"(v[r].y), "+v"(v[r].z), "+v"(v[r].w));
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (i0 + (int)threadIdx.x + r * QD_THREADS < tn * per) xs[i0 + threadIdx.x + r * QD_THREADS] = v[r];
+            }
         }
         __syncthreads();
 #pragma unroll 1
@@ -625,10 +642,21 @@ __device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R
     }
     __syncthreads();
     QD_TS(3);
-    const int ush = (SI / 16) * 3, uex = (I / 16) * 3;
-    for (int i = threadIdx.x; i < ush + K * uex; i += blockDim.x) {
-        const uint4 *src = i < ush ? a.qsh + (size_t)t * ush + i : a.qact + (size_t)t * K * uex + (i - ush);
-        xa[i] = qw_ld4_coh(a.scr, (uint32_t)(reinterpret_cast<const char *>(src) - a.scr));
+    const int ush = (SI / 16) * 3, uex = (I / 16) * 3, nxa = ush + K * uex;
+    {
+        // up to QD_DOWN_XA uint4 a thread, all issued before any is stored
+        uint4 v[QD_DOWN_XA];
+#pragma unroll
+        for (int r = 0; r < QD_DOWN_XA; r++) {
+            const int i = min((int)threadIdx.x + r * QD_THREADS, nxa - 1);
+            const uint4 *src = i < ush ? a.qsh + (size_t)t * ush + i : a.qact + (size_t)t * K * uex + (i - ush);
+            v[r] = qw_ld4_coh(a.scr, (uint32_t)(reinterpret_cast<const char *>(src) - a.scr));
+        }
+#pragma unroll
+        for (int r = 0; r < QD_DOWN_XA; r++) asm volatile("" : "+v"(v[r].x), "+v"(v[r].y), "+v"(v[r].z), "+v"(v[r].w));
+#pragma unroll
+        for (int r = 0; r < QD_DOWN_XA; r++)
+            if (threadIdx.x + r * QD_THREADS < nxa) xa[threadIdx.x + r * QD_THREADS] = v[r];
     }
     __syncthreads();
     QD_TS(4);
@@ -655,7 +683,9 @@ __device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R
             if (lr == 0) ys[m][slot + RPP * i] = v;
         }
     }
+    QD_TS(6);
     __syncthreads();
+    QD_TS(7);
     // The combine: the shared term first, then an fma per slot, in order.
     for (int r = threadIdx.x; r < RPG; r += blockDim.x) {
         const int row = row0 + r;

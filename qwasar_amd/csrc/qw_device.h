@@ -10,6 +10,12 @@
 
 #define QW_WAVE 64
 
+// Timeline stamps inside shared helpers; a kernel file that records a trace
+// defines QW_STAMP before including this header.
+#ifndef QW_STAMP
+#define QW_STAMP(slot) do { } while (0)
+#endif
+
 __device__ __forceinline__ float qw_bf16(uint16_t v) {
     return __uint_as_float((uint32_t)v << 16);
 }
@@ -318,13 +324,19 @@ __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E
     float m = -__builtin_huge_valf();
 #pragma unroll
     for (int j = 0; j < PL; j++) {
-        const int e = lane + 64 * j;
-        const int ec = e < E ? e : E - 1;
-        const float x = COH ? qw_ldf_coh(l, (uint32_t)ec * 4u) : l[ec];
-        v[j] = e < E ? x : -__builtin_huge_valf();
+        const int ec = min(lane + 64 * j, E - 1);
+        v[j] = COH ? qw_ldf_coh(l, (uint32_t)ec * 4u) : l[ec];
+    }
+    // every load issued before the first is used (one memory round trip)
+#pragma unroll
+    for (int j = 0; j < PL; j++) asm volatile("" : "+v"(v[j]));
+#pragma unroll
+    for (int j = 0; j < PL; j++) {
+        v[j] = lane + 64 * j < E ? v[j] : -__builtin_huge_valf();
         m = fmaxf(m, v[j]);
     }
     m = qw_wave_max(m);
+    QW_STAMP(6);
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < PL; j++) {
@@ -356,6 +368,7 @@ __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E
     // (bits(p) + 2) << 2 | (3 - slot % 4): p < 2 has bits below 2^30, so the
     // key orders by p and then by the lower slot.  A slot past E has key < 4,
     // an emptied one 0, both below every probability (keys >= 8).
+    QW_STAMP(7);
     constexpr int NG = PL / 4;
     uint32_t g[NG][4];
 #pragma unroll
