@@ -106,6 +106,15 @@ __global__ __launch_bounds__(G16_THREADS) void k_stage16(_Float16 *__restrict__ 
 
 // ---- the product ------------------------------------------------------------------
 
+// (w >> 4j) nibble pairs into f16 1024 + q.  Plain C++ (not inline asm, so
+// the compiler sees the instruction and keeps its wait states against MFMAs
+// still reading registers); with the mask in an SGPR and the f16 1024
+// pattern in a VGPR it selects one v_and_or_b32.
+__device__ __forceinline__ uint32_t g16_nib(uint32_t w, uint32_t mask, uint32_t magic)
+{
+    return (w & mask) | magic;
+}
+
 struct Gmm16Args {
     float *y;
     long ldy;
@@ -119,6 +128,7 @@ struct Gmm16Args {
     int K, x_by_pair;               // grouped A row of pair p: x_by_pair ? p : p / K
     int rows;                       // dense: rows
     int nblk;                       // column blocks per tile
+    int nbw;                        // column blocks a workgroup runs back to back
 };
 
 #ifndef G16_OCC
@@ -138,8 +148,10 @@ __global__ __launch_bounds__(G16_THREADS, G16_OCC) void k_gmm16(Gmm16Args a)
     __shared__ float Fr[G16_BM];
     __shared__ int srow[G16_BM], drow[G16_BM];
 
-    const int bid = blockIdx.x, xcd = bid & 7, r = bid >> 3;
-    const int tile = (r / a.nblk) * 8 + xcd, nb = r % a.nblk;
+    // Workgroup b: XCD b % 8; tile (r / ng) * 8 + b % 8 and column blocks
+    // [nb0, nb0 + nitems) with r = b / 8, run as one stream of chunks.
+    const int bid = blockIdx.x, xcd = bid & 7, r = bid >> 3, ngr = (a.nblk + a.nbw - 1) / a.nbw;
+    const int tile = (r / ngr) * 8 + xcd, nb0 = (r % ngr) * a.nbw, nitems = min(a.nbw, a.nblk - nb0);
     int expert, first, len;
     if (DENSE) {
         first = tile * G16_BM;
@@ -153,7 +165,7 @@ __global__ __launch_bounds__(G16_THREADS, G16_OCC) void k_gmm16(Gmm16Args a)
         len = a.tiles[3 + 3 * tile];
     }
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, ln = lane & 15, kg = lane >> 4;
-    const int k = a.k, words = k / 8, groups = k / G, nch = k / KC;
+    const int k = a.k, words = k / 8, groups = k / G, nch = k / KC, T = nitems * nch;
     if (t < G16_BM) {
         int sr = -1, dr = -1;
         if (t < len) {
@@ -186,8 +198,8 @@ __global__ __launch_bounds__(G16_THREADS, G16_OCC) void k_gmm16(Gmm16Args a)
     float rx;
     // every fetch is issued, at a chunk clamped to the last: the same loads in
     // every pass, so the waits before each use count exactly
-    auto fetch_a = [&](int c) {
-        c = min(c, nch - 1);
+    auto fetch_a = [&](int step) {
+        const int c = min(step, T - 1) % nch;
 #pragma unroll
         for (int i = 0; i < AU4; i++)
             ra[i] = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rA, offA + c * KC * 2 + 16 * i, 0, 0));
@@ -200,32 +212,33 @@ __global__ __launch_bounds__(G16_THREADS, G16_OCC) void k_gmm16(Gmm16Args a)
         if (xw) Xs[q][xm][xgi] = xsrc >= 0 ? rx : 0.0f;
     };
 
-    // Weights: lane (ln, kg) of wave w owns weight row col(nt) of tile nt; per
-    // chunk, SPG words of each of the GPC groups, and the groups' scales and
-    // biases (GPC consecutive bf16 each).
+    // Weights: lane (ln, kg) of wave w owns weight row col(item, nt) of tile
+    // nt; per chunk, SPG words of each of the GPC groups, and the groups'
+    // scales and biases (GPC consecutive bf16 each).
     __amdgpu_buffer_rsrc_t rW[2], rS[2], rB[2];
-    uint32_t offW[2], offG[2];
 #pragma unroll
     for (int nt = 0; nt < 2; nt++) {
         const bool up = SWIGLU && nt == 1;
-        const int col = SWIGLU ? nb * 64 + wave * 16 + ln : nb * G16_BN + wave * 32 + nt * 16 + ln;
-        const int cc = col < a.n ? col : 0;
         rW[nt] = qw_rsrc((up ? a.w1 : a.w0) + (size_t)expert * a.ew);
         rS[nt] = qw_rsrc((up ? a.s1 : a.s0) + (size_t)expert * a.eg);
         rB[nt] = qw_rsrc((up ? a.b1 : a.b0) + (size_t)expert * a.eg);
-        offW[nt] = (uint32_t)((cc * words + kg * SPG) * 4);
-        offG[nt] = (uint32_t)(cc * groups * 2);
     }
+    auto colof = [&](int item, int nt) {
+        const int nb = nb0 + item;
+        return SWIGLU ? nb * 64 + wave * 16 + ln : nb * G16_BN + wave * 32 + nt * 16 + ln;
+    };
     // wq holds, group by group, the words of the chunk being computed; as
-    // soon as group gg is consumed its registers take the next chunk's group
+    // soon as group gg is consumed its registers take the next step's group
     // gg (an in-place ring: the loads get the rest of the chunk to land).
     uint32_t wq[2][WPC];
     uint32_t sq[2][(GPC + 1) / 2], bq[2][(GPC + 1) / 2];   // bf16 pairs
-    auto fetch_group = [&](int c, int gg) {
-        c = min(c, nch - 1);
+    auto fetch_group = [&](int step, int gg) {
+        step = min(step, T - 1);
+        const int item = step / nch, c = step % nch;
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
-            const uint32_t o = offW[nt] + (uint32_t)((c * (KC / 8) + gg * (G / 8)) * 4);
+            const int col = colof(item, nt), cc = col < a.n ? col : 0;
+            const uint32_t o = (uint32_t)((cc * words + kg * SPG + c * (KC / 8) + gg * (G / 8)) * 4);
             if (SPG == 1) wq[nt][gg] = __builtin_amdgcn_raw_buffer_load_b32(rW[nt], o, 0, 0);
             if (SPG == 2) {
                 const g16_u2 v = __builtin_bit_cast(g16_u2, __builtin_amdgcn_raw_buffer_load_b64(rW[nt], o, 0, 0));
@@ -238,11 +251,13 @@ __global__ __launch_bounds__(G16_THREADS, G16_OCC) void k_gmm16(Gmm16Args a)
         }
     };
     // the chunk's GPC scales and biases of each weight tile, as bf16 pairs
-    auto fetch_sb = [&](int c) {
-        c = min(c, nch - 1);
+    auto fetch_sb = [&](int step) {
+        step = min(step, T - 1);
+        const int item = step / nch, c = step % nch;
 #pragma unroll
         for (int nt = 0; nt < 2; nt++) {
-            const uint32_t o = offG[nt] + (uint32_t)(c * GPC * 2);
+            const int col = colof(item, nt), cc = col < a.n ? col : 0;
+            const uint32_t o = (uint32_t)((cc * groups + c * GPC) * 2);
             if (GPC == 1) {
                 sq[nt][0] = __builtin_amdgcn_raw_buffer_load_b16(rS[nt], o, 0, 0);
                 bq[nt][0] = __builtin_amdgcn_raw_buffer_load_b16(rB[nt], o, 0, 0);
@@ -266,6 +281,8 @@ __global__ __launch_bounds__(G16_THREADS, G16_OCC) void k_gmm16(Gmm16Args a)
     };
 
     g16_f4 acc[2][2], C[2][2];
+    uint32_t magic = 0x64006400u, mask = 0x000F000Fu;
+    asm volatile("" : "+v"(magic), "+s"(mask));   // one in a VGPR, one in an SGPR
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
 #pragma unroll
@@ -279,8 +296,8 @@ __global__ __launch_bounds__(G16_THREADS, G16_OCC) void k_gmm16(Gmm16Args a)
     fetch_sb(0);
     __syncthreads();
 
-    for (int c = 0; c < nch; c++) {
-        const int q = c & 1;
+    for (int i = 0; i < T; i++) {
+        const int q = i & 1, item = i / nch, c = i % nch;
         // this chunk's scales and biases (kept raw), then the next chunk's in flight
         uint32_t sqc[2][(GPC + 1) / 2], bqc[2][(GPC + 1) / 2];
 #pragma unroll
@@ -290,77 +307,94 @@ __global__ __launch_bounds__(G16_THREADS, G16_OCC) void k_gmm16(Gmm16Args a)
                 sqc[nt][i] = sq[nt][i];
                 bqc[nt][i] = bq[nt][i];
             }
-        fetch_sb(c + 1);
+        fetch_sb(i + 1);
+        // Group gg's MFMAs, then group gg - 1's affine epilogue: the epilogue
+        // reads partials whose MFMAs had the current group's to finish behind.
+        g16_f4 Cp[2][2];
 #pragma unroll
-        for (int gg = 0; gg < GPC; gg++) {
+        for (int gg = 0; gg <= GPC; gg++) {
             // keeps each group's LDS reads from being hoisted into earlier ones
             __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++) C[mt][nt] = g16_f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int s = 0; s < SPG; s++) {
-                g16_h8 bf[2];
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++) {
-                    uint32_t wd = wq[nt][gg * SPG + s];
-                    asm volatile("" : "+v"(wd));      // dequantised here, not ahead of time
-                    const g16_u4 u = {(wd & 0x000F000Fu) | 0x64006400u, ((wd >> 4) & 0x000F000Fu) | 0x64006400u,
-                                      ((wd >> 8) & 0x000F000Fu) | 0x64006400u,
-                                      ((wd >> 12) & 0x000F000Fu) | 0x64006400u};
-                    bf[nt] = __builtin_bit_cast(g16_h8, u);
-                }
-                const int ah = gg * G + 8 * (kg * SPG + s);
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++) {
-                    const g16_h8 af = *reinterpret_cast<const g16_h8 *>(&As[q][mt * 16 + ln][ah]);
-#pragma unroll
-                    for (int nt = 0; nt < 2; nt++)
-                        C[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[nt], C[mt][nt], 0, 0, 0);
-                }
-            }
-            fetch_group(c + 1, gg);
-#pragma unroll
-            for (int nt = 0; nt < 2; nt++) {
-                const float sc = __uint_as_float((sqc[nt][gg / 2] >> (16 * (gg % 2))) << 16);
-                const float bc =
-                    __builtin_fmaf(-1024.0f, sc, __uint_as_float((bqc[nt][gg / 2] >> (16 * (gg % 2))) << 16));
+            if (gg < GPC) {
 #pragma unroll
                 for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float xg = Xs[q][mt * 16 + 4 * kg + i][gg];
-                        acc[mt][nt][i] = __builtin_fmaf(sc, C[mt][nt][i], __builtin_fmaf(bc, xg, acc[mt][nt][i]));
+                    for (int nt = 0; nt < 2; nt++) C[mt][nt] = g16_f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < SPG; s++) {
+                    g16_h8 bf[2];
+#pragma unroll
+                    for (int nt = 0; nt < 2; nt++) {
+                        uint32_t wd = wq[nt][gg * SPG + s];
+                        asm volatile("" : "+v"(wd));      // dequantised here, not ahead of time
+                        const g16_u4 u = {g16_nib(wd, mask, magic), g16_nib(wd >> 4, mask, magic),
+                                          g16_nib(wd >> 8, mask, magic), g16_nib(wd >> 12, mask, magic)};
+                        bf[nt] = __builtin_bit_cast(g16_h8, u);
                     }
+                    const int ah = gg * G + 8 * (kg * SPG + s);
+#pragma unroll
+                    for (int mt = 0; mt < 2; mt++) {
+                        const g16_h8 af = *reinterpret_cast<const g16_h8 *>(&As[q][mt * 16 + ln][ah]);
+#pragma unroll
+                        for (int nt = 0; nt < 2; nt++)
+                            C[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[nt], C[mt][nt], 0, 0, 0);
+                    }
+                }
+                fetch_group(i + 1, gg);
             }
-        }
-        stash_a(q ^ 1);
-        fetch_a(c + 2);
-        __syncthreads();
-    }
-
-    // out: y = F (acc), with SWIGLU silu(F g) * (F u)
-#pragma unroll
-    for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = mt * 16 + 4 * kg + i;
-            const int dr = drow[m];
-            if (dr < 0) continue;
-            const float f = Fr[m];
-            float *yr = a.y + (size_t)dr * a.ldy;
-            if (SWIGLU) {
-                const int col = nb * 64 + wave * 16 + ln;
-                if (col < a.n) yr[col] = qw_silu(f * acc[mt][0][i]) * (f * acc[mt][1][i]);
-            } else {
+            if (gg > 0) {
+                const int pg = gg - 1;
 #pragma unroll
                 for (int nt = 0; nt < 2; nt++) {
-                    const int col = nb * G16_BN + wave * 32 + nt * 16 + ln;
-                    if (col < a.n) yr[col] = f * acc[mt][nt][i];
+                    const float sc = __uint_as_float((sqc[nt][pg / 2] >> (16 * (pg % 2))) << 16);
+                    const float bc =
+                        __builtin_fmaf(-1024.0f, sc, __uint_as_float((bqc[nt][pg / 2] >> (16 * (pg % 2))) << 16));
+#pragma unroll
+                    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const float xg = Xs[q][mt * 16 + 4 * kg + e][pg];
+                            acc[mt][nt][e] = __builtin_fmaf(sc, Cp[mt][nt][e], __builtin_fmaf(bc, xg, acc[mt][nt][e]));
+                        }
                 }
             }
+            if (gg < GPC) {
+#pragma unroll
+                for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                    for (int nt = 0; nt < 2; nt++) Cp[mt][nt] = C[mt][nt];
+            }
         }
+        if (c == nch - 1) {
+            // the item is done: out, y = F (acc), with SWIGLU silu(F g) * (F u)
+#pragma unroll
+            for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int m = mt * 16 + 4 * kg + e;
+                    const int dr = drow[m];
+                    if (dr >= 0) {
+                        const float f = Fr[m];
+                        float *yr = a.y + (size_t)dr * a.ldy;
+                        if (SWIGLU) {
+                            const int col = colof(item, 0);
+                            if (col < a.n) yr[col] = qw_silu(f * acc[mt][0][e]) * (f * acc[mt][1][e]);
+                        } else {
+#pragma unroll
+                            for (int nt = 0; nt < 2; nt++) {
+                                const int col = colof(item, nt);
+                                if (col < a.n) yr[col] = f * acc[mt][nt][e];
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int nt = 0; nt < 2; nt++) acc[mt][nt][e] = 0.0f;
+                }
+        }
+        stash_a(q ^ 1);
+        fetch_a(i + 2);
+        __syncthreads();
+    }
 }
 
 // ---- host side ---------------------------------------------------------------------
@@ -415,8 +449,16 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
     a.nblk = swiglu ? (n + 63) / 64 : (n + G16_BN - 1) / G16_BN;
     const int ntiles = dense ? (dense_rows + G16_BM - 1) / G16_BM : max_tiles;
     if (ntiles <= 0) return 0;
-    // tile = (r / nblk) * 8 + b % 8 with r = b / 8: a multiple of 8 tiles
-    const unsigned grid = (unsigned)(a.nblk * ((ntiles + 7) / 8) * 8);
+    // column blocks per workgroup: long streams, but enough workgroups to
+    // fill the chip (max_tiles bounds the grouped tile count from above)
+    {
+        const long per = (long)ntiles * a.nblk / 1024;
+        a.nbw = per < 1 ? 1 : per > 8 ? 8 : (int)per;
+        if (a.nbw > a.nblk) a.nbw = a.nblk;
+    }
+    // tile = (r / ngr) * 8 + b % 8 with r = b / 8: a multiple of 8 tiles
+    const int ngr = (a.nblk + a.nbw - 1) / a.nbw;
+    const unsigned grid = (unsigned)(ngr * ((ntiles + 7) / 8) * 8);
     if (kc == G16_KC) {
         switch (group) {
         case 32: g16_launch<32, G16_KC>(s, a, swiglu, dense, grid); break;
