@@ -194,6 +194,8 @@ def main():
     ap.add_argument("--calib-copy", type=int, default=0, help="bytes: run only the copy calibration")
     ap.add_argument("--decode-only-steps", type=int, default=0,
                     help="profiling aid: only run this many decode steps after setup")
+    ap.add_argument("--prefill-only-rows", type=int, default=0,
+                    help="profiling aid: only time prefill of this many uniform-routed rows")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -214,6 +216,12 @@ def main():
 
     if args.decode_only_steps:
         time_decode(gpu, lb, xpool, args.decode_only_steps, 0, False)
+        return
+    if args.prefill_only_rows:
+        rows = args.prefill_only_rows
+        x = synth.make_x(seed + rows, rows, L.H, name=f"bench.prefill{rows}")
+        ms, _, _ = time_prefill(gpu, lb, x, reps=5)
+        print(json.dumps({"prefill_rows": rows, "ms": round(ms, 3)}), flush=True)
         return
 
     nb = decode_bytes(cfg)

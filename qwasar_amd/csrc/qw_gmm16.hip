@@ -3,39 +3,34 @@
 //
 // Staging (k_stage16).  A row of k activations is scaled by one power of two
 // 2^sh chosen so that its largest magnitude lands in [2^14, 2^15), and
-// rounded to f16: h = f16(x 2^sh).  The stage keeps F = 2^-sh per row and
-// Xh = sum(h) per (row, quantisation group of G).  No input overflows f16;
-// f16's normal range then covers every value within 2^-28 of the row's
-// largest.  Within every 8-element block the f16 values are stored in the
-// order 0,4,1,5,2,6,3,7: the order in which one packed weight word yields its
-// nibbles (below), so A and B fragments agree element for element.
+// rounded to f16: h = f16(x 2^sh); the stage keeps F = 2^-sh per row.  No
+// input overflows f16; f16's normal range then covers every value within
+// 2^-28 of the row's largest.  Within every 8-element block the f16 values
+// are stored in the order 0,4,1,5,2,6,3,7: the order in which one packed
+// weight word yields its nibble pairs (below), so A and B fragments agree
+// element for element.
 //
-// Exactness of the weight operand.  A nibble q enters the MFMA as the f16
-// value 1024 + q, built from its packed word with one and-or per pair
-// ((w >> 4j) & 0x000F000F | 0x64006400).  Per group the MFMA accumulates
-// C = sum_i (1024 + q_i) h_i in fp32, and the group's affine map is applied
-// to that partial:
+// Weight operand.  Each packed word is dequantised in registers to four f16
+// pairs w = s q + b (one rounding each, g16_dq) and fed to the MFMA as the
+// B fragment; accumulation is fp32 across all of k, and the output row is
+// scaled by F at the end.  Activations and weights both carry one f16
+// rounding.
 //
-//   sum_i (s q_i + b) x_i = F (s C + (b - 1024 s) Xh)
+// Tiles.  A workgroup (4 waves) owns up to 64 rows (a tile of one expert's
+// pairs, or of dense rows) against 256 weight rows: with SWIGLU, 128 gate
+// and the same 128 up features, so gate and up meet in one lane and leave as
+// silu(g) * u.  Wave w holds 4 weight tiles of 16 rows against 4 row tiles
+// of 16.  K streams in chunks of KC (256 where k allows): the activation
+// chunk through double-buffered LDS, its loads two chunks ahead; each lane's
+// own weight words straight from memory into registers, one chunk ahead.
+// Per chunk lane group kg (lanes 16 kg .. 16 kg + 15) holds KC / 4
+// consecutive k of each of its weight rows (one quantisation group when
+// G = KC / 4), so the 4 lane groups' loads cover whole 128-byte lines.
 //
-// so weights carry no rounding; activations carry f16 rounding only.
-//
-// Tiles.  A workgroup (4 waves) owns up to 32 rows (a tile of one expert's
-// pairs, or of dense rows) against 128 weight rows: with SWIGLU, 64 gate and
-// the same 64 up features, so gate and up meet in one lane and leave as
-// silu(g) * u.  Wave w holds 2 weight tiles of 16 rows against 2 row tiles of
-// 16.  K streams in chunks of KC (256 where k allows): the activation chunk
-// through double-buffered LDS, the next one's loads in flight while the
-// current one runs; each lane's own weight words straight from memory into
-// registers, one chunk ahead.  Within a quantisation group of G, lane group
-// kg (lanes 16 kg .. 16 kg + 15) holds words [kg G/32, (kg + 1) G/32) of each
-// row and MFMA step s of the group takes word kg G/32 + s from every lane
-// group, so a step never spans two groups and a chunk's loads cover whole
-// 128-byte lines of every weight row at once.
-//
-// Order of tiles.  Workgroup b runs on XCD b % 8; an expert's column blocks
-// stay on one XCD (they share its activation rows in that XCD's L2) and
-// consecutive tiles go to consecutive XCDs.
+// Order of tiles.  Workgroup b runs on XCD b % 8.  Each XCD takes a
+// contiguous range of tiles, walked with the column block fastest: the
+// workgroups resident together on one XCD share activation chunks and (for
+// an expert's adjacent tiles) weight lines in that XCD's L2.
 #include "qw_device.h"
 #include "qw_kernels.h"
 
@@ -43,22 +38,19 @@ typedef _Float16 g16_h8 __attribute__((ext_vector_type(8)));
 typedef float g16_f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t g16_u4 __attribute__((ext_vector_type(4)));   // native vectors: selects stay in registers
 typedef uint32_t g16_u2 __attribute__((ext_vector_type(2)));
+typedef _Float16 g16_h2 __attribute__((ext_vector_type(2)));
 
-#define G16_BM 32
-#define G16_BN 128
+#define G16_BM 64
+#define G16_BN 256
 #define G16_THREADS 256
 
 // ---- staging ------------------------------------------------------------------------
 
 // One wave per row.  Pass 1: the row's largest magnitude.  Pass 2: lane l
-// converts 8-blocks l, l + 64, ...; a group is G / 8 consecutive blocks, so
-// G / 8 consecutive lanes, whose sum meets by xor steps.
-template <int G>
+// converts 8-blocks l, l + 64, ...
 __global__ __launch_bounds__(G16_THREADS) void k_stage16(_Float16 *__restrict__ h, float *__restrict__ F,
-                                                         float *__restrict__ X, const float *__restrict__ x,
-                                                         int rows, int k)
+                                                         const float *__restrict__ x, int rows, int k)
 {
-    constexpr int TPG = G / 8;
     const int row = blockIdx.x * (G16_THREADS / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= rows) return;
     const int nb = k / 8;
@@ -77,49 +69,52 @@ __global__ __launch_bounds__(G16_THREADS) void k_stage16(_Float16 *__restrict__ 
     }
     if (lane == 0) F[row] = __builtin_ldexpf(1.0f, -sh);
     g16_h8 *hr = reinterpret_cast<g16_h8 *>(h + (size_t)row * k);
-    float *Xr = X + (size_t)row * (k / G);
-    for (int b0 = 0; b0 < nb; b0 += 64) {
-        const int b = b0 + lane;
-        float v[8];
-        if (b < nb) {
-            const float4 lo = xr[2 * b], hi = xr[2 * b + 1];
-            v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
-            v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = 0.0f;
-        }
+    for (int b = lane; b < nb; b += 64) {
+        const float4 lo = xr[2 * b], hi = xr[2 * b + 1];
+        const float v[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
         _Float16 q[8];
-        float s = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            q[j] = (_Float16)__builtin_ldexpf(v[j], sh);
-            s += (float)q[j];
-        }
-        s = qw_xor_sum<TPG>(s);
-        if (b < nb) {
-            hr[b] = g16_h8{q[0], q[4], q[1], q[5], q[2], q[6], q[3], q[7]};
-            if (b % TPG == 0) Xr[b / TPG] = s;
-        }
+        for (int j = 0; j < 8; j++) q[j] = (_Float16)__builtin_ldexpf(v[j], sh);
+        hr[b] = g16_h8{q[0], q[4], q[1], q[5], q[2], q[6], q[3], q[7]};
     }
 }
 
 // ---- the product ------------------------------------------------------------------
 
-// (w >> 4j) nibble pairs into f16 1024 + q.  Plain C++ (not inline asm, so
-// the compiler sees the instruction and keeps its wait states against MFMAs
-// still reading registers); with the mask in an SGPR and the f16 1024
-// pattern in a VGPR it selects one v_and_or_b32.
-__device__ __forceinline__ uint32_t g16_nib(uint32_t w, uint32_t mask, uint32_t magic)
+// One packed word (8 nibbles, k order 0..7) into 4 f16 pairs in the staged
+// order (0,4),(1,5),(2,6),(3,7), each w = s q + b rounded once to f16.  The
+// and-or puts a nibble pair into the mantissa of an f16 pair whose exponent
+// makes the nibble an exact integer offset: 1024 + q for bits 0-3 (ulp 1),
+// 64 + q for bits 4-7 (ulp 1/16).  Subtracting the offset is exact; the fma
+// rounds once.  lo, hi: the two and-or patterns, kept in VGPRs by the caller
+// (with the masks as SGPR literals each and-or reads one scalar).
+__device__ __forceinline__ void g16_dq(uint32_t w, g16_h2 s2, g16_h2 b2, uint32_t lo, uint32_t hi,
+                                       uint32_t (&o)[4])
 {
-    return (w & mask) | magic;
+    const uint32_t w8 = w >> 8;
+    const g16_h2 o1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f}, o64 = {(_Float16)-64.0f, (_Float16)-64.0f};
+    const g16_h2 q0 = __builtin_bit_cast(g16_h2, (w & 0x000F000Fu) | lo) + o1024;
+    const g16_h2 q1 = __builtin_bit_cast(g16_h2, (w & 0x00F000F0u) | hi) + o64;
+    const g16_h2 q2 = __builtin_bit_cast(g16_h2, (w8 & 0x000F000Fu) | lo) + o1024;
+    const g16_h2 q3 = __builtin_bit_cast(g16_h2, (w8 & 0x00F000F0u) | hi) + o64;
+    o[0] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q0, s2, b2));
+    o[1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q1, s2, b2));
+    o[2] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q2, s2, b2));
+    o[3] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(q3, s2, b2));
+}
+
+// bf16 (low or high half of a word) to an f16 pair holding it twice
+__device__ __forceinline__ g16_h2 g16_bf2h2(uint32_t v, int hi)
+{
+    const _Float16 h = (_Float16)__uint_as_float(hi ? (v & 0xFFFF0000u) : (v << 16));
+    return g16_h2{h, h};
 }
 
 struct Gmm16Args {
     float *y;
     long ldy;
     const _Float16 *ah;             // staged A [source rows, k]
-    const float *aF, *aX;           // [source rows, k / G]
+    const float *aF;                // [source rows]: the stage's per-row scale
     const int32_t *perm, *tiles;    // grouped: pair permutation and tile list
     const uint32_t *w0, *w1;        // weight banks (w1: the up rows with SWIGLU)
     const uint16_t *s0, *b0, *s1, *b1;
@@ -131,35 +126,39 @@ struct Gmm16Args {
     int nbw;                        // column blocks a workgroup runs back to back
 };
 
-#ifndef G16_OCC
-#define G16_OCC 2
-#endif
 template <int G, bool SWIGLU, bool DENSE, int KC>
-__global__ __launch_bounds__(G16_THREADS, G16_OCC) void k_gmm16(Gmm16Args a)
+__global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16(Gmm16Args a)
 {
-    constexpr int GPC = KC / G;              // groups per chunk
-    constexpr int SPG = G / 32;              // MFMA steps per group (= words a lane holds per group)
-    constexpr int WPC = KC / 32;             // words a lane holds per chunk, per weight tile
-    constexpr int AST = KC + 8;              // halfs per A row in LDS (pad: conflict-free fragment reads)
+    constexpr int WPL = KC / 32;                         // words (MFMA k steps) per lane per chunk
+    constexpr int KPL = WPL * 8;                         // k a lane covers per chunk
+    constexpr int NGL = KPL > G ? KPL / G : 1;           // quantisation groups in that span
+    constexpr int AST = KC + 8;                          // halfs per A row in LDS (pad: conflict-free reads)
     constexpr int AU4 = G16_BM * KC / 8 / G16_THREADS;   // uint4 of A a thread moves per chunk
-    static_assert(G <= KC && KC % G == 0 && AU4 >= 1, "chunk shape");
+    static_assert(NGL <= 2 && AU4 >= 1 && (WPL == 2 || WPL == 4 || WPL == 8), "chunk shape");
+    static_assert(G16_BM * (KC + 8) < 65536, "LDS offsets of A fit 16 bits");
     __shared__ __align__(16) _Float16 As[2][G16_BM][AST];
-    __shared__ float Xs[2][G16_BM][GPC];
     __shared__ float Fr[G16_BM];
     __shared__ int srow[G16_BM], drow[G16_BM];
 
-    // Workgroup b: XCD b % 8; tile (r / ng) * 8 + b % 8 and column blocks
-    // [nb0, nb0 + nitems) with r = b / 8, run as one stream of chunks.
+    // Workgroup b runs on XCD b % 8 (round-robin dispatch).  Each XCD takes a
+    // contiguous range of tiles, and with r = b / 8 its workgroups walk
+    // (tile, column group) with the column group fastest.  Workgroups that
+    // run together on one XCD then share each activation chunk, and the
+    // tiles of one expert (adjacent in the list) share its weights, in that
+    // XCD's L2.  A workgroup runs column blocks [nb0, nb0 + nitems) as one
+    // stream of chunks.
     const int bid = blockIdx.x, xcd = bid & 7, r = bid >> 3, ngr = (a.nblk + a.nbw - 1) / a.nbw;
-    const int tile = (r / ngr) * 8 + xcd, nb0 = (r % ngr) * a.nbw, nitems = min(a.nbw, a.nblk - nb0);
+    const int ntl = DENSE ? (a.rows + G16_BM - 1) / G16_BM : a.tiles[0];
+    const int tpx = (ntl + 7) / 8, tl = r / ngr;
+    if (tl >= tpx) return;
+    const int tile = xcd * tpx + tl, nb0 = (r % ngr) * a.nbw, nitems = min(a.nbw, a.nblk - nb0);
+    if (tile >= ntl) return;
     int expert, first, len;
     if (DENSE) {
         first = tile * G16_BM;
-        if (first >= a.rows) return;
         expert = 0;
         len = min(G16_BM, a.rows - first);
     } else {
-        if (tile >= a.tiles[0]) return;
         expert = a.tiles[1 + 3 * tile];
         first = a.tiles[2 + 3 * tile];
         len = a.tiles[3 + 3 * tile];
@@ -182,193 +181,138 @@ __global__ __launch_bounds__(G16_THREADS, G16_OCC) void k_gmm16(Gmm16Args a)
     // Loads are buffer loads: a wave-uniform base (a descriptor in SGPRs) and a
     // 32-bit per-lane offset in place of a 64-bit address.
     //
-    // Activations: thread t moves AU4 consecutive uint4 of A row t / TPR and
-    // (t < 32 GPC) the group sum of row t / GPC.  Loads go to valid (clamped)
+    // Activations: a chunk is G16_BM rows of KC halfs, LPR 128-byte lines a
+    // row.  Load i of thread t takes 16 bytes (t % 8) of line
+    // i * (threads / 8) + t / 8, so each load instruction of a wave covers 8
+    // whole lines (a cache tag per 128 bytes).  Loads go to valid (clamped)
     // addresses; rows outside the tile are zeroed by selects.
-    constexpr int TPR = KC / 8 / AU4;        // threads per A row
-    const int am = t / TPR, aseg = (t % TPR) * AU4 * 8;   // row, first half
-    const bool aok = srow[am] >= 0;
-    const __amdgpu_buffer_rsrc_t rA = qw_rsrc(a.ah), rX = qw_rsrc(a.aX);
-    const uint32_t offA = (uint32_t)(((aok ? srow[am] : 0) * k + aseg) * 2);
-    const int xm = t / GPC, xgi = t % GPC;
-    const bool xw = t < G16_BM * GPC;
-    const int xsrc = xw ? srow[xm] : -1;
-    const uint32_t offX = (uint32_t)(((xsrc >= 0 ? xsrc : 0) * groups + xgi) * 4);
+    constexpr int LPR = KC * 2 / 128;
+    const __amdgpu_buffer_rsrc_t rA = qw_rsrc(a.ah);
+    uint32_t offA[AU4];
+    uint16_t ldsA[AU4];
+    uint32_t aokm = 0;
+#pragma unroll
+    for (int i = 0; i < AU4; i++) {
+        const int L = i * (G16_THREADS / 8) + (t >> 3), row = L / LPR, seg = L % LPR;
+        const int sr = srow[row];
+        if (sr >= 0) aokm |= 1u << i;
+        offA[i] = (uint32_t)(((sr >= 0 ? sr : 0) * k + seg * 64 + (t & 7) * 8) * 2);
+        ldsA[i] = (uint16_t)(row * AST + seg * 64 + (t & 7) * 8);
+    }
     g16_u4 ra[AU4];
-    float rx;
     // every fetch is issued, at a chunk clamped to the last: the same loads in
     // every pass, so the waits before each use count exactly
     auto fetch_a = [&](int step) {
         const int c = min(step, T - 1) % nch;
 #pragma unroll
         for (int i = 0; i < AU4; i++)
-            ra[i] = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rA, offA + c * KC * 2 + 16 * i, 0, 0));
-        rx = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rX, offX + c * GPC * 4, 0, 0));
+            ra[i] = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rA, offA[i] + c * KC * 2, 0, 0));
     };
     auto stash_a = [&](int q) {
         const g16_u4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int i = 0; i < AU4; i++) *reinterpret_cast<g16_u4 *>(&As[q][am][aseg + 8 * i]) = aok ? ra[i] : z;
-        if (xw) Xs[q][xm][xgi] = xsrc >= 0 ? rx : 0.0f;
+        for (int i = 0; i < AU4; i++)
+            *reinterpret_cast<g16_u4 *>(&As[q][0][0] + ldsA[i]) = (aokm >> i) & 1 ? ra[i] : z;
     };
 
     // Weights: lane (ln, kg) of wave w owns weight row col(item, nt) of tile
-    // nt; per chunk, SPG words of each of the GPC groups, and the groups'
-    // scales and biases (GPC consecutive bf16 each).
+    // nt (4 tiles of 16 rows); per chunk, the KPL consecutive k from
+    // kg KPL: WPL consecutive words, and the scales and biases of the NGL
+    // groups they fall in.  MFMA step s takes word s of every lane, so the A
+    // fragment of lane group kg is k = c KC + kg KPL + 8 s .. + 7.
     __amdgpu_buffer_rsrc_t rW[2], rS[2], rB[2];
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
-        const bool up = SWIGLU && nt == 1;
-        rW[nt] = qw_rsrc((up ? a.w1 : a.w0) + (size_t)expert * a.ew);
-        rS[nt] = qw_rsrc((up ? a.s1 : a.s0) + (size_t)expert * a.eg);
-        rB[nt] = qw_rsrc((up ? a.b1 : a.b0) + (size_t)expert * a.eg);
+    for (int h = 0; h < 2; h++) {
+        const bool up = SWIGLU && h == 1;
+        rW[h] = qw_rsrc((up ? a.w1 : a.w0) + (size_t)expert * a.ew);
+        rS[h] = qw_rsrc((up ? a.s1 : a.s0) + (size_t)expert * a.eg);
+        rB[h] = qw_rsrc((up ? a.b1 : a.b0) + (size_t)expert * a.eg);
     }
+    // SWIGLU: tiles 0, 1 are gate features, 2, 3 the same features of up
     auto colof = [&](int item, int nt) {
         const int nb = nb0 + item;
-        return SWIGLU ? nb * 64 + wave * 16 + ln : nb * G16_BN + wave * 32 + nt * 16 + ln;
+        return SWIGLU ? nb * (G16_BN / 2) + wave * 32 + (nt & 1) * 16 + ln : nb * G16_BN + wave * 64 + nt * 16 + ln;
     };
-    // wq holds, group by group, the words of the chunk being computed; as
-    // soon as group gg is consumed its registers take the next step's group
-    // gg (an in-place ring: the loads get the rest of the chunk to land).
-    uint32_t wq[2][WPC];
-    uint32_t sq[2][(GPC + 1) / 2], bq[2][(GPC + 1) / 2];   // bf16 pairs
-    auto fetch_group = [&](int step, int gg) {
+    auto fetch_b = [&](int step, uint32_t (&wq)[4][WPL], uint32_t (&sq)[4], uint32_t (&bq)[4]) {
         step = min(step, T - 1);
         const int item = step / nch, c = step % nch;
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
+        for (int nt = 0; nt < 4; nt++) {
+            const int h = SWIGLU ? nt >> 1 : 0;
             const int col = colof(item, nt), cc = col < a.n ? col : 0;
-            const uint32_t o = (uint32_t)((cc * words + kg * SPG + c * (KC / 8) + gg * (G / 8)) * 4);
-            if (SPG == 1) wq[nt][gg] = __builtin_amdgcn_raw_buffer_load_b32(rW[nt], o, 0, 0);
-            if (SPG == 2) {
-                const g16_u2 v = __builtin_bit_cast(g16_u2, __builtin_amdgcn_raw_buffer_load_b64(rW[nt], o, 0, 0));
-                wq[nt][2 * gg] = v.x; wq[nt][2 * gg + 1] = v.y;
-            }
-            if (SPG == 4) {
-                const g16_u4 v = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rW[nt], o, 0, 0));
-                wq[nt][4 * gg] = v.x; wq[nt][4 * gg + 1] = v.y; wq[nt][4 * gg + 2] = v.z; wq[nt][4 * gg + 3] = v.w;
-            }
-        }
-    };
-    // the chunk's GPC scales and biases of each weight tile, as bf16 pairs
-    auto fetch_sb = [&](int step) {
-        step = min(step, T - 1);
-        const int item = step / nch, c = step % nch;
+            const uint32_t o = (uint32_t)((cc * words + c * (KC / 8) + kg * WPL) * 4);
+            if (WPL == 2) {
+                const g16_u2 v = __builtin_bit_cast(g16_u2, __builtin_amdgcn_raw_buffer_load_b64(rW[h], o, 0, 0));
+                wq[nt][0] = v.x; wq[nt][1] = v.y;
+            } else {
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) {
-            const int col = colof(item, nt), cc = col < a.n ? col : 0;
-            const uint32_t o = (uint32_t)((cc * groups + c * GPC) * 2);
-            if (GPC == 1) {
-                sq[nt][0] = __builtin_amdgcn_raw_buffer_load_b16(rS[nt], o, 0, 0);
-                bq[nt][0] = __builtin_amdgcn_raw_buffer_load_b16(rB[nt], o, 0, 0);
+                for (int j = 0; j < WPL / 4; j++) {
+                    const g16_u4 v = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rW[h], o + 16 * j, 0, 0));
+                    wq[nt][4 * j] = v.x; wq[nt][4 * j + 1] = v.y; wq[nt][4 * j + 2] = v.z; wq[nt][4 * j + 3] = v.w;
+                }
             }
-            if (GPC == 2) {
-                sq[nt][0] = __builtin_amdgcn_raw_buffer_load_b32(rS[nt], o, 0, 0);
-                bq[nt][0] = __builtin_amdgcn_raw_buffer_load_b32(rB[nt], o, 0, 0);
-            }
-            if (GPC == 4) {
-                const g16_u2 vs = __builtin_bit_cast(g16_u2, __builtin_amdgcn_raw_buffer_load_b64(rS[nt], o, 0, 0));
-                const g16_u2 vb = __builtin_bit_cast(g16_u2, __builtin_amdgcn_raw_buffer_load_b64(rB[nt], o, 0, 0));
-                sq[nt][0] = vs.x; sq[nt][1] = vs.y; bq[nt][0] = vb.x; bq[nt][1] = vb.y;
-            }
-            if (GPC == 8) {
-                const g16_u4 vs = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rS[nt], o, 0, 0));
-                const g16_u4 vb = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rB[nt], o, 0, 0));
-                sq[nt][0] = vs.x; sq[nt][1] = vs.y; sq[nt][2] = vs.z; sq[nt][3] = vs.w;
-                bq[nt][0] = vb.x; bq[nt][1] = vb.y; bq[nt][2] = vb.z; bq[nt][3] = vb.w;
+            const uint32_t og = (uint32_t)((cc * groups + (c * KC + kg * KPL) / G) * 2);
+            if (NGL == 1) {
+                sq[nt] = __builtin_amdgcn_raw_buffer_load_b16(rS[h], og, 0, 0);
+                bq[nt] = __builtin_amdgcn_raw_buffer_load_b16(rB[h], og, 0, 0);
+            } else {
+                sq[nt] = __builtin_amdgcn_raw_buffer_load_b32(rS[h], og, 0, 0);
+                bq[nt] = __builtin_amdgcn_raw_buffer_load_b32(rB[h], og, 0, 0);
             }
         }
     };
 
-    g16_f4 acc[2][2], C[2][2];
-    uint32_t magic = 0x64006400u, mask = 0x000F000Fu;
-    asm volatile("" : "+v"(magic), "+s"(mask));   // one in a VGPR, one in an SGPR
+    g16_f4 acc[4][4];
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int mt = 0; mt < 4; mt++)
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++) acc[mt][nt] = g16_f4{0.f, 0.f, 0.f, 0.f};
+        for (int nt = 0; nt < 4; nt++) acc[mt][nt] = g16_f4{0.f, 0.f, 0.f, 0.f};
+    uint32_t lo = 0x64006400u, hi = 0x54005400u;
+    asm volatile("" : "+v"(lo), "+v"(hi));
 
-    fetch_a(0);
-    stash_a(0);
-    fetch_a(1);
-#pragma unroll
-    for (int gg = 0; gg < GPC; gg++) fetch_group(0, gg);
-    fetch_sb(0);
-    __syncthreads();
-
-    for (int i = 0; i < T; i++) {
+    // One chunk: MFMAs from As[i & 1] and the weights in (wq, sq, bq), the
+    // next chunk's weights into (wn, sn, bn), the chunk after next's
+    // activations into registers once this one's are in LDS.
+    auto step = [&](int i, uint32_t (&wq)[4][WPL], uint32_t (&sq)[4], uint32_t (&bq)[4],
+                    uint32_t (&wn)[4][WPL], uint32_t (&sn)[4], uint32_t (&bn)[4]) {
         const int q = i & 1, item = i / nch, c = i % nch;
-        // this chunk's scales and biases (kept raw), then the next chunk's in flight
-        uint32_t sqc[2][(GPC + 1) / 2], bqc[2][(GPC + 1) / 2];
+        g16_h2 s2[4][NGL], b2[4][NGL];
 #pragma unroll
-        for (int nt = 0; nt < 2; nt++)
+        for (int nt = 0; nt < 4; nt++)
 #pragma unroll
-            for (int i = 0; i < (GPC + 1) / 2; i++) {
-                sqc[nt][i] = sq[nt][i];
-                bqc[nt][i] = bq[nt][i];
+            for (int g = 0; g < NGL; g++) {
+                s2[nt][g] = g16_bf2h2(sq[nt], g);
+                b2[nt][g] = g16_bf2h2(bq[nt], g);
             }
-        fetch_sb(i + 1);
-        // Group gg's MFMAs, then group gg - 1's affine epilogue: the epilogue
-        // reads partials whose MFMAs had the current group's to finish behind.
-        g16_f4 Cp[2][2];
+        // the next chunk's weights are issued here, ahead of this chunk's
+        // MFMAs (left to itself the scheduler sinks them below, which
+        // serialises memory and compute)
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_b(i + 1, wn, sn, bn);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int gg = 0; gg <= GPC; gg++) {
-            // keeps each group's LDS reads from being hoisted into earlier ones
-            __builtin_amdgcn_sched_barrier(0);
-            if (gg < GPC) {
+        for (int s = 0; s < WPL; s++) {
+            const int g = NGL == 1 ? 0 : s * 8 / G;
+            g16_h8 bf[4];
 #pragma unroll
-                for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                    for (int nt = 0; nt < 2; nt++) C[mt][nt] = g16_f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int s = 0; s < SPG; s++) {
-                    g16_h8 bf[2];
-#pragma unroll
-                    for (int nt = 0; nt < 2; nt++) {
-                        uint32_t wd = wq[nt][gg * SPG + s];
-                        asm volatile("" : "+v"(wd));      // dequantised here, not ahead of time
-                        const g16_u4 u = {g16_nib(wd, mask, magic), g16_nib(wd >> 4, mask, magic),
-                                          g16_nib(wd >> 8, mask, magic), g16_nib(wd >> 12, mask, magic)};
-                        bf[nt] = __builtin_bit_cast(g16_h8, u);
-                    }
-                    const int ah = gg * G + 8 * (kg * SPG + s);
-#pragma unroll
-                    for (int mt = 0; mt < 2; mt++) {
-                        const g16_h8 af = *reinterpret_cast<const g16_h8 *>(&As[q][mt * 16 + ln][ah]);
-#pragma unroll
-                        for (int nt = 0; nt < 2; nt++)
-                            C[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[nt], C[mt][nt], 0, 0, 0);
-                    }
-                }
-                fetch_group(i + 1, gg);
+            for (int nt = 0; nt < 4; nt++) {
+                uint32_t o[4];
+                g16_dq(wq[nt][s], s2[nt][g], b2[nt][g], lo, hi, o);
+                bf[nt] = __builtin_bit_cast(g16_h8, g16_u4{o[0], o[1], o[2], o[3]});
             }
-            if (gg > 0) {
-                const int pg = gg - 1;
+            const int ah = kg * KPL + 8 * s;
 #pragma unroll
-                for (int nt = 0; nt < 2; nt++) {
-                    const float sc = __uint_as_float((sqc[nt][pg / 2] >> (16 * (pg % 2))) << 16);
-                    const float bc =
-                        __builtin_fmaf(-1024.0f, sc, __uint_as_float((bqc[nt][pg / 2] >> (16 * (pg % 2))) << 16));
+            for (int mt = 0; mt < 4; mt++) {
+                const g16_h8 af = *reinterpret_cast<const g16_h8 *>(&As[q][mt * 16 + ln][ah]);
 #pragma unroll
-                    for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            const float xg = Xs[q][mt * 16 + 4 * kg + e][pg];
-                            acc[mt][nt][e] = __builtin_fmaf(sc, Cp[mt][nt][e], __builtin_fmaf(bc, xg, acc[mt][nt][e]));
-                        }
-                }
-            }
-            if (gg < GPC) {
-#pragma unroll
-                for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-                    for (int nt = 0; nt < 2; nt++) Cp[mt][nt] = C[mt][nt];
+                for (int nt = 0; nt < 4; nt++)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[nt], acc[mt][nt], 0, 0, 0);
             }
         }
         if (c == nch - 1) {
-            // the item is done: out, y = F (acc), with SWIGLU silu(F g) * (F u)
+            // the item is done: out, y = F acc, with SWIGLU silu(F g) * (F u)
 #pragma unroll
-            for (int mt = 0; mt < 2; mt++)
+            for (int mt = 0; mt < 4; mt++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int m = mt * 16 + 4 * kg + e;
@@ -377,41 +321,53 @@ __global__ __launch_bounds__(G16_THREADS, G16_OCC) void k_gmm16(Gmm16Args a)
                         const float f = Fr[m];
                         float *yr = a.y + (size_t)dr * a.ldy;
                         if (SWIGLU) {
-                            const int col = colof(item, 0);
-                            if (col < a.n) yr[col] = qw_silu(f * acc[mt][0][e]) * (f * acc[mt][1][e]);
-                        } else {
 #pragma unroll
                             for (int nt = 0; nt < 2; nt++) {
+                                const int col = colof(item, nt);
+                                if (col < a.n) yr[col] = qw_silu(f * acc[mt][nt][e]) * (f * acc[mt][nt + 2][e]);
+                            }
+                        } else {
+#pragma unroll
+                            for (int nt = 0; nt < 4; nt++) {
                                 const int col = colof(item, nt);
                                 if (col < a.n) yr[col] = f * acc[mt][nt][e];
                             }
                         }
                     }
 #pragma unroll
-                    for (int nt = 0; nt < 2; nt++) acc[mt][nt][e] = 0.0f;
+                    for (int nt = 0; nt < 4; nt++) acc[mt][nt][e] = 0.0f;
                 }
         }
         stash_a(q ^ 1);
         fetch_a(i + 2);
         __syncthreads();
+    };
+
+    uint32_t wqa[4][WPL], sqa[4], bqa[4], wqb[4][WPL], sqb[4], bqb[4];
+    // the same issue order as a step's (weights, then activations two ahead),
+    // so the loop head waits for the same loads from either side
+    fetch_a(0);
+    fetch_b(0, wqa, sqa, bqa);
+    stash_a(0);
+    fetch_a(1);
+    __syncthreads();
+    int i = 0;
+    for (; i + 1 < T; i += 2) {
+        step(i, wqa, sqa, bqa, wqb, sqb, bqb);
+        step(i + 1, wqb, sqb, bqb, wqa, sqa, bqa);
     }
+    if (i < T) step(i, wqa, sqa, bqa, wqb, sqb, bqb);
 }
 
 // ---- host side ---------------------------------------------------------------------
 
-extern "C" int qwk_stage16(hipStream_t s, uint16_t *hb, float *F, float *X, const float *x, int rows, int k,
-                           int group)
+extern "C" int qwk_stage16(hipStream_t s, uint16_t *hb, float *F, const float *x, int rows, int k)
 {
     _Float16 *h = reinterpret_cast<_Float16 *>(hb);
-    if (rows < 1 || k < group || k % group || ((uintptr_t)x & 15u) || ((uintptr_t)h & 15u))
+    if (rows < 1 || k < 8 || k % 8 || ((uintptr_t)x & 15u) || ((uintptr_t)h & 15u))
         return (int)hipErrorInvalidValue;
     const dim3 grid((unsigned)((rows + G16_THREADS / 64 - 1) / (G16_THREADS / 64))), blk(G16_THREADS);
-    switch (group) {
-    case 32: hipLaunchKernelGGL(k_stage16<32>, grid, blk, 0, s, h, F, X, x, rows, k); break;
-    case 64: hipLaunchKernelGGL(k_stage16<64>, grid, blk, 0, s, h, F, X, x, rows, k); break;
-    case 128: hipLaunchKernelGGL(k_stage16<128>, grid, blk, 0, s, h, F, X, x, rows, k); break;
-    default: return (int)hipErrorInvalidValue;
-    }
+    hipLaunchKernelGGL(k_stage16, grid, blk, 0, s, h, F, x, rows, k);
     return (int)hipGetLastError();
 }
 
@@ -426,49 +382,51 @@ static void g16_launch(hipStream_t s, const Gmm16Args &a, int swiglu, int dense,
 }
 
 extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb, const float *aF,
-                         const float *aX, const int32_t *perm, const int32_t *tiles, int max_tiles,
+                         const int32_t *perm, const int32_t *tiles, int max_tiles,
                          qwk_q4 m0, qwk_q4 m1, long ew, long eg, int k, int n, int K, int x_by_pair,
                          int group, int swiglu, int dense_rows)
 {
-    // chunks of G16_KC where k allows, else 64 (groups up to 64)
-#ifndef G16_KC
-#define G16_KC 256
-#endif
-    const int kc = k % G16_KC == 0 ? G16_KC : 64;
-    if (k < 64 || k % kc || n < 1 || (group != 32 && group != 64 && group != 128) || group > kc ||
+    // chunks of 256 where k allows, else 64
+    const int kc = k % 256 == 0 ? 256 : 64;
+    if (k < 64 || k % kc || n < 1 || (group != 32 && group != 64 && group != 128) || k % group ||
         ((uintptr_t)ahb & 15u) || ((uintptr_t)m0.w & 15u) || (swiglu && ((uintptr_t)m1.w & 15u)))
         return (int)hipErrorInvalidValue;
     const _Float16 *ah = reinterpret_cast<const _Float16 *>(ahb);
     const bool dense = dense_rows > 0;
     if (!dense && (!perm || !tiles || K < 1)) return (int)hipErrorInvalidValue;
     Gmm16Args a;
-    a.y = y; a.ldy = ldy; a.ah = ah; a.aF = aF; a.aX = aX; a.perm = perm; a.tiles = tiles;
+    a.y = y; a.ldy = ldy; a.ah = ah; a.aF = aF; a.perm = perm; a.tiles = tiles;
     a.w0 = m0.w; a.s0 = m0.s; a.b0 = m0.b;
     a.w1 = swiglu ? m1.w : m0.w; a.s1 = swiglu ? m1.s : m0.s; a.b1 = swiglu ? m1.b : m0.b;
     a.ew = ew; a.eg = eg; a.k = k; a.n = n; a.K = K; a.x_by_pair = x_by_pair; a.rows = dense_rows;
-    a.nblk = swiglu ? (n + 63) / 64 : (n + G16_BN - 1) / G16_BN;
+    a.nblk = swiglu ? (n + G16_BN / 2 - 1) / (G16_BN / 2) : (n + G16_BN - 1) / G16_BN;
     const int ntiles = dense ? (dense_rows + G16_BM - 1) / G16_BM : max_tiles;
     if (ntiles <= 0) return 0;
     // column blocks per workgroup: long streams, but enough workgroups to
     // fill the chip (max_tiles bounds the grouped tile count from above)
     {
-        const long per = (long)ntiles * a.nblk / 1024;
+#ifndef G16_NBW
+        const long per = (long)ntiles * a.nblk / 2048;
         a.nbw = per < 1 ? 1 : per > 8 ? 8 : (int)per;
+#else
+        a.nbw = G16_NBW;
+#endif
         if (a.nbw > a.nblk) a.nbw = a.nblk;
     }
-    // tile = (r / ngr) * 8 + b % 8 with r = b / 8: a multiple of 8 tiles
+    // r = b / 8 < ngr * ceil(ntiles / 8) covers every XCD's tile range
     const int ngr = (a.nblk + a.nbw - 1) / a.nbw;
     const unsigned grid = (unsigned)(ngr * ((ntiles + 7) / 8) * 8);
-    if (kc == G16_KC) {
+    if (kc == 256) {
         switch (group) {
-        case 32: g16_launch<32, G16_KC>(s, a, swiglu, dense, grid); break;
-        case 64: g16_launch<64, G16_KC>(s, a, swiglu, dense, grid); break;
-        default: g16_launch<128, G16_KC>(s, a, swiglu, dense, grid); break;
+        case 32: g16_launch<32, 256>(s, a, swiglu, dense, grid); break;
+        case 64: g16_launch<64, 256>(s, a, swiglu, dense, grid); break;
+        default: g16_launch<128, 256>(s, a, swiglu, dense, grid); break;
         }
     } else {
         switch (group) {
         case 32: g16_launch<32, 64>(s, a, swiglu, dense, grid); break;
-        default: g16_launch<64, 64>(s, a, swiglu, dense, grid); break;
+        case 64: g16_launch<64, 64>(s, a, swiglu, dense, grid); break;
+        default: g16_launch<128, 64>(s, a, swiglu, dense, grid); break;
         }
     }
     return (int)hipGetLastError();

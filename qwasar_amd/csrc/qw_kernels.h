@@ -58,19 +58,18 @@ int qwk_gather_gemm(hipStream_t s, float *y, const float *x, const int32_t *perm
 int qwk_qmm(hipStream_t s, float *y, const float *x, qwk_q4 m, int k, int n, int rows, int group);
 
 /* Prefill products on MFMA over f16-staged activations (qw_gmm16.hip).
- * Staging: per (row, group of `group`), h = f16(x 2^sh) with the group's
- * largest magnitude in [2^14, 2^15), F = 2^-sh, X = F * sum(h); h in
- * 8-blocks ordered 0,4,1,5,2,6,3,7.  h [rows, k] f16 (bits), F/X [rows, k/group]. */
-int qwk_stage16(hipStream_t s, uint16_t *h, float *F, float *X, const float *x, int rows, int k,
-                int group);
-/* y[row, :] = W_e . A(row) in fp32 with the affine map applied per group.
- * Grouped (dense_rows == 0): tiles from qwk_moe_group cut at 32 rows; tile
+ * Staging: per row, h = f16(x 2^sh) with the row's largest magnitude in
+ * [2^14, 2^15) and F = 2^-sh; h in 8-blocks ordered 0,4,1,5,2,6,3,7.
+ * h [rows, k] f16 (bits), F [rows].  k % 8 == 0. */
+int qwk_stage16(hipStream_t s, uint16_t *h, float *F, const float *x, int rows, int k);
+/* y[row, :] = W_e . A(row) in fp32, weights dequantised to f16 (one rounding).
+ * Grouped (dense_rows == 0): tiles from qwk_moe_group cut at 64 rows; tile
  * row j is pair p = perm[start + j], its A row is (x_by_pair ? p : p / K),
  * its output row p.  Dense (dense_rows > 0): rows 0..dense_rows-1, expert 0.
  * m0 (and with swiglu m1, the up rows) point at expert 0 of the bank; ew/eg
  * are the per-expert strides in words / groups.  With swiglu, n = features
- * and y = silu(W0 A) * (W1 A).  k % 64 == 0 (k % 256 == 0 for group 128). */
-int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ah, const float *aF, const float *aX,
+ * and y = silu(W0 A) * (W1 A).  k % 64 == 0 and k % group == 0. */
+int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ah, const float *aF,
               const int32_t *perm, const int32_t *tiles, int max_tiles, qwk_q4 m0, qwk_q4 m1, long ew,
               long eg, int k, int n, int K, int x_by_pair, int group, int swiglu, int dense_rows);
 

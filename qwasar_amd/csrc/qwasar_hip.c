@@ -600,7 +600,7 @@ static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 /* Prefill: the grouped path on the one stream.  Activations are staged as
  * f16 once (x, then the SwiGLU output, then the shared expert's); the
  * routed and shared products run on MFMA with SwiGLU fused into gate / up. */
-#define QW_PF_BM 32    /* tile height of the prefill product (qw_gmm16.hip) */
+#define QW_PF_BM 64    /* tile height of the prefill product (qw_gmm16.hip) */
 static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const float *x,
                         const qw_moe_layer *M, int32_t rows) {
     const int32_t H = M->H, E = M->E, K = M->K, I = M->I, SI = M->SI, pairs = rows * K;
@@ -608,52 +608,48 @@ static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const floa
     const int32_t grp = M->split ? M->gate.group : M->gate_up.group;
     size_t off = 0;
     const size_t o_xh = off;     off += al256((size_t)rows * H * 2);
-    const size_t o_xF = off;     off += al256((size_t)rows * (H / grp) * 4);
-    const size_t o_xX = off;     off += al256((size_t)rows * (H / grp) * 4);
+    const size_t o_xF = off;     off += al256((size_t)rows * 4);
     const size_t o_logits = off; off += al256((size_t)rows * E * 4);
     const size_t o_perm = off;   off += al256((size_t)pairs * 4);
     const size_t o_tiles = off;  off += al256((size_t)(1 + 3 * mt) * 4);
     const size_t o_act = off;    off += al256((size_t)pairs * I * 4);
     const size_t o_ah = off;     off += al256((size_t)pairs * I * 2);
-    const size_t o_aF = off;     off += al256((size_t)pairs * (I / grp) * 4);
-    const size_t o_aX = off;     off += al256((size_t)pairs * (I / grp) * 4);
+    const size_t o_aF = off;     off += al256((size_t)pairs * 4);
     const size_t o_ey = off;     off += al256((size_t)pairs * H * 4);
     const size_t o_sa = off;     off += al256((size_t)rows * SI * 4);
     const size_t o_sh16 = off;   off += al256((size_t)rows * SI * 2);
-    const size_t o_sF = off;     off += al256((size_t)rows * (SI / grp) * 4);
-    const size_t o_sX = off;     off += al256((size_t)rows * (SI / grp) * 4);
+    const size_t o_sF = off;     off += al256((size_t)rows * 4);
     const size_t o_sh = off;     off += al256((size_t)rows * H * 4);
     const size_t o_g1 = off;     off += al256((size_t)rows * 4);
     char *S = scratch(off);
     if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", off); return false; }
     uint16_t *xh = (uint16_t *)(S + o_xh), *ah = (uint16_t *)(S + o_ah), *sh16 = (uint16_t *)(S + o_sh16);
-    float *xF = (float *)(S + o_xF), *xX = (float *)(S + o_xX), *aF = (float *)(S + o_aF);
-    float *aX = (float *)(S + o_aX), *sF = (float *)(S + o_sF), *sX = (float *)(S + o_sX);
+    float *xF = (float *)(S + o_xF), *aF = (float *)(S + o_aF), *sF = (float *)(S + o_sF);
     float *logits = (float *)(S + o_logits), *act = (float *)(S + o_act), *ey = (float *)(S + o_ey);
     float *sa = (float *)(S + o_sa), *sh = (float *)(S + o_sh), *g1 = (float *)(S + o_g1);
     int32_t *perm = (int32_t *)(S + o_perm), *tiles = (int32_t *)(S + o_tiles);
     hipStream_t s = G.stream;
     const long words = H / 8, groups = H / grp;
-    int rc = qwk_stage16(s, xh, xF, xX, x, rows, H, grp);
+    int rc = qwk_stage16(s, xh, xF, x, rows, H);
     if (!rc) rc = qwk_dmat_bf16(s, logits, x, dp(M->router), H, E, rows);
     if (!rc) rc = qwk_route(s, idx, w, logits, rows, E, K, M->norm ? 1 : 0);
     if (!rc) rc = qwk_moe_group(s, perm, tiles, idx, pairs, E, QW_PF_BM, mt);
     if (M->split) {
-        if (!rc) rc = qwk_gmm16(s, act, I, xh, xF, xX, perm, tiles, mt, q4r(&M->gate), q4r(&M->up),
+        if (!rc) rc = qwk_gmm16(s, act, I, xh, xF, perm, tiles, mt, q4r(&M->gate), q4r(&M->up),
                                 (long)I * words, (long)I * groups, H, I, K, 0, grp, 1, 0);
     } else {
         const qwk_q4 g0 = q4r(&M->gate_up);
         const qwk_q4 u0 = { g0.w + (size_t)I * words, g0.s + (size_t)I * groups, g0.b + (size_t)I * groups };
-        if (!rc) rc = qwk_gmm16(s, act, I, xh, xF, xX, perm, tiles, mt, g0, u0,
+        if (!rc) rc = qwk_gmm16(s, act, I, xh, xF, perm, tiles, mt, g0, u0,
                                 2L * I * words, 2L * I * groups, H, I, K, 0, grp, 1, 0);
     }
-    if (!rc) rc = qwk_stage16(s, ah, aF, aX, act, pairs, I, grp);
-    if (!rc) rc = qwk_gmm16(s, ey, H, ah, aF, aX, perm, tiles, mt, q4r(&M->down), q4r(&M->down),
+    if (!rc) rc = qwk_stage16(s, ah, aF, act, pairs, I);
+    if (!rc) rc = qwk_gmm16(s, ey, H, ah, aF, perm, tiles, mt, q4r(&M->down), q4r(&M->down),
                             (long)H * (I / 8), (long)H * (I / grp), I, H, K, 1, grp, 0, 0);
-    if (!rc) rc = qwk_gmm16(s, sa, SI, xh, xF, xX, NULL, NULL, 0, q4r(&M->sh_gate), q4r(&M->sh_up),
+    if (!rc) rc = qwk_gmm16(s, sa, SI, xh, xF, NULL, NULL, 0, q4r(&M->sh_gate), q4r(&M->sh_up),
                             0, 0, H, SI, 1, 0, grp, 1, rows);
-    if (!rc) rc = qwk_stage16(s, sh16, sF, sX, sa, rows, SI, grp);
-    if (!rc) rc = qwk_gmm16(s, sh, H, sh16, sF, sX, NULL, NULL, 0, q4r(&M->sh_down), q4r(&M->sh_down),
+    if (!rc) rc = qwk_stage16(s, sh16, sF, sa, rows, SI);
+    if (!rc) rc = qwk_gmm16(s, sh, H, sh16, sF, NULL, NULL, 0, q4r(&M->sh_down), q4r(&M->sh_down),
                             0, 0, SI, H, 1, 0, grp, 0, rows);
     if (!rc) rc = qwk_dmat_bf16(s, g1, x, dp(M->sh_gate_w), H, 1, rows);
     if (!rc) rc = qwk_moe_combine(s, out, ey, w, sh, g1, rows, K, H);

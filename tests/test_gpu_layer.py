@@ -50,6 +50,7 @@ def check(got, want, tol_rel, tol_abs=2e-2):
     assert np.array_equal(w.view(np.uint32), ww.view(np.uint32)), "routing weights not bit-exact"
     e = rel_l2(out, wout)
     m = np.abs(out - wout).max()
+    print(f"rel-L2 {e:.3g} max-abs {m:.3g}")
     assert e < tol_rel and m < tol_abs, f"rel-L2 {e:.3g} max-abs {m:.3g}"
     return e
 
