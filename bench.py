@@ -62,7 +62,7 @@ def decode_bytes(c):
 def measured_traffic(kernel):
     """HBM bytes per dispatch of `kernel` (fetch + write) from the committed
     rocprofv3 counter passes, or None when no summary covers it."""
-    path = os.path.join(ROOT, "profiles", "decode_config1_traffic.json")
+    path = os.path.join(ROOT, "profiles", "k_decode_fused_config1_traffic.json")
     try:
         with open(path) as f:
             return json.load(f)["bytes_per_dispatch"].get(kernel)
