@@ -11,9 +11,9 @@
 //            leave staged as q16 units
 //   down     per (token, block of output rows): route, load the down rows of
 //            the shared expert and of each of the token's K experts into
-//            registers, then wait for the activations and finish with the
-//            combine: sigmoid(g) * shared + sum_k w_k * y_k, an fma chain in
-//            slot order
+//            registers; each matrix's wave waits for that matrix's
+//            activations and computes; then the combine:
+//            sigmoid(g) * shared + sum_k w_k * y_k, an fma chain in slot order
 //
 // Hand-offs between roles go through device memory past the per-XCD L2: the
 // producer writes with device-coherent (sc1) stores, waits for them, and
@@ -58,18 +58,16 @@ extern "C" int qd_trace_read(unsigned long long *dst)
 #define QD_WAVES 16                 // every role: 16 waves
 #define QD_THREADS (QD_WAVES * 64)
 #define QD_GU_MAXRPB (QD_WAVES * 4)
-#define QD_LDS (48 * 1024)          // dynamic LDS: staged inputs, or router partials
+#define QD_LDS (64 * 1024)          // dynamic LDS: staged inputs, or the router's rows and partials
 #define QD_DOWN_LPR 16
 #define QD_DOWN_RIT 4               // down rows per lane slot
 #define QD_DOWN_RPG ((64 / QD_DOWN_LPR) * QD_DOWN_RIT)
-#define QD_DOWN_XA 3                // activation uint4 a thread: (K + 1) * 64 units * 3 <= 3 * QD_THREADS
 #define QD_SPIN_LIMIT (1 << 16)     // polls (each a memory round trip plus a sleep)
 
-static_assert((64 * 68 + 4 * 64) * 4 <= QD_LDS, "router: a padded token row and partials fit the dynamic LDS");
 static_assert(QWK_DECODE_MAX_K + 1 <= QD_WAVES, "down: one wave per matrix");
-// down: the K + 1 activation vectors (at most 64 units each) in LDS
+// down: the K + 1 activation vectors (at most 64 units each), one LDS region a wave
 static_assert((QWK_DECODE_MAX_K + 1) * 64 * QW_Q16_BYTES <= QD_LDS, "down activations fit the dynamic LDS");
-static_assert((QWK_DECODE_MAX_K + 1) * 64 * 3 <= QD_DOWN_XA * QD_THREADS, "down activations: one pass");
+
 
 // Lanes per row for a row of `units` q16 units, and units per lane.
 static __host__ __device__ constexpr int qd_lpr(int units) { return units >= 128 ? 64 : units >= 64 ? 32 : 16; }
@@ -203,8 +201,14 @@ struct QdArgs {
 // through LDS one at a time, chunk c of 64 inputs at c * QD_XPAD floats (the
 // pad makes the per-lane chunk reads conflict-free).
 
+#ifndef QD_RT_ROWS
 #define QD_RT_ROWS 4
+#endif
 #define QD_XPAD 68
+#define QD_WPAD 36                  // dwords a router-row chunk takes in LDS (32 + pad)
+// a padded token row (k <= 4096), every wave's partials, and the rows
+static_assert((64 * QD_XPAD + QD_WAVES * 64 + QD_RT_ROWS * 64 * QD_WPAD) * 4 <= QD_LDS,
+              "router: a padded token row, partials and the rows fit the dynamic LDS");
 
 // Order-R dot of one bf16 row with one token row xl (LDS, padded chunks):
 // lane l computes the fmaf chain of chunk l (k <= 64 * 64); the chunk
@@ -255,7 +259,7 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int H = a.m.H, E = a.m.E, nch = H / 64;
     const int o = b * QD_RT_ROWS + wave;
-    float *xl = lds, *part = lds + nch * QD_XPAD + wave * 64;
+    float *xl = lds, *pbase = lds + nch * QD_XPAD, *part = pbase + wave * 64;
     // the token rows, staged as q16 units for the gate / up roles
     const int units = H / 16;
     for (int i = b * QD_THREADS + threadIdx.x; i < a.rows * units; i += a.n_rt * QD_THREADS) {
@@ -273,13 +277,37 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
         qd_st4(a.qx + (size_t)i * 3 + 2, u[2]);
     }
     QD_TS(1);
-    // this wave's row in registers: lane c holds chunk c
+    // this wave's row in registers, lane c holding chunk c (64 inputs, 8
+    // uint4).  Loaded contiguously (each load instruction covers 8 whole
+    // cache lines, where lane-per-chunk loads would touch 64 lines for 16
+    // bytes each), then passed through the wave's own LDS region, chunk c at
+    // c * QD_WPAD dwords (conflict-free reads); a wave's LDS accesses run in
+    // order, so no barrier.
     const bool row = wave < QD_RT_ROWS && o <= E;
     const uint16_t *wr = o < E ? a.m.router + (size_t)o * H : a.m.sh_gate_w;
     uint4 w[8];
+    if (wave < QD_RT_ROWS) {
+        uint32_t *wl = reinterpret_cast<uint32_t *>(pbase + QD_WAVES * 64) + wave * 64 * QD_WPAD;
+        const int npc = H / 8;                      // uint4 pieces of the row
+        uint4 v[8];
 #pragma unroll
-    for (int q = 0; q < 8; q++)
-        w[q] = row && lane < nch ? reinterpret_cast<const uint4 *>(wr + lane * 64)[q] : make_uint4(0, 0, 0, 0);
+        for (int r = 0; r < 8; r++) {
+            const int i = min(lane + 64 * r, npc - 1);
+            v[r] = row ? reinterpret_cast<const uint4 *>(wr)[i] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            const int i = lane + 64 * r;
+            if (i < npc) *reinterpret_cast<uint4 *>(wl + (i / 8) * QD_WPAD + (i % 8) * 4) = v[r];
+        }
+        const int c = min(lane, nch - 1);
+#pragma unroll
+        for (int q = 0; q < 8; q++) w[q] = *reinterpret_cast<const uint4 *>(wl + c * QD_WPAD + 4 * q);
+#ifdef QD_TRACE
+        if (threadIdx.x == 0)
+            qd_trace[blockIdx.x * 8 + 3] = (w[7].w ^ w[0].x) == 0x12345678u ? 0 : wall_clock64();
+#endif
+    }
     for (int t = 0; t < a.rows; t++) {
         if (t) __syncthreads();
         for (int i = threadIdx.x; i < H / 4; i += blockDim.x) {
@@ -287,6 +315,7 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
             *reinterpret_cast<float4 *>(xl + (i / 16) * QD_XPAD + (i % 16) * 4) = v;
         }
         __syncthreads();
+        if (t == 0) QD_TS(4);
         if (row) qd_router_row(w, xl, nch, o < E ? a.logits + (size_t)t * E + o : a.g1 + t, part);
     }
     QD_TS(2);
@@ -337,30 +366,71 @@ __device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, i
     const int rl = wave * SL + slot, row = row0 + rl;
     // Every load is issued (at a clamped, valid address) before any is used;
     // out-of-range lanes are zeroed afterwards.
-    uint2 wv[2][NUL];
-    uint32_t sv[2][NUL], bv[2][NUL];
+    //
+    // With a whole wave on a row (LPR 64), lane lr takes units 4 lr .. 4 lr + 3
+    // (64 consecutive inputs: two 16-byte loads a matrix, and one scale and
+    // one bias load -- a b32 of two when G = 32); else lane lr takes units
+    // lr, lr + LPR, ... (NUL of them).
+    constexpr bool CG = LPR == 64;
+    constexpr int NW = CG ? 4 : NUL;               // units a lane
+    uint2 wv[2][NW];
+    uint32_t sb[2][CG ? 2 : NUL];                  // bf16 scale (low half) and bias (high half)
     const int rowc = min(row, n - 1);
+    if constexpr (CG) {
+        const int nl = units / 4, lc = min(lr, nl - 1);
+        const bool ok = row < n && lr < nl;
+        uint4 w4[2][2];
+        uint32_t sv[2], bv[2];
 #pragma unroll
-    for (int z = 0; z < 2; z++) {
-        const qwk_q4 q = z ? um : gm;
-#pragma unroll
-        for (int j = 0; j < NUL; j++) {
-            const int c = min(j * LPR + lr, units - 1);
-            wv[z][j] = *reinterpret_cast<const uint2 *>(q.w + (size_t)rowc * words + 2 * c);
-            const size_t gi = (size_t)rowc * groups + ((16 * c) >> lgG);
-            sv[z][j] = q.s[gi];
-            bv[z][j] = q.b[gi];
+        for (int z = 0; z < 2; z++) {
+            const qwk_q4 q = z ? um : gm;
+            const uint4 *src = reinterpret_cast<const uint4 *>(q.w + (size_t)rowc * words + 8 * lc);
+            w4[z][0] = src[0];
+            w4[z][1] = src[1];
+            const size_t gi = (size_t)rowc * groups + ((64 * lc) >> lgG);
+            if (lgG == 5) {
+                sv[z] = *reinterpret_cast<const uint32_t *>(q.s + gi);
+                bv[z] = *reinterpret_cast<const uint32_t *>(q.b + gi);
+            } else {
+                sv[z] = q.s[gi];
+                bv[z] = q.b[gi];
+            }
         }
+#pragma unroll
+        for (int z = 0; z < 2; z++) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                wv[z][2 * h] = ok ? make_uint2(w4[z][h].x, w4[z][h].y) : make_uint2(0, 0);
+                wv[z][2 * h + 1] = ok ? make_uint2(w4[z][h].z, w4[z][h].w) : make_uint2(0, 0);
+            }
+            // group of unit j: one for all four when G >= 64, j / 2 when G = 32
+            sb[z][0] = ok ? (sv[z] & 0xFFFFu) | (bv[z] << 16) : 0u;
+            sb[z][1] = ok ? (sv[z] >> 16) | (bv[z] & 0xFFFF0000u) : 0u;
+            if (lgG != 5) sb[z][1] = sb[z][0];
+        }
+    } else {
+        uint32_t sv[2][NUL], bv[2][NUL];
+#pragma unroll
+        for (int z = 0; z < 2; z++) {
+            const qwk_q4 q = z ? um : gm;
+#pragma unroll
+            for (int j = 0; j < NUL; j++) {
+                const int c = min(j * LPR + lr, units - 1);
+                wv[z][j] = *reinterpret_cast<const uint2 *>(q.w + (size_t)rowc * words + 2 * c);
+                const size_t gi = (size_t)rowc * groups + ((16 * c) >> lgG);
+                sv[z][j] = q.s[gi];
+                bv[z][j] = q.b[gi];
+            }
+        }
+#pragma unroll
+        for (int z = 0; z < 2; z++)
+#pragma unroll
+            for (int j = 0; j < NUL; j++) {
+                const bool ok = row < n && j * LPR + lr < units;
+                wv[z][j] = ok ? wv[z][j] : make_uint2(0, 0);
+                sb[z][j] = ok ? sv[z][j] | (bv[z][j] << 16) : 0u;
+            }
     }
-    uint32_t sb[2][NUL];          // bf16 scale (low half) and bias (high half)
-#pragma unroll
-    for (int z = 0; z < 2; z++)
-#pragma unroll
-        for (int j = 0; j < NUL; j++) {
-            const bool ok = row < n && j * LPR + lr < units;
-            wv[z][j] = ok ? wv[z][j] : make_uint2(0, 0);
-            sb[z][j] = ok ? sv[z][j] | (bv[z][j] << 16) : 0u;
-        }
     for (int t0 = 0; t0 < nt; t0 += a.tch) {
         const int tn = min(a.tch, nt - t0);
         if (!staged) {
@@ -386,16 +456,17 @@ __device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, i
             const uint4 *xt = xs + (size_t)t * units * 3;
             float acc[2] = {0.0f, 0.0f};
 #pragma unroll
-            for (int j = 0; j < NUL; j++) {
-                const int c = j * LPR + lr;
-                if (c < units) {
+            for (int j = 0; j < NW; j++) {
+                const int c = CG ? min(4 * lr + j, units - 1) : j * LPR + lr;
+                if (CG || c < units) {
                     const uint4 p0 = xt[3 * c], p1 = xt[3 * c + 1];
                     const uint4 rr = xt[3 * c + 2];
                     const float4 r = *reinterpret_cast<const float4 *>(&rr);
+                    const int si = CG ? j / 2 : j;
 #pragma unroll
                     for (int z = 0; z < 2; z++)
-                        acc[z] = qw_unit_dot(wv[z][j], p0, p1, r, __uint_as_float(sb[z][j] << 16),
-                                             __uint_as_float(sb[z][j] & 0xFFFF0000u), acc[z]);
+                        acc[z] = qw_unit_dot(wv[z][j], p0, p1, r, __uint_as_float(sb[z][si] << 16),
+                                             __uint_as_float(sb[z][si] & 0xFFFF0000u), acc[z]);
                 }
             }
 #ifdef QD_TRACE
@@ -571,12 +642,12 @@ __device__ __forceinline__ void qd_role_experts(const QdArgs &a, int bb, uint4 *
 //
 // A workgroup owns QD_DOWN_RPG output rows of one token; wave m holds those
 // rows of matrix m (0 = the shared expert, 1 + k = the token's k-th expert)
-// in registers from the moment routing is known, then waits for the
-// activations.  The per-matrix rows meet in LDS and the combine runs in slot
-// order.
+// in registers from the moment routing is known, then waits for its own
+// matrix's activation vector, loads it into registers and computes.  The
+// per-matrix rows meet in LDS and the combine runs in slot order.
 template <int NUL, int PL>
 __device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R, uint4 *xa,
-                                             float (*ys)[QD_DOWN_RPG])
+                                             float (*ys)[QD_DOWN_RPG], uint32_t *dready)
 {
     constexpr int LPR = QD_DOWN_LPR, RPP = 64 / LPR, RIT = QD_DOWN_RIT, RPG = QD_DOWN_RPG;
     const int H = a.m.H, I = a.m.I, SI = a.m.SI, K = a.m.K;
@@ -585,6 +656,7 @@ __device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R
     const int slot = lane / LPR, lr = lane % LPR;
     const int row0 = rb * RPG;
     const int lgG = a.lgG;
+    if (threadIdx.x == 0) *dready = 0u;     // seen by all after routing's barriers
     qd_wait_router(a);
     QD_TS(1);
     qd_route_all<PL>(a, R);
@@ -602,6 +674,12 @@ __device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R
         sm = a.m.down.s + e * H * groups;
         bm = a.m.down.b + e * H * groups;
     }
+#ifdef QD_DOWN_DELAY
+    {
+        const unsigned long long t0 = wall_clock64();
+        while (wall_clock64() - t0 < QD_DOWN_DELAY) __builtin_amdgcn_s_sleep(2);
+    }
+#endif
     // Every load is issued (at a clamped, valid address) before any is used;
     // out-of-range lanes are zeroed afterwards.
     uint2 wv[NUL][RIT];
@@ -627,41 +705,70 @@ __device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R
             wv[j][i] = ok ? wv[j][i] : make_uint2(0, 0);
             sb[j][i] = ok ? sv[j][i] | (bv[j][i] << 16) : 0u;
         }
-    // the activations: the shared expert's and this token's K experts', into
-    // LDS (vector m at xa + base(m)), device-coherently
-    if (threadIdx.x < 64) {
-        // lanes [0, gsh): the shared groups; then K * ngu lanes, the groups of
-        // each of the token's experts
-        const int lane = threadIdx.x, gsh = (a.n_sh + QD_GROUP - 1) / QD_GROUP;
-        int idx = QD_FL_SH + lane;
+    // One wave polls every flag this workgroup hangs on (lanes [0, gsh): the
+    // shared expert's groups; then ngu lanes for each of the token's experts)
+    // and publishes in LDS which matrices have their activations (bit m), or
+    // bit 31 if a wait gave up.  Wave m starts on its matrix as soon as its
+    // bit is set, so the matrices finish as their experts do, and only the
+    // last one's load and dot trail the last expert.  The poller is an idle
+    // wave when there is one (K + 1 < 16), else wave 0 before its own matrix.
+    const int pw = K + 1 < QD_WAVES ? QD_WAVES - 1 : 0;
+    if (m == pw) {
+        const int gsh = (a.n_sh + QD_GROUP - 1) / QD_GROUP, nfl = gsh + K * a.ngu;
+        int fidx = QD_FL_SH + lane;
         if (lane >= gsh) {
             const int q = lane - gsh, k = q / a.ngu;
-            idx = k < K ? QD_FL_EX + R.mark[R.picks[t * K + k]] * a.ngu + q % a.ngu : 0;
+            fidx = k < K ? QD_FL_EX + R.mark[R.picks[t * K + k]] * a.ngu + q % a.ngu : 0;
         }
-        qd_wait_flags(a.sync, lane < gsh + K * a.ngu, idx, a.epoch);
-    }
-    __syncthreads();
-    QD_TS(3);
-    const int ush = (SI / 16) * 3, uex = (I / 16) * 3, nxa = ush + K * uex;
-    {
-        // up to QD_DOWN_XA uint4 a thread, all issued before any is stored
-        uint4 v[QD_DOWN_XA];
-#pragma unroll
-        for (int r = 0; r < QD_DOWN_XA; r++) {
-            const int i = min((int)threadIdx.x + r * QD_THREADS, nxa - 1);
-            const uint4 *src = i < ush ? a.qsh + (size_t)t * ush + i : a.qact + (size_t)t * K * uex + (i - ush);
-            v[r] = qw_ld4_coh(a.scr, (uint32_t)(reinterpret_cast<const char *>(src) - a.scr));
+        const bool has = lane < nfl;
+        const uint32_t *f = &a.sync->flag[has ? fidx : 0];
+        const uint32_t all = (2u << K) - 1u;
+        for (int spins = 0;; spins++) {
+            uint32_t v = qd_poll_ld(f), e = qd_poll_ld(&a.sync->err);
+            asm volatile("s_waitcnt vmcnt(0)" : "+v"(v), "+v"(e)::"memory");
+            const unsigned long long on = __ballot(has && v == a.epoch);
+            const unsigned long long g0 = (1ull << gsh) - 1ull, gk = (1ull << a.ngu) - 1ull;
+            uint32_t mask = (on & g0) == g0 ? 1u : 0u;
+            for (int k = 0; k < K; k++)
+                if (((on >> (gsh + k * a.ngu)) & gk) == gk) mask |= 2u << k;
+            const bool done = mask == all;
+            const bool fail = !done && (spins >= QD_SPIN_LIMIT || __ballot(e != 0u) != 0ull);
+            if (fail) {
+                mask = 0x80000000u;
+                if (lane == 0) __hip_atomic_fetch_or(&a.sync->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            if (lane == 0) __hip_atomic_store(dready, mask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (done || fail) break;
+            __builtin_amdgcn_s_sleep(1);
         }
-#pragma unroll
-        for (int r = 0; r < QD_DOWN_XA; r++) asm volatile("" : "+v"(v[r].x), "+v"(v[r].y), "+v"(v[r].z), "+v"(v[r].w));
-#pragma unroll
-        for (int r = 0; r < QD_DOWN_XA; r++)
-            if (threadIdx.x + r * QD_THREADS < nxa) xa[threadIdx.x + r * QD_THREADS] = v[r];
     }
-    __syncthreads();
-    QD_TS(4);
     if (busy) {
-        const uint4 *xm = xa + (m == 0 ? 0 : ush + (m - 1) * uex);
+        uint32_t rd;
+        for (;;) {
+            rd = __hip_atomic_load(dready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (((rd >> m) & 1u) || (rd >> 31)) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (rd >> 31) goto gave_up;
+        // this matrix's vector, coalesced, into the wave's own LDS region (a
+        // wave's LDS accesses run in order: no barrier)
+        const int nv = units * 3;
+        const uint4 *xm = m == 0 ? a.qsh + (size_t)t * ((SI / 16) * 3)
+                                 : a.qact + ((size_t)t * K + (m - 1)) * ((I / 16) * 3);
+        uint4 *xw = xa + (m == 0 ? 0 : (SI / 16) * 3 + (m - 1) * ((I / 16) * 3));
+        const uint32_t xo = (uint32_t)(reinterpret_cast<const char *>(xm) - a.scr);
+        // a vector has units <= NUL * LPR, so 3 NUL LPR uint4: XW a lane
+        constexpr int XW = (3 * NUL * LPR + 63) / 64;
+        uint4 v[XW];
+#pragma unroll
+        for (int r = 0; r < XW; r++)
+            v[r] = qw_ld4_coh(a.scr, xo + (uint32_t)min(lane + 64 * r, nv - 1) * 16u);
+#pragma unroll
+        for (int r = 0; r < XW; r++) asm volatile("" : "+v"(v[r].x), "+v"(v[r].y), "+v"(v[r].z), "+v"(v[r].w));
+#pragma unroll
+        for (int r = 0; r < XW; r++)
+            if (lane + 64 * r < nv) xw[lane + 64 * r] = v[r];
+        QD_TS(4);
         float y[RIT];
 #pragma unroll
         for (int i = 0; i < RIT; i++) y[i] = 0.0f;
@@ -669,7 +776,7 @@ __device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R
         for (int j = 0; j < NUL; j++) {
             const int c = j * LPR + lr;
             if (c < units) {
-                const uint4 p0 = xm[3 * c], p1 = xm[3 * c + 1], rr = xm[3 * c + 2];
+                const uint4 p0 = xw[3 * c], p1 = xw[3 * c + 1], rr = xw[3 * c + 2];
                 const float4 r = *reinterpret_cast<const float4 *>(&rr);
 #pragma unroll
                 for (int i = 0; i < RIT; i++)
@@ -683,6 +790,7 @@ __device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R
             if (lr == 0) ys[m][slot + RPP * i] = v;
         }
     }
+gave_up:
     QD_TS(6);
     __syncthreads();
     QD_TS(7);
@@ -708,6 +816,7 @@ __global__ __launch_bounds__(QD_THREADS, 8) void k_decode_fused(QdArgs a)
     __shared__ QdRoute R;
     __shared__ int vin[QD_MAXT], vout[QD_MAXT];
     __shared__ float ys[QD_MAXT][QD_GU_MAXRPB];
+    __shared__ uint32_t dready;
     static_assert(QD_MAXT * QD_GU_MAXRPB >= (QWK_DECODE_MAX_K + 1) * QD_DOWN_RPG, "down shares ys");
     constexpr int RPB = QD_WAVES * (64 / LPR);
     QD_TS(0);
@@ -738,7 +847,7 @@ __global__ __launch_bounds__(QD_THREADS, 8) void k_decode_fused(QdArgs a)
         return;
     }
     b -= a.n_ex;
-    qd_role_down<NULD, PL>(a, b, R, xs, reinterpret_cast<float (*)[QD_DOWN_RPG]>(&ys[0][0]));
+    qd_role_down<NULD, PL>(a, b, R, xs, reinterpret_cast<float (*)[QD_DOWN_RPG]>(&ys[0][0]), &dready);
 }
 
 // ---- host side -------------------------------------------------------------------
