@@ -16,16 +16,22 @@
 // scaled by F at the end.  Activations and weights both carry one f16
 // rounding.
 //
-// Tiles.  A workgroup (4 waves) owns up to 64 rows (a tile of one expert's
-// pairs, or of dense rows) against 256 weight rows: with SWIGLU, 128 gate
-// and the same 128 up features, so gate and up meet in one lane and leave as
-// silu(g) * u.  Wave w holds 4 weight tiles of 16 rows against 4 row tiles
-// of 16.  K streams in chunks of KC (256 where k allows): the activation
-// chunk through double-buffered LDS, its loads two chunks ahead; each lane's
-// own weight words straight from memory into registers, one chunk ahead.
+// Tiles.  A workgroup (8 waves, one a CU) owns up to 64 rows (a tile of one
+// expert's pairs, or of dense rows) against 512 weight rows: with SWIGLU,
+// 256 gate and the same 256 up features, so gate and up meet in one lane and
+// leave as silu(g) * u.  Wave w holds 4 weight tiles of 16 rows against 4
+// row tiles of 16.  K streams in chunks of KC (256 where k allows):
+//   activations  through double-buffered LDS, loaded two chunks ahead;
+//   weights      each lane's own words straight into registers, a ring
+//                refilled with the next chunk's words as soon as a load
+//                group is dequantised;
+//   scales and   blocks of up to 16 groups a row, loaded straight into LDS
+//   biases       (buffer loads with the lds bit), one block ahead.
 // Per chunk lane group kg (lanes 16 kg .. 16 kg + 15) holds KC / 4
 // consecutive k of each of its weight rows (one quantisation group when
-// G = KC / 4), so the 4 lane groups' loads cover whole 128-byte lines.
+// G = KC / 4), so the 4 lane groups' loads cover whole 128-byte lines.  MFMA
+// step s runs while step s + 1's A fragments are read and its words
+// dequantised.
 //
 // Order of tiles.  Workgroup b runs on XCD b % 8.  Each XCD takes a
 // contiguous range of tiles, walked with the column block fastest: the
@@ -41,8 +47,8 @@ typedef uint32_t g16_u2 __attribute__((ext_vector_type(2)));
 typedef _Float16 g16_h2 __attribute__((ext_vector_type(2)));
 
 #define G16_BM 64
-#define G16_BN 256
-#define G16_THREADS 256
+#define G16_BN 512
+#define G16_THREADS 512
 
 // ---- staging ------------------------------------------------------------------------
 
@@ -124,10 +130,11 @@ struct Gmm16Args {
     int rows;                       // dense: rows
     int nblk;                       // column blocks per tile
     int nbw;                        // column blocks a workgroup runs back to back
+    int gpb;                        // quantisation groups per scale / bias block (1 .. 16)
 };
 
 template <int G, bool SWIGLU, bool DENSE, int KC>
-__global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16(Gmm16Args a)
+__global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
 {
     constexpr int WPL = KC / 32;                         // words (MFMA k steps) per lane per chunk
     constexpr int KPL = WPL * 8;                         // k a lane covers per chunk
@@ -136,7 +143,9 @@ __global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16(Gmm16Args a)
     constexpr int AU4 = G16_BM * KC / 8 / G16_THREADS;   // uint4 of A a thread moves per chunk
     static_assert(NGL <= 2 && AU4 >= 1 && (WPL == 2 || WPL == 4 || WPL == 8), "chunk shape");
     static_assert(G16_BM * (KC + 8) < 65536, "LDS offsets of A fit 16 bits");
+    static_assert(G16_THREADS == G16_BN, "a thread per weight row loads the scale / bias blocks");
     __shared__ __align__(16) _Float16 As[2][G16_BM][AST];
+    __shared__ __align__(16) uint8_t Sb[2][4 * G16_BN * 16];      // scale / bias blocks (below)
     __shared__ float Fr[G16_BM];
     __shared__ int srow[G16_BM], drow[G16_BM];
 
@@ -165,6 +174,7 @@ __global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16(Gmm16Args a)
     }
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, ln = lane & 15, kg = lane >> 4;
     const int k = a.k, words = k / 8, groups = k / G, nch = k / KC, T = nitems * nch;
+    const int gpb = a.gpb, sbc = gpb * G / KC, nbk = groups / gpb;   // chunks a block, blocks an item
     if (t < G16_BM) {
         int sr = -1, dr = -1;
         if (t < len) {
@@ -215,11 +225,11 @@ __global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16(Gmm16Args a)
             *reinterpret_cast<g16_u4 *>(&As[q][0][0] + ldsA[i]) = (aokm >> i) & 1 ? ra[i] : z;
     };
 
-    // Weights: lane (ln, kg) of wave w owns weight row col(item, nt) of tile
-    // nt (4 tiles of 16 rows); per chunk, the KPL consecutive k from
-    // kg KPL: WPL consecutive words, and the scales and biases of the NGL
-    // groups they fall in.  MFMA step s takes word s of every lane, so the A
-    // fragment of lane group kg is k = c KC + kg KPL + 8 s .. + 7.
+    // Weight rows.  Row j of the workgroup's G16_BN (the LDS row of the scale
+    // / bias blocks) is column col(item, j); with SWIGLU rows [0, BN/2) are
+    // gate features and [BN/2, BN) the same features of up.  Lane (ln, kg) of
+    // wave w owns rows rowof(w, nt) of 4 tiles of 16: with SWIGLU tiles 0, 1
+    // are gate and 2, 3 up, so gate and up of a feature meet in one lane.
     __amdgpu_buffer_rsrc_t rW[2], rS[2], rB[2];
 #pragma unroll
     for (int h = 0; h < 2; h++) {
@@ -228,39 +238,77 @@ __global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16(Gmm16Args a)
         rS[h] = qw_rsrc((up ? a.s1 : a.s0) + (size_t)expert * a.eg);
         rB[h] = qw_rsrc((up ? a.b1 : a.b0) + (size_t)expert * a.eg);
     }
-    // SWIGLU: tiles 0, 1 are gate features, 2, 3 the same features of up
-    auto colof = [&](int item, int nt) {
-        const int nb = nb0 + item;
-        return SWIGLU ? nb * (G16_BN / 2) + wave * 32 + (nt & 1) * 16 + ln : nb * G16_BN + wave * 64 + nt * 16 + ln;
+    auto rowof = [&](int nt) {
+        return SWIGLU ? (nt >> 1) * (G16_BN / 2) + wave * 32 + (nt & 1) * 16 + ln : wave * 64 + nt * 16 + ln;
     };
-    auto fetch_b = [&](int step, uint32_t (&wq)[4][WPL], uint32_t (&sq)[4], uint32_t (&bq)[4]) {
+    auto colof = [&](int item, int j) {
+        const int nb = nb0 + item;
+        return SWIGLU ? nb * (G16_BN / 2) + (j % (G16_BN / 2)) : nb * G16_BN + j;
+    };
+    // Per chunk, lane kg holds the KPL consecutive k from kg KPL of each of
+    // its rows: WPL consecutive words.  MFMA step s takes word s of every
+    // lane, so the A fragment of lane group kg is k = c KC + kg KPL + 8 s ...
+    // Weight words come in load groups of WGP (one 16- or 8-byte load a
+    // row): group lg of chunk `step` into wq[nt][lg WGP ..].
+    constexpr int WGP = WPL == 2 ? 2 : 4, NLG = WPL / WGP;
+    auto fetch_bg = [&](int step, int lg, uint32_t (&wq)[4][WPL]) {
         step = min(step, T - 1);
         const int item = step / nch, c = step % nch;
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) {
             const int h = SWIGLU ? nt >> 1 : 0;
-            const int col = colof(item, nt), cc = col < a.n ? col : 0;
-            const uint32_t o = (uint32_t)((cc * words + c * (KC / 8) + kg * WPL) * 4);
-            if (WPL == 2) {
+            const int col = colof(item, rowof(nt)), cc = col < a.n ? col : 0;
+            const uint32_t o = (uint32_t)((cc * words + c * (KC / 8) + kg * WPL + lg * WGP) * 4);
+            if (WGP == 2) {
                 const g16_u2 v = __builtin_bit_cast(g16_u2, __builtin_amdgcn_raw_buffer_load_b64(rW[h], o, 0, 0));
-                wq[nt][0] = v.x; wq[nt][1] = v.y;
+                wq[nt][lg * WGP] = v.x; wq[nt][lg * WGP + 1] = v.y;
             } else {
-#pragma unroll
-                for (int j = 0; j < WPL / 4; j++) {
-                    const g16_u4 v = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rW[h], o + 16 * j, 0, 0));
-                    wq[nt][4 * j] = v.x; wq[nt][4 * j + 1] = v.y; wq[nt][4 * j + 2] = v.z; wq[nt][4 * j + 3] = v.w;
-                }
-            }
-            const uint32_t og = (uint32_t)((cc * groups + (c * KC + kg * KPL) / G) * 2);
-            if (NGL == 1) {
-                sq[nt] = __builtin_amdgcn_raw_buffer_load_b16(rS[h], og, 0, 0);
-                bq[nt] = __builtin_amdgcn_raw_buffer_load_b16(rB[h], og, 0, 0);
-            } else {
-                sq[nt] = __builtin_amdgcn_raw_buffer_load_b32(rS[h], og, 0, 0);
-                bq[nt] = __builtin_amdgcn_raw_buffer_load_b32(rB[h], og, 0, 0);
+                const g16_u4 v = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rW[h], o, 0, 0));
+                wq[nt][lg * WGP] = v.x; wq[nt][lg * WGP + 1] = v.y;
+                wq[nt][lg * WGP + 2] = v.z; wq[nt][lg * WGP + 3] = v.w;
             }
         }
     };
+    // Scales and biases, a block of gpb groups (sbc chunks) at a time, loaded
+    // straight into LDS (buffer loads with the lds bit: no registers, so
+    // nothing for the compiler to wait on or copy): thread t moves row t's
+    // run of the block, DS bytes a load, for one cache tag per row per block
+    // where a per-chunk load takes one per row per chunk.  A load of wave w
+    // writes DS bytes per lane contiguously, so region j of a block holds
+    // [row][DS bytes]: scales in regions [0, nrg), biases in [nrg, 2 nrg).
+    // Blocks follow the stream: block beta = item * nbk + c / sbc.
+    const int nblocks = nitems * nbk;
+    const int DS = gpb >= 8 ? 16 : gpb >= 2 ? 4 : 2, gpr = DS / 2, nrg = gpb / gpr;   // bytes a load, groups a region
+    auto fetch_sb = [&](int beta, int q) {
+        beta = min(beta, nblocks - 1);
+        const int item = beta / nbk, blk = beta % nbk;
+        const int h = SWIGLU ? __builtin_amdgcn_readfirstlane(t / (G16_BN / 2)) : 0;
+        const int col = colof(item, t), cc = col < a.n ? col : 0;
+        const uint32_t o = (uint32_t)((cc * groups + blk * gpb) * 2);
+        // this wave's 64 rows of region j start at j * BN * DS + wave * 64 * DS
+        __attribute__((address_space(3))) uint8_t *base =
+            (__attribute__((address_space(3))) uint8_t *)(&Sb[q][0]) + wave * 64 * DS;
+        for (int j = 0; j < nrg; j++) {
+            if (DS == 16) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rS[h], base + j * G16_BN * 16, 16, o + 16 * j, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rB[h], base + (nrg + j) * G16_BN * 16, 16, o + 16 * j, 0, 0, 0);
+            } else if (DS == 4) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rS[h], base + j * G16_BN * 4, 4, o + 4 * j, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rB[h], base + (nrg + j) * G16_BN * 4, 4, o + 4 * j, 0, 0, 0);
+            } else {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rS[h], base + j * G16_BN * 2, 2, o + 2 * j, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rB[h], base + (nrg + j) * G16_BN * 2, 2, o + 2 * j, 0, 0, 0);
+            }
+        }
+    };
+    // scale / bias of group gl of LDS row j in block buffer q, as bf16 bits
+    auto sb_at = [&](int q, int j, int gl, int bias) -> uint32_t {
+        const uint8_t *p = &Sb[q][((bias ? nrg : 0) + gl / gpr) * G16_BN * DS + j * DS + (gl % gpr) * 2];
+        return *reinterpret_cast<const uint16_t *>(p);
+    };
+    // loads a step issues after the block's: the weights (the wait before the
+    // barrier that publishes a block leaves them in flight)
+    constexpr int NBL = 4 * (WPL == 2 ? 1 : WPL / 4);
 
     g16_f4 acc[4][4];
 #pragma unroll
@@ -270,43 +318,66 @@ __global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16(Gmm16Args a)
     uint32_t lo = 0x64006400u, hi = 0x54005400u;
     asm volatile("" : "+v"(lo), "+v"(hi));
 
-    // One chunk: MFMAs from As[i & 1] and the weights in (wq, sq, bq), the
-    // next chunk's weights into (wn, sn, bn), the chunk after next's
-    // activations into registers once this one's are in LDS.
-    auto step = [&](int i, uint32_t (&wq)[4][WPL], uint32_t (&sq)[4], uint32_t (&bq)[4],
-                    uint32_t (&wn)[4][WPL], uint32_t (&sn)[4], uint32_t (&bn)[4]) {
+    // One chunk: MFMAs from As[i & 1], the weights in wq and the scale /
+    // bias block in Sb.  MFMA step s runs while step s + 1's A fragments are
+    // read and its weight words dequantised; a load group of wq is refilled
+    // with the next chunk's words as soon as its last word is dequantised (a
+    // ring: every word has a chunk's time to land).  At a block's first chunk
+    // the next block's scales and biases are issued; the chunk after next's
+    // activations go to registers once this one's are in LDS.
+    uint32_t wq[4][WPL];
+    auto step = [&](int i) {
         const int q = i & 1, item = i / nch, c = i % nch;
+        const int beta = item * nbk + c / sbc;
+        const bool bstart = c % sbc == 0;
         g16_h2 s2[4][NGL], b2[4][NGL];
+        {
+            const int gl = ((c % sbc) * KC + kg * KPL) / G;
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++)
+            for (int nt = 0; nt < 4; nt++)
 #pragma unroll
-            for (int g = 0; g < NGL; g++) {
-                s2[nt][g] = g16_bf2h2(sq[nt], g);
-                b2[nt][g] = g16_bf2h2(bq[nt], g);
-            }
-        // the next chunk's weights are issued here, ahead of this chunk's
-        // MFMAs (left to itself the scheduler sinks them below, which
-        // serialises memory and compute)
+                for (int g = 0; g < NGL; g++) {
+                    s2[nt][g] = g16_bf2h2(sb_at(beta & 1, rowof(nt), gl + g, 0), 0);
+                    b2[nt][g] = g16_bf2h2(sb_at(beta & 1, rowof(nt), gl + g, 1), 0);
+                }
+        }
         __builtin_amdgcn_sched_barrier(0);
-        fetch_b(i + 1, wn, sn, bn);
+        if (bstart) fetch_sb(beta + 1, (beta + 1) & 1);
         __builtin_amdgcn_sched_barrier(0);
+        auto lda = [&](int st, g16_h8 (&o)[4]) {
+            const int ah = kg * KPL + 8 * st;
 #pragma unroll
-        for (int s = 0; s < WPL; s++) {
-            const int g = NGL == 1 ? 0 : s * 8 / G;
-            g16_h8 bf[4];
+            for (int mt = 0; mt < 4; mt++) o[mt] = *reinterpret_cast<const g16_h8 *>(&As[q][mt * 16 + ln][ah]);
+        };
+        auto dqs = [&](int st, g16_h8 (&o)[4]) {
+            const int g = NGL == 1 ? 0 : st * 8 / G;
 #pragma unroll
             for (int nt = 0; nt < 4; nt++) {
-                uint32_t o[4];
-                g16_dq(wq[nt][s], s2[nt][g], b2[nt][g], lo, hi, o);
-                bf[nt] = __builtin_bit_cast(g16_h8, g16_u4{o[0], o[1], o[2], o[3]});
+                uint32_t d[4];
+                g16_dq(wq[nt][st], s2[nt][g], b2[nt][g], lo, hi, d);
+                o[nt] = __builtin_bit_cast(g16_h8, g16_u4{d[0], d[1], d[2], d[3]});
             }
-            const int ah = kg * KPL + 8 * s;
+        };
+        g16_h8 af[2][4], bf[2][4];
+        lda(0, af[0]);
+        dqs(0, bf[0]);
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++) {
-                const g16_h8 af = *reinterpret_cast<const g16_h8 *>(&As[q][mt * 16 + ln][ah]);
+        for (int st = 0; st < WPL; st++) {
+            const int cu = st & 1;
+            if (st + 1 < WPL) {
+                lda(st + 1, af[cu ^ 1]);
+                dqs(st + 1, bf[cu ^ 1]);
+            }
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++)
 #pragma unroll
                 for (int nt = 0; nt < 4; nt++)
-                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[nt], acc[mt][nt], 0, 0, 0);
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[cu][mt], bf[cu][nt], acc[mt][nt], 0, 0, 0);
+            // word st + 1 was a load group's last: refill the group
+            if (st + 1 < WPL && (st + 2) % WGP == 0) {
+                __builtin_amdgcn_sched_barrier(0);
+                fetch_bg(i + 1, (st + 1) / WGP, wq);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         if (c == nch - 1) {
@@ -323,13 +394,13 @@ __global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16(Gmm16Args a)
                         if (SWIGLU) {
 #pragma unroll
                             for (int nt = 0; nt < 2; nt++) {
-                                const int col = colof(item, nt);
+                                const int col = colof(item, rowof(nt));
                                 if (col < a.n) yr[col] = qw_silu(f * acc[mt][nt][e]) * (f * acc[mt][nt + 2][e]);
                             }
                         } else {
 #pragma unroll
                             for (int nt = 0; nt < 4; nt++) {
-                                const int col = colof(item, nt);
+                                const int col = colof(item, rowof(nt));
                                 if (col < a.n) yr[col] = f * acc[mt][nt][e];
                             }
                         }
@@ -339,24 +410,25 @@ __global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16(Gmm16Args a)
                 }
         }
         stash_a(q ^ 1);
+        // the next block's scales and biases landed in LDS (the weights
+        // issued after them stay in flight) before the barrier publishes them
+        if (bstart) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NBL) : "memory");
         fetch_a(i + 2);
         __syncthreads();
     };
 
-    uint32_t wqa[4][WPL], sqa[4], bqa[4], wqb[4][WPL], sqb[4], bqb[4];
-    // the same issue order as a step's (weights, then activations two ahead),
-    // so the loop head waits for the same loads from either side
+    // the same issue order as a step's (scales and biases, weights, then
+    // activations two ahead), so the loop head waits for the same loads from
+    // either side
     fetch_a(0);
-    fetch_b(0, wqa, sqa, bqa);
+    fetch_sb(0, 0);
+#pragma unroll
+    for (int lg = 0; lg < NLG; lg++) fetch_bg(0, lg, wq);
     stash_a(0);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NBL) : "memory");
     fetch_a(1);
     __syncthreads();
-    int i = 0;
-    for (; i + 1 < T; i += 2) {
-        step(i, wqa, sqa, bqa, wqb, sqb, bqb);
-        step(i + 1, wqb, sqb, bqb, wqa, sqa, bqa);
-    }
-    if (i < T) step(i, wqa, sqa, bqa, wqb, sqb, bqb);
+    for (int i = 0; i < T; i++) step(i);
 }
 
 // ---- host side ---------------------------------------------------------------------
@@ -400,13 +472,22 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
     a.w1 = swiglu ? m1.w : m0.w; a.s1 = swiglu ? m1.s : m0.s; a.b1 = swiglu ? m1.b : m0.b;
     a.ew = ew; a.eg = eg; a.k = k; a.n = n; a.K = K; a.x_by_pair = x_by_pair; a.rows = dense_rows;
     a.nblk = swiglu ? (n + G16_BN / 2 - 1) / (G16_BN / 2) : (n + G16_BN - 1) / G16_BN;
+    {
+        // the largest scale / bias block (groups) that divides a row's groups
+        // and ends on a chunk boundary
+        const int groups = k / group;
+        a.gpb = 0;
+        for (int g = 16; g >= 1 && !a.gpb; g /= 2)
+            if (groups % g == 0 && (g * group) % kc == 0) a.gpb = g;
+        if (!a.gpb) return (int)hipErrorInvalidValue;
+    }
     const int ntiles = dense ? (dense_rows + G16_BM - 1) / G16_BM : max_tiles;
     if (ntiles <= 0) return 0;
     // column blocks per workgroup: long streams, but enough workgroups to
     // fill the chip (max_tiles bounds the grouped tile count from above)
     {
 #ifndef G16_NBW
-        const long per = (long)ntiles * a.nblk / 2048;
+        const long per = (long)ntiles * a.nblk / 1024;
         a.nbw = per < 1 ? 1 : per > 8 ? 8 : (int)per;
 #else
         a.nbw = G16_NBW;

@@ -31,7 +31,9 @@ int qwk_route(hipStream_t s, int32_t *idx, float *w, const float *logits,
 
 /* Stable sort of pairs by expert; tiles = [count, (expert, start, len)...]. */
 int qwk_moe_group(hipStream_t s, int32_t *perm, int32_t *tiles, const int32_t *idx,
-                  int pairs, int E, int bm, int max_tiles);
+                  int pairs, int E, int bm, int max_tiles, void *work, size_t work_bytes);
+/* Bytes of the work buffer qwk_moe_group needs for `pairs` pairs of E experts. */
+size_t qwk_moe_group_work_bytes(int pairs, int E);
 
 /* Quantised matvec over (token, slot) pairs.
  *   y[z][p, 0:n] = W_z(e_p) . in(p)

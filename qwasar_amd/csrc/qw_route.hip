@@ -269,71 +269,100 @@ extern "C" int qwk_route(hipStream_t s, int32_t *idx, float *w, const float *log
 // ---- the dispatch permutation ------------------------------------------------
 //
 // Pairs sorted by expert, stably: within an expert, ascending pair index.
-// Eight waves each own a contiguous run of pairs.  Counts per (wave, expert)
-// are order-free (LDS atomics); an exclusive scan over experts and then over
-// waves gives every (wave, expert) its first slot; each wave then walks its
-// run 64 pairs at a time, ranking a lane among the lower lanes that share
-// its expert with ballots over the expert id's bits.
+// The pairs are cut into chunks of QW_GROUP_CHUNK, one workgroup each, and
+// within a chunk into eight contiguous runs, one a wave.  Three launches:
+//
+//   count  per (chunk, wave, expert) counts (order-free LDS atomics)
+//   scan   one workgroup: an exclusive scan over experts and then, within an
+//          expert, over (chunk, wave) gives every (chunk, wave, expert) its
+//          first slot; the tile list follows from the per-expert totals
+//   place  each wave walks its run 64 pairs at a time, ranking a lane among
+//          the lower lanes that share its expert with ballots over the
+//          expert id's bits, from its (chunk, wave, expert) slots
+//
+// The counts live in a work buffer of qwk_moe_group_work_bytes(pairs, E).
 
 #define QW_GROUP_WAVES 8
 #define QW_GROUP_THREADS (QW_GROUP_WAVES * 64)
+#define QW_GROUP_RUN 256                                    // pairs a wave walks
+#define QW_GROUP_CHUNK (QW_GROUP_WAVES * QW_GROUP_RUN)
+#define QW_SCAN_THREADS 1024
 
-// Exclusive scan of v over the block (QW_GROUP_THREADS values); returns the
-// prefix and writes the total to *total.
-__device__ int qw_block_excl_scan(int v, int *tmp, int *total)
+// Exclusive scan of v over the block (nthr values); returns the prefix and
+// writes the total to *total.
+__device__ int qw_block_excl_scan(int v, int *tmp, int *total, int nthr)
 {
     const int t = threadIdx.x;
     tmp[t] = v;
     __syncthreads();
-    for (int off = 1; off < QW_GROUP_THREADS; off <<= 1) {
+    for (int off = 1; off < nthr; off <<= 1) {
         const int add = t >= off ? tmp[t - off] : 0;
         __syncthreads();
         tmp[t] += add;
         __syncthreads();
     }
     const int incl = tmp[t];
-    *total = tmp[QW_GROUP_THREADS - 1];
+    *total = tmp[nthr - 1];
     __syncthreads();
     return incl - v;
 }
 
-__global__ __launch_bounds__(QW_GROUP_THREADS) void k_moe_group(
-    int *__restrict__ perm, int *__restrict__ tiles, const int *__restrict__ idx,
-    int pairs, int E, int bm, int max_tiles)
+// work[(chunk * WAVES + wave) * E + e] = pairs of expert e in that run
+__global__ __launch_bounds__(QW_GROUP_THREADS) void k_group_count(int *__restrict__ work,
+                                                                  const int *__restrict__ idx, int pairs, int E)
 {
     __shared__ int cnt[QW_GROUP_WAVES][QWK_GROUP_MAX_E];
-    __shared__ int tmp[QW_GROUP_THREADS];
     const int t = threadIdx.x, wave = t / 64, lane = t % 64;
-    const int per = (pairs + QW_GROUP_WAVES - 1) / QW_GROUP_WAVES;
-    const int p0 = min(pairs, wave * per), p1 = min(pairs, p0 + per);
-
-    for (int i = t; i < QW_GROUP_WAVES * QWK_GROUP_MAX_E; i += QW_GROUP_THREADS)
-        (&cnt[0][0])[i] = 0;
+    for (int i = t; i < QW_GROUP_WAVES * E; i += QW_GROUP_THREADS) cnt[i / E][i % E] = 0;
     __syncthreads();
+    const int p0 = min(pairs, blockIdx.x * QW_GROUP_CHUNK + wave * QW_GROUP_RUN), p1 = min(pairs, p0 + QW_GROUP_RUN);
     for (int p = p0 + lane; p < p1; p += 64) atomicAdd(&cnt[wave][idx[p]], 1);
     __syncthreads();
+    int *w = work + (size_t)blockIdx.x * QW_GROUP_WAVES * E;
+    for (int i = t; i < QW_GROUP_WAVES * E; i += QW_GROUP_THREADS) w[i] = cnt[i / E][i % E];
+}
 
-    // Each thread owns experts [e0, e0 + per_t): their totals, scanned.
-    const int per_t = (E + QW_GROUP_THREADS - 1) / QW_GROUP_THREADS;
+// Counts to first slots, in place, and the tile list.  Thread t owns experts
+// [t * per_t, (t + 1) * per_t).
+__global__ __launch_bounds__(QW_SCAN_THREADS) void k_group_scan(int *__restrict__ work, int *__restrict__ tiles,
+                                                                 int nruns, int E, int bm, int max_tiles)
+{
+    __shared__ int tmp[QW_SCAN_THREADS];
+    const int t = threadIdx.x;
+    const int per_t = (E + QW_SCAN_THREADS - 1) / QW_SCAN_THREADS;
     const int e0 = min(E, t * per_t), e1 = min(E, e0 + per_t);
+    // the run counts are read 16 at a time (independent loads in flight
+    // together, not one memory round trip each)
+    constexpr int RB = 16;
     int mytot = 0, mytiles = 0;
     for (int e = e0; e < e1; e++) {
         int c = 0;
-        for (int wv = 0; wv < QW_GROUP_WAVES; wv++) c += cnt[wv][e];
+        for (int r0 = 0; r0 < nruns; r0 += RB) {
+            int v[RB];
+#pragma unroll
+            for (int j = 0; j < RB; j++) v[j] = r0 + j < nruns ? work[(size_t)(r0 + j) * E + e] : 0;
+#pragma unroll
+            for (int j = 0; j < RB; j++) c += v[j];
+        }
         mytot += c;
         mytiles += (c + bm - 1) / bm;
     }
     int total_pairs, total_tiles;
-    int base = qw_block_excl_scan(mytot, tmp, &total_pairs);
-    int tbase = qw_block_excl_scan(mytiles, tmp, &total_tiles);
+    int base = qw_block_excl_scan(mytot, tmp, &total_pairs, QW_SCAN_THREADS);
+    int tbase = qw_block_excl_scan(mytiles, tmp, &total_tiles, QW_SCAN_THREADS);
     for (int e = e0; e < e1; e++) {
-        int run = base, c = 0;
-        for (int wv = 0; wv < QW_GROUP_WAVES; wv++) {
-            const int x = cnt[wv][e];
-            cnt[wv][e] = run;
-            run += x;
-            c += x;
+        int run = base;
+        for (int r0 = 0; r0 < nruns; r0 += RB) {
+            int v[RB];
+#pragma unroll
+            for (int j = 0; j < RB; j++) v[j] = r0 + j < nruns ? work[(size_t)(r0 + j) * E + e] : 0;
+#pragma unroll
+            for (int j = 0; j < RB; j++) {
+                if (r0 + j < nruns) work[(size_t)(r0 + j) * E + e] = run;
+                run += v[j];
+            }
         }
+        const int c = run - base;
         for (int s = 0; s < c; s += bm, tbase++) {
             if (tbase < max_tiles) {
                 tiles[1 + 3 * tbase + 0] = e;
@@ -341,11 +370,21 @@ __global__ __launch_bounds__(QW_GROUP_THREADS) void k_moe_group(
                 tiles[1 + 3 * tbase + 2] = min(bm, c - s);
             }
         }
-        base += c;
+        base = run;
     }
     if (t == 0) tiles[0] = min(total_tiles, max_tiles);
-    __syncthreads();
+}
 
+__global__ __launch_bounds__(QW_GROUP_THREADS) void k_group_place(int *__restrict__ perm,
+                                                                  const int *__restrict__ work,
+                                                                  const int *__restrict__ idx, int pairs, int E)
+{
+    __shared__ int cnt[QW_GROUP_WAVES][QWK_GROUP_MAX_E];
+    const int t = threadIdx.x, wave = t / 64, lane = t % 64;
+    const int *w = work + (size_t)blockIdx.x * QW_GROUP_WAVES * E;
+    for (int i = t; i < QW_GROUP_WAVES * E; i += QW_GROUP_THREADS) cnt[i / E][i % E] = w[i];
+    __syncthreads();
+    const int p0 = min(pairs, blockIdx.x * QW_GROUP_CHUNK + wave * QW_GROUP_RUN), p1 = min(pairs, p0 + QW_GROUP_RUN);
     int nbits = 1;
     while ((1 << nbits) < E) nbits++;
     const unsigned long long below = (1ull << lane) - 1ull;
@@ -371,12 +410,23 @@ __global__ __launch_bounds__(QW_GROUP_THREADS) void k_moe_group(
     }
 }
 
-extern "C" int qwk_moe_group(hipStream_t s, int32_t *perm, int32_t *tiles, const int32_t *idx,
-                             int pairs, int E, int bm, int max_tiles)
+extern "C" size_t qwk_moe_group_work_bytes(int pairs, int E)
 {
-    if (pairs < 0 || E < 1 || E > QWK_GROUP_MAX_E || bm < 1 || max_tiles < 0)
+    const size_t chunks = pairs > 0 ? (size_t)(pairs + QW_GROUP_CHUNK - 1) / QW_GROUP_CHUNK : 1;
+    return chunks * QW_GROUP_WAVES * (size_t)(E > 0 ? E : 1) * sizeof(int);
+}
+
+extern "C" int qwk_moe_group(hipStream_t s, int32_t *perm, int32_t *tiles, const int32_t *idx,
+                             int pairs, int E, int bm, int max_tiles, void *work, size_t work_bytes)
+{
+    if (pairs < 0 || E < 1 || E > QWK_GROUP_MAX_E || bm < 1 || max_tiles < 0 || !work ||
+        work_bytes < qwk_moe_group_work_bytes(pairs, E))
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(QW_GROUP_THREADS), 0, s, perm, tiles, idx,
-                       pairs, E, bm, max_tiles);
+    const int chunks = pairs > 0 ? (pairs + QW_GROUP_CHUNK - 1) / QW_GROUP_CHUNK : 1;
+    int *wk = static_cast<int *>(work);
+    hipLaunchKernelGGL(k_group_count, dim3(chunks), dim3(QW_GROUP_THREADS), 0, s, wk, idx, pairs, E);
+    hipLaunchKernelGGL(k_group_scan, dim3(1), dim3(QW_SCAN_THREADS), 0, s, wk, tiles,
+                       chunks * QW_GROUP_WAVES, E, bm, max_tiles);
+    hipLaunchKernelGGL(k_group_place, dim3(chunks), dim3(QW_GROUP_THREADS), 0, s, perm, wk, idx, pairs, E);
     return (int)hipGetLastError();
 }

@@ -546,6 +546,8 @@ int32_t qw_moe_tile_rows(int32_t pairs, int32_t E) {
     return 16;
 }
 
+static void *scratch(size_t bytes);
+
 void qw_op_moe_group(qw_cmd c, qw_ref perm, qw_ref tiles, qw_ref cursor, qw_ref idx,
                      int32_t pairs, int32_t E) {
     (void)cursor;
@@ -556,8 +558,11 @@ void qw_op_moe_group(qw_cmd c, qw_ref perm, qw_ref tiles, qw_ref cursor, qw_ref 
     }
     touch(c, idx, 0); touch(c, perm, 1); touch(c, tiles, 1);
     const int32_t bm = qw_moe_tile_rows(pairs, E);
+    const size_t wb = qwk_moe_group_work_bytes(pairs, E);
+    void *work = scratch(wb);
+    if (!work) { cmd_fail(c, hipErrorOutOfMemory, "moe_group: scratch of %zu bytes", wb); return; }
     launched(c, "moe_group", qwk_moe_group(G.stream, dp(perm), dp(tiles), dp(idx), pairs, E, bm,
-                                           tiles_for(pairs, E, bm)));
+                                           tiles_for(pairs, E, bm), work, wb));
 }
 
 void qw_op_qmm_q4_gather(qw_cmd c, qw_ref y, qw_ref x, qw_ref perm, qw_ref tiles, qw_ref w,
@@ -621,6 +626,7 @@ static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const floa
     const size_t o_sF = off;     off += al256((size_t)rows * 4);
     const size_t o_sh = off;     off += al256((size_t)rows * H * 4);
     const size_t o_g1 = off;     off += al256((size_t)rows * 4);
+    const size_t o_gw = off;     off += al256(qwk_moe_group_work_bytes(pairs, E));
     char *S = scratch(off);
     if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", off); return false; }
     uint16_t *xh = (uint16_t *)(S + o_xh), *ah = (uint16_t *)(S + o_ah), *sh16 = (uint16_t *)(S + o_sh16);
@@ -633,7 +639,8 @@ static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const floa
     int rc = qwk_stage16(s, xh, xF, x, rows, H);
     if (!rc) rc = qwk_dmat_bf16(s, logits, x, dp(M->router), H, E, rows);
     if (!rc) rc = qwk_route(s, idx, w, logits, rows, E, K, M->norm ? 1 : 0);
-    if (!rc) rc = qwk_moe_group(s, perm, tiles, idx, pairs, E, QW_PF_BM, mt);
+    if (!rc) rc = qwk_moe_group(s, perm, tiles, idx, pairs, E, QW_PF_BM, mt, S + o_gw,
+                                qwk_moe_group_work_bytes(pairs, E));
     if (M->split) {
         if (!rc) rc = qwk_gmm16(s, act, I, xh, xF, perm, tiles, mt, q4r(&M->gate), q4r(&M->up),
                                 (long)I * words, (long)I * groups, H, I, K, 0, grp, 1, 0);
