@@ -26,16 +26,49 @@ __global__ void k_swiglu_split(float *__restrict__ act, const float *__restrict_
 
 // out[r, i] = [sh[r, i] * sigmoid(g[r])] + sum_k w[r, k] * y[r*K + k, i], an fma
 // chain in slot order starting from the shared term (or from 0 without one).
+// out[r, i] = sigmoid(g[r]) * sh[r, i] (if sh) + sum_k w[r, k] * y[r K + k, i],
+// the shared term first, then one fma a slot in slot order.  Row r is
+// blockIdx.y; a thread takes 4 consecutive columns (H % 4 == 0: float4), or
+// one column in the scalar form.
+template <bool V4>
 __global__ void k_moe_combine(float *__restrict__ out, const float *__restrict__ y,
                               const float *__restrict__ w, const float *__restrict__ sh,
                               const float *__restrict__ g, int rows, int K, int H)
 {
-    const int64_t t = (int64_t)blockIdx.x * QW_EW_THREADS + threadIdx.x;
-    if (t >= (int64_t)rows * H) return;
-    const int64_t r = t / H, i = t % H;
-    float acc = sh ? sh[t] * qw_sigmoid(g[r]) : 0.0f;
-    for (int k = 0; k < K; k++) acc = __builtin_fmaf(w[r * K + k], y[(r * K + k) * H + i], acc);
-    out[t] = acc;
+    const int r = blockIdx.y;
+    const int i = (blockIdx.x * QW_EW_THREADS + threadIdx.x) * (V4 ? 4 : 1);
+    if (i >= H) return;
+    const size_t row = (size_t)r * H;
+    if (V4) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (sh) {
+            const float gs = qw_sigmoid(g[r]);
+            const float4 v = *reinterpret_cast<const float4 *>(sh + row + i);
+            acc = make_float4(v.x * gs, v.y * gs, v.z * gs, v.w * gs);
+        }
+        // every slot's loads in flight together
+        float4 yv[16];
+        for (int k0 = 0; k0 < K; k0 += 16) {
+            const int kn = min(16, K - k0);
+#pragma unroll
+            for (int k = 0; k < 16; k++)
+                if (k < kn) yv[k] = *reinterpret_cast<const float4 *>(y + ((size_t)r * K + k0 + k) * H + i);
+#pragma unroll
+            for (int k = 0; k < 16; k++)
+                if (k < kn) {
+                    const float wk = w[(size_t)r * K + k0 + k];
+                    acc.x = __builtin_fmaf(wk, yv[k].x, acc.x);
+                    acc.y = __builtin_fmaf(wk, yv[k].y, acc.y);
+                    acc.z = __builtin_fmaf(wk, yv[k].z, acc.z);
+                    acc.w = __builtin_fmaf(wk, yv[k].w, acc.w);
+                }
+        }
+        *reinterpret_cast<float4 *>(out + row + i) = acc;
+    } else {
+        float acc = sh ? sh[row + i] * qw_sigmoid(g[r]) : 0.0f;
+        for (int k = 0; k < K; k++) acc = __builtin_fmaf(w[(size_t)r * K + k], y[((size_t)r * K + k) * H + i], acc);
+        out[row + i] = acc;
+    }
 }
 
 __global__ void k_scale_rows_sigmoid(float *__restrict__ y, const float *__restrict__ g, int rows, int dim)
@@ -68,8 +101,12 @@ extern "C" int qwk_moe_combine(hipStream_t s, float *out, const float *y, const 
                                const float *sh, const float *g, int rows, int K, int H)
 {
     if ((int64_t)rows * H <= 0) return 0;
-    hipLaunchKernelGGL(k_moe_combine, ew_grid((int64_t)rows * H), dim3(QW_EW_THREADS), 0, s,
-                       out, y, w, sh, g, rows, K, H);
+    const bool v4 = H % 4 == 0 && ((uintptr_t)out & 15u) == 0 && ((uintptr_t)y & 15u) == 0 &&
+                    (!sh || ((uintptr_t)sh & 15u) == 0);
+    const int per = v4 ? 4 * QW_EW_THREADS : QW_EW_THREADS;
+    const dim3 grid((unsigned)((H + per - 1) / per), (unsigned)rows);
+    if (v4) hipLaunchKernelGGL(k_moe_combine<true>, grid, dim3(QW_EW_THREADS), 0, s, out, y, w, sh, g, rows, K, H);
+    else hipLaunchKernelGGL(k_moe_combine<false>, grid, dim3(QW_EW_THREADS), 0, s, out, y, w, sh, g, rows, K, H);
     return (int)hipGetLastError();
 }
 
