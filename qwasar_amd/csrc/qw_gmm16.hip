@@ -131,6 +131,11 @@ struct Gmm16Args {
     int nblk;                       // column blocks per tile
     int nbw;                        // column blocks a workgroup runs back to back
     int gpb;                        // quantisation groups per scale / bias block (1 .. 16)
+    // the extra bank: tiles of expert xe use it; pairs p >= xpairs read A row
+    // p - xpairs (when not x_by_pair)
+    const uint32_t *xw0, *xw1;
+    const uint16_t *xs0, *xb0, *xs1, *xb1;
+    int xe, xpairs;
 };
 
 template <int G, bool SWIGLU, bool DENSE, int KC>
@@ -179,7 +184,7 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
         int sr = -1, dr = -1;
         if (t < len) {
             const int p = DENSE ? first + t : a.perm[first + t];
-            sr = DENSE ? p : (a.x_by_pair ? p : p / a.K);
+            sr = DENSE ? p : (a.x_by_pair ? p : (p < a.xpairs ? p / a.K : p - a.xpairs));
             dr = p;
         }
         srow[t] = sr;
@@ -234,9 +239,15 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
 #pragma unroll
     for (int h = 0; h < 2; h++) {
         const bool up = SWIGLU && h == 1;
-        rW[h] = qw_rsrc((up ? a.w1 : a.w0) + (size_t)expert * a.ew);
-        rS[h] = qw_rsrc((up ? a.s1 : a.s0) + (size_t)expert * a.eg);
-        rB[h] = qw_rsrc((up ? a.b1 : a.b0) + (size_t)expert * a.eg);
+        if (!DENSE && expert == a.xe) {
+            rW[h] = qw_rsrc(up ? a.xw1 : a.xw0);
+            rS[h] = qw_rsrc(up ? a.xs1 : a.xs0);
+            rB[h] = qw_rsrc(up ? a.xb1 : a.xb0);
+        } else {
+            rW[h] = qw_rsrc((up ? a.w1 : a.w0) + (size_t)expert * a.ew);
+            rS[h] = qw_rsrc((up ? a.s1 : a.s0) + (size_t)expert * a.eg);
+            rB[h] = qw_rsrc((up ? a.b1 : a.b0) + (size_t)expert * a.eg);
+        }
     }
     auto rowof = [&](int nt) {
         return SWIGLU ? (nt >> 1) * (G16_BN / 2) + wave * 32 + (nt & 1) * 16 + ln : wave * 64 + nt * 16 + ln;
@@ -456,7 +467,7 @@ static void g16_launch(hipStream_t s, const Gmm16Args &a, int swiglu, int dense,
 extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb, const float *aF,
                          const int32_t *perm, const int32_t *tiles, int max_tiles,
                          qwk_q4 m0, qwk_q4 m1, long ew, long eg, int k, int n, int K, int x_by_pair,
-                         int group, int swiglu, int dense_rows)
+                         int group, int swiglu, int dense_rows, const qwk_gmm_extra *xb)
 {
     // chunks of 256 where k allows, else 64
     const int kc = k % 256 == 0 ? 256 : 64;
@@ -471,6 +482,15 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
     a.w0 = m0.w; a.s0 = m0.s; a.b0 = m0.b;
     a.w1 = swiglu ? m1.w : m0.w; a.s1 = swiglu ? m1.s : m0.s; a.b1 = swiglu ? m1.b : m0.b;
     a.ew = ew; a.eg = eg; a.k = k; a.n = n; a.K = K; a.x_by_pair = x_by_pair; a.rows = dense_rows;
+    if (xb && !dense) {
+        if (((uintptr_t)xb->m0.w & 15u) || (swiglu && ((uintptr_t)xb->m1.w & 15u))) return (int)hipErrorInvalidValue;
+        a.xw0 = xb->m0.w; a.xs0 = xb->m0.s; a.xb0 = xb->m0.b;
+        a.xw1 = swiglu ? xb->m1.w : xb->m0.w; a.xs1 = swiglu ? xb->m1.s : xb->m0.s; a.xb1 = swiglu ? xb->m1.b : xb->m0.b;
+        a.xe = xb->expert; a.xpairs = xb->pairs;
+    } else {
+        a.xw0 = a.xw1 = m0.w; a.xs0 = a.xs1 = m0.s; a.xb0 = a.xb1 = m0.b;
+        a.xe = -1; a.xpairs = 0x7FFFFFFF;
+    }
     a.nblk = swiglu ? (n + G16_BN / 2 - 1) / (G16_BN / 2) : (n + G16_BN - 1) / G16_BN;
     {
         // the largest scale / bias block (groups) that divides a row's groups
@@ -486,13 +506,13 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
     // column blocks per workgroup: long streams, but enough workgroups to
     // fill the chip (max_tiles bounds the grouped tile count from above)
     {
-#ifndef G16_NBW
+        // the largest divisor of nblk up to the target, so every workgroup
+        // of a tile runs the same number of blocks
         const long per = (long)ntiles * a.nblk / 1024;
-        a.nbw = per < 1 ? 1 : per > 8 ? 8 : (int)per;
-#else
-        a.nbw = G16_NBW;
-#endif
-        if (a.nbw > a.nblk) a.nbw = a.nblk;
+        int nbw = per < 1 ? 1 : per > 8 ? 8 : (int)per;
+        if (nbw > a.nblk) nbw = a.nblk;
+        while (a.nblk % nbw) nbw--;
+        a.nbw = nbw;
     }
     // r = b / 8 < ngr * ceil(ntiles / 8) covers every XCD's tile range
     const int ngr = (a.nblk + a.nbw - 1) / a.nbw;

@@ -31,7 +31,7 @@ int qwk_route(hipStream_t s, int32_t *idx, float *w, const float *logits,
 
 /* Stable sort of pairs by expert; tiles = [count, (expert, start, len)...]. */
 int qwk_moe_group(hipStream_t s, int32_t *perm, int32_t *tiles, const int32_t *idx,
-                  int pairs, int E, int bm, int max_tiles, void *work, size_t work_bytes);
+                  int pairs, int E, int bm, int max_tiles, void *work, size_t work_bytes, int extra);
 /* Bytes of the work buffer qwk_moe_group needs for `pairs` pairs of E experts. */
 size_t qwk_moe_group_work_bytes(int pairs, int E);
 
@@ -59,6 +59,11 @@ int qwk_gather_gemm(hipStream_t s, float *y, const float *x, const int32_t *perm
 /* Dense prefill product y[rows, n] = x[rows, k] . W^T (the shared expert). */
 int qwk_qmm(hipStream_t s, float *y, const float *x, qwk_q4 m, int k, int n, int rows, int group);
 
+/* A second weight bank for grouped tiles of expert `expert` (qwk_moe_group's
+ * extra rows): its pairs p >= `pairs` read A row p - pairs when not
+ * x_by_pair. */
+typedef struct { qwk_q4 m0, m1; int expert, pairs; } qwk_gmm_extra;
+
 /* Prefill products on MFMA over f16-staged activations (qw_gmm16.hip).
  * Staging: per row, h = f16(x 2^sh) with the row's largest magnitude in
  * [2^14, 2^15) and F = 2^-sh; h in 8-blocks ordered 0,4,1,5,2,6,3,7.
@@ -73,7 +78,8 @@ int qwk_stage16(hipStream_t s, uint16_t *h, float *F, const float *x, int rows, 
  * and y = silu(W0 A) * (W1 A).  k % 64 == 0 and k % group == 0. */
 int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ah, const float *aF,
               const int32_t *perm, const int32_t *tiles, int max_tiles, qwk_q4 m0, qwk_q4 m1, long ew,
-              long eg, int k, int n, int K, int x_by_pair, int group, int swiglu, int dense_rows);
+              long eg, int k, int n, int K, int x_by_pair, int group, int swiglu, int dense_rows,
+              const qwk_gmm_extra *xb);
 
 /* Elementwise. */
 int qwk_swiglu(hipStream_t s, float *y, const float *gate, const float *up, int64_t n);

@@ -281,6 +281,9 @@ extern "C" int qwk_route(hipStream_t s, int32_t *idx, float *w, const float *log
 //          expert id's bits, from its (chunk, wave, expert) slots
 //
 // The counts live in a work buffer of qwk_moe_group_work_bytes(pairs, E).
+// `extra` rows may follow the pairs as one more expert, E (the prefill's
+// shared expert, run in the same grouped launches): slots pairs .. pairs +
+// extra - 1 in order, and their tiles after all the others.
 
 #define QW_GROUP_WAVES 8
 #define QW_GROUP_THREADS (QW_GROUP_WAVES * 64)
@@ -325,6 +328,7 @@ __global__ __launch_bounds__(QW_GROUP_THREADS) void k_group_count(int *__restric
 // Counts to first slots, in place, and the tile list.  Thread t owns experts
 // [t * per_t, (t + 1) * per_t).
 __global__ __launch_bounds__(QW_SCAN_THREADS) void k_group_scan(int *__restrict__ work, int *__restrict__ tiles,
+                                                                 int *__restrict__ perm, int pairs, int extra,
                                                                  int nruns, int E, int bm, int max_tiles)
 {
     __shared__ int tmp[QW_SCAN_THREADS];
@@ -372,7 +376,18 @@ __global__ __launch_bounds__(QW_SCAN_THREADS) void k_group_scan(int *__restrict_
         }
         base = run;
     }
-    if (t == 0) tiles[0] = min(total_tiles, max_tiles);
+    // `extra` rows after the pairs: expert E, identity slots, tiles of bm
+    const int xt = (extra + bm - 1) / bm;
+    for (int j = t; j < xt; j += QW_SCAN_THREADS) {
+        const int tb = total_tiles + j;
+        if (tb < max_tiles) {
+            tiles[1 + 3 * tb + 0] = E;
+            tiles[1 + 3 * tb + 1] = pairs + j * bm;
+            tiles[1 + 3 * tb + 2] = min(bm, extra - j * bm);
+        }
+    }
+    for (int j = t; j < extra; j += QW_SCAN_THREADS) perm[pairs + j] = pairs + j;
+    if (t == 0) tiles[0] = min(total_tiles + xt, max_tiles);
 }
 
 __global__ __launch_bounds__(QW_GROUP_THREADS) void k_group_place(int *__restrict__ perm,
@@ -417,15 +432,16 @@ extern "C" size_t qwk_moe_group_work_bytes(int pairs, int E)
 }
 
 extern "C" int qwk_moe_group(hipStream_t s, int32_t *perm, int32_t *tiles, const int32_t *idx,
-                             int pairs, int E, int bm, int max_tiles, void *work, size_t work_bytes)
+                             int pairs, int E, int bm, int max_tiles, void *work, size_t work_bytes,
+                             int extra)
 {
-    if (pairs < 0 || E < 1 || E > QWK_GROUP_MAX_E || bm < 1 || max_tiles < 0 || !work ||
+    if (pairs < 0 || E < 1 || E > QWK_GROUP_MAX_E || bm < 1 || max_tiles < 0 || !work || extra < 0 ||
         work_bytes < qwk_moe_group_work_bytes(pairs, E))
         return (int)hipErrorInvalidValue;
     const int chunks = pairs > 0 ? (pairs + QW_GROUP_CHUNK - 1) / QW_GROUP_CHUNK : 1;
     int *wk = static_cast<int *>(work);
     hipLaunchKernelGGL(k_group_count, dim3(chunks), dim3(QW_GROUP_THREADS), 0, s, wk, idx, pairs, E);
-    hipLaunchKernelGGL(k_group_scan, dim3(1), dim3(QW_SCAN_THREADS), 0, s, wk, tiles,
+    hipLaunchKernelGGL(k_group_scan, dim3(1), dim3(QW_SCAN_THREADS), 0, s, wk, tiles, perm, pairs, extra,
                        chunks * QW_GROUP_WAVES, E, bm, max_tiles);
     hipLaunchKernelGGL(k_group_place, dim3(chunks), dim3(QW_GROUP_THREADS), 0, s, perm, wk, idx, pairs, E);
     return (int)hipGetLastError();

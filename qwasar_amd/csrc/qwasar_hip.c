@@ -562,7 +562,7 @@ void qw_op_moe_group(qw_cmd c, qw_ref perm, qw_ref tiles, qw_ref cursor, qw_ref 
     void *work = scratch(wb);
     if (!work) { cmd_fail(c, hipErrorOutOfMemory, "moe_group: scratch of %zu bytes", wb); return; }
     launched(c, "moe_group", qwk_moe_group(G.stream, dp(perm), dp(tiles), dp(idx), pairs, E, bm,
-                                           tiles_for(pairs, E, bm), work, wb));
+                                           tiles_for(pairs, E, bm), work, wb, 0));
 }
 
 void qw_op_qmm_q4_gather(qw_cmd c, qw_ref y, qw_ref x, qw_ref perm, qw_ref tiles, qw_ref w,
@@ -603,28 +603,35 @@ static void touch_q4(qw_cmd c, const qw_q4_ref *r) {
 static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 /* Prefill: the grouped path on the one stream.  Activations are staged as
- * f16 once (x, then the SwiGLU output, then the shared expert's); the
- * routed and shared products run on MFMA with SwiGLU fused into gate / up. */
+ * f16 once (x, then the SwiGLU output); the routed products run on MFMA with
+ * SwiGLU fused into gate / up.  When the shared expert has the routed
+ * experts' shape (SI == I, one group size) its rows join the same grouped
+ * launches as one more expert, E: its pairs are the token rows, appended
+ * after the routed pairs, and its down outputs are the combine's shared
+ * term.  Otherwise it runs as dense products of its own. */
 #define QW_PF_BM 64    /* tile height of the prefill product (qw_gmm16.hip) */
 static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const float *x,
                         const qw_moe_layer *M, int32_t rows) {
     const int32_t H = M->H, E = M->E, K = M->K, I = M->I, SI = M->SI, pairs = rows * K;
-    const int32_t mt = tiles_for(pairs, E, QW_PF_BM);
     const int32_t grp = M->split ? M->gate.group : M->gate_up.group;
+    const bool fuse = SI == I && M->sh_gate.group == grp && M->sh_up.group == grp && M->sh_down.group == grp;
+    const int32_t xr = fuse ? rows : 0, ntot = pairs + xr;
+    const int32_t mt = tiles_for(pairs, E, QW_PF_BM) + (xr + QW_PF_BM - 1) / QW_PF_BM;
+    const int32_t srows = fuse ? 0 : rows;      /* the unfused shared expert's buffers */
     size_t off = 0;
     const size_t o_xh = off;     off += al256((size_t)rows * H * 2);
     const size_t o_xF = off;     off += al256((size_t)rows * 4);
     const size_t o_logits = off; off += al256((size_t)rows * E * 4);
-    const size_t o_perm = off;   off += al256((size_t)pairs * 4);
+    const size_t o_perm = off;   off += al256((size_t)ntot * 4);
     const size_t o_tiles = off;  off += al256((size_t)(1 + 3 * mt) * 4);
-    const size_t o_act = off;    off += al256((size_t)pairs * I * 4);
-    const size_t o_ah = off;     off += al256((size_t)pairs * I * 2);
-    const size_t o_aF = off;     off += al256((size_t)pairs * 4);
-    const size_t o_ey = off;     off += al256((size_t)pairs * H * 4);
-    const size_t o_sa = off;     off += al256((size_t)rows * SI * 4);
-    const size_t o_sh16 = off;   off += al256((size_t)rows * SI * 2);
-    const size_t o_sF = off;     off += al256((size_t)rows * 4);
-    const size_t o_sh = off;     off += al256((size_t)rows * H * 4);
+    const size_t o_act = off;    off += al256((size_t)ntot * I * 4);
+    const size_t o_ah = off;     off += al256((size_t)ntot * I * 2);
+    const size_t o_aF = off;     off += al256((size_t)ntot * 4);
+    const size_t o_ey = off;     off += al256((size_t)ntot * H * 4);
+    const size_t o_sa = off;     off += al256((size_t)srows * SI * 4);
+    const size_t o_sh16 = off;   off += al256((size_t)srows * SI * 2);
+    const size_t o_sF = off;     off += al256((size_t)srows * 4);
+    const size_t o_sh = off;     off += al256((size_t)srows * H * 4);
     const size_t o_g1 = off;     off += al256((size_t)rows * 4);
     const size_t o_gw = off;     off += al256(qwk_moe_group_work_bytes(pairs, E));
     char *S = scratch(off);
@@ -636,30 +643,34 @@ static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const floa
     int32_t *perm = (int32_t *)(S + o_perm), *tiles = (int32_t *)(S + o_tiles);
     hipStream_t s = G.stream;
     const long words = H / 8, groups = H / grp;
+    const qwk_gmm_extra xgu = { q4r(&M->sh_gate), q4r(&M->sh_up), E, pairs };
+    const qwk_gmm_extra xdn = { q4r(&M->sh_down), q4r(&M->sh_down), E, pairs };
     int rc = qwk_stage16(s, xh, xF, x, rows, H);
     if (!rc) rc = qwk_dmat_bf16(s, logits, x, dp(M->router), H, E, rows);
     if (!rc) rc = qwk_route(s, idx, w, logits, rows, E, K, M->norm ? 1 : 0);
     if (!rc) rc = qwk_moe_group(s, perm, tiles, idx, pairs, E, QW_PF_BM, mt, S + o_gw,
-                                qwk_moe_group_work_bytes(pairs, E));
+                                qwk_moe_group_work_bytes(pairs, E), xr);
     if (M->split) {
         if (!rc) rc = qwk_gmm16(s, act, I, xh, xF, perm, tiles, mt, q4r(&M->gate), q4r(&M->up),
-                                (long)I * words, (long)I * groups, H, I, K, 0, grp, 1, 0);
+                                (long)I * words, (long)I * groups, H, I, K, 0, grp, 1, 0, fuse ? &xgu : NULL);
     } else {
         const qwk_q4 g0 = q4r(&M->gate_up);
         const qwk_q4 u0 = { g0.w + (size_t)I * words, g0.s + (size_t)I * groups, g0.b + (size_t)I * groups };
         if (!rc) rc = qwk_gmm16(s, act, I, xh, xF, perm, tiles, mt, g0, u0,
-                                2L * I * words, 2L * I * groups, H, I, K, 0, grp, 1, 0);
+                                2L * I * words, 2L * I * groups, H, I, K, 0, grp, 1, 0, fuse ? &xgu : NULL);
     }
-    if (!rc) rc = qwk_stage16(s, ah, aF, act, pairs, I);
+    if (!rc) rc = qwk_stage16(s, ah, aF, act, ntot, I);
     if (!rc) rc = qwk_gmm16(s, ey, H, ah, aF, perm, tiles, mt, q4r(&M->down), q4r(&M->down),
-                            (long)H * (I / 8), (long)H * (I / grp), I, H, K, 1, grp, 0, 0);
-    if (!rc) rc = qwk_gmm16(s, sa, SI, xh, xF, NULL, NULL, 0, q4r(&M->sh_gate), q4r(&M->sh_up),
-                            0, 0, H, SI, 1, 0, grp, 1, rows);
-    if (!rc) rc = qwk_stage16(s, sh16, sF, sa, rows, SI);
-    if (!rc) rc = qwk_gmm16(s, sh, H, sh16, sF, NULL, NULL, 0, q4r(&M->sh_down), q4r(&M->sh_down),
-                            0, 0, SI, H, 1, 0, grp, 0, rows);
+                            (long)H * (I / 8), (long)H * (I / grp), I, H, K, 1, grp, 0, 0, fuse ? &xdn : NULL);
+    if (!fuse) {
+        if (!rc) rc = qwk_gmm16(s, sa, SI, xh, xF, NULL, NULL, 0, q4r(&M->sh_gate), q4r(&M->sh_up),
+                                0, 0, H, SI, 1, 0, grp, 1, rows, NULL);
+        if (!rc) rc = qwk_stage16(s, sh16, sF, sa, rows, SI);
+        if (!rc) rc = qwk_gmm16(s, sh, H, sh16, sF, NULL, NULL, 0, q4r(&M->sh_down), q4r(&M->sh_down),
+                                0, 0, SI, H, 1, 0, grp, 0, rows, NULL);
+    }
     if (!rc) rc = qwk_dmat_bf16(s, g1, x, dp(M->sh_gate_w), H, 1, rows);
-    if (!rc) rc = qwk_moe_combine(s, out, ey, w, sh, g1, rows, K, H);
+    if (!rc) rc = qwk_moe_combine(s, out, ey, w, fuse ? ey + (size_t)pairs * H : sh, g1, rows, K, H);
     launched(c, "moe_layer (prefill)", rc);
     return rc == 0;
 }
