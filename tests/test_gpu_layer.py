@@ -156,6 +156,19 @@ def test_config3_prefill_sample(gpu):
     lb.free()
 
 
+@pytest.mark.parametrize("split", [True, False])
+def test_prefill_shared_expert_grouped(gpu, split):
+    """SI == I: the shared expert runs in the grouped launches as one more
+    expert (its rows after the routed pairs, tiles of its own).  200 tokens
+    (four shared tiles, one partial), split and fused gate / up banks, every
+    output against the oracle."""
+    L = synth.make_layer(321, H=512, E=32, K=4, I=128, SI=128, group=64, split=split, tag="shfuse.")
+    x = synth.make_x(322, 200, L.H, name="shfuse.x")
+    lb = gpu.LayerBufs(L)
+    check(run_layer(gpu, lb, x), ref.moe_forward(L, x), 1e-3)
+    lb.free()
+
+
 @pytest.mark.parametrize("rows", [1, 3])
 def test_decode_back_to_back(gpu, c1, rows):
     """Sixteen decode launches queued in one command, each on its own tokens
