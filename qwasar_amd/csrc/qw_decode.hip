@@ -508,6 +508,13 @@ struct QdRoute {
     int ustart[QD_MAXU];
     int upair[QD_MAXU];       // pairs grouped by unique expert, ascending pair index
     int mark[QWK_ROUTE_MAX_E];// after routing: the unique-expert slot of each selected expert
+    union alignas(16) {
+        uint32_t sx[QD_MAXT][QW_ROUTE_SX];  // selection scratch of routing wave w (w < rows <= QD_MAXT)
+        struct {                            // one token, routed by the whole workgroup
+            uint32_t sx[QW_ROUTE_SX];
+            float vb[QW_ROUTE_BLOCK_LDS];
+        } one;
+    } rs;
 };
 
 // Routes every token (a wave per token) with the arithmetic of the
@@ -520,13 +527,23 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
 {
     const int t = threadIdx.x, nthr = blockDim.x, wave = t >> 6, lane = t & 63, nw = nthr >> 6;
     const int E = a.m.E, K = a.m.K;
-    for (int r = wave; r < a.rows; r += nw) {
+    if (a.rows == 1 && nw >= PL) {
         int pi;
         float pw;
-        qw_route_wave<PL, true>(a.logits + (size_t)r * E, E, K, a.m.norm, lane, &pi, &pw);
-        if (lane < K) {
-            R.picks[r * K + lane] = pi;
-            R.pw[r * K + lane] = pw;
+        qw_route_block<PL, true>(a.logits, E, K, a.m.norm, wave, lane, &pi, &pw, R.rs.one.sx, R.rs.one.vb);
+        if (wave == 0 && lane < K) {
+            R.picks[lane] = pi;
+            R.pw[lane] = pw;
+        }
+    } else {
+        for (int r = wave; r < a.rows; r += nw) {
+            int pi;
+            float pw;
+            qw_route_wave<PL, true>(a.logits + (size_t)r * E, E, K, a.m.norm, lane, &pi, &pw, R.rs.sx[wave]);
+            if (lane < K) {
+                R.picks[r * K + lane] = pi;
+                R.pw[r * K + lane] = pw;
+            }
         }
     }
     __syncthreads();

@@ -270,14 +270,18 @@ __device__ __forceinline__ int qw_wave_min_i(int v)
 
 // Wave maximum of ints (probability bits, which order as the values for
 // p >= 0, or negative sentinels below every probability).
+// The row maxima (every lane of a row) meet across rows by row_bcast:15
+// (rows 1 and 3 take lane 15 of the row before) and row_bcast:31 (rows 2
+// and 3 take lane 31): lane 63 ends with the wave's maximum, read once.
 __device__ __forceinline__ int qw_wave_max_i(int v)
 {
     v = max(v, qw_dpp_i<QW_DPP_XOR1>(v));
     v = max(v, qw_dpp_i<QW_DPP_XOR2>(v));
     v = max(v, qw_dpp_i<QW_DPP_HMIRROR>(v));
     v = max(v, qw_dpp_i<QW_DPP_MIRROR>(v));
-    return max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
-               max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false));   // row_bcast:15
+    v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xC, 0xF, false));   // row_bcast:31
+    return __builtin_amdgcn_readlane(v, 63);
 }
 
 // Device-coherent loads (cache policy sc1: served past this XCD's L2, so
@@ -314,37 +318,30 @@ __device__ __forceinline__ uint32_t qw_ldu16(const void *base, uint32_t off)
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(qw_rsrc(base), off, 0, 0);
 }
 
-// COH: the logits were written by other workgroups of the same launch and are
-// read with device-coherent loads (past this XCD's L2).
-template <int PL, bool COH = false>
-__device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E, int K, int norm,
-                                              int lane, int *pick_i, float *pick_w)
+// Phase hooks inside routing for timing probes; empty unless the includer
+// defines them.
+#ifndef QW_RSTAMP
+#define QW_RSTAMP(slot) do { } while (0)
+#endif
+
+// Words of LDS scratch the routing selection takes (8-byte aligned): 66
+// survivor keys, then QWK_ROUTE_MAX_K pick keys, 64 bits each.
+#define QW_ROUTE_SX 196
+
+// The second half of routing one token in one wave: v[j] = e^(l - max) of
+// expert lane + 64 j (0 past E), the softmax p = v / sum, and the top K by
+// p, descending, ties to the lower expert.  The sum adds a lane's v[j] in j
+// order from 0, then the lane partials by the 64-lane xor tree.
+template <int PL>
+__device__ __forceinline__ void qw_route_finish(float (&v)[PL], int E, int K, int norm, int lane,
+                                               int *pick_i, float *pick_w, uint32_t *sx)
 {
-    float v[PL];
-    float m = -__builtin_huge_valf();
-#pragma unroll
-    for (int j = 0; j < PL; j++) {
-        const int ec = min(lane + 64 * j, E - 1);
-        v[j] = COH ? qw_ldf_coh(l, (uint32_t)ec * 4u) : l[ec];
-    }
-    // every load issued before the first is used (one memory round trip)
-#pragma unroll
-    for (int j = 0; j < PL; j++) asm volatile("" : "+v"(v[j]));
-#pragma unroll
-    for (int j = 0; j < PL; j++) {
-        v[j] = lane + 64 * j < E ? v[j] : -__builtin_huge_valf();
-        m = fmaxf(m, v[j]);
-    }
-    m = qw_wave_max(m);
-    QW_STAMP(6);
     float s = 0.0f;
 #pragma unroll
-    for (int j = 0; j < PL; j++) {
-        const float ex = qw_exp_spec(v[j] - m);
-        v[j] = lane + 64 * j < E ? ex : 0.0f;
-        s = s + v[j];
-    }
+    for (int j = 0; j < PL; j++) s = s + v[j];
+    QW_RSTAMP(2);
     s = qw_xor_sum<64>(s);
+    QW_RSTAMP(3);
     // p = v / s, correctly rounded: with y = 1/s correctly rounded and
     // q = v*y, q + (v - s q) y rounds to v/s (Markstein) for results in the
     // normal range; s >= 1 (the largest term is e^0), so only v below 2^-100
@@ -364,11 +361,77 @@ __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E
         for (int j = 0; j < PL; j++)
             if (lane + 64 * j < E) pb[j] = __float_as_int(v[j] / s);
     }
+    QW_STAMP(7);
+    QW_RSTAMP(4);
+    // Selection.  The order: bits(p) descending (p >= 0, so the bits order as
+    // the values), then e ascending.  tau, at most the K-th largest of the 64
+    // lane maxima, bounds the K-th largest p from below (K lanes hold a value
+    // >= tau), so every pick has p >= tau.  The survivors (p >= tau; about K
+    // for softmax outputs) go to LDS as keys bits(p) << 32 | (0xFFFF - e),
+    // larger = earlier; each lane ranks its survivor against all of them, and
+    // ranks below K are the picks in order.  With more than 64 survivors
+    // (heavy ties) a K-round tournament picks instead; both give the order
+    // above exactly.
+    {
+        int mx = -1;
+#pragma unroll
+        for (int j = 0; j < PL; j++)
+            if (lane + 64 * j < E) mx = max(mx, pb[j]);
+        // Two bits a step.  p <= 1 leaves bit 30 clear; the bits below 16 are
+        // left at zero, which lowers tau by under 2^-7 relative and only adds
+        // survivors.
+        uint32_t pref = 0;
+#pragma unroll
+        for (int b = 28; b >= 16; b -= 2) {
+            const uint32_t c1 = pref | (1u << b), c2 = pref | (2u << b), c3 = pref | (3u << b);
+            const int n1 = __popcll(__ballot(mx >= (int)c1));
+            const int n2 = __popcll(__ballot(mx >= (int)c2));
+            const int n3 = __popcll(__ballot(mx >= (int)c3));
+            pref = n3 >= K ? c3 : n2 >= K ? c2 : n1 >= K ? c1 : pref;
+        }
+        const int tau = (int)pref;
+        QW_RSTAMP(5);
+        // survivors to keys[0 .. C) in slot order (a position past 63 goes
+        // to the sink keys[64]; C > 64 takes the tournament below)
+        uint64_t *keys = reinterpret_cast<uint64_t *>(sx);  // [66]: 64 is a sink
+        uint64_t *picks = keys + 66;                         // [QWK_ROUTE_MAX_K]
+        const unsigned long long below = (1ull << lane) - 1ull;
+        int C = 0;
+#pragma unroll
+        for (int j = 0; j < PL; j++) {
+            const bool on = lane + 64 * j < E && pb[j] >= tau;
+            const unsigned long long sm = __ballot(on);
+            const int pos = on ? min(C + (int)__popcll(sm & below), 64) : 64;
+            keys[pos] = ((uint64_t)(uint32_t)pb[j] << 32) | (uint32_t)(0xFFFF - (lane + 64 * j));
+            C += __popcll(sm);
+        }
+        if (C <= 64) {
+            __builtin_amdgcn_wave_barrier();
+            const uint64_t mk = lane < C ? keys[lane] : 0;
+            QW_RSTAMP(6);
+            int rank = 0;
+            // four keys a step; those past C (at most keys[66], inside sx) do not count
+            for (int q = 0; q < C; q += 4)
+                rank += (keys[q] > mk) + (q + 1 < C && keys[q + 1] > mk) + (q + 2 < C && keys[q + 2] > mk) +
+                        (q + 3 < C && keys[q + 3] > mk);
+            QW_RSTAMP(7);
+            if (lane < C && rank < K) picks[rank] = mk;
+            __builtin_amdgcn_wave_barrier();
+            // the renormalising sum adds the picks in pick order
+            float wsum = 0.0f;
+            for (int n = 0; n < K; n++) wsum = wsum + __uint_as_float((uint32_t)(picks[n] >> 32));
+            const uint64_t pk = lane < K ? picks[lane] : 0;
+            const float mw = __uint_as_float((uint32_t)(pk >> 32));
+            *pick_i = lane < K ? 0xFFFF - (int)(uint32_t)pk : 0;
+            *pick_w = norm ? mw / wsum : mw;
+            QW_RSTAMP(8);
+            return;
+        }
+    }
     // A lane's slots in groups of four, each group sorted once by the key
     // (bits(p) + 2) << 2 | (3 - slot % 4): p < 2 has bits below 2^30, so the
     // key orders by p and then by the lower slot.  A slot past E has key < 4,
     // an emptied one 0, both below every probability (keys >= 8).
-    QW_STAMP(7);
     constexpr int NG = PL / 4;
     uint32_t g[NG][4];
 #pragma unroll
@@ -425,4 +488,81 @@ __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E
     }
     *pick_i = mine_i;
     *pick_w = norm ? mine_w / wsum : mine_w;
+}
+
+// COH: the logits were written by other workgroups of the same launch and are
+// read with device-coherent loads (past this XCD's L2).
+
+// Routes one token in one wave: lane l holds experts l + 64 j, j < PL.
+template <int PL, bool COH = false>
+__device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E, int K, int norm,
+                                              int lane, int *pick_i, float *pick_w, uint32_t *sx)
+{
+    float v[PL];
+    float m = -__builtin_huge_valf();
+#pragma unroll
+    for (int j = 0; j < PL; j++) {
+        const int ec = min(lane + 64 * j, E - 1);
+        v[j] = COH ? qw_ldf_coh(l, (uint32_t)ec * 4u) : l[ec];
+    }
+    // every load issued before the first is used (one memory round trip)
+#pragma unroll
+    for (int j = 0; j < PL; j++) asm volatile("" : "+v"(v[j]));
+#pragma unroll
+    for (int j = 0; j < PL; j++) {
+        v[j] = lane + 64 * j < E ? v[j] : -__builtin_huge_valf();
+        m = fmaxf(m, v[j]);
+    }
+    QW_RSTAMP(0);
+    m = qw_wave_max(m);
+    QW_STAMP(6);
+    QW_RSTAMP(1);
+#pragma unroll
+    for (int j = 0; j < PL; j++) {
+        const float ex = qw_exp_spec(v[j] - m);
+        v[j] = lane + 64 * j < E ? ex : 0.0f;
+    }
+    qw_route_finish<PL>(v, E, K, norm, lane, pick_i, pick_w, sx);
+}
+
+// Words of LDS qw_route_block takes besides the selection scratch.
+#define QW_ROUTE_BLOCK_LDS (QWK_ROUTE_MAX_E + 16)
+
+// Routes one token with a whole workgroup of at least PL waves (every
+// thread calls it; it holds __syncthreads): wave j takes the exponentials of
+// experts 64 j .. 64 j + 63, and wave 0 sums and selects exactly as
+// qw_route_wave does, so the picks and weights are the same bits.  The
+// results land in wave 0's lanes (lane n < K: pick n).
+template <int PL, bool COH = false>
+__device__ __forceinline__ void qw_route_block(const float *__restrict__ l, int E, int K, int norm, int wave,
+                                               int lane, int *pick_i, float *pick_w, uint32_t *sx,
+                                               float *vb)
+{
+    float *wm = vb + QWK_ROUTE_MAX_E;
+    const int e = lane + 64 * wave;
+    const bool on = wave < PL && e < E;
+    float x = -__builtin_huge_valf();
+    if (wave < PL) {
+        const int ec = min(e, E - 1);
+        x = COH ? qw_ldf_coh(l, (uint32_t)ec * 4u) : l[ec];
+        x = on ? x : -__builtin_huge_valf();
+        const float mw = qw_wave_max(x);
+        if (lane == 0) wm[wave] = mw;
+    }
+    __syncthreads();
+    if (wave < PL) {
+        float m = wm[0];
+#pragma unroll
+        for (int j = 1; j < PL; j++) m = fmaxf(m, wm[j]);
+        QW_STAMP(6);
+        const float ex = qw_exp_spec(x - m);
+        vb[e] = on ? ex : 0.0f;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float v[PL];
+#pragma unroll
+        for (int j = 0; j < PL; j++) v[j] = vb[lane + 64 * j];
+        qw_route_finish<PL>(v, E, K, norm, lane, pick_i, pick_w, sx);
+    }
 }

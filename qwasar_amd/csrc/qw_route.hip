@@ -247,13 +247,14 @@ __global__ __launch_bounds__(64) void k_route(int *__restrict__ idx, float *__re
                                               const float *__restrict__ logits, int rows,
                                               int E, int K, int norm)
 {
+    __shared__ __align__(16) uint32_t sx[QW_ROUTE_SX];
     const int r = blockIdx.x, lane = threadIdx.x;
     int pi;
     float pw;
     const float *l = logits + (size_t)r * E;
-    if (E <= 256) qw_route_wave<4>(l, E, K, norm, lane, &pi, &pw);
-    else if (E <= 512) qw_route_wave<8>(l, E, K, norm, lane, &pi, &pw);
-    else qw_route_wave<16>(l, E, K, norm, lane, &pi, &pw);
+    if (E <= 256) qw_route_wave<4>(l, E, K, norm, lane, &pi, &pw, sx);
+    else if (E <= 512) qw_route_wave<8>(l, E, K, norm, lane, &pi, &pw, sx);
+    else qw_route_wave<16>(l, E, K, norm, lane, &pi, &pw, sx);
     if (lane < K) { idx[(size_t)r * K + lane] = pi; w[(size_t)r * K + lane] = pw; }
 }
 

@@ -71,6 +71,41 @@ def test_route_bit_exact(gpu, E, K, rows):
         assert list(got_i[2, :4]) == [5, 69, 131, 133][:K]
 
 
+@pytest.mark.parametrize("E,K", [(512, 10), (256, 32), (128, 8), (1000, 4)])
+def test_route_selection_edges(gpu, E, K):
+    """Rows whose candidate set (p at or above the K-th largest lane maximum)
+    is exactly 64, 65 or all experts, ties inside one lane's slots, and
+    probabilities that underflow to zero: every row bit-exact to the oracle."""
+    rows = 8
+    g = np.random.default_rng(E * 100 + K)
+    lg = (g.standard_normal((rows, E)) * 3.0).astype(np.float32)
+    top = np.float32(20.0)
+    lg[0, g.choice(E, 64, replace=False)] = top           # 64 tied maxima
+    lg[1, g.choice(E, 65, replace=False)] = top           # 65: more than a wave
+    lg[2] *= 100.0                                        # most p round to zero
+    lg[3, :] = -1.0e4
+    lg[3, E - 1] = 0.0                                    # one p = 1, the rest 0
+    lg[4, g.choice(E, 40, replace=False)] = top
+    lg[4, 3] = top + 1.0                                  # one above forty ties
+    lane = [l for l in range(3, E, 64)]                   # one lane's slots
+    lg[5, lane] = top
+    lg[5, [1, 2]] = top                                   # and two other lanes
+    lg[6, :] = 0.0                                        # all equal
+    B = gpu.Buf
+    lgb, ib, wb = B.of(lg), B(rows * K * 4), B(rows * K * 4)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_op_moe_route(c, ib.ref(), wb.ref(), lgb.ref(), rows, E, K, True)
+    gpu.run(c, "moe_route edges")
+    idx, w = ref.route(lg, rows, E, K, norm=True)
+    got_i = ib.read(np.int32, (rows, K))
+    got_w = wb.read(np.float32, (rows, K))
+    for r in range(rows):
+        assert np.array_equal(got_i[r], idx[r]), f"row {r}: ids differ from the oracle"
+        assert np.array_equal(got_w[r].view(np.uint32), w[r].view(np.uint32)), f"row {r}: weights not bit-exact"
+    assert list(got_i[6]) == list(range(K))
+    assert got_i[3, 0] == E - 1
+
+
 def test_route_refuses_oversize(gpu, capfd):
     B = gpu.Buf
     lg, ib, wb = B(4 * 2048), B(4 * 40), B(4 * 40)
