@@ -16,11 +16,14 @@ reads its routed experts from HBM, not from the 256 MB Infinity Cache.
 Also reported: the decode launch's own duration, HBM bandwidth on the routed
 ("selected-expert") bytes and on all bytes, config 3 (512-token prefill with
 Zipf-skewed routing) and a 2048-token prefill chunk (config 4's per-layer
-step) in tokens/s and bf16-MFMA utilisation, and the CPU oracle's time on a
-bounded sample of the same decode workload (single-threaded scalar C, the
-reference's own CPU path restated; see oracle/).
+step) in tokens/s and bf16-MFMA utilisation; config 4, 48 such layers
+(~65 GB of weights written on the device) joined by the residual bf16 RMS
+norm, through one 2048-token prefill and 256 decode steps; and the CPU
+oracle's time on a bounded sample of the same decode workload
+(single-threaded scalar C, the reference's own CPU path restated; see
+oracle/).
 
-    python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-config4] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -159,6 +162,81 @@ def time_prefill(gpu, lb, x, reps):
     return ms, int(counts.max()), int((counts > 0).sum())
 
 
+def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444):
+    """`nlayers` layers of config 1's shape (weights written
+    on the device), joined by the residual bf16 RMS norm; one `rows`-token
+    prefill, then `steps` decode steps, each fed a fresh N(0, 1) token."""
+    from qwasar_amd import stack, synth
+    cfg = dict(synth.CONFIGS[1])
+    shape = {k: cfg[k] for k in ("H", "E", "K", "I", "SI", "group")}
+    H = shape["H"]
+    layers = [stack.DeviceLayer(seed, l, **shape) for l in range(nlayers)]
+    st = stack.Stack(layers, rows)
+    labels = [f"stack prefill L{l}".encode() for l in range(nlayers)]   # alive until the profile is read
+
+    def fresh_h(c, n, name):
+        gpu.qw_op_synth(c, st.h.ref(), synth.SYNTH_BF16_NORMAL, n * H, synth.sm_key(seed, name), 1.0, 0.0)
+
+    # prefill: one untimed pass, then the timed one, a mark after each layer
+    c = gpu.qw_cmd_begin()
+    fresh_h(c, rows, "h0.warm")
+    st.encode(c, rows)
+    gpu.run(c, "stack prefill warm-up")
+    c = gpu.qw_cmd_begin()
+    fresh_h(c, rows, "h0")
+    gpu.qw_op_residual_rms_norm_bf16(c, st.h.ref(), st.x.ref(), gpu.NULL_REF, H, rows, stack.EPS)
+    gpu.qw_prof_reset()
+    gpu.qw_prof_set_enabled(True)
+    gpu.qw_cmd_mark(c, b"stack prefill start")
+    for l in range(nlayers):
+        gpu.qw_prof_set_enabled(False)
+        st.encode(c, rows, first=l, count=1, start=False)
+        gpu.qw_prof_set_enabled(True)
+        gpu.qw_cmd_mark(c, labels[l])
+    gpu.run(c, "stack prefill")
+    per_layer = np.array([gpu.qw_prof_ms(labels[l], None) for l in range(nlayers)])
+    gpu.qw_prof_set_enabled(False)
+    gpu.qw_prof_reset()
+    pf_ms = float(per_layer.sum())
+
+    # decode
+    c = gpu.qw_cmd_begin()
+    for s in range(warmup):
+        fresh_h(c, 1, f"dec.warm{s}")
+        st.encode(c, 1)
+    gpu.run(c, "stack decode warm-up")
+    gpu.qw_prof_reset()
+    gpu.qw_prof_set_enabled(True)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_prof_set_enabled(False)
+    for s in range(steps):
+        fresh_h(c, 1, f"dec{s}")
+        st.encode(c, 1)
+    gpu.qw_prof_set_enabled(True)
+    gpu.qw_cmd_mark(c, b"stack decode region")
+    gpu.run(c, "stack decode")
+    dec_ms = gpu.qw_prof_ms(b"stack decode region", None)
+    gpu.qw_prof_set_enabled(False)
+    gpu.qw_prof_reset()
+    wbytes = sum(L.weight_bytes() for L in layers)
+    st.free()
+    for L in layers:
+        L.free()
+    us_tok = dec_ms * 1000.0 / steps
+    us_tl = us_tok / nlayers
+    routed = decode_bytes(cfg)["routed"]
+    fl = prefill_flops(cfg, rows) * nlayers
+    return {"layers": nlayers, "weights_gb": round(wbytes / 1e9, 2),
+            "prefill": {"rows": rows, "ms": round(pf_ms, 3), "tokens_per_s": round(rows / (pf_ms * 1e-3), 1),
+                        "ms_per_layer_median": round(float(np.median(per_layer)), 3),
+                        "ms_per_layer_max": round(float(per_layer.max()), 3),
+                        "mfma_util": round(fl / (pf_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
+            "decode": {"steps": steps, "us_per_token": round(us_tok, 2), "us_per_token_layer": round(us_tl, 3),
+                       "routed_hbm_frac": round(routed / (us_tl * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+            "includes": "per layer: the MoE block and the residual bf16 RMS norm; decode steps include "
+                        "writing the fresh token on the device"}
+
+
 def cpu_baseline(L, xpool, seconds):
     """The oracle (the reference's scalar moe_step restated in C, one thread)
     on the same decode tokens, for a bounded time."""
@@ -190,6 +268,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-config4", action="store_true", help="skip the 48-layer stack (config 4)")
+    ap.add_argument("--config4-only", action="store_true", help="run only the 48-layer stack and print it")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calib-copy", type=int, default=0, help="bytes: run only the copy calibration")
     ap.add_argument("--decode-only-steps", type=int, default=0,
@@ -214,6 +294,9 @@ def main():
     cand = synth.make_x(seed, 2048, L.H, name="bench.candidates")
     xpool, pool_ids = select_cold_pool(gpu, lb, cand, L.K)
 
+    if args.config4_only:
+        print(json.dumps({"config4": bench_stack(gpu, 48, 2048, 256, 4)}), flush=True)
+        return
     if args.decode_only_steps:
         time_decode(gpu, lb, xpool, args.decode_only_steps, 0, False)
         return
@@ -286,6 +369,9 @@ def main():
                         "weight_read_floor_ms": round(L.weight_bytes() / HBM_PEAK_GBS / 1e6, 3),
                         "hottest_expert_pairs": hot, "experts_touched": touched}
         out["prefill"] = pf
+
+    if not args.no_config4:
+        out["config4"] = bench_stack(gpu, 48, 2048, 256, 4)
 
     if not args.no_cpu:
         us, n = cpu_baseline(L, xpool, args.cpu_seconds)

@@ -125,6 +125,14 @@ void qw_op_qmvb_q4(qw_cmd c, qw_ref y, qw_ref x,
 void qw_op_dmat_bf16(qw_cmd c, qw_ref y, qw_ref x, qw_ref w,
                      int32_t k, int32_t n, int32_t rows);
 
+/* ---- normalisation (reference qwasar_gpu.h:269-276) ------------------------- */
+
+/* RMS norm over the last axis of an [rows, dim] fp32 buffer; `weight` (bf16
+ * [dim]) may be a null ref; `out_scale` applies after normalising, before the
+ * weight.  dim % 4 == 0 here. */
+void qw_op_rms_norm(qw_cmd c, qw_ref y, qw_ref x, qw_ref weight,
+                    int32_t dim, int32_t rows, float eps, float out_scale);
+
 /* ---- elementwise (reference qwasar_gpu.h:316-317, :384) --------------------- */
 
 void qw_op_swiglu(qw_cmd c, qw_ref y, qw_ref gate, qw_ref up, int32_t n);
@@ -175,6 +183,23 @@ void qw_op_moe_combine(qw_cmd c, qw_ref out, qw_ref y, qw_ref w, int32_t rows, i
 void qw_op_scale_rows_sigmoid(qw_cmd c, qw_ref y, qw_ref g, int32_t rows, int32_t dim);
 
 /* ---- additions without a reference counterpart ------------------------------ */
+
+/* The residual step between the layers of a MoE stack:
+ * h BF16 [rows, dim] <- bf16(h + y) (h kept when y is a null ref), then
+ * x F32 [rows, dim] = rms_norm(h), unit weight -- the reference's
+ * qw_op_add_inplace and qw_op_rms_norm with the bf16 carry between them,
+ * in one pass. */
+void qw_op_residual_rms_norm_bf16(qw_cmd c, qw_ref h, qw_ref x, qw_ref y,
+                                  int32_t dim, int32_t rows, float eps);
+
+/* Seeded synthetic data written on the device, for benchmarks and tests:
+ * n elements of `kind` from the counter-based SplitMix64 stream `key`.
+ *   0  u32 words (4-bit nibbles: the high 32 bits of each output)
+ *   1  bf16 uniform in [a, b)
+ *   2  bf16 of -8 * (kind 1's value for the same key, a, b): MLX biases
+ *   3  bf16 N(0, a) by Box-Muller
+ *   4  kind 3's value stored as fp32 */
+void qw_op_synth(qw_cmd c, qw_ref dst, int32_t kind, int64_t n, uint64_t key, float a, float b);
 
 /* The tile height the grouping and the grouped product agree on for a
  * given (pairs, E): 16, 32 or 64 rows. */

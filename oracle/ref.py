@@ -87,6 +87,7 @@ def reflib():
         R.qw_cpu_swiglu.argtypes = [_P, _P, _P, _I]
         R.qw_bf16_to_f32_c.restype = C.c_float
         R.qw_bf16_to_f32_c.argtypes = [C.c_uint16]
+        R.qw_cpu_rms_norm.argtypes = [_P, _P, _P, _I, _I, C.c_float, C.c_float]
         _ref = R
     return _ref
 
@@ -156,3 +157,45 @@ def moe_forward(layer, x, rows=None):
     w = np.zeros((rows, L.K), np.float32)
     lib().qr_moe_forward(_ptr(out), _ptr(idx), _ptr(w), _ptr(x), rows, C.byref(m))
     return out, idx, w
+
+
+# ---- the layer stack -------------------------------------
+
+STACK_EPS = 1e-6
+
+
+def rms_norm(x: np.ndarray, eps: float = STACK_EPS) -> np.ndarray:
+    """Unit-weight RMS norm of fp32 rows, qwasar_cpu.c:68-82's form."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().qr_rms_norm(_ptr(y), _ptr(x), x.shape[-1], x.size // x.shape[-1], eps)
+    return y
+
+
+def _bf16(a: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def residual_norm(h: np.ndarray, y=None, eps: float = STACK_EPS):
+    """(h', x): h' = bf16(h + y) (h when y is None), x = rms_norm(h').
+    h, h' are bf16 bits (uint16), y and x fp32."""
+    if y is not None:
+        h = _bf16(_f32(h) + np.asarray(y, np.float32))
+    return h, rms_norm(_f32(h), eps)
+
+
+def stack_forward(layers, h0: np.ndarray, eps: float = STACK_EPS):
+    """The stack on the CPU: x = norm(h); per layer y = MoE(x), h = bf16(h + y),
+    x = norm(h).  Returns the final h (bf16 bits) and each layer's (x, y)."""
+    h, x = residual_norm(h0, None, eps)
+    trace = []
+    for L in layers:
+        y, _, _ = moe_forward(L, x)
+        trace.append((x, y))
+        h, x = residual_norm(h, y, eps)
+    return h, trace

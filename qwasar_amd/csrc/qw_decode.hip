@@ -4,11 +4,11 @@
 //
 //   router   one wave per router row (E rows, plus the shared expert's gate
 //            vector): the order-R logits of every token
-//   shared   the shared expert's gate / up rows and SwiGLU (needs only x)
 //   experts  per (selected expert, 16-row block): route every token, then
 //            the gate / up rows of that expert for every token routed to it
 //            -- each weight byte read once; SwiGLU fused; the activations
 //            leave staged as q16 units
+//   shared   the shared expert's gate / up rows and SwiGLU (needs only x)
 //   down     per (token, block of output rows): route, load the down rows of
 //            the shared expert and of each of the token's K experts into
 //            registers; each matrix's wave waits for that matrix's
@@ -25,7 +25,14 @@
 //
 // Progress: a workgroup only waits on workgroups with smaller block indices,
 // which the dispatcher has already placed (workgroups are dispatched in index
-// order), so every wait ends.  Each wait is also bounded: past a spin limit
+// order), so every wait ends.
+//
+// Placement: two workgroups share a CU, and of two that fetch weights at
+// once the later-dispatched one waits a memory round trip longer (measured:
+// the last 64 experts workgroups reached their first dot ~1.7 us after the
+// rest).  The shared expert (done long before the down rows need it) sits
+// after the experts, so the latest-dispatched fetchers are the ones with
+// slack.  Each wait is also bounded: past a spin limit
 // it raises the error word, every later wait gives up at once, and the host
 // reports the error; no wave is left spinning.
 //
@@ -49,8 +56,17 @@ extern "C" int qd_trace_read(unsigned long long *dst)
 {
     return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(qd_trace), sizeof(qd_trace));
 }
+// and where it ran: HW_ID (CU, SH, SE in bits 8..15) and XCC_ID << 24
+__device__ unsigned int qd_hwid[8192];
+#define QD_HWID() do { if (threadIdx.x == 0) qd_hwid[blockIdx.x] = \
+    (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 4) | ((unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 24); } while (0)
+extern "C" int qd_hwid_read(unsigned int *dst)
+{
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(qd_hwid), sizeof(qd_hwid));
+}
 #else
 #define QD_TS(slot) do { } while (0)
+#define QD_HWID() do { } while (0)
 #endif
 
 #define QD_MAXT QWK_DECODE_MAX_ROWS
@@ -837,12 +853,18 @@ __global__ __launch_bounds__(QD_THREADS, 8) void k_decode_fused(QdArgs a)
     static_assert(QD_MAXT * QD_GU_MAXRPB >= (QWK_DECODE_MAX_K + 1) * QD_DOWN_RPG, "down shares ys");
     constexpr int RPB = QD_WAVES * (64 / LPR);
     QD_TS(0);
+    QD_HWID();
     int b = blockIdx.x;
     if (b < a.n_rt) {
         qd_role_router(a, b, reinterpret_cast<float *>(xs));
         return;
     }
     b -= a.n_rt;
+    if (b < a.n_ex) {
+        qd_role_experts<LPR, NUL, PL>(a, b, xs, R, vin, vout, ys);
+        return;
+    }
+    b -= a.n_ex;
     if (b < a.n_sh) {
         // All token rows fit one LDS pass: stage them here, no wait.
         // Otherwise copy them, pass by pass, from the router role's staging.
@@ -859,11 +881,6 @@ __global__ __launch_bounds__(QD_THREADS, 8) void k_decode_fused(QdArgs a)
         return;
     }
     b -= a.n_sh;
-    if (b < a.n_ex) {
-        qd_role_experts<LPR, NUL, PL>(a, b, xs, R, vin, vout, ys);
-        return;
-    }
-    b -= a.n_ex;
     qd_role_down<NULD, PL>(a, b, R, xs, reinterpret_cast<float (*)[QD_DOWN_RPG]>(&ys[0][0]), &dready);
 }
 

@@ -122,6 +122,23 @@ int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const floa
                    const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes,
                    void *sync, uint32_t epoch, hipEvent_t *ev);
 
+/* RMS norm of [rows, dim] fp32 rows (dim % 4 == 0), optional bf16 weight:
+ * y = x / sqrt(mean(x^2) + eps) * out_scale (* w). */
+int qwk_rms_norm(hipStream_t s, float *y, const float *x, const uint16_t *w, int dim, int rows,
+                 float eps, float out_scale);
+/* The residual step between stacked layers: h bf16 [rows, dim] <- bf16(h + y)
+ * (h unchanged when y is NULL), then x = rms_norm(h) in fp32, unit weight. */
+int qwk_resid_rms_bf16(hipStream_t s, uint16_t *h, float *x, const float *y, int dim, int rows, float eps);
+
+/* Seeded synthetic tensors (counter-based SplitMix64; value i of key k is
+ * the i-th output of SplitMix64 seeded with k). */
+#define QWK_SYNTH_U32 0             /* u32 words: the high half of each output */
+#define QWK_SYNTH_BF16_UNIFORM 1    /* bf16 of a + (b - a) u, u a 53-bit uniform */
+#define QWK_SYNTH_BF16_NEG8 2       /* bf16 of -8 times kind 1's value for the same key */
+#define QWK_SYNTH_BF16_NORMAL 3     /* bf16 of N(0, a), Box-Muller on outputs 2i, 2i+1 */
+#define QWK_SYNTH_F32_BF16_NORMAL 4 /* kind 3's value, stored as fp32 */
+int qwk_synth(hipStream_t s, void *dst, int kind, int64_t n, uint64_t key, float a, float b);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,7 +42,7 @@ struct qw_buf_s {
     void *host;
     void *dev;
     size_t len;
-    int owns_host;   /* host mirror allocated here (pinned) */
+    int owns_host;   /* host mirror allocated here (pinned, at the first qw_buf_contents) */
     int host_stale;  /* device holds newer data */
     int dev_stale;   /* host mirror may hold newer data */
     int exposed;     /* qw_buf_contents was called (or the memory is the caller's) */
@@ -177,12 +177,8 @@ qw_buf qw_buf_alloc(size_t len) {
     if (!b) return NULL;
     const size_t n = len ? len : 1;
     if (hipMalloc(&b->dev, n) != hipSuccess) { free(b); return NULL; }
-    if (hipHostMalloc(&b->host, n, hipHostMallocDefault) != hipSuccess) {
-        hipFree(b->dev);
-        free(b);
-        return NULL;
-    }
-    memset(b->host, 0, n);
+    /* The pinned mirror waits for the first qw_buf_contents, so buffers the
+     * host never reads (weights filled on the device) cost no host memory. */
     hipMemsetAsync(b->dev, 0, n, G.stream);
     hipStreamSynchronize(G.stream);
     b->len = len;
@@ -213,12 +209,17 @@ void qw_buf_free(qw_buf b) {
             if (c->written[i] == b) c->written[i] = c->written[--c->nwritten];
     hipStreamSynchronize(G.stream);
     hipFree(b->dev);
-    if (b->owns_host) hipHostFree(b->host);
+    if (b->owns_host && b->host) hipHostFree(b->host);
     free(b);
 }
 
 void *qw_buf_contents(qw_buf b) {
     if (!b) return NULL;
+    if (!b->host) {
+        const size_t n = b->len ? b->len : 1;
+        if (hipHostMalloc(&b->host, n, hipHostMallocDefault) != hipSuccess) { b->host = NULL; return NULL; }
+        if (!b->host_stale) memset(b->host, 0, n);   /* nothing has written the device copy */
+    }
     if (b->host_stale) {
         hipStreamSynchronize(G.stream);
         hipMemcpy(b->host, b->dev, b->len, hipMemcpyDeviceToHost);
@@ -453,6 +454,25 @@ void qw_op_add_inplace(qw_cmd c, qw_ref y, qw_ref x, int32_t n) {
     QW_OP(c);
     touch(c, x, 0); touch(c, y, 1);
     launched(c, "add_inplace", qwk_add_inplace(G.stream, dp(y), dp(x), n));
+}
+
+void qw_op_rms_norm(qw_cmd c, qw_ref y, qw_ref x, qw_ref weight,
+                    int32_t dim, int32_t rows, float eps, float out_scale) {
+    QW_OP(c);
+    touch(c, x, 0); touch(c, weight, 0); touch(c, y, 1);
+    launched(c, "rms_norm", qwk_rms_norm(G.stream, dp(y), dp(x), dp(weight), dim, rows, eps, out_scale));
+}
+
+void qw_op_residual_rms_norm_bf16(qw_cmd c, qw_ref h, qw_ref x, qw_ref y, int32_t dim, int32_t rows, float eps) {
+    QW_OP(c);
+    touch(c, y, 0); touch(c, h, 1); touch(c, x, 1);
+    launched(c, "residual_rms_norm_bf16", qwk_resid_rms_bf16(G.stream, dp(h), dp(x), dp(y), dim, rows, eps));
+}
+
+void qw_op_synth(qw_cmd c, qw_ref dst, int32_t kind, int64_t n, uint64_t key, float a, float b) {
+    QW_OP(c);
+    touch(c, dst, 1);
+    launched(c, "synth", qwk_synth(G.stream, dp(dst), kind, n, key, a, b));
 }
 
 void qw_op_moe_combine_shared(qw_cmd c, qw_ref out, qw_ref y, qw_ref w, qw_ref sh, qw_ref g,

@@ -213,3 +213,45 @@ def make_config(cfg: int, seed: int = 1234, split: bool = True, rows: Optional[i
     layer = make_layer(seed, split=split, logit_bias=bias, tag=tag, **c)
     x = make_x(seed, rows, c["H"], name=f"{tag}x", const_col0=const0)
     return layer, x
+
+
+# ---- device-generated tensors (the layer stack) ---------------------------------
+#
+# The stack's weights (config 4: 48 layers, ~65 GB) are written on the device
+# by qw_op_synth; these functions restate its arithmetic on the host so tests
+# can check the device's output element by element.  Value i of the stream
+# keyed k is the i-th output of SplitMix64 seeded with k.
+
+SM_GOLDEN = 0x9E3779B97F4A7C15
+SYNTH_U32, SYNTH_BF16_UNIFORM, SYNTH_BF16_NEG8, SYNTH_BF16_NORMAL, SYNTH_F32_BF16_NORMAL = range(5)
+
+
+def sm_key(seed: int, name: str) -> int:
+    h = hashlib.sha256(f"sm:{seed}:{name}".encode()).digest()
+    return int.from_bytes(h[:8], "little")
+
+
+def sm_raw(key: int, n: int, start: int = 0) -> np.ndarray:
+    """Outputs start .. start+n-1 of SplitMix64 seeded with `key` (uint64)."""
+    with np.errstate(over="ignore"):
+        i = np.arange(start + 1, start + n + 1, dtype=np.uint64)
+        z = np.uint64(key) + i * np.uint64(SM_GOLDEN)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def sm_values(kind: int, n: int, key: int, a: float = 0.0, b: float = 0.0) -> np.ndarray:
+    """The host restatement of qw_op_synth's output."""
+    if kind == SYNTH_U32:
+        return (sm_raw(key, n) >> np.uint64(32)).astype(np.uint32)
+    fa, fb = np.float64(np.float32(a)), np.float64(np.float32(b))
+    if kind in (SYNTH_BF16_UNIFORM, SYNTH_BF16_NEG8):
+        u = (sm_raw(key, n) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+        s = to_bf16((fa + (fb - fa) * u).astype(np.float32))
+        return s if kind == SYNTH_BF16_UNIFORM else to_bf16(np.float32(-8.0) * bf16_to_f32(s))
+    r = sm_raw(key, 2 * n).reshape(n, 2)
+    u1 = ((r[:, 0] >> np.uint64(11)).astype(np.float64) + 1.0) * (1.0 / 9007199254740992.0)
+    u2 = (r[:, 1] >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+    v = (fa * np.sqrt(-2.0 * np.log(u1)) * np.cos(6.283185307179586 * u2)).astype(np.float32)
+    return to_bf16(v) if kind == SYNTH_BF16_NORMAL else bf16_to_f32(to_bf16(v))
