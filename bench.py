@@ -203,7 +203,7 @@ def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444):
     c = gpu.qw_cmd_begin()
     for s in range(warmup):
         fresh_h(c, 1, f"dec.warm{s}")
-        st.encode(c, 1)
+        st.encode_fused(c, 1)
     gpu.run(c, "stack decode warm-up")
     gpu.qw_prof_reset()
     gpu.qw_prof_set_enabled(True)
@@ -211,7 +211,7 @@ def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444):
     gpu.qw_prof_set_enabled(False)
     for s in range(steps):
         fresh_h(c, 1, f"dec{s}")
-        st.encode(c, 1)
+        st.encode_fused(c, 1)
     gpu.qw_prof_set_enabled(True)
     gpu.qw_cmd_mark(c, b"stack decode region")
     gpu.run(c, "stack decode")
@@ -233,8 +233,9 @@ def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444):
                         "mfma_util": round(fl / (pf_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
             "decode": {"steps": steps, "us_per_token": round(us_tok, 2), "us_per_token_layer": round(us_tl, 3),
                        "routed_hbm_frac": round(routed / (us_tl * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
-            "includes": "per layer: the MoE block and the residual bf16 RMS norm; decode steps include "
-                        "writing the fresh token on the device"}
+            "includes": "per layer: the MoE block and the residual bf16 RMS norm (at decode folded into "
+                        "the layer's one launch, qw_op_moe_layer_residual); decode steps include writing the "
+                        "fresh token on the device and the closing residual step"}
 
 
 def cpu_baseline(L, xpool, seconds):

@@ -230,6 +230,15 @@ typedef struct {
 bool qw_op_moe_layer(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,
                      const qw_moe_layer *M, int32_t rows);
 
+/* One layer of a stack whose layers are joined by the residual bf16 RMS norm
+ * (qw_op_residual_rms_norm_bf16), with that step folded in:
+ * h_out = bf16(h + y_prev) (h when y_prev is a null ref), x_out =
+ * rms_norm(h_out) (unit weight), then out = MoE(x_out) as qw_op_moe_layer.  At decode sizes
+ * the step runs inside the layer's one launch.  h_out must be a buffer other
+ * than h and y_prev.  False (nothing encoded) where qw_op_moe_layer refuses. */
+bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref h, qw_ref y_prev,
+                              qw_ref h_out, qw_ref x_out, const qw_moe_layer *M, int32_t rows, float eps);
+
 /* Profiling for harnesses: force profiling on or off (overrides
  * QWASAR_PROFILE), and read one label's accumulated device milliseconds and
  * mark count. */

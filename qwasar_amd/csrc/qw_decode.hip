@@ -198,6 +198,12 @@ static QdLayout qd_layout(const qwk_moe *M, int rows)
 struct QdArgs {
     qwk_moe m;
     const float *x;
+    // with hin set, the input is x = rms_norm(bf16(hin + yprev)) instead
+    const uint16_t *hin;
+    const float *yprev;             // may be null: x = rms_norm(hin)
+    uint16_t *hout;                 // bf16(hin + yprev), written by workgroup 0
+    float *xout;                    // that x, written by workgroup 0
+    float eps;
     float *out;
     int32_t *idx;
     float *w;
@@ -210,6 +216,91 @@ struct QdArgs {
     QdSync *sync;
     uint32_t epoch;
 };
+
+// ---- the residual step as the launch's prologue ----------------------------------
+//
+// With RES (a.hin set), the launch's input rows are x = rms_norm(bf16(hin + yprev))
+// (the step between stacked layers).  Every workgroup that reads x builds the
+// rows it stages from hin and yprev, with the arithmetic and the summation
+// order of k_resid_rms_bf16 (qw_norm.hip: each of 256 threads an fmaf chain
+// over its float4 chunks, the xor tree, the four wave partials in order), so
+// x has the bits that kernel gives; workgroup 0 also writes hout and xout.
+
+__device__ __forceinline__ float qd_bf16r(float f)
+{
+    const uint32_t u = __float_as_uint(f);
+    return __uint_as_float((u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u);
+}
+
+// bf16(hin + yprev) of row t, columns 4 i4 .. 4 i4 + 3
+__device__ __forceinline__ float4 qd_v4(const QdArgs &a, int t, int i4)
+{
+    const uint2 hb = reinterpret_cast<const uint2 *>(a.hin + (size_t)t * a.m.H)[i4];
+    float4 v = make_float4(__uint_as_float(hb.x << 16), __uint_as_float(hb.x & 0xFFFF0000u),
+                           __uint_as_float(hb.y << 16), __uint_as_float(hb.y & 0xFFFF0000u));
+    if (a.yprev) {
+        const float4 y = reinterpret_cast<const float4 *>(a.yprev + (size_t)t * a.m.H)[i4];
+        v = make_float4(qd_bf16r(v.x + y.x), qd_bf16r(v.y + y.y), qd_bf16r(v.z + y.z), qd_bf16r(v.w + y.w));
+    }
+    return v;
+}
+
+// x of row t, columns 4 i4 .. 4 i4 + 3, with the prologue (RES) or from a.x
+template <bool RES>
+__device__ __forceinline__ float4 qd_x4(const QdArgs &a, const float *qinv, int t, int i4)
+{
+    if constexpr (!RES) return reinterpret_cast<const float4 *>(a.x + (size_t)t * a.m.H)[i4];
+    const float4 v = qd_v4(a, t, i4);
+    const float r = qinv[t];
+    return make_float4(v.x * r, v.y * r, v.z * r, v.w * r);
+}
+
+// qinv[t] = 1 / sqrt(mean(v^2) + eps) for every row; the whole workgroup
+// (1024 threads: four rows at a time, 256 threads a row), ends in a barrier.
+__device__ __forceinline__ void qd_norm_rows(const QdArgs &a, float *qinv, float *qpart)
+{
+    const int g = threadIdx.x >> 8, tid = threadIdx.x & 255, wave = threadIdx.x >> 6;
+    const int n4 = a.m.H / 4;
+    for (int t0 = 0; t0 < a.rows; t0 += 4) {
+        const int t = t0 + g;
+        float ss = 0.0f;
+        if (t < a.rows)
+            for (int i = tid; i < n4; i += 256) {
+                const float4 v = qd_v4(a, t, i);
+                ss = __builtin_fmaf(v.x, v.x, ss);
+                ss = __builtin_fmaf(v.y, v.y, ss);
+                ss = __builtin_fmaf(v.z, v.z, ss);
+                ss = __builtin_fmaf(v.w, v.w, ss);
+            }
+        ss = qw_xor_sum<64>(ss);
+        if ((threadIdx.x & 63) == 0) qpart[wave] = ss;
+        __syncthreads();
+        if (threadIdx.x < 4 && t0 + (int)threadIdx.x < a.rows) {
+            const float *p = qpart + 4 * threadIdx.x;
+            float sum = p[0];
+            sum = sum + p[1];
+            sum = sum + p[2];
+            sum = sum + p[3];
+            qinv[t0 + threadIdx.x] = 1.0f / sqrtf(sum / (float)a.m.H + a.eps);
+        }
+        __syncthreads();
+    }
+}
+
+// workgroup 0: hout = bf16(hin + yprev), xout = x
+__device__ __forceinline__ void qd_write_resid(const QdArgs &a, const float *qinv)
+{
+    const int n4 = a.m.H / 4;
+    for (int j = threadIdx.x; j < a.rows * n4; j += blockDim.x) {
+        const int t = j / n4, i = j % n4;
+        const float4 v = qd_v4(a, t, i);
+        const float r = qinv[t];
+        reinterpret_cast<uint2 *>(a.hout)[j] =
+            make_uint2((__float_as_uint(v.x) >> 16) | (__float_as_uint(v.y) & 0xFFFF0000u),
+                       (__float_as_uint(v.z) >> 16) | (__float_as_uint(v.w) & 0xFFFF0000u));
+        reinterpret_cast<float4 *>(a.xout)[j] = make_float4(v.x * r, v.y * r, v.z * r, v.w * r);
+    }
+}
 
 // ---- router ---------------------------------------------------------------------
 //
@@ -270,20 +361,23 @@ __device__ __forceinline__ void qd_router_row(const uint4 (&w)[8], const float *
     }
 }
 
-__device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *lds)
+template <bool RES>
+__device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *lds, float *qinv, float *qpart)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int H = a.m.H, E = a.m.E, nch = H / 64;
     const int o = b * QD_RT_ROWS + wave;
     float *xl = lds, *pbase = lds + nch * QD_XPAD, *part = pbase + wave * 64;
+    if constexpr (RES) qd_norm_rows(a, qinv, qpart);
     // the token rows, staged as q16 units for the gate / up roles
     const int units = H / 16;
     for (int i = b * QD_THREADS + threadIdx.x; i < a.rows * units; i += a.n_rt * QD_THREADS) {
-        const float4 *src = reinterpret_cast<const float4 *>(a.x + (size_t)i * 16);
         float v[16];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const float4 f = src[q];
+            float4 f;
+            if constexpr (RES) f = qd_x4<true>(a, qinv, i / units, (i % units) * 4 + q);
+            else f = reinterpret_cast<const float4 *>(a.x + (size_t)i * 16)[q];
             v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
         }
         uint4 u[3];
@@ -327,7 +421,7 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
     for (int t = 0; t < a.rows; t++) {
         if (t) __syncthreads();
         for (int i = threadIdx.x; i < H / 4; i += blockDim.x) {
-            const float4 v = reinterpret_cast<const float4 *>(a.x + (size_t)t * H)[i];
+            const float4 v = qd_x4<RES>(a, qinv, t, i);
             *reinterpret_cast<float4 *>(xl + (i / 16) * QD_XPAD + (i % 16) * 4) = v;
         }
         __syncthreads();
@@ -337,6 +431,8 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
     QD_TS(2);
     qd_signal(a.sync, QD_FL_RT, b, a.n_rt, a.epoch);
     QD_TS(5);
+    if constexpr (RES)
+        if (b == 0) qd_write_resid(a, qinv);
 }
 
 // ---- gate / up rows with SwiGLU ----------------------------------------------------
@@ -352,17 +448,17 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
 
 // Stages token rows x[vin[t]] (t < n; token t when vin is NULL) into LDS as
 // q16 units, with threads tid0.. of the workgroup.
-__device__ __forceinline__ void qd_stage_x(uint4 *xs, const float *x, const int *vin, int n, int H, int tid0,
-                                           int nthr)
+template <bool RES>
+__device__ __forceinline__ void qd_stage_x(uint4 *xs, const QdArgs &a, const float *qinv, const int *vin, int n,
+                                           int tid0, int nthr)
 {
-    const int units = H / 16;
+    const int units = a.m.H / 16;
     for (int i = threadIdx.x - tid0; i < n * units; i += nthr) {
         const int t = i / units, u = i % units;
-        const float4 *src = reinterpret_cast<const float4 *>(x + (size_t)(vin ? vin[t] : t) * H + 16 * u);
         float v[16];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const float4 f = src[q];
+            const float4 f = qd_x4<RES>(a, qinv, vin ? vin[t] : t, 4 * u + q);
             v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
         }
         qw_q16_stage(v, xs + (size_t)i * 3);
@@ -625,16 +721,19 @@ __device__ __forceinline__ void qd_wait_router(const QdArgs &a)
     __syncthreads();
 }
 
-template <int LPR, int NUL, int PL>
+template <int LPR, int NUL, int PL, bool RES>
 __device__ __forceinline__ void qd_role_experts(const QdArgs &a, int bb, uint4 *xs, QdRoute &R, int *vin,
-                                                int *vout, float (*ys)[QD_GU_MAXRPB])
+                                                int *vout, float (*ys)[QD_GU_MAXRPB], float *qinv, float *qpart)
 {
     constexpr int RPB = QD_WAVES * (64 / LPR);
     const int H = a.m.H, I = a.m.I, K = a.m.K;
     const int u = bb / a.gu_wg_per_u, rb = bb % a.gu_wg_per_u;
     // One token: its input is staged into LDS while the router runs.
     const bool one = a.rows == 1;
-    if (one) qd_stage_x(xs, a.x, nullptr, 1, H, 0, blockDim.x);
+    if (one) {
+        if constexpr (RES) qd_norm_rows(a, qinv, qpart);
+        qd_stage_x<RES>(xs, a, qinv, nullptr, 1, 0, blockDim.x);
+    }
     qd_wait_router(a);
     QD_TS(1);
     qd_route_all<PL>(a, R);
@@ -842,7 +941,7 @@ gave_up:
 
 // 8 waves per SIMD: two 16-wave workgroups per CU, which takes at most 64
 // VGPRs and 78 SGPRs a wave (at 80 SGPRs a CU holds one).
-template <int LPR, int NUL, int NULD, int PL>
+template <int LPR, int NUL, int NULD, int PL, bool RES>
 __global__ __launch_bounds__(QD_THREADS, 8) void k_decode_fused(QdArgs a)
 {
     extern __shared__ uint4 xs[];     // [tch][units][3], or the router's partials
@@ -850,18 +949,19 @@ __global__ __launch_bounds__(QD_THREADS, 8) void k_decode_fused(QdArgs a)
     __shared__ int vin[QD_MAXT], vout[QD_MAXT];
     __shared__ float ys[QD_MAXT][QD_GU_MAXRPB];
     __shared__ uint32_t dready;
+    __shared__ float qinv[QD_MAXT], qpart[QD_WAVES];   // the residual prologue's row scales
     static_assert(QD_MAXT * QD_GU_MAXRPB >= (QWK_DECODE_MAX_K + 1) * QD_DOWN_RPG, "down shares ys");
     constexpr int RPB = QD_WAVES * (64 / LPR);
     QD_TS(0);
     QD_HWID();
     int b = blockIdx.x;
     if (b < a.n_rt) {
-        qd_role_router(a, b, reinterpret_cast<float *>(xs));
+        qd_role_router<RES>(a, b, reinterpret_cast<float *>(xs), qinv, qpart);
         return;
     }
     b -= a.n_rt;
     if (b < a.n_ex) {
-        qd_role_experts<LPR, NUL, PL>(a, b, xs, R, vin, vout, ys);
+        qd_role_experts<LPR, NUL, PL, RES>(a, b, xs, R, vin, vout, ys, qinv, qpart);
         return;
     }
     b -= a.n_ex;
@@ -870,7 +970,10 @@ __global__ __launch_bounds__(QD_THREADS, 8) void k_decode_fused(QdArgs a)
         // Otherwise copy them, pass by pass, from the router role's staging.
         const bool own = a.rows <= a.tch;
         if (threadIdx.x < QD_MAXT) vin[threadIdx.x] = vout[threadIdx.x] = threadIdx.x;
-        if (own) qd_stage_x(xs, a.x, nullptr, a.rows, a.m.H, 0, blockDim.x);
+        if (own) {
+            if constexpr (RES) qd_norm_rows(a, qinv, qpart);
+            qd_stage_x<RES>(xs, a, qinv, nullptr, a.rows, 0, blockDim.x);
+        }
         else qd_wait_router(a);
         __syncthreads();
         qd_glu_block<LPR, NUL>(a.m.sh_gate, a.m.sh_up, a.m.SI, a, b * RPB, a.rows, own, xs, vin, vout, a.qsh,
@@ -898,10 +1001,10 @@ extern "C" int qwk_moe_decode_sync_error(const void *sync, uint32_t *err)
     return (int)hipMemcpy(err, &static_cast<const QdSync *>(sync)->err, sizeof *err, hipMemcpyDeviceToHost);
 }
 
-template <int LPR, int NUL, int NULD, int PL>
+template <int LPR, int NUL, int NULD, int PL, bool RES>
 static void qd_launch(hipStream_t s, const QdArgs &a, int grid, hipEvent_t e0, hipEvent_t e1)
 {
-    auto kern = k_decode_fused<LPR, NUL, NULD, PL>;
+    auto kern = k_decode_fused<LPR, NUL, NULD, PL, RES>;
     if (e0) hipExtLaunchKernelGGL(kern, dim3(grid), dim3(QD_THREADS), QD_LDS, s, e0, e1, 0, a);
     else hipLaunchKernelGGL(kern, dim3(grid), dim3(QD_THREADS), QD_LDS, s, a);
 }
@@ -936,11 +1039,15 @@ extern "C" int qwk_moe_decode_supported(const qwk_moe *M, int rows)
 }
 
 extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
-                              const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes,
-                              void *sync, uint32_t epoch, hipEvent_t *ev)
+                              const qwk_resid *res, const qwk_moe *M, int rows, void *scratch,
+                              size_t scratch_bytes, void *sync, uint32_t epoch, hipEvent_t *ev)
 {
     const int G = M->group;
-    if (!qwk_moe_decode_supported(M, rows) || ((uintptr_t)x & 15u) || !sync || epoch == 0u)
+    if (!qwk_moe_decode_supported(M, rows) || !sync || epoch == 0u) return (int)hipErrorInvalidValue;
+    if (res ? (!res->h || !res->h_out || !res->x_out || ((uintptr_t)res->h & 7u) || ((uintptr_t)res->h_out & 7u) ||
+               ((uintptr_t)res->y & 15u) || ((uintptr_t)res->x_out & 15u) ||
+               (const void *)res->h_out == (const void *)res->h || (const void *)res->h_out == (const void *)res->y)
+            : (!x || ((uintptr_t)x & 15u)))
         return (int)hipErrorInvalidValue;
     const QdLayout L = qd_layout(M, rows);
     if (scratch_bytes < L.total) return (int)hipErrorInvalidValue;
@@ -951,6 +1058,11 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     QdArgs a;
     a.m = *M;
     a.x = x; a.out = out; a.idx = idx; a.w = w; a.rows = rows;
+    a.hin = res ? res->h : nullptr;
+    a.yprev = res ? res->y : nullptr;
+    a.hout = res ? res->h_out : nullptr;
+    a.xout = res ? res->x_out : nullptr;
+    a.eps = res ? res->eps : 0.0f;
     a.umax = rows * M->K < M->E ? rows * M->K : M->E;
     a.lgG = G == 32 ? 5 : G == 64 ? 6 : 7;
     const int rpb = QD_WAVES * (64 / lpr_h);
@@ -978,7 +1090,10 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
 
     hipEvent_t e0 = ev ? ev[0] : 0, e1 = ev ? ev[1] : 0;
 #define QD_GO(L_, N_, D_, P_) \
-    if (lpr_h == L_ && nul_h == N_ && nul_d == D_ && pl == P_) qd_launch<L_, N_, D_, P_>(s, a, grid, e0, e1); else
+    if (lpr_h == L_ && nul_h == N_ && nul_d == D_ && pl == P_) {                                      \
+        if (res) qd_launch<L_, N_, D_, P_, true>(s, a, grid, e0, e1);                                   \
+        else qd_launch<L_, N_, D_, P_, false>(s, a, grid, e0, e1);                                      \
+    } else
     QD_SHAPES(QD_GO)
 #undef QD_GO
     return (int)hipErrorInvalidValue;

@@ -113,22 +113,37 @@ size_t qwk_moe_decode_sync_bytes(void);
 int qwk_moe_decode_sync_error(const void *sync, uint32_t *err);
 /* Non-zero when the decode path takes this layer shape and token count. */
 int qwk_moe_decode_supported(const qwk_moe *M, int rows);
+/* The residual step before a layer of a stack: the layer's input is
+ * x = rms_norm(bf16(h + y)) (rms_norm(h) when y is NULL), unit weight;
+ * h_out receives bf16(h + y) (or h), x_out that x.  h_out must not alias h
+ * or y on the decode path, whose workgroups read h while one writes h_out. */
+typedef struct {
+    const uint16_t *h;
+    const float *y;
+    uint16_t *h_out;
+    float *x_out;
+    float eps;
+} qwk_resid;
+
 /* Decode (rows <= QWK_DECODE_MAX_ROWS, K <= QWK_DECODE_MAX_K), one launch:
- * out [rows, H], idx/w [rows, K].  `ev`, when not NULL, holds 2 events, the
- * launch's start and end, stamped by the dispatch itself. */
+ * out [rows, H], idx/w [rows, K]; the input is x, or, when `res` is not NULL,
+ * the residual step's x computed inside the launch.  `ev`, when not NULL,
+ * holds 2 events, the launch's start and end, stamped by the dispatch itself. */
 #define QWK_DECODE_MAX_ROWS 8
 #define QWK_DECODE_MAX_K 15
 int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
-                   const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes,
+                   const qwk_resid *res, const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes,
                    void *sync, uint32_t epoch, hipEvent_t *ev);
 
 /* RMS norm of [rows, dim] fp32 rows (dim % 4 == 0), optional bf16 weight:
  * y = x / sqrt(mean(x^2) + eps) * out_scale (* w). */
 int qwk_rms_norm(hipStream_t s, float *y, const float *x, const uint16_t *w, int dim, int rows,
                  float eps, float out_scale);
-/* The residual step between stacked layers: h bf16 [rows, dim] <- bf16(h + y)
- * (h unchanged when y is NULL), then x = rms_norm(h) in fp32, unit weight. */
-int qwk_resid_rms_bf16(hipStream_t s, uint16_t *h, float *x, const float *y, int dim, int rows, float eps);
+/* The residual step between stacked layers: h_out bf16 [rows, dim] =
+ * bf16(h + y) (h when y is NULL; h_out may be h), then x = rms_norm(h_out)
+ * in fp32, unit weight. */
+int qwk_resid_rms_bf16(hipStream_t s, const uint16_t *h, uint16_t *h_out, float *x, const float *y, int dim,
+                       int rows, float eps);
 
 /* Seeded synthetic tensors (counter-based SplitMix64; value i of key k is
  * the i-th output of SplitMix64 seeded with k). */

@@ -66,12 +66,15 @@ __global__ void __launch_bounds__(QN_THREADS) k_rms_norm(float *__restrict__ y, 
     }
 }
 
-// h (bf16 [rows, dim]) <- bf16(h + y) when y is given; x = rms_norm(h)
-__global__ void __launch_bounds__(QN_THREADS) k_resid_rms_bf16(uint16_t *__restrict__ h, float *__restrict__ x,
+// h_out (bf16 [rows, dim]) = bf16(h + y) when y is given, else h (h_out may
+// be h); x = rms_norm(h_out)
+__global__ void __launch_bounds__(QN_THREADS) k_resid_rms_bf16(const uint16_t *h, uint16_t *h_out,
+                                                               float *__restrict__ x,
                                                                const float *__restrict__ y, int dim, float eps)
 {
     __shared__ float part[QN_THREADS / 64];
-    uint2 *hr = reinterpret_cast<uint2 *>(h + (size_t)blockIdx.x * dim);
+    const uint2 *hr = reinterpret_cast<const uint2 *>(h + (size_t)blockIdx.x * dim);
+    uint2 *ho = reinterpret_cast<uint2 *>(h_out + (size_t)blockIdx.x * dim);
     float4 *xr = reinterpret_cast<float4 *>(x + (size_t)blockIdx.x * dim);
     const float4 *yr = y ? reinterpret_cast<const float4 *>(y + (size_t)blockIdx.x * dim) : nullptr;
     const int n4 = dim / 4;
@@ -90,15 +93,15 @@ __global__ void __launch_bounds__(QN_THREADS) k_resid_rms_bf16(uint16_t *__restr
                 v[q] = __uint_as_float((uint32_t)b[q] << 16);
             }
             hb = make_uint2((uint32_t)b[0] | ((uint32_t)b[1] << 16), (uint32_t)b[2] | ((uint32_t)b[3] << 16));
-            hr[i] = hb;
         }
+        if (yr || ho != hr) ho[i] = hb;
 #pragma unroll
         for (int q = 0; q < 4; q++) ss = __builtin_fmaf(v[q], v[q], ss);
     }
     ss = qn_block_sum(ss, part);
     const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
     for (int i = threadIdx.x; i < n4; i += QN_THREADS) {
-        const uint2 hb = hr[i];   // this thread's own values (written above when y is given)
+        const uint2 hb = ho[i];   // this thread's own values, written above
         xr[i] = make_float4(__uint_as_float(hb.x << 16) * inv, __uint_as_float(hb.x & 0xFFFF0000u) * inv,
                             __uint_as_float(hb.y << 16) * inv, __uint_as_float(hb.y & 0xFFFF0000u) * inv);
     }
@@ -114,12 +117,13 @@ extern "C" int qwk_rms_norm(hipStream_t s, float *y, const float *x, const uint1
     return (int)hipGetLastError();
 }
 
-extern "C" int qwk_resid_rms_bf16(hipStream_t s, uint16_t *h, float *x, const float *y, int dim, int rows,
-                                  float eps)
+extern "C" int qwk_resid_rms_bf16(hipStream_t s, const uint16_t *h, uint16_t *h_out, float *x, const float *y,
+                                  int dim, int rows, float eps)
 {
     if (rows <= 0) return 0;
-    if (dim <= 0 || dim % 4 || ((uintptr_t)h & 7u) || ((uintptr_t)x & 15u) || ((uintptr_t)y & 15u))
+    if (dim <= 0 || dim % 4 || ((uintptr_t)h & 7u) || ((uintptr_t)h_out & 7u) || ((uintptr_t)x & 15u) ||
+        ((uintptr_t)y & 15u))
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_resid_rms_bf16, dim3(rows), dim3(QN_THREADS), 0, s, h, x, y, dim, eps);
+    hipLaunchKernelGGL(k_resid_rms_bf16, dim3(rows), dim3(QN_THREADS), 0, s, h, h_out, x, y, dim, eps);
     return (int)hipGetLastError();
 }

@@ -466,7 +466,7 @@ void qw_op_rms_norm(qw_cmd c, qw_ref y, qw_ref x, qw_ref weight,
 void qw_op_residual_rms_norm_bf16(qw_cmd c, qw_ref h, qw_ref x, qw_ref y, int32_t dim, int32_t rows, float eps) {
     QW_OP(c);
     touch(c, y, 0); touch(c, h, 1); touch(c, x, 1);
-    launched(c, "residual_rms_norm_bf16", qwk_resid_rms_bf16(G.stream, dp(h), dp(x), dp(y), dim, rows, eps));
+    launched(c, "residual_rms_norm_bf16", qwk_resid_rms_bf16(G.stream, dp(h), dp(h), dp(x), dp(y), dim, rows, eps));
 }
 
 void qw_op_synth(qw_cmd c, qw_ref dst, int32_t kind, int64_t n, uint64_t key, float a, float b) {
@@ -711,7 +711,7 @@ static void moe_desc(qwk_moe *mp, const qw_moe_layer *M) {
 
 /* Decode: one launch over only the selected experts. */
 static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float *x,
-                       const qwk_moe *mp, int32_t rows) {
+                       const qwk_resid *res, const qwk_moe *mp, int32_t rows) {
     const qwk_moe m = *mp;
     const size_t need = qwk_moe_decode_scratch(&m, rows);
     void *S = scratch(need);
@@ -723,7 +723,7 @@ static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float
     if (++G.depoch == 0u) G.depoch = 1u;   /* flags hold past epochs; 0 is "never" */
     hipEvent_t ev[2] = { NULL, NULL };
     const int per_kernel = G.prof && (ev[0] = cmd_event(c, 0)) && (ev[1] = cmd_event(c, 0));
-    const int rc = qwk_moe_decode(G.stream, out, idx, w, x, &m, rows, S, need, G.dsync, G.depoch,
+    const int rc = qwk_moe_decode(G.stream, out, idx, w, x, res, &m, rows, S, need, G.dsync, G.depoch,
                                   per_kernel ? ev : NULL);
     if (per_kernel) cmd_add_mark(c, "moe decode", ev[0], ev[1]);
     c->decoded = 1;
@@ -731,23 +731,53 @@ static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float
     return rc == 0;
 }
 
-bool qw_op_moe_layer(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,
-                     const qw_moe_layer *M, int32_t rows) {
+/* The layer's shape checks (false: refused, nothing encoded). */
+static bool moe_layer_ok(const qw_moe_layer *M, int32_t rows) {
     if (!M || rows < 1 || M->K > QWK_ROUTE_MAX_K || M->E > QWK_ROUTE_MAX_E || M->K > M->E ||
         M->H % 64 || M->I % 64 || M->SI % 64 || M->H > QWK_DMAT_MAX_K)
         return false;
     const int32_t grp = M->split ? M->gate.group : M->gate_up.group;
-    if (M->down.group != grp || M->sh_gate.group != grp || M->sh_up.group != grp ||
-        M->sh_down.group != grp || (M->split && M->up.group != grp))
-        return false;
-    if (!c) return true;
-    touch(c, x, 0); touch(c, M->router, 0); touch(c, M->sh_gate_w, 0);
+    return !(M->down.group != grp || M->sh_gate.group != grp || M->sh_up.group != grp ||
+             M->sh_down.group != grp || (M->split && M->up.group != grp));
+}
+
+static void touch_layer(qw_cmd c, const qw_moe_layer *M) {
+    touch(c, M->router, 0); touch(c, M->sh_gate_w, 0);
     if (M->split) { touch_q4(c, &M->gate); touch_q4(c, &M->up); } else touch_q4(c, &M->gate_up);
     touch_q4(c, &M->down); touch_q4(c, &M->sh_gate); touch_q4(c, &M->sh_up); touch_q4(c, &M->sh_down);
+}
+
+bool qw_op_moe_layer(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,
+                     const qw_moe_layer *M, int32_t rows) {
+    if (!moe_layer_ok(M, rows)) return false;
+    if (!c) return true;
+    touch(c, x, 0);
+    touch_layer(c, M);
     touch(c, out, 1); touch(c, idx, 1); touch(c, w, 1);
     qwk_moe m;
     moe_desc(&m, M);
     if (rows > QWK_DECODE_MAX_ROWS || !qwk_moe_decode_supported(&m, rows))
         return moe_prefill(c, dp(out), dp(idx), dp(w), dp(x), M, rows);
-    return moe_decode(c, dp(out), dp(idx), dp(w), dp(x), &m, rows);
+    return moe_decode(c, dp(out), dp(idx), dp(w), dp(x), NULL, &m, rows);
+}
+
+bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref h, qw_ref y_prev,
+                              qw_ref h_out, qw_ref x_out, const qw_moe_layer *M, int32_t rows, float eps) {
+    if (!moe_layer_ok(M, rows) || !h.buf || !h_out.buf || !x_out.buf) return false;
+    if (h_out.buf == h.buf || (y_prev.buf && h_out.buf == y_prev.buf)) return false;
+    if (!c) return true;
+    touch(c, h, 0); touch(c, y_prev, 0);
+    touch_layer(c, M);
+    touch(c, h_out, 1); touch(c, x_out, 1);
+    touch(c, out, 1); touch(c, idx, 1); touch(c, w, 1);
+    qwk_moe m;
+    moe_desc(&m, M);
+    if (rows > QWK_DECODE_MAX_ROWS || !qwk_moe_decode_supported(&m, rows)) {
+        const int rc = qwk_resid_rms_bf16(G.stream, dp(h), dp(h_out), dp(x_out), dp(y_prev), M->H, rows, eps);
+        launched(c, "moe_layer_residual (norm)", rc);
+        if (rc != 0) return false;
+        return moe_prefill(c, dp(out), dp(idx), dp(w), dp(x_out), M, rows);
+    }
+    const qwk_resid res = { dp(h), dp(y_prev), dp(h_out), dp(x_out), eps };
+    return moe_decode(c, dp(out), dp(idx), dp(w), NULL, &res, &m, rows);
 }

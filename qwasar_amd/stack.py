@@ -118,6 +118,9 @@ class Stack:
         self.h = gpu.Buf(rows_max * H * 2)       # bf16 carry
         self.x = gpu.Buf(rows_max * H * 4)       # the normalised input of the next layer
         self.y = gpu.Buf(rows_max * H * 4)       # a layer's output
+        self.h2 = gpu.Buf(rows_max * H * 2)      # the fused form's second h and y
+        self.y2 = gpu.Buf(rows_max * H * 4)
+        self.h_final = self.h
         self.idx = gpu.Buf(rows_max * K * 4)
         self.w = gpu.Buf(rows_max * K * 4)
 
@@ -133,6 +136,24 @@ class Stack:
                 raise RuntimeError(f"qw_op_moe_layer refused layer {l} at {rows} rows")
             gpu.qw_op_residual_rms_norm_bf16(c, self.h.ref(), self.x.ref(), self.y.ref(), self.H, rows, EPS)
 
+    def encode_fused(self, c, rows: int) -> None:
+        """The whole stack over h[:rows] with each residual step folded into
+        the next layer's op (qw_op_moe_layer_residual; at decode sizes inside
+        its one launch): layer l reads h from one of two buffers and writes
+        the other, y alternates the same way, and a last residual step
+        finishes h, which ends in self.h_final.  Same arithmetic, in the same
+        order, as encode()."""
+        hb, yb = (self.h, self.h2), (self.y, self.y2)
+        n = len(self.layers)
+        for l in range(n):
+            y_prev = yb[(l - 1) % 2].ref() if l else gpu.NULL_REF
+            if not gpu.qw_op_moe_layer_residual(c, yb[l % 2].ref(), self.idx.ref(), self.w.ref(),
+                                                hb[l % 2].ref(), y_prev, hb[(l + 1) % 2].ref(), self.x.ref(),
+                                                self.layers[l].desc, rows, EPS):
+                raise RuntimeError(f"qw_op_moe_layer_residual refused layer {l} at {rows} rows")
+        gpu.qw_op_residual_rms_norm_bf16(c, hb[n % 2].ref(), self.x.ref(), yb[(n - 1) % 2].ref(), self.H, rows, EPS)
+        self.h_final = hb[n % 2]
+
     def free(self) -> None:
-        for t in (self.h, self.x, self.y, self.idx, self.w):
+        for t in (self.h, self.x, self.y, self.h2, self.y2, self.idx, self.w):
             t.free()

@@ -173,10 +173,51 @@ def test_stack_config1_shape_layer_by_layer_and_free_running(gpu):
         L.free()
 
 
+def _fused_equals_unfused(gpu, layers, h0, rows):
+    st = stack.Stack(layers, rows)
+    st.h.write(h0)
+    c = gpu.qw_cmd_begin()
+    st.encode(c, rows)
+    gpu.run(c, "unfused stack")
+    want_h = st.h.read(np.uint16, (rows, st.H))
+    want_x = st.x.read(np.float32, (rows, st.H))
+    st.h.write(h0)
+    c = gpu.qw_cmd_begin()
+    st.encode_fused(c, rows)
+    gpu.run(c, "fused stack")
+    got_h = st.h_final.read(np.uint16, (rows, st.H))
+    got_x = st.x.read(np.float32, (rows, st.H))
+    st.free()
+    assert np.array_equal(got_h, want_h), "fused stack h differs from the unfused one"
+    assert np.array_equal(got_x.view(np.uint32), want_x.view(np.uint32)), "fused stack x differs"
+
+
+@pytest.mark.parametrize("rows", [1, 3, 8, 12])
+def test_stack_fused_residual_same_bits(gpu, rows):
+    """qw_op_moe_layer_residual (the residual step inside the decode launch at
+    <= 8 rows; the norm kernel then the grouped layer above) gives the
+    unfused stack's bits: 5 layers of config 1's shape, and 48 of config 0's."""
+    c1 = dict(synth.CONFIGS[1])
+    c1.pop("rows")
+    layers = [stack.DeviceLayer(31, l, **c1) for l in range(5)]
+    h0 = synth.to_bf16(synth.normal(31, f"stack.h0f.{rows}", rows * c1["H"]).astype(np.float32)).reshape(rows, -1)
+    _fused_equals_unfused(gpu, layers, h0, rows)
+    for L in layers:
+        L.free()
+    c0 = dict(synth.CONFIGS[0])
+    c0.pop("rows")
+    layers = [stack.DeviceLayer(32, l, **c0) for l in range(48)]
+    h0 = synth.to_bf16(synth.normal(32, f"stack.h0f0.{rows}", rows * c0["H"]).astype(np.float32)).reshape(rows, -1)
+    _fused_equals_unfused(gpu, layers, h0, rows)
+    for L in layers:
+        L.free()
+
+
 def test_stack_config4_full_size_decode(gpu):
     """Config 4 at full size: 48 layers of config 1's shape (~65 GB on the
     device), one decode token through all of them, twice: the same bits both
-    times, and the first and last layers against the oracle on their inputs."""
+    times and with the residual step folded into each launch, and the first
+    and last layers against the oracle on their inputs."""
     c1 = dict(synth.CONFIGS[1])
     c1.pop("rows")
     layers = [stack.DeviceLayer(2026, l, **c1) for l in range(48)]
@@ -190,6 +231,11 @@ def test_stack_config4_full_size_decode(gpu):
         gpu.run(c, "48-layer decode")
         outs.append(st.h.read(np.uint16, (1, c1["H"])))
     assert np.array_equal(outs[0], outs[1]), "the stack is not deterministic"
+    st.h.write(h0)
+    c = gpu.qw_cmd_begin()
+    st.encode_fused(c, 1)
+    gpu.run(c, "48-layer decode, residual folded in")
+    assert np.array_equal(st.h_final.read(np.uint16, (1, c1["H"])), outs[0]), "fused stack differs"
     assert np.isfinite(synth.bf16_to_f32(outs[0])).all()
     # the first and the last layer, each against the oracle on the GPU's input
     for l in (0, 47):
