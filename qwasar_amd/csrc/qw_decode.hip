@@ -15,7 +15,10 @@
 //            activations and computes; then the combine:
 //            sigmoid(g) * shared + sum_k w_k * y_k, an fma chain in slot order
 //
-// Hand-offs between roles go through device memory past the per-XCD L2: the
+// For one token the router's logits need no flag: each is stored together
+// with the launch's epoch in one 64-bit word, and the routing workgroups poll
+// the words themselves.  Other hand-offs go through device memory past the
+// per-XCD L2: the
 // producer writes with device-coherent (sc1) stores, waits for them, and
 // bumps a counter; the last arriver of a counter resets it to zero and
 // publishes the launch's epoch in the counter's flag.  A consumer polls the
@@ -105,6 +108,7 @@ static int qd_nul(int units, int lpr)
 
 #define QD_GROUP 16
 #define QD_NSYNC 2048
+
 #define QD_FL_RT 0           // router groups
 #define QD_FL_SH 64          // shared-expert groups
 #define QD_FL_EX 128         // experts: slot u, group h at QD_FL_EX + u * ngu + h
@@ -113,6 +117,10 @@ struct QdSync {
     uint32_t cnt[QD_NSYNC];
     uint32_t flag[QD_NSYNC];
     uint32_t err;
+    uint32_t pad;
+    // the router's logits, row t at t * (E + 1), the shared gate's at E:
+    // {epoch, fp32 bits}, each written by one 64-bit store
+    uint2 lgt[QD_MAXT * (QWK_ROUTE_MAX_E + 1)];
 };
 
 __device__ __forceinline__ void qd_stf(float *p, float v)
@@ -177,7 +185,7 @@ __device__ __forceinline__ bool qd_wait_flags(QdSync *S, bool has, int idx, uint
 }
 
 struct QdLayout {
-    size_t logits, g1, qx, qsh, qact, total;
+    size_t qx, qsh, qact, total;
 };
 
 static size_t al(size_t n) { return (n + 255) & ~(size_t)255; }
@@ -186,8 +194,6 @@ static QdLayout qd_layout(const qwk_moe *M, int rows)
 {
     QdLayout L;
     size_t o = 0;
-    L.logits = o; o += al((size_t)rows * M->E * 4);
-    L.g1 = o;     o += al((size_t)rows * 4);
     L.qx = o;     o += al((size_t)rows * (M->H / 16) * QW_Q16_BYTES);
     L.qsh = o;    o += al((size_t)rows * (M->SI / 16) * QW_Q16_BYTES);
     L.qact = o;   o += al((size_t)rows * M->K * (M->I / 16) * QW_Q16_BYTES);
@@ -211,11 +217,32 @@ struct QdArgs {
     int n_rt, n_sh, gu_wg_per_u, ngu, n_ex, n_down_rb;
     int tch;                        // input vectors per LDS pass
     char *scr;                      // the scratch base (device-coherent loads are offsets from it)
-    float *logits, *g1;
     uint4 *qx, *qsh, *qact;         // q16 units: [vector][units][3]
     QdSync *sync;
     uint32_t epoch;
 };
+
+// One wave: each lane with `has` waits until its tagged word {epoch, value}
+// at p holds this launch's epoch, bounded like qd_wait_flags (on giving up
+// the error word is raised and the value is whatever was read).  Each pass
+// reads the words and the error word in one batch.
+__device__ __forceinline__ uint2 qd_poll_tag(const QdArgs &a, const uint2 *p, bool has)
+{
+    for (int spins = 0;; spins++) {
+        unsigned long long v;
+        asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
+        uint32_t e = qd_poll_ld(&a.sync->err);
+        asm volatile("s_waitcnt vmcnt(0)" : "+v"(v), "+v"(e)::"memory");
+        const uint2 r = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+        if (__ballot(has && r.x != a.epoch) == 0ull) return r;
+        if (spins >= QD_SPIN_LIMIT || __ballot(e != 0u) != 0ull) {
+            if ((threadIdx.x & 63) == 0)
+                __hip_atomic_fetch_or(&a.sync->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return r;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
 
 // ---- the residual step as the launch's prologue ----------------------------------
 //
@@ -321,8 +348,8 @@ static_assert((64 * QD_XPAD + QD_WAVES * 64 + QD_RT_ROWS * 64 * QD_WPAD) * 4 <= 
 // lane l computes the fmaf chain of chunk l (k <= 64 * 64); the chunk
 // partials go to LDS and lane 0 adds them left to right, from -0 (so the
 // first addition is exact).
-__device__ __forceinline__ void qd_router_row(const uint4 (&w)[8], const float *xl, int nch, float *y,
-                                              float *part)
+__device__ __forceinline__ void qd_router_row(const uint4 (&w)[8], const float *xl, int nch, uint2 *y,
+                                              uint32_t epoch, float *part)
 {
     const int lane = threadIdx.x & 63;
     if (lane < nch) {
@@ -357,7 +384,11 @@ __device__ __forceinline__ void qd_router_row(const uint4 (&w)[8], const float *
             total = total + v.w;
         }
         for (; c < nch; c++) total = total + part[c];
-        qd_stf(y, total);
+        // the logit and the launch's epoch in one 64-bit store: a reader that
+        // sees this epoch sees this logit
+        __hip_atomic_store(reinterpret_cast<unsigned long long *>(y),
+                           (unsigned long long)epoch | ((unsigned long long)__float_as_uint(total) << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -426,10 +457,12 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
         }
         __syncthreads();
         if (t == 0) QD_TS(4);
-        if (row) qd_router_row(w, xl, nch, o < E ? a.logits + (size_t)t * E + o : a.g1 + t, part);
+        if (row) qd_router_row(w, xl, nch, a.sync->lgt + (size_t)t * (E + 1) + o, a.epoch, part);
     }
     QD_TS(2);
-    qd_signal(a.sync, QD_FL_RT, b, a.n_rt, a.epoch);
+    // one token: every reader polls the tagged logits (and stages x itself),
+    // so nothing waits on the router's flag
+    if (a.rows > 1) qd_signal(a.sync, QD_FL_RT, b, a.n_rt, a.epoch);
     QD_TS(5);
     if constexpr (RES)
         if (b == 0) qd_write_resid(a, qinv);
@@ -640,9 +673,15 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
     const int t = threadIdx.x, nthr = blockDim.x, wave = t >> 6, lane = t & 63, nw = nthr >> 6;
     const int E = a.m.E, K = a.m.K;
     if (a.rows == 1 && nw >= PL) {
+        // the token's logits, each wave its slice, as soon as their tags are this launch's
+        float x = 0.0f;
+        if (wave < PL) {
+            const int e = lane + 64 * wave;
+            x = __uint_as_float(qd_poll_tag(a, a.sync->lgt + min(e, E - 1), e < E).y);
+        }
         int pi;
         float pw;
-        qw_route_block<PL, true>(a.logits, E, K, a.m.norm, wave, lane, &pi, &pw, R.rs.one.sx, R.rs.one.vb);
+        qw_route_block<PL>(x, E, K, a.m.norm, wave, lane, &pi, &pw, R.rs.one.sx, R.rs.one.vb);
         if (wave == 0 && lane < K) {
             R.picks[lane] = pi;
             R.pw[lane] = pw;
@@ -651,7 +690,9 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
         for (int r = wave; r < a.rows; r += nw) {
             int pi;
             float pw;
-            qw_route_wave<PL, true>(a.logits + (size_t)r * E, E, K, a.m.norm, lane, &pi, &pw, R.rs.sx[wave]);
+            // after the router's flag: the fp32 halves of row r's tagged words
+            qw_route_wave<PL, true, 2>(reinterpret_cast<const float *>(a.sync->lgt + (size_t)r * (E + 1)) + 1, E, K,
+                                       a.m.norm, lane, &pi, &pw, R.rs.sx[wave]);
             if (lane < K) {
                 R.picks[r * K + lane] = pi;
                 R.pw[r * K + lane] = pw;
@@ -734,7 +775,7 @@ __device__ __forceinline__ void qd_role_experts(const QdArgs &a, int bb, uint4 *
         if constexpr (RES) qd_norm_rows(a, qinv, qpart);
         qd_stage_x<RES>(xs, a, qinv, nullptr, 1, 0, blockDim.x);
     }
-    qd_wait_router(a);
+    if (a.rows > 1) qd_wait_router(a);
     QD_TS(1);
     qd_route_all<PL>(a, R);
     QD_TS(2);
@@ -789,11 +830,12 @@ __device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R
     const int row0 = rb * RPG;
     const int lgG = a.lgG;
     if (threadIdx.x == 0) *dready = 0u;     // seen by all after routing's barriers
-    qd_wait_router(a);
+    if (a.rows > 1) qd_wait_router(a);
     QD_TS(1);
     qd_route_all<PL>(a, R);
     QD_TS(2);
-    const float gate = qw_sigmoid(qw_ldf_coh(a.g1, (uint32_t)t * 4u));
+    const float gate = qw_sigmoid(__uint_as_float(
+        qd_poll_tag(a, a.sync->lgt + (size_t)t * (a.m.E + 1) + a.m.E, (threadIdx.x & 63) == 0).y));
 
     const bool busy = m <= K;
     const int kin = m == 0 ? SI : I;
@@ -1075,8 +1117,6 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     a.n_ex = a.umax * a.gu_wg_per_u;
     a.n_down_rb = (M->H + QD_DOWN_RPG - 1) / QD_DOWN_RPG;
     a.scr = S;
-    a.logits = (float *)(S + L.logits);
-    a.g1 = (float *)(S + L.g1);
     a.qx = (uint4 *)(S + L.qx);
     a.qsh = (uint4 *)(S + L.qsh);
     a.qact = (uint4 *)(S + L.qact);

@@ -494,7 +494,8 @@ __device__ __forceinline__ void qw_route_finish(float (&v)[PL], int E, int K, in
 // read with device-coherent loads (past this XCD's L2).
 
 // Routes one token in one wave: lane l holds experts l + 64 j, j < PL.
-template <int PL, bool COH = false>
+// Expert e's logit is l[e * STRIDE].
+template <int PL, bool COH = false, int STRIDE = 1>
 __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E, int K, int norm,
                                               int lane, int *pick_i, float *pick_w, uint32_t *sx)
 {
@@ -502,7 +503,7 @@ __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E
     float m = -__builtin_huge_valf();
 #pragma unroll
     for (int j = 0; j < PL; j++) {
-        const int ec = min(lane + 64 * j, E - 1);
+        const int ec = min(lane + 64 * j, E - 1) * STRIDE;
         v[j] = COH ? qw_ldf_coh(l, (uint32_t)ec * 4u) : l[ec];
     }
     // every load issued before the first is used (one memory round trip)
@@ -529,22 +530,19 @@ __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E
 #define QW_ROUTE_BLOCK_LDS (QWK_ROUTE_MAX_E + 16)
 
 // Routes one token with a whole workgroup of at least PL waves (every
-// thread calls it; it holds __syncthreads): wave j takes the exponentials of
-// experts 64 j .. 64 j + 63, and wave 0 sums and selects exactly as
-// qw_route_wave does, so the picks and weights are the same bits.  The
-// results land in wave 0's lanes (lane n < K: pick n).
-template <int PL, bool COH = false>
-__device__ __forceinline__ void qw_route_block(const float *__restrict__ l, int E, int K, int norm, int wave,
-                                               int lane, int *pick_i, float *pick_w, uint32_t *sx,
-                                               float *vb)
+// thread calls it; it holds __syncthreads): wave j < PL brings the logit of
+// expert 64 j + lane in x (-inf past E; other waves' x is not read), takes the
+// exponentials of its slice, and wave 0 sums and selects exactly as
+// qw_route_wave does, so the picks and weights are the same bits.  The results
+// land in wave 0's lanes (lane n < K: pick n).
+template <int PL>
+__device__ __forceinline__ void qw_route_block(float x, int E, int K, int norm, int wave, int lane, int *pick_i,
+                                               float *pick_w, uint32_t *sx, float *vb)
 {
     float *wm = vb + QWK_ROUTE_MAX_E;
     const int e = lane + 64 * wave;
     const bool on = wave < PL && e < E;
-    float x = -__builtin_huge_valf();
     if (wave < PL) {
-        const int ec = min(e, E - 1);
-        x = COH ? qw_ldf_coh(l, (uint32_t)ec * 4u) : l[ec];
         x = on ? x : -__builtin_huge_valf();
         const float mw = qw_wave_max(x);
         if (lane == 0) wm[wave] = mw;

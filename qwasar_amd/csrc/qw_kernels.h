@@ -106,7 +106,8 @@ typedef struct {
 size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows);
 /* Bytes of the decode path's hand-off state.  It must be zeroed once before
  * first use (and again after an error); each launch then needs an epoch one
- * greater than the last (never 0), and launches on one state run in order. */
+ * greater than the last (never 0; zero the state again before an epoch
+ * repeats), and launches on one state run in order. */
 size_t qwk_moe_decode_sync_bytes(void);
 /* Reads the state's error word (non-zero: a launch's bounded wait gave up;
  * its outputs are garbage and the state must be zeroed).  Synchronous. */

@@ -720,7 +720,13 @@ static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float
         cmd_fail(c, hipErrorOutOfMemory, "moe_layer: decode hand-off state");
         return false;
     }
-    if (++G.depoch == 0u) G.depoch = 1u;   /* flags hold past epochs; 0 is "never" */
+    /* Flags and tagged logits hold past epochs, so an epoch is not reused
+     * until the state is zeroed again (0 is "never"). */
+    if (G.depoch == UINT32_MAX && !dsync_reset()) {
+        cmd_fail(c, hipErrorUnknown, "moe_layer: decode hand-off state");
+        return false;
+    }
+    ++G.depoch;
     hipEvent_t ev[2] = { NULL, NULL };
     const int per_kernel = G.prof && (ev[0] = cmd_event(c, 0)) && (ev[1] = cmd_event(c, 0));
     const int rc = qwk_moe_decode(G.stream, out, idx, w, x, res, &m, rows, S, need, G.dsync, G.depoch,
