@@ -400,9 +400,12 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
     const int o = b * QD_RT_ROWS + wave;
     float *xl = lds, *pbase = lds + nch * QD_XPAD, *part = pbase + wave * 64;
     if constexpr (RES) qd_norm_rows(a, qinv, qpart);
-    // the token rows, staged as q16 units for the gate / up roles
+    // the token rows, staged as q16 units for the gate / up workgroups that
+    // do not stage x themselves (there are none for one token); unit
+    // b + n_rt * thread, so every router workgroup takes a few
     const int units = H / 16;
-    for (int i = b * QD_THREADS + threadIdx.x; i < a.rows * units; i += a.n_rt * QD_THREADS) {
+    for (int i = a.rows > 1 ? b + a.n_rt * (int)threadIdx.x : a.rows * units; i < a.rows * units;
+         i += a.n_rt * QD_THREADS) {
         float v[16];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
