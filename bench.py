@@ -238,6 +238,105 @@ def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444):
                         "fresh token on the device and the closing residual step"}
 
 
+def bench_hc(gpu, steps, H=3072, S=4, k=320, G=64, pool=96, prefill_rows=2048, seed=777):
+    """The hyper-connection mixer around one block at config
+    1's width: decode (one token: inject + grouped norm, mix-down, the
+    injection logits, the fused mix-up) over a pool of `pool` weight sets
+    (~390 MB, past the Infinity Cache), and the prefill form at
+    `prefill_rows` tokens (the same with the 4-bit products as GEMMs and the
+    mix as its own pass)."""
+    from qwasar_amd import synth
+    B = gpu.Buf
+    HH = S * H
+
+    def q4(name, rows, cols):
+        w, sc, bi = B(rows * cols // 2), B(rows * cols // G * 2), B(rows * cols // G * 2)
+        kk = synth.sm_key(seed, name + ".scales")
+        gpu.qw_op_synth(c, w.ref(), synth.SYNTH_U32, rows * cols // 8, synth.sm_key(seed, name + ".w"), 0.0, 0.0)
+        gpu.qw_op_synth(c, sc.ref(), synth.SYNTH_BF16_UNIFORM, rows * cols // G, kk, 0.001, 0.02)
+        gpu.qw_op_synth(c, bi.ref(), synth.SYNTH_BF16_NEG8, rows * cols // G, kk, 0.001, 0.02)
+        return w, sc, bi
+
+    sets = []
+    c = gpu.qw_cmd_begin()
+    for p in range(pool):
+        wn, bj = B(HH * 2), B(S * HH * 2)
+        gpu.qw_op_synth(c, wn.ref(), synth.SYNTH_BF16_UNIFORM, HH, synth.sm_key(seed, f"hc{p}.norm"), 0.9, 1.1)
+        gpu.qw_op_synth(c, bj.ref(), synth.SYNTH_BF16_NORMAL, S * HH, synth.sm_key(seed, f"hc{p}.inj"), 0.02, 0.0)
+        sets.append((wn, q4(f"hc{p}.down", k, HH), q4(f"hc{p}.up", HH, k), bj))
+    rows = prefill_rows
+    h4, n4, out = B(rows * HH * 4), B(rows * HH * 4), B(rows * H * 4)
+    inj, d, x, m = B(rows * S * 4), B(rows * k * 4), B(rows * H * 4), B(rows * HH * 4)
+    gpu.qw_op_synth(c, h4.ref(), synth.SYNTH_F32_BF16_NORMAL, rows * HH, synth.sm_key(seed, "h4"), 1.0, 0.0)
+    gpu.qw_op_synth(c, out.ref(), synth.SYNTH_F32_BF16_NORMAL, rows * H, synth.sm_key(seed, "out"), 1.0, 0.0)
+    gpu.qw_op_synth(c, inj.ref(), synth.SYNTH_F32_BF16_NORMAL, rows * S, synth.sm_key(seed, "inj"), 1.0, 0.0)
+    gpu.run(c, "hc mixer setup")
+
+    def decode_step(c, p):
+        wn, (dw, ds, db), (uw, us, ub), bj = sets[p % pool]
+        gpu.qw_op_hc_inject_norm(c, h4.ref(), out.ref(), inj.ref(), wn.ref(), n4.ref(), 1, H, S, 1e-6)
+        gpu.qw_op_qmv_q4(c, d.ref(), n4.ref(), dw.ref(), ds.ref(), db.ref(), HH, k, 1, G)
+        gpu.qw_op_dmat_bf16(c, inj.ref(), n4.ref(), bj.ref(), HH, S, 1)
+        gpu.qw_op_hc_mix_up(c, x.ref(), d.ref(), n4.ref(), uw.ref(), us.ref(), ub.ref(), k, H, S, 1, 1.0 / S, G)
+
+    c = gpu.qw_cmd_begin()
+    for p in range(pool):
+        decode_step(c, p)
+    gpu.run(c, "hc decode warm-up")
+    gpu.qw_prof_reset()
+    gpu.qw_prof_set_enabled(True)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_prof_set_enabled(False)
+    for p in range(steps):
+        decode_step(c, p)
+    gpu.qw_prof_set_enabled(True)
+    gpu.qw_cmd_mark(c, b"hc decode region")
+    gpu.run(c, "hc decode")
+    dec_ms = gpu.qw_prof_ms(b"hc decode region", None)
+
+    wn, (dw, ds, db), (uw, us, ub), bj = sets[0]
+
+    def prefill(c):
+        gpu.qw_op_hc_inject_norm(c, h4.ref(), out.ref(), inj.ref(), wn.ref(), n4.ref(), rows, H, S, 1e-6)
+        gpu.qw_op_qmat_q4(c, d.ref(), n4.ref(), dw.ref(), ds.ref(), db.ref(), HH, k, rows, G)
+        gpu.qw_op_dmat_bf16(c, inj.ref(), n4.ref(), bj.ref(), HH, S, rows)
+        gpu.qw_op_silu_scale(c, d.ref(), rows * k, 1.0 / S)
+        gpu.qw_op_qmat_q4(c, m.ref(), d.ref(), uw.ref(), us.ref(), ub.ref(), k, HH, rows, G)
+        gpu.qw_op_hc_mix(c, x.ref(), n4.ref(), m.ref(), rows, H, S)
+
+    c = gpu.qw_cmd_begin()
+    prefill(c)
+    gpu.run(c, "hc prefill warm-up")
+    gpu.qw_prof_reset()
+    gpu.qw_prof_set_enabled(True)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_prof_set_enabled(False)
+    reps = 5
+    for _ in range(reps):
+        prefill(c)
+    gpu.qw_prof_set_enabled(True)
+    gpu.qw_cmd_mark(c, b"hc prefill region")
+    gpu.run(c, "hc prefill")
+    pf_ms = gpu.qw_prof_ms(b"hc prefill region", None) / reps
+    gpu.qw_prof_set_enabled(False)
+    gpu.qw_prof_reset()
+    for wn_, (a1, a2, a3), (b1, b2, b3), bj_ in sets:
+        for t in (wn_, a1, a2, a3, b1, b2, b3, bj_):
+            t.free()
+    for t in (h4, n4, out, inj, d, x, m):
+        t.free()
+    us_tok = dec_ms * 1000.0 / steps
+    wbytes = 2 * (k * HH // 2 + k * HH // G * 4) + S * HH * 2 + HH * 2
+    abytes = HH * 4 * 3 + H * 4 * 2 + k * 4 * 2          # h4 read and written, n4 written; out, x; d
+    flops = 2.0 * rows * (2 * HH * k + HH * S)
+    return {"shape": {"H": H, "S": S, "lowrank": k, "group": G},
+            "decode": {"us_per_token": round(us_tok, 2), "weight_bytes": wbytes,
+                       "hbm_gbs": round((wbytes + abytes) / (us_tok * 1e-6) / 1e9, 1),
+                       "launches": 4, "weight_sets": pool},
+            "prefill": {"rows": rows, "ms": round(pf_ms, 3),
+                        "tflops": round(flops / (pf_ms * 1e-3) / 1e12, 2)}}
+
+
 def cpu_baseline(L, xpool, seconds):
     """The oracle (the reference's scalar moe_step restated in C, one thread)
     on the same decode tokens, for a bounded time."""
@@ -271,6 +370,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-config4", action="store_true", help="skip the 48-layer stack (config 4)")
     ap.add_argument("--config4-only", action="store_true", help="run only the 48-layer stack and print it")
+    ap.add_argument("--no-hc", action="store_true", help="skip the hyper-connection mixer")
+    ap.add_argument("--hc-only", action="store_true", help="run only the hyper-connection mixer and print it")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--calib-copy", type=int, default=0, help="bytes: run only the copy calibration")
     ap.add_argument("--decode-only-steps", type=int, default=0,
@@ -295,6 +396,9 @@ def main():
     cand = synth.make_x(seed, 2048, L.H, name="bench.candidates")
     xpool, pool_ids = select_cold_pool(gpu, lb, cand, L.K)
 
+    if args.hc_only:
+        print(json.dumps({"hc_mixer": bench_hc(gpu, 200)}), flush=True)
+        return
     if args.config4_only:
         print(json.dumps({"config4": bench_stack(gpu, 48, 2048, 256, 4)}), flush=True)
         return
@@ -373,6 +477,8 @@ def main():
 
     if not args.no_config4:
         out["config4"] = bench_stack(gpu, 48, 2048, 256, 4)
+    if not args.no_hc:
+        out["hc_mixer"] = bench_hc(gpu, 200)
 
     if not args.no_cpu:
         us, n = cpu_baseline(L, xpool, args.cpu_seconds)

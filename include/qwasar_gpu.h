@@ -138,6 +138,30 @@ void qw_op_rms_norm(qw_cmd c, qw_ref y, qw_ref x, qw_ref weight,
 void qw_op_swiglu(qw_cmd c, qw_ref y, qw_ref gate, qw_ref up, int32_t n);
 void qw_op_add_inplace(qw_cmd c, qw_ref y, qw_ref x, int32_t n);
 
+/* ---- the hyper-connection mixer around a block (reference qwasar_gpu.h:549-578) -
+ *
+ * S streams of H per row (h4 [rows, S*H]).  H % 4 == 0 here. */
+
+/* h4 += out (x) 2*sigmoid(inj / S) per stream, then n4 = the streams normed
+ * with gains w (qw_op_hc_inject, qw_op_rms_norm_grouped): one pass. */
+void qw_op_hc_inject_norm(qw_cmd c, qw_ref h4, qw_ref out, qw_ref inj, qw_ref w, qw_ref n4,
+                          int32_t rows, int32_t H, int32_t S, float eps);
+/* x = mean_s sigmoid(W_s . silu(scale * d)) * n4_s, W_s the up-projection's
+ * rows s*H.. (4-bit, `group`), for few rows.  False, nothing encoded, if S > 4. */
+bool qw_op_hc_mix_up(qw_cmd c, qw_ref x, qw_ref d, qw_ref n4, qw_ref w, qw_ref scales, qw_ref biases,
+                     int32_t k, int32_t H, int32_t S, int32_t rows, float scale, int32_t group);
+/* h4[r, s*H+i] = x[r, i]. */
+void qw_op_repeat_cols(qw_cmd c, qw_ref h4, qw_ref x, int32_t rows, int32_t H, int32_t S);
+/* Grouped RMS norm: `groups` streams of `dim` per row, weight [groups*dim]. */
+void qw_op_rms_norm_grouped(qw_cmd c, qw_ref y, qw_ref x, qw_ref weight,
+                            int32_t dim, int32_t groups, int32_t rows, float eps);
+/* y = silu(y * scale) in place. */
+void qw_op_silu_scale(qw_cmd c, qw_ref y, int32_t n, float scale);
+/* x[r] = mean over streams of sigmoid(m) * n. */
+void qw_op_hc_mix(qw_cmd c, qw_ref x, qw_ref n, qw_ref m, int32_t rows, int32_t H, int32_t S);
+/* h4 += out (x) 2*sigmoid(inj / S), per stream. */
+void qw_op_hc_inject(qw_cmd c, qw_ref h4, qw_ref out, qw_ref inj, int32_t rows, int32_t H, int32_t S);
+
 /* ---- the MoE block (reference qwasar_gpu.h:559-616) ------------------------- */
 
 /* out[r] = sum_k w[r,k] y[r*K+k] + sigmoid(g[r]) sh[r]. */

@@ -276,3 +276,56 @@ void qr_rms_norm(float *y, const float *x, int32_t dim, int32_t rows, float eps)
         for (int32_t i = 0; i < dim; i++) yr[i] = xr[i] * inv;
     }
 }
+
+/* ---- the hyper-connection mixer ------------------------------------------- */
+
+void qr_rms_norm_grouped(float *y, const float *x, const uint16_t *w, int32_t dim, int32_t groups,
+                         int32_t rows, float eps) {
+    /* qwasar_flash_cpu.c:57-70 per row: each group normalised on its own
+     * (qwasar_cpu.c:68-82's form), times its slice of the full-width weight */
+    for (int32_t r = 0; r < rows; r++)
+        for (int32_t g = 0; g < groups; g++) {
+            const size_t o = ((size_t)r * groups + g) * (size_t)dim;
+            float ss = 0.0f;
+            for (int32_t i = 0; i < dim; i++) ss += x[o + i] * x[o + i];
+            const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+            for (int32_t i = 0; i < dim; i++) {
+                float v = x[o + i] * inv;
+                v *= qr_bf16_to_f32(w[(size_t)g * dim + i]);
+                y[o + i] = v;
+            }
+        }
+}
+
+void qr_silu_scale(float *y, int64_t n, float scale) {
+    for (int64_t i = 0; i < n; i++) y[i] = qr_silu(y[i] * scale);
+}
+
+void qr_hc_mix(float *x, const float *n, const float *m, int32_t rows, int32_t H, int32_t S) {
+    /* qwasar_flash_cpu.c:275-282 */
+    for (int32_t r = 0; r < rows; r++)
+        for (int32_t i = 0; i < H; i++) {
+            float acc = 0.0f;
+            for (int32_t s = 0; s < S; s++) {
+                const size_t j = (size_t)r * S * H + (size_t)s * H + i;
+                acc += qr_sigmoid(m[j]) * n[j];
+            }
+            x[(size_t)r * H + i] = acc / (float)S;
+        }
+}
+
+void qr_hc_inject(float *h4, const float *out, const float *inj, int32_t rows, int32_t H, int32_t S) {
+    /* qwasar_flash_cpu.c:283-285 and :289-293, with the GPU op's raw logits */
+    for (int32_t r = 0; r < rows; r++)
+        for (int32_t s = 0; s < S; s++) {
+            const float wgt = 2.0f * qr_sigmoid(inj[(size_t)r * S + s] / (float)S);
+            for (int32_t i = 0; i < H; i++)
+                h4[((size_t)r * S + s) * H + i] += out[(size_t)r * H + i] * wgt;
+        }
+}
+
+void qr_repeat_cols(float *h4, const float *x, int32_t rows, int32_t H, int32_t S) {
+    for (int32_t r = 0; r < rows; r++)
+        for (int32_t s = 0; s < S; s++)
+            for (int32_t i = 0; i < H; i++) h4[((size_t)r * S + s) * H + i] = x[(size_t)r * H + i];
+}

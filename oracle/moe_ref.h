@@ -120,6 +120,22 @@ void qr_moe_forward(float *out, int32_t *idx, float *w, const float *x, int32_t 
 /* One RMS norm with unit weight, eps (qwasar_cpu.c:68-82). */
 void qr_rms_norm(float *y, const float *x, int32_t dim, int32_t rows, float eps);
 
+/* ---- the hyper-connection mixer around a block (qwasar_flash_cpu.c:57-70,
+ * 263-293; the GPU ops' semantics, metal/sparse.metal:14-189) ---------------- */
+
+/* y[r, g*dim + i] = x * inv_g * w[g*dim + i], inv_g over group g of row r,
+ * each group in the form of qwasar_cpu.c:68-82. */
+void qr_rms_norm_grouped(float *y, const float *x, const uint16_t *w, int32_t dim, int32_t groups,
+                         int32_t rows, float eps);
+/* y = silu(y * scale), n elements. */
+void qr_silu_scale(float *y, int64_t n, float scale);
+/* x[r, i] = (sum over s, in order, of sigmoid(m[r, s*H+i]) * n[r, s*H+i]) / S. */
+void qr_hc_mix(float *x, const float *n, const float *m, int32_t rows, int32_t H, int32_t S);
+/* h4[r, s*H+i] += out[r, i] * (2 * sigmoid(inj[r, s] / S)). */
+void qr_hc_inject(float *h4, const float *out, const float *inj, int32_t rows, int32_t H, int32_t S);
+/* h4[r, s*H+i] = x[r, i]. */
+void qr_repeat_cols(float *h4, const float *x, int32_t rows, int32_t H, int32_t S);
+
 #ifdef __cplusplus
 }
 #endif

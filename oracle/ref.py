@@ -72,6 +72,11 @@ def lib():
         L.qr_silu.argtypes = [C.c_float]
         L.qr_moe_forward.argtypes = [_P, _P, _P, _P, _I, C.POINTER(_Moe)]
         L.qr_rms_norm.argtypes = [_P, _P, _I, _I, C.c_float]
+        L.qr_rms_norm_grouped.argtypes = [_P, _P, _P, _I, _I, _I, C.c_float]
+        L.qr_silu_scale.argtypes = [_P, C.c_int64, C.c_float]
+        L.qr_hc_mix.argtypes = [_P, _P, _P, _I, _I, _I]
+        L.qr_hc_inject.argtypes = [_P, _P, _P, _I, _I, _I]
+        L.qr_repeat_cols.argtypes = [_P, _P, _I, _I, _I]
         _lib = L
     return _lib
 
@@ -199,3 +204,52 @@ def stack_forward(layers, h0: np.ndarray, eps: float = STACK_EPS):
         trace.append((x, y))
         h, x = residual_norm(h, y, eps)
     return h, trace
+
+
+# ---- the hyper-connection mixer -------------------------------
+
+def rms_norm_grouped(x: np.ndarray, w: np.ndarray, dim: int, groups: int, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.uint16)
+    y = np.empty_like(x)
+    rows = x.size // (dim * groups)
+    lib().qr_rms_norm_grouped(_ptr(y), _ptr(x), _ptr(w), dim, groups, rows, eps)
+    return y
+
+
+def silu_scale(y: np.ndarray, scale: float) -> np.ndarray:
+    y = np.array(y, np.float32, copy=True)
+    lib().qr_silu_scale(_ptr(y), y.size, scale)
+    return y
+
+
+def hc_mix(n: np.ndarray, m: np.ndarray, rows: int, H: int, S: int) -> np.ndarray:
+    n = np.ascontiguousarray(n, np.float32)
+    m = np.ascontiguousarray(m, np.float32)
+    x = np.empty((rows, H), np.float32)
+    lib().qr_hc_mix(_ptr(x), _ptr(n), _ptr(m), rows, H, S)
+    return x
+
+
+def hc_inject(h4: np.ndarray, out: np.ndarray, inj: np.ndarray, rows: int, H: int, S: int) -> np.ndarray:
+    h4 = np.array(h4, np.float32, copy=True)
+    out = np.ascontiguousarray(out, np.float32)
+    inj = np.ascontiguousarray(inj, np.float32)
+    lib().qr_hc_inject(_ptr(h4), _ptr(out), _ptr(inj), rows, H, S)
+    return h4
+
+
+def repeat_cols(x: np.ndarray, rows: int, H: int, S: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    h4 = np.empty((rows, S * H), np.float32)
+    lib().qr_repeat_cols(_ptr(h4), _ptr(x), rows, H, S)
+    return h4
+
+
+def hc_mix_up(d, n4, w, s, b, k, H, S, rows, scale, group):
+    """x = mean_s sigmoid(W_s . silu(scale * d)) * n4_s: the reference's
+    silu_scale, the up-projection's matvec (qwasar_flash_cpu.c:272-273) and
+    hc_mix, composed."""
+    ds = silu_scale(np.asarray(d, np.float32).reshape(rows, k), scale)
+    m = qmv_q4(ds, w, s, b, k, S * H, rows, group)
+    return hc_mix(n4, m, rows, H, S)

@@ -1,0 +1,249 @@
+// qw_hc.hip -- the hyper-connection mixer that wraps every Flash-Next block
+// (the step on either side of the MoE layer; reference semantics
+// metal/sparse.metal:14-189, qwasar_flash_cpu.c:57-70 and 263-293):
+//
+//   n4  = grouped_rms_norm(h4) * w            (S streams of H, each its own norm)
+//   x   = mean_s sigmoid(up(silu(down(n4) / S)))_s * n4_s
+//   inj = block_inject(n4)                    (raw logits, [S])
+//   h4 += out (x) 2 sigmoid(inj / S)          (a block's output into the streams)
+//
+// Memory-bound elementwise and row kernels, and one fused GEMV for the
+// mixer's up-projection at few rows.  The row sums run in the order of
+// qw_norm.hip: each of 256 threads an fmaf chain over its float4 chunks, the
+// xor tree, the four wave partials in order.
+#include "qw_device.h"
+#include "qw_kernels.h"
+
+#define QH_THREADS 256
+
+__device__ __forceinline__ float qh_sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+__device__ __forceinline__ float qh_block_sum(float v, float *part)
+{
+    v = qw_xor_sum<64>(v);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) part[wave] = v;
+    __syncthreads();
+    float s = part[0];
+#pragma unroll
+    for (int i = 1; i < QH_THREADS / 64; i++) s = s + part[i];
+    return s;
+}
+
+// h4[r, s*H + i] = x[r, i]
+__global__ void k_repeat_cols(float4 *__restrict__ h4, const float4 *__restrict__ x, int rows, int H4, int S)
+{
+    const int64_t n = (int64_t)rows * S * H4;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = j / ((int64_t)S * H4);
+        h4[j] = x[r * H4 + j % H4];
+    }
+}
+
+// One workgroup per (row, group): y = x * inv * w[g], dim % 4 == 0.  With
+// `out` and `inj` set, x first takes the block's output (x += out * 2
+// sigmoid(inj / S)) and is written back: qw_hc_inject and the norm in one pass.
+__global__ void __launch_bounds__(QH_THREADS) k_norm_grouped(float *__restrict__ y, float *x,
+                                                             const uint16_t *__restrict__ w, int dim, int groups,
+                                                             float eps, const float *__restrict__ out,
+                                                             const float *__restrict__ inj)
+{
+    __shared__ float part[QH_THREADS / 64];
+    const int q = blockIdx.x, g = q % groups, r = q / groups;
+    float4 *xr = reinterpret_cast<float4 *>(x + (size_t)q * dim);
+    float4 *yr = reinterpret_cast<float4 *>(y + (size_t)q * dim);
+    const uint2 *wr = reinterpret_cast<const uint2 *>(w + (size_t)g * dim);
+    const int n4 = dim / 4;
+    float wgt = 0.0f;
+    const float4 *orow = nullptr;
+    if (out) {
+        wgt = 2.0f * qh_sigmoid(inj[(size_t)r * groups + g] / (float)groups);
+        orow = reinterpret_cast<const float4 *>(out + (size_t)r * dim);
+    }
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n4; i += QH_THREADS) {
+        float4 v = xr[i];
+        if (out) {
+            const float4 o = orow[i];
+            v.x += o.x * wgt; v.y += o.y * wgt; v.z += o.z * wgt; v.w += o.w * wgt;
+            xr[i] = v;
+        }
+        ss = __builtin_fmaf(v.x, v.x, ss);
+        ss = __builtin_fmaf(v.y, v.y, ss);
+        ss = __builtin_fmaf(v.z, v.z, ss);
+        ss = __builtin_fmaf(v.w, v.w, ss);
+    }
+    ss = qh_block_sum(ss, part);
+    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (int i = threadIdx.x; i < n4; i += QH_THREADS) {
+        float4 v = xr[i];   // this thread's own values
+        const uint2 wb = wr[i];
+        v.x = v.x * inv * __uint_as_float(wb.x << 16);
+        v.y = v.y * inv * __uint_as_float(wb.x & 0xFFFF0000u);
+        v.z = v.z * inv * __uint_as_float(wb.y << 16);
+        v.w = v.w * inv * __uint_as_float(wb.y & 0xFFFF0000u);
+        yr[i] = v;
+    }
+}
+
+// y = silu(y * scale)
+__global__ void k_silu_scale(float *__restrict__ y, int64_t n, float scale)
+{
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += (int64_t)gridDim.x * blockDim.x) {
+        const float v = y[j] * scale;
+        y[j] = v * qh_sigmoid(v);
+    }
+}
+
+// x[r, i] = (sum_s sigmoid(m) n, in stream order) / S
+__global__ void k_hc_mix(float *__restrict__ x, const float *__restrict__ n, const float *__restrict__ m, int rows,
+                         int H, int S)
+{
+    const int64_t total = (int64_t)rows * H;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < total; j += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = j / H, i = j % H;
+        float acc = 0.0f;
+        for (int s = 0; s < S; s++) {
+            const int64_t q = r * S * H + (int64_t)s * H + i;
+            acc = acc + qh_sigmoid(m[q]) * n[q];
+        }
+        x[j] = acc / (float)S;
+    }
+}
+
+// h4[r, s*H+i] += out[r, i] * 2 sigmoid(inj[r, s] / S)
+__global__ void k_hc_inject(float *__restrict__ h4, const float *__restrict__ out, const float *__restrict__ inj,
+                            int rows, int H, int S)
+{
+    const int64_t total = (int64_t)rows * S * H;
+    for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < total; j += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = j / ((int64_t)S * H), s = (j / H) % S, i = j % H;
+        h4[j] += out[r * H + i] * (2.0f * qh_sigmoid(inj[r * S + s] / (float)S));
+    }
+}
+
+// The mixer's up-projection, its input silu and the stream mix, for few rows:
+// a wave per output i holds the S up-projection rows s*H + i that feed it
+// (lane: 8-input words wi = lane, lane + 64, ...), each row's dot an fmaf
+// chain over the lane's words then the xor tree; lane 0 mixes the streams in
+// order.  S <= 4.
+__global__ void __launch_bounds__(QH_THREADS) k_hc_mix_up(float *__restrict__ x, const float *__restrict__ d,
+                                                          const float *__restrict__ n4,
+                                                          const uint32_t *__restrict__ w,
+                                                          const uint16_t *__restrict__ sc,
+                                                          const uint16_t *__restrict__ bi, int k, int H, int S,
+                                                          int rows, float scale, int lgG)
+{
+    const int lane = threadIdx.x & 63;
+    const int i = blockIdx.x * (QH_THREADS / 64) + (threadIdx.x >> 6);
+    if (i >= H) return;   // whole waves
+    const int words = k / 8, groups = k >> lgG;
+    for (int r = 0; r < rows; r++) {
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int wi = lane; wi < words; wi += 64) {
+            float xs[8];
+            const float4 *dv = reinterpret_cast<const float4 *>(d + (size_t)r * k + 8 * wi);
+            const float4 d0 = dv[0], d1 = dv[1];
+            const float dd[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float v = dd[j] * scale;
+                xs[j] = v * qh_sigmoid(v);
+            }
+            const int gi = (8 * wi) >> lgG;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                if (s >= S) break;
+                const size_t row = (size_t)s * H + i;
+                const uint32_t q = w[row * words + wi];
+                const float sv = __uint_as_float((uint32_t)sc[row * groups + gi] << 16);
+                const float bv = __uint_as_float((uint32_t)bi[row * groups + gi] << 16);
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    acc[s] = __builtin_fmaf(__builtin_fmaf(sv, (float)((q >> (4 * j)) & 0xFu), bv), xs[j], acc[s]);
+            }
+        }
+        float mix = 0.0f;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const float m = qw_xor_sum<64>(acc[s]);
+            if (s < S) mix = mix + qh_sigmoid(m) * n4[(size_t)r * S * H + (size_t)s * H + i];
+        }
+        if (lane == 0) x[(size_t)r * H + i] = mix / (float)S;
+    }
+}
+
+static dim3 qh_grid(int64_t n)
+{
+    const int64_t b = (n + QH_THREADS - 1) / QH_THREADS;
+    return dim3((unsigned)(b < 16384 ? (b > 0 ? b : 1) : 16384));
+}
+
+extern "C" int qwk_repeat_cols(hipStream_t s, float *h4, const float *x, int rows, int H, int S)
+{
+    if (rows <= 0) return 0;
+    if (H % 4 || S < 1 || ((uintptr_t)h4 & 15u) || ((uintptr_t)x & 15u)) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_repeat_cols, qh_grid((int64_t)rows * S * H / 4), dim3(QH_THREADS), 0, s,
+                       reinterpret_cast<float4 *>(h4), reinterpret_cast<const float4 *>(x), rows, H / 4, S);
+    return (int)hipGetLastError();
+}
+
+extern "C" int qwk_rms_norm_grouped(hipStream_t s, float *y, const float *x, const uint16_t *w, int dim, int groups,
+                                    int rows, float eps)
+{
+    if (rows <= 0) return 0;
+    if (dim <= 0 || dim % 4 || groups < 1 || !w || ((uintptr_t)x & 15u) || ((uintptr_t)y & 15u) || ((uintptr_t)w & 7u))
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_norm_grouped, dim3((unsigned)(rows * groups)), dim3(QH_THREADS), 0, s, y,
+                       const_cast<float *>(x), w, dim, groups, eps, nullptr, nullptr);
+    return (int)hipGetLastError();
+}
+
+extern "C" int qwk_hc_inject_norm(hipStream_t s, float *h4, const float *out, const float *inj, const uint16_t *w,
+                                  float *n4, int rows, int H, int S, float eps)
+{
+    if (rows <= 0) return 0;
+    if (H <= 0 || H % 4 || S < 1 || !w || !out || !inj || ((uintptr_t)h4 & 15u) || ((uintptr_t)n4 & 15u) ||
+        ((uintptr_t)out & 15u) || ((uintptr_t)w & 7u))
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_norm_grouped, dim3((unsigned)(rows * S)), dim3(QH_THREADS), 0, s, n4, h4, w, H, S, eps, out,
+                       inj);
+    return (int)hipGetLastError();
+}
+
+extern "C" int qwk_silu_scale(hipStream_t s, float *y, int64_t n, float scale)
+{
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_silu_scale, qh_grid(n), dim3(QH_THREADS), 0, s, y, n, scale);
+    return (int)hipGetLastError();
+}
+
+extern "C" int qwk_hc_mix(hipStream_t s, float *x, const float *n, const float *m, int rows, int H, int S)
+{
+    if (rows <= 0) return 0;
+    if (H <= 0 || S < 1) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_hc_mix, qh_grid((int64_t)rows * H), dim3(QH_THREADS), 0, s, x, n, m, rows, H, S);
+    return (int)hipGetLastError();
+}
+
+extern "C" int qwk_hc_inject(hipStream_t s, float *h4, const float *out, const float *inj, int rows, int H, int S)
+{
+    if (rows <= 0) return 0;
+    if (H <= 0 || S < 1) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_hc_inject, qh_grid((int64_t)rows * S * H), dim3(QH_THREADS), 0, s, h4, out, inj, rows, H, S);
+    return (int)hipGetLastError();
+}
+
+extern "C" int qwk_hc_mix_up(hipStream_t s, float *x, const float *d, const float *n4, const uint32_t *w,
+                             const uint16_t *sc, const uint16_t *bi, int k, int H, int S, int rows, float scale,
+                             int group)
+{
+    if (rows <= 0) return 0;
+    if (S < 1 || S > 4 || k <= 0 || k % 8 || H <= 0 || (group != 32 && group != 64 && group != 128) ||
+        k % group || ((uintptr_t)d & 15u))
+        return (int)hipErrorInvalidValue;
+    const int lgG = group == 32 ? 5 : group == 64 ? 6 : 7;
+    hipLaunchKernelGGL(k_hc_mix_up, dim3((unsigned)((H + 3) / 4)), dim3(QH_THREADS), 0, s, x, d, n4, w, sc, bi, k, H,
+                       S, rows, scale, lgG);
+    return (int)hipGetLastError();
+}

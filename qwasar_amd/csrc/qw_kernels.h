@@ -155,6 +155,18 @@ int qwk_resid_rms_bf16(hipStream_t s, const uint16_t *h, uint16_t *h_out, float 
 #define QWK_SYNTH_F32_BF16_NORMAL 4 /* kind 3's value, stored as fp32 */
 int qwk_synth(hipStream_t s, void *dst, int kind, int64_t n, uint64_t key, float a, float b);
 
+/* The hyper-connection mixer around a block (qw_hc.hip); H % 4 == 0. */
+int qwk_repeat_cols(hipStream_t s, float *h4, const float *x, int rows, int H, int S);
+int qwk_rms_norm_grouped(hipStream_t s, float *y, const float *x, const uint16_t *w, int dim, int groups,
+                         int rows, float eps);
+int qwk_hc_inject_norm(hipStream_t s, float *h4, const float *out, const float *inj, const uint16_t *w,
+                       float *n4, int rows, int H, int S, float eps);
+int qwk_silu_scale(hipStream_t s, float *y, int64_t n, float scale);
+int qwk_hc_mix(hipStream_t s, float *x, const float *n, const float *m, int rows, int H, int S);
+int qwk_hc_inject(hipStream_t s, float *h4, const float *out, const float *inj, int rows, int H, int S);
+int qwk_hc_mix_up(hipStream_t s, float *x, const float *d, const float *n4, const uint32_t *w,
+                  const uint16_t *sc, const uint16_t *bi, int k, int H, int S, int rows, float scale, int group);
+
 #ifdef __cplusplus
 }
 #endif

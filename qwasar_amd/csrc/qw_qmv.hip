@@ -115,6 +115,73 @@ __global__ __launch_bounds__(QW_MV_WAVES * 64) void k_q4mv(QwMvArgs a)
     }
 }
 
+// Few rows over a long input (the mixer's down-projection at decode: n = 320,
+// k = 4 H), where a wave per RIT rows would leave most CUs idle: a
+// workgroup per row slot set, its QW_MV_WAVES waves splitting the segments
+// (wave w takes segments w, w + QW_MV_WAVES, ... of each lane's walk), the
+// wave partials added in wave order through LDS.  One matrix, one token row,
+// no expert index.
+template <int G, int LPR>
+__global__ __launch_bounds__(QW_MV_WAVES * 64) void k_q4mv_ks(QwMvArgs a)
+{
+    constexpr int SLOTS = 64 / LPR;
+    __shared__ float part[QW_MV_WAVES][SLOTS];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int slot = lane / LPR, lr = lane % LPR;
+    const int n = a.n[0], k = a.k, words = k / 8, groups = k / G;
+    const int row = blockIdx.x * SLOTS + slot;
+    const bool live = row < n;
+    const uint32_t *wr = a.m[0].w + (size_t)(live ? row : 0) * words;
+    const uint16_t *sr = a.m[0].s + (size_t)(live ? row : 0) * groups;
+    const uint16_t *br = a.m[0].b + (size_t)(live ? row : 0) * groups;
+    const int spl = (k / 32) / LPR;
+    float acc = 0.0f;
+    for (int j = wave; j < spl; j += QW_MV_WAVES) {
+        const int seg = j * LPR + lr;
+        const int g = seg * 32 / G;
+        const uint4 wv = *reinterpret_cast<const uint4 *>(wr + seg * 4);
+        const float sc = qw_bf16(sr[g]), bi = qw_bf16(br[g]);
+        float xs[32];
+        const float4 *xv = reinterpret_cast<const float4 *>(a.x + seg * 32);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const float4 t = xv[q];
+            xs[4 * q] = t.x; xs[4 * q + 1] = t.y; xs[4 * q + 2] = t.z; xs[4 * q + 3] = t.w;
+        }
+        float xsum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) xsum += xs[i];
+        float d = qw_dot8_q(wv.x, xs, 0.0f);
+        d = qw_dot8_q(wv.y, xs + 8, d);
+        d = qw_dot8_q(wv.z, xs + 16, d);
+        d = qw_dot8_q(wv.w, xs + 24, d);
+        acc = __builtin_fmaf(sc, d, acc);
+        acc = __builtin_fmaf(bi, xsum, acc);
+    }
+    acc = qw_xor_sum<LPR>(acc);
+    if (lr == 0) part[wave][slot] = acc;
+    __syncthreads();
+    if (wave == 0 && lr == 0 && live) {
+        float v = part[0][slot];
+#pragma unroll
+        for (int w = 1; w < QW_MV_WAVES; w++) v = v + part[w][slot];
+        a.y[0][row] = v;
+    }
+}
+
+template <int G>
+static void launch_ks(int lpr, int n, hipStream_t s, const QwMvArgs &a)
+{
+    const dim3 blk(QW_MV_WAVES * 64);
+    const int slots = 64 / lpr;
+    const dim3 grid((unsigned)((n + slots - 1) / slots));
+    switch (lpr) {
+    case 64: hipLaunchKernelGGL((k_q4mv_ks<G, 64>), grid, blk, 0, s, a); break;
+    case 32: hipLaunchKernelGGL((k_q4mv_ks<G, 32>), grid, blk, 0, s, a); break;
+    default: hipLaunchKernelGGL((k_q4mv_ks<G, 16>), grid, blk, 0, s, a); break;
+    }
+}
+
 static int qw_lpr(int k)
 {
     const int S = k / 32;
@@ -145,6 +212,16 @@ static int qw_mv_launch(hipStream_t s, const QwMvArgs &a, int nmat, int group, b
     int nmax = 0;
     for (int i = 0; i < nmat; i++) nmax = a.n[i] > nmax ? a.n[i] : nmax;
     const dim3 grid((nmax + rpb - 1) / rpb, a.pairs, nmat);
+    // Split the segments across a workgroup's waves when the row plan would
+    // give under 4 waves a CU and each lane has at least 4 segments to walk.
+    if (nmat == 1 && a.pairs == 1 && !a.idx && !swiglu && lpr >= 16 &&
+        (long)grid.x * QW_MV_WAVES < 4L * 256 && (a.k / 32) / lpr >= QW_MV_WAVES) {
+        if (group == 64) launch_ks<64>(lpr, a.n[0], s, a);
+        else if (group == 32) launch_ks<32>(lpr, a.n[0], s, a);
+        else if (group == 128) launch_ks<128>(lpr, a.n[0], s, a);
+        else return (int)hipErrorInvalidValue;
+        return (int)hipGetLastError();
+    }
     if (group == 64) {
         if (swiglu) launch_lpr<64, true>(lpr, grid, s, a); else launch_lpr<64, false>(lpr, grid, s, a);
     } else if (group == 32) {

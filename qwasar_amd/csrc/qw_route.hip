@@ -219,11 +219,62 @@ __global__ __launch_bounds__(QW_DROWS_WAVES * 64) void k_dmat_rows(float *__rest
     }
 }
 
+// Few outputs over a long input (the mixer's injection logits: n = 4, k =
+// 4 H) for a few token rows: a workgroup per output, a thread per 64-input
+// chunk (every load issued before the chain), the chunk partials to LDS and
+// added left to right by one thread a row -- order R, in one memory round trip
+// where a wave per output walks its chunks one after another.
+#define QW_DW_THREADS 256
+#define QW_DW_MAXCH 256
+#define QW_DW_MAXR 8
+__global__ __launch_bounds__(QW_DW_THREADS) void k_dmat_wide(float *__restrict__ y, const float *__restrict__ x,
+                                                             const uint16_t *__restrict__ w, int k, int n, int rows)
+{
+    __shared__ float part[QW_DW_MAXCH][QW_DW_MAXR];
+    const int o = blockIdx.x, c = threadIdx.x, nch = k / 64;
+    if (c < nch) {
+        const uint4 *wv = reinterpret_cast<const uint4 *>(w + (size_t)o * k + 64 * c);
+        uint4 ww[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) ww[q] = wv[q];
+        for (int r = 0; r < rows; r++) {
+            const float4 *xv = reinterpret_cast<const float4 *>(x + (size_t)r * k + 64 * c);
+            float4 xa[16];
+#pragma unroll
+            for (int q = 0; q < 16; q++) xa[q] = xv[q];
+            float t = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const uint32_t wd[4] = {ww[q].x, ww[q].y, ww[q].z, ww[q].w};
+                const float4 a = xa[2 * q], b = xa[2 * q + 1];
+                const float xx[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    t = __builtin_fmaf(__uint_as_float(wd[j] << 16), xx[2 * j], t);
+                    t = __builtin_fmaf(__uint_as_float(wd[j] & 0xFFFF0000u), xx[2 * j + 1], t);
+                }
+            }
+            part[c][r] = t;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < rows) {
+        const int r = threadIdx.x;
+        float tot = part[0][r];
+        for (int i = 1; i < nch; i++) tot = tot + part[i][r];
+        y[(size_t)r * n + o] = tot;
+    }
+}
+
 extern "C" int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint16_t *w,
                              int k, int n, int rows)
 {
     if (k < 1 || k > QWK_DMAT_MAX_K || n < 1 || rows < 1) return (int)hipErrorInvalidValue;
     const bool vec = k % 8 == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)x % 16) == 0;
+    if (vec && k % 64 == 0 && n < 8 && rows <= QW_DW_MAXR && k / 64 <= QW_DW_MAXCH && k >= 64 * 64) {
+        hipLaunchKernelGGL(k_dmat_wide, dim3((unsigned)n), dim3(QW_DW_THREADS), 0, s, y, x, w, k, n, rows);
+        return (int)hipGetLastError();
+    }
     if (vec && k % 64 == 0 && n < 8 && rows >= 8) {
         const long items = (long)rows * n;
         hipLaunchKernelGGL(k_dmat_rows, dim3((unsigned)((items + QW_DROWS_WAVES - 1) / QW_DROWS_WAVES)),

@@ -469,6 +469,57 @@ void qw_op_residual_rms_norm_bf16(qw_cmd c, qw_ref h, qw_ref x, qw_ref y, int32_
     launched(c, "residual_rms_norm_bf16", qwk_resid_rms_bf16(G.stream, dp(h), dp(h), dp(x), dp(y), dim, rows, eps));
 }
 
+/* ---- the hyper-connection mixer (reference qwasar_gpu.h:549-578) ------------ */
+
+void qw_op_repeat_cols(qw_cmd c, qw_ref h4, qw_ref x, int32_t rows, int32_t H, int32_t S) {
+    QW_OP(c);
+    touch(c, x, 0); touch(c, h4, 1);
+    launched(c, "repeat_cols", qwk_repeat_cols(G.stream, dp(h4), dp(x), rows, H, S));
+}
+
+void qw_op_rms_norm_grouped(qw_cmd c, qw_ref y, qw_ref x, qw_ref weight,
+                            int32_t dim, int32_t groups, int32_t rows, float eps) {
+    QW_OP(c);
+    touch(c, x, 0); touch(c, weight, 0); touch(c, y, 1);
+    launched(c, "rms_norm_grouped", qwk_rms_norm_grouped(G.stream, dp(y), dp(x), dp(weight), dim, groups, rows, eps));
+}
+
+void qw_op_hc_inject_norm(qw_cmd c, qw_ref h4, qw_ref out, qw_ref inj, qw_ref w, qw_ref n4,
+                          int32_t rows, int32_t H, int32_t S, float eps) {
+    QW_OP(c);
+    touch(c, out, 0); touch(c, inj, 0); touch(c, w, 0); touch(c, h4, 1); touch(c, n4, 1);
+    launched(c, "hc_inject_norm", qwk_hc_inject_norm(G.stream, dp(h4), dp(out), dp(inj), dp(w), dp(n4), rows, H, S, eps));
+}
+
+bool qw_op_hc_mix_up(qw_cmd c, qw_ref x, qw_ref d, qw_ref n4, qw_ref w, qw_ref scales, qw_ref biases,
+                     int32_t k, int32_t H, int32_t S, int32_t rows, float scale, int32_t group) {
+    if (S < 1 || S > 4) return false;
+    if (!c) return true;
+    touch(c, d, 0); touch(c, n4, 0); touch(c, w, 0); touch(c, scales, 0); touch(c, biases, 0); touch(c, x, 1);
+    const int rc = qwk_hc_mix_up(G.stream, dp(x), dp(d), dp(n4), dp(w), dp(scales), dp(biases), k, H, S, rows,
+                                 scale, group);
+    launched(c, "hc_mix_up", rc);
+    return rc == 0;
+}
+
+void qw_op_silu_scale(qw_cmd c, qw_ref y, int32_t n, float scale) {
+    QW_OP(c);
+    touch(c, y, 1);
+    launched(c, "silu_scale", qwk_silu_scale(G.stream, dp(y), n, scale));
+}
+
+void qw_op_hc_mix(qw_cmd c, qw_ref x, qw_ref n, qw_ref m, int32_t rows, int32_t H, int32_t S) {
+    QW_OP(c);
+    touch(c, n, 0); touch(c, m, 0); touch(c, x, 1);
+    launched(c, "hc_mix", qwk_hc_mix(G.stream, dp(x), dp(n), dp(m), rows, H, S));
+}
+
+void qw_op_hc_inject(qw_cmd c, qw_ref h4, qw_ref out, qw_ref inj, int32_t rows, int32_t H, int32_t S) {
+    QW_OP(c);
+    touch(c, out, 0); touch(c, inj, 0); touch(c, h4, 1);
+    launched(c, "hc_inject", qwk_hc_inject(G.stream, dp(h4), dp(out), dp(inj), rows, H, S));
+}
+
 void qw_op_synth(qw_cmd c, qw_ref dst, int32_t kind, int64_t n, uint64_t key, float a, float b) {
     QW_OP(c);
     touch(c, dst, 1);

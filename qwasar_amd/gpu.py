@@ -112,6 +112,13 @@ _sig("qw_op_scale_rows_sigmoid", None, _P, _R, _R, _I, _I)
 _sig("qw_op_moe_layer", _B, _P, _R, _R, _R, _R, C.POINTER(qw_moe_layer), _I)
 _sig("qw_op_moe_layer_residual", _B, _P, _R, _R, _R, _R, _R, _R, _R, C.POINTER(qw_moe_layer), _I, C.c_float)
 _sig("qw_op_rms_norm", None, _P, _R, _R, _R, _I, _I, C.c_float, C.c_float)
+_sig("qw_op_hc_inject_norm", None, _P, _R, _R, _R, _R, _R, _I, _I, _I, C.c_float)
+_sig("qw_op_hc_mix_up", _B, _P, _R, _R, _R, _R, _R, _R, _I, _I, _I, _I, C.c_float, _I)
+_sig("qw_op_repeat_cols", None, _P, _R, _R, _I, _I, _I)
+_sig("qw_op_rms_norm_grouped", None, _P, _R, _R, _R, _I, _I, _I, C.c_float)
+_sig("qw_op_silu_scale", None, _P, _R, _I, C.c_float)
+_sig("qw_op_hc_mix", None, _P, _R, _R, _R, _I, _I, _I)
+_sig("qw_op_hc_inject", None, _P, _R, _R, _R, _I, _I, _I)
 _sig("qw_op_residual_rms_norm_bf16", None, _P, _R, _R, _R, _I, _I, C.c_float)
 _sig("qw_op_synth", None, _P, _R, _I, C.c_int64, C.c_uint64, C.c_float, C.c_float)
 
