@@ -263,6 +263,31 @@ bool qw_op_moe_layer(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,
 bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref h, qw_ref y_prev,
                               qw_ref h_out, qw_ref x_out, const qw_moe_layer *M, int32_t rows, float eps);
 
+/* ---- checkpoint loading (reference qwasar.c:700-775 config, :1426-1461
+ * qw_bind_small, :1469-1495 qw_bind_qbank, :1532-1563 qw_bind_moe) ---------
+ *
+ * A checkpoint directory: config.json (text fields under text_config, or at
+ * the root of a qwen4_exp_text export) and every *.safetensors file in it,
+ * mapped read-only.  NULL / false with a message in err on failure. */
+typedef struct qw_checkpoint_s *qw_checkpoint;
+qw_checkpoint qw_checkpoint_open(const char *dir, char *err, size_t errcap);
+void qw_checkpoint_close(qw_checkpoint ck);
+/* num_hidden_layers */
+int32_t qw_checkpoint_layers(qw_checkpoint ck);
+/* One tensor of the table, by name: its bytes in the mapping (valid until
+ * close), shape and safetensors dtype name.  False if absent. */
+bool qw_checkpoint_tensor(qw_checkpoint ck, const char *name, const void **data, size_t *nbytes,
+                          int32_t *ndim, int64_t shape[8], char dtype[16]);
+/* Layer `layer`'s MoE block (language_model.model.layers.<layer>.mlp) in new
+ * device buffers: the fused `experts.gate_up_proj` bank or the MLX split
+ * `switch_mlp.*` banks (whichever the checkpoint holds), the shared expert,
+ * and the router and shared-expert gate as bf16 -- dequantised from 4 or 8
+ * bits when stored quantised.  Group 32 or 64, read from the scale shapes.
+ * The checkpoint may be closed afterwards. */
+bool qw_moe_layer_load(qw_checkpoint ck, int32_t layer, qw_moe_layer *m, char *err, size_t errcap);
+/* Frees the buffers qw_moe_layer_load made and clears their refs. */
+void qw_moe_layer_free(qw_moe_layer *m);
+
 /* Profiling for harnesses: force profiling on or off (overrides
  * QWASAR_PROFILE), and read one label's accumulated device milliseconds and
  * mark count. */

@@ -285,20 +285,23 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     // nothing for the compiler to wait on or copy): thread t moves row t's
     // run of the block, DS bytes a load, for one cache tag per row per block
     // where a per-chunk load takes one per row per chunk.  A load of wave w
-    // writes DS bytes per lane contiguously, so region j of a block holds
-    // [row][DS bytes]: scales in regions [0, nrg), biases in [nrg, 2 nrg).
+    // writes its lanes LS bytes apart, so region j of a block holds
+    // [row][LS bytes]: scales in regions [0, nrg), biases in [nrg, 2 nrg).
+    // A sub-dword load still puts each lane a dword apart in LDS, so the
+    // 2-byte load (one group a block) has LS = 4, its value in the low half.
     // Blocks follow the stream: block beta = item * nbk + c / sbc.
     const int nblocks = nitems * nbk;
     const int DS = gpb >= 8 ? 16 : gpb >= 2 ? 4 : 2, gpr = DS / 2, nrg = gpb / gpr;   // bytes a load, groups a region
+    const int LS = DS == 2 ? 4 : DS;                                                   // LDS bytes a row a region
     auto fetch_sb = [&](int beta, int q) {
         beta = min(beta, nblocks - 1);
         const int item = beta / nbk, blk = beta % nbk;
         const int h = SWIGLU ? __builtin_amdgcn_readfirstlane(t / (G16_BN / 2)) : 0;
         const int col = colof(item, t), cc = col < a.n ? col : 0;
         const uint32_t o = (uint32_t)((cc * groups + blk * gpb) * 2);
-        // this wave's 64 rows of region j start at j * BN * DS + wave * 64 * DS
+        // this wave's 64 rows of region j start at j * BN * LS + wave * 64 * LS
         __attribute__((address_space(3))) uint8_t *base =
-            (__attribute__((address_space(3))) uint8_t *)(&Sb[q][0]) + wave * 64 * DS;
+            (__attribute__((address_space(3))) uint8_t *)(&Sb[q][0]) + wave * 64 * LS;
         for (int j = 0; j < nrg; j++) {
             if (DS == 16) {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rS[h], base + j * G16_BN * 16, 16, o + 16 * j, 0, 0, 0);
@@ -307,14 +310,14 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rS[h], base + j * G16_BN * 4, 4, o + 4 * j, 0, 0, 0);
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rB[h], base + (nrg + j) * G16_BN * 4, 4, o + 4 * j, 0, 0, 0);
             } else {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rS[h], base + j * G16_BN * 2, 2, o + 2 * j, 0, 0, 0);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rB[h], base + (nrg + j) * G16_BN * 2, 2, o + 2 * j, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rS[h], base + j * G16_BN * 4, 2, o + 2 * j, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rB[h], base + (nrg + j) * G16_BN * 4, 2, o + 2 * j, 0, 0, 0);
             }
         }
     };
     // scale / bias of group gl of LDS row j in block buffer q, as bf16 bits
     auto sb_at = [&](int q, int j, int gl, int bias) -> uint32_t {
-        const uint8_t *p = &Sb[q][((bias ? nrg : 0) + gl / gpr) * G16_BN * DS + j * DS + (gl % gpr) * 2];
+        const uint8_t *p = &Sb[q][((bias ? nrg : 0) + gl / gpr) * G16_BN * LS + j * LS + (gl % gpr) * 2];
         return *reinterpret_cast<const uint16_t *>(p);
     };
     // loads a step issues after the block's: the weights (the wait before the

@@ -186,6 +186,18 @@ qw_buf qw_buf_alloc(size_t len) {
     return b;
 }
 
+/* For the checkpoint loader (qw_load.c), not exported: a device buffer
+ * holding `len` bytes copied from host memory the caller keeps. */
+__attribute__((visibility("hidden"))) qw_buf qw_buf_from_bytes_(const void *src, size_t len) {
+    qw_buf b = qw_buf_alloc(len);
+    if (b && len && hipMemcpy(b->dev, src, len, hipMemcpyHostToDevice) != hipSuccess) {
+        qw_buf_free(b);
+        return NULL;
+    }
+    if (b) b->host_stale = 1;   /* the device copy is the data */
+    return b;
+}
+
 qw_buf qw_buf_wrap(void *ptr, size_t len) {
     if (!ensure_init() || !ptr) return NULL;
     qw_buf b = calloc(1, sizeof *b);

@@ -109,6 +109,13 @@ _sig("qw_op_qmm_q4_gather", None, _P, _R, _R, _R, _R, _R, _R, _R, _I, _I, _I, _I
 _sig("qw_op_swiglu_split", None, _P, _R, _R, _I, _I)
 _sig("qw_op_moe_combine", None, _P, _R, _R, _R, _I, _I, _I)
 _sig("qw_op_scale_rows_sigmoid", None, _P, _R, _R, _I, _I)
+_sig("qw_checkpoint_open", _P, C.c_char_p, C.c_char_p, C.c_size_t)
+_sig("qw_checkpoint_close", None, _P)
+_sig("qw_checkpoint_layers", _I, _P)
+_sig("qw_checkpoint_tensor", _B, _P, C.c_char_p, C.POINTER(_P), C.POINTER(C.c_size_t), C.POINTER(_I),
+     C.POINTER(C.c_int64), C.c_char_p)
+_sig("qw_moe_layer_load", _B, _P, _I, C.POINTER(qw_moe_layer), C.c_char_p, C.c_size_t)
+_sig("qw_moe_layer_free", None, C.POINTER(qw_moe_layer))
 _sig("qw_op_moe_layer", _B, _P, _R, _R, _R, _R, C.POINTER(qw_moe_layer), _I)
 _sig("qw_op_moe_layer_residual", _B, _P, _R, _R, _R, _R, _R, _R, _R, C.POINTER(qw_moe_layer), _I, C.c_float)
 _sig("qw_op_rms_norm", None, _P, _R, _R, _R, _I, _I, C.c_float, C.c_float)

@@ -12,6 +12,12 @@
 2. c0_golden.npz -- BASELINE config 0 (seeded synthetic tensors) with the
    oracle's routing and output for one token, and the tiny-q4 layer on
    seeded inputs with the oracle's routing and outputs: regression vectors.
+3. ckpt_tiny_q4/, ckpt_tiny_mlx/ -- trimmed copies of the two toy
+   checkpoints for the native loader (qw_checkpoint_open /
+   qw_moe_layer_load): the reference's config.json as it is, and the MoE
+   tensors of layers 0 and 1 rewritten byte for byte into safetensors files
+   (two shards for the fused checkpoint, one with the mlx metadata for the
+   split one).  `python tests/golden/make_fixtures.py ckpt` writes only these.
 """
 from __future__ import annotations
 
@@ -119,6 +125,60 @@ def tiny_mlx():
     return out
 
 
+def raw_entries(path):
+    """(name, dtype, shape, bytes) of every tensor, and the metadata."""
+    with open(path, "rb") as f:
+        raw = f.read()
+    n = struct.unpack("<Q", raw[:8])[0]
+    hdr = json.loads(raw[8:8 + n])
+    meta = hdr.pop("__metadata__", None)
+    base = 8 + n
+    return [(k, v["dtype"], v["shape"], raw[base + v["data_offsets"][0]:base + v["data_offsets"][1]])
+            for k, v in hdr.items()], meta
+
+
+def write_safetensors(path, entries, meta=None):
+    hdr, off, body = {}, 0, []
+    if meta is not None:
+        hdr["__metadata__"] = meta
+    for name, dt, shape, data in sorted(entries):
+        hdr[name] = {"dtype": dt, "shape": shape, "data_offsets": [off, off + len(data)]}
+        off += len(data)
+        body.append(data)
+    h = json.dumps(hdr, separators=(",", ":")).encode()
+    h += b" " * (-len(h) % 8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)) + h + b"".join(body))
+
+
+def trimmed_ckpts():
+    for src, dst, shards in (("flashnext-tiny-q4", "ckpt_tiny_q4", 2), ("flashnext-tiny-mlx", "ckpt_tiny_mlx", 1)):
+        d = os.path.join(REF, src)
+        out = os.path.join(HERE, dst)
+        os.makedirs(out, exist_ok=True)
+        for f in os.listdir(out):
+            os.remove(os.path.join(out, f))
+        with open(os.path.join(d, "config.json"), "rb") as f:
+            cfg = f.read()
+        with open(os.path.join(out, "config.json"), "wb") as f:
+            f.write(cfg)
+        by_layer, meta = {0: [], 1: []}, None
+        for fn in sorted(os.listdir(d)):
+            if fn.endswith(".safetensors") and fn.startswith("model"):
+                ents, m = raw_entries(os.path.join(d, fn))
+                meta = meta or m
+                for e in ents:
+                    for layer in by_layer:
+                        if e[0].startswith(f"language_model.model.layers.{layer}.mlp."):
+                            by_layer[layer].append(e)
+        if shards == 1:
+            write_safetensors(os.path.join(out, "model.safetensors"), by_layer[0] + by_layer[1], meta)
+        else:
+            for layer in by_layer:
+                write_safetensors(os.path.join(out, f"model-{layer + 1:05d}-of-00002.safetensors"),
+                                  by_layer[layer], meta)
+
+
 def main():
     from qwasar_amd import synth
     from oracle import ref
@@ -142,4 +202,8 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["ckpt"]:
+        trimmed_ckpts()
+    else:
+        main()
+        trimmed_ckpts()
