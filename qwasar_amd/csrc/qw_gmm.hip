@@ -39,6 +39,8 @@ struct QwGmmArgs {
     const int32_t *tiles;
     qwk_q4 m;
     int k, n, K, x_by_pair, rows, nblk;
+    int kslice;      // k range of a blockIdx.y slice (k: no split)
+    float *part;     // dense split-K: slice s writes part[s][rows][n]
 };
 
 union qw_h8u { qw_h8 h; uint32_t u[4]; uint4 v; };
@@ -73,6 +75,7 @@ __global__ __launch_bounds__(QW_GMM_THREADS) void k_gather_gemm(QwGmmArgs a)
     }
     const int k = a.k, n = a.n, words = k / 8, groups = k / G;
     const int n0 = nb * QW_GMM_BN;
+    const int kb = (int)blockIdx.y * a.kslice, ke = min(k, kb + a.kslice);
     const uint32_t *wb = a.m.w + (size_t)expert * n * words;
     const uint16_t *sb = a.m.s + (size_t)expert * n * groups;
     const uint16_t *bb = a.m.b + (size_t)expert * n * groups;
@@ -88,8 +91,8 @@ __global__ __launch_bounds__(QW_GMM_THREADS) void k_gather_gemm(QwGmmArgs a)
         C[mt] = acc[mt];
     }
 
-    for (int k0 = 0; k0 < k; k0 += QW_GMM_BK) {
-        const int klen = min(QW_GMM_BK, k - k0);
+    for (int k0 = kb; k0 < ke; k0 += QW_GMM_BK) {
+        const int klen = min(QW_GMM_BK, ke - k0);
         // Activations: 8-element blocks, f16, written in nibble register order.
         for (int blk = t; blk < BM * (QW_GMM_BK / 8); blk += QW_GMM_THREADS) {
             const int m = blk / (QW_GMM_BK / 8), bk = blk % (QW_GMM_BK / 8);
@@ -149,7 +152,7 @@ __global__ __launch_bounds__(QW_GMM_THREADS) void k_gather_gemm(QwGmmArgs a)
                 const qw_h8 af = *reinterpret_cast<const qw_h8 *>(&As[mt * 16 + ln][32 * s + 8 * lg]);
                 C[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf.h, C[mt], 0, 0, 0);
             }
-            if ((kk + 32) % G == 0 || kk + 32 >= k) {
+            if ((kk + 32) % G == 0 || kk + 32 >= ke) {
                 const int gabs = kk / G, gi = (kk - k0) / G;
                 float sc = 0.0f, bp = 0.0f;
                 if (col < n) {
@@ -169,6 +172,7 @@ __global__ __launch_bounds__(QW_GMM_THREADS) void k_gather_gemm(QwGmmArgs a)
         __syncthreads();
     }
 
+    float *yo = DENSE && a.part ? a.part + (size_t)blockIdx.y * a.rows * n : a.y;
     if (col < n) {
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
@@ -177,10 +181,20 @@ __global__ __launch_bounds__(QW_GMM_THREADS) void k_gather_gemm(QwGmmArgs a)
                 const int m = mt * 16 + 4 * lg + i;
                 if (m < len) {
                     const int row = DENSE ? first + m : a.perm[first + m];
-                    a.y[(size_t)row * n + col] = acc[mt][i];
+                    yo[(size_t)row * n + col] = acc[mt][i];
                 }
             }
         }
+    }
+}
+
+// y[i] = part[0][i] + part[1][i] + ... in slice order
+__global__ void k_qmm_reduce(float *__restrict__ y, const float *__restrict__ part, long total, int splits)
+{
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+        float v = part[i];
+        for (int sp = 1; sp < splits; sp++) v = v + part[(size_t)sp * total + i];
+        y[i] = v;
     }
 }
 
@@ -198,10 +212,10 @@ static int gmm_bm(int bm, dim3 grid, hipStream_t s, const QwGmmArgs &a)
 }
 
 template <bool DENSE>
-static int gmm_launch(hipStream_t s, const QwGmmArgs &a, int group, int bm, int ntiles)
+static int gmm_launch(hipStream_t s, const QwGmmArgs &a, int group, int bm, int ntiles, int splits = 1)
 {
     if (ntiles <= 0) return 0;
-    const dim3 grid((unsigned)(a.nblk * ntiles));
+    const dim3 grid((unsigned)(a.nblk * ntiles), (unsigned)splits);
     switch (group) {
     case 32: return gmm_bm<32, DENSE>(bm, grid, s, a);
     case 64: return gmm_bm<64, DENSE>(bm, grid, s, a);
@@ -221,14 +235,59 @@ extern "C" int qwk_gather_gemm(hipStream_t s, float *y, const float *x, const in
                                int group, int bm, int max_tiles)
 {
     if (!gmm_shape_ok(x, m, k, n, group) || K < 1) return (int)hipErrorInvalidValue;
-    QwGmmArgs a = {y, x, perm, tiles, m, k, n, K, x_by_pair, 0, (n + QW_GMM_BN - 1) / QW_GMM_BN};
+    QwGmmArgs a = {y, x, perm, tiles, m, k, n, K, x_by_pair, 0, (n + QW_GMM_BN - 1) / QW_GMM_BN, k, nullptr};
     return gmm_launch<false>(s, a, group, bm, max_tiles);
 }
 
-extern "C" int qwk_qmm(hipStream_t s, float *y, const float *x, qwk_q4 m, int k, int n, int rows, int group)
+// Split-K for the dense product when the tiles alone would leave the chip
+// under two workgroups a CU: enough k slices for ~QW_QMM_SPLIT_WG workgroups,
+// each a whole number of QW_GMM_BK steps (so of quantisation groups) and no
+// shorter than QW_QMM_SPLIT_MIN_K.  The plan is a function of the shape only.
+#define QW_QMM_SPLIT_BELOW 512
+#define QW_QMM_SPLIT_WG 1024
+#define QW_QMM_SPLIT_MIN_K 512
+
+static int qmm_bm(int rows) { return rows >= 64 ? 64 : (rows >= 32 ? 32 : 16); }
+
+static int qmm_splits(int k, int n, int rows, int *kslice)
+{
+    const int bm = qmm_bm(rows);
+    const long tiles = (long)((n + QW_GMM_BN - 1) / QW_GMM_BN) * ((rows + bm - 1) / bm);
+    *kslice = k;
+    if (tiles >= QW_QMM_SPLIT_BELOW) return 1;
+    long sp = (QW_QMM_SPLIT_WG + tiles - 1) / tiles;
+    if (sp > k / QW_QMM_SPLIT_MIN_K) sp = k / QW_QMM_SPLIT_MIN_K;
+    if (sp < 2) return 1;
+    const int ks = (int)(((k + sp - 1) / sp + QW_GMM_BK - 1) / QW_GMM_BK * QW_GMM_BK);
+    *kslice = ks;
+    return (k + ks - 1) / ks;
+}
+
+extern "C" size_t qwk_qmm_work_bytes(int k, int n, int rows)
+{
+    int ks;
+    const int sp = k > 0 && n > 0 && rows > 0 ? qmm_splits(k, n, rows, &ks) : 1;
+    return sp > 1 ? (size_t)sp * rows * n * sizeof(float) : 0;
+}
+
+extern "C" int qwk_qmm(hipStream_t s, float *y, const float *x, qwk_q4 m, int k, int n, int rows, int group,
+                       void *work, size_t work_bytes)
 {
     if (!gmm_shape_ok(x, m, k, n, group) || rows < 1) return (int)hipErrorInvalidValue;
-    const int bm = rows >= 64 ? 64 : (rows >= 32 ? 32 : 16);
-    QwGmmArgs a = {y, x, nullptr, nullptr, m, k, n, 1, 1, rows, (n + QW_GMM_BN - 1) / QW_GMM_BN};
-    return gmm_launch<true>(s, a, group, bm, (rows + bm - 1) / bm);
+    const int bm = qmm_bm(rows);
+    int ks;
+    int sp = qmm_splits(k, n, rows, &ks);
+    if (sp > 1 && (!work || work_bytes < qwk_qmm_work_bytes(k, n, rows) || ((uintptr_t)work & 15u))) {
+        sp = 1;
+        ks = k;
+    }
+    QwGmmArgs a = {y, x, nullptr, nullptr, m, k, n, 1, 1, rows, (n + QW_GMM_BN - 1) / QW_GMM_BN, ks,
+                   sp > 1 ? static_cast<float *>(work) : nullptr};
+    int rc = gmm_launch<true>(s, a, group, bm, (rows + bm - 1) / bm, sp);
+    if (rc || sp == 1) return rc;
+    const long total = (long)rows * n;
+    const long want = (total + 255) / 256;
+    hipLaunchKernelGGL(k_qmm_reduce, dim3((unsigned)(want < 4096 ? want : 4096)), dim3(256), 0, s, y,
+                       static_cast<const float *>(work), total, sp);
+    return (int)hipGetLastError();
 }

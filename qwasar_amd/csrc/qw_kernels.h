@@ -57,7 +57,11 @@ int qwk_gather_gemm(hipStream_t s, float *y, const float *x, const int32_t *perm
                     int group, int bm, int max_tiles);
 
 /* Dense prefill product y[rows, n] = x[rows, k] . W^T (the shared expert). */
-int qwk_qmm(hipStream_t s, float *y, const float *x, qwk_q4 m, int k, int n, int rows, int group);
+/* work: qwk_qmm_work_bytes(k, n, rows) bytes for the split-K partials (none
+ * needed when it returns 0; with less, the product runs unsplit). */
+int qwk_qmm(hipStream_t s, float *y, const float *x, qwk_q4 m, int k, int n, int rows, int group,
+            void *work, size_t work_bytes);
+size_t qwk_qmm_work_bytes(int k, int n, int rows);
 
 /* A second weight bank for grouped tiles of expert `expert` (qwk_moe_group's
  * extra rows): its pairs p >= `pairs` read A row p - pairs when not

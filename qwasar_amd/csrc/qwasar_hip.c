@@ -416,11 +416,17 @@ void qw_op_qmvb_q4(qw_cmd c, qw_ref y, qw_ref x, qw_ref w, qw_ref scales, qw_ref
     qw_op_qmv_q4(c, y, x, w, scales, biases, k, n, rows, group);
 }
 
+/* The backend's device scratch, grown on demand (defined below). */
+static void *scratch(size_t bytes);
+
 void qw_op_qmm_q4(qw_cmd c, qw_ref y, qw_ref x, qw_ref w, qw_ref scales, qw_ref biases,
                   int32_t k, int32_t n, int32_t rows, int32_t group) {
     QW_OP(c);
     touch(c, x, 0); touch(c, w, 0); touch(c, scales, 0); touch(c, biases, 0); touch(c, y, 1);
-    launched(c, "qmm_q4", qwk_qmm(G.stream, dp(y), dp(x), q4(w, scales, biases), k, n, rows, group));
+    const size_t wb = qwk_qmm_work_bytes(k, n, rows);
+    void *work = wb ? scratch(wb) : NULL;
+    launched(c, "qmm_q4", qwk_qmm(G.stream, dp(y), dp(x), q4(w, scales, biases), k, n, rows, group, work,
+                                  work ? wb : 0));
 }
 
 void qw_op_qmat_q4(qw_cmd c, qw_ref y, qw_ref x, qw_ref w, qw_ref scales, qw_ref biases,
@@ -628,8 +634,6 @@ int32_t qw_moe_tile_rows(int32_t pairs, int32_t E) {
     if (avg4 >= 4 * 12) return 32;
     return 16;
 }
-
-static void *scratch(size_t bytes);
 
 void qw_op_moe_group(qw_cmd c, qw_ref perm, qw_ref tiles, qw_ref cursor, qw_ref idx,
                      int32_t pairs, int32_t E) {

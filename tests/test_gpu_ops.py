@@ -255,6 +255,24 @@ def test_qmat(gpu, rows):
     assert rel_l2(yb.read(np.float32, (rows, n)), want) < tol
 
 
+@pytest.mark.parametrize("k,n,rows,G", [(12288, 320, 300, 64), (1024, 64, 17, 32), (4096, 200, 90, 128),
+                                        (640, 96, 40, 64)])
+def test_qmm_splitk(gpu, k, n, rows, G):
+    """The dense MFMA product with its k range sliced across workgroups (the
+    hyper-connection down-projection's shape first; 2 slices; group 128 with a
+    ragged column block; and a k too short to split), against the oracle."""
+    print(f"qmm splitk k={k} n={n} rows={rows} G={G}", flush=True)
+    q = synth.make_q4(71 + rows, "qsk", n, k, G)
+    x = rnd((rows, k), 81 + rows)
+    B = gpu.Buf
+    wb, sb, bb, xb, yb = B(wrap=q.w), B(wrap=q.s), B(wrap=q.b), B.of(x), B(rows * n * 4)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_op_qmm_q4(c, yb.ref(), xb.ref(), wb.ref(), sb.ref(), bb.ref(), k, n, rows, G)
+    gpu.run(c, "qmm splitk")
+    want = ref.qmv_q4(x, q.w, q.s, q.b, k, n, rows, G)
+    assert rel_l2(yb.read(np.float32, (rows, n)), want) < 5e-4
+
+
 # ---- elementwise and the combine ----------------------------------------------
 
 def test_combine_shared(gpu):
