@@ -272,11 +272,19 @@ def bench_hc(gpu, steps, H=3072, S=4, k=320, G=64, pool=96, prefill_rows=2048, s
     gpu.qw_op_synth(c, inj.ref(), synth.SYNTH_F32_BF16_NORMAL, rows * S, synth.sm_key(seed, "inj"), 1.0, 0.0)
     gpu.run(c, "hc mixer setup")
 
+    h4b, injb = B(rows * HH * 4), B(rows * S * 4)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_op_synth(c, injb.ref(), synth.SYNTH_F32_BF16_NORMAL, rows * S, synth.sm_key(seed, "inj"), 1.0, 0.0)
+    gpu.run(c, "hc mixer setup (decode pair)")
+    hpair, ipair = (h4, h4b), (inj, injb)
+
     def decode_step(c, p):
+        # two launches: inject + norm + down + injection logits, then up + mix;
+        # h4 and the logits alternate between two buffers
         wn, (dw, ds, db), (uw, us, ub), bj = sets[p % pool]
-        gpu.qw_op_hc_inject_norm(c, h4.ref(), out.ref(), inj.ref(), wn.ref(), n4.ref(), 1, H, S, 1e-6)
-        gpu.qw_op_qmv_q4(c, d.ref(), n4.ref(), dw.ref(), ds.ref(), db.ref(), HH, k, 1, G)
-        gpu.qw_op_dmat_bf16(c, inj.ref(), n4.ref(), bj.ref(), HH, S, 1)
+        assert gpu.qw_op_hc_pre_decode(c, hpair[(p + 1) % 2].ref(), n4.ref(), d.ref(), ipair[(p + 1) % 2].ref(),
+                                       hpair[p % 2].ref(), out.ref(), ipair[p % 2].ref(), wn.ref(), dw.ref(),
+                                       ds.ref(), db.ref(), bj.ref(), H, S, k, G, 1e-6)
         gpu.qw_op_hc_mix_up(c, x.ref(), d.ref(), n4.ref(), uw.ref(), us.ref(), ub.ref(), k, H, S, 1, 1.0 / S, G)
 
     c = gpu.qw_cmd_begin()
@@ -323,7 +331,7 @@ def bench_hc(gpu, steps, H=3072, S=4, k=320, G=64, pool=96, prefill_rows=2048, s
     for wn_, (a1, a2, a3), (b1, b2, b3), bj_ in sets:
         for t in (wn_, a1, a2, a3, b1, b2, b3, bj_):
             t.free()
-    for t in (h4, n4, out, inj, d, x, m):
+    for t in (h4, n4, out, inj, d, x, m, h4b, injb):
         t.free()
     us_tok = dec_ms * 1000.0 / steps
     wbytes = 2 * (k * HH // 2 + k * HH // G * 4) + S * HH * 2 + HH * 2
@@ -332,7 +340,7 @@ def bench_hc(gpu, steps, H=3072, S=4, k=320, G=64, pool=96, prefill_rows=2048, s
     return {"shape": {"H": H, "S": S, "lowrank": k, "group": G},
             "decode": {"us_per_token": round(us_tok, 2), "weight_bytes": wbytes,
                        "hbm_gbs": round((wbytes + abytes) / (us_tok * 1e-6) / 1e9, 1),
-                       "launches": 4, "weight_sets": pool},
+                       "launches": 2, "weight_sets": pool},
             "prefill": {"rows": rows, "ms": round(pf_ms, 3),
                         "tflops": round(flops / (pf_ms * 1e-3) / 1e12, 2)}}
 

@@ -179,6 +179,176 @@ static dim3 qh_grid(int64_t n)
     return dim3((unsigned)(b < 16384 ? (b > 0 ? b : 1) : 16384));
 }
 
+// The mixer's first half at decode (one row) in one launch: inject + grouped
+// norm, the down-projection and the injection logits.  Every workgroup redoes
+// the inject and the norm of all S streams (S*H floats, from L2) into LDS --
+// the same arithmetic, in the same order, as k_norm_grouped -- so nothing
+// waits on another workgroup.  Workgroup b < lowrank then computes d[b] (a
+// 4-bit row over S*H inputs; thread t takes segments t, t + 256, ..., the
+// block sum in wave order), and workgroup lowrank + s the injection logit s
+// in order R (a thread per 64-input chunk, chunk sums left to right).
+// Workgroup s < S writes stream s of h4_out and n4.  h4_out must not alias h4.
+#define QH_PRE_MAXS 4
+__global__ void __launch_bounds__(QH_THREADS) k_hc_pre(float *__restrict__ h4_out, float *__restrict__ n4,
+                                                       float *__restrict__ d, float *__restrict__ inj_out,
+                                                       const float *__restrict__ h4, const float *__restrict__ out,
+                                                       const float *__restrict__ inj, const uint16_t *__restrict__ wn,
+                                                       qwk_q4 dn, const uint16_t *__restrict__ bj, int H, int S,
+                                                       int lowrank, int G, float eps)
+{
+    extern __shared__ float4 nl[];          // [S * H / 4]
+    __shared__ float part[QH_PRE_MAXS][QH_THREADS / 64];
+    __shared__ float pc[QH_THREADS];
+    const int b = blockIdx.x, t = threadIdx.x, n4q = H / 4, HH = S * H;
+    const int wave = t >> 6, lane = t & 63;
+    const int words = HH / 8, groups = HH / G, nseg = HH / 32;
+
+    // the down row's weights first: their latency runs under the norm
+    uint4 wv[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    float sc[2] = {0.0f, 0.0f}, bi[2] = {0.0f, 0.0f};
+    if (b < lowrank) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int seg = t + QH_THREADS * j;
+            if (seg < nseg) {
+                const int g = seg * 32 / G;
+                wv[j] = *reinterpret_cast<const uint4 *>(dn.w + (size_t)b * words + seg * 4);
+                sc[j] = qw_bf16(dn.s[(size_t)b * groups + g]);
+                bi[j] = qw_bf16(dn.b[(size_t)b * groups + g]);
+            }
+        }
+    }
+
+    // inject and the sums of squares of all streams together; per stream the
+    // order of k_norm_grouped (a chain over this thread's float4s ascending,
+    // the xor tree, the wave partials in order)
+    const float4 *orow = reinterpret_cast<const float4 *>(out);
+    float wgt[QH_PRE_MAXS], ss[QH_PRE_MAXS];
+#pragma unroll
+    for (int s = 0; s < QH_PRE_MAXS; s++) {
+        wgt[s] = s < S ? 2.0f * qh_sigmoid(inj[s] / (float)S) : 0.0f;
+        ss[s] = 0.0f;
+    }
+    for (int i = t; i < n4q; i += QH_THREADS) {
+        const float4 o = orow[i];
+#pragma unroll
+        for (int s = 0; s < QH_PRE_MAXS; s++) {
+            if (s < S) {
+                float4 v = reinterpret_cast<const float4 *>(h4 + (size_t)s * H)[i];
+                v.x += o.x * wgt[s]; v.y += o.y * wgt[s]; v.z += o.z * wgt[s]; v.w += o.w * wgt[s];
+                nl[s * n4q + i] = v;
+                if (b == s) reinterpret_cast<float4 *>(h4_out + (size_t)s * H)[i] = v;
+                ss[s] = __builtin_fmaf(v.x, v.x, ss[s]);
+                ss[s] = __builtin_fmaf(v.y, v.y, ss[s]);
+                ss[s] = __builtin_fmaf(v.z, v.z, ss[s]);
+                ss[s] = __builtin_fmaf(v.w, v.w, ss[s]);
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < QH_PRE_MAXS; s++) {
+        const float v = qw_xor_sum<64>(ss[s]);
+        if (lane == 0) part[s][wave] = v;
+    }
+    __syncthreads();
+    float inv[QH_PRE_MAXS];
+#pragma unroll
+    for (int s = 0; s < QH_PRE_MAXS; s++) {
+        float tot = part[s][0];
+#pragma unroll
+        for (int w = 1; w < QH_THREADS / 64; w++) tot = tot + part[s][w];
+        inv[s] = 1.0f / sqrtf(tot / (float)H + eps);
+    }
+    for (int i = t; i < n4q; i += QH_THREADS) {
+#pragma unroll
+        for (int s = 0; s < QH_PRE_MAXS; s++) {
+            if (s < S) {
+                float4 v = nl[s * n4q + i];     // this thread's own values
+                const uint2 wb = reinterpret_cast<const uint2 *>(wn + (size_t)s * H)[i];
+                v.x = v.x * inv[s] * __uint_as_float(wb.x << 16);
+                v.y = v.y * inv[s] * __uint_as_float(wb.x & 0xFFFF0000u);
+                v.z = v.z * inv[s] * __uint_as_float(wb.y << 16);
+                v.w = v.w * inv[s] * __uint_as_float(wb.y & 0xFFFF0000u);
+                nl[s * n4q + i] = v;
+                if (b == s) reinterpret_cast<float4 *>(n4 + (size_t)s * H)[i] = v;
+            }
+        }
+    }
+    __syncthreads();
+    if (b < lowrank) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int seg = t + QH_THREADS * j;
+            if (seg < nseg) {
+                float xs[32];
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const float4 v = nl[seg * 8 + q];
+                    xs[4 * q] = v.x; xs[4 * q + 1] = v.y; xs[4 * q + 2] = v.z; xs[4 * q + 3] = v.w;
+                }
+                float xsum = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 32; e++) xsum += xs[e];
+                float dd = qw_dot8_q(wv[j].x, xs, 0.0f);
+                dd = qw_dot8_q(wv[j].y, xs + 8, dd);
+                dd = qw_dot8_q(wv[j].z, xs + 16, dd);
+                dd = qw_dot8_q(wv[j].w, xs + 24, dd);
+                acc = __builtin_fmaf(sc[j], dd, acc);
+                acc = __builtin_fmaf(bi[j], xsum, acc);
+            }
+        }
+        acc = qh_block_sum(acc, &part[0][0]);
+        if (t == 0) d[b] = acc;
+    } else {
+        const int s = b - lowrank, nch = HH / 64;
+        if (t < nch) {
+            // the chunk's 64 weights and inputs all requested before the chain
+            const uint4 *wr = reinterpret_cast<const uint4 *>(bj + (size_t)s * HH + 64 * t);
+            uint4 ww[8];
+            float4 xa[16];
+#pragma unroll
+            for (int q = 0; q < 8; q++) ww[q] = wr[q];
+#pragma unroll
+            for (int q = 0; q < 16; q++) xa[q] = nl[16 * t + q];
+            float p = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const uint32_t wd[4] = {ww[q].x, ww[q].y, ww[q].z, ww[q].w};
+                const float4 a = xa[2 * q], c = xa[2 * q + 1];
+                const float xx[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    p = __builtin_fmaf(__uint_as_float(wd[j] << 16), xx[2 * j], p);
+                    p = __builtin_fmaf(__uint_as_float(wd[j] & 0xFFFF0000u), xx[2 * j + 1], p);
+                }
+            }
+            pc[t] = p;
+        }
+        __syncthreads();
+        if (t == 0) {
+            float tot = pc[0];
+            for (int e = 1; e < nch; e++) tot = tot + pc[e];
+            inj_out[s] = tot;
+        }
+    }
+}
+
+extern "C" int qwk_hc_pre_decode(hipStream_t s, float *h4_out, float *n4, float *d, float *inj_out, const float *h4,
+                                 const float *out, const float *inj, const uint16_t *wn, qwk_q4 dn,
+                                 const uint16_t *bj, int H, int S, int lowrank, int group, float eps)
+{
+    const int HH = S * H;
+    if (H <= 0 || H % 4 || S < 1 || S > QH_PRE_MAXS || HH % 64 || HH / 64 > QH_THREADS || (size_t)HH * 4 > 64 * 1024 ||
+        lowrank < 1 || (group != 32 && group != 64 && group != 128) || HH % group || h4_out == h4 ||
+        inj_out == inj || ((uintptr_t)h4 & 15u) || ((uintptr_t)h4_out & 15u) || ((uintptr_t)n4 & 15u) ||
+        ((uintptr_t)out & 15u) || ((uintptr_t)wn & 7u) || ((uintptr_t)dn.w & 15u) || ((uintptr_t)bj & 15u))
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_hc_pre, dim3((unsigned)(lowrank + S)), dim3(QH_THREADS), (size_t)HH * 4, s, h4_out, n4, d,
+                       inj_out, h4, out, inj, wn, dn, bj, H, S, lowrank, group, eps);
+    return (int)hipGetLastError();
+}
+
 extern "C" int qwk_repeat_cols(hipStream_t s, float *h4, const float *x, int rows, int H, int S)
 {
     if (rows <= 0) return 0;

@@ -166,6 +166,9 @@ int qwk_rms_norm_grouped(hipStream_t s, float *y, const float *x, const uint16_t
 int qwk_hc_inject_norm(hipStream_t s, float *h4, const float *out, const float *inj, const uint16_t *w,
                        float *n4, int rows, int H, int S, float eps);
 int qwk_silu_scale(hipStream_t s, float *y, int64_t n, float scale);
+int qwk_hc_pre_decode(hipStream_t s, float *h4_out, float *n4, float *d, float *inj_out, const float *h4,
+                      const float *out, const float *inj, const uint16_t *wn, qwk_q4 dn, const uint16_t *bj,
+                      int H, int S, int lowrank, int group, float eps);
 int qwk_hc_mix(hipStream_t s, float *x, const float *n, const float *m, int rows, int H, int S);
 int qwk_hc_inject(hipStream_t s, float *h4, const float *out, const float *inj, int rows, int H, int S);
 int qwk_hc_mix_up(hipStream_t s, float *x, const float *d, const float *n4, const uint32_t *w,

@@ -520,6 +520,24 @@ bool qw_op_hc_mix_up(qw_cmd c, qw_ref x, qw_ref d, qw_ref n4, qw_ref w, qw_ref s
     return rc == 0;
 }
 
+bool qw_op_hc_pre_decode(qw_cmd c, qw_ref h4_out, qw_ref n4, qw_ref d, qw_ref inj_out, qw_ref h4, qw_ref out,
+                         qw_ref inj, qw_ref norm_w, qw_ref down_w, qw_ref down_s, qw_ref down_b, qw_ref inj_w,
+                         int32_t H, int32_t S, int32_t lowrank, int32_t group, float eps) {
+    const int32_t HH = S * H;
+    if (H < 4 || H % 4 || S < 1 || S > 4 || HH % 64 || HH > 16384 || lowrank < 1 || HH % group ||
+        (group != 32 && group != 64 && group != 128) ||
+        (h4_out.buf == h4.buf && h4_out.off == h4.off) || (inj_out.buf == inj.buf && inj_out.off == inj.off))
+        return false;
+    if (!c) return true;
+    touch(c, h4, 0); touch(c, out, 0); touch(c, inj, 0); touch(c, norm_w, 0);
+    touch(c, down_w, 0); touch(c, down_s, 0); touch(c, down_b, 0); touch(c, inj_w, 0);
+    touch(c, h4_out, 1); touch(c, n4, 1); touch(c, d, 1); touch(c, inj_out, 1);
+    const int rc = qwk_hc_pre_decode(G.stream, dp(h4_out), dp(n4), dp(d), dp(inj_out), dp(h4), dp(out), dp(inj),
+                                     dp(norm_w), q4(down_w, down_s, down_b), dp(inj_w), H, S, lowrank, group, eps);
+    launched(c, "hc_pre_decode", rc);
+    return rc == 0;
+}
+
 void qw_op_silu_scale(qw_cmd c, qw_ref y, int32_t n, float scale) {
     QW_OP(c);
     touch(c, y, 1);

@@ -154,3 +154,48 @@ def test_mixer_around_the_moe_layer(gpu):
     assert np.allclose(hb.read(np.float32, (rows, S * H)),
                        ref.hc_inject(gh, ob.read(np.float32, (rows, H)), inj, rows, H, S), rtol=2e-6, atol=1e-6)
     lb.free()
+
+
+@pytest.mark.parametrize("H,S,k,G", [(3072, 4, 320, 64), (1024, 4, 96, 32), (256, 2, 64, 128)])
+def test_pre_decode_fused(gpu, H, S, k, G):
+    """qw_op_hc_pre_decode (one launch) against the separate ops on the same
+    inputs: injected streams, normed streams and injection logits bit-exact
+    (the same arithmetic in the same order), the down-projection against the
+    oracle; then against the oracle end to end."""
+    print(f"hc pre decode H={H} S={S} k={k} G={G}", flush=True)
+    g = _rng(31 + H)
+    h4 = g.standard_normal((1, S * H)).astype(np.float32)
+    prev = g.standard_normal((1, H)).astype(np.float32)
+    pinj = g.standard_normal((1, S)).astype(np.float32)
+    wn = synth.to_bf16(1.0 + 0.05 * g.standard_normal(S * H).astype(np.float32))
+    down = _q4(32 + H, "hcf.down", k, S * H, G)
+    binj = synth.to_bf16((0.02 * g.standard_normal((S, S * H))).astype(np.float32))
+    B = gpu.Buf
+    h_sep, pb, ib, wnb, bjb = B.of(h4), B.of(prev), B.of(pinj), B.of(wn), B.of(binj)
+    dwb, dsb, dbb = B.of(down.w), B.of(down.s), B.of(down.b)
+    n_sep, d_sep, i_sep = B(S * H * 4), B(k * 4), B(S * 4)
+    h_in, h_out, n_f, d_f, i_f = B.of(h4), B(S * H * 4), B(S * H * 4), B(k * 4), B(S * 4)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_op_hc_inject_norm(c, h_sep.ref(), pb.ref(), ib.ref(), wnb.ref(), n_sep.ref(), 1, H, S, 1e-6)
+    gpu.qw_op_qmv_q4(c, d_sep.ref(), n_sep.ref(), dwb.ref(), dsb.ref(), dbb.ref(), S * H, k, 1, G)
+    gpu.qw_op_dmat_bf16(c, i_sep.ref(), n_sep.ref(), bjb.ref(), S * H, S, 1)
+    assert gpu.qw_op_hc_pre_decode(c, h_out.ref(), n_f.ref(), d_f.ref(), i_f.ref(), h_in.ref(), pb.ref(), ib.ref(),
+                                   wnb.ref(), dwb.ref(), dsb.ref(), dbb.ref(), bjb.ref(), H, S, k, G, 1e-6)
+    assert not gpu.qw_op_hc_pre_decode(c, h_in.ref(), n_f.ref(), d_f.ref(), i_f.ref(), h_in.ref(), pb.ref(),
+                                       ib.ref(), wnb.ref(), dwb.ref(), dsb.ref(), dbb.ref(), bjb.ref(), H, S, k, G,
+                                       1e-6), "h4_out aliasing h4 is refused"
+    gpu.run(c, "hc pre decode")
+    u32 = lambda b, n: b.read(np.float32, (1, n)).view(np.uint32)
+    assert np.array_equal(u32(h_out, S * H), u32(h_sep, S * H))
+    assert np.array_equal(u32(n_f, S * H), u32(n_sep, S * H))
+    assert np.array_equal(u32(i_f, S), u32(i_sep, S))
+    assert np.array_equal(u32(h_in, S * H), h4.view(np.uint32)), "h4 is left as it was"
+    n4 = n_f.read(np.float32, (1, S * H))
+    assert rel_l2(d_f.read(np.float32, (1, k)), ref.qmv_q4(n4, down.w, down.s, down.b, S * H, k, 1, G)) < 1e-5
+    assert rel_l2(d_f.read(np.float32, (1, k)), d_sep.read(np.float32, (1, k))) < 1e-5
+    gh = ref.hc_inject(h4, prev, pinj, 1, H, S)
+    assert np.allclose(h_out.read(np.float32, (1, S * H)), gh, rtol=2e-6, atol=1e-6)
+    # the norm on the GPU's own injected streams, as the step-by-step test
+    assert np.allclose(n4, ref.rms_norm_grouped(h_out.read(np.float32, (1, S * H)), wn, H, S, 1e-6),
+                       rtol=2e-5, atol=0)
+    assert np.array_equal(u32(i_f, S), ref.dmat_bf16(n4, binj, S * H, S, 1).view(np.uint32))
