@@ -177,45 +177,52 @@ __global__ __launch_bounds__(64) void k_dmat_tiled(float *__restrict__ y, const 
     }
 }
 
-// A few outputs (the shared expert's gate, n = 1) over many token rows: one
-// wave per (row, output); lane c runs chunk c's fmaf chain (c < 64 * 4), the
-// partials meet in LDS and lane 0 adds them left to right.  k % 64 == 0.
+// A few outputs (the shared expert's gate, n = 1; the mixer's injection
+// logits, n = 4) over many token rows: one wave per row; lane c loads chunk c
+// of the row once and runs its fmaf chain for every output (c < 64 * 4), the
+// partials meet in LDS and lane o adds output o's left to right.  k % 64 == 0.
 #define QW_DROWS_WAVES 4
+#define QW_DROWS_MAXN 8                    // outputs a row (n < 8 takes this path)
 __global__ __launch_bounds__(QW_DROWS_WAVES * 64) void k_dmat_rows(float *__restrict__ y, const float *__restrict__ x,
                                                                   const uint16_t *__restrict__ w, int k, int n,
                                                                   int rows)
 {
-    __shared__ float part[QW_DROWS_WAVES][QW_DMAT_MAXCH];
+    __shared__ float part[QW_DROWS_WAVES][QW_DROWS_MAXN][QW_DMAT_MAXCH];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int item = blockIdx.x * QW_DROWS_WAVES + wave;
-    if (item >= rows * n) return;
-    const int r = item / n, o = item % n, nch = k / 64;
-    const uint16_t *wr = w + (size_t)o * k;
+    const int r = blockIdx.x * QW_DROWS_WAVES + wave;
+    if (r >= rows) return;
+    const int nch = k / 64;
     const float *xr = x + (size_t)r * k;
     for (int c = lane; c < nch; c += 64) {
-        const uint4 *wv = reinterpret_cast<const uint4 *>(wr + c * 64);
+        // the row's chunk once, for every output
         const float4 *xv = reinterpret_cast<const float4 *>(xr + c * 64);
-        float p = 0.0f;
+        float4 xa[16];
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const uint4 ww = wv[q];
-            const float4 a = xv[2 * q], b = xv[2 * q + 1];
-            p = __builtin_fmaf(__uint_as_float(ww.x << 16), a.x, p);
-            p = __builtin_fmaf(__uint_as_float(ww.x & 0xFFFF0000u), a.y, p);
-            p = __builtin_fmaf(__uint_as_float(ww.y << 16), a.z, p);
-            p = __builtin_fmaf(__uint_as_float(ww.y & 0xFFFF0000u), a.w, p);
-            p = __builtin_fmaf(__uint_as_float(ww.z << 16), b.x, p);
-            p = __builtin_fmaf(__uint_as_float(ww.z & 0xFFFF0000u), b.y, p);
-            p = __builtin_fmaf(__uint_as_float(ww.w << 16), b.z, p);
-            p = __builtin_fmaf(__uint_as_float(ww.w & 0xFFFF0000u), b.w, p);
+        for (int q = 0; q < 16; q++) xa[q] = xv[q];
+        for (int o = 0; o < n; o++) {
+            const uint4 *wv = reinterpret_cast<const uint4 *>(w + (size_t)o * k + c * 64);
+            float p = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const uint4 ww = wv[q];
+                const float4 a = xa[2 * q], b = xa[2 * q + 1];
+                p = __builtin_fmaf(__uint_as_float(ww.x << 16), a.x, p);
+                p = __builtin_fmaf(__uint_as_float(ww.x & 0xFFFF0000u), a.y, p);
+                p = __builtin_fmaf(__uint_as_float(ww.y << 16), a.z, p);
+                p = __builtin_fmaf(__uint_as_float(ww.y & 0xFFFF0000u), a.w, p);
+                p = __builtin_fmaf(__uint_as_float(ww.z << 16), b.x, p);
+                p = __builtin_fmaf(__uint_as_float(ww.z & 0xFFFF0000u), b.y, p);
+                p = __builtin_fmaf(__uint_as_float(ww.w << 16), b.z, p);
+                p = __builtin_fmaf(__uint_as_float(ww.w & 0xFFFF0000u), b.w, p);
+            }
+            part[wave][o][c] = p;
         }
-        part[wave][c] = p;
     }
-    // the wave's LDS accesses run in order: lane 0 reads what the wave wrote
-    if (lane == 0) {
-        float total = part[wave][0];
-        for (int c = 1; c < nch; c++) total = total + part[wave][c];
-        y[(size_t)r * n + o] = total;
+    // the wave's LDS accesses run in order: lane o reads what the wave wrote
+    if (lane < n) {
+        float total = part[wave][lane][0];
+        for (int c = 1; c < nch; c++) total = total + part[wave][lane][c];
+        y[(size_t)r * n + lane] = total;
     }
 }
 
@@ -276,8 +283,7 @@ extern "C" int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint
         return (int)hipGetLastError();
     }
     if (vec && k % 64 == 0 && n < 8 && rows >= 8) {
-        const long items = (long)rows * n;
-        hipLaunchKernelGGL(k_dmat_rows, dim3((unsigned)((items + QW_DROWS_WAVES - 1) / QW_DROWS_WAVES)),
+        hipLaunchKernelGGL(k_dmat_rows, dim3((unsigned)((rows + QW_DROWS_WAVES - 1) / QW_DROWS_WAVES)),
                            dim3(QW_DROWS_WAVES * 64), 0, s, y, x, w, k, n, rows);
         return (int)hipGetLastError();
     }

@@ -120,7 +120,7 @@ def test_route_refuses_oversize(gpu, capfd):
 @pytest.mark.parametrize("k,n,rows", [(3072, 512, 1), (3072, 512, 8), (3072, 64, 20), (256, 16, 3), (100, 7, 2),
                                       (3072, 512, 70), (2560, 100, 33), (256, 16, 64), (192, 40, 97),
                                       (3072, 1, 2048), (256, 3, 40), (64, 1, 9), (8192, 2, 12),
-                                      (3072, 512, 2048), (3072, 515, 1024)])
+                                      (3072, 512, 2048), (3072, 515, 1024), (12288, 4, 300), (16384, 7, 9)])
 def test_dmat_bf16_order_r_bit_exact(gpu, k, n, rows):
     """Small row counts take one wave per output; from 32 rows on (k % 64 == 0)
     the register-tiled kernel, including ragged row and output blocks (the
