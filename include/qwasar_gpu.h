@@ -154,7 +154,7 @@ bool qw_op_hc_mix_up(qw_cmd c, qw_ref x, qw_ref d, qw_ref n4, qw_ref w, qw_ref s
  * the block's output injected, n4 its grouped norm (qw_op_hc_inject_norm),
  * d = down . n4 (4-bit [lowrank, S*H], `group`), inj_out = inj_w . n4 (bf16
  * [S, S*H], order R).  h4_out and inj_out must not be h4 and inj.  False,
- * nothing encoded, for S above 4, or S*H above 16384 or not a multiple of 64. */
+ * nothing encoded, for S above 4, or S*H above 15360 or not a multiple of 64. */
 bool qw_op_hc_pre_decode(qw_cmd c, qw_ref h4_out, qw_ref n4, qw_ref d, qw_ref inj_out, qw_ref h4, qw_ref out,
                          qw_ref inj, qw_ref norm_w, qw_ref down_w, qw_ref down_s, qw_ref down_b, qw_ref inj_w,
                          int32_t H, int32_t S, int32_t lowrank, int32_t group, float eps);

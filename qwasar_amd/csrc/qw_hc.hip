@@ -189,6 +189,9 @@ static dim3 qh_grid(int64_t n)
 // in order R (a thread per 64-input chunk, chunk sums left to right).
 // Workgroup s < S writes stream s of h4_out and n4.  h4_out must not alias h4.
 #define QH_PRE_MAXS 4
+// NI > 0: each thread holds exactly NI float4s a stream (n4q <= NI * 256), all
+// loaded up front; NI == 0: a loop over them
+template <int NI>
 __global__ void __launch_bounds__(QH_THREADS) k_hc_pre(float *__restrict__ h4_out, float *__restrict__ n4,
                                                        float *__restrict__ d, float *__restrict__ inj_out,
                                                        const float *__restrict__ h4, const float *__restrict__ out,
@@ -223,26 +226,59 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_pre(float *__restrict__ h4_ou
     // order of k_norm_grouped (a chain over this thread's float4s ascending,
     // the xor tree, the wave partials in order)
     const float4 *orow = reinterpret_cast<const float4 *>(out);
-    float wgt[QH_PRE_MAXS], ss[QH_PRE_MAXS];
+    float wgt[QH_PRE_MAXS], ss[QH_PRE_MAXS], inv[QH_PRE_MAXS];
 #pragma unroll
     for (int s = 0; s < QH_PRE_MAXS; s++) {
         wgt[s] = s < S ? 2.0f * qh_sigmoid(inj[s] / (float)S) : 0.0f;
         ss[s] = 0.0f;
     }
-    for (int i = t; i < n4q; i += QH_THREADS) {
-        const float4 o = orow[i];
+    auto inject = [&](int s, int i, float4 v, float4 o) {
+        v.x += o.x * wgt[s]; v.y += o.y * wgt[s]; v.z += o.z * wgt[s]; v.w += o.w * wgt[s];
+        nl[s * n4q + i] = v;
+        if (b == s) reinterpret_cast<float4 *>(h4_out + (size_t)s * H)[i] = v;
+        ss[s] = __builtin_fmaf(v.x, v.x, ss[s]);
+        ss[s] = __builtin_fmaf(v.y, v.y, ss[s]);
+        ss[s] = __builtin_fmaf(v.z, v.z, ss[s]);
+        ss[s] = __builtin_fmaf(v.w, v.w, ss[s]);
+    };
+    auto scale = [&](int s, int i, uint2 wb) {
+        float4 v = nl[s * n4q + i];     // this thread's own values
+        v.x = v.x * inv[s] * __uint_as_float(wb.x << 16);
+        v.y = v.y * inv[s] * __uint_as_float(wb.x & 0xFFFF0000u);
+        v.z = v.z * inv[s] * __uint_as_float(wb.y << 16);
+        v.w = v.w * inv[s] * __uint_as_float(wb.y & 0xFFFF0000u);
+        nl[s * n4q + i] = v;
+        if (b == s) reinterpret_cast<float4 *>(n4 + (size_t)s * H)[i] = v;
+    };
+    constexpr int NR = NI > 0 ? NI : 1;
+    float4 hv[QH_PRE_MAXS][NR], ov[NR];
+    uint2 gw[QH_PRE_MAXS][NR];
+    if (NI > 0) {
 #pragma unroll
-        for (int s = 0; s < QH_PRE_MAXS; s++) {
-            if (s < S) {
-                float4 v = reinterpret_cast<const float4 *>(h4 + (size_t)s * H)[i];
-                v.x += o.x * wgt[s]; v.y += o.y * wgt[s]; v.z += o.z * wgt[s]; v.w += o.w * wgt[s];
-                nl[s * n4q + i] = v;
-                if (b == s) reinterpret_cast<float4 *>(h4_out + (size_t)s * H)[i] = v;
-                ss[s] = __builtin_fmaf(v.x, v.x, ss[s]);
-                ss[s] = __builtin_fmaf(v.y, v.y, ss[s]);
-                ss[s] = __builtin_fmaf(v.z, v.z, ss[s]);
-                ss[s] = __builtin_fmaf(v.w, v.w, ss[s]);
+        for (int j = 0; j < NR; j++) {
+            const int i = t + QH_THREADS * j;
+            const bool ok = i < n4q;
+            ov[j] = ok ? orow[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int s = 0; s < QH_PRE_MAXS; s++) {
+                const bool in = ok && s < S;
+                hv[s][j] = in ? reinterpret_cast<const float4 *>(h4 + (size_t)s * H)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                gw[s][j] = in ? reinterpret_cast<const uint2 *>(wn + (size_t)s * H)[i] : make_uint2(0, 0);
             }
+        }
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+            const int i = t + QH_THREADS * j;
+#pragma unroll
+            for (int s = 0; s < QH_PRE_MAXS; s++)
+                if (s < S && i < n4q) inject(s, i, hv[s][j], ov[j]);
+        }
+    } else {
+        for (int i = t; i < n4q; i += QH_THREADS) {
+            const float4 o = orow[i];
+#pragma unroll
+            for (int s = 0; s < QH_PRE_MAXS; s++)
+                if (s < S) inject(s, i, reinterpret_cast<const float4 *>(h4 + (size_t)s * H)[i], o);
         }
     }
 #pragma unroll
@@ -251,7 +287,6 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_pre(float *__restrict__ h4_ou
         if (lane == 0) part[s][wave] = v;
     }
     __syncthreads();
-    float inv[QH_PRE_MAXS];
 #pragma unroll
     for (int s = 0; s < QH_PRE_MAXS; s++) {
         float tot = part[s][0];
@@ -259,19 +294,19 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_pre(float *__restrict__ h4_ou
         for (int w = 1; w < QH_THREADS / 64; w++) tot = tot + part[s][w];
         inv[s] = 1.0f / sqrtf(tot / (float)H + eps);
     }
-    for (int i = t; i < n4q; i += QH_THREADS) {
+    if (NI > 0) {
 #pragma unroll
-        for (int s = 0; s < QH_PRE_MAXS; s++) {
-            if (s < S) {
-                float4 v = nl[s * n4q + i];     // this thread's own values
-                const uint2 wb = reinterpret_cast<const uint2 *>(wn + (size_t)s * H)[i];
-                v.x = v.x * inv[s] * __uint_as_float(wb.x << 16);
-                v.y = v.y * inv[s] * __uint_as_float(wb.x & 0xFFFF0000u);
-                v.z = v.z * inv[s] * __uint_as_float(wb.y << 16);
-                v.w = v.w * inv[s] * __uint_as_float(wb.y & 0xFFFF0000u);
-                nl[s * n4q + i] = v;
-                if (b == s) reinterpret_cast<float4 *>(n4 + (size_t)s * H)[i] = v;
-            }
+        for (int j = 0; j < NR; j++) {
+            const int i = t + QH_THREADS * j;
+#pragma unroll
+            for (int s = 0; s < QH_PRE_MAXS; s++)
+                if (s < S && i < n4q) scale(s, i, gw[s][j]);
+        }
+    } else {
+        for (int i = t; i < n4q; i += QH_THREADS) {
+#pragma unroll
+            for (int s = 0; s < QH_PRE_MAXS; s++)
+                if (s < S) scale(s, i, reinterpret_cast<const uint2 *>(wn + (size_t)s * H)[i]);
         }
     }
     __syncthreads();
@@ -339,13 +374,23 @@ extern "C" int qwk_hc_pre_decode(hipStream_t s, float *h4_out, float *n4, float 
                                  const uint16_t *bj, int H, int S, int lowrank, int group, float eps)
 {
     const int HH = S * H;
-    if (H <= 0 || H % 4 || S < 1 || S > QH_PRE_MAXS || HH % 64 || HH / 64 > QH_THREADS || (size_t)HH * 4 > 64 * 1024 ||
+    if (H <= 0 || H % 4 || S < 1 || S > QH_PRE_MAXS || HH % 64 || HH / 64 > QH_THREADS || HH > 15360 ||   /* LDS: S*H floats plus ~1 KB static */
         lowrank < 1 || (group != 32 && group != 64 && group != 128) || HH % group || h4_out == h4 ||
         inj_out == inj || ((uintptr_t)h4 & 15u) || ((uintptr_t)h4_out & 15u) || ((uintptr_t)n4 & 15u) ||
         ((uintptr_t)out & 15u) || ((uintptr_t)wn & 7u) || ((uintptr_t)dn.w & 15u) || ((uintptr_t)bj & 15u))
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_hc_pre, dim3((unsigned)(lowrank + S)), dim3(QH_THREADS), (size_t)HH * 4, s, h4_out, n4, d,
-                       inj_out, h4, out, inj, wn, dn, bj, H, S, lowrank, group, eps);
+    const int ni = (H / 4 + QH_THREADS - 1) / QH_THREADS;
+#define QH_PRE_LAUNCH(N)                                                                                             \
+    hipLaunchKernelGGL(k_hc_pre<N>, dim3((unsigned)(lowrank + S)), dim3(QH_THREADS), (size_t)HH * 4, s, h4_out, n4, \
+                       d, inj_out, h4, out, inj, wn, dn, bj, H, S, lowrank, group, eps)
+    switch (ni) {
+    case 1: QH_PRE_LAUNCH(1); break;
+    case 2: QH_PRE_LAUNCH(2); break;
+    case 3: QH_PRE_LAUNCH(3); break;
+    case 4: QH_PRE_LAUNCH(4); break;
+    default: QH_PRE_LAUNCH(0); break;
+    }
+#undef QH_PRE_LAUNCH
     return (int)hipGetLastError();
 }
 

@@ -524,7 +524,7 @@ bool qw_op_hc_pre_decode(qw_cmd c, qw_ref h4_out, qw_ref n4, qw_ref d, qw_ref in
                          qw_ref inj, qw_ref norm_w, qw_ref down_w, qw_ref down_s, qw_ref down_b, qw_ref inj_w,
                          int32_t H, int32_t S, int32_t lowrank, int32_t group, float eps) {
     const int32_t HH = S * H;
-    if (H < 4 || H % 4 || S < 1 || S > 4 || HH % 64 || HH > 16384 || lowrank < 1 || HH % group ||
+    if (H < 4 || H % 4 || S < 1 || S > 4 || HH % 64 || HH > 15360 || lowrank < 1 || HH % group ||
         (group != 32 && group != 64 && group != 128) ||
         (h4_out.buf == h4.buf && h4_out.off == h4.off) || (inj_out.buf == inj.buf && inj_out.off == inj.off))
         return false;

@@ -156,7 +156,8 @@ def test_mixer_around_the_moe_layer(gpu):
     lb.free()
 
 
-@pytest.mark.parametrize("H,S,k,G", [(3072, 4, 320, 64), (1024, 4, 96, 32), (256, 2, 64, 128)])
+@pytest.mark.parametrize("H,S,k,G", [(3072, 4, 320, 64), (1024, 4, 96, 32), (256, 2, 64, 128), (7680, 2, 64, 64),
+                                     (1536, 3, 40, 32)])
 def test_pre_decode_fused(gpu, H, S, k, G):
     """qw_op_hc_pre_decode (one launch) against the separate ops on the same
     inputs: injected streams, normed streams and injection logits bit-exact
