@@ -139,7 +139,10 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_mix_up(float *__restrict__ x,
     if (i >= H) return;   // whole waves
     const int words = k / 8, groups = k >> lgG;
     for (int r = 0; r < rows; r++) {
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, nv[4];
+        // the streams' values this output mixes, requested with the weights
+#pragma unroll
+        for (int s = 0; s < 4; s++) nv[s] = s < S ? n4[(size_t)r * S * H + (size_t)s * H + i] : 0.0f;
         for (int wi = lane; wi < words; wi += 64) {
             float xs[8];
             const float4 *dv = reinterpret_cast<const float4 *>(d + (size_t)r * k + 8 * wi);
@@ -167,7 +170,7 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_mix_up(float *__restrict__ x,
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             const float m = qw_xor_sum<64>(acc[s]);
-            if (s < S) mix = mix + qh_sigmoid(m) * n4[(size_t)r * S * H + (size_t)s * H + i];
+            if (s < S) mix = mix + qh_sigmoid(m) * nv[s];
         }
         if (lane == 0) x[(size_t)r * H + i] = mix / (float)S;
     }
