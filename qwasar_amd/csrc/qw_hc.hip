@@ -7,10 +7,12 @@
 //   inj = block_inject(n4)                    (raw logits, [S])
 //   h4 += out (x) 2 sigmoid(inj / S)          (a block's output into the streams)
 //
-// Memory-bound elementwise and row kernels, and one fused GEMV for the
-// mixer's up-projection at few rows.  The row sums run in the order of
-// qw_norm.hip: each of 256 threads an fmaf chain over its float4 chunks, the
-// xor tree, the four wave partials in order.
+// Memory-bound elementwise and row kernels, and two fused kernels for a
+// decode step: k_hc_pre (inject, grouped norm, down-projection and injection
+// logits in one launch) and k_hc_mix_up (up-projection, its silu and the
+// stream mix at few rows).  The row sums run in the order of qw_norm.hip:
+// each of 256 threads an fmaf chain over its float4 chunks, the xor tree, the
+// four wave partials in order.
 #include "qw_device.h"
 #include "qw_kernels.h"
 
