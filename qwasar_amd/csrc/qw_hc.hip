@@ -45,6 +45,9 @@ __global__ void k_repeat_cols(float4 *__restrict__ h4, const float4 *__restrict_
 // One workgroup per (row, group): y = x * inv * w[g], dim % 4 == 0.  With
 // `out` and `inj` set, x first takes the block's output (x += out * 2
 // sigmoid(inj / S)) and is written back: qw_hc_inject and the norm in one pass.
+// NI > 0: each thread's NI float4s held in registers between the passes
+// (dim <= NI * 1024), so the second pass reads nothing again; NI == 0 loops.
+template <int NI>
 __global__ void __launch_bounds__(QH_THREADS) k_norm_grouped(float *__restrict__ y, float *x,
                                                              const uint16_t *__restrict__ w, int dim, int groups,
                                                              float eps, const float *__restrict__ out,
@@ -55,16 +58,14 @@ __global__ void __launch_bounds__(QH_THREADS) k_norm_grouped(float *__restrict__
     float4 *xr = reinterpret_cast<float4 *>(x + (size_t)q * dim);
     float4 *yr = reinterpret_cast<float4 *>(y + (size_t)q * dim);
     const uint2 *wr = reinterpret_cast<const uint2 *>(w + (size_t)g * dim);
-    const int n4 = dim / 4;
+    const int n4 = dim / 4, t = threadIdx.x;
     float wgt = 0.0f;
     const float4 *orow = nullptr;
     if (out) {
         wgt = 2.0f * qh_sigmoid(inj[(size_t)r * groups + g] / (float)groups);
         orow = reinterpret_cast<const float4 *>(out + (size_t)r * dim);
     }
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < n4; i += QH_THREADS) {
-        float4 v = xr[i];
+    auto take = [&](int i, float4 v, float &ss) -> float4 {
         if (out) {
             const float4 o = orow[i];
             v.x += o.x * wgt; v.y += o.y * wgt; v.z += o.z * wgt; v.w += o.w * wgt;
@@ -74,17 +75,56 @@ __global__ void __launch_bounds__(QH_THREADS) k_norm_grouped(float *__restrict__
         ss = __builtin_fmaf(v.y, v.y, ss);
         ss = __builtin_fmaf(v.z, v.z, ss);
         ss = __builtin_fmaf(v.w, v.w, ss);
-    }
-    ss = qh_block_sum(ss, part);
-    const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
-    for (int i = threadIdx.x; i < n4; i += QH_THREADS) {
-        float4 v = xr[i];   // this thread's own values
+        return v;
+    };
+    auto put = [&](int i, float4 v, float inv) {
         const uint2 wb = wr[i];
         v.x = v.x * inv * __uint_as_float(wb.x << 16);
         v.y = v.y * inv * __uint_as_float(wb.x & 0xFFFF0000u);
         v.z = v.z * inv * __uint_as_float(wb.y << 16);
         v.w = v.w * inv * __uint_as_float(wb.y & 0xFFFF0000u);
         yr[i] = v;
+    };
+    float ss = 0.0f;
+    if (NI > 0) {
+        constexpr int NR = NI > 0 ? NI : 1;
+        float4 hv[NR];
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+            const int i = t + QH_THREADS * j;
+            hv[j] = i < n4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+            const int i = t + QH_THREADS * j;
+            if (i < n4) hv[j] = take(i, hv[j], ss);
+        }
+        ss = qh_block_sum(ss, part);
+        const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+            const int i = t + QH_THREADS * j;
+            if (i < n4) put(i, hv[j], inv);
+        }
+    } else {
+        for (int i = t; i < n4; i += QH_THREADS) take(i, xr[i], ss);
+        ss = qh_block_sum(ss, part);
+        const float inv = 1.0f / sqrtf(ss / (float)dim + eps);
+        for (int i = t; i < n4; i += QH_THREADS) put(i, xr[i], inv);   // this thread's own values
+    }
+}
+
+static void qh_norm_launch(hipStream_t s, int blocks, float *y, float *x, const uint16_t *w, int dim, int groups,
+                           float eps, const float *out, const float *inj)
+{
+    const int ni = (dim / 4 + QH_THREADS - 1) / QH_THREADS;
+    const dim3 g((unsigned)blocks), b(QH_THREADS);
+    switch (ni) {
+    case 1: hipLaunchKernelGGL(k_norm_grouped<1>, g, b, 0, s, y, x, w, dim, groups, eps, out, inj); break;
+    case 2: hipLaunchKernelGGL(k_norm_grouped<2>, g, b, 0, s, y, x, w, dim, groups, eps, out, inj); break;
+    case 3: hipLaunchKernelGGL(k_norm_grouped<3>, g, b, 0, s, y, x, w, dim, groups, eps, out, inj); break;
+    case 4: hipLaunchKernelGGL(k_norm_grouped<4>, g, b, 0, s, y, x, w, dim, groups, eps, out, inj); break;
+    default: hipLaunchKernelGGL(k_norm_grouped<0>, g, b, 0, s, y, x, w, dim, groups, eps, out, inj); break;
     }
 }
 
@@ -414,8 +454,7 @@ extern "C" int qwk_rms_norm_grouped(hipStream_t s, float *y, const float *x, con
     if (rows <= 0) return 0;
     if (dim <= 0 || dim % 4 || groups < 1 || !w || ((uintptr_t)x & 15u) || ((uintptr_t)y & 15u) || ((uintptr_t)w & 7u))
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_norm_grouped, dim3((unsigned)(rows * groups)), dim3(QH_THREADS), 0, s, y,
-                       const_cast<float *>(x), w, dim, groups, eps, nullptr, nullptr);
+    qh_norm_launch(s, rows * groups, y, const_cast<float *>(x), w, dim, groups, eps, nullptr, nullptr);
     return (int)hipGetLastError();
 }
 
@@ -426,8 +465,7 @@ extern "C" int qwk_hc_inject_norm(hipStream_t s, float *h4, const float *out, co
     if (H <= 0 || H % 4 || S < 1 || !w || !out || !inj || ((uintptr_t)h4 & 15u) || ((uintptr_t)n4 & 15u) ||
         ((uintptr_t)out & 15u) || ((uintptr_t)w & 7u))
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_norm_grouped, dim3((unsigned)(rows * S)), dim3(QH_THREADS), 0, s, n4, h4, w, H, S, eps, out,
-                       inj);
+    qh_norm_launch(s, rows * S, n4, h4, w, H, S, eps, out, inj);
     return (int)hipGetLastError();
 }
 

@@ -27,7 +27,7 @@ def _rng(seed):
     return np.random.default_rng(seed)
 
 
-@pytest.mark.parametrize("rows,H,S", [(1, 3072, 4), (5, 2560, 4), (33, 256, 3)])
+@pytest.mark.parametrize("rows,H,S", [(1, 3072, 4), (5, 2560, 4), (33, 256, 3), (3, 6144, 2), (2, 1000, 2)])
 def test_grouped_norm_and_inject_norm(gpu, rows, H, S):
     g = _rng(rows * H + S)
     h4 = (g.standard_normal((rows, S * H)) * 2).astype(np.float32)
