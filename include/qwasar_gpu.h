@@ -104,7 +104,8 @@ void qw_op_qmat_q4(qw_cmd c, qw_ref y, qw_ref x,
                    int32_t k, int32_t n, int32_t rows, int32_t group);
 
 /* Up to four one-token matvecs sharing x [1, k] and group, in one launch.
- * False, nothing encoded, for count outside 1..4. */
+ * False, nothing encoded, for count outside 1..4 or k < 2048 (reference
+ * qwasar_gpu.h:105-110); the caller then encodes one qmv per part. */
 typedef struct { qw_ref y, w, scales, biases; int32_t n; } qw_qmv_part;
 bool qw_op_qmv_q4_multi(qw_cmd c, qw_ref x, int32_t k, int32_t group,
                         int32_t count, const qw_qmv_part *parts);
@@ -153,8 +154,9 @@ bool qw_op_hc_mix_up(qw_cmd c, qw_ref x, qw_ref d, qw_ref n4, qw_ref w, qw_ref s
 /* The first half of a decode step (one row) in one launch: h4_out = h4 with
  * the block's output injected, n4 its grouped norm (qw_op_hc_inject_norm),
  * d = down . n4 (4-bit [lowrank, S*H], `group`), inj_out = inj_w . n4 (bf16
- * [S, S*H], order R).  h4_out and inj_out must not be h4 and inj.  False,
- * nothing encoded, for S above 4, or S*H above 15360 or not a multiple of 64. */
+ * [S, S*H], order R).  No output (h4_out, n4, d, inj_out) may overlap an
+ * input (h4, out, inj) or another output.  False, nothing encoded, for such
+ * an overlap, for S above 4, or S*H above 15360 or not a multiple of 64. */
 bool qw_op_hc_pre_decode(qw_cmd c, qw_ref h4_out, qw_ref n4, qw_ref d, qw_ref inj_out, qw_ref h4, qw_ref out,
                          qw_ref inj, qw_ref norm_w, qw_ref down_w, qw_ref down_s, qw_ref down_b, qw_ref inj_w,
                          int32_t H, int32_t S, int32_t lowrank, int32_t group, float eps);
@@ -301,6 +303,15 @@ void qw_moe_layer_free(qw_moe_layer *m);
  * mark count. */
 void   qw_prof_set_enabled(bool on);
 double qw_prof_ms(const char *label, int64_t *count);
+
+/* For tests of the decode path's failure handling; no reference counterpart
+ * (the Metal backend has no cross-workgroup waits).  Sets the hand-off error
+ * word as if the next decode launch's first bounded wait had given up: every
+ * wait of that launch and of later ones gives up at once (each kernel still
+ * runs to its end), qw_cmd_error of every command that launched one of them
+ * reports it after qw_cmd_wait, and the state is then zeroed so that the
+ * next launch runs normally. */
+bool qw_debug_decode_handoff_fail(void);
 
 #ifdef __cplusplus
 }

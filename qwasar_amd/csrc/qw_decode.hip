@@ -146,6 +146,17 @@ __device__ __forceinline__ uint32_t qd_poll_ld(const uint32_t *p)
     return v;
 }
 
+// A wait gave up: the error word takes the launch's epoch unless an earlier
+// failure already set it, so the host learns the first failing launch (and
+// every later launch, whose waits see the word and give up at once, failed
+// with it).  The word is never 0 once raised: epochs start at 1.
+__device__ __forceinline__ void qd_raise(QdSync *S, uint32_t epoch)
+{
+    uint32_t expect = 0u;
+    __hip_atomic_compare_exchange_strong(&S->err, &expect, epoch, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Member i of a producer family of n workgroups whose groups' counters and
 // flags start at `base`: the workgroup's device-coherent stores are done;
 // count it, and publish the epoch if it completes its group.
@@ -176,8 +187,7 @@ __device__ __forceinline__ bool qd_wait_flags(QdSync *S, bool has, int idx, uint
         asm volatile("s_waitcnt vmcnt(0)" : "+v"(v), "+v"(e)::"memory");
         if (__ballot(has && v != epoch) == 0ull) return true;
         if (spins >= QD_SPIN_LIMIT || __ballot(e != 0u) != 0ull) {
-            if ((threadIdx.x & 63) == 0)
-                __hip_atomic_fetch_or(&S->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((threadIdx.x & 63) == 0) qd_raise(S, epoch);
             return false;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -236,8 +246,7 @@ __device__ __forceinline__ uint2 qd_poll_tag(const QdArgs &a, const uint2 *p, bo
         const uint2 r = make_uint2((uint32_t)v, (uint32_t)(v >> 32));
         if (__ballot(has && r.x != a.epoch) == 0ull) return r;
         if (spins >= QD_SPIN_LIMIT || __ballot(e != 0u) != 0ull) {
-            if ((threadIdx.x & 63) == 0)
-                __hip_atomic_fetch_or(&a.sync->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((threadIdx.x & 63) == 0) qd_raise(a.sync, a.epoch);
             return r;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -685,8 +694,10 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
         int pi;
         float pw;
         qw_route_block<PL>(x, E, K, a.m.norm, wave, lane, &pi, &pw, R.rs.one.sx, R.rs.one.vb);
+        // clamped: after a given-up wait the logits are whatever was read,
+        // and no pick may then address outside the banks
         if (wave == 0 && lane < K) {
-            R.picks[lane] = pi;
+            R.picks[lane] = min(max(pi, 0), E - 1);
             R.pw[lane] = pw;
         }
     } else {
@@ -697,7 +708,7 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
             qw_route_wave<PL, true, 2>(reinterpret_cast<const float *>(a.sync->lgt + (size_t)r * (E + 1)) + 1, E, K,
                                        a.m.norm, lane, &pi, &pw, R.rs.sx[wave]);
             if (lane < K) {
-                R.picks[r * K + lane] = pi;
+                R.picks[r * K + lane] = min(max(pi, 0), E - 1);
                 R.pw[r * K + lane] = pw;
             }
         }
@@ -912,7 +923,7 @@ __device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R
             const bool fail = !done && (spins >= QD_SPIN_LIMIT || __ballot(e != 0u) != 0ull);
             if (fail) {
                 mask = 0x80000000u;
-                if (lane == 0) __hip_atomic_fetch_or(&a.sync->err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (lane == 0) qd_raise(a.sync, a.epoch);
             }
             if (lane == 0) __hip_atomic_store(dready, mask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             if (done || fail) break;
@@ -1044,6 +1055,11 @@ extern "C" size_t qwk_moe_decode_sync_bytes(void) { return sizeof(QdSync); }
 extern "C" int qwk_moe_decode_sync_error(const void *sync, uint32_t *err)
 {
     return (int)hipMemcpy(err, &static_cast<const QdSync *>(sync)->err, sizeof *err, hipMemcpyDeviceToHost);
+}
+
+extern "C" int qwk_moe_decode_sync_raise(void *sync, uint32_t epoch)
+{
+    return (int)hipMemcpy(&static_cast<QdSync *>(sync)->err, &epoch, sizeof epoch, hipMemcpyHostToDevice);
 }
 
 template <int LPR, int NUL, int NULD, int PL, bool RES>

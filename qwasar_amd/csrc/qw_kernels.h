@@ -113,9 +113,14 @@ size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows);
  * greater than the last (never 0; zero the state again before an epoch
  * repeats), and launches on one state run in order. */
 size_t qwk_moe_decode_sync_bytes(void);
-/* Reads the state's error word (non-zero: a launch's bounded wait gave up;
- * its outputs are garbage and the state must be zeroed).  Synchronous. */
+/* Reads the state's error word.  Non-zero: the epoch of the first launch
+ * whose bounded wait gave up; that launch's outputs and those of every later
+ * launch on the state are garbage, and the state must be zeroed.
+ * Synchronous. */
 int qwk_moe_decode_sync_error(const void *sync, uint32_t *err);
+/* Sets the error word as a failed wait of launch `epoch` would (synchronous);
+ * every wait of a later launch then gives up at once. */
+int qwk_moe_decode_sync_raise(void *sync, uint32_t epoch);
 /* Non-zero when the decode path takes this layer shape and token count. */
 int qwk_moe_decode_supported(const qwk_moe *M, int rows);
 /* The residual step before a layer of a stack: the layer's input is

@@ -9,9 +9,11 @@
  * The reference does this in qwasar.c: config parse (:700-775), the
  * safetensors table, qw_bind_moe (:1532-1563) with qw_bind_qbank
  * (:1469-1495), qw_bind_qlinear (:906-940), qw_qgroup_from_shapes (:892-903)
- * and qw_bind_small (:1426-1461).  Same tensor names, same shape checks and
- * the same dequantisation of a small quantised matrix to bf16 (w = scale * q
- * + bias per group, rounded to nearest even), done on the host at load.
+ * and qw_bind_small (:1426-1461).  What a checkpoint must satisfy is the
+ * same -- the tensor names and shapes the formats dictate, and a small
+ * quantised matrix expanded to bf16 as w = scale * q + bias per group,
+ * rounded to nearest even -- but the checks here run from a per-format plan
+ * through one shape check of their own (see "binding" below).
  *
  * Files are mapped read-only; each bound tensor is copied once into its own
  * device buffer, and the mapping is released when the checkpoint is closed.
@@ -228,13 +230,6 @@ static const st_tensor *find(const qw_checkpoint ck, const char *name)
     return bsearch(&key, ck->t, ck->nt, sizeof *ck->t, cmp_name);
 }
 
-static const st_tensor *findf(const qw_checkpoint ck, const char *fmt, const char *prefix)
-{
-    char name[400];
-    snprintf(name, sizeof name, fmt, prefix);
-    return find(ck, name);
-}
-
 static bool add_file(qw_checkpoint ck, const char *path, char *err, size_t cap)
 {
     const int fd = open(path, O_RDONLY);
@@ -283,10 +278,18 @@ static bool add_file(qw_checkpoint ck, const char *path, char *err, size_t cap)
         for (int i = 0; i < DT_COUNT; i++)
             if (!strcmp(dt, dt_names[i])) t.dtype = i;
         if (t.dtype < 0) { errf(err, cap, "%s: %.*s has unknown dtype %s", path, (int)kl, k, dt); ok = false; break; }
-        int64_t count = 1;
-        for (int i = 0; i < t.ndim; i++) count *= t.shape[i];
-        if (off[0] < 0 || off[1] < off[0] || (uint64_t)off[1] > body ||
-            (uint64_t)(off[1] - off[0]) != (uint64_t)count * (uint64_t)dt_size[t.dtype]) {
+        /* the element count and byte size, each product checked: a header
+         * with negative or huge dims must not wrap to the data's length */
+        uint64_t bytes = (uint64_t)dt_size[t.dtype];
+        bool dims_ok = true;
+        for (int i = 0; i < t.ndim && dims_ok; i++)
+            dims_ok = t.shape[i] >= 0 && !__builtin_mul_overflow(bytes, (uint64_t)t.shape[i], &bytes);
+        if (!dims_ok) {
+            errf(err, cap, "%s: %.*s has a negative or oversized shape", path, (int)kl, k);
+            ok = false;
+            break;
+        }
+        if (off[0] < 0 || off[1] < off[0] || (uint64_t)off[1] > body || (uint64_t)(off[1] - off[0]) != bytes) {
             errf(err, cap, "%s: %.*s's data offsets [%lld, %lld) do not hold its shape", path, (int)kl, k,
                  (long long)off[0], (long long)off[1]);
             ok = false;
@@ -416,7 +419,15 @@ bool qw_checkpoint_tensor(qw_checkpoint ck, const char *name, const void **data,
     return true;
 }
 
-/* ---- binding --------------------------------------------------------------- */
+/* ---- binding ------------------------------------------------------------------
+ *
+ * A layer is bound from a plan: the list of tensors its format holds (fused
+ * or MLX split banks, the shared expert, the router and the shared gate),
+ * each with the dims the config implies.  Every tensor goes through one
+ * check, expect(), which names the tensor and prints what was found beside
+ * what the layer needs.  Quantised matrices take their group from the scale
+ * columns; the two small matrices are taken as bf16, or expanded to bf16 from
+ * 4 or 8 bits a group at a time. */
 
 static uint16_t f32_to_bf16(float f)
 {
@@ -436,116 +447,146 @@ static float bf16_to_f32(uint16_t b)
 static bool upload(qw_ref *r, const void *src, size_t len, const char *what, char *err, size_t cap)
 {
     qw_buf b = qw_buf_from_bytes_(src, len);
-    if (!b) { errf(err, cap, "cannot place %s (%zu bytes) on the device", what, len); return false; }
+    if (!b) { errf(err, cap, "%s: no device memory for %zu bytes", what, len); return false; }
     *r = (qw_ref){b, 0};
     return true;
 }
 
-static bool is_word(const st_tensor *t) { return t->dtype == DT_U32 || t->dtype == DT_I32; }
+/* Element types a slot accepts: packed words (U32 or I32, as exporters
+ * differ) or bf16. */
+enum { ANY_WORDS, ANY_BF16 };
 
-/* group from the scale count, as qwasar.c:892-903: 32 or 64 */
-static bool group_from_shapes(const st_tensor *sc, int32_t in, const char *prefix, int32_t *g, char *err,
-                              size_t cap)
+static bool type_ok(const st_tensor *t, int want)
 {
-    const int64_t groups = sc->ndim ? sc->shape[sc->ndim - 1] : 0;
-    const int32_t gs = groups > 0 ? (int32_t)(in / groups) : 0;
-    if ((gs != 32 && gs != 64) || (int64_t)gs * groups != in) {
-        errf(err, cap, "%s: %lld scale groups over %d inputs is not group 32 or 64", prefix, (long long)groups, in);
-        return false;
-    }
-    *g = gs;
-    return true;
+    return want == ANY_BF16 ? t->dtype == DT_BF16 : (t->dtype == DT_U32 || t->dtype == DT_I32);
 }
 
-/* a 4-bit matrix [out, in] (count == 0) or bank [count, out, in] */
-static bool bind_q4(qw_checkpoint ck, qw_q4_ref *q, const char *prefix, int32_t count, int32_t in, int32_t out,
-                    char *err, size_t cap)
+static void dims_text(char *buf, size_t cap, int nd, const int64_t *d)
 {
-    const st_tensor *w = findf(ck, "%s.weight", prefix), *s = findf(ck, "%s.scales", prefix),
-                    *b = findf(ck, "%s.biases", prefix);
-    if (!w || !s || !b) {
-        errf(err, cap, count ? "missing quantised bank %s" : "missing quantised tensors for %s", prefix);
-        return false;
-    }
-    int32_t g;
-    if (!group_from_shapes(s, in, prefix, &g, err, cap)) return false;
-    const int nd = count ? 3 : 2;
-    const int64_t lead = count ? count : out, mid = count ? out : in / 8, words = in / 8, groups = in / g;
-    if (!is_word(w) || w->ndim != nd || w->shape[0] != lead || (count && w->shape[1] != out) ||
-        w->shape[nd - 1] != words || in % 8) {
-        if (count)
-            errf(err, cap, "%s.weight is [%lld,%lld,%lld], expected [%d,%d,%lld]", prefix, (long long)w->shape[0],
-                 (long long)(w->ndim > 1 ? w->shape[1] : 0), (long long)(w->ndim > 2 ? w->shape[2] : 0), count, out,
-                 (long long)words);
-        else
-            errf(err, cap, "%s.weight is [%lld,%lld], expected [%d,%lld]", prefix, (long long)w->shape[0],
-                 (long long)(w->ndim > 1 ? w->shape[1] : 0), out, (long long)mid);
-        return false;
-    }
-    if (s->dtype != DT_BF16 || s->ndim != nd || s->shape[0] != lead || (count && s->shape[1] != out) ||
-        s->shape[nd - 1] != groups) {
-        errf(err, cap, "%s.scales has %lld groups, expected %lld", prefix, (long long)s->shape[s->ndim - 1],
-             (long long)groups);
-        return false;
-    }
-    if (b->dtype != DT_BF16 || b->nbytes != s->nbytes) {
-        errf(err, cap, "%s.biases does not match its scales", prefix);
-        return false;
-    }
-    q->group = g;
-    return upload(&q->w, w->data, w->nbytes, prefix, err, cap) &&
-           upload(&q->scales, s->data, s->nbytes, prefix, err, cap) &&
-           upload(&q->biases, b->data, b->nbytes, prefix, err, cap);
+    size_t n = (size_t)snprintf(buf, cap, "[");
+    for (int i = 0; i < nd && n < cap; i++)
+        n += (size_t)snprintf(buf + n, cap - n, i ? ",%lld" : "%lld", (long long)d[i]);
+    if (n < cap) snprintf(buf + n, cap - n, "]");
 }
 
-/* A small bf16 [rows, cols] matrix: as stored when bf16, else dequantised
- * from a 4- or 8-bit affine matrix (qwasar.c:1426-1461). */
-static bool bind_small(qw_checkpoint ck, qw_ref *r, const char *prefix, int64_t rows, int64_t cols, char *err,
-                       size_t cap)
+/* The tensor `name`, required present with element type `want` and dims
+ * d[0..nd) (d[i] < 0: any); NULL with a message otherwise. */
+static const st_tensor *expect(qw_checkpoint ck, const char *name, int want, int nd, const int64_t *d, char *err,
+                               size_t cap)
 {
-    char p[320];
-    snprintf(p, sizeof p, "%s.weight", prefix);
-    const st_tensor *w = find(ck, p);
-    if (w && w->dtype == DT_BF16) {
-        if (w->ndim != 2 || w->shape[0] != rows || w->shape[1] != cols) {
-            errf(err, cap, "%s is BF16 [%lld,%lld], expected bf16 [%lld,%lld]", p, (long long)w->shape[0],
-                 (long long)(w->ndim > 1 ? w->shape[1] : 0), (long long)rows, (long long)cols);
-            return false;
-        }
-        return upload(r, w->data, w->nbytes, p, err, cap);
-    }
-    const st_tensor *sc = findf(ck, "%s.scales", prefix), *bi = findf(ck, "%s.biases", prefix);
-    if (!w || !sc || !bi || !is_word(w) || w->ndim != 2 || w->shape[0] != rows || sc->ndim != 2 ||
-        sc->shape[0] != rows || sc->dtype != DT_BF16 || bi->dtype != DT_BF16 || bi->nbytes != sc->nbytes) {
-        errf(err, cap, "%s: neither bf16 [%lld,%lld] nor a quantised matrix of that shape", prefix, (long long)rows,
-             (long long)cols);
+    const st_tensor *t = find(ck, name);
+    if (!t) { errf(err, cap, "checkpoint has no tensor %s", name); return NULL; }
+    bool fits = type_ok(t, want) && t->ndim == nd;
+    for (int i = 0; fits && i < nd; i++) fits = d[i] < 0 || t->shape[i] == d[i];
+    if (fits) return t;
+    char got[96], need[96];
+    dims_text(got, sizeof got, t->ndim, t->shape);
+    dims_text(need, sizeof need, nd, d);   /* -1 marks a free dim */
+    errf(err, cap, "%s: stored as %s %s; this layer needs %s %s", name, dt_names[t->dtype], got,
+         want == ANY_BF16 ? "BF16" : "U32 (or I32)", need);
+    return NULL;
+}
+
+/* One quantised slot of the plan: `nbank` matrices (0: a single matrix) of
+ * [out, in], 4-bit, at "<base>.{weight,scales,biases}". */
+typedef struct {
+    qw_q4_ref *dst;
+    char base[200];
+    int32_t nbank, out, in;
+} q4_slot;
+
+static bool bind_slot(qw_checkpoint ck, const q4_slot *sl, char *err, size_t cap)
+{
+    char nw[224], ns[224], nb[224];
+    snprintf(nw, sizeof nw, "%s.weight", sl->base);
+    snprintf(ns, sizeof ns, "%s.scales", sl->base);
+    snprintf(nb, sizeof nb, "%s.biases", sl->base);
+    if (sl->in % 8) { errf(err, cap, "%s: %d inputs do not pack into 4-bit words", sl->base, sl->in); return false; }
+    /* dims: [nbank,] out, cols; rc points at [out, cols] */
+    const int lead = sl->nbank ? 1 : 0, nd = 2 + lead;
+    int64_t d[3] = {sl->nbank, 0, 0};
+    int64_t *rc = d + lead;
+    rc[0] = sl->out;
+    rc[1] = sl->in / 8;
+    const st_tensor *w = expect(ck, nw, ANY_WORDS, nd, d, err, cap);
+    if (!w) return false;
+    /* the scale columns fix the group: one scale per `group` inputs */
+    rc[1] = -1;
+    const st_tensor *sc = expect(ck, ns, ANY_BF16, nd, d, err, cap);
+    if (!sc) return false;
+    const int64_t ncol = sc->shape[nd - 1];
+    const int64_t group = ncol > 0 && sl->in % ncol == 0 ? sl->in / ncol : 0;
+    if (group != 32 && group != 64) {
+        errf(err, cap, "%s: %lld scale columns over %d inputs; the kernels take groups of 32 or 64", ns,
+             (long long)ncol, sl->in);
         return false;
     }
-    const int64_t bits = w->shape[1] * 32 / cols, groups = sc->shape[1];
-    const int64_t group = groups ? cols / groups : 0;
-    if ((bits != 4 && bits != 8) || w->shape[1] * 32 != bits * cols || group * groups != cols ||
-        group % (32 / bits) != 0) {
-        errf(err, cap, "%s: %lld words and %lld groups per row do not describe %lld inputs", prefix,
-             (long long)w->shape[1], (long long)groups, (long long)cols);
+    rc[1] = ncol;
+    const st_tensor *bi = expect(ck, nb, ANY_BF16, nd, d, err, cap);
+    if (!bi) return false;
+    sl->dst->group = (int32_t)group;
+    return upload(&sl->dst->w, w->data, w->nbytes, nw, err, cap) &&
+           upload(&sl->dst->scales, sc->data, sc->nbytes, ns, err, cap) &&
+           upload(&sl->dst->biases, bi->data, bi->nbytes, nb, err, cap);
+}
+
+/* A small [rows, cols] matrix bound as bf16: "<base>.weight" as stored when
+ * bf16, else expanded on the host from packed 4- or 8-bit values with
+ * per-group bf16 scales and biases, w = s * q + b rounded to nearest even
+ * (the reference's arithmetic for these, qwasar.c:1426-1461). */
+static bool bind_bf16(qw_checkpoint ck, qw_ref *dst, const char *base, int64_t rows, int64_t cols, char *err,
+                      size_t cap)
+{
+    char nw[224], ns[224], nb[224];
+    snprintf(nw, sizeof nw, "%s.weight", base);
+    const st_tensor *w = find(ck, nw);
+    if (!w) { errf(err, cap, "checkpoint has no tensor %s", nw); return false; }
+    const int64_t d[2] = {rows, cols};
+    if (w->dtype == DT_BF16) {
+        if (!expect(ck, nw, ANY_BF16, 2, d, err, cap)) return false;
+        return upload(dst, w->data, w->nbytes, nw, err, cap);
+    }
+    /* packed: the word count per row says how wide a value is */
+    const int64_t dw[2] = {rows, -1};
+    if (!expect(ck, nw, ANY_WORDS, 2, dw, err, cap)) return false;
+    const int64_t wpr = w->shape[1];
+    const int bits = wpr * 8 == cols ? 4 : wpr * 4 == cols ? 8 : 0;
+    if (!bits) {
+        errf(err, cap, "%s: %lld words a row hold neither 4- nor 8-bit values for %lld columns", nw,
+             (long long)wpr, (long long)cols);
         return false;
     }
-    uint16_t *out = malloc((size_t)(rows * cols) * 2);
-    if (!out) { errf(err, cap, "out of memory for %s", p); return false; }
-    const int64_t per = 32 / bits, words = w->shape[1];
-    const uint32_t mask = (1u << bits) - 1u;
-    for (int64_t i = 0; i < rows; i++) {
-        for (int64_t j = 0; j < cols; j++) {
-            uint32_t word;
-            uint16_t s, b;
-            memcpy(&word, w->data + 4 * (i * words + j / per), 4);
-            memcpy(&s, sc->data + 2 * (i * groups + j / group), 2);
-            memcpy(&b, bi->data + 2 * (i * groups + j / group), 2);
-            const uint32_t q = (word >> (bits * (j % per))) & mask;
-            out[i * cols + j] = f32_to_bf16(bf16_to_f32(s) * (float)q + bf16_to_f32(b));
-        }
+    snprintf(ns, sizeof ns, "%s.scales", base);
+    snprintf(nb, sizeof nb, "%s.biases", base);
+    const st_tensor *sc = expect(ck, ns, ANY_BF16, 2, dw, err, cap);
+    if (!sc) return false;
+    const int64_t ng = sc->shape[1], gw = ng > 0 && cols % ng == 0 ? cols / ng : 0;
+    if (gw == 0 || gw % (32 / bits)) {
+        errf(err, cap, "%s: %lld scale columns do not cut %lld %d-bit columns into whole words", ns,
+             (long long)ng, (long long)cols, bits);
+        return false;
     }
-    const bool ok = upload(r, out, (size_t)(rows * cols) * 2, p, err, cap);
-    free(out);
+    const int64_t db[2] = {rows, ng};
+    const st_tensor *bi = expect(ck, nb, ANY_BF16, 2, db, err, cap);
+    if (!bi) return false;
+    uint16_t *o = malloc((size_t)(rows * cols) * sizeof *o);
+    if (!o) { errf(err, cap, "%s: host memory for the bf16 copy", nw); return false; }
+    const uint32_t *W = (const uint32_t *)w->data;   /* safetensors data is 8-byte aligned in the file */
+    const uint16_t *S = (const uint16_t *)sc->data, *B = (const uint16_t *)bi->data;
+    const int vals = 32 / bits;
+    const uint32_t m = (1u << bits) - 1u;
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t g = 0; g < ng; g++) {
+            const float s = bf16_to_f32(S[r * ng + g]), b = bf16_to_f32(B[r * ng + g]);
+            const uint32_t *src = W + r * wpr + g * (gw / vals);
+            uint16_t *dst_row = o + r * cols + g * gw;
+            for (int64_t k = 0; k < gw; k++) {
+                const uint32_t q = (src[k / vals] >> (bits * (int)(k % vals))) & m;
+                dst_row[k] = f32_to_bf16(s * (float)q + b);
+            }
+        }
+    const bool ok = upload(dst, o, (size_t)(rows * cols) * sizeof *o, nw, err, cap);
+    free(o);
     return ok;
 }
 
@@ -560,32 +601,36 @@ bool qw_moe_layer_load(qw_checkpoint ck, int32_t layer, qw_moe_layer *m, char *e
     }
     const int32_t H = ck->H, I = ck->I, SI = ck->SI, E = ck->E;
     m->H = H; m->E = E; m->K = ck->K; m->I = I; m->SI = SI; m->norm = ck->norm;
-    char prefix[256], p[320];
-    snprintf(prefix, sizeof prefix, "language_model.model.layers.%d.mlp", layer);
-    bool ok;
-    snprintf(p, sizeof p, "%s.gate", prefix);
-    ok = bind_small(ck, &m->router, p, E, H, err, errcap);
-    m->split = findf(ck, "%s.switch_mlp.gate_proj.weight", prefix) != NULL;
-    if (ok && m->split) {
-        snprintf(p, sizeof p, "%s.switch_mlp.gate_proj", prefix);
-        ok = bind_q4(ck, &m->gate, p, E, H, I, err, errcap);
-        snprintf(p, sizeof p, "%s.switch_mlp.up_proj", prefix);
-        if (ok) ok = bind_q4(ck, &m->up, p, E, H, I, err, errcap);
-        snprintf(p, sizeof p, "%s.switch_mlp.down_proj", prefix);
-    } else if (ok) {
-        snprintf(p, sizeof p, "%s.experts.gate_up_proj", prefix);
-        ok = bind_q4(ck, &m->gate_up, p, E, H, 2 * I, err, errcap);
-        snprintf(p, sizeof p, "%s.experts.down_proj", prefix);
+    char mlp[160], base[200];
+    snprintf(mlp, sizeof mlp, "language_model.model.layers.%d.mlp", layer);
+    snprintf(base, sizeof base, "%s.switch_mlp.gate_proj.weight", mlp);
+    m->split = find(ck, base) != NULL;
+
+    /* the plan: banks first, then the shared expert's three matrices */
+    typedef struct { qw_q4_ref *dst; const char *leaf; int32_t nbank, out, in; } plan_row;
+    plan_row plan[6];
+    int n = 0;
+    if (m->split) {
+        plan[n++] = (plan_row){&m->gate, "switch_mlp.gate_proj", E, I, H};
+        plan[n++] = (plan_row){&m->up, "switch_mlp.up_proj", E, I, H};
+        plan[n++] = (plan_row){&m->down, "switch_mlp.down_proj", E, H, I};
+    } else {
+        plan[n++] = (plan_row){&m->gate_up, "experts.gate_up_proj", E, 2 * I, H};
+        plan[n++] = (plan_row){&m->down, "experts.down_proj", E, H, I};
     }
-    if (ok) ok = bind_q4(ck, &m->down, p, E, I, H, err, errcap);
-    snprintf(p, sizeof p, "%s.shared_expert.gate_proj", prefix);
-    if (ok) ok = bind_q4(ck, &m->sh_gate, p, 0, H, SI, err, errcap);
-    snprintf(p, sizeof p, "%s.shared_expert.up_proj", prefix);
-    if (ok) ok = bind_q4(ck, &m->sh_up, p, 0, H, SI, err, errcap);
-    snprintf(p, sizeof p, "%s.shared_expert.down_proj", prefix);
-    if (ok) ok = bind_q4(ck, &m->sh_down, p, 0, SI, H, err, errcap);
-    snprintf(p, sizeof p, "%s.shared_expert_gate", prefix);
-    if (ok) ok = bind_small(ck, &m->sh_gate_w, p, 1, H, err, errcap);
+    plan[n++] = (plan_row){&m->sh_gate, "shared_expert.gate_proj", 0, SI, H};
+    plan[n++] = (plan_row){&m->sh_up, "shared_expert.up_proj", 0, SI, H};
+    plan[n++] = (plan_row){&m->sh_down, "shared_expert.down_proj", 0, H, SI};
+
+    snprintf(base, sizeof base, "%s.gate", mlp);
+    bool ok = bind_bf16(ck, &m->router, base, E, H, err, errcap);
+    for (int i = 0; ok && i < n; i++) {
+        q4_slot sl = {plan[i].dst, "", plan[i].nbank, plan[i].out, plan[i].in};
+        snprintf(sl.base, sizeof sl.base, "%s.%s", mlp, plan[i].leaf);
+        ok = bind_slot(ck, &sl, err, errcap);
+    }
+    snprintf(base, sizeof base, "%s.shared_expert_gate", mlp);
+    if (ok) ok = bind_bf16(ck, &m->sh_gate_w, base, 1, H, err, errcap);
     if (!ok) qw_moe_layer_free(m);
     return ok;
 }

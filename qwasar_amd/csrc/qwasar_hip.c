@@ -60,7 +60,7 @@ struct qw_cmd_s {
     hipEvent_t *evs;         /* every event this command created */
     int nevs, capevs;
     hipEvent_t last;         /* where the next mark starts */
-    int decoded;             /* launched the decode path since the last wait */
+    uint32_t ep_hi;          /* the last decode epoch this command launched, 0: none unchecked */
     struct qw_cmd_s *next;   /* live commands, for qw_buf_free */
 };
 
@@ -311,8 +311,10 @@ static void touch(qw_cmd c, qw_ref r, int writes) {
 
 static void *dp(qw_ref r) { return r.buf ? (char *)r.buf->dev + r.off : NULL; }
 
+
 /* The decode launch's hand-off state: allocated and zeroed on first use,
- * zeroed again (epoch restarting) after a launch reported an error. */
+ * zeroed again (epochs restarting at 1) after a launch reported an error and
+ * before an epoch would repeat. */
 static int dsync_reset(void) {
     hipStreamSynchronize(G.stream);
     if (!G.dsync && hipMalloc(&G.dsync, qwk_moe_decode_sync_bytes()) != hipSuccess) {
@@ -322,6 +324,39 @@ static int dsync_reset(void) {
     if (hipMemset(G.dsync, 0, qwk_moe_decode_sync_bytes()) != hipSuccess) return 0;
     G.depoch = 0;
     return 1;
+}
+
+/* With the stream drained: reads the hand-off error word, which holds the
+ * epoch of the first decode launch whose wait gave up.  That launch and
+ * every later one failed, so every live command that launched an epoch at or
+ * after it is failed, whichever command is waiting.  Then the state is zeroed
+ * and, every launch so far being checked, the commands' epoch marks are
+ * cleared.  Returns 0 when the state could not be read or zeroed. */
+static int dsync_check(int force_reset) {
+    if (!G.dsync) return 1;
+    int pending = force_reset;
+    for (qw_cmd q = G.live; q; q = q->next) pending |= q->ep_hi != 0;
+    if (!pending) return 1;
+    uint32_t first = 0;
+    if (qwk_moe_decode_sync_error(G.dsync, &first) != 0) first = 1;   /* unreadable: fail them all */
+    if (first != 0)
+        for (qw_cmd q = G.live; q; q = q->next)
+            if (q->ep_hi >= first)
+                cmd_fail(q, hipErrorLaunchFailure,
+                         "moe_layer (decode): a hand-off wait gave up (launch %u of this state)", first);
+    for (qw_cmd q = G.live; q; q = q->next) q->ep_hi = 0;
+    return first != 0 || force_reset ? dsync_reset() : 1;
+}
+
+/* For tests of the failure path: the hand-off error word is set as if the
+ * next decode launch's first wait had given up, so every wait of that launch
+ * and of later ones gives up at once (each kernel still runs to its end) and
+ * the waiting command reports the failure. */
+bool qw_debug_decode_handoff_fail(void) {
+    if (!ensure_init()) return false;
+    if (!G.dsync && !dsync_reset()) return false;
+    hipStreamSynchronize(G.stream);
+    return qwk_moe_decode_sync_raise(G.dsync, G.depoch + 1u) == 0;
 }
 
 /* Launch result of one op: a refusal (invalid shape) is printed, as the
@@ -347,14 +382,7 @@ void qw_cmd_wait(qw_cmd c) {
     if (!c) return;
     hipError_t e = hipStreamSynchronize(G.stream);
     if (e != hipSuccess) cmd_fail(c, e, "device: %s", hipGetErrorString(e));
-    if (c->decoded) {
-        c->decoded = 0;
-        uint32_t derr = 0;
-        if (qwk_moe_decode_sync_error(G.dsync, &derr) != 0 || derr != 0) {
-            cmd_fail(c, hipErrorLaunchFailure, "moe_layer (decode): a hand-off wait gave up");
-            dsync_reset();
-        }
-    }
+    dsync_check(0);
     for (int i = 0; i < c->nwritten; i++) {
         qw_buf b = c->written[i];
         if (b->exposed && b->host_stale) {
@@ -439,8 +467,12 @@ void qw_op_qmat_q4(qw_cmd c, qw_ref y, qw_ref x, qw_ref w, qw_ref scales, qw_ref
 
 bool qw_op_qmv_q4_multi(qw_cmd c, qw_ref x, int32_t k, int32_t group, int32_t count,
                         const qw_qmv_part *parts) {
-    if (count < 1 || count > 4) return false;
+    /* The reference's contract (qwasar_gpu.h:105-107): one to four parts
+     * over an input of at least 2048, else false and nothing encoded; its
+     * caller then falls back to one qmv per part. */
+    if (count < 1 || count > 4 || k < 2048) return false;
     if (!c) return true;
+    if (!parts) return false;
     qwk_q4 m[4];
     float *ys[4];
     int ns[4];
@@ -452,8 +484,9 @@ bool qw_op_qmv_q4_multi(qw_cmd c, qw_ref x, int32_t k, int32_t group, int32_t co
         ys[i] = dp(parts[i].y);
         ns[i] = parts[i].n;
     }
-    launched(c, "qmv_q4_multi", qwk_q4mv_multi(G.stream, dp(x), k, group, count, m, ys, ns));
-    return true;
+    const int rc = qwk_q4mv_multi(G.stream, dp(x), k, group, count, m, ys, ns);
+    launched(c, "qmv_q4_multi", rc);
+    return rc == 0;
 }
 
 void qw_op_dmat_bf16(qw_cmd c, qw_ref y, qw_ref x, qw_ref w, int32_t k, int32_t n, int32_t rows) {
@@ -520,14 +553,27 @@ bool qw_op_hc_mix_up(qw_cmd c, qw_ref x, qw_ref d, qw_ref n4, qw_ref w, qw_ref s
     return rc == 0;
 }
 
+/* Whether [a, a + la) and [b, b + lb) share a byte of one buffer. */
+static bool refs_overlap(qw_ref a, size_t la, qw_ref b, size_t lb) {
+    return a.buf && a.buf == b.buf && a.off < b.off + lb && b.off < a.off + la;
+}
+
 bool qw_op_hc_pre_decode(qw_cmd c, qw_ref h4_out, qw_ref n4, qw_ref d, qw_ref inj_out, qw_ref h4, qw_ref out,
                          qw_ref inj, qw_ref norm_w, qw_ref down_w, qw_ref down_s, qw_ref down_b, qw_ref inj_w,
                          int32_t H, int32_t S, int32_t lowrank, int32_t group, float eps) {
     const int32_t HH = S * H;
     if (H < 4 || H % 4 || S < 1 || S > 4 || HH % 64 || HH > 15360 || lowrank < 1 || HH % group ||
-        (group != 32 && group != 64 && group != 128) ||
-        (h4_out.buf == h4.buf && h4_out.off == h4.off) || (inj_out.buf == inj.buf && inj_out.off == inj.off))
+        (group != 32 && group != 64 && group != 128))
         return false;
+    /* Every workgroup reads all of h4, out and inj while others write the
+     * outputs, so no output may share a byte with an input or another output. */
+    const qw_ref outs[4] = { h4_out, n4, d, inj_out }, ins[3] = { h4, out, inj };
+    const size_t lo[4] = { 4u * (size_t)HH, 4u * (size_t)HH, 4u * (size_t)lowrank, 4u * (size_t)S };
+    const size_t li[3] = { 4u * (size_t)HH, 4u * (size_t)H, 4u * (size_t)S };
+    for (int i = 0; i < 4; i++) {
+        for (int j = 0; j < 3; j++) if (refs_overlap(outs[i], lo[i], ins[j], li[j])) return false;
+        for (int j = i + 1; j < 4; j++) if (refs_overlap(outs[i], lo[i], outs[j], lo[j])) return false;
+    }
     if (!c) return true;
     touch(c, h4, 0); touch(c, out, 0); touch(c, inj, 0); touch(c, norm_w, 0);
     touch(c, down_w, 0); touch(c, down_s, 0); touch(c, down_b, 0); touch(c, inj_w, 0);
@@ -807,7 +853,7 @@ static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float
     }
     /* Flags and tagged logits hold past epochs, so an epoch is not reused
      * until the state is zeroed again (0 is "never"). */
-    if (G.depoch == UINT32_MAX && !dsync_reset()) {
+    if (G.depoch == UINT32_MAX && !dsync_check(1)) {
         cmd_fail(c, hipErrorUnknown, "moe_layer: decode hand-off state");
         return false;
     }
@@ -817,7 +863,7 @@ static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float
     const int rc = qwk_moe_decode(G.stream, out, idx, w, x, res, &m, rows, S, need, G.dsync, G.depoch,
                                   per_kernel ? ev : NULL);
     if (per_kernel) cmd_add_mark(c, "moe decode", ev[0], ev[1]);
-    c->decoded = 1;
+    c->ep_hi = G.depoch;
     launched(c, "moe_layer (decode)", rc);
     return rc == 0;
 }

@@ -88,6 +88,7 @@ _sig("qw_cmd_mark", None, _P, C.c_char_p)
 _sig("qw_prof_reset", None)
 _sig("qw_prof_set_enabled", None, _B)
 _sig("qw_prof_ms", C.c_double, C.c_char_p, C.POINTER(C.c_int64))
+_sig("qw_debug_decode_handoff_fail", _B)
 
 _sig("qw_op_qmat_q4", None, _P, _R, _R, _R, _R, _R, _I, _I, _I, _I)
 _sig("qw_op_qmv_q4", None, _P, _R, _R, _R, _R, _R, _I, _I, _I, _I)

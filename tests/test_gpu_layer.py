@@ -14,6 +14,7 @@ import pytest
 
 from oracle import ref
 from qwasar_amd import synth
+from tests import oracle_par
 from tests.fixture_layers import layer_from_npz
 
 pytestmark = pytest.mark.gpu
@@ -143,8 +144,9 @@ def test_config3_prefill_sample(gpu):
     widx, ww = ref.route(logits, x.shape[0], L.E, L.K, norm=True)
     assert np.array_equal(idx, widx)
     assert np.array_equal(w.view(np.uint32), ww.view(np.uint32))
-    sel = np.arange(0, 512, 37)
-    wout, _, _ = ref.moe_forward(L, np.ascontiguousarray(x[sel]))
+    # 128 tokens: every fourth, which takes hot and cold experts alike
+    sel = np.arange(0, 512, 4)
+    wout, _, _ = oracle_par.moe_rows(L, x[sel])
     e = rel_l2(out[sel], wout)
     assert e < 1e-3 and np.abs(out[sel] - wout).max() < 2e-2, f"rel-L2 {e:.3g}"
     # the skew: the hottest expert takes many tokens
@@ -154,6 +156,28 @@ def test_config3_prefill_sample(gpu):
     out2, _, _ = run_layer(gpu, lb, x)
     assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
     lb.free()
+
+
+def test_config4_prefill_chunk_2048(gpu, c1):
+    """Config 4's prefill leg on one layer: a 2048-token chunk at config 1's
+    shape (20,480 pairs, about 40 a expert, 64-row tiles).  All 2048 x 10
+    routing ids and weights bit-exact; outputs of 128 tokens spread over the
+    chunk to the bar; a second run bit-identical."""
+    L, lb = c1
+    rows = 2048
+    x = synth.make_x(2048_0001, rows, L.H)
+    out, idx, w = run_layer(gpu, lb, x)
+    widx, ww = oracle_par.route_rows(L, x)
+    assert np.array_equal(idx, widx), f"{(idx != widx).sum()} routing ids differ"
+    assert np.array_equal(w.view(np.uint32), ww.view(np.uint32)), "routing weights not bit-exact"
+    sel = np.arange(7, rows, 16)
+    wout, _, _ = oracle_par.moe_rows(L, x[sel])
+    e = rel_l2(out[sel], wout)
+    m = float(np.abs(out[sel] - wout).max())
+    print(f"2048-row chunk: rel-L2 {e:.3g} max-abs {m:.3g} on {sel.size} rows")
+    assert e < 1e-3 and m < 2e-2
+    out2, _, _ = run_layer(gpu, lb, x)
+    assert np.array_equal(out.view(np.uint32), out2.view(np.uint32)), "prefill not deterministic"
 
 
 @pytest.mark.parametrize("split", [True, False])

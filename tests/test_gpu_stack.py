@@ -253,3 +253,69 @@ def test_stack_config4_full_size_decode(gpu):
     st.free()
     for L in layers:
         L.free()
+
+
+def test_stack_config4_full_size_prefill(gpu):
+    """Config 4's prefill at full size: 48 layers of config 1's shape, one
+    2048-token chunk, twice (the same bits both times, and with the residual
+    step folded into each layer's op); then the first and the last layer on
+    their GPU inputs against the oracle: all 2048 x 10 routing ids and
+    weights bit-exact, 128 sampled rows of y to the grouped bar, the bf16
+    carry bit-exact on every row."""
+    from tests import oracle_par
+    c1 = dict(synth.CONFIGS[1])
+    c1.pop("rows")
+    rows = 2048
+    layers = [stack.DeviceLayer(2027, l, **c1) for l in range(48)]
+    st = stack.Stack(layers, rows)
+    H, K = c1["H"], c1["K"]
+    h0 = synth.to_bf16(synth.normal(2027, "stack.h0.prefill", rows * H).astype(np.float32)).reshape(rows, -1)
+    outs = []
+    for _ in range(2):
+        st.h.write(h0)
+        c = gpu.qw_cmd_begin()
+        st.encode(c, rows)
+        gpu.run(c, "48-layer prefill")
+        outs.append(st.h.read(np.uint16, (rows, H)))
+    assert np.array_equal(outs[0], outs[1]), "the prefill stack is not deterministic"
+    st.h.write(h0)
+    c = gpu.qw_cmd_begin()
+    st.encode_fused(c, rows)
+    gpu.run(c, "48-layer prefill, residual folded in")
+    assert np.array_equal(st.h_final.read(np.uint16, (rows, H)), outs[0]), "fused stack differs"
+    assert np.isfinite(synth.bf16_to_f32(outs[0])).all()
+    sel = np.arange(3, rows, 16)
+    for l in (0, 47):
+        st.h.write(h0)
+        c = gpu.qw_cmd_begin()
+        st.encode(c, rows, first=0, count=l)
+        gpu.run(c, f"layers before {l}")
+        x = st.x.read(np.float32, (rows, H))
+        h_in = st.h.read(np.uint16, (rows, H))
+        c = gpu.qw_cmd_begin()
+        st.encode(c, rows, first=l, count=1, start=False)
+        gpu.run(c, f"layer {l}")
+        L = layers[l].host()
+        widx, ww = oracle_par.route_rows(L, x)
+        idx = st.idx.read(np.int32, (rows, K))
+        assert np.array_equal(idx, widx), f"layer {l}: {(idx != widx).sum()} routing ids differ"
+        assert np.array_equal(st.w.read(np.float32, (rows, K)).view(np.uint32), ww.view(np.uint32)), \
+            f"layer {l}: routing weights not bit-exact"
+        y = st.y.read(np.float32, (rows, H))
+        wy, _, _ = oracle_par.moe_rows(L, x[sel])
+        e = rel_l2(y[sel], wy)
+        m = float(np.abs(y[sel] - wy).max())
+        ymax = float(np.abs(wy).max())
+        print(f"layer {l}: y rel-L2 {e:.3g} max-abs {m:.3g} (max |y| {ymax:.4g}) on {sel.size} rows")
+        # The max-abs bar is for outputs of order one.  Deep in the stack the
+        # synthetic weights' non-zero mean (bias -8 * scale: mean -scale / 2)
+        # has grown h along one direction and |y| reaches the thousands, so
+        # there the bar scales with the output's largest magnitude.
+        assert e < 1e-3 and m < 2e-2 * max(1.0, ymax), f"layer {l}: rel-L2 {e:.3g} max-abs {m:.3g}"
+        wh, wx = ref.residual_norm(h_in, y)
+        assert np.array_equal(st.h.read(np.uint16, (rows, H)), wh), f"layer {l}: bf16 carry differs"
+        check_norm(st.x.read(np.float32, (rows, H)), wh, wx)
+        del L
+    st.free()
+    for L in layers:
+        L.free()

@@ -49,6 +49,7 @@ def test_null_command_encodes_nothing():
     assert not gpu.qw_op_qmv_q4_bank2(None, r, r, r, r, r, r, r, r, r, 1024, 8, 1, 1, 64)
     assert gpu.qw_op_qmv_q4_bank2(None, r, r, r, r, r, r, r, r, r, 2048, 8, 1, 1, 64)
     assert not gpu.qw_op_qmv_q4_multi(None, r, 2048, 64, 5, None)
+    assert not gpu.qw_op_qmv_q4_multi(None, r, 1024, 64, 2, None)   # too short to take (reference :105-107)
     assert gpu.qw_op_qmv_q4_multi(None, r, 2048, 64, 2, None)
 
 
@@ -69,3 +70,46 @@ def test_init_reports_a_missing_gpu():
     if gpu.qw_gpu_init(err, 256):
         pytest.skip("a gfx950 GPU is present")
     assert err.value
+
+
+def test_hc_pre_decode_refuses_overlaps():
+    """No output of qw_op_hc_pre_decode may share a byte with an input or with
+    another output (its workgroups read every input while others write);
+    checked on the shape alone, with no command and no device."""
+    from qwasar_amd import gpu
+    H, S, lr = 256, 4, 32
+    HH = S * H
+    A, B = 0x1000, 0x2000          # two stand-in buffer handles, never dereferenced
+    r = lambda buf, off=0: gpu.qw_ref(buf, off)
+    N = gpu.NULL_REF
+
+    def call(h4_out, n4, d, inj_out, h4, out, inj):
+        return gpu.qw_op_hc_pre_decode(None, h4_out, n4, d, inj_out, h4, out, inj, N, N, N, N, N,
+                                       H, S, lr, 64, 1e-6)
+
+    # outputs laid end to end in A, inputs in B: accepted
+    o = [0, 4 * HH, 8 * HH, 8 * HH + 4 * lr]
+    i = [0, 4 * HH, 4 * HH + 4 * H]
+    ok = dict(h4_out=r(A, o[0]), n4=r(A, o[1]), d=r(A, o[2]), inj_out=r(A, o[3]),
+              h4=r(B, i[0]), out=r(B, i[1]), inj=r(B, i[2]))
+    assert call(**ok)
+    for name, bad in (("n4", r(B, 4 * HH - 4)),          # n4's first float is h4's last
+                      ("d", r(B, 4 * HH + 4 * H - 8)),   # d over out's tail
+                      ("inj_out", r(B, i[2])),           # inj_out is inj
+                      ("h4_out", r(B, 16)),              # h4_out inside h4
+                      ("n4", r(A, o[0] + 4 * HH - 4))):  # two outputs sharing a float
+        args = dict(ok)
+        args[name] = bad
+        assert not call(**args), name
+
+
+def test_c_caller_compiles_as_c99():
+    """include/qwasar_gpu.h and the C caller of the boundary are plain C99
+    (gcc -std=c99 -pedantic -Werror), as the reference's C drivers need."""
+    import subprocess
+    here = os.path.dirname(os.path.abspath(__file__))
+    src = os.path.join(here, "c_boundary", "encode_moe.c")
+    inc = os.path.join(os.path.dirname(here), "include")
+    r = subprocess.run(["gcc", "-std=c99", "-pedantic", "-Wall", "-Wextra", "-Werror", "-fsyntax-only",
+                        "-I", inc, src], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

@@ -100,6 +100,14 @@ def test_errors(tmp_path):
     ck, err = open_ck(str(d))
     assert not ck and "overruns" in err
 
+    # dims whose product wraps 64 bits to the data's length (2^62 * 4 bytes = 2^64 == 0
+    # mod 2^64, against an empty range), and a negative dim
+    for shape in ([1 << 62], [-4], [1 << 40, 1 << 40]):
+        d = copy_ckpt(tmp_path, "q4")
+        write_st(d / "extra.safetensors", {"t": {"dtype": "F32", "shape": shape, "data_offsets": [0, 0]}}, b"")
+        ck, err = open_ck(str(d))
+        assert not ck and "negative or oversized shape" in err, (shape, err)
+
     d = copy_ckpt(tmp_path, "q4")
     for f in d.glob("*.safetensors"):
         f.unlink()
@@ -118,5 +126,59 @@ def test_layer_errors_before_upload():
         assert "outside 0..7" in e.value.decode()
         assert not gpu.qw_moe_layer_load(ck, 5, C.byref(m), e, 512)    # not in the trimmed copy
         assert "layers.5.mlp.gate" in e.value.decode()
+    finally:
+        gpu.qw_checkpoint_close(ck)
+
+
+def _rewrite_header(path, edit):
+    raw = path.read_bytes()
+    n = struct.unpack("<Q", raw[:8])[0]
+    hdr = json.loads(raw[8:8 + n])
+    edit(hdr)
+    write_st(path, hdr, raw[8 + n:])
+
+
+def _file_holding(d, name):
+    for f in sorted(d.glob("*.safetensors")):
+        raw = f.read_bytes()
+        n = struct.unpack("<Q", raw[:8])[0]
+        if name in json.loads(raw[8:8 + n]):
+            return f
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("tag", ["q4", "mlx"])
+def test_layer_shape_errors_before_upload(tmp_path, tag):
+    """A router stored with the right bytes but the wrong dims, and one that
+    is missing, are refused with the tensor's name before any device call."""
+    name = "language_model.model.layers.0.mlp.gate.weight"
+    d = copy_ckpt(tmp_path, tag)
+    f = _file_holding(d, name)
+
+    def reshape(h):
+        r, c = h[name]["shape"]
+        h[name]["shape"] = [r * 2, c // 2]
+    _rewrite_header(f, reshape)
+    ck, err = open_ck(str(d))
+    assert ck, err
+    try:
+        m = gpu.qw_moe_layer()
+        e = C.create_string_buffer(512)
+        assert not gpu.qw_moe_layer_load(ck, 0, C.byref(m), e, 512)
+        msg = e.value.decode()
+        assert name in msg and "this layer needs" in msg, msg
+    finally:
+        gpu.qw_checkpoint_close(ck)
+
+    d = copy_ckpt(tmp_path, tag)
+    f = _file_holding(d, name)
+    _rewrite_header(f, lambda h: h.__setitem__("renamed", h.pop(name)))
+    ck, err = open_ck(str(d))
+    assert ck, err
+    try:
+        m = gpu.qw_moe_layer()
+        e = C.create_string_buffer(512)
+        assert not gpu.qw_moe_layer_load(ck, 0, C.byref(m), e, 512)
+        assert f"checkpoint has no tensor {name}" in e.value.decode()
     finally:
         gpu.qw_checkpoint_close(ck)

@@ -93,3 +93,58 @@ def test_synth_distributions():
     nib = ((w[:, None] >> (np.arange(8, dtype=np.uint32) * 4)) & 0xF).ravel()
     counts = np.bincount(nib, minlength=16)
     assert counts.min() > 0.9 * counts.mean()
+
+
+def _bits(v):
+    return synth.to_bf16(np.array([v], np.float32))[0]
+
+
+def test_residual_carry_rounds_to_nearest_even():
+    """The bf16 carry h' = bf16(h + y) rounds to nearest, ties to even, on the
+    fp32 sum.  At h = 1 the bf16 spacing is 2^-7: y = 2^-8 is a tie (even
+    keeps 1), y = 3*2^-8 a tie whose even neighbour is above (1 + 2^-6),
+    y = 3*2^-9 above the midpoint (up; truncation would go down), y = 2^-9
+    below it (down); and the same mirrored.  Truncation, round-half-up or
+    round-half-away each fail one of these."""
+    u = 2.0 ** -7
+    cases = [  # (h, y, expected h')
+        (1.0, 2.0 ** -8, 1.0),
+        (1.0, 3 * 2.0 ** -8, 1.0 + 2 * u),
+        (1.0, 3 * 2.0 ** -9, 1.0 + u),
+        (1.0, 2.0 ** -9, 1.0),
+        (1.0 + u, 2.0 ** -8, 1.0 + 2 * u),         # a tie from an odd mantissa: up to even
+        (-1.0, -(2.0 ** -8), -1.0),
+        (-1.0, -3 * 2.0 ** -8, -1.0 - 2 * u),
+        (-1.0, -3 * 2.0 ** -9, -1.0 - u),
+        (-1.0 - u, -(2.0 ** -8), -1.0 - 2 * u),
+        (1.0, -(2.0 ** -9), 1.0),                  # below 1 the spacing halves: 1 - 2^-9 is a tie
+        (1.0, -3 * 2.0 ** -10, 1.0 - 2.0 ** -8),   # between 1 - 2^-8 and 1, nearer the former
+    ]
+    h = np.array([_bits(c[0]) for c in cases], np.uint16).reshape(1, -1)
+    y = np.array([c[1] for c in cases], np.float32).reshape(1, -1)
+    got, _ = ref.residual_norm(h, y)
+    want = np.array([_bits(c[2]) for c in cases], np.uint16)
+    assert np.array_equal(got.ravel(), want), f"{got.ravel()} vs {want}"
+
+
+def test_residual_carry_is_the_nearest_bf16():
+    """On random sums: h' is one of the two bf16 values around the fp32 sum
+    h + y, the nearer (distances in fp64), the even one at a tie."""
+    g = np.random.default_rng(31)
+    h = synth.to_bf16(g.standard_normal(200000).astype(np.float32)).reshape(1, -1)
+    y = (g.standard_normal(200000) * 0.05).astype(np.float32).reshape(1, -1)
+    # some exact ties: y = half a bf16 spacing of h
+    hf = synth.bf16_to_f32(h)
+    e = np.floor(np.log2(np.abs(hf[0, :1000]) + 1e-30))
+    y[0, :1000] = (2.0 ** (e - 8)).astype(np.float32)
+    got, _ = ref.residual_norm(h, y)
+    s = (synth.bf16_to_f32(h) + y).astype(np.float32).ravel().astype(np.float64)
+    lo = (np.asarray(s, np.float32).view(np.uint32) & 0xFFFF0000).view(np.float32).astype(np.float64)
+    lo_bits = (np.asarray(s, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    hi_bits = (lo_bits.astype(np.uint32) + 1).astype(np.uint16)
+    hi = synth.bf16_to_f32(hi_bits).astype(np.float64)
+    d_lo, d_hi = np.abs(s - lo), np.abs(hi - s)
+    want = np.where(d_lo < d_hi, lo_bits, np.where(d_hi < d_lo, hi_bits,
+                                                   np.where(lo_bits % 2 == 0, lo_bits, hi_bits)))
+    assert np.array_equal(got.ravel(), want)
+    assert (d_lo == d_hi).sum() >= 900   # the ties were exercised
