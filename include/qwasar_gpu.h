@@ -273,6 +273,25 @@ bool qw_op_moe_layer(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,
 bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref h, qw_ref y_prev,
                               qw_ref h_out, qw_ref x_out, const qw_moe_layer *M, int32_t rows, float eps);
 
+/* qw_op_moe_layer's decode path (rows <= 8) with no allocation.  No
+ * counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The launch's staging and hand-off state live in a
+ * static device array of 320 KiB per GPU (held until the process ends), whose
+ * address the library resolves at qw_gpu_init; this call makes no
+ * allocation of any kind and gives qw_op_moe_layer's bits.  False, nothing
+ * encoded, where qw_op_moe_layer would not take the decode path, or where
+ * the layer's staging at `rows` exceeds what the array holds past its
+ * 82 KB hand-off state (245,504 bytes: config 1's shape at 8 rows stages
+ * 208,896; H 4096 with K 15 at 8 rows, 294,912, is refused).
+ * Every call on one GPU shares the array and finds it as the last call
+ * left it (the hand-off state stays valid between calls; the staging needs
+ * no clearing).  Calls whose launches overlap on one GPU -- the library's
+ * single stream serialises its own -- would race on it.  Hand-off failures are reported as qw_op_moe_layer's
+ * are, by qw_cmd_error after qw_cmd_wait. */
+bool qw_op_moe_layer_noalloc(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,
+                             const qw_moe_layer *M, int32_t rows);
+
 /* ---- checkpoint loading (reference qwasar.c:700-775 config, :1426-1461
  * qw_bind_small, :1469-1495 qw_bind_qbank, :1532-1563 qw_bind_moe) ---------
  *

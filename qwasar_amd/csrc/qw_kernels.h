@@ -121,6 +121,19 @@ int qwk_moe_decode_sync_error(const void *sync, uint32_t *err);
 /* Sets the error word as a failed wait of launch `epoch` would (synchronous);
  * every wait of a later launch then gives up at once. */
 int qwk_moe_decode_sync_raise(void *sync, uint32_t epoch);
+/* The allocation-free decode entry's device scratch (qw_static.hip): a
+ * file-scope device array of this many bytes per GPU, holding the hand-off
+ * state and then the staging area. */
+#define QWK_STATIC_SCRATCH_BYTES (320u * 1024u)
+/* Resolves the array's address on the current device (hipGetSymbolAddress)
+ * and zeroes it; once per device, at init.  Synchronous. */
+int qwk_static_init(hipStream_t s);
+/* The array's address on the current device (NULL before qwk_static_init),
+ * and its size in *bytes. */
+void *qwk_static_scratch(size_t *bytes);
+/* Zeroes `bytes` (a multiple of 16, 16-byte aligned) at p with a fill kernel
+ * on s (no memset node, so it may sit in a captured graph). */
+int qwk_zero_fill(hipStream_t s, void *p, size_t bytes);
 /* Non-zero when the decode path takes this layer shape and token count. */
 int qwk_moe_decode_supported(const qwk_moe *M, int rows);
 /* The residual step before a layer of a stack: the layer's input is

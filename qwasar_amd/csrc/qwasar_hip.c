@@ -60,7 +60,7 @@ struct qw_cmd_s {
     hipEvent_t *evs;         /* every event this command created */
     int nevs, capevs;
     hipEvent_t last;         /* where the next mark starts */
-    uint32_t ep_hi;          /* the last decode epoch this command launched, 0: none unchecked */
+    uint32_t ep_hi[2];       /* per hand-off state: the last decode epoch this command launched (0: none unchecked) */
     struct qw_cmd_s *next;   /* live commands, for qw_buf_free */
 };
 
@@ -74,9 +74,16 @@ static struct {
     qw_cmd live;
     void *scratch;
     size_t scratch_len;
-    void *dsync;          /* the decode launch's hand-off state (zeroed) */
-    uint32_t depoch;      /* epoch of the last decode launch */
+    /* The decode launch's hand-off states: [QW_DS_HEAP] allocated at first
+     * use, [QW_DS_STATIC] at the head of the static device array that the
+     * allocation-free entry uses (its staging follows it there). */
+    struct { void *sync; uint32_t epoch; } ds[2];
+    char *static_stage;   /* the static array past its hand-off state */
+    size_t static_stage_len;
 } G;
+
+#define QW_DS_HEAP 0
+#define QW_DS_STATIC 1
 
 /* ---- profiling table ---------------------------------------------------- */
 
@@ -134,6 +141,20 @@ bool qw_gpu_init(char *err, size_t errcap) {
         if (err && errcap) snprintf(err, errcap, "cannot create a HIP stream");
         return false;
     }
+    /* The static device array of the allocation-free decode entry: its
+     * address on this device, once, and zeroed.  Without it that entry
+     * refuses; everything else works. */
+    {
+        size_t sb = 0;
+        char *sp = qwk_static_init(G.stream) == 0 ? qwk_static_scratch(&sb) : NULL;
+        const size_t hs = (qwk_moe_decode_sync_bytes() + 255) & ~(size_t)255;
+        if (sp && sb > hs) {
+            G.ds[QW_DS_STATIC].sync = sp;
+            G.ds[QW_DS_STATIC].epoch = 0;
+            G.static_stage = sp + hs;
+            G.static_stage_len = sb - hs;
+        }
+    }
     size_t fr = 0, tot = 0;
     (void)hipMemGetInfo(&fr, &tot);
     G.free0 = fr;
@@ -159,8 +180,9 @@ void qw_gpu_shutdown(void) {
     if (G.scratch) hipFree(G.scratch);
     G.scratch = NULL;
     G.scratch_len = 0;
-    if (G.dsync) hipFree(G.dsync);
-    G.dsync = NULL;
+    if (G.ds[QW_DS_HEAP].sync) hipFree(G.ds[QW_DS_HEAP].sync);
+    G.ds[QW_DS_HEAP].sync = NULL;
+    G.ds[QW_DS_STATIC].sync = NULL;   /* the static array stays with the process */
     hipStreamDestroy(G.stream);
     G.ready = 0;
 }
@@ -311,41 +333,65 @@ static void touch(qw_cmd c, qw_ref r, int writes) {
 
 static void *dp(qw_ref r) { return r.buf ? (char *)r.buf->dev + r.off : NULL; }
 
-
-/* The decode launch's hand-off state: allocated and zeroed on first use,
- * zeroed again (epochs restarting at 1) after a launch reported an error and
- * before an epoch would repeat. */
-static int dsync_reset(void) {
-    hipStreamSynchronize(G.stream);
-    if (!G.dsync && hipMalloc(&G.dsync, qwk_moe_decode_sync_bytes()) != hipSuccess) {
-        G.dsync = NULL;
-        return 0;
+/* touch() without the command's written list (which can grow): the buffer's
+ * mirror is marked stale, so qw_buf_contents copies it back when the host
+ * next asks for it.  For the allocation-free entry. */
+static void touch_fixed(qw_ref r, int writes) {
+    qw_buf b = r.buf;
+    if (!b) return;
+    if (b->dev_stale) {
+        hipMemcpyAsync(b->dev, b->host, b->len, hipMemcpyHostToDevice, G.stream);
+        hipStreamSynchronize(G.stream);
+        b->dev_stale = 0;
     }
-    if (hipMemset(G.dsync, 0, qwk_moe_decode_sync_bytes()) != hipSuccess) return 0;
-    G.depoch = 0;
+    if (writes) b->host_stale = 1;
+}
+
+
+/* A decode hand-off state: the heap one is allocated on first use; both are
+ * zeroed (epochs restarting at 1) at first use, after a launch reported an
+ * error and before an epoch would repeat.  Zeroed by a fill kernel. */
+/* The hand-off state's size, rounded up to the fill kernel's 16 bytes (and
+ * allocated at that size). */
+static size_t dsync_bytes(void) { return (qwk_moe_decode_sync_bytes() + 15) & ~(size_t)15; }
+
+static int dsync_reset(int k) {
+    hipStreamSynchronize(G.stream);
+    if (!G.ds[k].sync) {
+        if (k == QW_DS_STATIC) return 0;   /* set up at init or not at all */
+        if (hipMalloc(&G.ds[k].sync, dsync_bytes()) != hipSuccess) {
+            G.ds[k].sync = NULL;
+            return 0;
+        }
+    }
+    if (qwk_zero_fill(G.stream, G.ds[k].sync, dsync_bytes()) != 0 ||
+        hipStreamSynchronize(G.stream) != hipSuccess)
+        return 0;
+    G.ds[k].epoch = 0;
     return 1;
 }
 
-/* With the stream drained: reads the hand-off error word, which holds the
+/* With the stream drained: reads state k's error word, which holds the
  * epoch of the first decode launch whose wait gave up.  That launch and
- * every later one failed, so every live command that launched an epoch at or
- * after it is failed, whichever command is waiting.  Then the state is zeroed
- * and, every launch so far being checked, the commands' epoch marks are
- * cleared.  Returns 0 when the state could not be read or zeroed. */
-static int dsync_check(int force_reset) {
-    if (!G.dsync) return 1;
+ * every later one on the state failed, so every live command that launched
+ * an epoch at or after it is failed, whichever command is waiting.  Then the
+ * state is zeroed and, every launch so far being checked, the commands'
+ * epoch marks for it are cleared.  Returns 0 when the state could not be
+ * read or zeroed. */
+static int dsync_check(int k, int force_reset) {
+    if (!G.ds[k].sync) return 1;
     int pending = force_reset;
-    for (qw_cmd q = G.live; q; q = q->next) pending |= q->ep_hi != 0;
+    for (qw_cmd q = G.live; q; q = q->next) pending |= q->ep_hi[k] != 0;
     if (!pending) return 1;
     uint32_t first = 0;
-    if (qwk_moe_decode_sync_error(G.dsync, &first) != 0) first = 1;   /* unreadable: fail them all */
+    if (qwk_moe_decode_sync_error(G.ds[k].sync, &first) != 0) first = 1;   /* unreadable: fail them all */
     if (first != 0)
         for (qw_cmd q = G.live; q; q = q->next)
-            if (q->ep_hi >= first)
+            if (q->ep_hi[k] >= first)
                 cmd_fail(q, hipErrorLaunchFailure,
                          "moe_layer (decode): a hand-off wait gave up (launch %u of this state)", first);
-    for (qw_cmd q = G.live; q; q = q->next) q->ep_hi = 0;
-    return first != 0 || force_reset ? dsync_reset() : 1;
+    for (qw_cmd q = G.live; q; q = q->next) q->ep_hi[k] = 0;
+    return first != 0 || force_reset ? dsync_reset(k) : 1;
 }
 
 /* For tests of the failure path: the hand-off error word is set as if the
@@ -354,9 +400,9 @@ static int dsync_check(int force_reset) {
  * the waiting command reports the failure. */
 bool qw_debug_decode_handoff_fail(void) {
     if (!ensure_init()) return false;
-    if (!G.dsync && !dsync_reset()) return false;
+    if (!G.ds[QW_DS_HEAP].sync && !dsync_reset(QW_DS_HEAP)) return false;
     hipStreamSynchronize(G.stream);
-    return qwk_moe_decode_sync_raise(G.dsync, G.depoch + 1u) == 0;
+    return qwk_moe_decode_sync_raise(G.ds[QW_DS_HEAP].sync, G.ds[QW_DS_HEAP].epoch + 1u) == 0;
 }
 
 /* Launch result of one op: a refusal (invalid shape) is printed, as the
@@ -382,7 +428,8 @@ void qw_cmd_wait(qw_cmd c) {
     if (!c) return;
     hipError_t e = hipStreamSynchronize(G.stream);
     if (e != hipSuccess) cmd_fail(c, e, "device: %s", hipGetErrorString(e));
-    dsync_check(0);
+    dsync_check(QW_DS_HEAP, 0);
+    dsync_check(QW_DS_STATIC, 0);
     for (int i = 0; i < c->nwritten; i++) {
         qw_buf b = c->written[i];
         if (b->exposed && b->host_stale) {
@@ -840,31 +887,35 @@ static void moe_desc(qwk_moe *mp, const qw_moe_layer *M) {
     *mp = m;
 }
 
-/* Decode: one launch over only the selected experts. */
+/* Decode: one launch over only the selected experts.  Its staging and
+ * hand-off state are the backend's heap scratch (k = QW_DS_HEAP) or the
+ * static device array (k = QW_DS_STATIC: nothing allocated; the caller has
+ * checked that the staging fits). */
 static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float *x,
-                       const qwk_resid *res, const qwk_moe *mp, int32_t rows) {
+                       const qwk_resid *res, const qwk_moe *mp, int32_t rows, int k) {
     const qwk_moe m = *mp;
     const size_t need = qwk_moe_decode_scratch(&m, rows);
-    void *S = scratch(need);
+    void *S = k == QW_DS_STATIC ? (void *)G.static_stage : scratch(need);
+    const size_t have = k == QW_DS_STATIC ? G.static_stage_len : need;
     if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", need); return false; }
-    if (!G.dsync && !dsync_reset()) {
+    if (!G.ds[k].sync && !dsync_reset(k)) {
         cmd_fail(c, hipErrorOutOfMemory, "moe_layer: decode hand-off state");
         return false;
     }
     /* Flags and tagged logits hold past epochs, so an epoch is not reused
      * until the state is zeroed again (0 is "never"). */
-    if (G.depoch == UINT32_MAX && !dsync_check(1)) {
+    if (G.ds[k].epoch == UINT32_MAX && !dsync_check(k, 1)) {
         cmd_fail(c, hipErrorUnknown, "moe_layer: decode hand-off state");
         return false;
     }
-    ++G.depoch;
+    const uint32_t epoch = ++G.ds[k].epoch;
     hipEvent_t ev[2] = { NULL, NULL };
-    const int per_kernel = G.prof && (ev[0] = cmd_event(c, 0)) && (ev[1] = cmd_event(c, 0));
-    const int rc = qwk_moe_decode(G.stream, out, idx, w, x, res, &m, rows, S, need, G.dsync, G.depoch,
+    const int per_kernel = k == QW_DS_HEAP && G.prof && (ev[0] = cmd_event(c, 0)) && (ev[1] = cmd_event(c, 0));
+    const int rc = qwk_moe_decode(G.stream, out, idx, w, x, res, &m, rows, S, have, G.ds[k].sync, epoch,
                                   per_kernel ? ev : NULL);
     if (per_kernel) cmd_add_mark(c, "moe decode", ev[0], ev[1]);
-    c->ep_hi = G.depoch;
-    launched(c, "moe_layer (decode)", rc);
+    c->ep_hi[k] = epoch;
+    launched(c, k == QW_DS_STATIC ? "moe_layer_noalloc" : "moe_layer (decode)", rc);
     return rc == 0;
 }
 
@@ -895,7 +946,34 @@ bool qw_op_moe_layer(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,
     moe_desc(&m, M);
     if (rows > QWK_DECODE_MAX_ROWS || !qwk_moe_decode_supported(&m, rows))
         return moe_prefill(c, dp(out), dp(idx), dp(w), dp(x), M, rows);
-    return moe_decode(c, dp(out), dp(idx), dp(w), dp(x), NULL, &m, rows);
+    return moe_decode(c, dp(out), dp(idx), dp(w), dp(x), NULL, &m, rows, QW_DS_HEAP);
+}
+
+bool qw_op_moe_layer_noalloc(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,
+                             const qw_moe_layer *M, int32_t rows) {
+    if (!moe_layer_ok(M, rows)) return false;
+    qwk_moe m;
+    moe_desc(&m, M);
+    if (rows > QWK_DECODE_MAX_ROWS || !qwk_moe_decode_supported(&m, rows)) return false;
+    if (!G.static_stage) {
+        fprintf(stderr, "qwasar: moe_layer_noalloc: the static device scratch is not set up (qw_gpu_init)\n");
+        return false;
+    }
+    const size_t need = qwk_moe_decode_scratch(&m, rows);
+    if (need > G.static_stage_len) {
+        fprintf(stderr, "qwasar: moe_layer_noalloc: %d rows of this layer stage %zu bytes, over the %zu the "
+                "static scratch holds\n", rows, need, G.static_stage_len);
+        return false;
+    }
+    if (!c) return true;
+    const qw_ref in[] = { x, M->router, M->sh_gate_w, M->gate_up.w, M->gate_up.scales, M->gate_up.biases,
+                          M->gate.w, M->gate.scales, M->gate.biases, M->up.w, M->up.scales, M->up.biases,
+                          M->down.w, M->down.scales, M->down.biases, M->sh_gate.w, M->sh_gate.scales,
+                          M->sh_gate.biases, M->sh_up.w, M->sh_up.scales, M->sh_up.biases, M->sh_down.w,
+                          M->sh_down.scales, M->sh_down.biases };
+    for (size_t i = 0; i < sizeof in / sizeof in[0]; i++) touch_fixed(in[i], 0);
+    touch_fixed(out, 1); touch_fixed(idx, 1); touch_fixed(w, 1);
+    return moe_decode(c, dp(out), dp(idx), dp(w), dp(x), NULL, &m, rows, QW_DS_STATIC);
 }
 
 bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref h, qw_ref y_prev,
@@ -916,5 +994,5 @@ bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref
         return moe_prefill(c, dp(out), dp(idx), dp(w), dp(x_out), M, rows);
     }
     const qwk_resid res = { dp(h), dp(y_prev), dp(h_out), dp(x_out), eps };
-    return moe_decode(c, dp(out), dp(idx), dp(w), NULL, &res, &m, rows);
+    return moe_decode(c, dp(out), dp(idx), dp(w), NULL, &res, &m, rows, QW_DS_HEAP);
 }

@@ -118,6 +118,7 @@ _sig("qw_checkpoint_tensor", _B, _P, C.c_char_p, C.POINTER(_P), C.POINTER(C.c_si
 _sig("qw_moe_layer_load", _B, _P, _I, C.POINTER(qw_moe_layer), C.c_char_p, C.c_size_t)
 _sig("qw_moe_layer_free", None, C.POINTER(qw_moe_layer))
 _sig("qw_op_moe_layer", _B, _P, _R, _R, _R, _R, C.POINTER(qw_moe_layer), _I)
+_sig("qw_op_moe_layer_noalloc", _B, _P, _R, _R, _R, _R, C.POINTER(qw_moe_layer), _I)
 _sig("qw_op_moe_layer_residual", _B, _P, _R, _R, _R, _R, _R, _R, _R, C.POINTER(qw_moe_layer), _I, C.c_float)
 _sig("qw_op_rms_norm", None, _P, _R, _R, _R, _I, _I, C.c_float, C.c_float)
 _sig("qw_op_hc_inject_norm", None, _P, _R, _R, _R, _R, _R, _I, _I, _I, C.c_float)
