@@ -14,14 +14,15 @@ that any 12 consecutive tokens select pairwise disjoint experts: every step
 reads its routed experts from HBM, not from the 256 MB Infinity Cache.
 
 Also reported: the decode launch's own duration, HBM bandwidth on the routed
-("selected-expert") bytes and on all bytes, config 3 (512-token prefill with
+("selected-expert") bytes and on all bytes; config 2 (eight tokens a step
+sharing three forced experts, judged on the batch's unique-expert bytes);
+config 3 (512-token prefill with
 Zipf-skewed routing) and a 2048-token prefill chunk (config 4's per-layer
 step) in tokens/s and bf16-MFMA utilisation; config 4, 48 such layers
 (~65 GB of weights written on the device) joined by the residual bf16 RMS
 norm, through one 2048-token prefill and 256 decode steps; and the CPU
-oracle's time on a bounded sample of the same decode workload
-(single-threaded scalar C, the reference's own CPU path restated; see
-oracle/).
+oracle's time on bounded samples of configs 0-3 (single-threaded scalar C,
+the reference's own CPU path restated; see oracle/).
 
     python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-config4] [--no-cpu]
 """
@@ -345,16 +346,96 @@ def bench_hc(gpu, steps, H=3072, S=4, k=320, G=64, pool=96, prefill_rows=2048, s
                         "tflops": round(flops / (pf_ms * 1e-3) / 1e12, 2)}}
 
 
-def cpu_baseline(L, xpool, seconds):
-    """The oracle (the reference's scalar moe_step restated in C, one thread)
-    on the same decode tokens, for a bounded time."""
+def bench_config2(gpu, lb, L, cfg, seed, steps, warmup, nbatch=32):
+    """eight tokens a step whose router logits carry +8 on
+    three experts (every token picks them), so one launch reads the union U of
+    the batch's experts.  Batches are chosen by the GPU's own routing so that
+    consecutive batches share no expert outside the three forced ones: each
+    step reads its other experts from HBM."""
+    from qwasar_amd import synth
+    bias = np.zeros(L.E, np.float32)
+    bias[list(synth.C2_HOT)] = synth.C2_BIAS
+    r2 = synth.make_router(seed, L.E, L.H, bias)
+    rb2 = gpu.Buf(wrap=r2)
+    d2 = gpu.qw_moe_layer.from_buffer_copy(lb.desc)
+    d2.router = rb2.ref()
+    n = 2048
+    cand = synth.make_x(seed + 2, n, L.H, name="bench.c2cand", const_col0=True)
+    B = gpu.Buf
+    xb, lg, ib, wb = B.of(cand), B(n * L.E * 4), B(n * L.K * 4), B(n * L.K * 4)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_op_dmat_bf16(c, lg.ref(), xb.ref(), rb2.ref(), L.H, L.E, n)
+    gpu.qw_op_moe_route(c, ib.ref(), wb.ref(), lg.ref(), n, L.E, L.K, True)
+    gpu.run(c, "route config-2 candidates")
+    ids = ib.read(np.int32, (n, L.K))
+    for t in (xb, lg, ib, wb):
+        t.free()
+    hot = set(synth.C2_HOT)
+    left, batches, prev = list(range(n)), [], set()
+    while len(batches) < nbatch:
+        cur, members = set(), []
+        for i in list(left):
+            e = set(ids[i].tolist()) - hot
+            if not e & prev:
+                members.append(i)
+                cur |= e
+                left.remove(i)
+                if len(members) == 8:
+                    break
+        if len(members) < 8:
+            raise RuntimeError("could not build config-2 batches; raise the candidate count")
+        batches.append(members)
+        prev = cur
+    uniq = [len(set(ids[b].ravel().tolist())) for b in batches]
+    xs = np.ascontiguousarray(cand[np.concatenate(batches)])
+    xp = B.of(xs)
+    ob, ib, wb = B(8 * L.H * 4), B(8 * L.K * 4), B(8 * L.K * 4)
+    stride = 8 * L.H * 4
+
+    def step(c, s):
+        gpu.qw_op_moe_layer(c, ob.ref(), ib.ref(), wb.ref(), xp.ref((s % nbatch) * stride), d2, 8)
+
+    c = gpu.qw_cmd_begin()
+    for s in range(warmup):
+        step(c, s)
+    gpu.run(c, "config 2 warm-up")
+    gpu.qw_prof_reset()
+    gpu.qw_prof_set_enabled(True)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_prof_set_enabled(False)
+    for s in range(steps):
+        step(c, warmup + s)
+    gpu.qw_prof_set_enabled(True)
+    gpu.qw_cmd_mark(c, b"config2 region")
+    gpu.run(c, "config 2")
+    ms = gpu.qw_prof_ms(b"config2 region", None)
+    gpu.qw_prof_set_enabled(False)
+    gpu.qw_prof_reset()
+    for t in (xp, ob, ib, wb, rb2):
+        t.free()
+    us = ms * 1000.0 / steps
+    u_mean = float(np.mean([uniq[(warmup + s) % nbatch] for s in range(steps)]))
+    ub = u_mean * L.expert_bytes()
+    nb = decode_bytes(cfg)
+    other = nb["all"] - nb["routed"]
+    return {"rows": 8, "forced_shared_experts": list(synth.C2_HOT), "batches": nbatch,
+            "us_per_step": round(us, 3), "us_per_token": round(us / 8, 3),
+            "unique_experts_mean": round(u_mean, 2), "unique_expert_bytes": int(ub),
+            "unique_hbm_gbs": round(ub / (us * 1e-6) / 1e9, 1),
+            "unique_hbm_frac": round(ub / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "all_hbm_frac": round((ub + other) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "ideal_us_at_peak": round(ub / HBM_PEAK_GBS / 1e3, 2)}, r2, xs
+
+
+def cpu_sample(L, x, seconds, rows_per_call):
+    """Seconds per call of the oracle's moe_forward on `rows_per_call` rows of
+    x at a time, over a bounded time; returns (seconds per call, calls)."""
     from oracle import ref
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds and n < xpool.shape[0]:
-        ref.moe_forward(L, xpool[n:n + 1])
+    while (n == 0 or time.perf_counter() - t0 < seconds) and (n + 1) * rows_per_call <= x.shape[0]:
+        ref.moe_forward(L, x[n * rows_per_call:(n + 1) * rows_per_call])
         n += 1
-    dt = time.perf_counter() - t0
-    return dt / n * 1e6, n
+    return (time.perf_counter() - t0) / n, n
 
 
 def calib_copy(nbytes):
@@ -376,11 +457,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-config2", action="store_true", help="skip config 2 (batch-8 decode)")
     ap.add_argument("--no-config4", action="store_true", help="skip the 48-layer stack (config 4)")
     ap.add_argument("--config4-only", action="store_true", help="run only the 48-layer stack and print it")
     ap.add_argument("--no-hc", action="store_true", help="skip the hyper-connection mixer")
     ap.add_argument("--hc-only", action="store_true", help="run only the hyper-connection mixer and print it")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy", type=int, default=0, help="bytes: run only the copy calibration")
     ap.add_argument("--decode-only-steps", type=int, default=0,
                     help="profiling aid: only run this many decode steps after setup")
@@ -439,7 +521,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u4xf32",
+        "dtype": "u4 x f16 (pow2-scaled 16-element units) -> fp32 acc",
         "data": "synthetic (seeded MLX-affine 4-bit weights, N(0,1) bf16 tokens)",
         "config": {"workload": "BASELINE config 1: Flash-Next-shaped MoE layer decode, batch 1",
                    "H": cfg["H"], "E": cfg["E"], "K": cfg["K"], "I": cfg["I"], "SI": cfg["SI"],
@@ -459,6 +541,11 @@ def main():
                      "algorithmic_bytes": nb["all"]},
     }
 
+    c2, c2_router, c2_x = None, None, None
+    if not args.no_config2:
+        c2, c2_router, c2_x = bench_config2(gpu, lb, L, cfg, seed, args.steps, args.warmup)
+        out["config2"] = c2
+    x3, r3 = None, None
     if not args.no_prefill:
         pf = {}
         zb = synth.zipf_bias(seed, L.E)
@@ -474,6 +561,8 @@ def main():
         for name, rows, lbx, const0 in (("config3_zipf_512", 512, lb3, True),
                                         ("chunk_2048_uniform", 2048, lb, False)):
             x = synth.make_x(seed + rows, rows, L.H, name=f"bench.prefill{rows}", const_col0=const0)
+            if rows == 512:
+                x3 = x
             ms, hot, touched = time_prefill(gpu, lbx, x, reps=5)
             fl = prefill_flops(cfg, rows)
             pf[name] = {"rows": rows, "ms": round(ms, 3), "tokens_per_s": round(rows / (ms * 1e-3), 1),
@@ -481,6 +570,18 @@ def main():
                         "mfma_util": round(fl / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
                         "weight_read_floor_ms": round(L.weight_bytes() / HBM_PEAK_GBS / 1e6, 3),
                         "hottest_expert_pairs": hot, "experts_touched": touched}
+        rb3.free()
+        # flat numbers first (the 2048-token chunk, config 4's per-layer step), then config 3
+        ch, z = pf["chunk_2048_uniform"], pf["config3_zipf_512"]
+        flat = {"workload": "2048-token prefill chunk of one config-1-shaped layer (config 4's per-layer step)",
+                "rows": ch["rows"], "ms": ch["ms"], "tokens_per_s": ch["tokens_per_s"],
+                "useful_tflops": ch["useful_tflops"], "mfma_util": ch["mfma_util"],
+                "weight_read_floor_ms": ch["weight_read_floor_ms"],
+                "hbm_frac_of_weight_floor": round(ch["weight_read_floor_ms"] / ch["ms"], 4),
+                "config3_rows": z["rows"], "config3_ms": z["ms"], "config3_tokens_per_s": z["tokens_per_s"],
+                "config3_mfma_util": z["mfma_util"], "config3_hottest_expert_pairs": z["hottest_expert_pairs"],
+                "config3_experts_touched": z["experts_touched"]}
+        pf = flat
         out["prefill"] = pf
 
     if not args.no_config4:
@@ -489,10 +590,28 @@ def main():
         out["hc_mixer"] = bench_hc(gpu, 200)
 
     if not args.no_cpu:
-        us, n = cpu_baseline(L, xpool, args.cpu_seconds)
-        out["cpu_baseline"] = {"value": round(us, 1), "unit": "us/token", "cores": 1, "kind": "port",
-                               "sample": f"{n} decode tokens of config 1 through oracle/moe_ref.c "
-                                         "(scalar C, -O2, one thread), same weights and tokens"}
+        # the oracle (scalar C, one thread) on bounded samples of the same
+        # workloads: config 1 (the headline's tokens), config 0, config 2 (the
+        # first timed batches) and config 3 (its first tokens)
+        import dataclasses
+        s1, n1 = cpu_sample(L, xpool, args.cpu_seconds, 1)
+        by = {}
+        L0, x0 = synth.make_config(0, rows=64)
+        s0, n0 = cpu_sample(L0, x0, 1.0, 1)
+        by["config0"] = {"us_per_token": round(s0 * 1e6, 1), "sample": f"{n0} tokens"}
+        if c2 is not None:
+            L2 = dataclasses.replace(L, router=c2_router)
+            s2, n2 = cpu_sample(L2, c2_x, 3.0, 8)
+            by["config2"] = {"us_per_step": round(s2 * 1e6, 1), "us_per_token": round(s2 * 1e6 / 8, 1),
+                             "sample": f"{n2} batches of 8 tokens"}
+        if x3 is not None:
+            L3 = dataclasses.replace(L, router=r3)
+            s3, n3 = cpu_sample(L3, x3, 3.0, 8)
+            by["config3"] = {"tokens_per_s": round(8 / s3, 2), "sample": f"the first {8 * n3} of its 512 tokens"}
+        out["cpu_baseline"] = {"value": round(s1 * 1e6, 1), "unit": "us/token", "cores": 1, "kind": "port",
+                               "sample": f"{n1} decode tokens of config 1 through oracle/moe_ref.c "
+                                         "(scalar C, -O2, one thread), same weights and tokens",
+                               "by_config": by}
     print(json.dumps(out), flush=True)
 
 
