@@ -18,6 +18,12 @@
    tensors of layers 0 and 1 rewritten byte for byte into safetensors files
    (two shards for the fused checkpoint, one with the mlx metadata for the
    split one).  `python tests/golden/make_fixtures.py ckpt` writes only these.
+4. tiny_q4_sparse.npz -- the weights the QSA and gated-DeltaNet tests take
+   from the same toy checkpoint, as data: layer 0's A_log, dt_bias, conv1d
+   taps and output-norm gain (a linear-attention layer) and layer 3's
+   indexer k_layernorm / q_layernorm gains (a QSA layer), with the config's
+   shape fields (heads, head dims, ratio, budget, rope theta and sections).
+   `python tests/golden/make_fixtures.py sparse` writes only this.
 """
 from __future__ import annotations
 
@@ -179,6 +185,34 @@ def trimmed_ckpts():
                                   by_layer[layer], meta)
 
 
+def tiny_sparse():
+    d = os.path.join(REF, "flashnext-tiny-q4")
+    t = load_dir(d)
+    with open(os.path.join(d, "config.json")) as f:
+        cfg = json.load(f)
+    c = cfg.get("text_config", cfg)
+    rp = c["rope_parameters"]
+    la, sa = "language_model.model.layers.0.linear_attn.", "language_model.model.layers.3.self_attn.indexer."
+    out = {
+        "A_log": t[la + "A_log"], "dt_bias": t[la + "dt_bias"],
+        "conv1d": t[la + "conv1d.weight"].reshape(t[la + "conv1d.weight"].shape[0], -1),
+        "gdn_norm": t[la + "norm.weight"],
+        "k_norm": t[sa + "k_layernorm.weight"], "q_norm": t[sa + "q_layernorm.weight"],
+        "hk": np.int32(c["linear_num_key_heads"]), "hv": np.int32(c["linear_num_value_heads"]),
+        "dk": np.int32(c["linear_key_head_dim"]), "dv": np.int32(c["linear_value_head_dim"]),
+        "conv_k": np.int32(c["linear_conv_kernel_dim"]),
+        "nq": np.int32(c["indexer_n_heads"]), "d": np.int32(c["indexer_head_dim"]),
+        "ratio": np.int32(c["indexer_compress_ratio"]), "budget": np.int32(c["indexer_budget"]),
+        "q_heads": np.int32(c["num_attention_heads"]), "kv_heads": np.int32(c["num_key_value_heads"]),
+        "head_dim": np.int32(c["head_dim"]),
+        "rotary_dim": np.int32(int(c["head_dim"] * rp["partial_rotary_factor"])),
+        "rope_theta": np.float32(rp["rope_theta"]),
+        "mrope_section": np.asarray(rp["mrope_section"], np.int32),
+        "eps": np.float32(c["rms_norm_eps"]),
+    }
+    np.savez_compressed(os.path.join(HERE, "tiny_q4_sparse.npz"), **out)
+
+
 def main():
     from qwasar_amd import synth
     from oracle import ref
@@ -204,6 +238,9 @@ def main():
 if __name__ == "__main__":
     if sys.argv[1:] == ["ckpt"]:
         trimmed_ckpts()
+    elif sys.argv[1:] == ["sparse"]:
+        tiny_sparse()
     else:
         main()
         trimmed_ckpts()
+        tiny_sparse()
