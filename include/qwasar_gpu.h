@@ -172,6 +172,92 @@ void qw_op_hc_mix(qw_cmd c, qw_ref x, qw_ref n, qw_ref m, int32_t rows, int32_t 
 /* h4 += out (x) 2*sigmoid(inj / S), per stream. */
 void qw_op_hc_inject(qw_cmd c, qw_ref h4, qw_ref out, qw_ref inj, int32_t rows, int32_t H, int32_t S);
 
+/* ---- gated DeltaNet (reference qwasar_gpu.h:318-358) ------------------------
+ *
+ * The recurrent sublayer's ops.  They carry state across calls: `state` is
+ * read and written in place.  `snap` receives the state as it stood after
+ * each of the first n_snap rows, snap_stride floats apart (n_snap 0: none). */
+
+/* Causal depthwise conv over [rows, channels] with silu fused; state
+ * [ksize-1, channels] fp32 in and out, oldest sample first; weight bf16
+ * [channels, ksize].  ksize 4 only (refused otherwise, as the reference's). */
+void qw_op_conv1d_causal_silu(qw_cmd c, qw_ref y, qw_ref x, qw_ref state,
+                              qw_ref weight, int32_t channels, int32_t rows,
+                              int32_t ksize, qw_ref snap, int32_t n_snap,
+                              int32_t snap_stride);
+/* g = exp(-exp(A_log) * softplus(a + dt_bias)),  beta = sigmoid(b);
+ * a, b, g, beta F32 [rows, n_v_heads]; A_log, dt_bias BF16 [n_v_heads]. */
+void qw_op_gdn_gates(qw_cmd c, qw_ref g, qw_ref beta, qw_ref a, qw_ref b,
+                     qw_ref A_log, qw_ref dt_bias, int32_t n_v_heads, int32_t rows);
+/* The delta rule per value head over `rows` timesteps: S *= g; kv = S k;
+ * S += k (v - kv) beta; y = S q.  state F32 [hv, dv, dk]; q, k [rows, hk, dk]
+ * already l2-normed; v, y [rows, hv, dv]; value head h reads key head
+ * h / (hv / hk).  dk = dv = 128 only (refused otherwise, as the reference's). */
+void qw_op_gated_delta(qw_cmd c, qw_ref y, qw_ref q, qw_ref k, qw_ref v,
+                       qw_ref g, qw_ref beta, qw_ref state,
+                       int32_t hk, int32_t hv, int32_t dk, int32_t dv, int32_t rows,
+                       qw_ref snap, int32_t n_snap, int32_t snap_stride);
+/* The same with its inputs' preparation inside: q and k raw, normed as
+ * x / sqrt(mean x^2 + l2eps) * q_scale (k_scale); g and beta from a, b,
+ * A_log and dt_bias as qw_op_gdn_gates. */
+typedef struct {
+    qw_ref a, b, A_log, dt_bias;
+    float l2eps, q_scale, k_scale;
+} qw_gdn_prep;
+void qw_op_gated_delta_prep(qw_cmd c, qw_ref y, qw_ref q, qw_ref k, qw_ref v,
+                            const qw_gdn_prep *prep, qw_ref state,
+                            int32_t hk, int32_t hv, int32_t dk, int32_t dv, int32_t rows,
+                            qw_ref snap, int32_t n_snap, int32_t snap_stride);
+/* rms_norm(x, weight) * sigmoid(gate) per row of `dim` (reference
+ * qwasar_gpu.h:618-620): the delta net's output gate.  weight may be a null
+ * ref (unit gain). */
+void qw_op_rms_norm_gated_sigmoid(qw_cmd c, qw_ref y, qw_ref x, qw_ref weight, qw_ref gate,
+                                  int32_t dim, int32_t rows, float eps, float out_scale);
+
+/* ---- QSA: block indexer, selection, masked attention (reference
+ * qwasar_gpu.h:621-646) ------------------------------------------------------
+ *
+ * A query row r sits at position base_pos + r and sees keys 0..base_pos + r;
+ * its complete blocks of `ratio` keys are n = (base_pos + r + 1) / ratio.
+ * Block scores: scores F32 [rows, max_blocks], entry (r, b) for b < n:
+ *   key_b = rope(rms_norm(mean of the block's raw keys) * k_norm) at position
+ *           b * ratio (the first 64 dims, pairs (j, j + 32));
+ *   score = sum over query heads of max(0, qn[r, h] . key_b) / sqrt(d).
+ * qn F32 [rows, nq, d] normed and rotated by the caller; ikeys F32
+ * [max_ctx, d]; k_norm BF16 [d]; inv_freq F32 [32].  rotary_dim 64 and d a
+ * multiple of 32 up to 256 (refused otherwise, as the reference's). */
+void qw_op_qsa_scores(qw_cmd c, qw_ref scores, qw_ref qn, qw_ref ikeys, qw_ref k_norm,
+                      qw_ref inv_freq, int32_t rows, int32_t nq, int32_t d, int32_t ratio,
+                      int32_t base_pos, int32_t rotary_dim, int32_t max_blocks, float eps);
+/* Blocks [b0, b1)'s keys, computed exactly as qw_op_qsa_scores does, into
+ * pool F32 [max_blocks, d]; qw_op_qsa_scores_pooled scores from them and
+ * gives qw_op_qsa_scores' bits. */
+void qw_op_qsa_pool(qw_cmd c, qw_ref pool, qw_ref ikeys, qw_ref k_norm, qw_ref inv_freq,
+                    int32_t d, int32_t ratio, int32_t b0, int32_t b1, int32_t rotary_dim, float eps);
+void qw_op_qsa_scores_pooled(qw_cmd c, qw_ref scores, qw_ref qn, qw_ref pool, int32_t rows,
+                             int32_t nq, int32_t d, int32_t ratio, int32_t base_pos, int32_t max_blocks);
+/* Selection: the block_topk best complete blocks (score descending, ties to
+ * the lower block; a score of -FLT_MAX or below, or NaN, is never taken) and
+ * the incomplete tail are visible.  mask U8 [rows, max_ctx] gets 1/0 for
+ * positions 0..base_pos + r; list U32 [rows, 1 + qw_qsa_list_cap] the count,
+ * then the visible positions ascending.  Up to 65536 blocks a row. */
+static inline int32_t qw_qsa_list_cap(int32_t block_topk, int32_t ratio) {
+    return block_topk * ratio + ratio;
+}
+void qw_op_qsa_select(qw_cmd c, qw_ref mask, qw_ref list, qw_ref scores, int32_t rows, int32_t ratio,
+                      int32_t base_pos, int32_t block_topk, int32_t max_ctx, int32_t max_blocks);
+/* Attention over the listed positions only: out F32 [rows, q_heads, 256] =
+ * softmax(scale q . K) V, q F32 [rows, q_heads, 256], the caches FP16
+ * [kv_heads, max_ctx, 256]; query head h reads kv head h / (q_heads /
+ * kv_heads), a ratio of 1, 2, 4 or 8.  The gated form then multiplies by
+ * sigmoid(gate) [rows, q_heads, 256].  head_dim 256 only. */
+void qw_op_attn_masked(qw_cmd c, qw_ref out, qw_ref q, qw_ref kcache, qw_ref vcache, qw_ref list,
+                       int32_t rows, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                       int32_t max_ctx, int32_t base_pos, float scale, int32_t block_topk, int32_t ratio);
+void qw_op_attn_masked_gated(qw_cmd c, qw_ref out, qw_ref gate, qw_ref q, qw_ref kcache, qw_ref vcache,
+                             qw_ref list, int32_t rows, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                             int32_t max_ctx, int32_t base_pos, float scale, int32_t block_topk, int32_t ratio);
+
 /* ---- the MoE block (reference qwasar_gpu.h:559-616) ------------------------- */
 
 /* out[r] = sum_k w[r,k] y[r*K+k] + sigmoid(g[r]) sh[r]. */

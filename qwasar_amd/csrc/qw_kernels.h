@@ -192,6 +192,39 @@ int qwk_hc_inject(hipStream_t s, float *h4, const float *out, const float *inj, 
 int qwk_hc_mix_up(hipStream_t s, float *x, const float *d, const float *n4, const uint32_t *w,
                   const uint16_t *sc, const uint16_t *bi, int k, int H, int S, int rows, float scale, int group);
 
+/* The gated DeltaNet (qw_gdn.hip).  dk = dv = 128; ksize 4. */
+typedef struct {
+    const float *a, *b;
+    const uint16_t *A_log, *dt_bias;
+    float l2eps, q_scale, k_scale;
+} qwk_gdn_prep;
+int qwk_conv1d_causal_silu(hipStream_t s, float *y, const float *x, float *state, const uint16_t *w,
+                           int channels, int rows, int ksize, float *snap, int n_snap, int snap_stride);
+int qwk_gdn_gates(hipStream_t s, float *g, float *beta, const float *a, const float *b,
+                  const uint16_t *A_log, const uint16_t *dt_bias, int hv, int rows);
+/* prep NULL: q, k normed and g, beta given; else g and beta are unused. */
+int qwk_gated_delta(hipStream_t s, float *y, const float *q, const float *k, const float *v,
+                    const float *g, const float *beta, float *state, int hk, int hv, int dk, int dv,
+                    int rows, float *snap, int n_snap, int snap_stride, const qwk_gdn_prep *prep);
+/* rms_norm(x) (* w) * sigmoid(gate) per row (qw_norm.hip); dim % 4 == 0. */
+int qwk_rms_norm_gated_sigmoid(hipStream_t s, float *y, const float *x, const uint16_t *w, const float *gate,
+                               int dim, int rows, float eps, float out_scale);
+
+/* QSA (qw_qsa.hip): rotary_dim 64, d % 32 == 0, 64 <= d <= 256. */
+int qwk_qsa_scores(hipStream_t s, float *scores, const float *qn, const float *ikeys, const uint16_t *kw,
+                   const float *inv_freq, int rows, int nq, int d, int ratio, int base_pos,
+                   int rotary_dim, int max_blocks, float eps);
+int qwk_qsa_pool(hipStream_t s, float *pool, const float *ikeys, const uint16_t *kw, const float *inv_freq,
+                 int d, int ratio, int b0, int b1, int rotary_dim, float eps);
+int qwk_qsa_scores_pooled(hipStream_t s, float *scores, const float *qn, const float *pool, int rows,
+                          int nq, int d, int ratio, int base_pos, int max_blocks);
+int qwk_qsa_select(hipStream_t s, uint8_t *mask, uint32_t *list, const float *scores, int rows, int ratio,
+                   int base_pos, int block_topk, int max_ctx, int max_blocks);
+/* head_dim 256; q_heads / kv_heads in {1, 2, 4, 8}; gate may be NULL. */
+int qwk_attn_masked(hipStream_t s, float *out, const float *gate, const float *q, const uint16_t *kc,
+                    const uint16_t *vc, const uint32_t *list, int rows, int q_heads, int kv_heads,
+                    int head_dim, int max_ctx, float scale, int cap);
+
 #ifdef __cplusplus
 }
 #endif

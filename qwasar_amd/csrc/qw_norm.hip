@@ -33,10 +33,11 @@ __device__ __forceinline__ uint16_t qn_bf16(float f)
     return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
-// y = x * inv (* w): dim % 4 == 0, rows are float4-aligned
+// y = x * inv (* w) (* sigmoid(gate), the delta net's output gate):
+// dim % 4 == 0, rows are float4-aligned
 __global__ void __launch_bounds__(QN_THREADS) k_rms_norm(float *__restrict__ y, const float *__restrict__ x,
                                                          const uint16_t *__restrict__ w, int dim, float eps,
-                                                         float out_scale)
+                                                         float out_scale, const float *__restrict__ gate)
 {
     __shared__ float part[QN_THREADS / 64];
     const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)blockIdx.x * dim);
@@ -61,6 +62,13 @@ __global__ void __launch_bounds__(QN_THREADS) k_rms_norm(float *__restrict__ y, 
             v.y *= __uint_as_float(wb.x & 0xFFFF0000u);
             v.z *= __uint_as_float(wb.y << 16);
             v.w *= __uint_as_float(wb.y & 0xFFFF0000u);
+        }
+        if (gate) {
+            const float4 g = reinterpret_cast<const float4 *>(gate + (size_t)blockIdx.x * dim)[i];
+            v.x *= 1.0f / (1.0f + expf(-g.x));
+            v.y *= 1.0f / (1.0f + expf(-g.y));
+            v.z *= 1.0f / (1.0f + expf(-g.z));
+            v.w *= 1.0f / (1.0f + expf(-g.w));
         }
         yr[i] = v;
     }
@@ -113,7 +121,18 @@ extern "C" int qwk_rms_norm(hipStream_t s, float *y, const float *x, const uint1
     if (rows <= 0) return 0;
     if (dim <= 0 || dim % 4 || ((uintptr_t)x & 15u) || ((uintptr_t)y & 15u) || ((uintptr_t)w & 7u))
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_rms_norm, dim3(rows), dim3(QN_THREADS), 0, s, y, x, w, dim, eps, out_scale);
+    hipLaunchKernelGGL(k_rms_norm, dim3(rows), dim3(QN_THREADS), 0, s, y, x, w, dim, eps, out_scale, nullptr);
+    return (int)hipGetLastError();
+}
+
+extern "C" int qwk_rms_norm_gated_sigmoid(hipStream_t s, float *y, const float *x, const uint16_t *w,
+                                          const float *gate, int dim, int rows, float eps, float out_scale)
+{
+    if (rows <= 0) return 0;
+    if (!gate || dim <= 0 || dim % 4 || ((uintptr_t)x & 15u) || ((uintptr_t)y & 15u) || ((uintptr_t)w & 7u) ||
+        ((uintptr_t)gate & 15u))
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_rms_norm, dim3(rows), dim3(QN_THREADS), 0, s, y, x, w, dim, eps, out_scale, gate);
     return (int)hipGetLastError();
 }
 

@@ -996,3 +996,141 @@ bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref
     const qwk_resid res = { dp(h), dp(y_prev), dp(h_out), dp(x_out), eps };
     return moe_decode(c, dp(out), dp(idx), dp(w), NULL, &res, &m, rows, QW_DS_HEAP);
 }
+
+/* ---- gated DeltaNet (reference qwasar_gpu.h:318-358, qwasar_metal.m:1101-1215) ---- */
+
+void qw_op_conv1d_causal_silu(qw_cmd c, qw_ref y, qw_ref x, qw_ref state, qw_ref weight, int32_t channels,
+                              int32_t rows, int32_t ksize, qw_ref snap, int32_t n_snap, int32_t snap_stride) {
+    QW_OP(c);
+    if (ksize != 4) {
+        fprintf(stderr, "qwasar: conv kernel size %d unsupported (expected 4)\n", ksize);
+        return;
+    }
+    touch(c, x, 0); touch(c, weight, 0); touch(c, state, 1); touch(c, y, 1);
+    if (n_snap > 0) touch(c, snap, 1);
+    launched(c, "conv1d_causal_silu", qwk_conv1d_causal_silu(G.stream, dp(y), dp(x), dp(state), dp(weight), channels,
+                                                             rows, ksize, n_snap > 0 ? dp(snap) : NULL, n_snap,
+                                                             snap_stride));
+}
+
+void qw_op_gdn_gates(qw_cmd c, qw_ref g, qw_ref beta, qw_ref a, qw_ref b, qw_ref A_log, qw_ref dt_bias,
+                     int32_t n_v_heads, int32_t rows) {
+    QW_OP(c);
+    touch(c, a, 0); touch(c, b, 0); touch(c, A_log, 0); touch(c, dt_bias, 0); touch(c, g, 1); touch(c, beta, 1);
+    launched(c, "gdn_gates", qwk_gdn_gates(G.stream, dp(g), dp(beta), dp(a), dp(b), dp(A_log), dp(dt_bias),
+                                           n_v_heads, rows));
+}
+
+static void gated_delta(qw_cmd c, qw_ref y, qw_ref q, qw_ref k, qw_ref v, qw_ref g, qw_ref beta,
+                        const qw_gdn_prep *prep, qw_ref state, int32_t hk, int32_t hv, int32_t dk, int32_t dv,
+                        int32_t rows, qw_ref snap, int32_t n_snap, int32_t snap_stride) {
+    QW_OP(c);
+    if (dk != 128 || dv != 128) {
+        fprintf(stderr, "qwasar: gated-delta head dims %dx%d unsupported (kernel is built for 128x128)\n", dk, dv);
+        return;
+    }
+    touch(c, q, 0); touch(c, k, 0); touch(c, v, 0); touch(c, state, 1); touch(c, y, 1);
+    if (n_snap > 0) touch(c, snap, 1);
+    qwk_gdn_prep pp;
+    if (prep) {
+        touch(c, prep->a, 0); touch(c, prep->b, 0); touch(c, prep->A_log, 0); touch(c, prep->dt_bias, 0);
+        pp.a = dp(prep->a); pp.b = dp(prep->b); pp.A_log = dp(prep->A_log); pp.dt_bias = dp(prep->dt_bias);
+        pp.l2eps = prep->l2eps; pp.q_scale = prep->q_scale; pp.k_scale = prep->k_scale;
+    } else {
+        touch(c, g, 0); touch(c, beta, 0);
+    }
+    launched(c, prep ? "gated_delta_prep" : "gated_delta",
+             qwk_gated_delta(G.stream, dp(y), dp(q), dp(k), dp(v), dp(g), dp(beta), dp(state), hk, hv, dk, dv, rows,
+                             n_snap > 0 ? dp(snap) : NULL, n_snap, snap_stride, prep ? &pp : NULL));
+}
+
+void qw_op_gated_delta(qw_cmd c, qw_ref y, qw_ref q, qw_ref k, qw_ref v, qw_ref g, qw_ref beta, qw_ref state,
+                       int32_t hk, int32_t hv, int32_t dk, int32_t dv, int32_t rows, qw_ref snap, int32_t n_snap,
+                       int32_t snap_stride) {
+    gated_delta(c, y, q, k, v, g, beta, NULL, state, hk, hv, dk, dv, rows, snap, n_snap, snap_stride);
+}
+
+void qw_op_gated_delta_prep(qw_cmd c, qw_ref y, qw_ref q, qw_ref k, qw_ref v, const qw_gdn_prep *prep,
+                            qw_ref state, int32_t hk, int32_t hv, int32_t dk, int32_t dv, int32_t rows, qw_ref snap,
+                            int32_t n_snap, int32_t snap_stride) {
+    if (!prep) return;
+    const qw_ref none = { 0 };
+    gated_delta(c, y, q, k, v, none, none, prep, state, hk, hv, dk, dv, rows, snap, n_snap, snap_stride);
+}
+
+void qw_op_rms_norm_gated_sigmoid(qw_cmd c, qw_ref y, qw_ref x, qw_ref weight, qw_ref gate, int32_t dim,
+                                  int32_t rows, float eps, float out_scale) {
+    QW_OP(c);
+    touch(c, x, 0); touch(c, weight, 0); touch(c, gate, 0); touch(c, y, 1);
+    launched(c, "rms_norm_gated_sigmoid", qwk_rms_norm_gated_sigmoid(G.stream, dp(y), dp(x), dp(weight), dp(gate),
+                                                                     dim, rows, eps, out_scale));
+}
+
+/* ---- QSA (reference qwasar_gpu.h:621-646, qwasar_metal.m:1898-1966,2042-2068) ---- */
+
+static bool qsa_shape_ok(int32_t rotary_dim, int32_t d) {
+    if (rotary_dim == 64 && d % 32 == 0 && d >= 64 && d <= 256) return true;
+    fprintf(stderr, "qwasar: QSA indexer shape (rotary %d, head %d) unsupported\n", rotary_dim, d);
+    return false;
+}
+
+void qw_op_qsa_scores(qw_cmd c, qw_ref scores, qw_ref qn, qw_ref ikeys, qw_ref k_norm, qw_ref inv_freq,
+                      int32_t rows, int32_t nq, int32_t d, int32_t ratio, int32_t base_pos, int32_t rotary_dim,
+                      int32_t max_blocks, float eps) {
+    if (!qsa_shape_ok(rotary_dim, d)) return;
+    QW_OP(c);
+    touch(c, qn, 0); touch(c, ikeys, 0); touch(c, k_norm, 0); touch(c, inv_freq, 0); touch(c, scores, 1);
+    launched(c, "qsa_scores", qwk_qsa_scores(G.stream, dp(scores), dp(qn), dp(ikeys), dp(k_norm), dp(inv_freq), rows,
+                                             nq, d, ratio, base_pos, rotary_dim, max_blocks, eps));
+}
+
+void qw_op_qsa_pool(qw_cmd c, qw_ref pool, qw_ref ikeys, qw_ref k_norm, qw_ref inv_freq, int32_t d, int32_t ratio,
+                    int32_t b0, int32_t b1, int32_t rotary_dim, float eps) {
+    if (b1 <= b0) return;
+    if (!qsa_shape_ok(rotary_dim, d)) return;
+    QW_OP(c);
+    touch(c, ikeys, 0); touch(c, k_norm, 0); touch(c, inv_freq, 0); touch(c, pool, 1);
+    launched(c, "qsa_pool", qwk_qsa_pool(G.stream, dp(pool), dp(ikeys), dp(k_norm), dp(inv_freq), d, ratio, b0, b1,
+                                         rotary_dim, eps));
+}
+
+void qw_op_qsa_scores_pooled(qw_cmd c, qw_ref scores, qw_ref qn, qw_ref pool, int32_t rows, int32_t nq, int32_t d,
+                             int32_t ratio, int32_t base_pos, int32_t max_blocks) {
+    if (!qsa_shape_ok(64, d)) return;
+    QW_OP(c);
+    touch(c, qn, 0); touch(c, pool, 0); touch(c, scores, 1);
+    launched(c, "qsa_scores_pooled", qwk_qsa_scores_pooled(G.stream, dp(scores), dp(qn), dp(pool), rows, nq, d, ratio,
+                                                           base_pos, max_blocks));
+}
+
+void qw_op_qsa_select(qw_cmd c, qw_ref mask, qw_ref list, qw_ref scores, int32_t rows, int32_t ratio,
+                      int32_t base_pos, int32_t block_topk, int32_t max_ctx, int32_t max_blocks) {
+    QW_OP(c);
+    touch(c, scores, 0); touch(c, mask, 1); touch(c, list, 1);
+    launched(c, "qsa_select", qwk_qsa_select(G.stream, dp(mask), dp(list), dp(scores), rows, ratio, base_pos,
+                                             block_topk, max_ctx, max_blocks));
+}
+
+void qw_op_attn_masked_gated(qw_cmd c, qw_ref out, qw_ref gate, qw_ref q, qw_ref kcache, qw_ref vcache, qw_ref list,
+                             int32_t rows, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t max_ctx,
+                             int32_t base_pos, float scale, int32_t block_topk, int32_t ratio) {
+    (void)base_pos;   /* the list names the positions */
+    if (head_dim != 256) {
+        fprintf(stderr, "qwasar: attention head_dim %d unsupported (kernel is built for 256)\n", head_dim);
+        return;
+    }
+    QW_OP(c);
+    touch(c, q, 0); touch(c, kcache, 0); touch(c, vcache, 0); touch(c, list, 0); touch(c, gate, 0);
+    touch(c, out, 1);
+    launched(c, "attn_masked", qwk_attn_masked(G.stream, dp(out), dp(gate), dp(q), dp(kcache), dp(vcache), dp(list),
+                                               rows, q_heads, kv_heads, head_dim, max_ctx, scale,
+                                               qw_qsa_list_cap(block_topk, ratio)));
+}
+
+void qw_op_attn_masked(qw_cmd c, qw_ref out, qw_ref q, qw_ref kcache, qw_ref vcache, qw_ref list, int32_t rows,
+                       int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t max_ctx, int32_t base_pos,
+                       float scale, int32_t block_topk, int32_t ratio) {
+    const qw_ref none = { 0 };
+    qw_op_attn_masked_gated(c, out, none, q, kcache, vcache, list, rows, q_heads, kv_heads, head_dim, max_ctx,
+                            base_pos, scale, block_topk, ratio);
+}

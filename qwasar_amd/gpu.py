@@ -53,7 +53,13 @@ class qw_moe_layer(C.Structure):
                 ("sh_down", qw_q4_ref), ("sh_gate_w", qw_ref)]
 
 
+class qw_gdn_prep(C.Structure):
+    _fields_ = [("a", qw_ref), ("b", qw_ref), ("A_log", qw_ref), ("dt_bias", qw_ref),
+                ("l2eps", C.c_float), ("q_scale", C.c_float), ("k_scale", C.c_float)]
+
+
 _R = qw_ref
+_F = C.c_float
 
 
 def _sig(name, res, *args):
@@ -131,6 +137,25 @@ _sig("qw_op_hc_mix", None, _P, _R, _R, _R, _I, _I, _I)
 _sig("qw_op_hc_inject", None, _P, _R, _R, _R, _I, _I, _I)
 _sig("qw_op_residual_rms_norm_bf16", None, _P, _R, _R, _R, _I, _I, C.c_float)
 _sig("qw_op_synth", None, _P, _R, _I, C.c_int64, C.c_uint64, C.c_float, C.c_float)
+_sig("qw_op_conv1d_causal_silu", None, _P, _R, _R, _R, _R, _I, _I, _I, _R, _I, _I)
+_sig("qw_op_gdn_gates", None, _P, _R, _R, _R, _R, _R, _R, _I, _I)
+_sig("qw_op_gated_delta", None, _P, _R, _R, _R, _R, _R, _R, _R, _I, _I, _I, _I, _I, _R, _I, _I)
+_sig("qw_op_gated_delta_prep", None, _P, _R, _R, _R, _R, C.POINTER(qw_gdn_prep), _R, _I, _I, _I, _I, _I, _R, _I,
+     _I)
+_sig("qw_op_rms_norm_gated_sigmoid", None, _P, _R, _R, _R, _R, _I, _I, _F, _F)
+_sig("qw_op_qsa_scores", None, _P, _R, _R, _R, _R, _R, _I, _I, _I, _I, _I, _I, _I, _F)
+_sig("qw_op_qsa_pool", None, _P, _R, _R, _R, _R, _I, _I, _I, _I, _I, _F)
+_sig("qw_op_qsa_scores_pooled", None, _P, _R, _R, _R, _I, _I, _I, _I, _I, _I)
+_sig("qw_op_qsa_select", None, _P, _R, _R, _R, _I, _I, _I, _I, _I, _I)
+_sig("qw_op_attn_masked", None, _P, _R, _R, _R, _R, _R, _I, _I, _I, _I, _I, _I, _F, _I, _I)
+_sig("qw_op_attn_masked_gated", None, _P, _R, _R, _R, _R, _R, _R, _I, _I, _I, _I, _I, _I, _F, _I, _I)
+
+
+def qw_qsa_list_cap(block_topk: int, ratio: int) -> int:
+    """The header's static inline (qwasar_gpu.h): entries after the count in
+    one row of the selection's position list."""
+    return block_topk * ratio + ratio
+
 
 EXPORTED = [n for n in dir() if n.startswith(("qw_op_", "qw_buf_", "qw_cmd_", "qw_gpu_", "qw_prof_",
                                               "qw_residency_", "qw_moe_"))

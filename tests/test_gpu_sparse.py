@@ -1,0 +1,330 @@
+"""QSA (block scores, stored keys, selection, masked attention) and the gated
+DeltaNet (conv, gates, delta rule, prep, output gate) on the GPU, through the
+C ABI, against the CPU oracle (oracle/sparse_ref.c, pinned in
+tests/test_oracle_sparse.py).  The cases follow the reference's own tests
+(tests/test_sparse.c:348-470,562-620,887-915; tests/test_gdn.c) with the toy
+checkpoint's weights and shapes, then the full model's shapes.
+
+Bars, written per test:
+- selection: bit-exact (mask and position list) on the same scores;
+- scores: |diff| <= 1e-5 * (1 + |score|) -- the GPU sums the rms norm and the
+  head dots in another order than the oracle's serial loops, and rounds the
+  rotation as one fma; stored-key scores bit-identical to direct scores;
+- attention: 2e-6 absolute on O(1) outputs (online softmax in chunks of 256
+  against the oracle's two-pass form);
+- delta rule: rel-L2 5e-6 on outputs and state (the reference's own bar,
+  tests/test_gdn.c:197-198), and a run of single steps bit-identical to one
+  batched call;
+- conv, gates, output gate: 2e-6 relative (fma and the device's expf)."""
+import os
+
+import numpy as np
+import pytest
+
+from oracle import sparse
+from qwasar_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+FX = dict(np.load(os.path.join(GOLD, "tiny_q4_sparse.npz")))
+EPS = float(FX["eps"])
+
+
+def rnd(shape, seed, lo=-1.0, hi=1.0):
+    return np.random.default_rng(seed).uniform(lo, hi, shape).astype(np.float32)
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return float(np.sqrt(((a - b) ** 2).sum() / max((b * b).sum(), 1e-300)))
+
+
+def same_bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+def rope_inv():
+    _, inv = sparse.rope_tables(int(FX["rotary_dim"]), float(FX["rope_theta"]), FX["mrope_section"])
+    return inv
+
+
+# ---- QSA scores ------------------------------------------------------------------
+
+def gpu_scores(gpu, qn, ikeys, kw, inv, rows, nq, d, ratio, base, max_blocks, pooled=False):
+    B = gpu.Buf
+    qb, kb, wb, ib = B.of(qn), B.of(ikeys), B.of(np.ascontiguousarray(kw)), B.of(inv)
+    sb = B.of(np.full((rows, max_blocks), np.nan, np.float32))
+    c = gpu.qw_cmd_begin()
+    if pooled:
+        pb = B(max_blocks * d * 4)
+        allb = (base + rows) // ratio
+        gpu.qw_op_qsa_pool(c, pb.ref(), kb.ref(), wb.ref(), ib.ref(), d, ratio, 0, allb // 2, 64, EPS)
+        gpu.qw_op_qsa_pool(c, pb.ref(), kb.ref(), wb.ref(), ib.ref(), d, ratio, allb // 2, allb, 64, EPS)
+        gpu.qw_op_qsa_scores_pooled(c, sb.ref(), qb.ref(), pb.ref(), rows, nq, d, ratio, base, max_blocks)
+    else:
+        gpu.qw_op_qsa_scores(c, sb.ref(), qb.ref(), kb.ref(), wb.ref(), ib.ref(), rows, nq, d, ratio, base, 64,
+                             max_blocks, EPS)
+    gpu.run(c, "qsa scores")
+    out = sb.read(np.float32, (rows, max_blocks))
+    pool = pb.read(np.float32, (max_blocks, d)) if pooled else None
+    return out, pool
+
+
+@pytest.mark.parametrize("rows,base,max_ctx,d", [(5, 13, 64, 128), (3, 4000, 4096, 128), (40, 0, 64, 128),
+                                                 (2, 700, 1024, 256), (9, 130, 256, 96)])
+def test_qsa_scores_and_pooled(gpu, rows, base, max_ctx, d):
+    """The reference's case (tests/test_sparse.c:348-421: 5 rows at 13, 64
+    keys), a long context, a prefill from position 0 and the widest and an
+    odd head size; then the same scores from keys stored in two stretches."""
+    nq, ratio = int(FX["nq"]), int(FX["ratio"])
+    mb = max_ctx // ratio
+    kw = FX["k_norm"] if d == 128 else synth.to_bf16(1.0 + 0.1 * rnd(d, d))
+    qn, ik, inv = rnd((rows, nq, d), 51 + d), rnd((max_ctx, d), 52 + d), rope_inv()
+    got, _ = gpu_scores(gpu, qn, ik, kw, inv, rows, nq, d, ratio, base, mb)
+    want = sparse.qsa_scores(qn, ik, kw, inv, rows, nq, d, ratio, base, 64, mb, EPS)
+    for r in range(rows):
+        nb = (base + r + 1) // ratio
+        assert np.all(np.abs(got[r, :nb] - want[r, :nb]) <= 1e-5 * (1 + np.abs(want[r, :nb]))), f"row {r}"
+        assert np.isnan(got[r, nb:]).all(), "entries past the row's complete blocks are left alone"
+    got2, pool = gpu_scores(gpu, qn, ik, kw, inv, rows, nq, d, ratio, base, mb, pooled=True)
+    for r in range(rows):
+        nb = (base + r + 1) // ratio
+        assert same_bits(got2[r, :nb], got[r, :nb]), f"pooled row {r}"
+    allb = (base + rows) // ratio
+    wp = np.zeros((mb, d), np.float32)
+    sparse.qsa_pool(wp, ik, kw, inv, d, ratio, 0, allb, 64, EPS)
+    assert np.allclose(pool[:allb], wp[:allb], rtol=1e-5, atol=1e-6)
+
+
+# ---- selection -------------------------------------------------------------------
+
+def gpu_select(gpu, scores, rows, ratio, base, topk, max_ctx, max_blocks):
+    B = gpu.Buf
+    cap = gpu.qw_qsa_list_cap(topk, ratio)
+    sb = B.of(np.ascontiguousarray(scores, np.float32))
+    mb = B.of(np.full((rows, max_ctx), 7, np.uint8))
+    lb = B.of(np.zeros((rows, 1 + cap), np.uint32))
+    c = gpu.qw_cmd_begin()
+    gpu.qw_op_qsa_select(c, mb.ref(), lb.ref(), sb.ref(), rows, ratio, base, topk, max_ctx, max_blocks)
+    gpu.run(c, "qsa select")
+    return mb.read(np.uint8, (rows, max_ctx)), lb.read(np.uint32, (rows, 1 + cap))
+
+
+def check_select(gpu, scores, rows, ratio, base, topk, max_ctx, max_blocks):
+    m, lst = gpu_select(gpu, scores, rows, ratio, base, topk, max_ctx, max_blocks)
+    wm, wl = sparse.qsa_select(scores, rows, ratio, base, topk, max_ctx, max_blocks)
+    for r in range(rows):
+        n = base + r + 1
+        assert np.array_equal(m[r, :n], wm[r, :n]), f"mask row {r}"
+        assert (m[r, n:] == 7).all(), "positions past the row's keys are left alone"
+        assert np.array_equal(lst[r, :1 + wl[r, 0]], wl[r, :1 + wl[r, 0]]), f"list row {r}"
+    return m, lst
+
+
+def test_qsa_select_reference_case(gpu):
+    """tests/test_sparse.c:423-458: random distinct scores, budget 2 blocks."""
+    rows, base, max_ctx, ratio = 5, 13, 64, 4
+    check_select(gpu, rnd((rows, 16), 53), rows, ratio, base, 2, max_ctx, 16)
+
+
+@pytest.mark.parametrize("base", [2047, 2051, 2052, 4164, 9000, 40001])
+def test_qsa_select_at_scale_with_ties(gpu, base):
+    """tests/test_sparse.c:562-620: budget 512 blocks, 97 score levels, so
+    many blocks tie at the cut."""
+    rows, ratio, topk = 3, 4, 512
+    max_ctx = base + rows + 8
+    mb = max_ctx // ratio
+    st = np.random.default_rng(base).integers(0, 97, (rows, mb))
+    check_select(gpu, (st * 0.25).astype(np.float32), rows, ratio, base, topk, max_ctx, mb)
+
+
+def test_qsa_select_edges(gpu):
+    ratio = 4
+    # every score equal: the lowest blocks win
+    check_select(gpu, np.ones((2, 64), np.float32), 2, ratio, 200, 10, 256, 64)
+    # negative zero ties with zero; -FLT_MAX, -inf and NaN are never taken
+    s = rnd((1, 64), 3)
+    s[0, :5] = [0.0, -0.0, -np.finfo(np.float32).max, -np.inf, np.nan]
+    check_select(gpu, s, 1, ratio, 255, 60, 256, 64)
+    s = np.full((1, 64), -np.finfo(np.float32).max, np.float32)
+    s[0, [3, 40]] = [1.0, -1e30]
+    check_select(gpu, s, 1, ratio, 255, 8, 256, 64)
+    # the budget covers every block; no complete block at all
+    check_select(gpu, rnd((3, 16), 4), 3, ratio, 9, 8, 64, 16)
+    check_select(gpu, rnd((3, 16), 5), 3, ratio, 0, 8, 64, 16)
+    # large magnitudes of both signs
+    check_select(gpu, rnd((2, 1024), 6, -1e30, 1e30), 2, ratio, 4090, 100, 4096, 1024)
+
+
+# ---- masked attention ----------------------------------------------------------------
+
+def attn_case(gpu, rows, qh, kvh, base, topk, ratio, seed, gated=False):
+    D = 256
+    max_ctx = base + rows + 4
+    mb = max_ctx // ratio
+    scores = rnd((rows, mb), seed)
+    m, lst = check_select(gpu, scores, rows, ratio, base, topk, max_ctx, mb)
+    cap = gpu.qw_qsa_list_cap(topk, ratio)
+    q = rnd((rows, qh, D), seed + 1)
+    kc = sparse.f16_bits(rnd((kvh, max_ctx, D), seed + 2))
+    vc = sparse.f16_bits(rnd((kvh, max_ctx, D), seed + 3))
+    gate = rnd((rows, qh, D), seed + 4, -4, 4) if gated else None
+    B = gpu.Buf
+    qb, kb, vb, lb, ob = B.of(q), B.of(kc), B.of(vc), B.of(lst), B(rows * qh * D * 4)
+    c = gpu.qw_cmd_begin()
+    scale = 1.0 / 16.0
+    if gated:
+        gb = B.of(gate)
+        gpu.qw_op_attn_masked_gated(c, ob.ref(), gb.ref(), qb.ref(), kb.ref(), vb.ref(), lb.ref(), rows, qh, kvh, D,
+                                    max_ctx, base, scale, topk, ratio)
+    else:
+        gpu.qw_op_attn_masked(c, ob.ref(), qb.ref(), kb.ref(), vb.ref(), lb.ref(), rows, qh, kvh, D, max_ctx, base,
+                              scale, topk, ratio)
+    gpu.run(c, "attn masked")
+    got = ob.read(np.float32, (rows, qh, D))
+    want = sparse.attn_masked(q, kc, vc, lst, rows, qh, kvh, D, max_ctx, scale, cap, gate=gate)
+    assert np.abs(got - want).max() < 2e-6, f"max |diff| {np.abs(got - want).max():.3g}"
+
+
+@pytest.mark.parametrize("qh,kvh", [(4, 1), (1, 1), (4, 2), (8, 1)])
+def test_attn_masked_small(gpu, qh, kvh):
+    """The toy model's heads (4 query, 1 kv) and the other supported ratios,
+    5 rows at position 13 with a budget of 2 blocks."""
+    attn_case(gpu, 5, qh, kvh, 13, 2, 4, 71 + qh + kvh)
+
+
+def test_attn_masked_long_list_and_gate(gpu):
+    """A budget of 512 blocks at 9000 keys: lists of 2048+ positions walk
+    nine chunks of the online softmax; and the gated form."""
+    attn_case(gpu, 2, 4, 1, 9000, 512, 4, 81)
+    attn_case(gpu, 3, 8, 2, 300, 16, 4, 82, gated=True)
+
+
+# ---- gated DeltaNet ----------------------------------------------------------------
+
+@pytest.mark.parametrize("channels,rows", [(1024, 1), (1024, 7), (10240, 3)])
+def test_conv1d_causal_silu(gpu, channels, rows):
+    w = np.ascontiguousarray(FX["conv1d"]) if channels == 1024 else synth.to_bf16(0.3 * rnd((channels, 4), 9))
+    x, st = rnd((rows, channels), 81), rnd((3, channels), 82)
+    B = gpu.Buf
+    xb, sb, wb, yb = B.of(x), B.of(st), B.of(w), B(rows * channels * 4)
+    nb = B((rows) * 3 * channels * 4)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_op_conv1d_causal_silu(c, yb.ref(), xb.ref(), sb.ref(), wb.ref(), channels, rows, 4, nb.ref(), rows,
+                                 3 * channels)
+    gpu.run(c, "conv1d")
+    y, s1, snap = sparse.conv1d_causal_silu(x, st, w, channels, rows, 4, n_snap=rows)
+    assert np.allclose(yb.read(np.float32, (rows, channels)), y, rtol=2e-6, atol=1e-7)
+    assert same_bits(sb.read(np.float32, (3, channels)), s1), "the window is a copy of inputs"
+    assert same_bits(nb.read(np.float32, (rows, 3, channels)), snap)
+
+
+def test_gdn_gates(gpu):
+    hv, rows = int(FX["hv"]), 9
+    a, b = rnd((rows, hv), 91, -30, 30), rnd((rows, hv), 92, -8, 8)
+    a[0, 0] = 25.0
+    B = gpu.Buf
+    ab, bb, Al, dt = B.of(a), B.of(b), B.of(np.ascontiguousarray(FX["A_log"])), B.of(np.ascontiguousarray(FX["dt_bias"]))
+    gb, tb = B(rows * hv * 4), B(rows * hv * 4)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_op_gdn_gates(c, gb.ref(), tb.ref(), ab.ref(), bb.ref(), Al.ref(), dt.ref(), hv, rows)
+    gpu.run(c, "gdn gates")
+    g, beta = sparse.gdn_gates(a, b, FX["A_log"], FX["dt_bias"], hv, rows)
+    assert np.allclose(gb.read(np.float32, (rows, hv)), g, rtol=4e-6, atol=1e-30)
+    assert np.allclose(tb.read(np.float32, (rows, hv)), beta, rtol=2e-6)
+
+
+def delta_inputs(hk, hv, rows, seed):
+    dk = dv = 128
+    q, k = rnd((rows, hk, dk), seed), rnd((rows, hk, dk), seed + 1)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True) * np.sqrt(dk)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rnd((rows, hv, dv), seed + 2)
+    g = (0.9 + 0.09 * np.abs(rnd((rows, hv), seed + 3))).astype(np.float32)
+    beta = (0.3 + 0.4 * (np.arange(rows * hv).reshape(rows, hv) % 7) / 7.0).astype(np.float32)
+    s0 = rnd((hv, dv, dk), seed + 4) * np.float32(0.05)
+    return [np.ascontiguousarray(a, np.float32) for a in (q, k, v, g, beta, s0)]
+
+
+def gpu_delta(gpu, q, k, v, g, beta, s0, hk, hv, rows, n_snap=0):
+    B = gpu.Buf
+    qb, kb, vb, gb, bb, sb = B.of(q), B.of(k), B.of(v), B.of(g), B.of(beta), B.of(s0)
+    yb = B(rows * hv * 128 * 4)
+    nb = B(max(n_snap, 1) * hv * 128 * 128 * 4)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_op_gated_delta(c, yb.ref(), qb.ref(), kb.ref(), vb.ref(), gb.ref(), bb.ref(), sb.ref(), hk, hv, 128, 128,
+                          rows, nb.ref(), n_snap, hv * 128 * 128)
+    gpu.run(c, "gated delta")
+    return (yb.read(np.float32, (rows, hv, 128)), sb.read(np.float32, (hv, 128, 128)),
+            nb.read(np.float32, (max(n_snap, 1), hv, 128, 128))[:n_snap])
+
+
+@pytest.mark.parametrize("hk,hv,rows", [(2, 4, 1), (2, 4, 3), (2, 4, 40), (16, 48, 1), (16, 48, 64)])
+def test_gated_delta(gpu, hk, hv, rows):
+    """The toy model's heads (2 key, 4 value) and the full model's (16, 48),
+    one step, a few, and runs past one 16-step chunk; snapshots of the first
+    steps; and one step at a time lands on the batched call's bits."""
+    q, k, v, g, beta, s0 = delta_inputs(hk, hv, rows, 7 + rows)
+    ns = min(rows, 3)
+    y, s1, snap = gpu_delta(gpu, q, k, v, g, beta, s0, hk, hv, rows, n_snap=ns)
+    wy, ws, wsnap = sparse.gated_delta(q, k, v, g, beta, s0, hk, hv, 128, 128, rows, n_snap=ns)
+    assert rel_l2(y, wy) < 5e-6 and rel_l2(s1, ws) < 5e-6, (rel_l2(y, wy), rel_l2(s1, ws))
+    for t in range(ns):
+        assert rel_l2(snap[t], wsnap[t]) < 5e-6
+    if rows > 1 and rows <= 40:
+        st = s0
+        for t in range(rows):
+            yt, st, _ = gpu_delta(gpu, q[t:t + 1], k[t:t + 1], v[t:t + 1], g[t:t + 1], beta[t:t + 1], st, hk, hv, 1)
+            assert same_bits(yt[0], y[t]), f"step {t}"
+            if t < ns:
+                assert same_bits(snap[t], st)
+        assert same_bits(st, s1)
+
+
+@pytest.mark.parametrize("hk,hv,rows", [(2, 4, 3), (16, 48, 20)])
+def test_gated_delta_prep(gpu, hk, hv, rows):
+    """Norms and gates inside the recurrence, against the oracle's prep and
+    against the GPU's own composition of rms_norm, gates and the recurrence
+    (tests/test_sparse.c:887-915)."""
+    dk = dv = 128
+    q, k, v = rnd((rows, hk, dk), 41), rnd((rows, hk, dk), 42), rnd((rows, hv, dv), 43)
+    a, b = rnd((rows, hv), 44), rnd((rows, hv), 45)
+    s0 = rnd((hv, dv, dk), 46) * np.float32(0.05)
+    Al = np.ascontiguousarray(np.resize(FX["A_log"], hv))
+    dt = np.ascontiguousarray(np.resize(FX["dt_bias"], hv))
+    eps, qs, ks = 1e-6 / dk, 1.0 / dk, 1.0 / np.sqrt(dk)
+    B = gpu.Buf
+    qb, kb, vb, ab, bb, Ab, db = B.of(q), B.of(k), B.of(v), B.of(a), B.of(b), B.of(Al), B.of(dt)
+    s1b, s2b = B.of(s0), B.of(s0)
+    y1b, y2b = B(rows * hv * dv * 4), B(rows * hv * dv * 4)
+    q1b, k1b, gb, tb = B(q.nbytes), B(k.nbytes), B(rows * hv * 4), B(rows * hv * 4)
+    c = gpu.qw_cmd_begin()
+    prep = gpu.qw_gdn_prep(ab.ref(), bb.ref(), Ab.ref(), db.ref(), eps, qs, ks)
+    gpu.qw_op_gated_delta_prep(c, y2b.ref(), qb.ref(), kb.ref(), vb.ref(), prep, s2b.ref(), hk, hv, dk, dv, rows,
+                               gpu.NULL_REF, 0, 0)
+    gpu.qw_op_rms_norm(c, q1b.ref(), qb.ref(), gpu.NULL_REF, dk, rows * hk, eps, qs)
+    gpu.qw_op_rms_norm(c, k1b.ref(), kb.ref(), gpu.NULL_REF, dk, rows * hk, eps, ks)
+    gpu.qw_op_gdn_gates(c, gb.ref(), tb.ref(), ab.ref(), bb.ref(), Ab.ref(), db.ref(), hv, rows)
+    gpu.qw_op_gated_delta(c, y1b.ref(), q1b.ref(), k1b.ref(), vb.ref(), gb.ref(), tb.ref(), s1b.ref(), hk, hv, dk,
+                          dv, rows, gpu.NULL_REF, 0, 0)
+    gpu.run(c, "gated delta prep")
+    y2, s2 = y2b.read(np.float32, (rows, hv, dv)), s2b.read(np.float32, (hv, dv, dk))
+    y1, s1 = y1b.read(np.float32, (rows, hv, dv)), s1b.read(np.float32, (hv, dv, dk))
+    wy, ws, _ = sparse.gated_delta_prep(q, k, v, a, b, Al, dt, eps, qs, ks, s0, hk, hv, dk, dv, rows)
+    assert rel_l2(y2, wy) < 5e-6 and rel_l2(s2, ws) < 5e-6, (rel_l2(y2, wy), rel_l2(s2, ws))
+    assert rel_l2(y2, y1) < 5e-6 and rel_l2(s2, s1) < 5e-6
+
+
+def test_rms_norm_gated_sigmoid(gpu):
+    dim, rows = 128, 48
+    x, gate = rnd((rows, dim), 7), rnd((rows, dim), 8, -6, 6)
+    w = np.ascontiguousarray(FX["gdn_norm"])
+    B = gpu.Buf
+    xb, gb, wb, yb = B.of(x), B.of(gate), B.of(w), B(x.nbytes)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_op_rms_norm_gated_sigmoid(c, yb.ref(), xb.ref(), wb.ref(), gb.ref(), dim, rows, EPS, 1.0)
+    gpu.run(c, "rms norm gated sigmoid")
+    want = sparse.rms_norm_gated_sigmoid(x, w, gate, dim, rows, EPS)
+    assert np.allclose(yb.read(np.float32, (rows, dim)), want, rtol=3e-6, atol=1e-7)
