@@ -427,6 +427,144 @@ def bench_config2(gpu, lb, L, cfg, seed, steps, warmup, nbatch=32):
             "ideal_us_at_peak": round(ub / HBM_PEAK_GBS / 1e3, 2)}, r2, xs
 
 
+def bench_sparse(gpu, steps=40, seed=99):
+    """The rest of a Flash-Next layer at the full model's shapes: QSA decode
+    at 32K keys (stored-key scores over 8192 blocks, top-512 selection,
+    attention of 24 query / 2 kv heads x 256 over the ~2K kept positions, gated)
+    and its 2048-row prefill scoring; the gated DeltaNet's decode step (conv
+    over 10240 channels, the delta rule over 48 value heads of 128x128 state)
+    and its 2048-step prefill.  Layers cycle through NL copies of the caches
+    and states (past the Infinity Cache) so every step reads HBM.  Times are
+    device time (see timed())."""
+    from qwasar_amd import synth
+    B = gpu.Buf
+    rng = np.random.default_rng(seed)
+    f32 = lambda *sh: rng.standard_normal(sh).astype(np.float32)
+    res = {}
+
+    # ---- QSA decode at C keys
+    C, ratio, nq, d, topk, qh, kvh, D = 32768, 4, 16, 128, 512, 24, 2, 256
+    NL = 12
+    nb = C // ratio
+    cap = gpu.qw_qsa_list_cap(topk, ratio)
+    c = gpu.qw_cmd_begin()
+    layers = []
+    for l in range(NL):
+        pool, kc, vc = B(nb * d * 4), B(kvh * C * D * 2), B(kvh * C * D * 2)
+        gpu.qw_op_synth(c, pool.ref(), synth.SYNTH_F32_BF16_NORMAL, nb * d, synth.sm_key(seed, f"pool{l}"), 1.0, 0.0)
+        gpu.qw_op_synth(c, kc.ref(), synth.SYNTH_BF16_NORMAL, kvh * C * D, synth.sm_key(seed, f"kc{l}"), 0.5, 0.0)
+        gpu.qw_op_synth(c, vc.ref(), synth.SYNTH_BF16_NORMAL, kvh * C * D, synth.sm_key(seed, f"vc{l}"), 0.5, 0.0)
+        layers.append((pool, kc, vc))
+    gpu.run(c, "qsa setup")
+    # the caches hold bf16 patterns of N(0, 0.5): as fp16 bits they are finite
+    # values of a similar spread (the kernel reads them as fp16)
+    qn, q, gate = B.of(f32(1, nq, d)), B.of(f32(1, qh, D)), B.of(f32(1, qh, D))
+    sc, mk, ls, out = B(nb * 4), B(C), B((1 + cap) * 4), B(qh * D * 4)
+
+    def qsa_step(c, l):
+        pool, kc, vc = layers[l % NL]
+        gpu.qw_op_qsa_scores_pooled(c, sc.ref(), qn.ref(), pool.ref(), 1, nq, d, ratio, C - 1, nb)
+        gpu.qw_op_qsa_select(c, mk.ref(), ls.ref(), sc.ref(), 1, ratio, C - 1, topk, C, nb)
+        gpu.qw_op_attn_masked_gated(c, out.ref(), gate.ref(), q.ref(), kc.ref(), vc.ref(), ls.ref(), 1, qh, kvh, D, C,
+                                    C - 1, 1.0 / 16.0, topk, ratio)
+
+    blocker = B(1 << 30)
+
+    def timed(label, fn, n):
+        """Device ms per call of fn: the region starts after ~1 ms of other
+        GPU work (writes to a 1 GiB buffer), during which the host queues every
+        call, so host launch gaps stay outside the region."""
+        c = gpu.qw_cmd_begin()
+        for i in range(4):
+            fn(c, i)
+        gpu.run(c, label + " warm-up")
+        gpu.qw_prof_reset()
+        gpu.qw_prof_set_enabled(True)
+        c = gpu.qw_cmd_begin()
+        for _ in range(4):
+            gpu.qw_op_synth(c, blocker.ref(), synth.SYNTH_U32, (1 << 30) // 4, 1, 0.0, 0.0)
+        gpu.qw_cmd_mark(c, b"blocker")
+        gpu.qw_prof_set_enabled(False)
+        for i in range(n):
+            fn(c, i)
+        gpu.qw_prof_set_enabled(True)
+        gpu.qw_cmd_mark(c, label.encode())
+        gpu.run(c, label)
+        ms = gpu.qw_prof_ms(label.encode(), None)
+        gpu.qw_prof_set_enabled(False)
+        gpu.qw_prof_reset()
+        return ms / n
+
+    ms = timed("qsa decode", qsa_step, steps)
+    kept = topk * ratio + (C % ratio if C % ratio else 0)
+    qbytes = (nb * d * 4 + nq * d * 4 + 2 * nb * 4 + C + (1 + cap) * 4
+              + 2 * kvh * kept * D * 2 + 3 * qh * D * 4)
+    res["qsa_decode"] = {"keys": C, "blocks": nb, "block_topk": topk, "q_heads": qh, "kv_heads": kvh,
+                         "launches": 3, "us_per_token": round(ms * 1e3, 2), "bytes": qbytes,
+                         "hbm_gbs": round(qbytes / (ms * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(qbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    # ---- QSA prefill scoring: 2048 rows at the end of the 32K context
+    R = 2048
+    qnR, scR = B.of(f32(R, nq, d)), B(R * nb * 4)
+
+    def qsa_prefill(c, l):
+        gpu.qw_op_qsa_scores_pooled(c, scR.ref(), qnR.ref(), layers[l % NL][0].ref(), R, nq, d, ratio, C - R, nb)
+
+    ms = timed("qsa prefill scores", qsa_prefill, 10)
+    fl = sum(2.0 * nq * d * ((C - R + r + 1) // ratio) for r in range(R))
+    res["qsa_prefill_scores"] = {"rows": R, "keys": C, "ms": round(ms, 3),
+                                 "tflops_fp32": round(fl / (ms * 1e-3) / 1e12, 2),
+                                 "vs_fp32_peak": round(fl / (ms * 1e-3) / 1e12 / 157.3, 4)}
+    for t in (qn, q, gate, sc, mk, ls, out, qnR, scR):
+        t.free()
+    for tt in layers:
+        for t in tt:
+            t.free()
+
+    # ---- gated DeltaNet decode and prefill (48 value heads, 16 key heads, 128x128)
+    hk, hv, dk, ch = 16, 48, 128, 10240
+    NG = 96
+    c = gpu.qw_cmd_begin()
+    states = []
+    for l in range(NG):
+        st, cs = B(hv * dk * dk * 4), B(3 * ch * 4)
+        gpu.qw_op_synth(c, st.ref(), synth.SYNTH_F32_BF16_NORMAL, hv * dk * dk, synth.sm_key(seed, f"S{l}"), 0.05, 0.0)
+        gpu.qw_op_synth(c, cs.ref(), synth.SYNTH_F32_BF16_NORMAL, 3 * ch, synth.sm_key(seed, f"cs{l}"), 1.0, 0.0)
+        states.append((st, cs))
+    gpu.run(c, "gdn setup")
+    cw = B.of(synth.to_bf16(0.3 * f32(ch, 4)))
+    Al = B.of(synth.to_bf16(np.linspace(-0.5, 1.0, hv).astype(np.float32)))
+    dt = B.of(synth.to_bf16(np.linspace(-0.2, 0.3, hv).astype(np.float32)))
+    R = 2048
+    xin, xmix = B.of(f32(R, ch)), B(R * ch * 4)
+    ab, bb, yb = B.of(f32(R, hv)), B.of(f32(R, hv)), B(R * hv * dk * 4)
+    prep = gpu.qw_gdn_prep(ab.ref(), bb.ref(), Al.ref(), dt.ref(), 1e-6 / dk, 1.0 / dk, 1.0 / np.sqrt(dk))
+
+    def gdn(c, l, rows):
+        st, cs = states[l % NG]
+        gpu.qw_op_conv1d_causal_silu(c, xmix.ref(), xin.ref(), cs.ref(), cw.ref(), ch, rows, 4, gpu.NULL_REF, 0, 0)
+        # q, k, v: packed [rows, heads, 128] inputs of the recurrence
+        gpu.qw_op_gated_delta_prep(c, yb.ref(), qkv[0].ref(), qkv[1].ref(), qkv[2].ref(), prep, st.ref(), hk, hv, dk,
+                                   dk, rows, gpu.NULL_REF, 0, 0)
+
+    qkv = (B.of(f32(R, hk, dk)), B.of(f32(R, hk, dk)), B.of(f32(R, hv, dk)))
+    ms = timed("gdn decode", lambda c, l: gdn(c, l, 1), steps)
+    gbytes = 2 * hv * dk * dk * 4 + 2 * 3 * ch * 4 + ch * 4 * 2 + ch * 4 * 2 + (2 * hk + hv) * dk * 4 + hv * dk * 4
+    res["gdn_decode"] = {"hk": hk, "hv": hv, "dk": dk, "conv_channels": ch, "launches": 2,
+                         "us_per_token": round(ms * 1e3, 2), "bytes": gbytes,
+                         "hbm_gbs": round(gbytes / (ms * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(gbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    ms = timed("gdn prefill", lambda c, l: gdn(c, l, R), 3)
+    res["gdn_prefill"] = {"rows": R, "ms": round(ms, 3), "tokens_per_s": round(R / (ms * 1e-3), 1)}
+    for t in (cw, Al, dt, xin, xmix, ab, bb, yb, blocker) + qkv:
+        t.free()
+    for tt in states:
+        for t in tt:
+            t.free()
+    return res
+
+
 def cpu_sample(L, x, seconds, rows_per_call):
     """Seconds per call of the oracle's moe_forward on `rows_per_call` rows of
     x at a time, over a bounded time; returns (seconds per call, calls)."""
@@ -462,6 +600,8 @@ def main():
     ap.add_argument("--config4-only", action="store_true", help="run only the 48-layer stack and print it")
     ap.add_argument("--no-hc", action="store_true", help="skip the hyper-connection mixer")
     ap.add_argument("--hc-only", action="store_true", help="run only the hyper-connection mixer and print it")
+    ap.add_argument("--no-sparse", action="store_true", help="skip QSA and the gated DeltaNet")
+    ap.add_argument("--sparse-only", action="store_true", help="run only QSA and the gated DeltaNet and print them")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--calib-copy", type=int, default=0, help="bytes: run only the copy calibration")
     ap.add_argument("--decode-only-steps", type=int, default=0,
@@ -488,6 +628,9 @@ def main():
 
     if args.hc_only:
         print(json.dumps({"hc_mixer": bench_hc(gpu, 200)}), flush=True)
+        return
+    if args.sparse_only:
+        print(json.dumps({"sparse": bench_sparse(gpu)}), flush=True)
         return
     if args.config4_only:
         print(json.dumps({"config4": bench_stack(gpu, 48, 2048, 256, 4)}), flush=True)
@@ -588,6 +731,8 @@ def main():
         out["config4"] = bench_stack(gpu, 48, 2048, 256, 4)
     if not args.no_hc:
         out["hc_mixer"] = bench_hc(gpu, 200)
+    if not args.no_sparse:
+        out["sparse"] = bench_sparse(gpu)
 
     if not args.no_cpu:
         # the oracle (scalar C, one thread) on bounded samples of the same

@@ -249,7 +249,7 @@ void qw_op_qsa_select(qw_cmd c, qw_ref mask, qw_ref list, qw_ref scores, int32_t
 /* Attention over the listed positions only: out F32 [rows, q_heads, 256] =
  * softmax(scale q . K) V, q F32 [rows, q_heads, 256], the caches FP16
  * [kv_heads, max_ctx, 256]; query head h reads kv head h / (q_heads /
- * kv_heads), a ratio of 1, 2, 4 or 8.  The gated form then multiplies by
+ * kv_heads), a ratio of 1, 2, 4, 8, 12 or 16.  The gated form then multiplies by
  * sigmoid(gate) [rows, q_heads, 256].  head_dim 256 only. */
 void qw_op_attn_masked(qw_cmd c, qw_ref out, qw_ref q, qw_ref kcache, qw_ref vcache, qw_ref list,
                        int32_t rows, int32_t q_heads, int32_t kv_heads, int32_t head_dim,

@@ -220,10 +220,13 @@ int qwk_qsa_scores_pooled(hipStream_t s, float *scores, const float *qn, const f
                           int nq, int d, int ratio, int base_pos, int max_blocks);
 int qwk_qsa_select(hipStream_t s, uint8_t *mask, uint32_t *list, const float *scores, int rows, int ratio,
                    int base_pos, int block_topk, int max_ctx, int max_blocks);
-/* head_dim 256; q_heads / kv_heads in {1, 2, 4, 8}; gate may be NULL. */
+/* head_dim 256; q_heads / kv_heads in {1, 2, 4, 8, 12, 16}; gate may be NULL.
+ * work: qwk_attn_masked_work_bytes bytes for the split partials (none needed
+ * when it returns 0; with less, the list is not split). */
 int qwk_attn_masked(hipStream_t s, float *out, const float *gate, const float *q, const uint16_t *kc,
                     const uint16_t *vc, const uint32_t *list, int rows, int q_heads, int kv_heads,
-                    int head_dim, int max_ctx, float scale, int cap);
+                    int head_dim, int max_ctx, float scale, int cap, void *work, size_t work_bytes);
+size_t qwk_attn_masked_work_bytes(int rows, int q_heads, int kv_heads, int cap);
 
 #ifdef __cplusplus
 }

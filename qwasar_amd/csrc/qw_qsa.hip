@@ -20,18 +20,23 @@
 //
 // Selection (k_qsa_select): a workgroup of 1024 threads per query.  Scores
 // map to 32-bit keys that order as the floats do (-0 as +0; -FLT_MAX, -inf
-// and NaN, which the reference's scan never picks, to 0).  A radix search in
-// three passes of 11, 11 and 10 bits finds the exact key T of the last block
-// taken; keys above T are taken and the rest of the budget comes from keys
+// and NaN, which the reference's scan never picks, to 0).  A radix search
+// over key - kmin (the selectable keys' range), 8 bits a pass from the
+// range's top bit and counted into per-wave histograms, finds the exact key
+// T of the last block taken (scores of similar size share their leading
+// bits: counted from bit 31 they would pile into a few bins and serialise
+// the atomics); keys above T are taken and the rest of the budget comes from keys
 // equal to T in block order.  Each thread owns a contiguous run of blocks, so
 // block order is thread order and the position list is one prefix sum.
 //
-// Masked attention (k_attn_masked<G>): a workgroup per (query row, kv head)
-// with its G query heads.  Positions from the list go 256 at a time: a thread
-// per position scores its fp16 key row against the G heads, the chunk's
-// maxima and exponentials update an online softmax, and the waves accumulate
-// the chunk's value rows with lanes over dims (each value row one coalesced
-// 512-byte read).
+// Masked attention (k_attn_masked<G>): a workgroup per (query row, kv head,
+// split of the position list) with its G query heads.  Positions go 32 at a
+// time: eight threads per position score its fp16 key row against the G
+// heads, the pass's maxima and exponentials update an online softmax, and
+// the waves accumulate the pass's value rows with lanes over dims (each value
+// row one coalesced 512-byte read).  When rows x kv heads alone would leave
+// the chip idle (decode), the list is split over enough workgroups to fill
+// it and k_attn_merge combines the splits' softmax states in split order.
 #include "qw_device.h"
 #include "qw_kernels.h"
 
@@ -92,6 +97,10 @@ __device__ __forceinline__ void qs_score_rows(float *__restrict__ scores, const 
         const float4 v = *reinterpret_cast<const float4 *>(kl + lane * (D + 4) + i);
         kr[i] = v.x; kr[i + 1] = v.y; kr[i + 2] = v.z; kr[i + 3] = v.w;
     }
+    // keeps the key in registers: without this the compiler re-reads it from
+    // LDS inside every head's dot
+#pragma unroll
+    for (int i = 0; i < D; i++) asm volatile("" : "+v"(kr[i]));
     const float rs = sqrtf((float)d);
     for (int r = r0; r < min(r0 + QS_ROWS, rows); r++) {
         const int nb = (base_pos + r + 1) / ratio;
@@ -128,7 +137,7 @@ __device__ __forceinline__ void qs_score_rows(float *__restrict__ scores, const 
 }
 
 template <int D, bool POOLED>
-__global__ void __launch_bounds__(QS_THREADS) k_qsa_scores(float *__restrict__ scores, const float *__restrict__ qn,
+__global__ void __launch_bounds__(QS_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) k_qsa_scores(float *__restrict__ scores, const float *__restrict__ qn,
                                                            const float *__restrict__ src,
                                                            const uint16_t *__restrict__ kw,
                                                            const float *__restrict__ inv_freq, int rows, int nq,
@@ -147,15 +156,8 @@ __global__ void __launch_bounds__(QS_THREADS) k_qsa_scores(float *__restrict__ s
             const int bl = i / (D / 4), j = 4 * (i % (D / 4));
             float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             const int b = b0 + bl;
-            if (b < nb_hi) {
-                const float *p = src + (size_t)b * d + j;
-                if (j + 3 < d) v = make_float4(p[0], p[1], p[2], p[3]);
-                else {
-                    if (j < d) v.x = p[0];
-                    if (j + 1 < d) v.y = p[1];
-                    if (j + 2 < d) v.z = p[2];
-                }
-            }
+            if (b < nb_hi && j < d)   // d % 32 == 0: a float4 is wholly in or out
+                v = *reinterpret_cast<const float4 *>(src + (size_t)b * d + j);
             *reinterpret_cast<float4 *>(kl + bl * (D + 4) + j) = v;
         }
     } else {
@@ -205,6 +207,21 @@ __device__ __forceinline__ uint32_t qs_key(float v)
     return (u >> 31) ? ~u : (u | 0x80000000u);
 }
 
+// Minimum over the workgroup; every thread calls it and gets the result.
+__device__ __forceinline__ uint32_t qs_block_min(uint32_t v, uint32_t *wt)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, 64));
+    if (lane == 0) wt[wave] = v;
+    __syncthreads();
+    uint32_t r = wt[0];
+#pragma unroll
+    for (int w = 1; w < QS_SEL_WAVES; w++) r = min(r, wt[w]);
+    __syncthreads();
+    return r;
+}
+
 // Exclusive prefix sum of one value per thread over the workgroup, thread
 // order; *total gets the sum.  Every thread calls it.
 __device__ __forceinline__ uint32_t qs_scan(uint32_t v, uint32_t *wt, uint32_t *total)
@@ -234,70 +251,89 @@ __device__ __forceinline__ uint32_t qs_scan(uint32_t v, uint32_t *wt, uint32_t *
     return r;
 }
 
+#define QS_SEL_KREG 8      // keys a thread keeps in registers (up to 8192 blocks)
+
+// A thread's contiguous run of blocks [lo, hi): its keys, from registers
+// when the run fits (every load issued at once), else from the scores.
+#define QS_RUN(body)                                                              \
+    if (in_regs) {                                                                \
+        _Pragma("unroll") for (int i = 0; i < QS_SEL_KREG; i++)                   \
+            if (lo + i < hi) { const int b = lo + i; const uint32_t k = kr[i]; body } \
+    } else {                                                                      \
+        for (int b = lo; b < hi; b++) { const uint32_t k = qs_key(sc[b]); body }  \
+    }
+
 __global__ void __launch_bounds__(QS_SEL_THREADS) k_qsa_select(uint8_t *__restrict__ mask, uint32_t *__restrict__ list,
                                                                const float *__restrict__ scores, int ratio,
                                                                int base_pos, int block_topk, int max_ctx,
                                                                int max_blocks, int cap)
 {
     extern __shared__ uint8_t sel[];
-    __shared__ uint32_t hist[2048];
+    __shared__ uint32_t hist[QS_SEL_WAVES][256];   // a histogram per wave: no cross-wave atomics
     __shared__ uint32_t wt[QS_SEL_WAVES];
     __shared__ uint32_t sh_total, sh_bin, sh_need;
-    const int tid = threadIdx.x, r = blockIdx.x;
+    const int tid = threadIdx.x, wave = tid >> 6, r = blockIdx.x;
     const int n_keys = base_pos + r + 1, nb = n_keys / ratio;
     const float *sc = scores + (size_t)r * max_blocks;
     const int per = (nb + QS_SEL_THREADS - 1) / QS_SEL_THREADS;
     const int lo = min(tid * per, nb), hi = min(lo + per, nb);
+    const bool in_regs = per <= QS_SEL_KREG;
+    uint32_t kr[QS_SEL_KREG];
+#pragma unroll
+    for (int i = 0; i < QS_SEL_KREG; i++) kr[i] = in_regs && lo + i < hi ? qs_key(sc[lo + i]) : 0u;
 
-    uint32_t cnt = 0;
-    for (int b = lo; b < hi; b++) {
-        sel[b] = 0;
-        cnt += qs_key(sc[b]) != 0u;
-    }
+    uint32_t cnt = 0, mn = 0xFFFFFFFFu, mx = 0u;
+    QS_RUN(sel[b] = 0; if (k) { cnt++; mn = min(mn, k); mx = max(mx, k); })
     qs_scan(cnt, wt, &sh_total);
     const uint32_t S = sh_total;
     const uint32_t take = min((uint32_t)max(block_topk, 0), S);
     if (take == S) {
-        for (int b = lo; b < hi; b++) sel[b] = qs_key(sc[b]) != 0u;
+        QS_RUN(sel[b] = k != 0u;)
     } else if (take > 0) {
-        uint32_t prefix = 0, known = 0, need = take;
-        const int shifts[3] = { 21, 10, 0 }, widths[3] = { 11, 11, 10 };
-        for (int p = 0; p < 3; p++) {
-            const int shift = shifts[p], nbins = 1 << widths[p];
-            const uint32_t bmask = (uint32_t)nbins - 1u;
-            for (int i = tid; i < nbins; i += QS_SEL_THREADS) hist[i] = 0;
+        // the key of the take-th largest.  The passes count u = key - kmin
+        // (kmin, kmax: the selectable keys' range), 8 bits at a time from
+        // the range's top bit, so even scores that share their leading bits
+        // spread over the bins
+        mn = qs_block_min(mn, wt);
+        mx = ~qs_block_min(~mx, wt);
+        const uint32_t range = mx - mn;
+        const int nbits = range ? 32 - __builtin_clz(range) : 0;
+        uint32_t prefix = 0, need = take;
+        int prev = 32, shift = nbits > 8 ? nbits - 8 : 0;
+        while (true) {
+            const uint32_t bmask = prev - shift >= 32 ? 0xFFFFFFFFu : ((1u << (prev - shift)) - 1u);
+            for (int i = tid; i < QS_SEL_WAVES * 256; i += QS_SEL_THREADS) (&hist[0][0])[i] = 0;
             __syncthreads();
-            for (int b = tid; b < nb; b += QS_SEL_THREADS) {
-                const uint32_t k = qs_key(sc[b]);
-                if ((k & known) == prefix) atomicAdd(&hist[(k >> shift) & bmask], 1u);
-            }
+            const uint32_t hp = prev >= 32 ? 0u : prefix >> prev;
+            QS_RUN(if (k) {
+                const uint32_t u = k - mn;
+                if ((prev >= 32 ? 0u : u >> prev) == hp) atomicAdd(&hist[wave][(u >> shift) & bmask], 1u);
+            })
             __syncthreads();
-            // bins from the top: thread t holds bins nbins-1-2t and nbins-2-2t
-            // (one bin, nbins-1-t, in the 10-bit pass)
-            const int per_t = nbins / QS_SEL_THREADS;
-            const int top = nbins - 1 - per_t * tid;
-            const uint32_t c0 = hist[top], c1 = per_t == 2 ? hist[top - 1] : 0u;
-            const uint32_t above = qs_scan(c0 + c1, wt, &sh_total);
-            if (above < need && above + c0 + c1 >= need) {
-                if (above + c0 >= need) { sh_bin = (uint32_t)top; sh_need = need - above; }
-                else { sh_bin = (uint32_t)(top - 1); sh_need = need - above - c0; }
+            // thread t < 256 holds bin 255 - t summed over the waves (in wave
+            // order); a scan from the top bin finds where the count reaches `need`
+            uint32_t cbin = 0;
+            if (tid < 256)
+                for (int w = 0; w < QS_SEL_WAVES; w++) cbin += hist[w][255 - tid];
+            const uint32_t above = qs_scan(cbin, wt, &sh_total);
+            if (tid < 256 && above < need && above + cbin >= need) {
+                sh_bin = 255u - (uint32_t)tid;
+                sh_need = need - above;
             }
             __syncthreads();
             prefix |= sh_bin << shift;
-            known |= bmask << shift;
             need = sh_need;
             __syncthreads();
+            if (shift == 0) break;
+            prev = shift;
+            shift = shift > 8 ? shift - 8 : 0;
         }
-        const uint32_t T = prefix;
+        const uint32_t T = prefix + mn;   // back from the range's offset to the key
+        // everything above T; then the first `need` equal to T, by block
         uint32_t eq = 0;
-        for (int b = lo; b < hi; b++) {
-            const uint32_t k = qs_key(sc[b]);
-            if (k > T) sel[b] = 1;
-            else eq += k == T;
-        }
+        QS_RUN(if (k > T) sel[b] = 1; else eq += k == T;)
         uint32_t rank = qs_scan(eq, wt, &sh_total);
-        for (int b = lo; b < hi && rank < need; b++)
-            if (qs_key(sc[b]) == T) { sel[b] = 1; rank++; }
+        QS_RUN(if (k == T && rank < need) { sel[b] = 1; rank++; })
     }
     __syncthreads();
     uint32_t mine = 0;
@@ -317,41 +353,40 @@ __global__ void __launch_bounds__(QS_SEL_THREADS) k_qsa_select(uint8_t *__restri
     uint8_t *mr = mask + (size_t)r * max_ctx;
     for (int t = tid; t < n_keys; t += QS_SEL_THREADS) mr[t] = t >= nb * ratio ? 1 : sel[t / ratio];
 }
+#undef QS_RUN
 
 // ---- masked attention -------------------------------------------------------------
 
 #define QA_D 256
-#define QA_CHUNK 256
+#define QA_P 32            // positions a workgroup takes per pass
 
 __device__ __forceinline__ float qa_f16(uint32_t bits)
 {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)bits);
 }
 
-__device__ __forceinline__ void qa_h8(uint4 u, float *f)
-{
-    const uint32_t w[4] = { u.x, u.y, u.z, u.w };
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        f[2 * i] = qa_f16(w[i] & 0xFFFFu);
-        f[2 * i + 1] = qa_f16(w[i] >> 16);
-    }
-}
-
+// A workgroup per (query row, kv head, split): the split's share of the
+// row's listed positions, QA_P at a time.  With one split it writes the
+// output; otherwise its softmax state (max, sum, unnormalised output per
+// head) goes to `part` and k_attn_merge combines the splits in order.
 template <int G>
-__global__ void __launch_bounds__(256) k_attn_masked(float *__restrict__ out, const float *__restrict__ gate,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) k_attn_masked(float *__restrict__ out, const float *__restrict__ gate,
                                                      const float *__restrict__ q, const uint16_t *__restrict__ kc,
                                                      const uint16_t *__restrict__ vc, const uint32_t *__restrict__ list,
-                                                     int q_heads, int kv_heads, int max_ctx, float scale, int cap)
+                                                     int q_heads, int kv_heads, int max_ctx, float scale, int cap,
+                                                     int nsplit, float *__restrict__ part)
 {
     __shared__ float4 qs4[G][QA_D / 4];          // the G heads, pre-scaled
-    __shared__ float ps[G][QA_CHUNK];            // the chunk's scores, then weights
+    __shared__ float ps[G][QA_P];                // a pass's scores, then weights
     __shared__ float red[G][4];
-    __shared__ float accw[4][G][QA_D];           // the waves' partial outputs
+    __shared__ float wbuf[G][QA_D];              // the waves' partial outputs meet here
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int row = blockIdx.x / kv_heads, kvh = blockIdx.x % kv_heads;
+    const int split = blockIdx.x % nsplit, rk = blockIdx.x / nsplit;
+    const int row = rk / kv_heads, kvh = rk % kv_heads;
     const uint32_t *lr = list + (size_t)row * (1 + cap);
     const int n_sel = (int)lr[0];
+    const int passes = (n_sel + QA_P - 1) / QA_P, per = (passes + nsplit - 1) / nsplit;
+    const int j_lo = min(split * per * QA_P, n_sel), j_hi = min(j_lo + per * QA_P, n_sel);
     const float *qp = q + ((size_t)row * q_heads + (size_t)kvh * G) * QA_D;
     for (int i = tid; i < G * QA_D; i += 256) reinterpret_cast<float *>(qs4)[i] = qp[i] * scale;
     const uint16_t *kbase = kc + (size_t)kvh * max_ctx * QA_D;
@@ -364,35 +399,50 @@ __global__ void __launch_bounds__(256) k_attn_masked(float *__restrict__ out, co
         acc[g][0] = acc[g][1] = acc[g][2] = acc[g][3] = 0.0f;
     }
     __syncthreads();
-    for (int j0 = 0; j0 < n_sel; j0 += QA_CHUNK) {
-        const int n = min(QA_CHUNK, n_sel - j0);
-        // scores: a thread per position
-        if (tid < n) {
-            const uint4 *kr = reinterpret_cast<const uint4 *>(kbase + (size_t)lr[1 + j0 + tid] * QA_D);
-            float s[G];
+    for (int j0 = j_lo; j0 < j_hi; j0 += QA_P) {
+        const int n = min(QA_P, j_hi - j0);
+        // scores: eight threads per position, 32 dims each (one 64-byte
+        // piece of the fp16 key row), every load issued first; the eight
+        // partial dots meet in the xor tree of their 8-lane run
+        {
+            const int jj = tid >> 3, part = tid & 7;
+            float sg[G];
 #pragma unroll
-            for (int g = 0; g < G; g++) s[g] = 0.0f;
-            for (int c = 0; c < QA_D / 8; c++) {
-                float kf[8];
-                qa_h8(kr[c], kf);
+            for (int g = 0; g < G; g++) sg[g] = 0.0f;
+            if (jj < n) {
+                const uint4 *kr = reinterpret_cast<const uint4 *>(kbase + (size_t)lr[1 + j0 + jj] * QA_D + 32 * part);
+                uint4 kv[4];
 #pragma unroll
-                for (int g = 0; g < G; g++) {
-                    const float4 a = qs4[g][2 * c], b = qs4[g][2 * c + 1];
-                    s[g] = __builtin_fmaf(a.x, kf[0], s[g]);
-                    s[g] = __builtin_fmaf(a.y, kf[1], s[g]);
-                    s[g] = __builtin_fmaf(a.z, kf[2], s[g]);
-                    s[g] = __builtin_fmaf(a.w, kf[3], s[g]);
-                    s[g] = __builtin_fmaf(b.x, kf[4], s[g]);
-                    s[g] = __builtin_fmaf(b.y, kf[5], s[g]);
-                    s[g] = __builtin_fmaf(b.z, kf[6], s[g]);
-                    s[g] = __builtin_fmaf(b.w, kf[7], s[g]);
+                for (int c = 0; c < 4; c++) kv[c] = kr[c];
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    const uint32_t w[4] = { kv[c].x, kv[c].y, kv[c].z, kv[c].w };
+                    const int d0 = 32 * part + 8 * c;
+                    float kf[8];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) { kf[2 * e] = qa_f16(w[e] & 0xFFFFu); kf[2 * e + 1] = qa_f16(w[e] >> 16); }
+#pragma unroll
+                    for (int g = 0; g < G; g++) {
+                        const float4 a = qs4[g][d0 / 4], b = qs4[g][d0 / 4 + 1];
+                        sg[g] = __builtin_fmaf(a.x, kf[0], sg[g]);
+                        sg[g] = __builtin_fmaf(a.y, kf[1], sg[g]);
+                        sg[g] = __builtin_fmaf(a.z, kf[2], sg[g]);
+                        sg[g] = __builtin_fmaf(a.w, kf[3], sg[g]);
+                        sg[g] = __builtin_fmaf(b.x, kf[4], sg[g]);
+                        sg[g] = __builtin_fmaf(b.y, kf[5], sg[g]);
+                        sg[g] = __builtin_fmaf(b.z, kf[6], sg[g]);
+                        sg[g] = __builtin_fmaf(b.w, kf[7], sg[g]);
+                    }
                 }
             }
 #pragma unroll
-            for (int g = 0; g < G; g++) ps[g][tid] = s[g];
+            for (int g = 0; g < G; g++) {
+                const float t = qw_xor_sum<8>(sg[g]);
+                if (jj < n && part == 0) ps[g][jj] = t;
+            }
         }
         __syncthreads();
-        // the chunk's max per head
+        // the pass's max per head
 #pragma unroll
         for (int g = 0; g < G; g++) {
             float v = tid < n ? ps[g][tid] : -FLT_MAX;
@@ -400,17 +450,15 @@ __global__ void __launch_bounds__(256) k_attn_masked(float *__restrict__ out, co
             if (lane == 0) red[g][wave] = v;
         }
         __syncthreads();
-        float scale_old[G];
+        float rescale[G];
 #pragma unroll
         for (int g = 0; g < G; g++) {
             const float cm = fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3]));
             const float mn = fmaxf(m[g], cm);
-            scale_old[g] = expf(m[g] - mn);
+            rescale[g] = expf(m[g] - mn);
             m[g] = mn;
         }
-        __syncthreads();                             // red free, every thread has the maxima
-        // weights, and the chunk's sum per head (lane-serial, then the wave
-        // trees, then the waves in order)
+        __syncthreads();                             // red read by every thread
 #pragma unroll
         for (int g = 0; g < G; g++) {
             float e = 0.0f;
@@ -424,41 +472,130 @@ __global__ void __launch_bounds__(256) k_attn_masked(float *__restrict__ out, co
         __syncthreads();
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            l[g] = l[g] * scale_old[g] + ((red[g][0] + red[g][1]) + (red[g][2] + red[g][3]));
+            l[g] = l[g] * rescale[g] + ((red[g][0] + red[g][1]) + (red[g][2] + red[g][3]));
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[g][i] *= scale_old[g];
+            for (int i = 0; i < 4; i++) acc[g][i] *= rescale[g];
         }
-        // values: wave w takes positions w, w+4, ...; lane owns dims 4l..4l+3
-        for (int jj = wave; jj < n; jj += 4) {
-            const uint2 u = *reinterpret_cast<const uint2 *>(vbase + (size_t)lr[1 + j0 + jj] * QA_D + 4 * lane);
-            const float v0 = qa_f16(u.x & 0xFFFFu);
-            const float v1 = qa_f16(u.x >> 16);
-            const float v2 = qa_f16(u.y & 0xFFFFu);
-            const float v3 = qa_f16(u.y >> 16);
+        // values: wave w takes the pass's positions 8w..8w+7, lane dims
+        // 4l..4l+3; the rows are requested before any is used
+        {
+            const int jb = (QA_P / 4) * wave, nj = max(0, min(QA_P / 4, n - jb));
+            uint2 vv[QA_P / 4];
 #pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float p = ps[g][jj];
-                acc[g][0] = __builtin_fmaf(p, v0, acc[g][0]);
-                acc[g][1] = __builtin_fmaf(p, v1, acc[g][1]);
-                acc[g][2] = __builtin_fmaf(p, v2, acc[g][2]);
-                acc[g][3] = __builtin_fmaf(p, v3, acc[g][3]);
+            for (int i = 0; i < QA_P / 4; i++)
+                if (i < nj) vv[i] = *reinterpret_cast<const uint2 *>(vbase + (size_t)lr[1 + j0 + jb + i] * QA_D + 4 * lane);
+#pragma unroll
+            for (int i = 0; i < QA_P / 4; i++) {
+                if (i < nj) {
+                    const float v0 = qa_f16(vv[i].x & 0xFFFFu), v1 = qa_f16(vv[i].x >> 16);
+                    const float v2 = qa_f16(vv[i].y & 0xFFFFu), v3 = qa_f16(vv[i].y >> 16);
+#pragma unroll
+                    for (int g = 0; g < G; g++) {
+                        const float p = ps[g][jb + i];
+                        acc[g][0] = __builtin_fmaf(p, v0, acc[g][0]);
+                        acc[g][1] = __builtin_fmaf(p, v1, acc[g][1]);
+                        acc[g][2] = __builtin_fmaf(p, v2, acc[g][2]);
+                        acc[g][3] = __builtin_fmaf(p, v3, acc[g][3]);
+                    }
+                }
             }
         }
-        __syncthreads();                             // ps and red free for the next chunk
+        __syncthreads();                             // ps and red free for the next pass
     }
+    // the waves' partial outputs meet as (w0 + w1) + (w2 + w3), through wbuf
+    // and the query array (no longer read)
+    float *bufA = &wbuf[0][0], *bufB = reinterpret_cast<float *>(&qs4[0][0]);
+    if (wave == 1 || wave == 3) {
+        float *dst = wave == 1 ? bufA : bufB;
 #pragma unroll
-    for (int g = 0; g < G; g++)
+        for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) accw[wave][g][4 * lane + i] = acc[g][i];
+            for (int i = 0; i < 4; i++) dst[g * QA_D + 4 * lane + i] = acc[g][i];
+    }
     __syncthreads();
-    for (int i = tid; i < G * QA_D; i += 256) {
-        const int g = i / QA_D, dim = i % QA_D;
-        const float s = (accw[0][g][dim] + accw[1][g][dim]) + (accw[2][g][dim] + accw[3][g][dim]);
-        float o = l[g] > 0.0f ? s / l[g] : 0.0f;
-        const size_t oi = ((size_t)row * q_heads + (size_t)kvh * G + g) * QA_D + dim;
-        if (gate) o *= 1.0f / (1.0f + expf(-gate[oi]));
-        out[oi] = o;
+    if (wave == 0 || wave == 2) {
+        const float *src = wave == 0 ? bufA : bufB;
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[g][i] = acc[g][i] + src[g * QA_D + 4 * lane + i];
     }
+    __syncthreads();
+    if (wave == 2) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) bufA[g * QA_D + 4 * lane + i] = acc[g][i];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    if (nsplit == 1) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const size_t ob = ((size_t)row * q_heads + (size_t)kvh * G + g) * QA_D + 4 * lane;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float s = acc[g][i] + bufA[g * QA_D + 4 * lane + i];
+                float o = l[g] > 0.0f ? s / l[g] : 0.0f;
+                if (gate) o *= 1.0f / (1.0f + expf(-gate[ob + i]));
+                out[ob + i] = o;
+            }
+        }
+    } else {
+        float *pr = part + (size_t)blockIdx.x * G * (QA_D + 2);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            if (lane == 0) { pr[g] = m[g]; pr[G + g] = l[g]; }
+#pragma unroll
+            for (int i = 0; i < 4; i++) pr[2 * G + g * QA_D + 4 * lane + i] = acc[g][i] + bufA[g * QA_D + 4 * lane + i];
+        }
+    }
+}
+
+// The splits of one (row, kv head, head), combined in split order: their
+// maxima and sums go to LDS first, then thread t adds dim t of every split's
+// output with all its loads in flight at once.
+#define QA_MAX_SPLITS 128
+
+template <int G>
+__global__ void __launch_bounds__(256) k_attn_merge(float *__restrict__ out, const float *__restrict__ gate,
+                                                    const float *__restrict__ part, int q_heads, int kv_heads,
+                                                    int nsplit)
+{
+    __shared__ float sm[QA_MAX_SPLITS], sl[QA_MAX_SPLITS], sf[QA_MAX_SPLITS];
+    __shared__ float sL;
+    const int g = blockIdx.x % G, rk = blockIdx.x / G, row = rk / kv_heads, kvh = rk % kv_heads, t = threadIdx.x;
+    const size_t stride = (size_t)G * (QA_D + 2);
+    const float *pr = part + (size_t)rk * nsplit * stride;
+    if (t < nsplit) {
+        sm[t] = pr[t * stride + g];
+        sl[t] = pr[t * stride + G + g];
+    }
+    __syncthreads();
+    if (t == 0) {
+        float M = -FLT_MAX;
+        for (int s = 0; s < nsplit; s++) M = fmaxf(M, sm[s]);
+        float L = 0.0f;
+        for (int s = 0; s < nsplit; s++) {
+            sf[s] = expf(sm[s] - M);
+            L = __builtin_fmaf(sl[s], sf[s], L);
+        }
+        sL = L;
+    }
+    __syncthreads();
+    float a[QA_MAX_SPLITS];
+#pragma unroll
+    for (int s = 0; s < QA_MAX_SPLITS; s++)
+        if (s < nsplit) a[s] = pr[s * stride + 2 * G + (size_t)g * QA_D + t];
+    float A = 0.0f;
+#pragma unroll
+    for (int s = 0; s < QA_MAX_SPLITS; s++)
+        if (s < nsplit) A = __builtin_fmaf(a[s], sf[s], A);
+    const float L = sL;
+    const size_t oi = ((size_t)row * q_heads + (size_t)kvh * G + g) * QA_D + t;
+    float o = L > 0.0f ? A / L : 0.0f;
+    if (gate) o *= 1.0f / (1.0f + expf(-gate[oi]));
+    out[oi] = o;
 }
 
 // ---- launchers ----------------------------------------------------------------------
@@ -550,18 +687,52 @@ extern "C" int qwk_qsa_select(hipStream_t s, uint8_t *mask, uint32_t *list, cons
     return (int)hipGetLastError();
 }
 
+// Splits of the position list per (row, kv head): enough workgroups to
+// cover the chip when rows * kv_heads alone would not, each split at least
+// one pass of QA_P positions.
+static int qa_splits(int rows, int kv_heads, int cap)
+{
+    const int rk = rows * kv_heads, passes = (cap + QA_P - 1) / QA_P;
+    if (rk >= 256 || passes <= 1) return 1;
+    return max(1, min(min(passes, QA_MAX_SPLITS), (512 + rk - 1) / rk));
+}
+
+extern "C" size_t qwk_attn_masked_work_bytes(int rows, int q_heads, int kv_heads, int cap)
+{
+    if (kv_heads < 1 || rows < 1) return 0;
+    const int ns = qa_splits(rows, kv_heads, cap);
+    if (ns == 1) return 0;
+    return (size_t)rows * kv_heads * ns * (q_heads / kv_heads) * (QA_D + 2) * sizeof(float);
+}
+
+template <int G>
+static void qa_launch(hipStream_t s, float *out, const float *gate, const float *q, const uint16_t *kc,
+                      const uint16_t *vc, const uint32_t *list, int rows, int q_heads, int kv_heads, int max_ctx,
+                      float scale, int cap, int ns, float *part)
+{
+    hipLaunchKernelGGL(k_attn_masked<G>, dim3(rows * kv_heads * ns), dim3(256), 0, s, out, gate, q, kc, vc, list,
+                       q_heads, kv_heads, max_ctx, scale, cap, ns, part);
+    if (ns > 1)
+        hipLaunchKernelGGL(k_attn_merge<G>, dim3(rows * kv_heads * G), dim3(256), 0, s, out, gate, part, q_heads,
+                           kv_heads, ns);
+}
+
 extern "C" int qwk_attn_masked(hipStream_t s, float *out, const float *gate, const float *q, const uint16_t *kc,
                                const uint16_t *vc, const uint32_t *list, int rows, int q_heads, int kv_heads,
-                               int head_dim, int max_ctx, float scale, int cap)
+                               int head_dim, int max_ctx, float scale, int cap, void *work, size_t work_bytes)
 {
     if (head_dim != QA_D || kv_heads < 1 || q_heads % kv_heads || rows < 0 || cap < 0) return hipErrorInvalidValue;
     if (rows == 0) return 0;
-    const dim3 grid(rows * kv_heads);
+    int ns = qa_splits(rows, kv_heads, cap);
+    if (ns > 1 && (!work || work_bytes < qwk_attn_masked_work_bytes(rows, q_heads, kv_heads, cap))) ns = 1;
+    float *part = (float *)work;
     switch (q_heads / kv_heads) {
-    case 1: hipLaunchKernelGGL(k_attn_masked<1>, grid, dim3(256), 0, s, out, gate, q, kc, vc, list, q_heads, kv_heads, max_ctx, scale, cap); break;
-    case 2: hipLaunchKernelGGL(k_attn_masked<2>, grid, dim3(256), 0, s, out, gate, q, kc, vc, list, q_heads, kv_heads, max_ctx, scale, cap); break;
-    case 4: hipLaunchKernelGGL(k_attn_masked<4>, grid, dim3(256), 0, s, out, gate, q, kc, vc, list, q_heads, kv_heads, max_ctx, scale, cap); break;
-    case 8: hipLaunchKernelGGL(k_attn_masked<8>, grid, dim3(256), 0, s, out, gate, q, kc, vc, list, q_heads, kv_heads, max_ctx, scale, cap); break;
+    case 1: qa_launch<1>(s, out, gate, q, kc, vc, list, rows, q_heads, kv_heads, max_ctx, scale, cap, ns, part); break;
+    case 2: qa_launch<2>(s, out, gate, q, kc, vc, list, rows, q_heads, kv_heads, max_ctx, scale, cap, ns, part); break;
+    case 4: qa_launch<4>(s, out, gate, q, kc, vc, list, rows, q_heads, kv_heads, max_ctx, scale, cap, ns, part); break;
+    case 8: qa_launch<8>(s, out, gate, q, kc, vc, list, rows, q_heads, kv_heads, max_ctx, scale, cap, ns, part); break;
+    case 12: qa_launch<12>(s, out, gate, q, kc, vc, list, rows, q_heads, kv_heads, max_ctx, scale, cap, ns, part); break;
+    case 16: qa_launch<16>(s, out, gate, q, kc, vc, list, rows, q_heads, kv_heads, max_ctx, scale, cap, ns, part); break;
     default: return hipErrorInvalidValue;
     }
     return (int)hipGetLastError();

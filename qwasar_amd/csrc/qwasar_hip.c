@@ -1122,9 +1122,12 @@ void qw_op_attn_masked_gated(qw_cmd c, qw_ref out, qw_ref gate, qw_ref q, qw_ref
     QW_OP(c);
     touch(c, q, 0); touch(c, kcache, 0); touch(c, vcache, 0); touch(c, list, 0); touch(c, gate, 0);
     touch(c, out, 1);
+    const int32_t cap = qw_qsa_list_cap(block_topk, ratio);
+    const size_t wb = kv_heads > 0 && rows > 0 ? qwk_attn_masked_work_bytes(rows, q_heads, kv_heads, cap) : 0;
+    void *work = wb ? scratch(wb) : NULL;
     launched(c, "attn_masked", qwk_attn_masked(G.stream, dp(out), dp(gate), dp(q), dp(kcache), dp(vcache), dp(list),
-                                               rows, q_heads, kv_heads, head_dim, max_ctx, scale,
-                                               qw_qsa_list_cap(block_topk, ratio)));
+                                               rows, q_heads, kv_heads, head_dim, max_ctx, scale, cap, work,
+                                               work ? wb : 0));
 }
 
 void qw_op_attn_masked(qw_cmd c, qw_ref out, qw_ref q, qw_ref kcache, qw_ref vcache, qw_ref list, int32_t rows,

@@ -188,10 +188,10 @@ def attn_case(gpu, rows, qh, kvh, base, topk, ratio, seed, gated=False):
     assert np.abs(got - want).max() < 2e-6, f"max |diff| {np.abs(got - want).max():.3g}"
 
 
-@pytest.mark.parametrize("qh,kvh", [(4, 1), (1, 1), (4, 2), (8, 1)])
+@pytest.mark.parametrize("qh,kvh", [(4, 1), (1, 1), (4, 2), (8, 1), (24, 2), (16, 1)])
 def test_attn_masked_small(gpu, qh, kvh):
-    """The toy model's heads (4 query, 1 kv) and the other supported ratios,
-    5 rows at position 13 with a budget of 2 blocks."""
+    """The toy model's heads (4 query, 1 kv), the full model's (24, 2) and the
+    other supported ratios, 5 rows at position 13 with a budget of 2 blocks."""
     attn_case(gpu, 5, qh, kvh, 13, 2, 4, 71 + qh + kvh)
 
 
