@@ -510,7 +510,7 @@ __device__ __forceinline__ void qd_stage_x(uint4 *xs, const QdArgs &a, const flo
     }
 }
 
-template <int LPR, int NUL>
+template <int LPR, int NUL, bool PLAINX = false>
 __device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, int n, const QdArgs &a,
                                              int row0, int nt, bool staged, uint4 *xs, const int *vin,
                                              const int *vout, uint4 *dst, float (*ys)[QD_GU_MAXRPB])
@@ -598,7 +598,9 @@ __device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, i
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const int i = min(i0 + (int)threadIdx.x + r * QD_THREADS, tn * per - 1);
-                    v[r] = qw_ld4_coh(a.qx, (uint32_t)((vin[t0 + i / per] * per + i % per) * 16));
+                    const uint32_t off = (uint32_t)((vin[t0 + i / per] * per + i % per) * 16);
+                    // PLAINX: the rows were staged by an earlier launch, so cached loads see them
+                    v[r] = PLAINX ? a.qx[off / 16] : qw_ld4_coh(a.qx, off);
                 }
 #pragma unroll
                 for (int r = 0; r < 4; r++) asm volatile("" : "+v"(v[r].x), "+v"(v[r].y), "+v"(v[r].z), "+v"(v[r].w));
@@ -1155,6 +1157,362 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     } else
     QD_SHAPES(QD_GO)
 #undef QD_GO
+    return (int)hipErrorInvalidValue;
+    return (int)hipGetLastError();
+}
+
+// ---- decode of 2..8 tokens: four launches over the batch's unique experts --------
+//
+// With several tokens the one-launch path above routes every token in every
+// experts and down workgroup and needs more workgroups than fit at once;
+// measured at 8 tokens (config 2) it spent ~16 us routing in each of ~4000
+// workgroups.  Here each step is its own launch, so nothing waits on another
+// workgroup and the grid size is free:
+//
+//   router     order-R logits of every token
+//   (k_dmat_few in qw_route.hip, with the shared expert's gate logits in
+//              the same launch)
+//   k_batch_route   one workgroup: every token routed (a wave each, the
+//              standalone route's arithmetic), the table of unique experts
+//              (ascending, each with its pairs in ascending order), and the
+//              token rows staged as q16 units
+//   k_batch_gu      per (unique expert, 16-row block), and the shared
+//              expert's blocks: the weight rows read once for every token
+//              routed there (requested before the staged rows are copied into
+//              LDS); SwiGLU fused; the activations leave as q16 units
+//   k_batch_down    per (token, 16 output rows): the down rows of the shared
+//              expert and the token's K experts, each applied to its
+//              activation vector, then the combine in slot order (the
+//              fused path's).  A row block's workgroups for all tokens sit on
+//              one XCD (block index = rb mod 8 there), so an expert several
+//              tokens share is read from that XCD's L2 after the first.
+
+#define QB_TAB_U 0
+#define QB_TAB_UEXP 1
+#define QB_TAB_UCNT (1 + QD_MAXU)
+#define QB_TAB_USTART (1 + 2 * QD_MAXU)
+#define QB_TAB_UPAIR (1 + 3 * QD_MAXU)
+#define QB_TAB_GATE (1 + 4 * QD_MAXU)
+#define QB_TAB_INTS (1 + 4 * QD_MAXU + QD_MAXT)
+
+struct QbLayout {
+    size_t logits, tab, qx, qact, qsh, total;
+};
+
+static QbLayout qb_layout(const qwk_moe *M, int rows)
+{
+    QbLayout L;
+    size_t o = 0;
+    L.logits = o; o += al((size_t)rows * M->E * 4);
+    L.qx = o;     o += al((size_t)rows * (M->H / 16) * QW_Q16_BYTES);
+    L.tab = o;    o += al((size_t)QB_TAB_INTS * 4);
+    L.qact = o;   o += al((size_t)rows * M->K * (M->I / 16) * QW_Q16_BYTES);
+    L.qsh = o;    o += al((size_t)rows * (M->SI / 16) * QW_Q16_BYTES);
+    L.total = o;
+    return L;
+}
+
+struct QbArgs {
+    QdArgs d;                 // shapes, x, out, idx, w, rows, lgG, tch, qact, qsh
+    const float *logits;
+    int32_t *tab;
+};
+
+template <int PL>
+__global__ __launch_bounds__(QD_MAXT * 64) void k_batch_route(QbArgs b)
+{
+    __shared__ QdRoute R;
+    const QdArgs &a = b.d;
+    const int t = threadIdx.x, nthr = blockDim.x, wave = t >> 6, lane = t & 63;
+    const int E = a.m.E, K = a.m.K, H = a.m.H;
+    if (wave < a.rows) {
+        int pi;
+        float pw;
+        qw_route_wave<PL>(b.logits + (size_t)wave * E, E, K, a.m.norm, lane, &pi, &pw, R.rs.sx[wave]);
+        if (lane < K) {
+            R.picks[wave * K + lane] = pi;
+            R.pw[wave * K + lane] = pw;
+            a.idx[wave * K + lane] = pi;
+            a.w[wave * K + lane] = pw;
+        }
+    }
+    // the token rows as q16 units for the gate / up launch
+    const int units = H / 16;
+    for (int i = t; i < a.rows * units; i += nthr) {
+        float v[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 f = reinterpret_cast<const float4 *>(a.x + (size_t)i * 16)[q];
+            v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+        }
+        uint4 u[3];
+        qw_q16_make(v, u);
+        a.qx[(size_t)i * 3] = u[0];
+        a.qx[(size_t)i * 3 + 1] = u[1];
+        a.qx[(size_t)i * 3 + 2] = u[2];
+    }
+    __syncthreads();
+    // The union of the picks, ascending, with each expert's pairs in
+    // ascending order, in parallel steps: per token a bitmask of its picks;
+    // the marked experts compacted by ballots; counts by LDS atomics; the
+    // starts by one wave's scan; a pair's place in its expert's run is the
+    // number of earlier tokens that picked the same expert (a token's picks
+    // are distinct, so pairs of one expert are ordered by token).
+    __shared__ uint32_t tmask[QD_MAXT][QWK_ROUTE_MAX_E / 32];
+    __shared__ int cnt[QWK_ROUTE_MAX_E];
+    const int npk = a.rows * K, nwd = (E + 31) / 32;
+    for (int i = t; i < QD_MAXT * (QWK_ROUTE_MAX_E / 32); i += nthr) (&tmask[0][0])[i] = 0u;
+    for (int e = t; e < E; e += nthr) { R.mark[e] = 0; cnt[e] = 0; }
+    __syncthreads();
+    for (int p = t; p < npk; p += nthr) {
+        const int e = R.picks[p];
+        R.mark[e] = 1;
+        atomicOr(&tmask[p / K][e >> 5], 1u << (e & 31));
+        atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int base = 0;
+        for (int e0 = 0; e0 < E; e0 += 64) {
+            const int e = e0 + lane;
+            const bool on = e < E && R.mark[e];
+            const unsigned long long bal = __ballot(on);
+            if (on) {
+                const int u = base + __popcll(bal & ((1ull << lane) - 1ull));
+                R.uexp[u] = e;
+                R.mark[e] = u;              // from here on: the expert's slot
+            }
+            base += __popcll(bal);
+        }
+        // starts: lane l scans slots 2l and 2l + 1 (U <= QD_MAXU <= 128)
+        const int u0 = 2 * lane, u1 = 2 * lane + 1;
+        const int c0 = u0 < base ? cnt[R.uexp[u0]] : 0, c1 = u1 < base ? cnt[R.uexp[u1]] : 0;
+        int incl = c0 + c1;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        const int excl = incl - c0 - c1;
+        if (u0 < base) { R.ucnt[u0] = c0; R.ustart[u0] = excl; }
+        if (u1 < base) { R.ucnt[u1] = c1; R.ustart[u1] = excl + c0; }
+        if (lane == 0) R.U = base;
+    }
+    __syncthreads();
+    for (int p = t; p < npk; p += nthr) {
+        const int e = R.picks[p], tk = p / K;
+        int rank = 0;
+        for (int q = 0; q < tk; q++) rank += (tmask[q][e >> 5] >> (e & 31)) & 1u;
+        R.upair[R.ustart[R.mark[e]] + rank] = p;
+    }
+    __syncthreads();
+    if (t == 0) b.tab[QB_TAB_U] = R.U;
+    for (int u = t; u < R.U; u += nthr) {
+        b.tab[QB_TAB_UEXP + u] = R.uexp[u];
+        b.tab[QB_TAB_UCNT + u] = R.ucnt[u];
+        b.tab[QB_TAB_USTART + u] = R.ustart[u];
+    }
+    for (int p = t; p < npk; p += nthr) b.tab[QB_TAB_UPAIR + p] = R.upair[p];
+    (void)nwd;
+}
+
+template <int LPR, int NUL>
+__global__ __launch_bounds__(QD_THREADS, 8) void k_batch_gu(QbArgs b)
+{
+    extern __shared__ uint4 xs[];                    // [tch][units][3]
+    __shared__ int vin[QD_MAXT], vout[QD_MAXT];
+    __shared__ float ys[QD_MAXT][QD_GU_MAXRPB];
+    const QdArgs &a = b.d;
+    constexpr int RPB = QD_WAVES * (64 / LPR);
+    const int H = a.m.H, I = a.m.I, K = a.m.K;
+    const int bb = blockIdx.x;
+    QD_TS(0);
+    if (bb < a.n_ex) {
+        const int u = bb / a.gu_wg_per_u, rb = bb % a.gu_wg_per_u;
+        if (u >= b.tab[QB_TAB_U]) return;                              // uniform
+        const int e = b.tab[QB_TAB_UEXP + u], nt = b.tab[QB_TAB_UCNT + u], p0 = b.tab[QB_TAB_USTART + u];
+        if (threadIdx.x < nt) {
+            const int p = b.tab[QB_TAB_UPAIR + p0 + threadIdx.x];
+            vin[threadIdx.x] = p / K;
+            vout[threadIdx.x] = p;
+        }
+        __syncthreads();
+        const size_t words = H / 8, groups = H >> a.lgG;
+        qwk_q4 gm, um;
+        if (a.m.split) {
+            const size_t off = (size_t)e * I;
+            gm = {a.m.gate.w + off * words, a.m.gate.s + off * groups, a.m.gate.b + off * groups};
+            um = {a.m.up.w + off * words, a.m.up.s + off * groups, a.m.up.b + off * groups};
+        } else {
+            const size_t off = (size_t)e * 2 * I;
+            gm = {a.m.gate_up.w + off * words, a.m.gate_up.s + off * groups, a.m.gate_up.b + off * groups};
+            um = {gm.w + (size_t)I * words, gm.s + (size_t)I * groups, gm.b + (size_t)I * groups};
+        }
+        // the weights are requested first; the token rows follow from the
+        // staged copy, pass by pass
+        qd_glu_block<LPR, NUL, true>(gm, um, I, a, rb * RPB, nt, false, xs, vin, vout, a.qact, ys);
+        QD_TS(5);
+    } else {
+        const int sb = bb - a.n_ex;
+        if (threadIdx.x < QD_MAXT) vin[threadIdx.x] = vout[threadIdx.x] = threadIdx.x;
+        __syncthreads();
+        qd_glu_block<LPR, NUL, true>(a.m.sh_gate, a.m.sh_up, a.m.SI, a, sb * RPB, a.rows, false, xs, vin, vout,
+                                     a.qsh, ys);
+    }
+}
+
+template <int NUL>
+__global__ __launch_bounds__(QD_THREADS, 8) void k_batch_down(QbArgs b)
+{
+    extern __shared__ uint4 xa[];                    // the K + 1 activation vectors
+    __shared__ float ys[QWK_DECODE_MAX_K + 1][QD_DOWN_RPG];
+    const QdArgs &a = b.d;
+    constexpr int LPR = QD_DOWN_LPR, RPP = 64 / LPR, RIT = QD_DOWN_RIT, RPG = QD_DOWN_RPG;
+    const int H = a.m.H, I = a.m.I, SI = a.m.SI, K = a.m.K;
+    // block -> (token, row block): all tokens of row block rb on XCD rb mod 8
+    const int q = blockIdx.x >> 3, xcd = blockIdx.x & 7;
+    const int t = q % a.rows, rb = (q / a.rows) * 8 + xcd;
+    if (rb >= a.n_down_rb) return;                   // uniform
+    const int lane = threadIdx.x & 63, m = threadIdx.x >> 6;
+    const int slot = lane / LPR, lr = lane % LPR;
+    const int row0 = rb * RPG, lgG = a.lgG;
+    const bool busy = m <= K;
+    const int kin = m == 0 ? SI : I;
+    const int units = kin / 16, words = kin / 8, groups = kin >> lgG;
+    const uint32_t *wm = a.m.sh_down.w;
+    const uint16_t *sm = a.m.sh_down.s, *bm = a.m.sh_down.b;
+    if (busy && m > 0) {
+        const size_t e = (size_t)a.idx[t * K + m - 1];
+        wm = a.m.down.w + e * H * words;
+        sm = a.m.down.s + e * H * groups;
+        bm = a.m.down.b + e * H * groups;
+    }
+    uint2 wv[NUL][RIT];
+    uint32_t sv[NUL][RIT], bv[NUL][RIT];
+#pragma unroll
+    for (int j = 0; j < NUL; j++) {
+        const int c = min(j * LPR + lr, units - 1);
+        const int g = (16 * c) >> lgG;
+#pragma unroll
+        for (int i = 0; i < RIT; i++) {
+            const int row = min(row0 + slot + RPP * i, H - 1);
+            wv[j][i] = qw_ld2(wm, (uint32_t)(row * words + 2 * c) * 4u);
+            sv[j][i] = qw_ldu16(sm, (uint32_t)(row * groups + g) * 2u);
+            bv[j][i] = qw_ldu16(bm, (uint32_t)(row * groups + g) * 2u);
+        }
+    }
+    // this matrix's activation vector into the wave's own LDS region
+    const int nv = units * 3;
+    constexpr int XW = (3 * NUL * LPR + 63) / 64;
+    uint4 *xw = xa + (m == 0 ? 0 : (SI / 16) * 3 + (m - 1) * ((I / 16) * 3));
+    if (busy) {
+        const uint4 *xm = m == 0 ? a.qsh + (size_t)t * ((SI / 16) * 3)
+                                 : a.qact + ((size_t)t * K + (m - 1)) * ((I / 16) * 3);
+        uint4 v[XW];
+#pragma unroll
+        for (int r = 0; r < XW; r++) v[r] = xm[min(lane + 64 * r, nv - 1)];
+#pragma unroll
+        for (int r = 0; r < XW; r++)
+            if (lane + 64 * r < nv) xw[lane + 64 * r] = v[r];
+    }
+    const float gate = qw_sigmoid(__int_as_float(b.tab[QB_TAB_GATE + t]));
+    if (busy) {
+        uint32_t sb[NUL][RIT];
+#pragma unroll
+        for (int j = 0; j < NUL; j++)
+#pragma unroll
+            for (int i = 0; i < RIT; i++) {
+                const bool ok = j * LPR + lr < units && row0 + slot + RPP * i < H;
+                wv[j][i] = ok ? wv[j][i] : make_uint2(0, 0);
+                sb[j][i] = ok ? sv[j][i] | (bv[j][i] << 16) : 0u;
+            }
+        float y[RIT];
+#pragma unroll
+        for (int i = 0; i < RIT; i++) y[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NUL; j++) {
+            const int c = j * LPR + lr;
+            if (c < units) {
+                const uint4 p0 = xw[3 * c], p1 = xw[3 * c + 1], rr = xw[3 * c + 2];
+                const float4 r = *reinterpret_cast<const float4 *>(&rr);
+#pragma unroll
+                for (int i = 0; i < RIT; i++)
+                    y[i] = qw_unit_dot(wv[j][i], p0, p1, r, __uint_as_float(sb[j][i] << 16),
+                                       __uint_as_float(sb[j][i] & 0xFFFF0000u), y[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RIT; i++) {
+            const float v = qw_xor_sum<LPR>(y[i]);
+            if (lr == 0) ys[m][slot + RPP * i] = v;
+        }
+    }
+    __syncthreads();
+    // the combine: the shared term first, then an fma per slot, in order
+    for (int r = threadIdx.x; r < RPG; r += blockDim.x) {
+        const int row = row0 + r;
+        if (row >= H) continue;
+        float acc = ys[0][r] * gate;
+        for (int k = 0; k < K; k++) acc = __builtin_fmaf(a.w[t * K + k], ys[1 + k][r], acc);
+        a.out[(size_t)t * H + row] = acc;
+    }
+}
+
+extern "C" size_t qwk_moe_decode_batch_scratch(const qwk_moe *M, int rows)
+{
+    return qb_layout(M, rows).total;
+}
+
+extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
+                                    const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes)
+{
+    const int G = M->group;
+    if (rows < 2 || !qwk_moe_decode_supported(M, rows) || !x || ((uintptr_t)x & 15u)) return (int)hipErrorInvalidValue;
+    const QbLayout L = qb_layout(M, rows);
+    if (scratch_bytes < L.total) return (int)hipErrorInvalidValue;
+    int lpr_h, nul_h, nul_d, pl;
+    qd_shapes(M, &lpr_h, &nul_h, &nul_d, &pl);
+    char *S = (char *)scratch;
+    QbArgs b;
+    QdArgs &a = b.d;
+    a = QdArgs{};
+    a.m = *M;
+    a.x = x; a.out = out; a.idx = idx; a.w = w; a.rows = rows;
+    a.umax = rows * M->K < M->E ? rows * M->K : M->E;
+    a.lgG = G == 32 ? 5 : G == 64 ? 6 : 7;
+    const int rpb = QD_WAVES * (64 / lpr_h);
+    const int vbytes = (M->H / 16) * QW_Q16_BYTES;
+    a.tch = QD_LDS / vbytes < rows ? QD_LDS / vbytes : rows;
+    a.n_sh = (M->SI + rpb - 1) / rpb;
+    a.gu_wg_per_u = (M->I + rpb - 1) / rpb;
+    a.n_ex = a.umax * a.gu_wg_per_u;
+    a.n_down_rb = (M->H + QD_DOWN_RPG - 1) / QD_DOWN_RPG;
+    a.scr = S;
+    a.qx = (uint4 *)(S + L.qx);
+    a.qact = (uint4 *)(S + L.qact);
+    a.qsh = (uint4 *)(S + L.qsh);
+    b.logits = (const float *)(S + L.logits);
+    b.tab = (int32_t *)(S + L.tab);
+    const size_t xs_bytes = (size_t)a.tch * vbytes;
+    const size_t xa_bytes = ((size_t)(M->SI / 16) + (size_t)M->K * (M->I / 16)) * QW_Q16_BYTES;
+    if (a.tch < 1 || xa_bytes > QD_LDS || a.umax > QD_MAXU) return (int)hipErrorInvalidValue;
+    // the router logits and the shared expert's gate logits, one launch
+    float *lg = (float *)(S + L.logits), *gl = (float *)(b.tab + QB_TAB_GATE);
+    int rc = qwk_dmat_bf16_gate(s, lg, gl, x, M->router, M->sh_gate_w, M->H, M->E, rows);
+    if (rc == (int)hipErrorInvalidValue) {   // a layout the one launch does not take: two order-R launches
+        rc = qwk_dmat_bf16(s, lg, x, M->router, M->H, M->E, rows);
+        if (!rc) rc = qwk_dmat_bf16(s, gl, x, M->sh_gate_w, M->H, 1, rows);
+    }
+    if (rc) return rc;
+    const int nrb8 = (a.n_down_rb + 7) / 8 * 8;
+#define QB_GO(L_, N_, D_, P_)                                                                                   \
+    if (lpr_h == L_ && nul_h == N_ && nul_d == D_ && pl == P_) {                                              \
+        hipLaunchKernelGGL(k_batch_route<P_>, dim3(1), dim3(QD_MAXT * 64), 0, s, b);                          \
+        hipLaunchKernelGGL((k_batch_gu<L_, N_>), dim3(a.n_ex + a.n_sh), dim3(QD_THREADS), xs_bytes, s, b);    \
+        hipLaunchKernelGGL(k_batch_down<D_>, dim3(rows * nrb8), dim3(QD_THREADS), xa_bytes, s, b);            \
+    } else
+    QD_SHAPES(QB_GO)
+#undef QB_GO
     return (int)hipErrorInvalidValue;
     return (int)hipGetLastError();
 }

@@ -25,6 +25,12 @@ typedef struct { const uint32_t *w; const uint16_t *s; const uint16_t *b; } qwk_
 int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint16_t *w,
                   int k, int n, int rows);
 
+/* The same for up to 8 token rows (k % 64 == 0, k <= 4096, 16-byte aligned),
+ * with, when w2 is given, one more output: g[r] = order-R dot of w2 [k] with
+ * x row r, in the same launch. */
+int qwk_dmat_bf16_gate(hipStream_t s, float *y, float *g, const float *x, const uint16_t *w,
+                       const uint16_t *w2, int k, int n, int rows);
+
 /* Softmax, top-K, renormalise: idx/w [rows, K]. */
 int qwk_route(hipStream_t s, int32_t *idx, float *w, const float *logits,
               int rows, int E, int K, int norm);
@@ -157,6 +163,14 @@ typedef struct {
 int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
                    const qwk_resid *res, const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes,
                    void *sync, uint32_t epoch, hipEvent_t *ev);
+/* Decode of 2..QWK_DECODE_MAX_ROWS tokens over the batch's unique experts,
+ * in four launches with no cross-workgroup waits (router logits, routing and
+ * the unique-expert table, gate/up per unique expert, down and combine per
+ * token).  Same shapes as qwk_moe_decode; scratch of
+ * qwk_moe_decode_batch_scratch bytes, nothing in it initialised. */
+size_t qwk_moe_decode_batch_scratch(const qwk_moe *M, int rows);
+int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
+                         const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes);
 
 /* RMS norm of [rows, dim] fp32 rows (dim % 4 == 0), optional bf16 weight:
  * y = x / sqrt(mean(x^2) + eps) * out_scale (* w). */

@@ -273,6 +273,117 @@ __global__ __launch_bounds__(QW_DW_THREADS) void k_dmat_wide(float *__restrict__
     }
 }
 
+// A few token rows (<= 8) against many outputs (decode batches): a wave per
+// output, lane c the order-R chain of chunk c for every row.  The token rows
+// sit in LDS (chunk c of row r at (r nch + c) * QW_DF_PAD floats: the pad puts
+// neighbouring lanes' float4 reads 4 banks apart); the lane's 64 weights are
+// requested at once, before any is used.  Lane r then adds row r's chunk
+// partials left to right.  Output o == n, when w2 is given, is the dot with
+// the single row w2 into g[r] (the shared expert's gate, in the same launch).
+#define QW_DF_WAVES 8
+#define QW_DF_MAXR 8
+#define QW_DF_PAD 68
+__global__ __launch_bounds__(QW_DF_WAVES * 64) void k_dmat_few(float *__restrict__ y, float *__restrict__ g,
+                                                               const float *__restrict__ x,
+                                                               const uint16_t *__restrict__ w,
+                                                               const uint16_t *__restrict__ w2, int k, int n,
+                                                               int rows)
+{
+    extern __shared__ float xl[];                    // [rows][nch][QW_DF_PAD]
+    __shared__ float part[QW_DF_WAVES][QW_DF_MAXR][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nch = k / 64, o = blockIdx.x * QW_DF_WAVES + wave;
+    const bool has = o < n || (o == n && w2);
+    const uint16_t *wr = o < n ? w + (size_t)o * k : w2;
+    uint4 wv[8];
+    if (has && lane < nch) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(wr + 64 * lane);
+#pragma unroll
+        for (int q = 0; q < 8; q++) wv[q] = src[q];
+    }
+    // the token rows into LDS, eight float4 a thread in flight at a time
+    const int n4 = rows * (k / 4);
+    for (int i0 = 0; i0 < n4; i0 += 8 * QW_DF_WAVES * 64) {
+        float4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int i = min(i0 + j * QW_DF_WAVES * 64 + (int)threadIdx.x, n4 - 1);
+            v[j] = reinterpret_cast<const float4 *>(x)[(size_t)(i / (k / 4)) * (k / 4) + i % (k / 4)];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int i = i0 + j * QW_DF_WAVES * 64 + (int)threadIdx.x;
+            if (i < n4) {
+                const int r = i / (k / 4), c4 = i % (k / 4);
+                *reinterpret_cast<float4 *>(xl + ((size_t)r * nch + c4 / 16) * QW_DF_PAD + (c4 % 16) * 4) = v[j];
+            }
+        }
+    }
+    __syncthreads();
+    if (!has) return;
+    if (lane < nch) {
+#pragma unroll
+        for (int r = 0; r < QW_DF_MAXR; r++) {
+            if (r < rows) {
+                const float4 *xv = reinterpret_cast<const float4 *>(xl + ((size_t)r * nch + lane) * QW_DF_PAD);
+                float p = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const uint4 ww = wv[q];
+                    const float4 a = xv[2 * q], b = xv[2 * q + 1];
+                    p = __builtin_fmaf(__uint_as_float(ww.x << 16), a.x, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.x & 0xFFFF0000u), a.y, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.y << 16), a.z, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.y & 0xFFFF0000u), a.w, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.z << 16), b.x, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.z & 0xFFFF0000u), b.y, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.w << 16), b.z, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.w & 0xFFFF0000u), b.w, p);
+                }
+                part[wave][r][lane] = p;
+            }
+        }
+    }
+    // a wave's LDS accesses run in order: lane r reads what the wave wrote
+    if (lane < rows) {
+        float tot = part[wave][lane][0];
+        for (int c = 1; c < nch; c++) tot = tot + part[wave][lane][c];
+        if (o < n) y[(size_t)lane * n + o] = tot;
+        else g[lane] = tot;
+    }
+}
+
+static bool qw_few_ok(const float *x, const uint16_t *w, int k, int rows)
+{
+    return rows >= 1 && rows <= QW_DF_MAXR && k % 64 == 0 && k <= 64 * 64 && ((uintptr_t)w % 16) == 0 &&
+           ((uintptr_t)x % 16) == 0;
+}
+
+static int qw_launch_few(hipStream_t s, float *y, float *g, const float *x, const uint16_t *w, const uint16_t *w2,
+                         int k, int n, int rows)
+{
+    const size_t lds = (size_t)rows * (k / 64) * QW_DF_PAD * sizeof(float);
+    static bool attr = false;
+    if (!attr) {
+        attr = true;
+        // 8 rows of k = 4096: 139,264 bytes of token rows (with 16 KB of partials)
+        (void)hipFuncSetAttribute((const void *)k_dmat_few, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  QW_DF_MAXR * 64 * QW_DF_PAD * (int)sizeof(float));
+        (void)hipGetLastError();
+    }
+    const int outs = n + (w2 ? 1 : 0);
+    hipLaunchKernelGGL(k_dmat_few, dim3((outs + QW_DF_WAVES - 1) / QW_DF_WAVES), dim3(QW_DF_WAVES * 64), lds, s, y, g,
+                       x, w, w2, k, n, rows);
+    return (int)hipGetLastError();
+}
+
+extern "C" int qwk_dmat_bf16_gate(hipStream_t s, float *y, float *g, const float *x, const uint16_t *w,
+                                  const uint16_t *w2, int k, int n, int rows)
+{
+    if (n < 1 || !qw_few_ok(x, w, k, rows) || (w2 && ((uintptr_t)w2 % 16) != 0)) return (int)hipErrorInvalidValue;
+    return qw_launch_few(s, y, g, x, w, w2, k, n, rows);
+}
+
 extern "C" int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint16_t *w,
                              int k, int n, int rows)
 {
@@ -287,6 +398,7 @@ extern "C" int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint
                            dim3(QW_DROWS_WAVES * 64), 0, s, y, x, w, k, n, rows);
         return (int)hipGetLastError();
     }
+    if (vec && n >= 8 && qw_few_ok(x, w, k, rows)) return qw_launch_few(s, y, nullptr, x, w, nullptr, k, n, rows);
     if (vec && k % 64 == 0 && rows >= QW_DT) {
         hipLaunchKernelGGL(k_dmat_tiled, dim3((n + QW_DT - 1) / QW_DT, (rows + QW_DT - 1) / QW_DT), dim3(64), 0, s,
                            y, x, w, k, n, rows);

@@ -891,10 +891,30 @@ static void moe_desc(qwk_moe *mp, const qw_moe_layer *M) {
  * hand-off state are the backend's heap scratch (k = QW_DS_HEAP) or the
  * static device array (k = QW_DS_STATIC: nothing allocated; the caller has
  * checked that the staging fits). */
+/* Decode scratch: the one-launch path's (one token) or the batch path's. */
+static size_t decode_need(const qwk_moe *m, int32_t rows) {
+    return rows >= 2 ? qwk_moe_decode_batch_scratch(m, rows) : qwk_moe_decode_scratch(m, rows);
+}
+
 static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float *x,
                        const qwk_resid *res, const qwk_moe *mp, int32_t rows, int k) {
     const qwk_moe m = *mp;
-    const size_t need = qwk_moe_decode_scratch(&m, rows);
+    const size_t need = decode_need(&m, rows);
+    if (rows >= 2) {
+        /* several tokens: the batch path over their unique experts, after the
+         * residual step as its own pass when there is one */
+        void *S = k == QW_DS_STATIC ? (void *)G.static_stage : scratch(need);
+        const size_t have = k == QW_DS_STATIC ? G.static_stage_len : need;
+        if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", need); return false; }
+        int rc = 0;
+        if (res) {
+            rc = qwk_resid_rms_bf16(G.stream, res->h, res->h_out, res->x_out, res->y, m.H, rows, res->eps);
+            x = res->x_out;
+        }
+        if (!rc) rc = qwk_moe_decode_batch(G.stream, out, idx, w, x, &m, rows, S, have);
+        launched(c, k == QW_DS_STATIC ? "moe_layer_noalloc" : "moe_layer (decode batch)", rc);
+        return rc == 0;
+    }
     void *S = k == QW_DS_STATIC ? (void *)G.static_stage : scratch(need);
     const size_t have = k == QW_DS_STATIC ? G.static_stage_len : need;
     if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", need); return false; }
@@ -959,7 +979,7 @@ bool qw_op_moe_layer_noalloc(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref 
         fprintf(stderr, "qwasar: moe_layer_noalloc: the static device scratch is not set up (qw_gpu_init)\n");
         return false;
     }
-    const size_t need = qwk_moe_decode_scratch(&m, rows);
+    const size_t need = decode_need(&m, rows);
     if (need > G.static_stage_len) {
         fprintf(stderr, "qwasar: moe_layer_noalloc: %d rows of this layer stage %zu bytes, over the %zu the "
                 "static scratch holds\n", rows, need, G.static_stage_len);
