@@ -177,6 +177,121 @@ __global__ __launch_bounds__(64) void k_dmat_tiled(float *__restrict__ y, const 
     }
 }
 
+// The same order R on the fp32 matrix cores.  A K=1 MFMA,
+// v_mfma_f32_16x16x1f32, is four independent 16x16 outer products
+// D_b = C_b + a_b b_b^T, each element one fused multiply-add -- fmaf(a, b, c)
+// -- so a chunk's chain (from 0, k in index order) is 64 MFMAs on one
+// accumulator.  A workgroup owns 64 rows x 64 outputs; wave w owns rows
+// 16 w .. 16 w + 15 against all 64 outputs as the instruction's four blocks
+// (block b: outputs 16 b ..): lane l feeds block l / 16 with x[row l % 16][k]
+// and w[output l % 16][k].  The operands pass through LDS QW_DM_NC chunks at a
+// time (coalesced loads, the next stage requested while this one runs); a
+// wave runs the stage's chunk chains interleaved -- independent, so the
+// matrix pipe always has one ready -- and adds their partials to its running
+// total in chunk order (total = p_0, then total + p_c: the order above).
+// k % 64 == 0.
+typedef float qr_f16v __attribute__((ext_vector_type(16)));
+#define QW_DM_T 64
+#define QW_DM_NC 2                                 // chunks a stage (4 measured slower)
+#define QW_DM_KS (64 * QW_DM_NC + 4)               // floats a row of a stage (+ pad)
+__global__ __launch_bounds__(256) void k_dmat_mfma(float *__restrict__ y, const float *__restrict__ x,
+                                                   const uint16_t *__restrict__ w, int k, int n, int rows)
+{
+    extern __shared__ float4 dm_lds[];
+    float *xs = reinterpret_cast<float *>(dm_lds), *ws = xs + QW_DM_T * QW_DM_KS;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, blk = lane >> 4, i = lane & 15;
+    const int r0 = blockIdx.y * QW_DM_T, o0 = blockIdx.x * QW_DM_T;
+    const int nch = k / 64, rounds = (nch + QW_DM_NC - 1) / QW_DM_NC;
+    constexpr int SK = 64 * QW_DM_NC;                    // k a stage
+    constexpr int XF4 = QW_DM_T * SK / 4 / 256, WU4 = QW_DM_T * SK / 8 / 256;
+    // staging: x [64 rows][SK] as float4s, w [64 outputs][SK] bf16 as uint4s,
+    // consecutive threads along a row
+    float4 xr[XF4];
+    uint4 wr[WU4];
+    auto fetch = [&](int rd) {
+        const int k0 = SK * rd, kl = min(SK, k - k0);
+#pragma unroll
+        for (int j = 0; j < XF4; j++) {
+            const int q = t + 256 * j, row = q / (SK / 4), c4 = q % (SK / 4);
+            const int gr = min(r0 + row, rows - 1);
+            xr[j] = 4 * c4 < kl ? reinterpret_cast<const float4 *>(x + (size_t)gr * k + k0)[c4]
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < WU4; j++) {
+            const int q = t + 256 * j, o = q / (SK / 8), c8 = q % (SK / 8);
+            const int go = min(o0 + o, n - 1);
+            wr[j] = 8 * c8 < kl ? reinterpret_cast<const uint4 *>(w + (size_t)go * k + k0)[c8] : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int j = 0; j < XF4; j++) {
+            const int q = t + 256 * j, row = q / (SK / 4), c4 = q % (SK / 4);
+            *reinterpret_cast<float4 *>(xs + row * QW_DM_KS + 4 * c4) = xr[j];
+        }
+#pragma unroll
+        for (int j = 0; j < WU4; j++) {
+            const int q = t + 256 * j, o = q / (SK / 8), c8 = q % (SK / 8);
+            const uint32_t v[4] = {wr[j].x, wr[j].y, wr[j].z, wr[j].w};
+            float f[8];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                f[2 * e] = __uint_as_float(v[e] << 16);
+                f[2 * e + 1] = __uint_as_float(v[e] & 0xFFFF0000u);
+            }
+            float4 *d = reinterpret_cast<float4 *>(ws + o * QW_DM_KS + 8 * c8);
+            d[0] = make_float4(f[0], f[1], f[2], f[3]);
+            d[1] = make_float4(f[4], f[5], f[6], f[7]);
+        }
+    };
+    const qr_f16v zero = {};
+    qr_f16v tot = zero;
+    fetch(0);
+    const float *xa = xs + (16 * wave + i) * QW_DM_KS, *wa = ws + (16 * blk + i) * QW_DM_KS;
+    for (int rd = 0; rd < rounds; rd++) {
+        __syncthreads();                            // the previous stage is consumed
+        stash();
+        __syncthreads();
+        if (rd + 1 < rounds) fetch(rd + 1);
+        const int nc = min(QW_DM_NC, nch - QW_DM_NC * rd);
+        qr_f16v acc[QW_DM_NC];
+#pragma unroll
+        for (int c = 0; c < QW_DM_NC; c++) acc[c] = zero;
+#pragma unroll 2
+        for (int kk = 0; kk < 64; kk += 4) {
+            float4 av[QW_DM_NC], bv[QW_DM_NC];
+#pragma unroll
+            for (int c = 0; c < QW_DM_NC; c++) {
+                av[c] = *reinterpret_cast<const float4 *>(xa + 64 * c + kk);
+                bv[c] = *reinterpret_cast<const float4 *>(wa + 64 * c + kk);
+            }
+#pragma unroll
+            for (int c = 0; c < QW_DM_NC; c++) acc[c] = __builtin_amdgcn_mfma_f32_16x16x1f32(av[c].x, bv[c].x, acc[c], 0, 0, 0);
+#pragma unroll
+            for (int c = 0; c < QW_DM_NC; c++) acc[c] = __builtin_amdgcn_mfma_f32_16x16x1f32(av[c].y, bv[c].y, acc[c], 0, 0, 0);
+#pragma unroll
+            for (int c = 0; c < QW_DM_NC; c++) acc[c] = __builtin_amdgcn_mfma_f32_16x16x1f32(av[c].z, bv[c].z, acc[c], 0, 0, 0);
+#pragma unroll
+            for (int c = 0; c < QW_DM_NC; c++) acc[c] = __builtin_amdgcn_mfma_f32_16x16x1f32(av[c].w, bv[c].w, acc[c], 0, 0, 0);
+        }
+#pragma unroll
+        for (int c = 0; c < QW_DM_NC; c++)
+            if (c < nc) {
+#pragma unroll
+                for (int e = 0; e < 16; e++) tot[e] = rd == 0 && c == 0 ? acc[c][e] : tot[e] + acc[c][e];
+            }
+    }
+    // block b's values of this lane: rows 4 (lane / 16) + e of the wave's 16,
+    // output 16 b + lane % 16
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+        const int b = e >> 2;
+        const int row = r0 + 16 * wave + 4 * (lane >> 4) + (e & 3), o = o0 + 16 * b + (lane & 15);
+        if (row < rows && o < n) y[(size_t)row * n + o] = tot[e];
+    }
+}
+
 // A few outputs (the shared expert's gate, n = 1; the mixer's injection
 // logits, n = 4) over many token rows: one wave per row; lane c loads chunk c
 // of the row once and runs its fmaf chain for every output (c < 64 * 4), the
@@ -399,6 +514,18 @@ extern "C" int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint
         return (int)hipGetLastError();
     }
     if (vec && n >= 8 && qw_few_ok(x, w, k, rows)) return qw_launch_few(s, y, nullptr, x, w, nullptr, k, n, rows);
+    if (vec && k % 64 == 0 && rows >= QW_DT && n >= QW_DM_T) {
+        const int lds = 2 * QW_DM_T * QW_DM_KS * (int)sizeof(float);
+        static bool attr = false;
+        if (!attr) {
+            attr = true;
+            (void)hipFuncSetAttribute((const void *)k_dmat_mfma, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+            (void)hipGetLastError();
+        }
+        hipLaunchKernelGGL(k_dmat_mfma, dim3((n + QW_DM_T - 1) / QW_DM_T, (rows + QW_DM_T - 1) / QW_DM_T), dim3(256), lds,
+                           s, y, x, w, k, n, rows);
+        return (int)hipGetLastError();
+    }
     if (vec && k % 64 == 0 && rows >= QW_DT) {
         hipLaunchKernelGGL(k_dmat_tiled, dim3((n + QW_DT - 1) / QW_DT, (rows + QW_DT - 1) / QW_DT), dim3(64), 0, s,
                            y, x, w, k, n, rows);
