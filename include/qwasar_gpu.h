@@ -369,7 +369,7 @@ bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref
  * path for one token, the batch path for 2..8).  False, nothing encoded,
  * where qw_op_moe_layer would not take a decode path (past 8 rows, or shapes
  * the decode kernels do not take), or where the layer's staging at `rows`
- * exceeds what the array holds past its 82 KB hand-off state (245,504
+ * exceeds what the array holds past its 76 KB hand-off state (249,600
  * bytes: config 1's shape at 8 rows stages 227,328; H 4096 with K 15 at 8
  * rows, 313,344, is refused, at 5 rows, 196,608, taken).
  * Every call on one GPU shares the array and finds it as the last call

@@ -44,8 +44,9 @@
 #include <hip/hip_ext.h>
 
 #ifdef QD_TRACE
-extern __device__ unsigned long long qd_trace[8192 * 8];
-#define QW_STAMP(slot) do { if (threadIdx.x == 0) qd_trace[blockIdx.x * 8 + (slot)] = wall_clock64(); } while (0)
+extern __device__ unsigned long long qd_trace[8192 * 16];
+#define QW_STAMP(slot) do { if (threadIdx.x == 0) qd_trace[blockIdx.x * 16 + (slot)] = wall_clock64(); } while (0)
+#define QW_RSTAMP(slot) do { if (threadIdx.x == 0) qd_trace[blockIdx.x * 16 + 7 + (slot)] = wall_clock64(); } while (0)
 #endif
 #include "qw_device.h"
 #include "qw_kernels.h"
@@ -53,8 +54,8 @@ extern __device__ unsigned long long qd_trace[8192 * 8];
 // Built with -DQD_TRACE, every workgroup stamps the device wall clock
 // (100 MHz) at its phases into qd_trace[block][slot], for timelines.
 #ifdef QD_TRACE
-__device__ unsigned long long qd_trace[8192 * 8];
-#define QD_TS(slot) do { if (threadIdx.x == 0) qd_trace[blockIdx.x * 8 + (slot)] = wall_clock64(); } while (0)
+__device__ unsigned long long qd_trace[8192 * 16];
+#define QD_TS(slot) do { if (threadIdx.x == 0) qd_trace[blockIdx.x * 16 + (slot)] = wall_clock64(); } while (0)
 extern "C" int qd_trace_read(unsigned long long *dst)
 {
     return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(qd_trace), sizeof(qd_trace));
@@ -98,29 +99,30 @@ static int qd_nul(int units, int lpr)
 
 // ---- hand-off state (zeroed once by the host) -------------------------------------
 //
-// Producers (router, shared, experts workgroups) come in families: all router
-// workgroups, all shared ones, the experts workgroups of one selected expert.
-// A family is cut into groups of QD_GROUP consecutive workgroups; each group
-// has a counter and a flag.  A producer makes its device-coherent stores
-// visible, bumps its group's counter, and the group's last arriver resets the
-// counter and publishes the launch's epoch in the group's flag.  A consumer
-// polls the few flags of the groups it needs (one a lane, in one batch).
+// Every hand-off between workgroups is a tagged word: a 64-bit store of
+// {the launch's epoch, a 32-bit payload}, so a reader that sees this
+// launch's epoch sees the payload with it, and the producer needs no store
+// acknowledgement, counter or flag.  Words hold past epochs between launches;
+// an epoch is never reused before the state is zeroed.
+//
+//   lgt    the router's logits (and the shared expert's gate logit at E)
+//   rdone  router workgroup b's logits are all stored (its word b, payload
+//          unused), in QD_RDREP copies: a reader polls the copy of its XCD
+//          (blockIdx % 8), one wave, and then reads the logits once, rather
+//          than every wave of every workgroup polling the same 4 KB
+//   tact   the activation vectors the down rows read, as q16 units of 12
+//          dwords: vector 0 the shared expert's, 1 + k the k-th pick's
 
-#define QD_GROUP 16
-#define QD_NSYNC 2048
-
-#define QD_FL_RT 0           // router groups
-#define QD_FL_SH 64          // shared-expert groups
-#define QD_FL_EX 128         // experts: slot u, group h at QD_FL_EX + u * ngu + h
+#define QD_TU 32                  // q16 units a tagged activation vector holds (I, SI <= 512)
+#define QD_RDREP 8                // copies of the router's done words
+#define QD_RDSTRIDE 320           // words between copies (>= the router workgroups, (E + 4) / 4)
 
 struct QdSync {
-    uint32_t cnt[QD_NSYNC];
-    uint32_t flag[QD_NSYNC];
     uint32_t err;
-    uint32_t pad;
-    // the router's logits, row t at t * (E + 1), the shared gate's at E:
-    // {epoch, fp32 bits}, each written by one 64-bit store
-    uint2 lgt[QD_MAXT * (QWK_ROUTE_MAX_E + 1)];
+    uint32_t pad[3];
+    uint2 lgt[QWK_ROUTE_MAX_E + 1];
+    uint2 rdone[QD_RDREP * QD_RDSTRIDE];
+    uint2 tact[(QWK_DECODE_MAX_K + 1) * QD_TU * 12];
 };
 
 __device__ __forceinline__ void qd_stf(float *p, float v)
@@ -155,43 +157,6 @@ __device__ __forceinline__ void qd_raise(QdSync *S, uint32_t epoch)
     uint32_t expect = 0u;
     __hip_atomic_compare_exchange_strong(&S->err, &expect, epoch, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Member i of a producer family of n workgroups whose groups' counters and
-// flags start at `base`: the workgroup's device-coherent stores are done;
-// count it, and publish the epoch if it completes its group.
-__device__ __forceinline__ void qd_signal(QdSync *S, int base, int i, int n, uint32_t epoch)
-{
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int g = i / QD_GROUP, members = min(QD_GROUP, n - g * QD_GROUP);
-        uint32_t *c = &S->cnt[base + g];
-        const uint32_t old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old + 1u == (uint32_t)members) {
-            __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&S->flag[base + g], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
-}
-
-// Wave 0 only: waits until flag[idx] holds the epoch in every lane that has a
-// flag (has = true), bounded; each pass reads all the flags and the error
-// word in one batch.  Returns false (and raises the error word) when the wait
-// gave up or another wait already had.
-__device__ __forceinline__ bool qd_wait_flags(QdSync *S, bool has, int idx, uint32_t epoch)
-{
-    const uint32_t *f = &S->flag[has ? idx : 0];
-    for (int spins = 0;; spins++) {
-        uint32_t v = qd_poll_ld(f), e = qd_poll_ld(&S->err);
-        asm volatile("s_waitcnt vmcnt(0)" : "+v"(v), "+v"(e)::"memory");
-        if (__ballot(has && v != epoch) == 0ull) return true;
-        if (spins >= QD_SPIN_LIMIT || __ballot(e != 0u) != 0ull) {
-            if ((threadIdx.x & 63) == 0) qd_raise(S, epoch);
-            return false;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
 }
 
 struct QdLayout {
@@ -248,6 +213,34 @@ __device__ __forceinline__ uint2 qd_poll_tag(const QdArgs &a, const uint2 *p, bo
         if (spins >= QD_SPIN_LIMIT || __ballot(e != 0u) != 0ull) {
             if ((threadIdx.x & 63) == 0) qd_raise(a.sync, a.epoch);
             return r;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Wave 0: waits until every router workgroup's done word (the copy of this
+// workgroup's XCD) holds this launch's epoch, bounded like qd_poll_tag.
+__device__ __forceinline__ void qd_wait_rdone(const QdArgs &a)
+{
+    const int lane = threadIdx.x & 63, n = a.n_rt;
+    const uint2 *d = a.sync->rdone + (blockIdx.x & (QD_RDREP - 1)) * QD_RDSTRIDE;
+    static_assert(QD_RDSTRIDE <= 5 * 64, "five words a lane");
+    for (int spins = 0;; spins++) {
+        unsigned long long q0, q1, q2, q3, q4;
+        asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(q0) : "v"(d + min(lane, n - 1)) : "memory");
+        asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(q1) : "v"(d + min(lane + 64, n - 1)) : "memory");
+        asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(q2) : "v"(d + min(lane + 128, n - 1)) : "memory");
+        asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(q3) : "v"(d + min(lane + 192, n - 1)) : "memory");
+        asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(q4) : "v"(d + min(lane + 256, n - 1)) : "memory");
+        uint32_t e = qd_poll_ld(&a.sync->err);
+        asm volatile("s_waitcnt vmcnt(0)" : "+v"(q0), "+v"(q1), "+v"(q2), "+v"(q3), "+v"(q4), "+v"(e)::"memory");
+        const uint32_t ep = a.epoch;
+        const bool stale = (uint32_t)q0 != ep || (uint32_t)q1 != ep || (uint32_t)q2 != ep || (uint32_t)q3 != ep ||
+                           (uint32_t)q4 != ep;
+        if (__ballot(stale) == 0ull) return;
+        if (spins >= QD_SPIN_LIMIT || __ballot(e != 0u) != 0ull) {
+            if (lane == 0) qd_raise(a.sync, a.epoch);
+            return;
         }
         __builtin_amdgcn_s_sleep(1);
     }
@@ -409,26 +402,6 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
     const int o = b * QD_RT_ROWS + wave;
     float *xl = lds, *pbase = lds + nch * QD_XPAD, *part = pbase + wave * 64;
     if constexpr (RES) qd_norm_rows(a, qinv, qpart);
-    // the token rows, staged as q16 units for the gate / up workgroups that
-    // do not stage x themselves (there are none for one token); unit
-    // b + n_rt * thread, so every router workgroup takes a few
-    const int units = H / 16;
-    for (int i = a.rows > 1 ? b + a.n_rt * (int)threadIdx.x : a.rows * units; i < a.rows * units;
-         i += a.n_rt * QD_THREADS) {
-        float v[16];
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            float4 f;
-            if constexpr (RES) f = qd_x4<true>(a, qinv, i / units, (i % units) * 4 + q);
-            else f = reinterpret_cast<const float4 *>(a.x + (size_t)i * 16)[q];
-            v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
-        }
-        uint4 u[3];
-        qw_q16_make(v, u);
-        qd_st4(a.qx + (size_t)i * 3, u[0]);
-        qd_st4(a.qx + (size_t)i * 3 + 1, u[1]);
-        qd_st4(a.qx + (size_t)i * 3 + 2, u[2]);
-    }
     QD_TS(1);
     // this wave's row in registers, lane c holding chunk c (64 inputs, 8
     // uint4).  Loaded contiguously (each load instruction covers 8 whole
@@ -458,7 +431,7 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
         for (int q = 0; q < 8; q++) w[q] = *reinterpret_cast<const uint4 *>(wl + c * QD_WPAD + 4 * q);
 #ifdef QD_TRACE
         if (threadIdx.x == 0)
-            qd_trace[blockIdx.x * 8 + 3] = (w[7].w ^ w[0].x) == 0x12345678u ? 0 : wall_clock64();
+            qd_trace[blockIdx.x * 16 + 3] = (w[7].w ^ w[0].x) == 0x12345678u ? 0 : wall_clock64();
 #endif
     }
     for (int t = 0; t < a.rows; t++) {
@@ -471,11 +444,14 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
         if (t == 0) QD_TS(4);
         if (row) qd_router_row(w, xl, nch, a.sync->lgt + (size_t)t * (E + 1) + o, a.epoch, part);
     }
+    // the logit stores are acknowledged (past this XCD's L2) before the
+    // done words say so
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x < QD_RDREP)
+        __hip_atomic_store(reinterpret_cast<unsigned long long *>(a.sync->rdone + threadIdx.x * QD_RDSTRIDE + b),
+                           (unsigned long long)a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     QD_TS(2);
-    // one token: every reader polls the tagged logits (and stages x itself),
-    // so nothing waits on the router's flag
-    if (a.rows > 1) qd_signal(a.sync, QD_FL_RT, b, a.n_rt, a.epoch);
-    QD_TS(5);
     if constexpr (RES)
         if (b == 0) qd_write_resid(a, qinv);
 }
@@ -510,7 +486,10 @@ __device__ __forceinline__ void qd_stage_x(uint4 *xs, const QdArgs &a, const flo
     }
 }
 
-template <int LPR, int NUL, bool PLAINX = false>
+// TAGGED (the one-launch path): each output unit leaves as 12 tagged words
+// {epoch, dword} in a.sync->tact, vector vout[t] (written without any wait);
+// else as q16 units at dst (the batch path, read after the launch ends).
+template <int LPR, int NUL, bool PLAINX = false, bool TAGGED = false>
 __device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, int n, const QdArgs &a,
                                              int row0, int nt, bool staged, uint4 *xs, const int *vin,
                                              const int *vout, uint4 *dst, float (*ys)[QD_GU_MAXRPB])
@@ -630,7 +609,7 @@ __device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, i
             }
 #ifdef QD_TRACE
             if (t0 + t == 0 && threadIdx.x == 0)
-                qd_trace[blockIdx.x * 8 + 3] = __builtin_amdgcn_readfirstlane(__float_as_int(acc[0] + acc[1])) == 12345 ? 0 : wall_clock64();
+                qd_trace[blockIdx.x * 16 + 3] = __builtin_amdgcn_readfirstlane(__float_as_int(acc[0] + acc[1])) == 12345 ? 0 : wall_clock64();
 #endif
             const float g = qw_xor_sum<LPR>(acc[0]);
             const float u = qw_xor_sum<LPR>(acc[1]);
@@ -649,10 +628,21 @@ __device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, i
         for (int q = 0; q < 16; q++) v[q] = ys[t][16 * uu + q];
         uint4 s[3];
         qw_q16_make(v, s);
-        uint4 *d = dst + ((size_t)vout[t] * outunits + row0 / 16 + uu) * 3;
-        qd_st4(d, s[0]);
-        qd_st4(d + 1, s[1]);
-        qd_st4(d + 2, s[2]);
+        if (TAGGED) {
+            unsigned long long *d = reinterpret_cast<unsigned long long *>(
+                a.sync->tact + ((size_t)vout[t] * QD_TU + row0 / 16 + uu) * 12);
+            const uint32_t w[12] = {s[0].x, s[0].y, s[0].z, s[0].w, s[1].x, s[1].y, s[1].z, s[1].w,
+                                    s[2].x, s[2].y, s[2].z, s[2].w};
+#pragma unroll
+            for (int j = 0; j < 12; j++)
+                __hip_atomic_store(d + j, (unsigned long long)a.epoch | ((unsigned long long)w[j] << 32),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            uint4 *d = dst + ((size_t)vout[t] * outunits + row0 / 16 + uu) * 3;
+            qd_st4(d, s[0]);
+            qd_st4(d + 1, s[1]);
+            qd_st4(d + 2, s[2]);
+        }
     }
 }
 
@@ -687,7 +677,10 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
     const int t = threadIdx.x, nthr = blockDim.x, wave = t >> 6, lane = t & 63, nw = nthr >> 6;
     const int E = a.m.E, K = a.m.K;
     if (a.rows == 1 && nw >= PL) {
-        // the token's logits, each wave its slice, as soon as their tags are this launch's
+        // wave 0 waits for every router workgroup's done word, then each
+        // wave reads its slice of the logits (their tags checked too)
+        if (wave == 0) qd_wait_rdone(a);
+        __syncthreads();
         float x = 0.0f;
         if (wave < PL) {
             const int e = lane + 64 * wave;
@@ -696,6 +689,9 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
         int pi;
         float pw;
         qw_route_block<PL>(x, E, K, a.m.norm, wave, lane, &pi, &pw, R.rs.one.sx, R.rs.one.vb);
+#ifdef QD_TRACE
+        if (blockIdx.x >= a.n_rt && blockIdx.x < a.n_rt + a.n_ex) QD_TS(5);
+#endif
         // clamped: after a given-up wait the logits are whatever was read,
         // and no pick may then address outside the banks
         if (wave == 0 && lane < K) {
@@ -768,16 +764,6 @@ __device__ void qd_route_all(const QdArgs &a, QdRoute &R)
     __syncthreads();
 }
 
-// Waits, with the whole workgroup, until the router workgroups are done.
-__device__ __forceinline__ void qd_wait_router(const QdArgs &a)
-{
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        qd_wait_flags(a.sync, lane < (a.n_rt + QD_GROUP - 1) / QD_GROUP, QD_FL_RT + lane, a.epoch);
-    }
-    __syncthreads();
-}
-
 template <int LPR, int NUL, int PL, bool RES>
 __device__ __forceinline__ void qd_role_experts(const QdArgs &a, int bb, uint4 *xs, QdRoute &R, int *vin,
                                                 int *vout, float (*ys)[QD_GU_MAXRPB], float *qinv, float *qpart)
@@ -785,27 +771,21 @@ __device__ __forceinline__ void qd_role_experts(const QdArgs &a, int bb, uint4 *
     constexpr int RPB = QD_WAVES * (64 / LPR);
     const int H = a.m.H, I = a.m.I, K = a.m.K;
     const int u = bb / a.gu_wg_per_u, rb = bb % a.gu_wg_per_u;
-    // One token: its input is staged into LDS while the router runs.
-    const bool one = a.rows == 1;
-    if (one) {
-        if constexpr (RES) qd_norm_rows(a, qinv, qpart);
-        qd_stage_x<RES>(xs, a, qinv, nullptr, 1, 0, blockDim.x);
-    }
-    if (a.rows > 1) qd_wait_router(a);
+    // the token is staged into LDS while the router runs
+    if constexpr (RES) qd_norm_rows(a, qinv, qpart);
+    qd_stage_x<RES>(xs, a, qinv, nullptr, 1, 0, blockDim.x);
     QD_TS(1);
     qd_route_all<PL>(a, R);
     QD_TS(2);
-    if (bb == 0)
-        for (int p = threadIdx.x; p < a.rows * K; p += blockDim.x) {
-            a.idx[p] = R.picks[p];
-            a.w[p] = R.pw[p];
-        }
-    if (u >= R.U) return;
-    const int e = R.uexp[u], nt = R.ucnt[u], p0 = R.ustart[u];
-    if (threadIdx.x < nt) {
-        const int p = R.upair[p0 + threadIdx.x];
-        vin[threadIdx.x] = p / K;
-        vout[threadIdx.x] = p;
+    if (bb == 0 && threadIdx.x < K) {
+        a.idx[threadIdx.x] = R.picks[threadIdx.x];
+        a.w[threadIdx.x] = R.pw[threadIdx.x];
+    }
+    // one token: slot u is pick u; its activation vector is tagged vector 1 + u
+    const int e = R.picks[u];
+    if (threadIdx.x == 0) {
+        vin[0] = 0;
+        vout[0] = 1 + u;
     }
     __syncthreads();
     // Split banks: gate and up [E, I, H]; fused: gate_up [E, 2I, H], gate rows
@@ -821,10 +801,62 @@ __device__ __forceinline__ void qd_role_experts(const QdArgs &a, int bb, uint4 *
         gm = {a.m.gate_up.w + off * words, a.m.gate_up.s + off * groups, a.m.gate_up.b + off * groups};
         um = {gm.w + (size_t)I * words, gm.s + (size_t)I * groups, gm.b + (size_t)I * groups};
     }
-    qd_glu_block<LPR, NUL>(gm, um, I, a, rb * RPB, nt, one, xs, vin, vout, a.qact, ys);
+    qd_glu_block<LPR, NUL, false, true>(gm, um, I, a, rb * RPB, 1, true, xs, vin, vout, nullptr, ys);
     QD_TS(4);
-    qd_signal(a.sync, QD_FL_EX + u * a.ngu, rb, a.gu_wg_per_u, a.epoch);
-    QD_TS(5);
+}
+
+// One wave: waits until tagged activation vector v (units q16 units) holds
+// this launch's epoch in every word, then writes its dwords into the wave's
+// LDS region xw in q16 layout (a wave's LDS accesses run in order: no
+// barrier).  First one word of each unit (one per producing workgroup) is
+// polled, then every word is read and checked, so the polling stays light
+// while the experts still run.  Bounded like qd_poll_tag; returns false (the
+// error word raised) if a wait gave up.
+__device__ __forceinline__ bool qd_wait_tact(const QdArgs &a, int v, int units, uint4 *xw)
+{
+    const int lane = threadIdx.x & 63;
+    const uint2 *tv = a.sync->tact + (size_t)v * QD_TU * 12;
+    const int nw = units * 12;
+    for (int spins = 0;; spins++) {
+        unsigned long long q;
+        const uint2 *p = tv + (size_t)min(lane, units - 1) * 12;
+        asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(q) : "v"(p) : "memory");
+        uint32_t e = qd_poll_ld(&a.sync->err);
+        asm volatile("s_waitcnt vmcnt(0)" : "+v"(q), "+v"(e)::"memory");
+        if (__ballot(lane < units && (uint32_t)q != a.epoch) == 0ull) break;
+        if (spins >= QD_SPIN_LIMIT || __ballot(e != 0u) != 0ull) {
+            if (lane == 0) qd_raise(a.sync, a.epoch);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    // then the whole vector in one pass, six words a lane
+    uint32_t *x32 = reinterpret_cast<uint32_t *>(xw);
+    static_assert(QD_TU * 12 <= 6 * 64, "six words a lane");
+    for (int spins = 0;; spins++) {
+        unsigned long long q[6];
+#pragma unroll
+        for (int j = 0; j < 6; j++)
+            asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(q[j]) : "v"(tv + min(lane + 64 * j, nw - 1)) : "memory");
+        uint32_t e = qd_poll_ld(&a.sync->err);
+        // every loaded register is tied to the wait, so no use moves above it
+        asm volatile("s_waitcnt vmcnt(0)"
+                     : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(q[4]), "+v"(q[5]), "+v"(e)::"memory");
+        bool stale = false;
+#pragma unroll
+        for (int j = 0; j < 6; j++) stale |= lane + 64 * j < nw && (uint32_t)q[j] != a.epoch;
+        if (__ballot(stale) == 0ull) {
+#pragma unroll
+            for (int j = 0; j < 6; j++)
+                if (lane + 64 * j < nw) x32[lane + 64 * j] = (uint32_t)(q[j] >> 32);
+            return true;
+        }
+        if (spins >= QD_SPIN_LIMIT || __ballot(e != 0u) != 0ull) {
+            if (lane == 0) qd_raise(a.sync, a.epoch);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
 }
 
 // ---- down: the shared expert and every expert of a token, and the combine -------
@@ -836,30 +868,25 @@ __device__ __forceinline__ void qd_role_experts(const QdArgs &a, int bb, uint4 *
 // per-matrix rows meet in LDS and the combine runs in slot order.
 template <int NUL, int PL>
 __device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R, uint4 *xa,
-                                             float (*ys)[QD_DOWN_RPG], uint32_t *dready)
+                                             float (*ys)[QD_DOWN_RPG])
 {
     constexpr int LPR = QD_DOWN_LPR, RPP = 64 / LPR, RIT = QD_DOWN_RIT, RPG = QD_DOWN_RPG;
     const int H = a.m.H, I = a.m.I, SI = a.m.SI, K = a.m.K;
-    const int rb = bd % a.n_down_rb, t = bd / a.n_down_rb;
+    const int rb = bd;
     const int lane = threadIdx.x & 63, m = threadIdx.x >> 6;
     const int slot = lane / LPR, lr = lane % LPR;
     const int row0 = rb * RPG;
     const int lgG = a.lgG;
-    if (threadIdx.x == 0) *dready = 0u;     // seen by all after routing's barriers
-    if (a.rows > 1) qd_wait_router(a);
     QD_TS(1);
     qd_route_all<PL>(a, R);
     QD_TS(2);
-    const float gate = qw_sigmoid(__uint_as_float(
-        qd_poll_tag(a, a.sync->lgt + (size_t)t * (a.m.E + 1) + a.m.E, (threadIdx.x & 63) == 0).y));
-
     const bool busy = m <= K;
     const int kin = m == 0 ? SI : I;
     const int units = kin / 16, words = kin / 8, groups = kin >> lgG;
     const uint32_t *wm = a.m.sh_down.w;
     const uint16_t *sm = a.m.sh_down.s, *bm = a.m.sh_down.b;
     if (busy && m > 0) {
-        const size_t e = (size_t)R.picks[t * K + m - 1];
+        const size_t e = (size_t)R.picks[m - 1];
         wm = a.m.down.w + e * H * words;
         sm = a.m.down.s + e * H * groups;
         bm = a.m.down.b + e * H * groups;
@@ -870,117 +897,64 @@ __device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R
         while (wall_clock64() - t0 < QD_DOWN_DELAY) __builtin_amdgcn_s_sleep(2);
     }
 #endif
-    // Every load is issued (at a clamped, valid address) before any is used;
-    // out-of-range lanes are zeroed afterwards.
+    // Every load is issued (at a clamped, valid address) before any is used.
+    // The scales and biases of the workgroup's RPG rows are contiguous
+    // (RPG * groups bf16 each, at most 256: kin <= 512, groups of >= 32):
+    // lanes 0-31 load the scales, 32-63 the biases, 16 bytes a lane, and
+    // pass them through LDS, so they take one register quad, not a register
+    // per (unit, row).
     uint2 wv[NUL][RIT];
-    uint32_t sv[NUL][RIT], bv[NUL][RIT];
 #pragma unroll
     for (int j = 0; j < NUL; j++) {
         const int c = min(j * LPR + lr, units - 1);
-        const int g = (16 * c) >> lgG;
 #pragma unroll
         for (int i = 0; i < RIT; i++) {
             const int row = min(row0 + slot + RPP * i, H - 1);
             wv[j][i] = qw_ld2(wm, (uint32_t)(row * words + 2 * c) * 4u);
-            sv[j][i] = qw_ldu16(sm, (uint32_t)(row * groups + g) * 2u);
-            bv[j][i] = qw_ldu16(bm, (uint32_t)(row * groups + g) * 2u);
         }
     }
-    uint32_t sb[NUL][RIT];        // bf16 scale (low half) and bias (high half)
-#pragma unroll
-    for (int j = 0; j < NUL; j++)
-#pragma unroll
-        for (int i = 0; i < RIT; i++) {
-            const bool ok = busy && j * LPR + lr < units && row0 + slot + RPP * i < H;
-            wv[j][i] = ok ? wv[j][i] : make_uint2(0, 0);
-            sb[j][i] = ok ? sv[j][i] | (bv[j][i] << 16) : 0u;
-        }
-    // One wave polls every flag this workgroup hangs on (lanes [0, gsh): the
-    // shared expert's groups; then ngu lanes for each of the token's experts)
-    // and publishes in LDS which matrices have their activations (bit m), or
-    // bit 31 if a wait gave up.  Wave m starts on its matrix as soon as its
-    // bit is set, so the matrices finish as their experts do, and only the
-    // last one's load and dot trail the last expert.  The poller is an idle
-    // wave when there is one (K + 1 < 16), else wave 0 before its own matrix.
-    const int pw = K + 1 < QD_WAVES ? QD_WAVES - 1 : 0;
-    if (m == pw) {
-        const int gsh = (a.n_sh + QD_GROUP - 1) / QD_GROUP, nfl = gsh + K * a.ngu;
-        int fidx = QD_FL_SH + lane;
-        if (lane >= gsh) {
-            const int q = lane - gsh, k = q / a.ngu;
-            fidx = k < K ? QD_FL_EX + R.mark[R.picks[t * K + k]] * a.ngu + q % a.ngu : 0;
-        }
-        const bool has = lane < nfl;
-        const uint32_t *f = &a.sync->flag[has ? fidx : 0];
-        const uint32_t all = (2u << K) - 1u;
-        for (int spins = 0;; spins++) {
-            uint32_t v = qd_poll_ld(f), e = qd_poll_ld(&a.sync->err);
-            asm volatile("s_waitcnt vmcnt(0)" : "+v"(v), "+v"(e)::"memory");
-            const unsigned long long on = __ballot(has && v == a.epoch);
-            const unsigned long long g0 = (1ull << gsh) - 1ull, gk = (1ull << a.ngu) - 1ull;
-            uint32_t mask = (on & g0) == g0 ? 1u : 0u;
-            for (int k = 0; k < K; k++)
-                if (((on >> (gsh + k * a.ngu)) & gk) == gk) mask |= 2u << k;
-            const bool done = mask == all;
-            const bool fail = !done && (spins >= QD_SPIN_LIMIT || __ballot(e != 0u) != 0ull);
-            if (fail) {
-                mask = 0x80000000u;
-                if (lane == 0) qd_raise(a.sync, a.epoch);
-            }
-            if (lane == 0) __hip_atomic_store(dready, mask, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (done || fail) break;
-            __builtin_amdgcn_s_sleep(1);
-        }
-    }
+    const int nsb = RPG * groups, li = lane & 31;
+    const uint32_t sboff = (uint32_t)(row0 * groups + 8 * li) * 2u;
+    uint4 sbr = make_uint4(0, 0, 0, 0);
+    if (busy && 8 * li < nsb) sbr = lane < 32 ? qw_ld4(sm, sboff) : qw_ld4(bm, sboff);
+    // the shared expert's gate logit (its round trip overlaps the loads)
+    const float gate = qw_sigmoid(__uint_as_float(
+        qd_poll_tag(a, a.sync->lgt + a.m.E, (threadIdx.x & 63) == 0).y));
+    // Wave m waits for its own matrix's activation vector (0: the shared
+    // expert's, 1 + k: the k-th pick's), so the matrices start as their
+    // experts finish and only the last one's wait and dot trail the last
+    // expert.
     if (busy) {
-        uint32_t rd;
-        for (;;) {
-            rd = __hip_atomic_load(dready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (((rd >> m) & 1u) || (rd >> 31)) break;
-            __builtin_amdgcn_s_sleep(1);
-        }
-        if (rd >> 31) goto gave_up;
-        // this matrix's vector, coalesced, into the wave's own LDS region (a
-        // wave's LDS accesses run in order: no barrier)
-        const int nv = units * 3;
-        const uint4 *xm = m == 0 ? a.qsh + (size_t)t * ((SI / 16) * 3)
-                                 : a.qact + ((size_t)t * K + (m - 1)) * ((I / 16) * 3);
         uint4 *xw = xa + (m == 0 ? 0 : (SI / 16) * 3 + (m - 1) * ((I / 16) * 3));
-        const uint32_t xo = (uint32_t)(reinterpret_cast<const char *>(xm) - a.scr);
-        // a vector has units <= NUL * LPR, so 3 NUL LPR uint4: XW a lane
-        constexpr int XW = (3 * NUL * LPR + 63) / 64;
-        uint4 v[XW];
+        uint16_t *sl = reinterpret_cast<uint16_t *>(xa + (SI / 16) * 3 + K * ((I / 16) * 3) + m * 64);
+        if (8 * li < nsb) *reinterpret_cast<uint4 *>(sl + (lane < 32 ? 0 : 256) + 8 * li) = sbr;
+        if (qd_wait_tact(a, m, units, xw)) {
+            QD_TS(4);
+            float y[RIT];
 #pragma unroll
-        for (int r = 0; r < XW; r++)
-            v[r] = qw_ld4_coh(a.scr, xo + (uint32_t)min(lane + 64 * r, nv - 1) * 16u);
+            for (int i = 0; i < RIT; i++) y[i] = 0.0f;
 #pragma unroll
-        for (int r = 0; r < XW; r++) asm volatile("" : "+v"(v[r].x), "+v"(v[r].y), "+v"(v[r].z), "+v"(v[r].w));
+            for (int j = 0; j < NUL; j++) {
+                const int c = j * LPR + lr;
+                if (c < units) {
+                    const int g = (16 * c) >> lgG;
+                    const uint4 p0 = xw[3 * c], p1 = xw[3 * c + 1], rr = xw[3 * c + 2];
+                    const float4 r = *reinterpret_cast<const float4 *>(&rr);
 #pragma unroll
-        for (int r = 0; r < XW; r++)
-            if (lane + 64 * r < nv) xw[lane + 64 * r] = v[r];
-        QD_TS(4);
-        float y[RIT];
+                    for (int i = 0; i < RIT; i++) {
+                        const int q = (slot + RPP * i) * groups + g;
+                        y[i] = qw_unit_dot(wv[j][i], p0, p1, r, __uint_as_float((uint32_t)sl[q] << 16),
+                                           __uint_as_float((uint32_t)sl[256 + q] << 16), y[i]);
+                    }
+                }
+            }
 #pragma unroll
-        for (int i = 0; i < RIT; i++) y[i] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < NUL; j++) {
-            const int c = j * LPR + lr;
-            if (c < units) {
-                const uint4 p0 = xw[3 * c], p1 = xw[3 * c + 1], rr = xw[3 * c + 2];
-                const float4 r = *reinterpret_cast<const float4 *>(&rr);
-#pragma unroll
-                for (int i = 0; i < RIT; i++)
-                    y[i] = qw_unit_dot(wv[j][i], p0, p1, r, __uint_as_float(sb[j][i] << 16),
-                                       __uint_as_float(sb[j][i] & 0xFFFF0000u), y[i]);
+            for (int i = 0; i < RIT; i++) {
+                const float v = qw_xor_sum<LPR>(y[i]);
+                if (lr == 0) ys[m][slot + RPP * i] = v;
             }
         }
-#pragma unroll
-        for (int i = 0; i < RIT; i++) {
-            const float v = qw_xor_sum<LPR>(y[i]);
-            if (lr == 0) ys[m][slot + RPP * i] = v;
-        }
     }
-gave_up:
     QD_TS(6);
     __syncthreads();
     QD_TS(7);
@@ -989,8 +963,8 @@ gave_up:
         const int row = row0 + r;
         if (row >= H) continue;
         float acc = ys[0][r] * gate;
-        for (int k = 0; k < K; k++) acc = __builtin_fmaf(R.pw[t * K + k], ys[1 + k][r], acc);
-        a.out[(size_t)t * H + row] = acc;
+        for (int k = 0; k < K; k++) acc = __builtin_fmaf(R.pw[k], ys[1 + k][r], acc);
+        a.out[row] = acc;
     }
     QD_TS(5);
 }
@@ -1006,7 +980,6 @@ __global__ __launch_bounds__(QD_THREADS, 8) void k_decode_fused(QdArgs a)
     __shared__ QdRoute R;
     __shared__ int vin[QD_MAXT], vout[QD_MAXT];
     __shared__ float ys[QD_MAXT][QD_GU_MAXRPB];
-    __shared__ uint32_t dready;
     __shared__ float qinv[QD_MAXT], qpart[QD_WAVES];   // the residual prologue's row scales
     static_assert(QD_MAXT * QD_GU_MAXRPB >= (QWK_DECODE_MAX_K + 1) * QD_DOWN_RPG, "down shares ys");
     constexpr int RPB = QD_WAVES * (64 / LPR);
@@ -1024,25 +997,18 @@ __global__ __launch_bounds__(QD_THREADS, 8) void k_decode_fused(QdArgs a)
     }
     b -= a.n_ex;
     if (b < a.n_sh) {
-        // All token rows fit one LDS pass: stage them here, no wait.
-        // Otherwise copy them, pass by pass, from the router role's staging.
-        const bool own = a.rows <= a.tch;
-        if (threadIdx.x < QD_MAXT) vin[threadIdx.x] = vout[threadIdx.x] = threadIdx.x;
-        if (own) {
-            if constexpr (RES) qd_norm_rows(a, qinv, qpart);
-            qd_stage_x<RES>(xs, a, qinv, nullptr, a.rows, 0, blockDim.x);
-        }
-        else qd_wait_router(a);
+        // the shared expert's activation is tagged vector 0
+        if (threadIdx.x == 0) vin[0] = vout[0] = 0;
+        if constexpr (RES) qd_norm_rows(a, qinv, qpart);
+        qd_stage_x<RES>(xs, a, qinv, nullptr, 1, 0, blockDim.x);
         __syncthreads();
-        qd_glu_block<LPR, NUL>(a.m.sh_gate, a.m.sh_up, a.m.SI, a, b * RPB, a.rows, own, xs, vin, vout, a.qsh,
-                               ys);
+        qd_glu_block<LPR, NUL, false, true>(a.m.sh_gate, a.m.sh_up, a.m.SI, a, b * RPB, 1, true, xs, vin, vout,
+                                            nullptr, ys);
         QD_TS(4);
-        qd_signal(a.sync, QD_FL_SH, b, a.n_sh, a.epoch);
-        QD_TS(5);
         return;
     }
     b -= a.n_sh;
-    qd_role_down<NULD, PL>(a, b, R, xs, reinterpret_cast<float (*)[QD_DOWN_RPG]>(&ys[0][0]), &dready);
+    qd_role_down<NULD, PL>(a, b, R, xs, reinterpret_cast<float (*)[QD_DOWN_RPG]>(&ys[0][0]));
 }
 
 // ---- host side -------------------------------------------------------------------
@@ -1106,7 +1072,8 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
                               size_t scratch_bytes, void *sync, uint32_t epoch, hipEvent_t *ev)
 {
     const int G = M->group;
-    if (!qwk_moe_decode_supported(M, rows) || !sync || epoch == 0u) return (int)hipErrorInvalidValue;
+    // the fused launch serves one token; 2..8 take qwk_moe_decode_batch
+    if (rows != 1 || !qwk_moe_decode_supported(M, rows) || !sync || epoch == 0u) return (int)hipErrorInvalidValue;
     if (res ? (!res->h || !res->h_out || !res->x_out || ((uintptr_t)res->h & 7u) || ((uintptr_t)res->h_out & 7u) ||
                ((uintptr_t)res->y & 15u) || ((uintptr_t)res->x_out & 15u) ||
                (const void *)res->h_out == (const void *)res->h || (const void *)res->h_out == (const void *)res->y)
@@ -1134,7 +1101,6 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     a.n_rt = (M->E + 1 + QD_RT_ROWS - 1) / QD_RT_ROWS;
     a.n_sh = (M->SI + rpb - 1) / rpb;
     a.gu_wg_per_u = (M->I + rpb - 1) / rpb;
-    a.ngu = (a.gu_wg_per_u + QD_GROUP - 1) / QD_GROUP;
     a.n_ex = a.umax * a.gu_wg_per_u;
     a.n_down_rb = (M->H + QD_DOWN_RPG - 1) / QD_DOWN_RPG;
     a.scr = S;
@@ -1143,9 +1109,8 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     a.qact = (uint4 *)(S + L.qact);
     a.sync = (QdSync *)sync;
     a.epoch = epoch;
-    const int gsh = (a.n_sh + QD_GROUP - 1) / QD_GROUP, grt = (a.n_rt + QD_GROUP - 1) / QD_GROUP;
-    if (a.tch < 1 || a.umax > QD_MAXU || grt > QD_FL_SH - QD_FL_RT || gsh > QD_FL_EX - QD_FL_SH ||
-        QD_FL_EX + a.umax * a.ngu > QD_NSYNC || gsh + M->K * a.ngu > 64 || grt > 64)
+    // one token: K + 1 activation vectors of at most QD_TU q16 units each
+    if (a.tch < 1 || a.umax > QD_MAXU || M->I / 16 > QD_TU || M->SI / 16 > QD_TU || a.n_rt > QD_RDSTRIDE)
         return (int)hipErrorInvalidValue;
     const int grid = a.n_rt + a.n_sh + a.n_ex + rows * a.n_down_rb;
 

@@ -313,6 +313,10 @@ __device__ __forceinline__ uint2 qw_ld2(const void *base, uint32_t off)
 {
     return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(qw_rsrc(base), off, 0, 0));
 }
+__device__ __forceinline__ uint4 qw_ld4(const void *base, uint32_t off)
+{
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(qw_rsrc(base), off, 0, 0));
+}
 __device__ __forceinline__ uint32_t qw_ldu16(const void *base, uint32_t off)
 {
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(qw_rsrc(base), off, 0, 0);
@@ -409,19 +413,24 @@ __device__ __forceinline__ void qw_route_finish(float (&v)[PL], int E, int K, in
             __builtin_amdgcn_wave_barrier();
             const uint64_t mk = lane < C ? keys[lane] : 0;
             QW_RSTAMP(6);
+            // each lane's rank among the C keys, the keys broadcast from
+            // their lanes (C is wave-uniform; keys are distinct)
+            const uint32_t mlo = (uint32_t)mk, mhi = (uint32_t)(mk >> 32);
             int rank = 0;
-            // four keys a step; those past C (at most keys[66], inside sx) do not count
-            for (int q = 0; q < C; q += 4)
-                rank += (keys[q] > mk) + (q + 1 < C && keys[q + 1] > mk) + (q + 2 < C && keys[q + 2] > mk) +
-                        (q + 3 < C && keys[q + 3] > mk);
+            for (int q = 0; q < C; q++) {
+                const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)mlo, q);
+                const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)mhi, q);
+                rank += (hi > mhi) | ((hi == mhi) & (lo > mlo));
+            }
             QW_RSTAMP(7);
             if (lane < C && rank < K) picks[rank] = mk;
             __builtin_amdgcn_wave_barrier();
-            // the renormalising sum adds the picks in pick order
-            float wsum = 0.0f;
-            for (int n = 0; n < K; n++) wsum = wsum + __uint_as_float((uint32_t)(picks[n] >> 32));
+            // the renormalising sum adds the picks in pick order, each
+            // broadcast from its lane
             const uint64_t pk = lane < K ? picks[lane] : 0;
             const float mw = __uint_as_float((uint32_t)(pk >> 32));
+            float wsum = 0.0f;
+            for (int n = 0; n < K; n++) wsum = wsum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mw), n));
             *pick_i = lane < K ? 0xFFFF - (int)(uint32_t)pk : 0;
             *pick_w = norm ? mw / wsum : mw;
             QW_RSTAMP(8);

@@ -43,7 +43,7 @@ def test_noalloc_refuses_oversized_staging(gpu):
     """Staging past the static array is refused with nothing encoded (no
     command is needed to ask); a fitting shape is accepted.  Several tokens
     take the batch path, whose staging (logits, the q16 token rows, the
-    unique-expert table, the activations) must fit the 245,504 bytes past the
+    unique-expert table, the activations) must fit the 249,600 bytes past the
     hand-off state."""
     r = gpu.NULL_REF
     q = gpu.qw_q4_ref(r, r, r, 64)
