@@ -280,8 +280,16 @@ def bench_hc(gpu, steps, H=3072, S=4, k=320, G=64, pool=96, prefill_rows=2048, s
     hpair, ipair = (h4, h4b), (inj, injb)
 
     def decode_step(c, p):
-        # two launches: inject + norm + down + injection logits, then up + mix;
-        # h4 and the logits alternate between two buffers
+        # one launch: inject + norm + down + injection logits, then up + mix
+        # after an in-launch hand-off; h4 and the logits alternate between two
+        # buffers
+        wn, (dw, ds, db), (uw, us, ub), bj = sets[p % pool]
+        assert gpu.qw_op_hc_decode(c, x.ref(), hpair[(p + 1) % 2].ref(), n4.ref(), d.ref(), ipair[(p + 1) % 2].ref(),
+                                   hpair[p % 2].ref(), out.ref(), ipair[p % 2].ref(), wn.ref(), dw.ref(), ds.ref(),
+                                   db.ref(), bj.ref(), uw.ref(), us.ref(), ub.ref(), H, S, k, G, 1e-6, 1.0 / S)
+
+    def decode_step_two(c, p):
+        # the same step as two launches (the pre-decode op, then the mix-up op)
         wn, (dw, ds, db), (uw, us, ub), bj = sets[p % pool]
         assert gpu.qw_op_hc_pre_decode(c, hpair[(p + 1) % 2].ref(), n4.ref(), d.ref(), ipair[(p + 1) % 2].ref(),
                                        hpair[p % 2].ref(), out.ref(), ipair[p % 2].ref(), wn.ref(), dw.ref(),
@@ -302,6 +310,16 @@ def bench_hc(gpu, steps, H=3072, S=4, k=320, G=64, pool=96, prefill_rows=2048, s
     gpu.qw_cmd_mark(c, b"hc decode region")
     gpu.run(c, "hc decode")
     dec_ms = gpu.qw_prof_ms(b"hc decode region", None)
+    gpu.qw_prof_reset()
+    gpu.qw_prof_set_enabled(True)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_prof_set_enabled(False)
+    for p in range(steps):
+        decode_step_two(c, p)
+    gpu.qw_prof_set_enabled(True)
+    gpu.qw_cmd_mark(c, b"hc decode two-launch region")
+    gpu.run(c, "hc decode (two launches)")
+    two_ms = gpu.qw_prof_ms(b"hc decode two-launch region", None)
 
     wn, (dw, ds, db), (uw, us, ub), bj = sets[0]
 
@@ -341,7 +359,8 @@ def bench_hc(gpu, steps, H=3072, S=4, k=320, G=64, pool=96, prefill_rows=2048, s
     return {"shape": {"H": H, "S": S, "lowrank": k, "group": G},
             "decode": {"us_per_token": round(us_tok, 2), "weight_bytes": wbytes,
                        "hbm_gbs": round((wbytes + abytes) / (us_tok * 1e-6) / 1e9, 1),
-                       "launches": 2, "weight_sets": pool},
+                       "launches": 1, "weight_sets": pool,
+                       "two_launch_us_per_token": round(two_ms * 1000.0 / steps, 2)},
             "prefill": {"rows": rows, "ms": round(pf_ms, 3),
                         "tflops": round(flops / (pf_ms * 1e-3) / 1e12, 2)}}
 

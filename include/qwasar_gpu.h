@@ -160,6 +160,19 @@ bool qw_op_hc_mix_up(qw_cmd c, qw_ref x, qw_ref d, qw_ref n4, qw_ref w, qw_ref s
 bool qw_op_hc_pre_decode(qw_cmd c, qw_ref h4_out, qw_ref n4, qw_ref d, qw_ref inj_out, qw_ref h4, qw_ref out,
                          qw_ref inj, qw_ref norm_w, qw_ref down_w, qw_ref down_s, qw_ref down_b, qw_ref inj_w,
                          int32_t H, int32_t S, int32_t lowrank, int32_t group, float eps);
+/* A whole mixer decode step (one row) in one launch: qw_op_hc_pre_decode's
+ * outputs (h4_out, n4, d, inj_out) and qw_op_hc_mix_up's x at rows 1 with
+ * the given scale, the up-projection 4-bit [S*H, lowrank].  The launch
+ * hands d over between its workgroups (a hand-off failure is reported as
+ * the MoE decode's is, by qw_cmd_error after qw_cmd_wait).  No counterpart
+ * op in the reference, which runs these steps as separate passes
+ * (metal/sparse.metal:14-189).  False, nothing encoded, for the overlaps and
+ * shapes qw_op_hc_pre_decode refuses (x counting as an output), and for
+ * lowrank above 512 or not a multiple of 8 and of group. */
+bool qw_op_hc_decode(qw_cmd c, qw_ref x, qw_ref h4_out, qw_ref n4, qw_ref d, qw_ref inj_out, qw_ref h4,
+                     qw_ref out, qw_ref inj, qw_ref norm_w, qw_ref down_w, qw_ref down_s, qw_ref down_b,
+                     qw_ref inj_w, qw_ref up_w, qw_ref up_s, qw_ref up_b, int32_t H, int32_t S, int32_t lowrank,
+                     int32_t group, float eps, float scale);
 /* h4[r, s*H+i] = x[r, i]. */
 void qw_op_repeat_cols(qw_cmd c, qw_ref h4, qw_ref x, int32_t rows, int32_t H, int32_t S);
 /* Grouped RMS norm: `groups` streams of `dim` per row, weight [groups*dim]. */

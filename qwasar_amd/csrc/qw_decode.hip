@@ -1020,6 +1020,15 @@ extern "C" size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows)
 
 extern "C" size_t qwk_moe_decode_sync_bytes(void) { return sizeof(QdSync); }
 
+extern "C" int qwk_decode_sync_words(void *sync, uint32_t **err, void **words, size_t *nwords)
+{
+    QdSync *S = static_cast<QdSync *>(sync);
+    *err = &S->err;
+    *words = S->tact;
+    *nwords = sizeof(S->tact) / sizeof(S->tact[0]);
+    return 0;
+}
+
 extern "C" int qwk_moe_decode_sync_error(const void *sync, uint32_t *err)
 {
     return (int)hipMemcpy(err, &static_cast<const QdSync *>(sync)->err, sizeof *err, hipMemcpyDeviceToHost);

@@ -17,6 +17,20 @@
 #include "qw_kernels.h"
 
 #define QH_THREADS 256
+#define QH_PRE_MAXS 4             // streams a fused decode kernel takes
+
+// Built with -DQH_TRACE, every workgroup stamps the device wall clock
+// (100 MHz) at its phases into qh_trace[block][slot], for timelines.
+#ifdef QH_TRACE
+__device__ unsigned long long qh_trace[2048 * 8];
+#define QH_TS(slot) do { if (threadIdx.x == 0) qh_trace[blockIdx.x * 8 + (slot)] = wall_clock64(); } while (0)
+extern "C" int qh_trace_read(unsigned long long *dst)
+{
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(qh_trace), sizeof(qh_trace));
+}
+#else
+#define QH_TS(slot) do { } while (0)
+#endif
 
 __device__ __forceinline__ float qh_sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
 
@@ -224,6 +238,161 @@ static dim3 qh_grid(int64_t n)
     return dim3((unsigned)(b < 16384 ? (b > 0 ? b : 1) : 16384));
 }
 
+// Inject and grouped norm of one row into LDS (nl: S*H floats): the streams
+// with the block's output injected, then each normed with its gains -- per
+// stream the order of k_norm_grouped (a chain over this thread's float4s
+// ascending, the xor tree, the wave partials in order).  Stream `ws` (< 0:
+// none) is also written to h4_out and n4.  inv gets the streams' 1/rms.
+// after_loads() runs once this function's loads are issued, so loads it
+// issues come after them in the memory counter's order (the norm does not
+// wait for them).  Every thread of the workgroup calls it (it holds
+// barriers).
+template <int NI, typename F>
+__device__ __forceinline__ void qh_inject_norm(float4 *nl, float (*part)[QH_THREADS / 64], int ws,
+                                               float *__restrict__ h4_out, float *__restrict__ n4,
+                                               const float *__restrict__ h4, const float *__restrict__ out,
+                                               const float *__restrict__ inj, const uint16_t *__restrict__ wn,
+                                               int H, int S, float eps, float (&inv)[QH_PRE_MAXS], F &&after_loads)
+{
+    const int t = threadIdx.x, n4q = H / 4;
+    const int wave = t >> 6, lane = t & 63;
+    const float4 *orow = reinterpret_cast<const float4 *>(out);
+    float injv[QH_PRE_MAXS], wgt[QH_PRE_MAXS], ss[QH_PRE_MAXS];
+#pragma unroll
+    for (int s = 0; s < QH_PRE_MAXS; s++) {
+        injv[s] = s < S ? inj[s] : 0.0f;
+        ss[s] = 0.0f;
+    }
+    constexpr int NR = NI > 0 ? NI : 1;
+    float4 hv[QH_PRE_MAXS][NR], ov[NR];
+    uint2 gw[QH_PRE_MAXS][NR];
+    if (NI > 0) {
+        // every value this thread needs, requested at once
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+            const int i = t + QH_THREADS * j;
+            const bool ok = i < n4q;
+            ov[j] = ok ? orow[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int s = 0; s < QH_PRE_MAXS; s++) {
+                const bool in = ok && s < S;
+                hv[s][j] = in ? reinterpret_cast<const float4 *>(h4 + (size_t)s * H)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                gw[s][j] = in ? reinterpret_cast<const uint2 *>(wn + (size_t)s * H)[i] : make_uint2(0, 0);
+            }
+        }
+    }
+    after_loads();
+#pragma unroll
+    for (int s = 0; s < QH_PRE_MAXS; s++) wgt[s] = s < S ? 2.0f * qh_sigmoid(injv[s] / (float)S) : 0.0f;
+    // inject and the sums of squares of all streams together
+    auto inject = [&](int s, int i, float4 &v, float4 o) {
+        v.x += o.x * wgt[s]; v.y += o.y * wgt[s]; v.z += o.z * wgt[s]; v.w += o.w * wgt[s];
+        if (ws == s) reinterpret_cast<float4 *>(h4_out + (size_t)s * H)[i] = v;
+        ss[s] = __builtin_fmaf(v.x, v.x, ss[s]);
+        ss[s] = __builtin_fmaf(v.y, v.y, ss[s]);
+        ss[s] = __builtin_fmaf(v.z, v.z, ss[s]);
+        ss[s] = __builtin_fmaf(v.w, v.w, ss[s]);
+    };
+    auto scale = [&](int s, int i, float4 v, uint2 wb) {
+        v.x = v.x * inv[s] * __uint_as_float(wb.x << 16);
+        v.y = v.y * inv[s] * __uint_as_float(wb.x & 0xFFFF0000u);
+        v.z = v.z * inv[s] * __uint_as_float(wb.y << 16);
+        v.w = v.w * inv[s] * __uint_as_float(wb.y & 0xFFFF0000u);
+        nl[s * n4q + i] = v;
+        if (ws == s) reinterpret_cast<float4 *>(n4 + (size_t)s * H)[i] = v;
+    };
+    if (NI > 0) {
+        // the injected values stay in registers until they are scaled
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+            const int i = t + QH_THREADS * j;
+#pragma unroll
+            for (int s = 0; s < QH_PRE_MAXS; s++)
+                if (s < S && i < n4q) inject(s, i, hv[s][j], ov[j]);
+        }
+    } else {
+        for (int i = t; i < n4q; i += QH_THREADS) {
+            const float4 o = orow[i];
+#pragma unroll
+            for (int s = 0; s < QH_PRE_MAXS; s++)
+                if (s < S) {
+                    float4 v = reinterpret_cast<const float4 *>(h4 + (size_t)s * H)[i];
+                    inject(s, i, v, o);
+                    nl[s * n4q + i] = v;
+                }
+        }
+    }
+    QH_TS(5);
+#pragma unroll
+    for (int s = 0; s < QH_PRE_MAXS; s++) {
+        const float v = qw_xor_sum<64>(ss[s]);
+        if (lane == 0) part[s][wave] = v;
+    }
+    __syncthreads();
+    QH_TS(6);
+#pragma unroll
+    for (int s = 0; s < QH_PRE_MAXS; s++) {
+        float tot = part[s][0];
+#pragma unroll
+        for (int w = 1; w < QH_THREADS / 64; w++) tot = tot + part[s][w];
+        inv[s] = 1.0f / sqrtf(tot / (float)H + eps);
+    }
+    if (NI > 0) {
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+            const int i = t + QH_THREADS * j;
+#pragma unroll
+            for (int s = 0; s < QH_PRE_MAXS; s++)
+                if (s < S && i < n4q) scale(s, i, hv[s][j], gw[s][j]);
+        }
+    } else {
+        for (int i = t; i < n4q; i += QH_THREADS) {
+#pragma unroll
+            for (int s = 0; s < QH_PRE_MAXS; s++)
+                if (s < S) scale(s, i, nl[s * n4q + i], reinterpret_cast<const uint2 *>(wn + (size_t)s * H)[i]);
+        }
+    }
+    __syncthreads();
+}
+
+// Injection logit s (order R: a thread per 64-input chunk, each chunk an
+// fmaf chain from 0, the chunk sums left to right) of the normed row in LDS.
+// Every thread of the workgroup calls it (it holds a barrier).
+__device__ __forceinline__ void qh_inj_logit(const float4 *nl, float *pc, const uint16_t *__restrict__ bj, int s,
+                                             int HH, float *__restrict__ inj_out)
+{
+    const int t = threadIdx.x, nch = HH / 64;
+    if (t < nch) {
+        // the chunk's 64 weights and inputs all requested before the chain
+        const uint4 *wr = reinterpret_cast<const uint4 *>(bj + (size_t)s * HH + 64 * t);
+        uint4 ww[8];
+        float4 xa[16];
+#pragma unroll
+        for (int q = 0; q < 8; q++) ww[q] = wr[q];
+#pragma unroll
+        for (int q = 0; q < 16; q++) xa[q] = nl[16 * t + q];
+        float p = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const uint32_t wd[4] = {ww[q].x, ww[q].y, ww[q].z, ww[q].w};
+            const float4 a = xa[2 * q], c = xa[2 * q + 1];
+            const float xx[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                p = __builtin_fmaf(__uint_as_float(wd[j] << 16), xx[2 * j], p);
+                p = __builtin_fmaf(__uint_as_float(wd[j] & 0xFFFF0000u), xx[2 * j + 1], p);
+            }
+        }
+        pc[t] = p;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float tot = pc[0];
+        for (int e = 1; e < nch; e++) tot = tot + pc[e];
+        inj_out[s] = tot;
+    }
+}
+
 // The mixer's first half at decode (one row) in one launch: inject + grouped
 // norm, the down-projection and the injection logits.  Every workgroup redoes
 // the inject and the norm of all S streams (S*H floats, from L2) into LDS --
@@ -233,7 +402,6 @@ static dim3 qh_grid(int64_t n)
 // block sum in wave order), and workgroup lowrank + s the injection logit s
 // in order R (a thread per 64-input chunk, chunk sums left to right).
 // Workgroup s < S writes stream s of h4_out and n4.  h4_out must not alias h4.
-#define QH_PRE_MAXS 4
 // NI > 0: each thread holds exactly NI float4s a stream (n4q <= NI * 256), all
 // loaded up front; NI == 0: a loop over them
 template <int NI>
@@ -251,110 +419,27 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_pre(float *__restrict__ h4_ou
     const int wave = t >> 6, lane = t & 63;
     const int words = HH / 8, groups = HH / G, nseg = HH / 32;
 
-    // the down row's weights first: their latency runs under the norm
+    // the down row's weights, requested after the streams: their latency runs
+    // under the norm
     uint4 wv[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
     float sc[2] = {0.0f, 0.0f}, bi[2] = {0.0f, 0.0f};
-    if (b < lowrank) {
+    auto weights = [&]() {
+        if (b < lowrank) {
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int seg = t + QH_THREADS * j;
-            if (seg < nseg) {
-                const int g = seg * 32 / G;
-                wv[j] = *reinterpret_cast<const uint4 *>(dn.w + (size_t)b * words + seg * 4);
-                sc[j] = qw_bf16(dn.s[(size_t)b * groups + g]);
-                bi[j] = qw_bf16(dn.b[(size_t)b * groups + g]);
+            for (int j = 0; j < 2; j++) {
+                const int seg = t + QH_THREADS * j;
+                if (seg < nseg) {
+                    const int g = seg * 32 / G;
+                    wv[j] = *reinterpret_cast<const uint4 *>(dn.w + (size_t)b * words + seg * 4);
+                    sc[j] = qw_bf16(dn.s[(size_t)b * groups + g]);
+                    bi[j] = qw_bf16(dn.b[(size_t)b * groups + g]);
+                }
             }
         }
-    }
+    };
 
-    // inject and the sums of squares of all streams together; per stream the
-    // order of k_norm_grouped (a chain over this thread's float4s ascending,
-    // the xor tree, the wave partials in order)
-    const float4 *orow = reinterpret_cast<const float4 *>(out);
-    float wgt[QH_PRE_MAXS], ss[QH_PRE_MAXS], inv[QH_PRE_MAXS];
-#pragma unroll
-    for (int s = 0; s < QH_PRE_MAXS; s++) {
-        wgt[s] = s < S ? 2.0f * qh_sigmoid(inj[s] / (float)S) : 0.0f;
-        ss[s] = 0.0f;
-    }
-    auto inject = [&](int s, int i, float4 v, float4 o) {
-        v.x += o.x * wgt[s]; v.y += o.y * wgt[s]; v.z += o.z * wgt[s]; v.w += o.w * wgt[s];
-        nl[s * n4q + i] = v;
-        if (b == s) reinterpret_cast<float4 *>(h4_out + (size_t)s * H)[i] = v;
-        ss[s] = __builtin_fmaf(v.x, v.x, ss[s]);
-        ss[s] = __builtin_fmaf(v.y, v.y, ss[s]);
-        ss[s] = __builtin_fmaf(v.z, v.z, ss[s]);
-        ss[s] = __builtin_fmaf(v.w, v.w, ss[s]);
-    };
-    auto scale = [&](int s, int i, uint2 wb) {
-        float4 v = nl[s * n4q + i];     // this thread's own values
-        v.x = v.x * inv[s] * __uint_as_float(wb.x << 16);
-        v.y = v.y * inv[s] * __uint_as_float(wb.x & 0xFFFF0000u);
-        v.z = v.z * inv[s] * __uint_as_float(wb.y << 16);
-        v.w = v.w * inv[s] * __uint_as_float(wb.y & 0xFFFF0000u);
-        nl[s * n4q + i] = v;
-        if (b == s) reinterpret_cast<float4 *>(n4 + (size_t)s * H)[i] = v;
-    };
-    constexpr int NR = NI > 0 ? NI : 1;
-    float4 hv[QH_PRE_MAXS][NR], ov[NR];
-    uint2 gw[QH_PRE_MAXS][NR];
-    if (NI > 0) {
-#pragma unroll
-        for (int j = 0; j < NR; j++) {
-            const int i = t + QH_THREADS * j;
-            const bool ok = i < n4q;
-            ov[j] = ok ? orow[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-            for (int s = 0; s < QH_PRE_MAXS; s++) {
-                const bool in = ok && s < S;
-                hv[s][j] = in ? reinterpret_cast<const float4 *>(h4 + (size_t)s * H)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-                gw[s][j] = in ? reinterpret_cast<const uint2 *>(wn + (size_t)s * H)[i] : make_uint2(0, 0);
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < NR; j++) {
-            const int i = t + QH_THREADS * j;
-#pragma unroll
-            for (int s = 0; s < QH_PRE_MAXS; s++)
-                if (s < S && i < n4q) inject(s, i, hv[s][j], ov[j]);
-        }
-    } else {
-        for (int i = t; i < n4q; i += QH_THREADS) {
-            const float4 o = orow[i];
-#pragma unroll
-            for (int s = 0; s < QH_PRE_MAXS; s++)
-                if (s < S) inject(s, i, reinterpret_cast<const float4 *>(h4 + (size_t)s * H)[i], o);
-        }
-    }
-#pragma unroll
-    for (int s = 0; s < QH_PRE_MAXS; s++) {
-        const float v = qw_xor_sum<64>(ss[s]);
-        if (lane == 0) part[s][wave] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < QH_PRE_MAXS; s++) {
-        float tot = part[s][0];
-#pragma unroll
-        for (int w = 1; w < QH_THREADS / 64; w++) tot = tot + part[s][w];
-        inv[s] = 1.0f / sqrtf(tot / (float)H + eps);
-    }
-    if (NI > 0) {
-#pragma unroll
-        for (int j = 0; j < NR; j++) {
-            const int i = t + QH_THREADS * j;
-#pragma unroll
-            for (int s = 0; s < QH_PRE_MAXS; s++)
-                if (s < S && i < n4q) scale(s, i, gw[s][j]);
-        }
-    } else {
-        for (int i = t; i < n4q; i += QH_THREADS) {
-#pragma unroll
-            for (int s = 0; s < QH_PRE_MAXS; s++)
-                if (s < S) scale(s, i, reinterpret_cast<const uint2 *>(wn + (size_t)s * H)[i]);
-        }
-    }
-    __syncthreads();
+    float inv[QH_PRE_MAXS];
+    qh_inject_norm<NI>(nl, part, b < S ? b : -1, h4_out, n4, h4, out, inj, wn, H, S, eps, inv, weights);
     if (b < lowrank) {
         float acc = 0.0f;
 #pragma unroll
@@ -381,36 +466,7 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_pre(float *__restrict__ h4_ou
         acc = qh_block_sum(acc, &part[0][0]);
         if (t == 0) d[b] = acc;
     } else {
-        const int s = b - lowrank, nch = HH / 64;
-        if (t < nch) {
-            // the chunk's 64 weights and inputs all requested before the chain
-            const uint4 *wr = reinterpret_cast<const uint4 *>(bj + (size_t)s * HH + 64 * t);
-            uint4 ww[8];
-            float4 xa[16];
-#pragma unroll
-            for (int q = 0; q < 8; q++) ww[q] = wr[q];
-#pragma unroll
-            for (int q = 0; q < 16; q++) xa[q] = nl[16 * t + q];
-            float p = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 8; q++) {
-                const uint32_t wd[4] = {ww[q].x, ww[q].y, ww[q].z, ww[q].w};
-                const float4 a = xa[2 * q], c = xa[2 * q + 1];
-                const float xx[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    p = __builtin_fmaf(__uint_as_float(wd[j] << 16), xx[2 * j], p);
-                    p = __builtin_fmaf(__uint_as_float(wd[j] & 0xFFFF0000u), xx[2 * j + 1], p);
-                }
-            }
-            pc[t] = p;
-        }
-        __syncthreads();
-        if (t == 0) {
-            float tot = pc[0];
-            for (int e = 1; e < nch; e++) tot = tot + pc[e];
-            inj_out[s] = tot;
-        }
+        qh_inj_logit(nl, pc, bj, b - lowrank, HH, inj_out);
     }
 }
 
@@ -503,5 +559,309 @@ extern "C" int qwk_hc_mix_up(hipStream_t s, float *x, const float *d, const floa
     const int lgG = group == 32 ? 5 : group == 64 ? 6 : 7;
     hipLaunchKernelGGL(k_hc_mix_up, dim3((unsigned)((H + 3) / 4)), dim3(QH_THREADS), 0, s, x, d, n4, w, sc, bi, k, H,
                        S, rows, scale, lgG);
+    return (int)hipGetLastError();
+}
+
+// ---- a whole decode step of the mixer in one launch ------------------------------
+//
+// k_hc_pre and k_hc_mix_up fused: the up-projection's weights are requested
+// at the start, so their memory latency runs under the norm and the
+// down-projection instead of after them.  Roles by workgroup:
+//
+//   b < nd           down: inject + norm (as k_hc_pre), then QH_DR rows of d,
+//                    their block sums together (each the order of k_hc_pre);
+//                    d leaves as tagged words {epoch, bits}; workgroup 0 also
+//                    publishes the streams' 1/rms.  Then, once those stores
+//                    are acknowledged, a done word in each of QH_DREP copies.
+//   nd <= b < nd+S   stream s = b - nd: inject + norm, writes stream s of
+//                    h4_out and n4 and the injection logit s (as k_hc_pre).
+//   the rest         up: OW = 32 / S outputs, 8 lanes on each of their S up
+//                    rows (lane: words lr, lr + 8, ...).  Weights in
+//                    registers first; then one wave polls the down
+//                    workgroups' done words (the copy of its XCD), the
+//                    workgroup reads d and 1/rms (tags checked), takes
+//                    silu(scale d) into LDS, and each row's dot meets in an
+//                    xor tree; n4's values for its outputs are recomputed
+//                    from h4, out and the 1/rms, and the streams mixed in
+//                    order.
+//
+// Nothing waits on a workgroup dispatched after it (the down workgroups come
+// first), and every wait is bounded: on giving up it raises the error word
+// (the launch's epoch, unless set) and the workgroup finishes.
+#define QH_DR 2                   // down rows a workgroup
+#define QH_MAX_LR 512             // lowrank
+#define QH_UP_NJ 8                // words an up lane holds (k <= 512)
+#define QH_DREP 8                 // copies of the done words
+#define QH_DSTRIDE 264            // words between copies (>= QH_MAX_LR / QH_DR)
+#define QH_TD 8                   // tag words: [0, S) 1/rms, [QH_TD, +lowrank) d,
+#define QH_TDONE (QH_TD + QH_MAX_LR)   // then the done copies
+#define QH_TAG_WORDS (QH_TDONE + QH_DREP * QH_DSTRIDE)
+#define QH_SPIN_LIMIT (1 << 16)
+
+
+__device__ __forceinline__ unsigned long long qh_ld(const uint2 *p)
+{
+    return __hip_atomic_load(reinterpret_cast<const unsigned long long *>(p), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void qh_st(uint2 *p, uint32_t epoch, uint32_t v)
+{
+    __hip_atomic_store(reinterpret_cast<unsigned long long *>(p), (unsigned long long)epoch | ((unsigned long long)v << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void qh_raise(uint32_t *err, uint32_t epoch)
+{
+    uint32_t expect = 0u;
+    __hip_atomic_compare_exchange_strong(err, &expect, epoch, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One wave: until words p[0, n) all hold the epoch; false (the error word
+// raised) if the wait gave up or another wait already had.
+__device__ bool qh_wait_words(const uint2 *p, int n, uint32_t *err, uint32_t epoch)
+{
+    const int lane = threadIdx.x & 63;
+    for (int spins = 0;; spins++) {
+        bool stale = false;
+        for (int i = lane; i < n; i += 64) stale |= (uint32_t)qh_ld(p + i) != epoch;
+        const uint32_t e = __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__ballot(stale) == 0ull) return true;
+        if (spins >= QH_SPIN_LIMIT || __ballot(e != 0u) != 0ull) {
+            if (lane == 0) qh_raise(err, epoch);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+struct QhArgs {
+    float *x, *h4_out, *n4, *d, *inj_out;
+    const float *h4, *out, *inj;
+    const uint16_t *wn, *bj;
+    qwk_q4 dn, up;
+    int H, S, lowrank, lgG, nd, ow;
+    float eps, scale;
+    uint32_t *err;
+    uint2 *tw;
+    uint32_t epoch;
+};
+
+template <int NI>
+__global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
+{
+    extern __shared__ float4 nl[];          // [S * H / 4]; the up role's staging
+    __shared__ float part[QH_PRE_MAXS][QH_THREADS / 64];
+    __shared__ float pc[QH_THREADS];
+    const int b = blockIdx.x, t = threadIdx.x, H = a.H, S = a.S, HH = S * H, k = a.lowrank;
+    const int wave = t >> 6, lane = t & 63;
+    QH_TS(0);
+#ifdef QH_TRACE
+    if (t == 0) qh_trace[blockIdx.x * 8 + 7] = __builtin_readcyclecounter();
+#endif
+    if (b < a.nd) {
+        const int words = HH / 8, groups = HH >> a.lgG, nseg = HH / 32, r0 = b * QH_DR;
+        // the rows' weights, requested after the streams: their latency runs
+        // under the norm
+        uint4 wv[QH_DR][2];
+        float sc[QH_DR][2], bi[QH_DR][2];
+        auto weights = [&]() {
+#pragma unroll
+            for (int q = 0; q < QH_DR; q++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int seg = t + QH_THREADS * j, r = r0 + q;
+                    const bool ok = seg < nseg && r < k;
+                    const int g = (seg * 32) >> a.lgG;
+                    wv[q][j] = ok ? *reinterpret_cast<const uint4 *>(a.dn.w + (size_t)r * words + seg * 4)
+                                  : make_uint4(0, 0, 0, 0);
+                    sc[q][j] = ok ? qw_bf16(a.dn.s[(size_t)r * groups + g]) : 0.0f;
+                    bi[q][j] = ok ? qw_bf16(a.dn.b[(size_t)r * groups + g]) : 0.0f;
+                }
+        };
+        float inv[QH_PRE_MAXS];
+        qh_inject_norm<NI>(nl, part, -1, a.h4_out, a.n4, a.h4, a.out, a.inj, a.wn, H, S, a.eps, inv, weights);
+        QH_TS(1);
+        float acc[QH_DR];
+#pragma unroll
+        for (int q = 0; q < QH_DR; q++) acc[q] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int seg = t + QH_THREADS * j;
+            if (seg < nseg) {
+                float xs[32];
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const float4 v = nl[seg * 8 + q];
+                    xs[4 * q] = v.x; xs[4 * q + 1] = v.y; xs[4 * q + 2] = v.z; xs[4 * q + 3] = v.w;
+                }
+                float xsum = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 32; e++) xsum += xs[e];
+#pragma unroll
+                for (int q = 0; q < QH_DR; q++) {
+                    float dd = qw_dot8_q(wv[q][j].x, xs, 0.0f);
+                    dd = qw_dot8_q(wv[q][j].y, xs + 8, dd);
+                    dd = qw_dot8_q(wv[q][j].z, xs + 16, dd);
+                    dd = qw_dot8_q(wv[q][j].w, xs + 24, dd);
+                    acc[q] = __builtin_fmaf(sc[q][j], dd, acc[q]);
+                    acc[q] = __builtin_fmaf(bi[q][j], xsum, acc[q]);
+                }
+            }
+        }
+        static_assert(QH_DR <= QH_PRE_MAXS, "the rows' partials share part");
+#pragma unroll
+        for (int q = 0; q < QH_DR; q++) {
+            const float v = qw_xor_sum<64>(acc[q]);
+            if (lane == 0) part[q][wave] = v;
+        }
+        __syncthreads();
+        if (t < QH_DR && r0 + t < k) {
+            float s = part[t][0];
+#pragma unroll
+            for (int w = 1; w < QH_THREADS / 64; w++) s = s + part[t][w];
+            a.d[r0 + t] = s;
+            qh_st(a.tw + QH_TD + r0 + t, a.epoch, __float_as_uint(s));
+        }
+        if (b == 0 && t >= 64 && t < 64 + S) qh_st(a.tw + (t - 64), a.epoch, __float_as_uint(inv[t - 64]));
+        // the tagged stores acknowledged before the done words say so
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        QH_TS(2);
+        if (t < QH_DREP) qh_st(a.tw + QH_TDONE + t * QH_DSTRIDE + b, a.epoch, 0u);
+        return;
+    }
+    if (b < a.nd + S) {
+        const int s = b - a.nd;
+        float inv[QH_PRE_MAXS];
+        qh_inject_norm<NI>(nl, part, s, a.h4_out, a.n4, a.h4, a.out, a.inj, a.wn, H, S, a.eps, inv, [] {});
+        QH_TS(1);
+        qh_inj_logit(nl, pc, a.bj, s, HH, a.inj_out);
+        QH_TS(2);
+        return;
+    }
+    // up
+    const int u = b - a.nd - S, ow = a.ow, i0 = u * ow;
+    const int rl = t >> 3, lr = t & 7, o = rl / S, s = rl % S;
+    const bool on = o < ow && i0 + o < H;
+    const int i = min(i0 + o, H - 1);
+    const size_t grow = (size_t)s * H + i;
+    const int words = k / 8, groups = k >> a.lgG;
+    uint32_t wq[QH_UP_NJ], sb[QH_UP_NJ];
+#pragma unroll
+    for (int j = 0; j < QH_UP_NJ; j++) {
+        const int wi = lr + 8 * j;
+        const bool ok = on && wi < words;
+        const size_t gi = grow * groups + ((8 * wi) >> a.lgG);
+        wq[j] = ok ? a.up.w[grow * words + wi] : 0u;
+        sb[j] = ok ? (uint32_t)a.up.s[gi] | ((uint32_t)a.up.b[gi] << 16) : 0u;
+    }
+    // this row's stream value with the block's output injected (as the
+    // inject of k_hc_pre), normed once the 1/rms is in
+    float v = 0.0f, wnv = 0.0f;
+    if (on && lr == 0) {
+        const float wgt = 2.0f * qh_sigmoid(a.inj[s] / (float)S);
+        v = a.h4[grow];
+        v += a.out[i] * wgt;
+        wnv = __uint_as_float((uint32_t)a.wn[grow] << 16);
+    }
+    float *xsl = reinterpret_cast<float *>(nl);            // [k]
+    float *invl = xsl + QH_MAX_LR;                          // [S]
+    float *mixv = invl + QH_PRE_MAXS;                       // [ow][S]
+    QH_TS(1);
+    // one wave polls the down workgroups' done words (its XCD's copy: the
+    // polling stays off the words the down workgroups write), then the
+    // workgroup reads d and 1/rms, every tag checked (the done words were
+    // stored after them, acknowledged, so a re-read is not expected)
+    __shared__ int fail;
+    if (t == 0) fail = 0;
+    __syncthreads();
+    if (wave == 0 && !qh_wait_words(a.tw + QH_TDONE + (b & (QH_DREP - 1)) * QH_DSTRIDE, a.nd, a.err, a.epoch))
+        fail = 1;
+    __syncthreads();
+    QH_TS(2);
+    if (!fail) {
+        for (int spins = 0;; spins++) {
+            bool stale = false;
+            for (int r = t; r < k + S; r += QH_THREADS) {
+                const unsigned long long q = qh_ld(r < k ? a.tw + QH_TD + r : a.tw + (r - k));
+                stale |= (uint32_t)q != a.epoch;
+                const float f = __uint_as_float((uint32_t)(q >> 32));
+                if (r < k) {
+                    const float dv = f * a.scale;
+                    xsl[r] = dv * qh_sigmoid(dv);
+                } else {
+                    invl[r - k] = f;
+                }
+            }
+            if (!__syncthreads_or(stale)) break;
+            if (spins >= QH_SPIN_LIMIT) {
+                if (t == 0) qh_raise(a.err, a.epoch);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    __syncthreads();
+    QH_TS(3);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < QH_UP_NJ; j++) {
+        const int wi = lr + 8 * j;
+        if (wi < words) {
+            const float sv = __uint_as_float(sb[j] << 16), bv = __uint_as_float(sb[j] & 0xFFFF0000u);
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                acc = __builtin_fmaf(__builtin_fmaf(sv, (float)((wq[j] >> (4 * e)) & 0xFu), bv), xsl[8 * wi + e], acc);
+        }
+    }
+    acc = qw_xor_sum<8>(acc);
+    if (on && lr == 0) mixv[o * S + s] = qh_sigmoid(acc) * (v * invl[s] * wnv);
+    __syncthreads();
+    if (t < ow && i0 + t < H) {
+        float mix = 0.0f;
+        for (int q = 0; q < S; q++) mix = mix + mixv[t * S + q];
+        a.x[i0 + t] = mix / (float)S;
+    }
+    QH_TS(4);
+#ifdef QH_TRACE
+    if (t == 0) qh_trace[blockIdx.x * 8 + 5] = __builtin_readcyclecounter();
+#endif
+}
+
+extern "C" size_t qwk_hc_decode_tag_words(void) { return QH_TAG_WORDS; }
+
+extern "C" int qwk_hc_decode(hipStream_t s, float *x, float *h4_out, float *n4, float *d, float *inj_out,
+                             const float *h4, const float *out, const float *inj, const uint16_t *wn, qwk_q4 dn,
+                             const uint16_t *bj, qwk_q4 up, int H, int S, int lowrank, int group, float eps,
+                             float scale, uint32_t *err, void *tags, uint32_t epoch)
+{
+    const int HH = S * H;
+    if (H <= 0 || H % 4 || S < 1 || S > QH_PRE_MAXS || HH % 64 || HH / 64 > QH_THREADS || HH > 15360 ||
+        lowrank < 8 || lowrank > QH_MAX_LR || lowrank % 8 || (group != 32 && group != 64 && group != 128) ||
+        HH % group || lowrank % group || h4_out == h4 || inj_out == inj || !err || !tags || epoch == 0u ||
+        ((uintptr_t)h4 & 15u) || ((uintptr_t)h4_out & 15u) || ((uintptr_t)n4 & 15u) || ((uintptr_t)out & 15u) ||
+        ((uintptr_t)wn & 7u) || ((uintptr_t)dn.w & 15u) || ((uintptr_t)bj & 15u) || ((uintptr_t)up.w & 3u))
+        return (int)hipErrorInvalidValue;
+    QhArgs a;
+    a.x = x; a.h4_out = h4_out; a.n4 = n4; a.d = d; a.inj_out = inj_out;
+    a.h4 = h4; a.out = out; a.inj = inj; a.wn = wn; a.bj = bj; a.dn = dn; a.up = up;
+    a.H = H; a.S = S; a.lowrank = lowrank; a.lgG = group == 32 ? 5 : group == 64 ? 6 : 7;
+    a.nd = (lowrank + QH_DR - 1) / QH_DR;
+    a.ow = 32 / S;
+    a.eps = eps; a.scale = scale;
+    a.err = err; a.tw = (uint2 *)tags; a.epoch = epoch;
+    const int nu = (H + a.ow - 1) / a.ow;
+    const int grid = a.nd + S + nu;
+    // LDS: the normed streams, or the up role's inputs, 1/rms and mix terms
+    const size_t lds = (size_t)HH * 4 > (size_t)(QH_MAX_LR + QH_PRE_MAXS + 32) * 4
+                           ? (size_t)HH * 4 : (size_t)(QH_MAX_LR + QH_PRE_MAXS + 32) * 4;
+    const int ni = (H / 4 + QH_THREADS - 1) / QH_THREADS;
+    switch (ni) {
+    case 1: hipLaunchKernelGGL(k_hc_decode<1>, dim3(grid), dim3(QH_THREADS), lds, s, a); break;
+    case 2: hipLaunchKernelGGL(k_hc_decode<2>, dim3(grid), dim3(QH_THREADS), lds, s, a); break;
+    case 3: hipLaunchKernelGGL(k_hc_decode<3>, dim3(grid), dim3(QH_THREADS), lds, s, a); break;
+    case 4: hipLaunchKernelGGL(k_hc_decode<4>, dim3(grid), dim3(QH_THREADS), lds, s, a); break;
+    default: hipLaunchKernelGGL(k_hc_decode<0>, dim3(grid), dim3(QH_THREADS), lds, s, a); break;
+    }
     return (int)hipGetLastError();
 }

@@ -127,6 +127,10 @@ int qwk_moe_decode_sync_error(const void *sync, uint32_t *err);
 /* Sets the error word as a failed wait of launch `epoch` would (synchronous);
  * every wait of a later launch then gives up at once. */
 int qwk_moe_decode_sync_raise(void *sync, uint32_t epoch);
+/* Another one-launch decode kernel (qwk_hc_decode) may share a hand-off
+ * state and its epochs: its error word and the 64-bit tagged words it may
+ * use (the two kernels run in stream order, so each finds only past epochs). */
+int qwk_decode_sync_words(void *sync, uint32_t **err, void **words, size_t *nwords);
 /* The allocation-free decode entry's device scratch (qw_static.hip): a
  * file-scope device array of this many bytes per GPU, holding the hand-off
  * state and then the staging area. */
@@ -203,6 +207,15 @@ int qwk_hc_pre_decode(hipStream_t s, float *h4_out, float *n4, float *d, float *
                       int H, int S, int lowrank, int group, float eps);
 int qwk_hc_mix(hipStream_t s, float *x, const float *n, const float *m, int rows, int H, int S);
 int qwk_hc_inject(hipStream_t s, float *h4, const float *out, const float *inj, int rows, int H, int S);
+/* A mixer decode step (one row) in one launch: qwk_hc_pre_decode and
+ * qwk_hc_mix_up(rows 1) fused, handing d over by tagged words in `tags`
+ * (qwk_hc_decode_tag_words() of them) under `epoch`; a wait that gives up
+ * raises *err.  lowrank <= 512, a multiple of 8 and of group. */
+size_t qwk_hc_decode_tag_words(void);
+int qwk_hc_decode(hipStream_t s, float *x, float *h4_out, float *n4, float *d, float *inj_out, const float *h4,
+                  const float *out, const float *inj, const uint16_t *wn, qwk_q4 dn, const uint16_t *bj, qwk_q4 up,
+                  int H, int S, int lowrank, int group, float eps, float scale, uint32_t *err, void *tags,
+                  uint32_t epoch);
 int qwk_hc_mix_up(hipStream_t s, float *x, const float *d, const float *n4, const uint32_t *w,
                   const uint16_t *sc, const uint16_t *bi, int k, int H, int S, int rows, float scale, int group);
 

@@ -389,7 +389,7 @@ static int dsync_check(int k, int force_reset) {
         for (qw_cmd q = G.live; q; q = q->next)
             if (q->ep_hi[k] >= first)
                 cmd_fail(q, hipErrorLaunchFailure,
-                         "moe_layer (decode): a hand-off wait gave up (launch %u of this state)", first);
+                         "decode: a hand-off wait gave up (launch %u of this state)", first);
     for (qw_cmd q = G.live; q; q = q->next) q->ep_hi[k] = 0;
     return first != 0 || force_reset ? dsync_reset(k) : 1;
 }
@@ -628,6 +628,56 @@ bool qw_op_hc_pre_decode(qw_cmd c, qw_ref h4_out, qw_ref n4, qw_ref d, qw_ref in
     const int rc = qwk_hc_pre_decode(G.stream, dp(h4_out), dp(n4), dp(d), dp(inj_out), dp(h4), dp(out), dp(inj),
                                      dp(norm_w), q4(down_w, down_s, down_b), dp(inj_w), H, S, lowrank, group, eps);
     launched(c, "hc_pre_decode", rc);
+    return rc == 0;
+}
+
+bool qw_op_hc_decode(qw_cmd c, qw_ref x, qw_ref h4_out, qw_ref n4, qw_ref d, qw_ref inj_out, qw_ref h4,
+                     qw_ref out, qw_ref inj, qw_ref norm_w, qw_ref down_w, qw_ref down_s, qw_ref down_b,
+                     qw_ref inj_w, qw_ref up_w, qw_ref up_s, qw_ref up_b, int32_t H, int32_t S, int32_t lowrank,
+                     int32_t group, float eps, float scale) {
+    const int32_t HH = S * H;
+    if (H < 4 || H % 4 || S < 1 || S > 4 || HH % 64 || HH > 15360 || lowrank < 8 || lowrank > 512 ||
+        lowrank % 8 || (group != 32 && group != 64 && group != 128) || HH % group || lowrank % group)
+        return false;
+    /* as qw_op_hc_pre_decode: no output shares a byte with an input or
+     * another output (x included) */
+    const qw_ref outs[5] = { h4_out, n4, d, inj_out, x }, ins[3] = { h4, out, inj };
+    const size_t lo[5] = { 4u * (size_t)HH, 4u * (size_t)HH, 4u * (size_t)lowrank, 4u * (size_t)S, 4u * (size_t)H };
+    const size_t li[3] = { 4u * (size_t)HH, 4u * (size_t)H, 4u * (size_t)S };
+    for (int i = 0; i < 5; i++) {
+        for (int j = 0; j < 3; j++) if (refs_overlap(outs[i], lo[i], ins[j], li[j])) return false;
+        for (int j = i + 1; j < 5; j++) if (refs_overlap(outs[i], lo[i], outs[j], lo[j])) return false;
+    }
+    if (!c) return true;
+    touch(c, h4, 0); touch(c, out, 0); touch(c, inj, 0); touch(c, norm_w, 0);
+    touch(c, down_w, 0); touch(c, down_s, 0); touch(c, down_b, 0); touch(c, inj_w, 0);
+    touch(c, up_w, 0); touch(c, up_s, 0); touch(c, up_b, 0);
+    touch(c, h4_out, 1); touch(c, n4, 1); touch(c, d, 1); touch(c, inj_out, 1); touch(c, x, 1);
+    /* the decode hand-off state and its epochs, shared with the MoE decode
+     * launch (stream order keeps them apart) */
+    const int k = QW_DS_HEAP;
+    if (!G.ds[k].sync && !dsync_reset(k)) {
+        cmd_fail(c, hipErrorOutOfMemory, "hc_decode: decode hand-off state");
+        return false;
+    }
+    if (G.ds[k].epoch == UINT32_MAX && !dsync_check(k, 1)) {
+        cmd_fail(c, hipErrorUnknown, "hc_decode: decode hand-off state");
+        return false;
+    }
+    uint32_t *err = NULL;
+    void *words = NULL;
+    size_t nwords = 0;
+    qwk_decode_sync_words(G.ds[k].sync, &err, &words, &nwords);
+    if (nwords < qwk_hc_decode_tag_words()) {
+        cmd_fail(c, hipErrorInvalidValue, "hc_decode: hand-off state too small");
+        return false;
+    }
+    const uint32_t epoch = ++G.ds[k].epoch;
+    const int rc = qwk_hc_decode(G.stream, dp(x), dp(h4_out), dp(n4), dp(d), dp(inj_out), dp(h4), dp(out), dp(inj),
+                                 dp(norm_w), q4(down_w, down_s, down_b), dp(inj_w), q4(up_w, up_s, up_b), H, S,
+                                 lowrank, group, eps, scale, err, words, epoch);
+    c->ep_hi[k] = epoch;
+    launched(c, "hc_decode", rc);
     return rc == 0;
 }
 

@@ -130,6 +130,7 @@ _sig("qw_op_rms_norm", None, _P, _R, _R, _R, _I, _I, C.c_float, C.c_float)
 _sig("qw_op_hc_inject_norm", None, _P, _R, _R, _R, _R, _R, _I, _I, _I, C.c_float)
 _sig("qw_op_hc_pre_decode", _B, _P, _R, _R, _R, _R, _R, _R, _R, _R, _R, _R, _R, _R, _I, _I, _I, _I, C.c_float)
 _sig("qw_op_hc_mix_up", _B, _P, _R, _R, _R, _R, _R, _R, _I, _I, _I, _I, C.c_float, _I)
+_sig("qw_op_hc_decode", _B, _P, _R, _R, _R, _R, _R, _R, _R, _R, _R, _R, _R, _R, _R, _R, _R, _R, _I, _I, _I, _I, C.c_float, C.c_float)
 _sig("qw_op_repeat_cols", None, _P, _R, _R, _I, _I, _I)
 _sig("qw_op_rms_norm_grouped", None, _P, _R, _R, _R, _I, _I, _I, C.c_float)
 _sig("qw_op_silu_scale", None, _P, _R, _I, C.c_float)

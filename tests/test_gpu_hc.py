@@ -200,3 +200,105 @@ def test_pre_decode_fused(gpu, H, S, k, G):
     assert np.allclose(n4, ref.rms_norm_grouped(h_out.read(np.float32, (1, S * H)), wn, H, S, 1e-6),
                        rtol=2e-5, atol=0)
     assert np.array_equal(u32(i_f, S), ref.dmat_bf16(n4, binj, S * H, S, 1).view(np.uint32))
+
+
+@pytest.mark.parametrize("H,S,k,G", [(3072, 4, 320, 64), (1024, 4, 96, 32), (256, 2, 128, 128), (7680, 2, 64, 64),
+                                     (1536, 3, 64, 32), (2048, 1, 512, 64)])
+def test_hc_decode_one_launch(gpu, H, S, k, G):
+    """qw_op_hc_decode (the whole step in one launch, d handed over between
+    workgroups) against qw_op_hc_pre_decode + qw_op_hc_mix_up on the same
+    inputs: h4_out, n4, d and the injection logits bit-exact (the same
+    arithmetic in the same order), x against the oracle on the GPU's own
+    d and n4 (rel-L2 1e-5, as the mix-up op); three steps in a row, each on
+    the last one's streams, so every launch takes a new epoch."""
+    print(f"hc decode H={H} S={S} k={k} G={G}", flush=True)
+    g = _rng(41 + H + k)
+    h4 = g.standard_normal((1, S * H)).astype(np.float32)
+    wn = synth.to_bf16(1.0 + 0.05 * g.standard_normal(S * H).astype(np.float32))
+    down = _q4(42 + H, "hcd.down", k, S * H, G)
+    up = _q4(43 + H, "hcd.up", S * H, k, G)
+    binj = synth.to_bf16((0.02 * g.standard_normal((S, S * H))).astype(np.float32))
+    B = gpu.Buf
+    wnb, bjb = B.of(wn), B.of(binj)
+    dwb, dsb, dbb = B.of(down.w), B.of(down.s), B.of(down.b)
+    uwb, usb, ubb = B.of(up.w), B.of(up.s), B.of(up.b)
+    u32 = lambda b, n: b.read(np.float32, (1, n)).view(np.uint32)
+    cur = h4
+    for step in range(3):
+        prev = g.standard_normal((1, H)).astype(np.float32)
+        pinj = g.standard_normal((1, S)).astype(np.float32)
+        hb, pb, ib = B.of(cur), B.of(prev), B.of(pinj)
+        h_s, n_s, d_s, i_s, x_s = B(S * H * 4), B(S * H * 4), B(k * 4), B(S * 4), B(H * 4)
+        h_f, n_f, d_f, i_f, x_f = B(S * H * 4), B(S * H * 4), B(k * 4), B(S * 4), B(H * 4)
+        c = gpu.qw_cmd_begin()
+        assert gpu.qw_op_hc_pre_decode(c, h_s.ref(), n_s.ref(), d_s.ref(), i_s.ref(), hb.ref(), pb.ref(), ib.ref(),
+                                       wnb.ref(), dwb.ref(), dsb.ref(), dbb.ref(), bjb.ref(), H, S, k, G, 1e-6)
+        assert gpu.qw_op_hc_mix_up(c, x_s.ref(), d_s.ref(), n_s.ref(), uwb.ref(), usb.ref(), ubb.ref(), k, H, S, 1,
+                                   1.0 / S, G)
+        assert gpu.qw_op_hc_decode(c, x_f.ref(), h_f.ref(), n_f.ref(), d_f.ref(), i_f.ref(), hb.ref(), pb.ref(),
+                                   ib.ref(), wnb.ref(), dwb.ref(), dsb.ref(), dbb.ref(), bjb.ref(), uwb.ref(),
+                                   usb.ref(), ubb.ref(), H, S, k, G, 1e-6, 1.0 / S)
+        assert not gpu.qw_op_hc_decode(c, x_f.ref(), hb.ref(), n_f.ref(), d_f.ref(), i_f.ref(), hb.ref(), pb.ref(),
+                                       ib.ref(), wnb.ref(), dwb.ref(), dsb.ref(), dbb.ref(), bjb.ref(), uwb.ref(),
+                                       usb.ref(), ubb.ref(), H, S, k, G, 1e-6, 1.0 / S), "h4_out aliasing h4"
+        gpu.run(c, f"hc decode step {step}")
+        assert np.array_equal(u32(h_f, S * H), u32(h_s, S * H)), "injected streams"
+        assert np.array_equal(u32(n_f, S * H), u32(n_s, S * H)), "normed streams"
+        assert np.array_equal(u32(i_f, S), u32(i_s, S)), "injection logits"
+        assert np.array_equal(u32(d_f, k), u32(d_s, k)), "down-projection"
+        n4 = n_f.read(np.float32, (1, S * H))
+        d = d_f.read(np.float32, (1, k))
+        want = ref.hc_mix_up(d, n4, up.w, up.s, up.b, k, H, S, 1, 1.0 / S, G)
+        e = rel_l2(x_f.read(np.float32, (1, H)), want)
+        assert e < 1e-5, f"step {step}: rel-L2 {e:.3g}"
+        assert rel_l2(x_f.read(np.float32, (1, H)), x_s.read(np.float32, (1, H))) < 1e-5
+        cur = h_f.read(np.float32, (1, S * H))
+
+
+def test_hc_decode_refusals(gpu):
+    """Shapes the one launch does not take are refused with nothing encoded
+    (no command is needed to ask)."""
+    r = gpu.NULL_REF
+    args = lambda H, S, k, G: (None, r, r, r, r, r, r, r, r, r, r, r, r, r, r, r, r, H, S, k, G, 1e-6, 0.25)
+    assert gpu.qw_op_hc_decode(*args(3072, 4, 320, 64))
+    assert not gpu.qw_op_hc_decode(*args(3072, 5, 320, 64)), "S above 4"
+    assert not gpu.qw_op_hc_decode(*args(3072, 4, 576, 64)), "lowrank above 512"
+    assert not gpu.qw_op_hc_decode(*args(3072, 4, 100, 32)), "lowrank not a multiple of 8 and of the group"
+    assert not gpu.qw_op_hc_decode(*args(4096, 4, 320, 64)), "S*H above 15360"
+
+
+def test_hc_decode_give_up(gpu):
+    """With the hand-off error word raised (as if a wait had given up), the
+    one launch still ends (its waits see the word and give up at once), the
+    command reports the failure, and the next launch runs normally."""
+    H, S, k, G = 1024, 4, 96, 32
+    g = _rng(4400)
+    h4 = g.standard_normal((1, S * H)).astype(np.float32)
+    prev = g.standard_normal((1, H)).astype(np.float32)
+    pinj = g.standard_normal((1, S)).astype(np.float32)
+    wn = synth.to_bf16(1.0 + 0.05 * g.standard_normal(S * H).astype(np.float32))
+    down, up = _q4(4401, "hcg.down", k, S * H, G), _q4(4402, "hcg.up", S * H, k, G)
+    binj = synth.to_bf16((0.02 * g.standard_normal((S, S * H))).astype(np.float32))
+    B = gpu.Buf
+    ins = [B.of(a) for a in (h4, prev, pinj, wn, down.w, down.s, down.b, binj, up.w, up.s, up.b)]
+    outs = [B(S * H * 4), B(S * H * 4), B(k * 4), B(S * 4), B(H * 4)]
+    hb, pb, ib, wnb, dwb, dsb, dbb, bjb, uwb, usb, ubb = ins
+    h_f, n_f, d_f, i_f, x_f = outs
+
+    def step():
+        c = gpu.qw_cmd_begin()
+        assert gpu.qw_op_hc_decode(c, x_f.ref(), h_f.ref(), n_f.ref(), d_f.ref(), i_f.ref(), hb.ref(), pb.ref(),
+                                   ib.ref(), wnb.ref(), dwb.ref(), dsb.ref(), dbb.ref(), bjb.ref(), uwb.ref(),
+                                   usb.ref(), ubb.ref(), H, S, k, G, 1e-6, 1.0 / S)
+        gpu.qw_cmd_wait(c)
+        e = gpu.qw_cmd_error(c)
+        gpu.qw_cmd_free(c)
+        return e
+
+    assert gpu.qw_debug_decode_handoff_fail()
+    e = step()
+    assert e is not None and b"hand-off wait gave up" in e
+    assert step() is None
+    want = ref.hc_mix_up(d_f.read(np.float32, (1, k)), n_f.read(np.float32, (1, S * H)), up.w, up.s, up.b, k, H,
+                         S, 1, 1.0 / S, G)
+    assert rel_l2(x_f.read(np.float32, (1, H)), want) < 1e-5
