@@ -82,7 +82,14 @@ extern "C" int qd_hwid_read(unsigned int *dst)
 #define QD_DOWN_LPR 16
 #define QD_DOWN_RIT 4               // down rows per lane slot
 #define QD_DOWN_RPG ((64 / QD_DOWN_LPR) * QD_DOWN_RIT)
-#define QD_SPIN_LIMIT (1 << 16)     // polls (each a memory round trip plus a sleep)
+#define QD_SPIN_LIMIT (1 << 16)
+// The sleep between polls (s_sleep units of 64 clocks): a longer one lets
+// the polled memory settle (A/B on config 1: 0 -> 23.70, 1 -> 23.45,
+// 4 -> 23.35, 8 -> 23.09–23.18, 16 -> 23.14–23.20 µs a token).
+#ifndef QD_SLEEP
+#define QD_SLEEP 8
+#endif
+#define QD_POLL_SLEEP() do { if (QD_SLEEP > 0) __builtin_amdgcn_s_sleep(QD_SLEEP); } while (0)     // polls (each a memory round trip plus a sleep)
 
 static_assert(QWK_DECODE_MAX_K + 1 <= QD_WAVES, "down: one wave per matrix");
 // down: the K + 1 activation vectors (at most 64 units each), one LDS region a wave
@@ -214,7 +221,7 @@ __device__ __forceinline__ uint2 qd_poll_tag(const QdArgs &a, const uint2 *p, bo
             if ((threadIdx.x & 63) == 0) qd_raise(a.sync, a.epoch);
             return r;
         }
-        __builtin_amdgcn_s_sleep(1);
+        QD_POLL_SLEEP();
     }
 }
 
@@ -242,7 +249,7 @@ __device__ __forceinline__ void qd_wait_rdone(const QdArgs &a)
             if (lane == 0) qd_raise(a.sync, a.epoch);
             return;
         }
-        __builtin_amdgcn_s_sleep(1);
+        QD_POLL_SLEEP();
     }
 }
 
@@ -444,9 +451,11 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
         if (t == 0) QD_TS(4);
         if (row) qd_router_row(w, xl, nch, a.sync->lgt + (size_t)t * (E + 1) + o, a.epoch, part);
     }
+#ifndef QD_NO_ACK
     // the logit stores are acknowledged (past this XCD's L2) before the
     // done words say so
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#endif
     __syncthreads();
     if (threadIdx.x < QD_RDREP)
         __hip_atomic_store(reinterpret_cast<unsigned long long *>(a.sync->rdone + threadIdx.x * QD_RDSTRIDE + b),
@@ -841,7 +850,7 @@ __device__ __forceinline__ bool qd_wait_tact(const QdArgs &a, int v, int units, 
             if (lane == 0) qd_raise(a.sync, a.epoch);
             return false;
         }
-        __builtin_amdgcn_s_sleep(1);
+        QD_POLL_SLEEP();
     }
 }
 

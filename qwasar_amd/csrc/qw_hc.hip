@@ -597,6 +597,9 @@ extern "C" int qwk_hc_mix_up(hipStream_t s, float *x, const float *d, const floa
 #define QH_TDONE (QH_TD + QH_MAX_LR)   // then the done copies
 #define QH_TAG_WORDS (QH_TDONE + QH_DREP * QH_DSTRIDE)
 #define QH_SPIN_LIMIT (1 << 16)
+#ifndef QH_SLEEP
+#define QH_SLEEP 1                // s_sleep between polls (units of 64 clocks)
+#endif
 
 
 __device__ __forceinline__ unsigned long long qh_ld(const uint2 *p)
@@ -630,7 +633,7 @@ __device__ bool qh_wait_words(const uint2 *p, int n, uint32_t *err, uint32_t epo
             if (lane == 0) qh_raise(err, epoch);
             return false;
         }
-        __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_s_sleep(QH_SLEEP);
     }
 }
 
@@ -798,7 +801,7 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
                 if (t == 0) qh_raise(a.err, a.epoch);
                 break;
             }
-            __builtin_amdgcn_s_sleep(1);
+            __builtin_amdgcn_s_sleep(QH_SLEEP);
         }
     }
     __syncthreads();
