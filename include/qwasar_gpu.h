@@ -371,6 +371,15 @@ bool qw_op_moe_layer(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,
  * than h and y_prev.  False (nothing encoded) where qw_op_moe_layer refuses. */
 bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref h, qw_ref y_prev,
                               qw_ref h_out, qw_ref x_out, const qw_moe_layer *M, int32_t rows, float eps);
+/* The same, with the layer that runs next: at decode sizes the launch also
+ * reads that layer's router rows and shared gate row (when it has this
+ * layer's E and H) once its own router rows are out, so that the next
+ * launch finds them in the caches.  No counterpart in the reference: for
+ * drivers of a layer stack, which know the next layer.  next may be NULL
+ * (then exactly qw_op_moe_layer_residual). */
+bool qw_op_moe_layer_residual_next(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref h, qw_ref y_prev,
+                                   qw_ref h_out, qw_ref x_out, const qw_moe_layer *M, const qw_moe_layer *next,
+                                   int32_t rows, float eps);
 
 /* qw_op_moe_layer's decode path (rows <= 8) with no allocation.  No
  * counterpart in the reference: for callers that cannot allocate device

@@ -192,6 +192,7 @@ struct QdArgs {
     uint16_t *hout;                 // bf16(hin + yprev), written by workgroup 0
     float *xout;                    // that x, written by workgroup 0
     float eps;
+    const uint16_t *pf_router, *pf_gate_w;   // the next layer's router rows, to read ahead (may be null)
     float *out;
     int32_t *idx;
     float *w;
@@ -461,8 +462,21 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
         __hip_atomic_store(reinterpret_cast<unsigned long long *>(a.sync->rdone + threadIdx.x * QD_RDSTRIDE + b),
                            (unsigned long long)a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     QD_TS(2);
-    if constexpr (RES)
+    if constexpr (RES) {
         if (b == 0) qd_write_resid(a, qinv);
+        // In a stack, the next layer's router workgroup b (same block, same
+        // XCD) reads these same rows: read them now, while this layer's
+        // experts stream, so that the next launch's router finds them in the
+        // caches instead of HBM.
+        if (a.pf_router && row) {
+            const uint16_t *pr = o < E ? a.pf_router + (size_t)o * H : a.pf_gate_w;
+            uint4 t[8];
+#pragma unroll
+            for (int r = 0; r < 8; r++) t[r] = reinterpret_cast<const uint4 *>(pr)[min(lane + 64 * r, H / 8 - 1)];
+#pragma unroll
+            for (int r = 0; r < 8; r++) asm volatile("" ::"v"(t[r].x));
+        }
+    }
 }
 
 // ---- gate / up rows with SwiGLU ----------------------------------------------------
@@ -1096,6 +1110,8 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     a.yprev = res ? res->y : nullptr;
     a.hout = res ? res->h_out : nullptr;
     a.xout = res ? res->x_out : nullptr;
+    a.pf_router = res ? res->next_router : nullptr;
+    a.pf_gate_w = res ? res->next_gate_w : nullptr;
     a.eps = res ? res->eps : 0.0f;
     a.umax = rows * M->K < M->E ? rows * M->K : M->E;
     a.lgG = G == 32 ? 5 : G == 64 ? 6 : 7;

@@ -156,6 +156,10 @@ typedef struct {
     uint16_t *h_out;
     float *x_out;
     float eps;
+    /* When not NULL: the router rows (bf16 [E, H]) and shared gate row of
+     * the layer that runs next, read by the router workgroups once their
+     * own rows are out so that the next launch finds them in the caches. */
+    const uint16_t *next_router, *next_gate_w;
 } qwk_resid;
 
 /* Decode (rows <= QWK_DECODE_MAX_ROWS, K <= QWK_DECODE_MAX_K), one launch:

@@ -1048,6 +1048,12 @@ bool qw_op_moe_layer_noalloc(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref 
 
 bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref h, qw_ref y_prev,
                               qw_ref h_out, qw_ref x_out, const qw_moe_layer *M, int32_t rows, float eps) {
+    return qw_op_moe_layer_residual_next(c, out, idx, w, h, y_prev, h_out, x_out, M, NULL, rows, eps);
+}
+
+bool qw_op_moe_layer_residual_next(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref h, qw_ref y_prev,
+                                   qw_ref h_out, qw_ref x_out, const qw_moe_layer *M, const qw_moe_layer *next,
+                                   int32_t rows, float eps) {
     if (!moe_layer_ok(M, rows) || !h.buf || !h_out.buf || !x_out.buf) return false;
     if (h_out.buf == h.buf || (y_prev.buf && h_out.buf == y_prev.buf)) return false;
     if (!c) return true;
@@ -1063,7 +1069,12 @@ bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref
         if (rc != 0) return false;
         return moe_prefill(c, dp(out), dp(idx), dp(w), dp(x_out), M, rows);
     }
-    const qwk_resid res = { dp(h), dp(y_prev), dp(h_out), dp(x_out), eps };
+    /* the next layer's router is read ahead only when it has this one's shape */
+    const int ahead = next && next->router.buf && next->sh_gate_w.buf && next->E == M->E && next->H == M->H;
+    if (ahead) { touch(c, next->router, 0); touch(c, next->sh_gate_w, 0); }
+    const qwk_resid res = { dp(h), dp(y_prev), dp(h_out), dp(x_out), eps,
+                            ahead ? (const uint16_t *)dp(next->router) : NULL,
+                            ahead ? (const uint16_t *)dp(next->sh_gate_w) : NULL };
     return moe_decode(c, dp(out), dp(idx), dp(w), NULL, &res, &m, rows, QW_DS_HEAP);
 }
 
