@@ -211,7 +211,10 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
         const int L = i * (G16_THREADS / 8) + (t >> 3), row = L / LPR, seg = L % LPR;
         const int sr = srow[row];
         if (sr >= 0) aokm |= 1u << i;
-        offA[i] = (uint32_t)(((sr >= 0 ? sr : 0) * k + seg * 64 + (t & 7) * 8) * 2);
+        // a row outside the tile gets an offset past the descriptor's range:
+        // its lanes read zeros without touching memory (the instruction is
+        // still issued, so the counted waits below stay exact)
+        offA[i] = sr >= 0 ? (uint32_t)((sr * k + seg * 64 + (t & 7) * 8) * 2) : 0x80000000u;
         ldsA[i] = (uint16_t)(row * AST + seg * 64 + (t & 7) * 8);
     }
     g16_u4 ra[AU4];
