@@ -401,6 +401,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     __syncthreads();
     for (int j0 = j_lo; j0 < j_hi; j0 += QA_P) {
         const int n = min(QA_P, j_hi - j0);
+        // the pass's value rows are requested first, with the keys below: both
+        // depend only on the list, so neither waits for the scores
+        const int jb = (QA_P / 4) * wave, nj = max(0, min(QA_P / 4, n - jb));
+        uint2 vv[QA_P / 4];
+#pragma unroll
+        for (int i = 0; i < QA_P / 4; i++)
+            if (i < nj) vv[i] = *reinterpret_cast<const uint2 *>(vbase + (size_t)lr[1 + j0 + jb + i] * QA_D + 4 * lane);
         // scores: eight threads per position, 32 dims each (one 64-byte
         // piece of the fp16 key row), every load issued first; the eight
         // partial dots meet in the xor tree of their 8-lane run
@@ -477,13 +484,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
             for (int i = 0; i < 4; i++) acc[g][i] *= rescale[g];
         }
         // values: wave w takes the pass's positions 8w..8w+7, lane dims
-        // 4l..4l+3; the rows are requested before any is used
+        // 4l..4l+3 (their rows were requested with the keys)
         {
-            const int jb = (QA_P / 4) * wave, nj = max(0, min(QA_P / 4, n - jb));
-            uint2 vv[QA_P / 4];
-#pragma unroll
-            for (int i = 0; i < QA_P / 4; i++)
-                if (i < nj) vv[i] = *reinterpret_cast<const uint2 *>(vbase + (size_t)lr[1 + j0 + jb + i] * QA_D + 4 * lane);
 #pragma unroll
             for (int i = 0; i < QA_P / 4; i++) {
                 if (i < nj) {
@@ -567,26 +569,41 @@ __global__ void __launch_bounds__(256) k_attn_merge(float *__restrict__ out, con
     const int g = blockIdx.x % G, rk = blockIdx.x / G, row = rk / kv_heads, kvh = rk % kv_heads, t = threadIdx.x;
     const size_t stride = (size_t)G * (QA_D + 2);
     const float *pr = part + (size_t)rk * nsplit * stride;
+    // dim t of every split's output, requested with the maxima and sums (one
+    // round trip for the kernel's loads)
+    float a[QA_MAX_SPLITS];
+#pragma unroll
+    for (int s = 0; s < QA_MAX_SPLITS; s++)
+        if (s < nsplit) a[s] = pr[s * stride + 2 * G + (size_t)g * QA_D + t];
     if (t < nsplit) {
         sm[t] = pr[t * stride + g];
         sl[t] = pr[t * stride + G + g];
     }
     __syncthreads();
-    if (t == 0) {
-        float M = -FLT_MAX;
-        for (int s = 0; s < nsplit; s++) M = fmaxf(M, sm[s]);
-        float L = 0.0f;
-        for (int s = 0; s < nsplit; s++) {
-            sf[s] = expf(sm[s] - M);
-            L = __builtin_fmaf(sl[s], sf[s], L);
-        }
-        sL = L;
+    // the maximum, each split's factor and the weighted sum of the splits'
+    // sums, a lane a split (up to 128: two waves), the sum in a fixed tree
+    // (each wave's xor tree, then wave 0's plus wave 1's)
+    __shared__ float wmax[2], wsum[2];
+    if (t < 128) {
+        float v = t < nsplit ? sm[t] : -FLT_MAX;
+        v = qw_wave_max(v);
+        if ((t & 63) == 0) wmax[t >> 6] = v;
     }
     __syncthreads();
-    float a[QA_MAX_SPLITS];
-#pragma unroll
-    for (int s = 0; s < QA_MAX_SPLITS; s++)
-        if (s < nsplit) a[s] = pr[s * stride + 2 * G + (size_t)g * QA_D + t];
+    if (t < 128) {
+        const float M = fmaxf(wmax[0], wmax[1]);
+        float f = 0.0f, c = 0.0f;
+        if (t < nsplit) {
+            f = expf(sm[t] - M);
+            sf[t] = f;
+            c = sl[t] * f;
+        }
+        c = qw_xor_sum<64>(c);
+        if ((t & 63) == 0) wsum[t >> 6] = c;
+    }
+    __syncthreads();
+    if (t == 0) sL = wsum[0] + wsum[1];
+    __syncthreads();
     float A = 0.0f;
 #pragma unroll
     for (int s = 0; s < QA_MAX_SPLITS; s++)
