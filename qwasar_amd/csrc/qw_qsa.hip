@@ -26,15 +26,19 @@
 // T of the last block taken (scores of similar size share their leading
 // bits: counted from bit 31 they would pile into a few bins and serialise
 // the atomics); keys above T are taken and the rest of the budget comes from keys
-// equal to T in block order.  Each thread owns a contiguous run of blocks, so
-// block order is thread order and the position list is one prefix sum.
+// equal to T in block order.  One wave sums the bins and finds the cut with a
+// suffix scan over its lanes; a pass whose cut bin holds exactly the blocks
+// still needed ends the search.  Each thread owns a contiguous run of blocks,
+// its keys loaded at once into registers, so block order is thread order and
+// the position list is one prefix sum.
 //
 // Masked attention (k_attn_masked<G>): a workgroup per (query row, kv head,
 // split of the position list) with its G query heads.  Positions go 32 at a
-// time: eight threads per position score its fp16 key row against the G
-// heads, the pass's maxima and exponentials update an online softmax, and
-// the waves accumulate the pass's value rows with lanes over dims (each value
-// row one coalesced 512-byte read).  When rows x kv heads alone would leave
+// time, 8 a wave: eight lanes per position score its fp16 key row against
+// the G heads, each wave's maxima and weights (2^(s - max), scores in log2
+// units) update its own online softmax, and the wave accumulates its
+// positions' value rows with lanes over dims (each value row one coalesced
+// 512-byte read); the four waves' states meet at the end.  When rows x kv heads alone would leave
 // the chip idle (decode), the list is split over enough workgroups to fill
 // it and k_attn_merge combines the splits' softmax states in split order.
 #include "qw_device.h"
@@ -207,21 +211,6 @@ __device__ __forceinline__ uint32_t qs_key(float v)
     return (u >> 31) ? ~u : (u | 0x80000000u);
 }
 
-// Minimum over the workgroup; every thread calls it and gets the result.
-__device__ __forceinline__ uint32_t qs_block_min(uint32_t v, uint32_t *wt)
-{
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, 64));
-    if (lane == 0) wt[wave] = v;
-    __syncthreads();
-    uint32_t r = wt[0];
-#pragma unroll
-    for (int w = 1; w < QS_SEL_WAVES; w++) r = min(r, wt[w]);
-    __syncthreads();
-    return r;
-}
-
 // Exclusive prefix sum of one value per thread over the workgroup, thread
 // order; *total gets the sum.  Every thread calls it.
 __device__ __forceinline__ uint32_t qs_scan(uint32_t v, uint32_t *wt, uint32_t *total)
@@ -251,10 +240,32 @@ __device__ __forceinline__ uint32_t qs_scan(uint32_t v, uint32_t *wt, uint32_t *
     return r;
 }
 
+// Built with -DQS_TRACE, thread 0 of each selection workgroup stamps the
+// device wall clock (100 MHz) at its phases into qs_trace[row][slot].
+#ifdef QS_TRACE
+__device__ unsigned long long qs_trace[64 * 16];
+#define QS_TS(slot) do { if (threadIdx.x == 0 && blockIdx.x < 64) qs_trace[blockIdx.x * 16 + (slot)] = wall_clock64(); } while (0)
+extern "C" int qs_trace_read(unsigned long long *dst)
+{
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(qs_trace), sizeof(qs_trace));
+}
+__device__ unsigned long long qa_trace[1024 * 16];
+#define QA_TS(slot) do { if (threadIdx.x == 0 && blockIdx.x < 1024) qa_trace[blockIdx.x * 16 + (slot)] = wall_clock64(); } while (0)
+#define QA_TSV(slot, v) do { if (threadIdx.x == 0 && blockIdx.x < 1024) qa_trace[blockIdx.x * 16 + (slot)] = (v) == 0x12345 ? 0 : wall_clock64(); } while (0)
+extern "C" int qa_trace_read(unsigned long long *dst)
+{
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(qa_trace), sizeof(qa_trace));
+}
+#else
+#define QS_TS(slot) do { } while (0)
+#define QA_TS(slot) do { } while (0)
+#define QA_TSV(slot, v) do { } while (0)
+#endif
+
 #define QS_SEL_KREG 8      // keys a thread keeps in registers (up to 8192 blocks)
 
 // A thread's contiguous run of blocks [lo, hi): its keys, from registers
-// when the run fits (every load issued at once), else from the scores.
+// when the run fits, else from the scores.
 #define QS_RUN(body)                                                              \
     if (in_regs) {                                                                \
         _Pragma("unroll") for (int i = 0; i < QS_SEL_KREG; i++)                   \
@@ -263,95 +274,214 @@ __device__ __forceinline__ uint32_t qs_scan(uint32_t v, uint32_t *wt, uint32_t *
         for (int b = lo; b < hi; b++) { const uint32_t k = qs_key(sc[b]); body }  \
     }
 
+// The count, minimum and maximum of the selectable keys over the workgroup
+// (one barrier); every thread gets all three.
+__device__ __forceinline__ void qs_reduce3(uint32_t &cnt, uint32_t &mn, uint32_t &mx, uint4 *wt3)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        cnt += (uint32_t)__shfl_xor((int)cnt, o, 64);
+        mn = min(mn, (uint32_t)__shfl_xor((int)mn, o, 64));
+        mx = max(mx, (uint32_t)__shfl_xor((int)mx, o, 64));
+    }
+    if (lane == 0) wt3[wave] = make_uint4(cnt, mn, mx, 0u);
+    __syncthreads();
+    cnt = 0; mn = 0xFFFFFFFFu; mx = 0u;
+#pragma unroll
+    for (int w = 0; w < QS_SEL_WAVES; w++) {
+        const uint4 v = wt3[w];
+        cnt += v.x; mn = min(mn, v.y); mx = max(mx, v.z);
+    }
+}
+
 __global__ void __launch_bounds__(QS_SEL_THREADS) k_qsa_select(uint8_t *__restrict__ mask, uint32_t *__restrict__ list,
                                                                const float *__restrict__ scores, int ratio,
                                                                int base_pos, int block_topk, int max_ctx,
                                                                int max_blocks, int cap)
 {
     extern __shared__ uint8_t sel[];
-    __shared__ uint32_t hist[QS_SEL_WAVES][256];   // a histogram per wave: no cross-wave atomics
+    // a histogram per wave (no cross-wave atomics), two sets: a pass counts
+    // into one while it clears the other for the next pass
+    __shared__ uint32_t hist[2][QS_SEL_WAVES][256];
     __shared__ uint32_t wt[QS_SEL_WAVES];
-    __shared__ uint32_t sh_total, sh_bin, sh_need;
-    const int tid = threadIdx.x, wave = tid >> 6, r = blockIdx.x;
+    __shared__ uint4 wt3[QS_SEL_WAVES];
+    __shared__ uint32_t sh_total, sh_bin, sh_need, sh_exact;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, r = blockIdx.x;
     const int n_keys = base_pos + r + 1, nb = n_keys / ratio;
     const float *sc = scores + (size_t)r * max_blocks;
     const int per = (nb + QS_SEL_THREADS - 1) / QS_SEL_THREADS;
     const int lo = min(tid * per, nb), hi = min(lo + per, nb);
     const bool in_regs = per <= QS_SEL_KREG;
+    QS_TS(0);
+    // every load of the run issued before the first use (in-range addresses
+    // for the lanes past the run, whose keys are then dropped)
     uint32_t kr[QS_SEL_KREG];
+    if (in_regs && nb > 0) {
+        float v[QS_SEL_KREG];
+        if (per == QS_SEL_KREG && (reinterpret_cast<uintptr_t>(sc) & 15) == 0 && lo + QS_SEL_KREG <= max_blocks) {
+            // two 16-byte loads (the run starts at a multiple of 8 blocks)
+            const float4 a = reinterpret_cast<const float4 *>(sc + lo)[0];
+            const float4 b = reinterpret_cast<const float4 *>(sc + lo)[1];
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        } else {
 #pragma unroll
-    for (int i = 0; i < QS_SEL_KREG; i++) kr[i] = in_regs && lo + i < hi ? qs_key(sc[lo + i]) : 0u;
+            for (int i = 0; i < QS_SEL_KREG; i++) v[i] = sc[min(lo + i, nb - 1)];
+        }
+#pragma unroll
+        for (int i = 0; i < QS_SEL_KREG; i++) kr[i] = lo + i < hi ? qs_key(v[i]) : 0u;
+    } else {
+#pragma unroll
+        for (int i = 0; i < QS_SEL_KREG; i++) kr[i] = 0u;
+    }
+#ifdef QS_TRACE
+    if (threadIdx.x == 0 && blockIdx.x < 64) qs_trace[blockIdx.x * 16 + 12] = kr[0] == 0x12345u ? 0 : wall_clock64();
+#endif
+    uint4 *h0 = reinterpret_cast<uint4 *>(&hist[0][0][0]);
+    h0[tid] = make_uint4(0u, 0u, 0u, 0u);   // 16 x 256 words: one uint4 a thread
 
-    uint32_t cnt = 0, mn = 0xFFFFFFFFu, mx = 0u;
-    QS_RUN(sel[b] = 0; if (k) { cnt++; mn = min(mn, k); mx = max(mx, k); })
-    qs_scan(cnt, wt, &sh_total);
-    const uint32_t S = sh_total;
+    uint32_t S = 0, mn = 0xFFFFFFFFu, mx = 0u;
+    QS_RUN(if (k) { S++; mn = min(mn, k); mx = max(mx, k); })
+    QS_TS(13);
+    qs_reduce3(S, mn, mx, wt3);
+    QS_TS(1);
     const uint32_t take = min((uint32_t)max(block_topk, 0), S);
-    if (take == S) {
-        QS_RUN(sel[b] = k != 0u;)
-    } else if (take > 0) {
+    // blocks taken: key > T, then the first `need` blocks whose key equals T
+    uint32_t T = 0u, need = 0u;
+    if (take == 0) {
+        T = 0xFFFFFFFFu;
+    } else if (take < S) {
         // the key of the take-th largest.  The passes count u = key - kmin
         // (kmin, kmax: the selectable keys' range), 8 bits at a time from
         // the range's top bit, so even scores that share their leading bits
-        // spread over the bins
-        mn = qs_block_min(mn, wt);
-        mx = ~qs_block_min(~mx, wt);
+        // spread over the bins.  A pass whose bin holds exactly the blocks
+        // still needed ends the search: the bin's lowest key bounds the take.
+        QS_TS(2);
         const uint32_t range = mx - mn;
         const int nbits = range ? 32 - __builtin_clz(range) : 0;
-        uint32_t prefix = 0, need = take;
-        int prev = 32, shift = nbits > 8 ? nbits - 8 : 0;
+        uint32_t prefix = 0;
+        bool exact = false;
+        int prev = 32, shift = nbits > 8 ? nbits - 8 : 0, cur = 0, pass = 0;
+        need = take;
         while (true) {
             const uint32_t bmask = prev - shift >= 32 ? 0xFFFFFFFFu : ((1u << (prev - shift)) - 1u);
-            for (int i = tid; i < QS_SEL_WAVES * 256; i += QS_SEL_THREADS) (&hist[0][0])[i] = 0;
-            __syncthreads();
             const uint32_t hp = prev >= 32 ? 0u : prefix >> prev;
+            reinterpret_cast<uint4 *>(&hist[cur ^ 1][0][0])[tid] = make_uint4(0u, 0u, 0u, 0u);
             QS_RUN(if (k) {
                 const uint32_t u = k - mn;
-                if ((prev >= 32 ? 0u : u >> prev) == hp) atomicAdd(&hist[wave][(u >> shift) & bmask], 1u);
+                if ((prev >= 32 ? 0u : u >> prev) == hp) atomicAdd(&hist[cur][wave][(u >> shift) & bmask], 1u);
             })
             __syncthreads();
-            // thread t < 256 holds bin 255 - t summed over the waves (in wave
-            // order); a scan from the top bin finds where the count reaches `need`
-            uint32_t cbin = 0;
-            if (tid < 256)
-                for (int w = 0; w < QS_SEL_WAVES; w++) cbin += hist[w][255 - tid];
-            const uint32_t above = qs_scan(cbin, wt, &sh_total);
-            if (tid < 256 && above < need && above + cbin >= need) {
-                sh_bin = 255u - (uint32_t)tid;
-                sh_need = need - above;
+            if (wave == 0) {
+                // lane l: bins 4l .. 4l+3 summed over the waves; counts above
+                // a lane's bins are a suffix sum over the lanes
+                uint4 c = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+                for (int w = 0; w < QS_SEL_WAVES; w++) {
+                    const uint4 v = reinterpret_cast<const uint4 *>(&hist[cur][w][0])[lane];
+                    c.x += v.x; c.y += v.y; c.z += v.z; c.w += v.w;
+                }
+                const uint32_t tl = c.x + c.y + c.z + c.w;
+                uint32_t sfx = tl;
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                    const uint32_t y = (uint32_t)__shfl_down((int)sfx, o, 64);
+                    if (lane + o < 64) sfx += y;
+                }
+                uint32_t a = sfx - tl;
+                const uint32_t cj[4] = {c.w, c.z, c.y, c.x};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    if (a < need && a + cj[j] >= need) {
+                        sh_bin = (uint32_t)(4 * lane + 3 - j);
+                        sh_need = need - a;
+                        sh_exact = a + cj[j] == need;
+                    }
+                    a += cj[j];
+                }
             }
             __syncthreads();
             prefix |= sh_bin << shift;
             need = sh_need;
-            __syncthreads();
-            if (shift == 0) break;
+            exact = sh_exact != 0u;
+            QS_TS(3 + min(pass++, 4));
+            if (exact || shift == 0) break;
             prev = shift;
             shift = shift > 8 ? shift - 8 : 0;
+            cur ^= 1;
         }
-        const uint32_t T = prefix + mn;   // back from the range's offset to the key
-        // everything above T; then the first `need` equal to T, by block
-        uint32_t eq = 0;
-        QS_RUN(if (k > T) sel[b] = 1; else eq += k == T;)
-        uint32_t rank = qs_scan(eq, wt, &sh_total);
-        QS_RUN(if (k == T && rank < need) { sel[b] = 1; rank++; })
+        T = prefix + mn;   // back from the range's offset to the key
+        if (exact) { T -= 1u; need = 0u; }   // T >= kmin >= 1
     }
-    __syncthreads();
+    uint32_t selm = 0, eq = 0;
+    if (in_regs) {
+#pragma unroll
+        for (int i = 0; i < QS_SEL_KREG; i++) {
+            if (lo + i < hi) {
+                if (kr[i] > T) selm |= 1u << i;
+                else eq += kr[i] == T;
+            }
+        }
+    } else {
+        for (int b = lo; b < hi; b++) {
+            const uint32_t k = qs_key(sc[b]);
+            sel[b] = k > T;
+            eq += k == T;
+        }
+    }
+    if (need > 0u) {   // uniform
+        uint32_t rank = qs_scan(eq, wt, &sh_total);
+        QS_RUN(if (k == T && rank < need) {
+            if (in_regs) selm |= 1u << (b - lo); else sel[b] = 1;
+            rank++;
+        })
+    }
     uint32_t mine = 0;
-    for (int b = lo; b < hi; b++) mine += sel[b];
-    const uint32_t first = qs_scan(mine, wt, &sh_total);
+    if (in_regs) {
+#pragma unroll
+        for (int i = 0; i < QS_SEL_KREG; i++)
+            if (lo + i < hi) sel[lo + i] = (uint8_t)((selm >> i) & 1u);
+        mine = __builtin_popcount(selm);
+    } else {
+        for (int b = lo; b < hi; b++) mine += sel[b];
+    }
+    QS_TS(8);
+    const uint32_t first = qs_scan(mine, wt, &sh_total);   // its barriers publish sel
     const uint32_t n_sel = sh_total;
+    QS_TS(9);
     uint32_t *lr = list + (size_t)r * (1 + cap);
-    uint32_t at = first * ratio;
-    for (int b = lo; b < hi; b++)
-        if (sel[b])
-            for (int t = 0; t < ratio; t++) lr[1 + at++] = (uint32_t)(b * ratio + t);
+    uint32_t at = 1 + first * ratio;
+    if (in_regs) {
+#pragma unroll
+        for (int i = 0; i < QS_SEL_KREG; i++)
+            if ((selm >> i) & 1u)
+                for (int t = 0; t < ratio; t++) lr[at++] = (uint32_t)((lo + i) * ratio + t);
+    } else {
+        for (int b = lo; b < hi; b++)
+            if (sel[b])
+                for (int t = 0; t < ratio; t++) lr[at++] = (uint32_t)(b * ratio + t);
+    }
     if (tid == 0) {
         uint32_t n = n_sel * ratio;
         for (int t = nb * ratio; t < n_keys; t++) lr[1 + n++] = (uint32_t)t;
         lr[0] = n;
     }
+    QS_TS(10);
     uint8_t *mr = mask + (size_t)r * max_ctx;
-    for (int t = tid; t < n_keys; t += QS_SEL_THREADS) mr[t] = t >= nb * ratio ? 1 : sel[t / ratio];
+    int t0 = 0;
+    if (ratio == 4 && (reinterpret_cast<uintptr_t>(mr) & 15) == 0) {
+        // four blocks (16 positions) a 16-byte store
+        const int n4 = nb >> 2;
+        for (int w = tid; w < n4; w += QS_SEL_THREADS) {
+            const uint32_t x = reinterpret_cast<const uint32_t *>(sel)[w];
+            reinterpret_cast<uint4 *>(mr)[w] = make_uint4((x & 1u) * 0x01010101u, ((x >> 8) & 1u) * 0x01010101u,
+                                                          ((x >> 16) & 1u) * 0x01010101u, (x >> 24) * 0x01010101u);
+        }
+        t0 = n4 * 16;
+    }
+    for (int t = t0 + tid; t < n_keys; t += QS_SEL_THREADS) mr[t] = t >= nb * ratio ? 1 : sel[t / ratio];
+    QS_TS(11);
 }
 #undef QS_RUN
 
@@ -359,6 +489,14 @@ __global__ void __launch_bounds__(QS_SEL_THREADS) k_qsa_select(uint8_t *__restri
 
 #define QA_D 256
 #define QA_P 32            // positions a workgroup takes per pass
+#define QA_QPOS(i) ((i) + (i) / 8)   // float4 i of a head in its padded LDS row
+#define QA_QROW (QA_D / 4 + QA_D / 32)
+
+#define QA_LOG2E 1.44269504088896340736f
+
+// 2^x by the hardware's exp2 (v_exp_f32); results below the normal range
+// flush to zero, which a softmax weight relative to the maximum can afford
+__device__ __forceinline__ float qa_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ float qa_f16(uint32_t bits)
 {
@@ -376,19 +514,50 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
                                                      int q_heads, int kv_heads, int max_ctx, float scale, int cap,
                                                      int nsplit, float *__restrict__ part)
 {
-    __shared__ float4 qs4[G][QA_D / 4];          // the G heads, pre-scaled
-    __shared__ float ps[G][QA_P];                // a pass's scores, then weights
-    __shared__ float red[G][4];
+    // the G heads, pre-scaled; each 32-dim piece padded by 16 bytes so the
+    // eight pieces a score reads at once start in different banks
+    __shared__ float4 qs4[G][QA_QROW];
+    __shared__ float ps[G][QA_P];                // a pass's weights (wave w: [8w, 8w + 8))
+    __shared__ float wm[4][G], wl[4][G];         // the waves' softmax states
     __shared__ float wbuf[G][QA_D];              // the waves' partial outputs meet here
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int split = blockIdx.x % nsplit, rk = blockIdx.x / nsplit;
     const int row = rk / kv_heads, kvh = rk % kv_heads;
     const uint32_t *lr = list + (size_t)row * (1 + cap);
+    QA_TS(0);
+    // the splits divide the list's capacity, so a split knows its range
+    // before the list's length arrives: its first pass's entries are
+    // requested with the length (entries past the length are not positions
+    // and are clamped to a valid row, then dropped)
+    const int per = ((cap + QA_P - 1) / QA_P + nsplit - 1) / nsplit;
+    const int j_lo = min(split * per * QA_P, cap), j_cap = min(j_lo + per * QA_P, cap);
+    const int jb = (QA_P / 4) * wave, jj = tid >> 3, kp = tid & 7;
+    uint32_t vi[QA_P / 4], ki = 0;
+    auto load_list = [&](int j0) {
+#pragma unroll
+        for (int i = 0; i < QA_P / 4; i++) vi[i] = lr[1 + min(j0 + jb + i, cap - 1)];
+        ki = lr[1 + min(j0 + jj, cap - 1)];
+    };
     const int n_sel = (int)lr[0];
-    const int passes = (n_sel + QA_P - 1) / QA_P, per = (passes + nsplit - 1) / nsplit;
-    const int j_lo = min(split * per * QA_P, n_sel), j_hi = min(j_lo + per * QA_P, n_sel);
-    const float *qp = q + ((size_t)row * q_heads + (size_t)kvh * G) * QA_D;
-    for (int i = tid; i < G * QA_D; i += 256) reinterpret_cast<float *>(qs4)[i] = qp[i] * scale;
+    if (j_lo < j_cap) load_list(j_lo);
+    QA_TSV(1, n_sel);
+    const int j_hi = min(j_cap, n_sel);
+    const float4 *qp = reinterpret_cast<const float4 *>(q + ((size_t)row * q_heads + (size_t)kvh * G) * QA_D);
+    const float sl2 = scale * QA_LOG2E;   // scores in log2 units: weights are 2^(s - max)
+    {
+        constexpr int NQ = (G * QA_D / 4 + 255) / 256;
+        float4 qv[NQ];
+#pragma unroll
+        for (int u = 0; u < NQ; u++)
+            if (tid + 256 * u < G * QA_D / 4) qv[u] = qp[tid + 256 * u];
+#pragma unroll
+        for (int u = 0; u < NQ; u++) {
+            const int f = tid + 256 * u;
+            if (f < G * QA_D / 4)
+                qs4[f / (QA_D / 4)][QA_QPOS(f % (QA_D / 4))] =
+                    make_float4(qv[u].x * sl2, qv[u].y * sl2, qv[u].z * sl2, qv[u].w * sl2);
+        }
+    }
     const uint16_t *kbase = kc + (size_t)kvh * max_ctx * QA_D;
     const uint16_t *vbase = vc + (size_t)kvh * max_ctx * QA_D;
 
@@ -400,113 +569,124 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     }
     __syncthreads();
     for (int j0 = j_lo; j0 < j_hi; j0 += QA_P) {
-        const int n = min(QA_P, j_hi - j0);
-        // the pass's value rows are requested first, with the keys below: both
-        // depend only on the list, so neither waits for the scores
-        const int jb = (QA_P / 4) * wave, nj = max(0, min(QA_P / 4, n - jb));
+        const int n = min(QA_P, j_hi - j0), nj = max(0, min(QA_P / 4, n - jb));
+        if (j0 != j_lo) load_list(j0);
+        // every key and value row of the pass at once, the keys first
+#pragma unroll
+        for (int i = 0; i < QA_P / 4; i++) vi[i] = min(vi[i], (uint32_t)(max_ctx - 1));
+        ki = min(ki, (uint32_t)(max_ctx - 1));
+        uint4 kv[4];
+        {
+            const uint4 *kr = reinterpret_cast<const uint4 *>(kbase + (size_t)ki * QA_D + 32 * kp);
+#pragma unroll
+            for (int c = 0; c < 4; c++) kv[c] = kr[c];
+        }
         uint2 vv[QA_P / 4];
 #pragma unroll
         for (int i = 0; i < QA_P / 4; i++)
-            if (i < nj) vv[i] = *reinterpret_cast<const uint2 *>(vbase + (size_t)lr[1 + j0 + jb + i] * QA_D + 4 * lane);
+            vv[i] = *reinterpret_cast<const uint2 *>(vbase + (size_t)vi[i] * QA_D + 4 * lane);
+        // the key rows, issued before the value rows, are waited for here
+        // (the value rows stay in flight through the scores)
+#pragma unroll
+        for (int c = 0; c < 4; c++) asm volatile("" : "+v"(kv[c].x), "+v"(kv[c].y), "+v"(kv[c].z), "+v"(kv[c].w));
         // scores: eight threads per position, 32 dims each (one 64-byte
-        // piece of the fp16 key row), every load issued first; the eight
-        // partial dots meet in the xor tree of their 8-lane run
-        {
-            const int jj = tid >> 3, part = tid & 7;
-            float sg[G];
+        // piece of the fp16 key row); the eight partial dots meet in the xor
+        // tree of their 8-lane run.  Wave w scores positions 8w .. 8w+7 of
+        // the pass, the ones its values take below, so the pass needs no
+        // barrier: each wave runs its own softmax state
+        const bool valid = jj < n;
+        float sg[G];
 #pragma unroll
-            for (int g = 0; g < G; g++) sg[g] = 0.0f;
-            if (jj < n) {
-                const uint4 *kr = reinterpret_cast<const uint4 *>(kbase + (size_t)lr[1 + j0 + jj] * QA_D + 32 * part);
-                uint4 kv[4];
+        for (int g = 0; g < G; g++) sg[g] = 0.0f;
+        if (valid) {
+            QA_TSV(2, kv[0].x);
 #pragma unroll
-                for (int c = 0; c < 4; c++) kv[c] = kr[c];
+            for (int c = 0; c < 4; c++) {
+                const uint32_t w[4] = { kv[c].x, kv[c].y, kv[c].z, kv[c].w };
+                const int d0 = 32 * kp + 8 * c;
+                float kf[8];
 #pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    const uint32_t w[4] = { kv[c].x, kv[c].y, kv[c].z, kv[c].w };
-                    const int d0 = 32 * part + 8 * c;
-                    float kf[8];
+                for (int e = 0; e < 4; e++) { kf[2 * e] = qa_f16(w[e] & 0xFFFFu); kf[2 * e + 1] = qa_f16(w[e] >> 16); }
 #pragma unroll
-                    for (int e = 0; e < 4; e++) { kf[2 * e] = qa_f16(w[e] & 0xFFFFu); kf[2 * e + 1] = qa_f16(w[e] >> 16); }
-#pragma unroll
-                    for (int g = 0; g < G; g++) {
-                        const float4 a = qs4[g][d0 / 4], b = qs4[g][d0 / 4 + 1];
-                        sg[g] = __builtin_fmaf(a.x, kf[0], sg[g]);
-                        sg[g] = __builtin_fmaf(a.y, kf[1], sg[g]);
-                        sg[g] = __builtin_fmaf(a.z, kf[2], sg[g]);
-                        sg[g] = __builtin_fmaf(a.w, kf[3], sg[g]);
-                        sg[g] = __builtin_fmaf(b.x, kf[4], sg[g]);
-                        sg[g] = __builtin_fmaf(b.y, kf[5], sg[g]);
-                        sg[g] = __builtin_fmaf(b.z, kf[6], sg[g]);
-                        sg[g] = __builtin_fmaf(b.w, kf[7], sg[g]);
-                    }
+                for (int g = 0; g < G; g++) {
+                    const float4 a = qs4[g][QA_QPOS(d0 / 4)], b = qs4[g][QA_QPOS(d0 / 4) + 1];
+                    sg[g] = __builtin_fmaf(a.x, kf[0], sg[g]);
+                    sg[g] = __builtin_fmaf(a.y, kf[1], sg[g]);
+                    sg[g] = __builtin_fmaf(a.z, kf[2], sg[g]);
+                    sg[g] = __builtin_fmaf(a.w, kf[3], sg[g]);
+                    sg[g] = __builtin_fmaf(b.x, kf[4], sg[g]);
+                    sg[g] = __builtin_fmaf(b.y, kf[5], sg[g]);
+                    sg[g] = __builtin_fmaf(b.z, kf[6], sg[g]);
+                    sg[g] = __builtin_fmaf(b.w, kf[7], sg[g]);
                 }
             }
-#pragma unroll
-            for (int g = 0; g < G; g++) {
-                const float t = qw_xor_sum<8>(sg[g]);
-                if (jj < n && part == 0) ps[g][jj] = t;
-            }
         }
-        __syncthreads();
-        // the pass's max per head
+        QA_TS(3);
+        // per head: the wave's maximum over its positions (lane bits 3-5),
+        // the online rescale, the weights (into this wave's slice of ps) and
+        // their sum in a fixed xor tree
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            float v = tid < n ? ps[g][tid] : -FLT_MAX;
-            v = qw_wave_max(v);
-            if (lane == 0) red[g][wave] = v;
-        }
-        __syncthreads();
-        float rescale[G];
+            const float sc = qw_xor_sum<8>(sg[g]);
+            float cm = valid ? sc : -FLT_MAX;
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float cm = fmaxf(fmaxf(red[g][0], red[g][1]), fmaxf(red[g][2], red[g][3]));
+            for (int o = 8; o < 64; o <<= 1) cm = fmaxf(cm, __shfl_xor(cm, o, 64));
             const float mn = fmaxf(m[g], cm);
-            rescale[g] = expf(m[g] - mn);
+            const float rs = qa_exp2(m[g] - mn);
             m[g] = mn;
+            float e = valid ? qa_exp2(sc - mn) : 0.0f;
+            if (kp == 0) ps[g][jj] = e;
+#pragma unroll
+            for (int o = 8; o < 64; o <<= 1) e += __shfl_xor(e, o, 64);
+            l[g] = l[g] * rs + e;
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[g][i] *= rs;
         }
-        __syncthreads();                             // red read by every thread
+        QA_TS(7);
+        // values: lane dims 4l..4l+3 of the wave's positions (their rows
+        // were requested with the keys); the weights come back from the
+        // wave's own slice of ps (its writes above, in program order)
+        QA_TSV(8, vv[0].x);
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            float e = 0.0f;
-            if (tid < n) {
-                e = expf(ps[g][tid] - m[g]);
-                ps[g][tid] = e;
-            }
-            e = qw_xor_sum<64>(e);
-            if (lane == 0) red[g][wave] = e;
-        }
-        __syncthreads();
+        for (int i = 0; i < QA_P / 4; i++) {
+            if (i < nj) {
+                const float v0 = qa_f16(vv[i].x & 0xFFFFu), v1 = qa_f16(vv[i].x >> 16);
+                const float v2 = qa_f16(vv[i].y & 0xFFFFu), v3 = qa_f16(vv[i].y >> 16);
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            l[g] = l[g] * rescale[g] + ((red[g][0] + red[g][1]) + (red[g][2] + red[g][3]));
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc[g][i] *= rescale[g];
-        }
-        // values: wave w takes the pass's positions 8w..8w+7, lane dims
-        // 4l..4l+3 (their rows were requested with the keys)
-        {
-#pragma unroll
-            for (int i = 0; i < QA_P / 4; i++) {
-                if (i < nj) {
-                    const float v0 = qa_f16(vv[i].x & 0xFFFFu), v1 = qa_f16(vv[i].x >> 16);
-                    const float v2 = qa_f16(vv[i].y & 0xFFFFu), v3 = qa_f16(vv[i].y >> 16);
-#pragma unroll
-                    for (int g = 0; g < G; g++) {
-                        const float p = ps[g][jb + i];
-                        acc[g][0] = __builtin_fmaf(p, v0, acc[g][0]);
-                        acc[g][1] = __builtin_fmaf(p, v1, acc[g][1]);
-                        acc[g][2] = __builtin_fmaf(p, v2, acc[g][2]);
-                        acc[g][3] = __builtin_fmaf(p, v3, acc[g][3]);
-                    }
+                for (int g = 0; g < G; g++) {
+                    const float p = ps[g][jb + i];
+                    acc[g][0] = __builtin_fmaf(p, v0, acc[g][0]);
+                    acc[g][1] = __builtin_fmaf(p, v1, acc[g][1]);
+                    acc[g][2] = __builtin_fmaf(p, v2, acc[g][2]);
+                    acc[g][3] = __builtin_fmaf(p, v3, acc[g][3]);
                 }
             }
         }
-        __syncthreads();                             // ps and red free for the next pass
+        QA_TSV(9, acc[0][0]);
     }
-    // the waves' partial outputs meet as (w0 + w1) + (w2 + w3), through wbuf
-    // and the query array (no longer read)
+    QA_TS(4);
+    // the four waves' states meet: the common maximum, each wave's factor,
+    // the sums (w0 + w1) + (w2 + w3), and the outputs in the same tree
+    // through wbuf and the query array (no longer read)
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++) { wm[wave][g] = m[g]; wl[wave][g] = l[g]; }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float M = fmaxf(fmaxf(wm[0][g], wm[1][g]), fmaxf(wm[2][g], wm[3][g]));
+        const float f = qa_exp2(m[g] - M);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[g][i] *= f;
+        if (wave == 0) {
+            l[g] = (wl[0][g] * qa_exp2(wm[0][g] - M) + wl[1][g] * qa_exp2(wm[1][g] - M)) +
+                   (wl[2][g] * qa_exp2(wm[2][g] - M) + wl[3][g] * qa_exp2(wm[3][g] - M));
+            m[g] = M;
+        }
+    }
     float *bufA = &wbuf[0][0], *bufB = reinterpret_cast<float *>(&qs4[0][0]);
+    __syncthreads();                                 // every wave's scores are done with qs4
     if (wave == 1 || wave == 3) {
         float *dst = wave == 1 ? bufA : bufB;
 #pragma unroll
@@ -530,16 +710,25 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
             for (int i = 0; i < 4; i++) bufA[g * QA_D + 4 * lane + i] = acc[g][i];
     }
     __syncthreads();
+    QA_TS(5);
     if (wave != 0) return;
     if (nsplit == 1) {
+        // the gate rows requested together, before the first is used
+        float4 gv[G];
+        if (gate) {
+#pragma unroll
+            for (int g = 0; g < G; g++)
+                gv[g] = *reinterpret_cast<const float4 *>(gate + ((size_t)row * q_heads + (size_t)kvh * G + g) * QA_D + 4 * lane);
+        }
 #pragma unroll
         for (int g = 0; g < G; g++) {
             const size_t ob = ((size_t)row * q_heads + (size_t)kvh * G + g) * QA_D + 4 * lane;
+            const float gg[4] = {gv[g].x, gv[g].y, gv[g].z, gv[g].w};
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const float s = acc[g][i] + bufA[g * QA_D + 4 * lane + i];
                 float o = l[g] > 0.0f ? s / l[g] : 0.0f;
-                if (gate) o *= 1.0f / (1.0f + expf(-gate[ob + i]));
+                if (gate) o *= 1.0f / (1.0f + expf(-gg[i]));
                 out[ob + i] = o;
             }
         }
@@ -594,7 +783,7 @@ __global__ void __launch_bounds__(256) k_attn_merge(float *__restrict__ out, con
         const float M = fmaxf(wmax[0], wmax[1]);
         float f = 0.0f, c = 0.0f;
         if (t < nsplit) {
-            f = expf(sm[t] - M);
+            f = qa_exp2(sm[t] - M);
             sf[t] = f;
             c = sl[t] * f;
         }

@@ -140,6 +140,17 @@ def test_qsa_select_at_scale_with_ties(gpu, base):
     check_select(gpu, (st * 0.25).astype(np.float32), rows, ratio, base, topk, max_ctx, mb)
 
 
+@pytest.mark.parametrize("ratio,base,max_ctx", [(4, 32766, 32768), (4, 32764, 32771), (4, 8190, 8208),
+                                                (3, 24574, 24580), (1, 4000, 4096), (4, 40001, 40016)])
+def test_qsa_select_distinct_scores(gpu, ratio, base, max_ctx):
+    """Continuous scores (the decode shape among them: 32K keys, 8192 blocks,
+    top 512): the search ends early when a bin holds exactly the blocks still
+    needed; rows whose mask start is or is not 16-byte aligned."""
+    rows, topk = 2, 512
+    mb = max_ctx // ratio
+    check_select(gpu, rnd((rows, mb), base + ratio), rows, ratio, base, topk, max_ctx, mb)
+
+
 def test_qsa_select_edges(gpu):
     ratio = 4
     # every score equal: the lowest blocks win
