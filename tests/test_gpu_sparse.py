@@ -213,6 +213,15 @@ def test_attn_masked_long_list_and_gate(gpu):
     attn_case(gpu, 3, 8, 2, 300, 16, 4, 82, gated=True)
 
 
+@pytest.mark.parametrize("rows,qh,kvh,base", [(1, 24, 2, 32767), (1, 8, 1, 9000), (2, 16, 2, 4000),
+                                               (3, 16, 4, 2500)])
+def test_attn_masked_split_merge(gpu, rows, qh, kvh, base):
+    """The split launch at decode shapes (the model's 24/2 heads over a
+    2048-position list among them) and its ordered merge; twice in a row."""
+    for _ in range(2):
+        attn_case(gpu, rows, qh, kvh, base, 512, 4, 90 + qh + rows, gated=True)
+
+
 # ---- gated DeltaNet ----------------------------------------------------------------
 
 @pytest.mark.parametrize("channels,rows", [(1024, 1), (1024, 7), (10240, 3)])
