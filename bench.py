@@ -548,10 +548,10 @@ def bench_sparse(gpu, steps=40, seed=99):
     c = gpu.qw_cmd_begin()
     states = []
     for l in range(NG):
-        st, cs = B(hv * dk * dk * 4), B(3 * ch * 4)
+        st, cs, cs2 = B(hv * dk * dk * 4), B(3 * ch * 4), B(3 * ch * 4)
         gpu.qw_op_synth(c, st.ref(), synth.SYNTH_F32_BF16_NORMAL, hv * dk * dk, synth.sm_key(seed, f"S{l}"), 0.05, 0.0)
         gpu.qw_op_synth(c, cs.ref(), synth.SYNTH_F32_BF16_NORMAL, 3 * ch, synth.sm_key(seed, f"cs{l}"), 1.0, 0.0)
-        states.append((st, cs))
+        states.append((st, cs, cs2))
     gpu.run(c, "gdn setup")
     cw = B.of(synth.to_bf16(0.3 * f32(ch, 4)))
     Al = B.of(synth.to_bf16(np.linspace(-0.5, 1.0, hv).astype(np.float32)))
@@ -562,7 +562,7 @@ def bench_sparse(gpu, steps=40, seed=99):
     prep = gpu.qw_gdn_prep(ab.ref(), bb.ref(), Al.ref(), dt.ref(), 1e-6 / dk, 1.0 / dk, 1.0 / np.sqrt(dk))
 
     def gdn(c, l, rows):
-        st, cs = states[l % NG]
+        st, cs, _ = states[l % NG]
         gpu.qw_op_conv1d_causal_silu(c, xmix.ref(), xin.ref(), cs.ref(), cw.ref(), ch, rows, 4, gpu.NULL_REF, 0, 0)
         # q, k, v: packed [rows, heads, 128] inputs of the recurrence
         gpu.qw_op_gated_delta_prep(c, yb.ref(), qkv[0].ref(), qkv[1].ref(), qkv[2].ref(), prep, st.ref(), hk, hv, dk,
@@ -575,6 +575,16 @@ def bench_sparse(gpu, steps=40, seed=99):
                          "us_per_token": round(ms * 1e3, 2), "bytes": gbytes,
                          "hbm_gbs": round(gbytes / (ms * 1e-3) / 1e9, 1),
                          "hbm_frac": round(gbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    def gdn_one(c, l):
+        # the one-launch step on the conv's own output channels; the layer's
+        # two windows alternate
+        st, cs, cs2 = states[l % NG]
+        wi, wo = (cs, cs2) if (l // NG) % 2 == 0 else (cs2, cs)
+        assert gpu.qw_op_gdn_decode(c, yb.ref(), xin.ref(), wi.ref(), wo.ref(), cw.ref(), prep, st.ref(), hk, hv, dk,
+                                    dk)
+
+    ms1 = timed("gdn decode one launch", gdn_one, steps)
+    res["gdn_decode"]["one_launch_us_per_token"] = round(ms1 * 1e3, 2)
     ms = timed("gdn prefill", lambda c, l: gdn(c, l, R), 3)
     res["gdn_prefill"] = {"rows": R, "ms": round(ms, 3), "tokens_per_s": round(R / (ms * 1e-3), 1)}
     for t in (cw, Al, dt, xin, xmix, ab, bb, yb, blocker) + qkv:

@@ -221,6 +221,19 @@ void qw_op_gated_delta_prep(qw_cmd c, qw_ref y, qw_ref q, qw_ref k, qw_ref v,
                             const qw_gdn_prep *prep, qw_ref state,
                             int32_t hk, int32_t hv, int32_t dk, int32_t dv, int32_t rows,
                             qw_ref snap, int32_t n_snap, int32_t snap_stride);
+/* One decode step of the recurrent sublayer in one launch: the conv with
+ * silu over the mixed channels x [2 hk dk + hv dv], then the prepared delta
+ * rule on its q [0, hk dk), k [hk dk, 2 hk dk) and v [2 hk dk, ...) channels
+ * (the split of the reference's gdn_step, qwasar_flash_cpu.c:318-320).  No
+ * counterpart in the reference, which runs qw_op_conv1d_causal_silu and then
+ * qw_op_gated_delta_prep on the conv's output; the same bits as those two.
+ * The conv window is read from conv_state and written to conv_state_out
+ * ([3, channels] each, oldest first), which may not overlap conv_state or x
+ * (callers alternate two windows); state as qw_op_gated_delta.  dk = dv =
+ * 128; false and nothing encoded for other shapes or overlapping windows. */
+bool qw_op_gdn_decode(qw_cmd c, qw_ref y, qw_ref x, qw_ref conv_state, qw_ref conv_state_out,
+                      qw_ref conv_weight, const qw_gdn_prep *prep, qw_ref state,
+                      int32_t hk, int32_t hv, int32_t dk, int32_t dv);
 /* rms_norm(x, weight) * sigmoid(gate) per row of `dim` (reference
  * qwasar_gpu.h:618-620): the delta net's output gate.  weight may be a null
  * ref (unit gain). */

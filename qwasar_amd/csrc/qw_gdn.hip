@@ -7,7 +7,8 @@
 //   k_gated_delta<PREP>   the delta-rule recurrence per value head,
 //                             S *= g;  kv = S k;  S += k (v - kv) beta;  y = S q
 //                         and, with PREP, q and k l2-normed and the gates
-//                         computed inside the kernel
+//                         computed inside the kernel; with CONV (one decode
+//                         step) the conv too, for the channels it reads
 //
 // The recurrence is serial in time but independent across the rows of each
 // head's [dv, dk] state.  A wave owns two value rows: each half-wave one
@@ -89,13 +90,47 @@ struct qg_prep {
     float l2eps, q_scale, k_scale;
 };
 
-template <bool PREP>
+// The fused decode step's conv: the mixed channels before the conv, the
+// window in and out (distinct buffers), the taps.
+struct qg_conv {
+    const float *x, *win;
+    float *wout;
+    const uint16_t *w;
+    int channels;
+};
+
+// One channel of the causal conv with silu at one step, the arithmetic of
+// k_conv1d_causal_silu (taps against the window oldest first, then the
+// new sample, in one fma chain from 0); the window after the step goes to
+// wout when `own`.
+__device__ __forceinline__ float qg_conv1(const qg_conv &cv, int ch, bool own)
+{
+    const int C = cv.channels;
+    float win[4], acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 3; j++) win[j] = cv.win[(size_t)j * C + ch];
+    win[3] = cv.x[ch];
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc = __builtin_fmaf(win[j], qw_bf16(cv.w[(size_t)ch * 4 + j]), acc);
+    if (own) {
+#pragma unroll
+        for (int j = 0; j < 3; j++) cv.wout[(size_t)j * C + ch] = win[j + 1];
+    }
+    return acc / (1.0f + expf(-acc));
+}
+
+// CONV (one step, PREP): q, k and v are the conv's outputs over the mixed
+// channels [0, hk dk), [hk dk, 2 hk dk) and [2 hk dk, ...), computed here
+// for the channels this workgroup reads; the first workgroup of each key
+// head's group writes the window of its q and k channels, every workgroup
+// that of its own v channels.
+template <bool PREP, bool CONV = false>
 __global__ void __launch_bounds__(QG_THREADS) k_gated_delta(float *__restrict__ y, const float *__restrict__ q,
                                                             const float *__restrict__ k, const float *__restrict__ v,
                                                             const float *__restrict__ g,
                                                             const float *__restrict__ beta, float *state, int hk,
                                                             int hv, int rows, float *__restrict__ snap, int n_snap,
-                                                            int snap_stride, qg_prep pp)
+                                                            int snap_stride, qg_prep pp, qg_conv cv = {})
 {
     __shared__ float4 sq[QG_CHUNK][QG_DK / 4], sk[QG_CHUNK][QG_DK / 4];
     __shared__ float sv[QG_CHUNK][QG_ROWS_PER_WG];
@@ -119,15 +154,24 @@ __global__ void __launch_bounds__(QG_THREADS) k_gated_delta(float *__restrict__ 
     for (int c0 = 0; c0 < rows; c0 += QG_CHUNK) {
         const int n = min(QG_CHUNK, rows - c0);
         __syncthreads();                           // the previous chunk is consumed
-        for (int i = tid; i < n * (QG_DK / 4); i += QG_THREADS) {
-            const int t = i / (QG_DK / 4), c = i % (QG_DK / 4);
-            const size_t off = (size_t)(c0 + t) * qstride + (size_t)hx * QG_DK;
-            sq[t][c] = reinterpret_cast<const float4 *>(q + off)[c];
-            sk[t][c] = reinterpret_cast<const float4 *>(k + off)[c];
-        }
-        if (tid < n * QG_ROWS_PER_WG) {
-            const int t = tid / QG_ROWS_PER_WG, j = tid % QG_ROWS_PER_WG;
-            sv[t][j] = v[(size_t)(c0 + t) * vstride + (size_t)h * QG_DV + r0 + j];
+        if (CONV) {
+            const int kd = hk * QG_DK;
+            const bool own_qk = h % (hv / hk) == 0 && r0 == 0;
+            float *fq = reinterpret_cast<float *>(&sq[0][0]), *fk = reinterpret_cast<float *>(&sk[0][0]);
+            if (tid < QG_DK) fq[tid] = qg_conv1(cv, hx * QG_DK + tid, own_qk);
+            else if (tid < 2 * QG_DK) fk[tid - QG_DK] = qg_conv1(cv, kd + hx * QG_DK + tid - QG_DK, own_qk);
+            if (tid < QG_ROWS_PER_WG) sv[0][tid] = qg_conv1(cv, 2 * kd + h * QG_DV + r0 + tid, true);
+        } else {
+            for (int i = tid; i < n * (QG_DK / 4); i += QG_THREADS) {
+                const int t = i / (QG_DK / 4), c = i % (QG_DK / 4);
+                const size_t off = (size_t)(c0 + t) * qstride + (size_t)hx * QG_DK;
+                sq[t][c] = reinterpret_cast<const float4 *>(q + off)[c];
+                sk[t][c] = reinterpret_cast<const float4 *>(k + off)[c];
+            }
+            if (tid < n * QG_ROWS_PER_WG) {
+                const int t = tid / QG_ROWS_PER_WG, j = tid % QG_ROWS_PER_WG;
+                sv[t][j] = v[(size_t)(c0 + t) * vstride + (size_t)h * QG_DV + r0 + j];
+            }
         }
         if (tid >= 128 && tid < 128 + n) {
             const int t = tid - 128;
@@ -198,6 +242,20 @@ extern "C" int qwk_conv1d_causal_silu(hipStream_t s, float *y, const float *x, f
     if (rows == 0) return 0;
     hipLaunchKernelGGL(k_conv1d_causal_silu<4>, dim3((channels + 255) / 256), dim3(256), 0, s, y, x, state, w,
                        channels, rows, snap, n_snap, snap_stride);
+    return (int)hipGetLastError();
+}
+
+extern "C" int qwk_gdn_decode(hipStream_t s, float *y, const float *x, const float *win, float *wout,
+                              const uint16_t *w, const qwk_gdn_prep *prep, float *state, int hk, int hv, int dk,
+                              int dv)
+{
+    if (dk != QG_DK || dv != QG_DV || hk < 1 || hv < 1 || hv % hk || !prep || !x || !win || !wout || !w)
+        return hipErrorInvalidValue;
+    const int channels = 2 * hk * dk + hv * dv;
+    const qg_prep pp = { prep->a, prep->b, prep->A_log, prep->dt_bias, prep->l2eps, prep->q_scale, prep->k_scale };
+    const qg_conv cv = { x, win, wout, w, channels };
+    hipLaunchKernelGGL((k_gated_delta<true, true>), dim3(hv * (QG_DV / QG_ROWS_PER_WG)), dim3(QG_THREADS), 0, s, y,
+                       nullptr, nullptr, nullptr, nullptr, nullptr, state, hk, hv, 1, nullptr, 0, 0, pp, cv);
     return (int)hipGetLastError();
 }
 

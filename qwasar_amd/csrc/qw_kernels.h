@@ -237,6 +237,12 @@ int qwk_gdn_gates(hipStream_t s, float *g, float *beta, const float *a, const fl
 int qwk_gated_delta(hipStream_t s, float *y, const float *q, const float *k, const float *v,
                     const float *g, const float *beta, float *state, int hk, int hv, int dk, int dv,
                     int rows, float *snap, int n_snap, int snap_stride, const qwk_gdn_prep *prep);
+/* One decode step: the conv over x [2 hk dk + hv dv] (window win in, wout
+ * out: distinct buffers, [3, channels] oldest first), then the prepared delta
+ * rule on its q, k and v channels; the bits of qwk_conv1d_causal_silu then
+ * qwk_gated_delta with prep. */
+int qwk_gdn_decode(hipStream_t s, float *y, const float *x, const float *win, float *wout, const uint16_t *w,
+                   const qwk_gdn_prep *prep, float *state, int hk, int hv, int dk, int dv);
 /* rms_norm(x) (* w) * sigmoid(gate) per row (qw_norm.hip); dim % 4 == 0. */
 int qwk_rms_norm_gated_sigmoid(hipStream_t s, float *y, const float *x, const uint16_t *w, const float *gate,
                                int dim, int rows, float eps, float out_scale);

@@ -1139,6 +1139,28 @@ void qw_op_gated_delta_prep(qw_cmd c, qw_ref y, qw_ref q, qw_ref k, qw_ref v, co
     gated_delta(c, y, q, k, v, none, none, prep, state, hk, hv, dk, dv, rows, snap, n_snap, snap_stride);
 }
 
+bool qw_op_gdn_decode(qw_cmd c, qw_ref y, qw_ref x, qw_ref conv_state, qw_ref conv_state_out, qw_ref conv_weight,
+                      const qw_gdn_prep *prep, qw_ref state, int32_t hk, int32_t hv, int32_t dk, int32_t dv) {
+    if (!prep || dk != 128 || dv != 128 || hk < 1 || hv < 1 || hv % hk) return false;
+    /* every workgroup reads the old window of the q and k channels while one
+     * writes the new: the window out may not share a byte with the window in
+     * or with x */
+    const size_t ch = (size_t)2 * hk * dk + (size_t)hv * dv;
+    if (refs_overlap(conv_state_out, 12 * ch, conv_state, 12 * ch) || refs_overlap(conv_state_out, 12 * ch, x, 4 * ch))
+        return false;
+    if (!c) return true;
+    touch(c, x, 0); touch(c, conv_state, 0); touch(c, conv_weight, 0);
+    touch(c, prep->a, 0); touch(c, prep->b, 0); touch(c, prep->A_log, 0); touch(c, prep->dt_bias, 0);
+    touch(c, conv_state_out, 1); touch(c, state, 1); touch(c, y, 1);
+    qwk_gdn_prep pp;
+    pp.a = dp(prep->a); pp.b = dp(prep->b); pp.A_log = dp(prep->A_log); pp.dt_bias = dp(prep->dt_bias);
+    pp.l2eps = prep->l2eps; pp.q_scale = prep->q_scale; pp.k_scale = prep->k_scale;
+    const int rc = qwk_gdn_decode(G.stream, dp(y), dp(x), dp(conv_state), dp(conv_state_out), dp(conv_weight), &pp,
+                                  dp(state), hk, hv, dk, dv);
+    launched(c, "gdn_decode", rc);
+    return rc == 0;
+}
+
 void qw_op_rms_norm_gated_sigmoid(qw_cmd c, qw_ref y, qw_ref x, qw_ref weight, qw_ref gate, int32_t dim,
                                   int32_t rows, float eps, float out_scale) {
     QW_OP(c);

@@ -145,6 +145,7 @@ _sig("qw_op_gdn_gates", None, _P, _R, _R, _R, _R, _R, _R, _I, _I)
 _sig("qw_op_gated_delta", None, _P, _R, _R, _R, _R, _R, _R, _R, _I, _I, _I, _I, _I, _R, _I, _I)
 _sig("qw_op_gated_delta_prep", None, _P, _R, _R, _R, _R, C.POINTER(qw_gdn_prep), _R, _I, _I, _I, _I, _I, _R, _I,
      _I)
+_sig("qw_op_gdn_decode", _B, _P, _R, _R, _R, _R, _R, C.POINTER(qw_gdn_prep), _R, _I, _I, _I, _I)
 _sig("qw_op_rms_norm_gated_sigmoid", None, _P, _R, _R, _R, _R, _I, _I, _F, _F)
 _sig("qw_op_qsa_scores", None, _P, _R, _R, _R, _R, _R, _I, _I, _I, _I, _I, _I, _I, _F)
 _sig("qw_op_qsa_pool", None, _P, _R, _R, _R, _R, _I, _I, _I, _I, _I, _F)

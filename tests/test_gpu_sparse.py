@@ -303,6 +303,54 @@ def test_gated_delta(gpu, hk, hv, rows):
         assert same_bits(st, s1)
 
 
+@pytest.mark.parametrize("hk,hv", [(2, 4), (16, 48)])
+def test_gdn_decode_one_launch(gpu, hk, hv):
+    """The fused decode step (conv, then the prepared delta rule on the
+    conv's q, k and v channels) against the two ops it replaces, bit for bit
+    in y, the state and the conv window, over three steps that alternate
+    the two windows; and the first step's y against the oracle."""
+    dk = dv = 128
+    ch = 2 * hk * dk + hv * dv
+    B = gpu.Buf
+    wq = synth.to_bf16(rnd((ch, 4), 60, -0.5, 0.5))
+    w = B.of(wq)
+    Al = np.ascontiguousarray(np.resize(FX["A_log"], hv))
+    dt = np.ascontiguousarray(np.resize(FX["dt_bias"], hv))
+    Ab, db = B.of(Al), B.of(dt)
+    eps, qs, ks = 1e-6 / dk, 1.0 / dk, 1.0 / np.sqrt(dk)
+    s0 = rnd((hv, dv, dk), 61) * np.float32(0.05)
+    c0 = rnd((3, ch), 62)
+    sA, sB = B.of(s0), B.of(s0)                      # fused, reference
+    wA0, wA1, wB = B.of(c0), B(3 * ch * 4), B.of(c0)  # windows: fused alternate, reference in place
+    yA, yB, mix = B(hv * dv * 4), B(hv * dv * 4), B(ch * 4)
+    for step in range(3):
+        x = rnd((1, ch), 70 + step)
+        a, bg = rnd((1, hv), 80 + step), rnd((1, hv), 90 + step)
+        xb, ab, bb = B.of(x), B.of(a), B.of(bg)
+        prep = gpu.qw_gdn_prep(ab.ref(), bb.ref(), Ab.ref(), db.ref(), eps, qs, ks)
+        win_in, win_out = (wA0, wA1) if step % 2 == 0 else (wA1, wA0)
+        c = gpu.qw_cmd_begin()
+        assert gpu.qw_op_gdn_decode(c, yA.ref(), xb.ref(), win_in.ref(), win_out.ref(), w.ref(), prep, sA.ref(),
+                                    hk, hv, dk, dv)
+        gpu.qw_op_conv1d_causal_silu(c, mix.ref(), xb.ref(), wB.ref(), w.ref(), ch, 1, 4, gpu.NULL_REF, 0, 0)
+        kd = hk * dk
+        gpu.qw_op_gated_delta_prep(c, yB.ref(), mix.ref(0), mix.ref(4 * kd), mix.ref(8 * kd), prep, sB.ref(), hk, hv,
+                                   dk, dv, 1, gpu.NULL_REF, 0, 0)
+        gpu.run(c, "gdn decode")
+        ya, yb = yA.read(np.float32, (hv, dv)), yB.read(np.float32, (hv, dv))
+        assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32)), f"y, step {step}"
+        assert np.array_equal(sA.read(np.uint32, (hv, dv, dk)), sB.read(np.uint32, (hv, dv, dk))), f"state, step {step}"
+        assert np.array_equal(win_out.read(np.uint32, (3, ch)), wB.read(np.uint32, (3, ch))), f"window, step {step}"
+        if step == 0:
+            m = sparse.conv1d_causal_silu(x, c0, wq, ch, 1, 4)[0]
+            wy, _, _ = sparse.gated_delta_prep(m[:, :kd].reshape(1, hk, dk), m[:, kd:2 * kd].reshape(1, hk, dk),
+                                               m[:, 2 * kd:].reshape(1, hv, dv), a, bg, Al, dt, eps, qs, ks, s0, hk,
+                                               hv, dk, dv, 1)
+            assert rel_l2(ya, wy.reshape(hv, dv)) < 5e-6
+        for t in (xb, ab, bb):
+            t.free()
+
+
 @pytest.mark.parametrize("hk,hv,rows", [(2, 4, 3), (16, 48, 20)])
 def test_gated_delta_prep(gpu, hk, hv, rows):
     """Norms and gates inside the recurrence, against the oracle's prep and
