@@ -113,3 +113,25 @@ def test_c_caller_compiles_as_c99():
     r = subprocess.run(["gcc", "-std=c99", "-pedantic", "-Wall", "-Wextra", "-Werror", "-fsyntax-only",
                         "-I", inc, src], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_gdn_decode_refuses_overlapping_windows():
+    """qw_op_gdn_decode's window out may not share a byte with the window in
+    or with x (its workgroups read the old window while one writes the new);
+    checked on the shape alone, with no command and no device."""
+    from qwasar_amd import gpu
+    hk, hv, d = 2, 4, 128
+    ch = 2 * hk * d + hv * d
+    A, B = 0x1000, 0x2000          # two stand-in buffer handles, never dereferenced
+    r = lambda buf, off=0: gpu.qw_ref(buf, off)
+    N = gpu.NULL_REF
+    prep = gpu.qw_gdn_prep(N, N, N, N, 1e-6, 1.0, 1.0)
+
+    def call(x, win, wout, dk=d):
+        return gpu.qw_op_gdn_decode(None, N, x, win, wout, N, prep, N, hk, hv, dk, d)
+
+    assert call(r(B), r(A), r(A, 12 * ch))
+    assert not call(r(B), r(A), r(A, 12 * ch - 4)), "window out over the window in's tail"
+    assert not call(r(B), r(A), r(B, 4 * ch - 4)), "window out over x"
+    assert not call(r(B), r(A), r(A)), "the same window"
+    assert not call(r(B), r(A), r(A, 12 * ch), dk=64), "head dims other than 128"
