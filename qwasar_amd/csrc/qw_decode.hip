@@ -79,6 +79,9 @@ extern "C" int qd_hwid_read(unsigned int *dst)
 #define QD_THREADS (QD_WAVES * 64)
 #define QD_GU_MAXRPB (QD_WAVES * 4)
 #define QD_LDS (64 * 1024)          // dynamic LDS: staged inputs, or the router's rows and partials
+#ifndef QD_DOWN_RATE
+#define QD_DOWN_RATE 35000.0        // bytes a 100 MHz tick the experts' stream moves (see down_delay)
+#endif
 #define QD_DOWN_LPR 16
 #define QD_DOWN_RIT 4               // down rows per lane slot
 #define QD_DOWN_RPG ((64 / QD_DOWN_LPR) * QD_DOWN_RIT)
@@ -203,6 +206,7 @@ struct QdArgs {
     uint4 *qx, *qsh, *qact;         // q16 units: [vector][units][3]
     QdSync *sync;
     uint32_t epoch;
+    uint32_t down_delay;            // wall-clock ticks (100 MHz) the down loads wait after routing
 };
 
 // One wave: each lane with `has` waits until its tagged word {epoch, value}
@@ -900,12 +904,14 @@ __device__ __forceinline__ void qd_role_down(const QdArgs &a, int bd, QdRoute &R
         sm = a.m.down.s + e * H * groups;
         bm = a.m.down.b + e * H * groups;
     }
-#ifdef QD_DOWN_DELAY
+    // The down rows are not needed before the experts' activations, and
+    // each CU's L1 passes misses at a bounded rate: requested at once they
+    // would slow the routed experts' gate/up stream on the CUs both share.
+    // So they wait, after routing, about the time that stream takes.
     {
         const unsigned long long t0 = wall_clock64();
-        while (wall_clock64() - t0 < QD_DOWN_DELAY) __builtin_amdgcn_s_sleep(2);
+        while (wall_clock64() - t0 < a.down_delay) __builtin_amdgcn_s_sleep(2);
     }
-#endif
     // Every load is issued (at a clamped, valid address) before any is used.
     // The scales and biases of the workgroup's RPG rows are contiguous
     // (RPG * groups bf16 each, at most 256: kin <= 512, groups of >= 32):
@@ -1129,6 +1135,13 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     a.qact = (uint4 *)(S + L.qact);
     a.sync = (QdSync *)sync;
     a.epoch = epoch;
+    {
+        // the routed experts' gate/up bytes at the rate the chip's L1s pass
+        // them (~3.5 TB/s, 35,000 bytes a tick): at config 1 (17.7 MB) ~5 us,
+        // measured best at 4.5-6 (3: 22.3 us a token, 10: 26.1, none: 23.6)
+        const double gu = (double)M->K * 2.0 * M->I * ((double)M->H / 2.0 + 4.0 * (M->H >> a.lgG));
+        a.down_delay = (uint32_t)(gu / QD_DOWN_RATE);
+    }
     // one token: K + 1 activation vectors of at most QD_TU q16 units each
     if (a.tch < 1 || a.umax > QD_MAXU || M->I / 16 > QD_TU || M->SI / 16 > QD_TU || a.n_rt > QD_RDSTRIDE)
         return (int)hipErrorInvalidValue;
