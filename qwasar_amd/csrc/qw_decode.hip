@@ -530,47 +530,44 @@ __device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, i
     // Every load is issued (at a clamped, valid address) before any is used;
     // out-of-range lanes are zeroed afterwards.
     //
-    // With a whole wave on a row (LPR 64), lane lr takes units 4 lr .. 4 lr + 3
-    // (64 consecutive inputs: two 16-byte loads a matrix, and one scale and
-    // one bias load -- a b32 of two when G = 32); else lane lr takes units
-    // lr, lr + LPR, ... (NUL of them).
+    // With a whole wave on a row (LPR 64), lane lr takes the unit pairs
+    // (2 lr, 2 lr + 1) and (128 + 2 lr, 128 + 2 lr + 1): two 16-byte loads a
+    // matrix, each instruction of the wave reading whole lines, and a scale
+    // and a bias a pair (a pair is 32 inputs, inside one group); else lane lr
+    // takes units lr, lr + LPR, ... (NUL of them).
     constexpr bool CG = LPR == 64;
     constexpr int NW = CG ? 4 : NUL;               // units a lane
     uint2 wv[2][NW];
     uint32_t sb[2][CG ? 2 : NUL];                  // bf16 scale (low half) and bias (high half)
     const int rowc = min(row, n - 1);
     if constexpr (CG) {
-        const int nl = units / 4, lc = min(lr, nl - 1);
-        const bool ok = row < n && lr < nl;
+        // lane lr: unit pairs (2 lr, 2 lr + 1) and (128 + 2 lr, 128 + 2 lr + 1),
+        // so each 16-byte load instruction of the wave reads whole lines
         uint4 w4[2][2];
-        uint32_t sv[2], bv[2];
+        uint32_t sv[2][2], bv[2][2];
+        bool okp[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) okp[h] = row < n && 128 * h + 2 * lr + 1 < units;
 #pragma unroll
         for (int z = 0; z < 2; z++) {
             const qwk_q4 q = z ? um : gm;
-            const uint4 *src = reinterpret_cast<const uint4 *>(q.w + (size_t)rowc * words + 8 * lc);
-            w4[z][0] = src[0];
-            w4[z][1] = src[1];
-            const size_t gi = (size_t)rowc * groups + ((64 * lc) >> lgG);
-            if (lgG == 5) {
-                sv[z] = *reinterpret_cast<const uint32_t *>(q.s + gi);
-                bv[z] = *reinterpret_cast<const uint32_t *>(q.b + gi);
-            } else {
-                sv[z] = q.s[gi];
-                bv[z] = q.b[gi];
-            }
-        }
-#pragma unroll
-        for (int z = 0; z < 2; z++) {
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                wv[z][2 * h] = ok ? make_uint2(w4[z][h].x, w4[z][h].y) : make_uint2(0, 0);
-                wv[z][2 * h + 1] = ok ? make_uint2(w4[z][h].z, w4[z][h].w) : make_uint2(0, 0);
+                const int c0 = min(128 * h + 2 * lr, units - 2);
+                w4[z][h] = *reinterpret_cast<const uint4 *>(q.w + (size_t)rowc * words + 2 * c0);
+                const size_t gi = (size_t)rowc * groups + ((16 * c0) >> lgG);
+                sv[z][h] = q.s[gi];
+                bv[z][h] = q.b[gi];
             }
-            // group of unit j: one for all four when G >= 64, j / 2 when G = 32
-            sb[z][0] = ok ? (sv[z] & 0xFFFFu) | (bv[z] << 16) : 0u;
-            sb[z][1] = ok ? (sv[z] >> 16) | (bv[z] & 0xFFFF0000u) : 0u;
-            if (lgG != 5) sb[z][1] = sb[z][0];
         }
+#pragma unroll
+        for (int z = 0; z < 2; z++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                wv[z][2 * h] = okp[h] ? make_uint2(w4[z][h].x, w4[z][h].y) : make_uint2(0, 0);
+                wv[z][2 * h + 1] = okp[h] ? make_uint2(w4[z][h].z, w4[z][h].w) : make_uint2(0, 0);
+                sb[z][h] = okp[h] ? sv[z][h] | (bv[z][h] << 16) : 0u;
+            }
     } else {
         uint32_t sv[2][NUL], bv[2][NUL];
 #pragma unroll
@@ -622,7 +619,7 @@ __device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, i
             float acc[2] = {0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < NW; j++) {
-                const int c = CG ? min(4 * lr + j, units - 1) : j * LPR + lr;
+                const int c = CG ? min(128 * (j / 2) + 2 * lr + (j % 2), units - 1) : j * LPR + lr;
                 if (CG || c < units) {
                     const uint4 p0 = xt[3 * c], p1 = xt[3 * c + 1];
                     const uint4 rr = xt[3 * c + 2];
