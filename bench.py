@@ -163,7 +163,7 @@ def time_prefill(gpu, lb, x, reps):
     return ms, int(counts.max()), int((counts > 0).sum())
 
 
-def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444, read_ahead=True):
+def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444, read_ahead=False):
     """`nlayers` layers of config 1's shape (weights written
     on the device), joined by the residual bf16 RMS norm; one `rows`-token
     prefill, then `steps` decode steps, each fed a fresh N(0, 1) token."""
@@ -628,8 +628,9 @@ def main():
     ap.add_argument("--no-config2", action="store_true", help="skip config 2 (batch-8 decode)")
     ap.add_argument("--no-config4", action="store_true", help="skip the 48-layer stack (config 4)")
     ap.add_argument("--config4-only", action="store_true", help="run only the 48-layer stack and print it")
-    ap.add_argument("--no-read-ahead", action="store_true",
-                    help="config 4 decode without reading the next layer's router rows ahead")
+    ap.add_argument("--read-ahead", action="store_true",
+                    help="config 4 decode reading the next layer's router rows ahead (off: slower since the "
+                         "down loads wait for the experts' stream)")
     ap.add_argument("--no-hc", action="store_true", help="skip the hyper-connection mixer")
     ap.add_argument("--hc-only", action="store_true", help="run only the hyper-connection mixer and print it")
     ap.add_argument("--no-sparse", action="store_true", help="skip QSA and the gated DeltaNet")
@@ -665,7 +666,7 @@ def main():
         print(json.dumps({"sparse": bench_sparse(gpu)}), flush=True)
         return
     if args.config4_only:
-        print(json.dumps({"config4": bench_stack(gpu, 48, 2048, 256, 4, read_ahead=not args.no_read_ahead)}),
+        print(json.dumps({"config4": bench_stack(gpu, 48, 2048, 256, 4, read_ahead=args.read_ahead)}),
               flush=True)
         return
     if args.decode_only_steps:
@@ -761,7 +762,7 @@ def main():
         out["prefill"] = pf
 
     if not args.no_config4:
-        out["config4"] = bench_stack(gpu, 48, 2048, 256, 4, read_ahead=not args.no_read_ahead)
+        out["config4"] = bench_stack(gpu, 48, 2048, 256, 4, read_ahead=args.read_ahead)
     if not args.no_hc:
         out["hc_mixer"] = bench_hc(gpu, 200)
     if not args.no_sparse:

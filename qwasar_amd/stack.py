@@ -136,7 +136,7 @@ class Stack:
                 raise RuntimeError(f"qw_op_moe_layer refused layer {l} at {rows} rows")
             gpu.qw_op_residual_rms_norm_bf16(c, self.h.ref(), self.x.ref(), self.y.ref(), self.H, rows, EPS)
 
-    def encode_fused(self, c, rows: int, read_ahead: bool = True) -> None:
+    def encode_fused(self, c, rows: int, read_ahead: bool = False) -> None:
         """The whole stack over h[:rows] with each residual step folded into
         the next layer's op (qw_op_moe_layer_residual_next; at decode sizes
         inside its one launch): layer l reads h from one of two buffers and
