@@ -637,6 +637,10 @@ __device__ bool qh_wait_words(const uint2 *p, int n, uint32_t *err, uint32_t epo
     }
 }
 
+#ifndef QH_UP_RATE
+#define QH_UP_RATE 200.0     // bytes a 100 MHz tick through one CU's L1 (~20 GB/s), for up_delay
+#endif
+
 struct QhArgs {
     float *x, *h4_out, *n4, *d, *inj_out;
     const float *h4, *out, *inj;
@@ -647,6 +651,7 @@ struct QhArgs {
     uint32_t *err;
     uint2 *tw;
     uint32_t epoch;
+    uint32_t up_delay;        // wall-clock ticks (100 MHz) before the up role requests its weights
 };
 
 template <int NI>
@@ -749,6 +754,13 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
     const int i = min(i0 + o, H - 1);
     const size_t grow = (size_t)s * H + i;
     const int words = k / 8, groups = k >> a.lgG;
+    // The up rows wait until the down workgroups have read their streams
+    // and rows (about the time those bytes take through a CU's L1): the two
+    // roles share CUs, and the down phase is the critical path.
+    {
+        const unsigned long long t0 = wall_clock64();
+        while (wall_clock64() - t0 < a.up_delay) __builtin_amdgcn_s_sleep(2);
+    }
     uint32_t wq[QH_UP_NJ], sb[QH_UP_NJ];
 #pragma unroll
     for (int j = 0; j < QH_UP_NJ; j++) {
@@ -853,6 +865,15 @@ extern "C" int qwk_hc_decode(hipStream_t s, float *x, float *h4_out, float *n4, 
     a.ow = 32 / S;
     a.eps = eps; a.scale = scale;
     a.err = err; a.tw = (uint2 *)tags; a.epoch = epoch;
+    {
+        // a down workgroup's bytes (streams, out row, norm gains, its rows'
+        // words, scales and biases) at ~20 GB/s, a CU's L1 under load: 5 us
+        // at H 3072, S 4 (A/B: 2.5 us 12.8, 5 us 12.6-12.7, 7 us 13.7,
+        // none 13.0 us a step)
+        const double bytes = (double)HH * 4 + (double)H * 4 + (double)HH * 2 +
+                             (double)QH_DR * ((double)HH / 2 + 4.0 * (HH / group));
+        a.up_delay = (uint32_t)(bytes / QH_UP_RATE);
+    }
     const int nu = (H + a.ow - 1) / a.ow;
     const int grid = a.nd + S + nu;
     // LDS: the normed streams, or the up role's inputs, 1/rms and mix terms
