@@ -398,16 +398,24 @@ __global__ __launch_bounds__(QW_DW_THREADS) void k_dmat_wide(float *__restrict__
 #define QW_DF_WAVES 8
 #define QW_DF_MAXR 8
 #define QW_DF_PAD 68
+#ifndef QW_DF_TPG
+#define QW_DF_TPG 2      // token rows a workgroup
+#endif
 __global__ __launch_bounds__(QW_DF_WAVES * 64) void k_dmat_few(float *__restrict__ y, float *__restrict__ g,
                                                                const float *__restrict__ x,
                                                                const uint16_t *__restrict__ w,
                                                                const uint16_t *__restrict__ w2, int k, int n,
                                                                int rows)
 {
-    extern __shared__ float xl[];                    // [rows][nch][QW_DF_PAD]
+    extern __shared__ float xl[];                    // [rows of this group][nch][QW_DF_PAD]
     __shared__ float part[QW_DF_WAVES][QW_DF_MAXR][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nch = k / 64, o = blockIdx.x * QW_DF_WAVES + wave;
+    // blockIdx.y: a group of QW_DF_TPG token rows (a workgroup stages only
+    // its group's rows: a CU's L1 passes a few tens of KB per round trip)
+    const int r0 = blockIdx.y * QW_DF_TPG;
+    x += (size_t)r0 * k;
+    rows = min(QW_DF_TPG, rows - r0);
     const bool has = o < n || (o == n && w2);
     const uint16_t *wr = o < n ? w + (size_t)o * k : w2;
     uint4 wv[8];
@@ -463,8 +471,8 @@ __global__ __launch_bounds__(QW_DF_WAVES * 64) void k_dmat_few(float *__restrict
     if (lane < rows) {
         float tot = part[wave][lane][0];
         for (int c = 1; c < nch; c++) tot = tot + part[wave][lane][c];
-        if (o < n) y[(size_t)lane * n + o] = tot;
-        else g[lane] = tot;
+        if (o < n) y[(size_t)(r0 + lane) * n + o] = tot;
+        else g[r0 + lane] = tot;
     }
 }
 
@@ -477,7 +485,7 @@ static bool qw_few_ok(const float *x, const uint16_t *w, int k, int rows)
 static int qw_launch_few(hipStream_t s, float *y, float *g, const float *x, const uint16_t *w, const uint16_t *w2,
                          int k, int n, int rows)
 {
-    const size_t lds = (size_t)rows * (k / 64) * QW_DF_PAD * sizeof(float);
+    const size_t lds = (size_t)min(rows, QW_DF_TPG) * (k / 64) * QW_DF_PAD * sizeof(float);
     static bool attr = false;
     if (!attr) {
         attr = true;
@@ -487,8 +495,8 @@ static int qw_launch_few(hipStream_t s, float *y, float *g, const float *x, cons
         (void)hipGetLastError();
     }
     const int outs = n + (w2 ? 1 : 0);
-    hipLaunchKernelGGL(k_dmat_few, dim3((outs + QW_DF_WAVES - 1) / QW_DF_WAVES), dim3(QW_DF_WAVES * 64), lds, s, y, g,
-                       x, w, w2, k, n, rows);
+    hipLaunchKernelGGL(k_dmat_few, dim3((outs + QW_DF_WAVES - 1) / QW_DF_WAVES, (rows + QW_DF_TPG - 1) / QW_DF_TPG),
+                       dim3(QW_DF_WAVES * 64), lds, s, y, g, x, w, w2, k, n, rows);
     return (int)hipGetLastError();
 }
 
