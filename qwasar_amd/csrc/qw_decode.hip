@@ -1211,6 +1211,7 @@ struct QbArgs {
     QdArgs d;                 // shapes, x, out, idx, w, rows, lgG, tch, qact, qsh
     const float *logits;
     int32_t *tab;
+    int xstaged;              // the router launch staged the token rows into qx
 };
 
 template <int PL>
@@ -1231,9 +1232,10 @@ __global__ __launch_bounds__(QD_MAXT * 64) void k_batch_route(QbArgs b)
             a.w[wave * K + lane] = pw;
         }
     }
-    // the token rows as q16 units for the gate / up launch
+    // the token rows as q16 units for the gate / up launch (unless the
+    // router's launch did)
     const int units = H / 16;
-    for (int i = t; i < a.rows * units; i += nthr) {
+    for (int i = t; i < (b.xstaged ? 0 : a.rows * units); i += nthr) {
         float v[16];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
@@ -1493,8 +1495,11 @@ extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, flo
     if (a.tch < 1 || xa_bytes > QD_LDS || a.umax > QD_MAXU) return (int)hipErrorInvalidValue;
     // the router logits and the shared expert's gate logits, one launch
     float *lg = (float *)(S + L.logits), *gl = (float *)(b.tab + QB_TAB_GATE);
-    int rc = qwk_dmat_bf16_gate(s, lg, gl, x, M->router, M->sh_gate_w, M->H, M->E, rows);
+    // (which also stages the token rows as q16 for the gate / up launch)
+    b.xstaged = 1;
+    int rc = qwk_dmat_bf16_gate(s, lg, gl, x, M->router, M->sh_gate_w, M->H, M->E, rows, a.qx);
     if (rc == (int)hipErrorInvalidValue) {   // a layout the one launch does not take: two order-R launches
+        b.xstaged = 0;
         rc = qwk_dmat_bf16(s, lg, x, M->router, M->H, M->E, rows);
         if (!rc) rc = qwk_dmat_bf16(s, gl, x, M->sh_gate_w, M->H, 1, rows);
     }

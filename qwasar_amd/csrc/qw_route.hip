@@ -405,7 +405,7 @@ __global__ __launch_bounds__(QW_DF_WAVES * 64) void k_dmat_few(float *__restrict
                                                                const float *__restrict__ x,
                                                                const uint16_t *__restrict__ w,
                                                                const uint16_t *__restrict__ w2, int k, int n,
-                                                               int rows)
+                                                               int rows, uint4 *__restrict__ qx)
 {
     extern __shared__ float xl[];                    // [rows of this group][nch][QW_DF_PAD]
     __shared__ float part[QW_DF_WAVES][QW_DF_MAXR][64];
@@ -443,6 +443,24 @@ __global__ __launch_bounds__(QW_DF_WAVES * 64) void k_dmat_few(float *__restrict
         }
     }
     __syncthreads();
+    if (qx && blockIdx.x == 0) {
+        // the group's rows also leave as q16 units (16 values, 3 uint4 each),
+        // for a launch that reads them after this one
+        const int units = k / 16;
+        for (int i = threadIdx.x; i < rows * units; i += QW_DF_WAVES * 64) {
+            const int r = i / units, u = i % units;
+            const float *src = xl + ((size_t)r * nch + (16 * u) / 64) * QW_DF_PAD + (16 * u) % 64;
+            float v[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = src[j];
+            uint4 q[3];
+            qw_q16_make(v, q);
+            uint4 *d = qx + ((size_t)(r0 + r) * units + u) * 3;
+            d[0] = q[0];
+            d[1] = q[1];
+            d[2] = q[2];
+        }
+    }
     if (!has) return;
     if (lane < nch) {
 #pragma unroll
@@ -483,7 +501,7 @@ static bool qw_few_ok(const float *x, const uint16_t *w, int k, int rows)
 }
 
 static int qw_launch_few(hipStream_t s, float *y, float *g, const float *x, const uint16_t *w, const uint16_t *w2,
-                         int k, int n, int rows)
+                         int k, int n, int rows, uint4 *qx = nullptr)
 {
     const size_t lds = (size_t)min(rows, QW_DF_TPG) * (k / 64) * QW_DF_PAD * sizeof(float);
     static bool attr = false;
@@ -496,15 +514,16 @@ static int qw_launch_few(hipStream_t s, float *y, float *g, const float *x, cons
     }
     const int outs = n + (w2 ? 1 : 0);
     hipLaunchKernelGGL(k_dmat_few, dim3((outs + QW_DF_WAVES - 1) / QW_DF_WAVES, (rows + QW_DF_TPG - 1) / QW_DF_TPG),
-                       dim3(QW_DF_WAVES * 64), lds, s, y, g, x, w, w2, k, n, rows);
+                       dim3(QW_DF_WAVES * 64), lds, s, y, g, x, w, w2, k, n, rows, qx);
     return (int)hipGetLastError();
 }
 
 extern "C" int qwk_dmat_bf16_gate(hipStream_t s, float *y, float *g, const float *x, const uint16_t *w,
-                                  const uint16_t *w2, int k, int n, int rows)
+                                  const uint16_t *w2, int k, int n, int rows, void *qx)
 {
-    if (n < 1 || !qw_few_ok(x, w, k, rows) || (w2 && ((uintptr_t)w2 % 16) != 0)) return (int)hipErrorInvalidValue;
-    return qw_launch_few(s, y, g, x, w, w2, k, n, rows);
+    if (n < 1 || !qw_few_ok(x, w, k, rows) || (w2 && ((uintptr_t)w2 % 16) != 0) || ((uintptr_t)qx % 16) != 0)
+        return (int)hipErrorInvalidValue;
+    return qw_launch_few(s, y, g, x, w, w2, k, n, rows, static_cast<uint4 *>(qx));
 }
 
 extern "C" int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint16_t *w,
