@@ -426,11 +426,14 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
                     for (int nt = 0; nt < 4; nt++) acc[mt][nt][e] = 0.0f;
                 }
         }
-        stash_a(q ^ 1);
+        // with at most 2 chunks an item, the two buffers hold every chunk
+        // once step 0 has stashed chunk 1, and the tile's rows are the same
+        // for every item: the activations are not read again
+        if (nch > 2 || i == 0) stash_a(q ^ 1);
         // the next block's scales and biases landed in LDS (the weights
         // issued after them stay in flight) before the barrier publishes them
         if (bstart) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NBL) : "memory");
-        fetch_a(i + 2);
+        if (nch > 2) fetch_a(i + 2);
         __syncthreads();
     };
 
