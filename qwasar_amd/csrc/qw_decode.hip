@@ -456,11 +456,9 @@ __device__ __forceinline__ void qd_role_router(const QdArgs &a, int b, float *ld
         if (t == 0) QD_TS(4);
         if (row) qd_router_row(w, xl, nch, a.sync->lgt + (size_t)t * (E + 1) + o, a.epoch, part);
     }
-#ifndef QD_NO_ACK
     // the logit stores are acknowledged (past this XCD's L2) before the
     // done words say so
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-#endif
     __syncthreads();
     if (threadIdx.x < QD_RDREP)
         __hip_atomic_store(reinterpret_cast<unsigned long long *>(a.sync->rdone + threadIdx.x * QD_RDSTRIDE + b),
