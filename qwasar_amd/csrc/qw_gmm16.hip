@@ -130,6 +130,7 @@ struct Gmm16Args {
     int rows;                       // dense: rows
     int nblk;                       // column blocks per tile
     int nbw;                        // column blocks a workgroup runs back to back
+    int cpx;                        // CUs an XCD (workgroups one round of items runs at once)
     int gpb;                        // quantisation groups per scale / bias block (1 .. 16)
     // the extra bank: tiles of expert xe use it; pairs p >= xpairs read A row
     // p - xpairs (when not x_by_pair)
@@ -161,12 +162,30 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     // tiles of one expert (adjacent in the list) share its weights, in that
     // XCD's L2.  A workgroup runs column blocks [nb0, nb0 + nitems) as one
     // stream of chunks.
+    //
+    // The items of an XCD (its tiles times their column groups) run on its
+    // cpx CUs in rounds.  The items past the last whole round are cut into
+    // single column blocks, so a part-filled last round holds short items
+    // spread over more CUs rather than whole ones on a few.
     const int bid = blockIdx.x, xcd = bid & 7, r = bid >> 3, ngr = (a.nblk + a.nbw - 1) / a.nbw;
     const int ntl = DENSE ? (a.rows + G16_BM - 1) / G16_BM : a.tiles[0];
-    const int tpx = (ntl + 7) / 8, tl = r / ngr;
-    if (tl >= tpx) return;
-    const int tile = xcd * tpx + tl, nb0 = (r % ngr) * a.nbw, nitems = min(a.nbw, a.nblk - nb0);
-    if (tile >= ntl) return;
+    const int tpx = (ntl + 7) / 8;
+    const int items = min(max(ntl - xcd * tpx, 0), tpx) * ngr, full = items - items % a.cpx;
+    int tl, nb0, nitems;
+    if (r < full || a.nbw == 1) {
+        if (r >= items) return;
+        tl = r / ngr;
+        nb0 = (r % ngr) * a.nbw;
+        nitems = min(a.nbw, a.nblk - nb0);
+    } else {
+        const int it = full + (r - full) / a.nbw;
+        if (it >= items) return;
+        tl = it / ngr;
+        nb0 = (it % ngr) * a.nbw + (r - full) % a.nbw;
+        if (nb0 >= a.nblk) return;
+        nitems = 1;
+    }
+    const int tile = xcd * tpx + tl;
     int expert, first, len;
     if (DENSE) {
         first = tile * G16_BM;
@@ -473,6 +492,20 @@ static void g16_launch(hipStream_t s, const Gmm16Args &a, int swiglu, int dense,
     else hipLaunchKernelGGL((k_gmm16<G, false, false, KC>), g, b, 0, s, a);
 }
 
+// CUs an XCD: the device's CUs over its 8 XCDs (of the current device, read
+// once; every device this library drives is an MI355X)
+static int g16_cus_per_xcd()
+{
+    static int cpx = 0;
+    if (!cpx) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = 256;
+        cpx = n >= 8 ? n / 8 : 1;
+    }
+    return cpx;
+}
+
 extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb, const float *aF,
                          const int32_t *perm, const int32_t *tiles, int max_tiles,
                          qwk_q4 m0, qwk_q4 m1, long ew, long eg, int k, int n, int K, int x_by_pair,
@@ -523,9 +556,11 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
         while (a.nblk % nbw) nbw--;
         a.nbw = nbw;
     }
-    // r = b / 8 < ngr * ceil(ntiles / 8) covers every XCD's tile range
+    a.cpx = g16_cus_per_xcd();
+    // r = b / 8 < ngr * ceil(ntiles / 8) covers every XCD's whole items, and
+    // cpx * nbw more its single blocks
     const int ngr = (a.nblk + a.nbw - 1) / a.nbw;
-    const unsigned grid = (unsigned)(ngr * ((ntiles + 7) / 8) * 8);
+    const unsigned grid = (unsigned)((ngr * ((ntiles + 7) / 8) + (a.nbw > 1 ? a.cpx * a.nbw : 0)) * 8);
     if (kc == 256) {
         switch (group) {
         case 32: g16_launch<32, 256>(s, a, swiglu, dense, grid); break;
