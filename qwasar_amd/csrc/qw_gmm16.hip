@@ -165,18 +165,32 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     //
     // The items of an XCD (its tiles times their column groups) run on its
     // cpx CUs in rounds.  The items past the last whole round are cut into
-    // single column blocks, so a part-filled last round holds short items
-    // spread over more CUs rather than whole ones on a few.
+    // shorter ones, so a part-filled last round holds short items spread
+    // over more CUs rather than whole ones on a few: into single column
+    // blocks; single blocks, when twice their number fits the CUs, into
+    // halves (half the weight rows: each wave owns 2 weight tiles of 16, not
+    // 4), and those, when twice their number fits again, into the tile's row
+    // halves.
     const int bid = blockIdx.x, xcd = bid & 7, r = bid >> 3, ngr = (a.nblk + a.nbw - 1) / a.nbw;
     const int ntl = DENSE ? (a.rows + G16_BM - 1) / G16_BM : a.tiles[0];
     const int tpx = (ntl + 7) / 8;
     const int items = min(max(ntl - xcd * tpx, 0), tpx) * ngr, full = items - items % a.cpx;
-    int tl, nb0, nitems;
-    if (r < full || a.nbw == 1) {
-        if (r >= items) return;
+    int tl, nb0, nitems, hc = 0, rh = -1;
+    bool half = false;
+    if (r < full) {
         tl = r / ngr;
         nb0 = (r % ngr) * a.nbw;
         nitems = min(a.nbw, a.nblk - nb0);
+    } else if (a.nbw == 1) {
+        const int rem = items - full, cs = 4 * rem <= 2 * a.cpx ? 2 : 1, rs = cs == 2 && 4 * rem <= a.cpx ? 2 : 1;
+        const int per = cs * rs, it = full + (r - full) / per, pc = (r - full) % per;
+        if (it >= items) return;
+        tl = it / ngr;
+        nb0 = it % ngr;
+        nitems = 1;
+        half = cs == 2;
+        hc = half ? pc & 1 : 0;
+        rh = rs == 2 ? pc >> 1 : -1;
     } else {
         const int it = full + (r - full) / a.nbw;
         if (it >= items) return;
@@ -186,6 +200,9 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
         nitems = 1;
     }
     const int tile = xcd * tpx + tl;
+    // NT weight tiles of 16 a wave: the item's BNT weight rows
+    auto body = [&](auto ntc) {
+    constexpr int NT = decltype(ntc)::value, NH = NT / 2, BNT = NT * 16 * (G16_THREADS / 64);
     int expert, first, len;
     if (DENSE) {
         first = tile * G16_BM;
@@ -201,7 +218,7 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     const int gpb = a.gpb, sbc = gpb * G / KC, nbk = groups / gpb;   // chunks a block, blocks an item
     if (t < G16_BM) {
         int sr = -1, dr = -1;
-        if (t < len) {
+        if (t < len && (rh < 0 || (t >> 5) == rh)) {
             const int p = DENSE ? first + t : a.perm[first + t];
             sr = DENSE ? p : (a.x_by_pair ? p : (p < a.xpairs ? p / a.K : p - a.xpairs));
             dr = p;
@@ -272,11 +289,11 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
         }
     }
     auto rowof = [&](int nt) {
-        return SWIGLU ? (nt >> 1) * (G16_BN / 2) + wave * 32 + (nt & 1) * 16 + ln : wave * 64 + nt * 16 + ln;
+        return SWIGLU ? (nt / NH) * (BNT / 2) + wave * (NH * 16) + (nt % NH) * 16 + ln : wave * (NT * 16) + nt * 16 + ln;
     };
     auto colof = [&](int item, int j) {
         const int nb = nb0 + item;
-        return SWIGLU ? nb * (G16_BN / 2) + (j % (G16_BN / 2)) : nb * G16_BN + j;
+        return SWIGLU ? nb * (G16_BN / 2) + hc * (BNT / 2) + (j % (BNT / 2)) : nb * G16_BN + hc * BNT + j;
     };
     // Per chunk, lane kg holds the KPL consecutive k from kg KPL of each of
     // its rows: WPL consecutive words.  MFMA step s takes word s of every
@@ -284,12 +301,12 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     // Weight words come in load groups of WGP (one 16- or 8-byte load a
     // row): group lg of chunk `step` into wq[nt][lg WGP ..].
     constexpr int WGP = WPL == 2 ? 2 : 4, NLG = WPL / WGP;
-    auto fetch_bg = [&](int step, int lg, uint32_t (&wq)[4][WPL]) {
+    auto fetch_bg = [&](int step, int lg, uint32_t (&wq)[NT][WPL]) {
         step = min(step, T - 1);
         const int item = step / nch, c = step % nch;
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++) {
-            const int h = SWIGLU ? nt >> 1 : 0;
+        for (int nt = 0; nt < NT; nt++) {
+            const int h = SWIGLU ? nt / NH : 0;
             const int col = colof(item, rowof(nt)), cc = col < a.n ? col : 0;
             const uint32_t o = (uint32_t)((cc * words + c * (KC / 8) + kg * WPL + lg * WGP) * 4);
             if (WGP == 2) {
@@ -318,7 +335,8 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     auto fetch_sb = [&](int beta, int q) {
         beta = min(beta, nblocks - 1);
         const int item = beta / nbk, blk = beta % nbk;
-        const int h = SWIGLU ? __builtin_amdgcn_readfirstlane(t / (G16_BN / 2)) : 0;
+        if (NT < 4 && t >= BNT) return;    // (wave-uniform) no row of this item
+        const int h = SWIGLU ? __builtin_amdgcn_readfirstlane(t / (BNT / 2)) : 0;
         const int col = colof(item, t), cc = col < a.n ? col : 0;
         const uint32_t o = (uint32_t)((cc * groups + blk * gpb) * 2);
         // this wave's 64 rows of region j start at j * BN * LS + wave * 64 * LS
@@ -344,13 +362,13 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     };
     // loads a step issues after the block's: the weights (the wait before the
     // barrier that publishes a block leaves them in flight)
-    constexpr int NBL = 4 * (WPL == 2 ? 1 : WPL / 4);
+    constexpr int NBL = NT * (WPL == 2 ? 1 : WPL / 4);
 
-    g16_f4 acc[4][4];
+    g16_f4 acc[4][NT];
 #pragma unroll
     for (int mt = 0; mt < 4; mt++)
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++) acc[mt][nt] = g16_f4{0.f, 0.f, 0.f, 0.f};
+        for (int nt = 0; nt < NT; nt++) acc[mt][nt] = g16_f4{0.f, 0.f, 0.f, 0.f};
     uint32_t lo = 0x64006400u, hi = 0x54005400u;
     asm volatile("" : "+v"(lo), "+v"(hi));
 
@@ -361,16 +379,16 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     // ring: every word has a chunk's time to land).  At a block's first chunk
     // the next block's scales and biases are issued; the chunk after next's
     // activations go to registers once this one's are in LDS.
-    uint32_t wq[4][WPL];
+    uint32_t wq[NT][WPL];
     auto step = [&](int i) {
         const int q = i & 1, item = i / nch, c = i % nch;
         const int beta = item * nbk + c / sbc;
         const bool bstart = c % sbc == 0;
-        g16_h2 s2[4][NGL], b2[4][NGL];
+        g16_h2 s2[NT][NGL], b2[NT][NGL];
         {
             const int gl = ((c % sbc) * KC + kg * KPL) / G;
 #pragma unroll
-            for (int nt = 0; nt < 4; nt++)
+            for (int nt = 0; nt < NT; nt++)
 #pragma unroll
                 for (int g = 0; g < NGL; g++) {
                     s2[nt][g] = g16_bf2h2(sb_at(beta & 1, rowof(nt), gl + g, 0), 0);
@@ -385,16 +403,16 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
 #pragma unroll
             for (int mt = 0; mt < 4; mt++) o[mt] = *reinterpret_cast<const g16_h8 *>(&As[q][mt * 16 + ln][ah]);
         };
-        auto dqs = [&](int st, g16_h8 (&o)[4]) {
+        auto dqs = [&](int st, g16_h8 (&o)[NT]) {
             const int g = NGL == 1 ? 0 : st * 8 / G;
 #pragma unroll
-            for (int nt = 0; nt < 4; nt++) {
+            for (int nt = 0; nt < NT; nt++) {
                 uint32_t d[4];
                 g16_dq(wq[nt][st], s2[nt][g], b2[nt][g], lo, hi, d);
                 o[nt] = __builtin_bit_cast(g16_h8, g16_u4{d[0], d[1], d[2], d[3]});
             }
         };
-        g16_h8 af[2][4], bf[2][4];
+        g16_h8 af[2][4], bf[2][NT];
         lda(0, af[0]);
         dqs(0, bf[0]);
 #pragma unroll
@@ -407,7 +425,7 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
 #pragma unroll
             for (int mt = 0; mt < 4; mt++)
 #pragma unroll
-                for (int nt = 0; nt < 4; nt++)
+                for (int nt = 0; nt < NT; nt++)
                     acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[cu][mt], bf[cu][nt], acc[mt][nt], 0, 0, 0);
             // word st + 1 was a load group's last: refill the group
             if (st + 1 < WPL && (st + 2) % WGP == 0) {
@@ -429,20 +447,20 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
                         float *yr = a.y + (size_t)dr * a.ldy;
                         if (SWIGLU) {
 #pragma unroll
-                            for (int nt = 0; nt < 2; nt++) {
+                            for (int nt = 0; nt < NH; nt++) {
                                 const int col = colof(item, rowof(nt));
-                                if (col < a.n) yr[col] = qw_silu(f * acc[mt][nt][e]) * (f * acc[mt][nt + 2][e]);
+                                if (col < a.n) yr[col] = qw_silu(f * acc[mt][nt][e]) * (f * acc[mt][nt + NH][e]);
                             }
                         } else {
 #pragma unroll
-                            for (int nt = 0; nt < 4; nt++) {
+                            for (int nt = 0; nt < NT; nt++) {
                                 const int col = colof(item, rowof(nt));
                                 if (col < a.n) yr[col] = f * acc[mt][nt][e];
                             }
                         }
                     }
 #pragma unroll
-                    for (int nt = 0; nt < 4; nt++) acc[mt][nt][e] = 0.0f;
+                    for (int nt = 0; nt < NT; nt++) acc[mt][nt][e] = 0.0f;
                 }
         }
         // with at most 2 chunks an item, the two buffers hold every chunk
@@ -468,6 +486,9 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     fetch_a(1);
     __syncthreads();
     for (int i = 0; i < T; i++) step(i);
+    };
+    if (half) body(std::integral_constant<int, 2>{});
+    else body(std::integral_constant<int, 4>{});
 }
 
 // ---- host side ---------------------------------------------------------------------
@@ -558,9 +579,9 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
     }
     a.cpx = g16_cus_per_xcd();
     // r = b / 8 < ngr * ceil(ntiles / 8) covers every XCD's whole items, and
-    // cpx * nbw more its single blocks
+    // cpx * max(nbw, 4) more the pieces of its last round's (fewer than cpx)
     const int ngr = (a.nblk + a.nbw - 1) / a.nbw;
-    const unsigned grid = (unsigned)((ngr * ((ntiles + 7) / 8) + (a.nbw > 1 ? a.cpx * a.nbw : 0)) * 8);
+    const unsigned grid = (unsigned)((ngr * ((ntiles + 7) / 8) + a.cpx * (a.nbw > 4 ? a.nbw : 4)) * 8);
     if (kc == 256) {
         switch (group) {
         case 32: g16_launch<32, 256>(s, a, swiglu, dense, grid); break;
