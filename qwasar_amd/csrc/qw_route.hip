@@ -200,7 +200,13 @@ __global__ __launch_bounds__(256) void k_dmat_mfma(float *__restrict__ y, const 
     extern __shared__ float4 dm_lds[];
     float *xs = reinterpret_cast<float *>(dm_lds), *ws = xs + QW_DM_T * QW_DM_KS;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, blk = lane >> 4, i = lane & 15;
-    const int r0 = blockIdx.y * QW_DM_T, o0 = blockIdx.x * QW_DM_T;
+    // Workgroup b runs on XCD b % 8: each XCD takes a contiguous range of
+    // tiles in (row tile, column tile) order, so the column tiles of one row
+    // tile share its token rows in that XCD's L2
+    const int nct = (n + QW_DM_T - 1) / QW_DM_T, ntt = nct * ((rows + QW_DM_T - 1) / QW_DM_T);
+    const int lt = (blockIdx.x & 7) * ((ntt + 7) / 8) + (blockIdx.x >> 3);
+    if (lt >= ntt) return;
+    const int r0 = lt / nct * QW_DM_T, o0 = lt % nct * QW_DM_T;
     const int nch = k / 64, rounds = (nch + QW_DM_NC - 1) / QW_DM_NC;
     constexpr int SK = 64 * QW_DM_NC;                    // k a stage
     constexpr int XF4 = QW_DM_T * SK / 4 / 256, WU4 = QW_DM_T * SK / 8 / 256;
@@ -549,7 +555,8 @@ extern "C" int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint
             (void)hipFuncSetAttribute((const void *)k_dmat_mfma, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
             (void)hipGetLastError();
         }
-        hipLaunchKernelGGL(k_dmat_mfma, dim3((n + QW_DM_T - 1) / QW_DM_T, (rows + QW_DM_T - 1) / QW_DM_T), dim3(256), lds,
+        const int ntt = ((n + QW_DM_T - 1) / QW_DM_T) * ((rows + QW_DM_T - 1) / QW_DM_T);
+        hipLaunchKernelGGL(k_dmat_mfma, dim3((ntt + 7) / 8 * 8), dim3(256), lds,
                            s, y, x, w, k, n, rows);
         return (int)hipGetLastError();
     }
