@@ -355,6 +355,86 @@ __device__ __forceinline__ void qh_inject_norm(float4 *nl, float (*part)[QH_THRE
     __syncthreads();
 }
 
+// Stream s alone of qh_inject_norm: the same arithmetic for that stream (its
+// injected values, sum of squares, 1/rms and normed values bit for bit),
+// normed into nl[0, H / 4), nothing written to memory; returns the 1/rms.
+// after_loads() runs once the stream's loads are issued.  Every thread of
+// the workgroup calls it (it holds barriers).
+template <int NI, typename F>
+__device__ __forceinline__ float qh_norm1(float4 *nl, float (*part)[QH_THREADS / 64], int s,
+                                          const float *__restrict__ h4, const float *__restrict__ out,
+                                          const float *__restrict__ inj, const uint16_t *__restrict__ wn, int H,
+                                          int S, float eps, F &&after_loads)
+{
+    const int t = threadIdx.x, n4q = H / 4;
+    const int wave = t >> 6, lane = t & 63;
+    const float4 *hrow = reinterpret_cast<const float4 *>(h4 + (size_t)s * H);
+    const float4 *orow = reinterpret_cast<const float4 *>(out);
+    const uint2 *wrow = reinterpret_cast<const uint2 *>(wn + (size_t)s * H);
+    const float injv = inj[s];
+    constexpr int NR = NI > 0 ? NI : 1;
+    float4 hv[NR], ov[NR];
+    uint2 gw[NR];
+    if (NI > 0) {
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+            const int i = t + QH_THREADS * j;
+            const bool ok = i < n4q;
+            ov[j] = ok ? orow[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            hv[j] = ok ? hrow[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            gw[j] = ok ? wrow[i] : make_uint2(0, 0);
+        }
+    }
+    after_loads();
+    const float wgt = 2.0f * qh_sigmoid(injv / (float)S);
+    float ss = 0.0f;
+    auto inject = [&](float4 &v, float4 o) {
+        v.x += o.x * wgt; v.y += o.y * wgt; v.z += o.z * wgt; v.w += o.w * wgt;
+        ss = __builtin_fmaf(v.x, v.x, ss);
+        ss = __builtin_fmaf(v.y, v.y, ss);
+        ss = __builtin_fmaf(v.z, v.z, ss);
+        ss = __builtin_fmaf(v.w, v.w, ss);
+    };
+    if (NI > 0) {
+#pragma unroll
+        for (int j = 0; j < NR; j++)
+            if (t + QH_THREADS * j < n4q) inject(hv[j], ov[j]);
+    } else {
+        for (int i = t; i < n4q; i += QH_THREADS) {
+            float4 v = hrow[i];
+            inject(v, orow[i]);
+            nl[i] = v;
+        }
+    }
+    {
+        const float v = qw_xor_sum<64>(ss);
+        if (lane == 0) part[0][wave] = v;
+    }
+    __syncthreads();
+    float tot = part[0][0];
+#pragma unroll
+    for (int w = 1; w < QH_THREADS / 64; w++) tot = tot + part[0][w];
+    const float inv = 1.0f / sqrtf(tot / (float)H + eps);
+    auto scale = [&](int i, float4 v, uint2 wb) {
+        v.x = v.x * inv * __uint_as_float(wb.x << 16);
+        v.y = v.y * inv * __uint_as_float(wb.x & 0xFFFF0000u);
+        v.z = v.z * inv * __uint_as_float(wb.y << 16);
+        v.w = v.w * inv * __uint_as_float(wb.y & 0xFFFF0000u);
+        nl[i] = v;
+    };
+    if (NI > 0) {
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+            const int i = t + QH_THREADS * j;
+            if (i < n4q) scale(i, hv[j], gw[j]);
+        }
+    } else {
+        for (int i = t; i < n4q; i += QH_THREADS) scale(i, nl[i], wrow[i]);
+    }
+    __syncthreads();
+    return inv;
+}
+
 // Injection logit s (order R: a thread per 64-input chunk, each chunk an
 // fmaf chain from 0, the chunk sums left to right) of the normed row in LDS.
 // Every thread of the workgroup calls it (it holds a barrier).
@@ -568,19 +648,22 @@ extern "C" int qwk_hc_mix_up(hipStream_t s, float *x, const float *d, const floa
 // at the start, so their memory latency runs under the norm and the
 // down-projection instead of after them.  Roles by workgroup:
 //
-//   b < nd           down: inject + norm (as k_hc_pre), then QH_DR rows of d,
-//                    their block sums together (each the order of k_hc_pre);
-//                    d leaves as tagged words {epoch, bits}; workgroup 0 also
-//                    publishes the streams' 1/rms.  Then, once those stores
-//                    are acknowledged, a done word in each of QH_DREP copies.
+//   b < nd           down: stream s = b % S of QH_DR rows of d: the stream
+//                    injected and normed alone (a grouped norm keeps the
+//                    streams apart: the same bits as k_hc_pre's), then each
+//                    row's dot over the stream's H inputs, 32 lanes a row;
+//                    the partials leave as tagged words {epoch, bits}; the
+//                    workgroups of rows 0.. also publish their stream's
+//                    1/rms.  Then a done word in each of QH_DREP copies.
 //   nd <= b < nd+S   stream s = b - nd: inject + norm, writes stream s of
 //                    h4_out and n4 and the injection logit s (as k_hc_pre).
 //   the rest         up: OW = 32 / S outputs, 8 lanes on each of their S up
 //                    rows (lane: words lr, lr + 8, ...).  Weights in
 //                    registers first; then one wave polls the down
 //                    workgroups' done words (the copy of its XCD), the
-//                    workgroup reads d and 1/rms (tags checked), takes
-//                    silu(scale d) into LDS, and each row's dot meets in an
+//                    workgroup reads the partials and 1/rms (tags checked),
+//                    adds each row's S partials in stream order into d,
+//                    takes silu(scale d) into LDS, and each row's dot meets in an
 //                    xor tree; n4's values for its outputs are recomputed
 //                    from h4, out and the 1/rms, and the streams mixed in
 //                    order.
@@ -588,13 +671,17 @@ extern "C" int qwk_hc_mix_up(hipStream_t s, float *x, const float *d, const floa
 // Nothing waits on a workgroup dispatched after it (the down workgroups come
 // first), and every wait is bounded: on giving up it raises the error word
 // (the launch's epoch, unless set) and the workgroup finishes.
-#define QH_DR 2                   // down rows a workgroup
+#ifndef QH_DR
+#define QH_DR 8                   // down rows a workgroup (of one stream; 32 lanes a row)
+#endif
+#define QH_DLPR (QH_THREADS / QH_DR)   // lanes a down row
+#define QH_NSJ 8                  // 32-input segments a down lane holds (H <= 32 * QH_DLPR * QH_NSJ)
 #define QH_MAX_LR 512             // lowrank
 #define QH_UP_NJ 8                // words an up lane holds (k <= 512)
 #define QH_DREP 8                 // copies of the done words
-#define QH_DSTRIDE 264            // words between copies (>= QH_MAX_LR / QH_DR)
-#define QH_TD 8                   // tag words: [0, S) 1/rms, [QH_TD, +lowrank) d,
-#define QH_TDONE (QH_TD + QH_MAX_LR)   // then the done copies
+#define QH_DSTRIDE (QH_PRE_MAXS * QH_MAX_LR / QH_DR + 8)   // words between copies (>= the down workgroups)
+#define QH_TD 8                   // tag words: [0, S) 1/rms, [QH_TD, + S lowrank) d's partials
+#define QH_TDONE (QH_TD + QH_PRE_MAXS * QH_MAX_LR)   // (stream-major), then the done copies
 #define QH_TAG_WORDS (QH_TDONE + QH_DREP * QH_DSTRIDE)
 #define QH_SPIN_LIMIT (1 << 16)
 #ifndef QH_SLEEP
@@ -667,72 +754,56 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
     if (t == 0) qh_trace[blockIdx.x * 8 + 7] = __builtin_readcyclecounter();
 #endif
     if (b < a.nd) {
-        const int words = HH / 8, groups = HH >> a.lgG, nseg = HH / 32, r0 = b * QH_DR;
-        // the rows' weights, requested after the streams: their latency runs
-        // under the norm
-        uint4 wv[QH_DR][2];
-        float sc[QH_DR][2], bi[QH_DR][2];
+        const int sd = b % S, r0 = (b / S) * QH_DR, words = HH / 8, nsg = H / 32;
+        const int q = t / QH_DLPR, l = t % QH_DLPR, r = r0 + q;
+        const bool rok = r < k;
+        // the rows' words of this stream, requested after the stream: their
+        // latency runs under the norm
+        uint4 wv[QH_NSJ];
+        float sc[QH_NSJ], bi[QH_NSJ];
         auto weights = [&]() {
 #pragma unroll
-            for (int q = 0; q < QH_DR; q++)
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const int seg = t + QH_THREADS * j, r = r0 + q;
-                    const bool ok = seg < nseg && r < k;
-                    const int g = (seg * 32) >> a.lgG;
-                    wv[q][j] = ok ? *reinterpret_cast<const uint4 *>(a.dn.w + (size_t)r * words + seg * 4)
-                                  : make_uint4(0, 0, 0, 0);
-                    sc[q][j] = ok ? qw_bf16(a.dn.s[(size_t)r * groups + g]) : 0.0f;
-                    bi[q][j] = ok ? qw_bf16(a.dn.b[(size_t)r * groups + g]) : 0.0f;
-                }
+            for (int j = 0; j < QH_NSJ; j++) {
+                const int seg = l + QH_DLPR * j;
+                const bool ok = rok && seg < nsg;
+                const int in0 = sd * H + 32 * seg, g = in0 >> a.lgG;
+                const size_t gi = (size_t)r * (HH >> a.lgG) + g;
+                wv[j] = ok ? *reinterpret_cast<const uint4 *>(a.dn.w + (size_t)r * words + in0 / 8)
+                           : make_uint4(0, 0, 0, 0);
+                sc[j] = ok ? qw_bf16(a.dn.s[gi]) : 0.0f;
+                bi[j] = ok ? qw_bf16(a.dn.b[gi]) : 0.0f;
+            }
         };
-        float inv[QH_PRE_MAXS];
-        qh_inject_norm<NI>(nl, part, -1, a.h4_out, a.n4, a.h4, a.out, a.inj, a.wn, H, S, a.eps, inv, weights);
+        const float inv = qh_norm1<NI>(nl, part, sd, a.h4, a.out, a.inj, a.wn, H, S, a.eps, weights);
         QH_TS(1);
-        float acc[QH_DR];
+        float acc = 0.0f;
 #pragma unroll
-        for (int q = 0; q < QH_DR; q++) acc[q] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int seg = t + QH_THREADS * j;
-            if (seg < nseg) {
+        for (int j = 0; j < QH_NSJ; j++) {
+            const int seg = l + QH_DLPR * j;
+            if (seg < nsg) {
                 float xs[32];
 #pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    const float4 v = nl[seg * 8 + q];
-                    xs[4 * q] = v.x; xs[4 * q + 1] = v.y; xs[4 * q + 2] = v.z; xs[4 * q + 3] = v.w;
+                for (int e = 0; e < 8; e++) {
+                    const float4 v = nl[seg * 8 + e];
+                    xs[4 * e] = v.x; xs[4 * e + 1] = v.y; xs[4 * e + 2] = v.z; xs[4 * e + 3] = v.w;
                 }
                 float xsum = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 32; e++) xsum += xs[e];
-#pragma unroll
-                for (int q = 0; q < QH_DR; q++) {
-                    float dd = qw_dot8_q(wv[q][j].x, xs, 0.0f);
-                    dd = qw_dot8_q(wv[q][j].y, xs + 8, dd);
-                    dd = qw_dot8_q(wv[q][j].z, xs + 16, dd);
-                    dd = qw_dot8_q(wv[q][j].w, xs + 24, dd);
-                    acc[q] = __builtin_fmaf(sc[q][j], dd, acc[q]);
-                    acc[q] = __builtin_fmaf(bi[q][j], xsum, acc[q]);
-                }
+                float dd = qw_dot8_q(wv[j].x, xs, 0.0f);
+                dd = qw_dot8_q(wv[j].y, xs + 8, dd);
+                dd = qw_dot8_q(wv[j].z, xs + 16, dd);
+                dd = qw_dot8_q(wv[j].w, xs + 24, dd);
+                acc = __builtin_fmaf(sc[j], dd, acc);
+                acc = __builtin_fmaf(bi[j], xsum, acc);
             }
         }
-        static_assert(QH_DR <= QH_PRE_MAXS, "the rows' partials share part");
-#pragma unroll
-        for (int q = 0; q < QH_DR; q++) {
-            const float v = qw_xor_sum<64>(acc[q]);
-            if (lane == 0) part[q][wave] = v;
-        }
-        __syncthreads();
-        if (t < QH_DR && r0 + t < k) {
-            float s = part[t][0];
-#pragma unroll
-            for (int w = 1; w < QH_THREADS / 64; w++) s = s + part[t][w];
-            a.d[r0 + t] = s;
-            qh_st(a.tw + QH_TD + r0 + t, a.epoch, __float_as_uint(s));
-        }
-        if (b == 0 && t >= 64 && t < 64 + S) qh_st(a.tw + (t - 64), a.epoch, __float_as_uint(inv[t - 64]));
-        // the tagged stores acknowledged before the done words say so
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        acc = qw_xor_sum<QH_DLPR>(acc);
+        if (l == 0 && rok) qh_st(a.tw + QH_TD + sd * k + r, a.epoch, __float_as_uint(acc));
+        if (r0 == 0 && t == 0) qh_st(a.tw + sd, a.epoch, __float_as_uint(inv));
+        // the done words follow without waiting for those stores'
+        // acknowledgement: a reader checks every partial's tag and re-reads
+        // stale ones, so the done words only say when to start reading
         __syncthreads();
         QH_TS(2);
         if (t < QH_DREP) qh_st(a.tw + QH_TDONE + t * QH_DSTRIDE + b, a.epoch, 0u);
@@ -780,13 +851,15 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
         wnv = __uint_as_float((uint32_t)a.wn[grow] << 16);
     }
     float *xsl = reinterpret_cast<float *>(nl);            // [k]
-    float *invl = xsl + QH_MAX_LR;                          // [S]
+    float *dl = xsl + QH_MAX_LR;                            // [k]
+    float *invl = dl + QH_MAX_LR;                           // [S]
     float *mixv = invl + QH_PRE_MAXS;                       // [ow][S]
     QH_TS(1);
     // one wave polls the down workgroups' done words (its XCD's copy: the
     // polling stays off the words the down workgroups write), then the
-    // workgroup reads d and 1/rms, every tag checked (the done words were
-    // stored after them, acknowledged, so a re-read is not expected)
+    // workgroup reads d's partials and the 1/rms, every tag checked (the
+    // done words were stored after them, so a stale word is rare: the
+    // workgroup then reads them all again)
     __shared__ int fail;
     if (t == 0) fail = 0;
     __syncthreads();
@@ -797,16 +870,39 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
     if (!fail) {
         for (int spins = 0;; spins++) {
             bool stale = false;
-            for (int r = t; r < k + S; r += QH_THREADS) {
-                const unsigned long long q = qh_ld(r < k ? a.tw + QH_TD + r : a.tw + (r - k));
-                stale |= (uint32_t)q != a.epoch;
-                const float f = __uint_as_float((uint32_t)(q >> 32));
+            // every word this thread reads requested at once: rows t + 256 j
+            // (j < QH_UPJ), their S partials each, and the 1/rms words
+            constexpr int QH_UPJ = (QH_MAX_LR + QH_THREADS - 1) / QH_THREADS;
+            unsigned long long q[QH_UPJ][QH_PRE_MAXS], qi = 0;
+#pragma unroll
+            for (int j = 0; j < QH_UPJ; j++) {
+                const int r = t + QH_THREADS * j;
+#pragma unroll
+                for (int sp = 0; sp < QH_PRE_MAXS; sp++)
+                    q[j][sp] = r < k && sp < S ? qh_ld(a.tw + QH_TD + sp * k + r) : (unsigned long long)a.epoch;
+            }
+            if (t < S) qi = qh_ld(a.tw + t);
+#pragma unroll
+            for (int j = 0; j < QH_UPJ; j++) {
+                const int r = t + QH_THREADS * j;
                 if (r < k) {
-                    const float dv = f * a.scale;
+                    // the row's partials, added in stream order
+                    float dv = __uint_as_float((uint32_t)(q[j][0] >> 32));
+                    stale |= (uint32_t)q[j][0] != a.epoch;
+#pragma unroll
+                    for (int sp = 1; sp < QH_PRE_MAXS; sp++)
+                        if (sp < S) {
+                            stale |= (uint32_t)q[j][sp] != a.epoch;
+                            dv = dv + __uint_as_float((uint32_t)(q[j][sp] >> 32));
+                        }
+                    dl[r] = dv;
+                    dv = dv * a.scale;
                     xsl[r] = dv * qh_sigmoid(dv);
-                } else {
-                    invl[r - k] = f;
                 }
+            }
+            if (t < S) {
+                stale |= (uint32_t)qi != a.epoch;
+                invl[t] = __uint_as_float((uint32_t)(qi >> 32));
             }
             if (!__syncthreads_or(stale)) break;
             if (spins >= QH_SPIN_LIMIT) {
@@ -818,6 +914,8 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
     }
     __syncthreads();
     QH_TS(3);
+    if (u == 0)
+        for (int r = t; r < k; r += QH_THREADS) a.d[r] = dl[r];
     float acc = 0.0f;
 #pragma unroll
     for (int j = 0; j < QH_UP_NJ; j++) {
@@ -852,7 +950,7 @@ extern "C" int qwk_hc_decode(hipStream_t s, float *x, float *h4_out, float *n4, 
 {
     const int HH = S * H;
     if (H <= 0 || H % 4 || S < 1 || S > QH_PRE_MAXS || HH % 64 || HH / 64 > QH_THREADS || HH > 15360 ||
-        lowrank < 8 || lowrank > QH_MAX_LR || lowrank % 8 || (group != 32 && group != 64 && group != 128) ||
+        H % 32 || H > 32 * QH_DLPR * QH_NSJ || lowrank < 8 || lowrank > QH_MAX_LR || lowrank % 8 || (group != 32 && group != 64 && group != 128) ||
         HH % group || lowrank % group || h4_out == h4 || inj_out == inj || !err || !tags || epoch == 0u ||
         ((uintptr_t)h4 & 15u) || ((uintptr_t)h4_out & 15u) || ((uintptr_t)n4 & 15u) || ((uintptr_t)out & 15u) ||
         ((uintptr_t)wn & 7u) || ((uintptr_t)dn.w & 15u) || ((uintptr_t)bj & 15u) || ((uintptr_t)up.w & 3u))
@@ -861,24 +959,25 @@ extern "C" int qwk_hc_decode(hipStream_t s, float *x, float *h4_out, float *n4, 
     a.x = x; a.h4_out = h4_out; a.n4 = n4; a.d = d; a.inj_out = inj_out;
     a.h4 = h4; a.out = out; a.inj = inj; a.wn = wn; a.bj = bj; a.dn = dn; a.up = up;
     a.H = H; a.S = S; a.lowrank = lowrank; a.lgG = group == 32 ? 5 : group == 64 ? 6 : 7;
-    a.nd = (lowrank + QH_DR - 1) / QH_DR;
+    a.nd = S * ((lowrank + QH_DR - 1) / QH_DR);
     a.ow = 32 / S;
     a.eps = eps; a.scale = scale;
     a.err = err; a.tw = (uint2 *)tags; a.epoch = epoch;
     {
-        // a down workgroup's bytes (streams, out row, norm gains, its rows'
-        // words, scales and biases) at ~20 GB/s, a CU's L1 under load: 5 us
-        // at H 3072, S 4 (A/B: 2.5 us 12.8, 5 us 12.6-12.7, 7 us 13.7,
-        // none 13.0 us a step)
-        const double bytes = (double)HH * 4 + (double)H * 4 + (double)HH * 2 +
-                             (double)QH_DR * ((double)HH / 2 + 4.0 * (HH / group));
+        // a down workgroup's bytes (its stream, the out row, the stream's
+        // norm gains, its rows' words, scales and biases of the stream) at
+        // ~20 GB/s, a CU's L1 under load: 2.2 us at H 3072, S 4 (A/B, us a
+        // step: twice the wait 12.0, half 11.3-11.4, none 11.4-11.5, this
+        // 11.2-11.3)
+        const double bytes = (double)H * 4 + (double)H * 4 + (double)H * 2 +
+                             (double)QH_DR * ((double)H / 2 + 4.0 * (H / group));
         a.up_delay = (uint32_t)(bytes / QH_UP_RATE);
     }
     const int nu = (H + a.ow - 1) / a.ow;
     const int grid = a.nd + S + nu;
     // LDS: the normed streams, or the up role's inputs, 1/rms and mix terms
-    const size_t lds = (size_t)HH * 4 > (size_t)(QH_MAX_LR + QH_PRE_MAXS + 32) * 4
-                           ? (size_t)HH * 4 : (size_t)(QH_MAX_LR + QH_PRE_MAXS + 32) * 4;
+    const size_t lds = (size_t)HH * 4 > (size_t)(2 * QH_MAX_LR + QH_PRE_MAXS + 32) * 4
+                           ? (size_t)HH * 4 : (size_t)(2 * QH_MAX_LR + QH_PRE_MAXS + 32) * 4;
     const int ni = (H / 4 + QH_THREADS - 1) / QH_THREADS;
     switch (ni) {
     case 1: hipLaunchKernelGGL(k_hc_decode<1>, dim3(grid), dim3(QH_THREADS), lds, s, a); break;
