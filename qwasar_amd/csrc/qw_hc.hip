@@ -238,6 +238,12 @@ static dim3 qh_grid(int64_t n)
     return dim3((unsigned)(b < 16384 ? (b > 0 ? b : 1) : 16384));
 }
 
+// The LDS slot of float4 p of the normed streams when the injection logits
+// read them (SW16): within each run of 16 (a 64-input chunk) rotated by the
+// run's index, so the lanes reading the same float4 of consecutive chunks hit
+// different banks.
+__device__ __forceinline__ int qh_swz16(int p) { return (p & ~15) | ((p + (p >> 4)) & 15); }
+
 // Inject and grouped norm of one row into LDS (nl: S*H floats): the streams
 // with the block's output injected, then each normed with its gains -- per
 // stream the order of k_norm_grouped (a chain over this thread's float4s
@@ -247,7 +253,7 @@ static dim3 qh_grid(int64_t n)
 // issues come after them in the memory counter's order (the norm does not
 // wait for them).  Every thread of the workgroup calls it (it holds
 // barriers).
-template <int NI, typename F>
+template <int NI, bool SW16 = false, typename F>
 __device__ __forceinline__ void qh_inject_norm(float4 *nl, float (*part)[QH_THREADS / 64], int ws,
                                                float *__restrict__ h4_out, float *__restrict__ n4,
                                                const float *__restrict__ h4, const float *__restrict__ out,
@@ -298,7 +304,7 @@ __device__ __forceinline__ void qh_inject_norm(float4 *nl, float (*part)[QH_THRE
         v.y = v.y * inv[s] * __uint_as_float(wb.x & 0xFFFF0000u);
         v.z = v.z * inv[s] * __uint_as_float(wb.y << 16);
         v.w = v.w * inv[s] * __uint_as_float(wb.y & 0xFFFF0000u);
-        nl[s * n4q + i] = v;
+        nl[SW16 ? qh_swz16(s * n4q + i) : s * n4q + i] = v;
         if (ws == s) reinterpret_cast<float4 *>(n4 + (size_t)s * H)[i] = v;
     };
     if (NI > 0) {
@@ -318,7 +324,7 @@ __device__ __forceinline__ void qh_inject_norm(float4 *nl, float (*part)[QH_THRE
                 if (s < S) {
                     float4 v = reinterpret_cast<const float4 *>(h4 + (size_t)s * H)[i];
                     inject(s, i, v, o);
-                    nl[s * n4q + i] = v;
+                    nl[SW16 ? qh_swz16(s * n4q + i) : s * n4q + i] = v;
                 }
         }
     }
@@ -349,15 +355,21 @@ __device__ __forceinline__ void qh_inject_norm(float4 *nl, float (*part)[QH_THRE
         for (int i = t; i < n4q; i += QH_THREADS) {
 #pragma unroll
             for (int s = 0; s < QH_PRE_MAXS; s++)
-                if (s < S) scale(s, i, nl[s * n4q + i], reinterpret_cast<const uint2 *>(wn + (size_t)s * H)[i]);
+                if (s < S) scale(s, i, nl[SW16 ? qh_swz16(s * n4q + i) : s * n4q + i], reinterpret_cast<const uint2 *>(wn + (size_t)s * H)[i]);
         }
     }
     __syncthreads();
 }
 
+// The LDS slot of float4 i of a stream normed by qh_norm1: within each run of 8
+// (a 32-input segment) rotated by the run's index, so 8 lanes reading the same
+// float4 of 8 consecutive segments hit different banks.
+__device__ __forceinline__ int qh_swz(int i) { return (i & ~7) | ((i + (i >> 3)) & 7); }
+
 // Stream s alone of qh_inject_norm: the same arithmetic for that stream (its
 // injected values, sum of squares, 1/rms and normed values bit for bit),
-// normed into nl[0, H / 4), nothing written to memory; returns the 1/rms.
+// normed into nl (float4 i at qh_swz(i), i < H / 4), nothing written to
+// memory; returns the 1/rms.
 // after_loads() runs once the stream's loads are issued.  Every thread of
 // the workgroup calls it (it holds barriers).
 template <int NI, typename F>
@@ -403,7 +415,7 @@ __device__ __forceinline__ float qh_norm1(float4 *nl, float (*part)[QH_THREADS /
         for (int i = t; i < n4q; i += QH_THREADS) {
             float4 v = hrow[i];
             inject(v, orow[i]);
-            nl[i] = v;
+            nl[qh_swz(i)] = v;
         }
     }
     {
@@ -420,7 +432,7 @@ __device__ __forceinline__ float qh_norm1(float4 *nl, float (*part)[QH_THREADS /
         v.y = v.y * inv * __uint_as_float(wb.x & 0xFFFF0000u);
         v.z = v.z * inv * __uint_as_float(wb.y << 16);
         v.w = v.w * inv * __uint_as_float(wb.y & 0xFFFF0000u);
-        nl[i] = v;
+        nl[qh_swz(i)] = v;
     };
     if (NI > 0) {
 #pragma unroll
@@ -429,7 +441,7 @@ __device__ __forceinline__ float qh_norm1(float4 *nl, float (*part)[QH_THREADS /
             if (i < n4q) scale(i, hv[j], gw[j]);
         }
     } else {
-        for (int i = t; i < n4q; i += QH_THREADS) scale(i, nl[i], wrow[i]);
+        for (int i = t; i < n4q; i += QH_THREADS) scale(i, nl[qh_swz(i)], wrow[i]);
     }
     __syncthreads();
     return inv;
@@ -438,19 +450,26 @@ __device__ __forceinline__ float qh_norm1(float4 *nl, float (*part)[QH_THREADS /
 // Injection logit s (order R: a thread per 64-input chunk, each chunk an
 // fmaf chain from 0, the chunk sums left to right) of the normed row in LDS.
 // Every thread of the workgroup calls it (it holds a barrier).
-__device__ __forceinline__ void qh_inj_logit(const float4 *nl, float *pc, const uint16_t *__restrict__ bj, int s,
-                                             int HH, float *__restrict__ inj_out)
+// qh_inj_load requests thread t's chunk of weights (row s) into ww; then
+// qh_inj_logit(nl, pc, ww, ...) takes them.
+__device__ __forceinline__ void qh_inj_load(const uint16_t *__restrict__ bj, int s, int HH, uint4 (&ww)[8])
+{
+    const int t = threadIdx.x;
+    if (t < HH / 64) {
+        const uint4 *wr = reinterpret_cast<const uint4 *>(bj + (size_t)s * HH + 64 * t);
+#pragma unroll
+        for (int q = 0; q < 8; q++) ww[q] = wr[q];
+    }
+}
+template <bool SW16 = false>
+__device__ __forceinline__ void qh_inj_logit(const float4 *nl, float *pc, const uint4 (&ww)[8], int s, int HH,
+                                             float *__restrict__ inj_out)
 {
     const int t = threadIdx.x, nch = HH / 64;
     if (t < nch) {
-        // the chunk's 64 weights and inputs all requested before the chain
-        const uint4 *wr = reinterpret_cast<const uint4 *>(bj + (size_t)s * HH + 64 * t);
-        uint4 ww[8];
         float4 xa[16];
 #pragma unroll
-        for (int q = 0; q < 8; q++) ww[q] = wr[q];
-#pragma unroll
-        for (int q = 0; q < 16; q++) xa[q] = nl[16 * t + q];
+        for (int q = 0; q < 16; q++) xa[q] = nl[SW16 ? qh_swz16(16 * t + q) : 16 * t + q];
         float p = 0.0f;
 #pragma unroll
         for (int q = 0; q < 8; q++) {
@@ -471,6 +490,14 @@ __device__ __forceinline__ void qh_inj_logit(const float4 *nl, float *pc, const 
         for (int e = 1; e < nch; e++) tot = tot + pc[e];
         inj_out[s] = tot;
     }
+}
+__device__ __forceinline__ void qh_inj_logit(const float4 *nl, float *pc, const uint16_t *__restrict__ bj, int s,
+                                             int HH, float *__restrict__ inj_out)
+{
+    // the chunk's 64 weights and inputs all requested before the chain
+    uint4 ww[8];
+    qh_inj_load(bj, s, HH, ww);
+    qh_inj_logit(nl, pc, ww, s, HH, inj_out);
 }
 
 // The mixer's first half at decode (one row) in one launch: inject + grouped
@@ -784,7 +811,7 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
                 float xs[32];
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
-                    const float4 v = nl[seg * 8 + e];
+                    const float4 v = nl[qh_swz(seg * 8 + e)];
                     xs[4 * e] = v.x; xs[4 * e + 1] = v.y; xs[4 * e + 2] = v.z; xs[4 * e + 3] = v.w;
                 }
                 float xsum = 0.0f;
@@ -812,9 +839,13 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
     if (b < a.nd + S) {
         const int s = b - a.nd;
         float inv[QH_PRE_MAXS];
-        qh_inject_norm<NI>(nl, part, s, a.h4_out, a.n4, a.h4, a.out, a.inj, a.wn, H, S, a.eps, inv, [] {});
+        // the injection row requested behind the streams: its latency runs
+        // under the norm
+        uint4 ww[8];
+        qh_inject_norm<NI, true>(nl, part, s, a.h4_out, a.n4, a.h4, a.out, a.inj, a.wn, H, S, a.eps, inv,
+                                 [&] { qh_inj_load(a.bj, s, HH, ww); });
         QH_TS(1);
-        qh_inj_logit(nl, pc, a.bj, s, HH, a.inj_out);
+        qh_inj_logit<true>(nl, pc, ww, s, HH, a.inj_out);
         QH_TS(2);
         return;
     }
