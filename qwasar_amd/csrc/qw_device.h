@@ -336,10 +336,16 @@ __device__ __forceinline__ uint32_t qw_ldu16(const void *base, uint32_t off)
 // expert lane + 64 j (0 past E), the softmax p = v / sum, and the top K by
 // p, descending, ties to the lower expert.  The sum adds a lane's v[j] in j
 // order from 0, then the lane partials by the 64-lane xor tree.
+#ifndef QW_ROUTE_PRIO
+#define QW_ROUTE_PRIO 3
+#endif
 template <int PL>
 __device__ __forceinline__ void qw_route_finish(float (&v)[PL], int E, int K, int norm, int lane,
                                                int *pick_i, float *pick_w, uint32_t *sx)
 {
+    // One wave's chain of dependent steps, on a SIMD it shares with the
+    // other waves of its CU's workgroups: issued ahead of them while it runs
+    if (QW_ROUTE_PRIO > 0) __builtin_amdgcn_s_setprio(QW_ROUTE_PRIO);
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < PL; j++) s = s + v[j];
@@ -434,6 +440,7 @@ __device__ __forceinline__ void qw_route_finish(float (&v)[PL], int E, int K, in
             *pick_i = lane < K ? 0xFFFF - (int)(uint32_t)pk : 0;
             *pick_w = norm ? mw / wsum : mw;
             QW_RSTAMP(8);
+            if (QW_ROUTE_PRIO > 0) __builtin_amdgcn_s_setprio(0);
             return;
         }
     }
@@ -497,6 +504,7 @@ __device__ __forceinline__ void qw_route_finish(float (&v)[PL], int E, int K, in
     }
     *pick_i = mine_i;
     *pick_w = norm ? mine_w / wsum : mine_w;
+    if (QW_ROUTE_PRIO > 0) __builtin_amdgcn_s_setprio(0);
 }
 
 // COH: the logits were written by other workgroups of the same launch and are
