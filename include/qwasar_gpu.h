@@ -398,15 +398,15 @@ bool qw_op_moe_layer_residual_next(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, q
  * counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  The launch's staging and hand-off state live in a
- * static device array of 320 KiB per GPU (held until the process ends), whose
+ * static device array of 512 KiB per GPU (held until the process ends), whose
  * address the library resolves at qw_gpu_init; this call makes no
  * allocation of any kind and gives qw_op_moe_layer's bits (the one-launch
  * path for one token, the batch path for 2..8).  False, nothing encoded,
  * where qw_op_moe_layer would not take a decode path (past 8 rows, or shapes
  * the decode kernels do not take), or where the layer's staging at `rows`
- * exceeds what the array holds past its 76 KB hand-off state (249,600
- * bytes: config 1's shape at 8 rows stages 227,328; H 4096 with K 15 at 8
- * rows, 313,344, is refused, at 5 rows, 196,608, taken).
+ * exceeds what the array holds past its 76 KB hand-off state (446,208
+ * bytes: config 1's shape at 8 rows stages 385,280; H 4096 with K 15 at 8
+ * rows, 545,024, is refused, at 5 rows, 342,272, taken).
  * Every call on one GPU shares the array and finds it as the last call
  * left it (the hand-off state stays valid between calls; the staging needs
  * no clearing).  Calls whose launches overlap on one GPU -- the library's

@@ -1189,18 +1189,49 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
 #define QB_TAB_INTS (1 + 4 * QD_MAXU + QD_MAXT)
 
 struct QbLayout {
-    size_t logits, tab, qx, qact, qsh, total;
+    size_t logits, tab, qx, qact, qsh, xh, xF, perm, tiles, act, total;
 };
+
+// The batch's gate / up runs on the matrix cores (qwk_gmm16, the shared
+// expert as one more expert of the grouped product) when the shared expert's
+// width is the routed experts' and the product takes the shapes and banks;
+// else as q16 dots (k_batch_gu).
+static qwk_q4 qb_up_bank(const qwk_moe *M)
+{
+    if (M->split) return M->up;
+    const qwk_q4 g = M->gate_up;
+    return qwk_q4{g.w + (size_t)M->I * (M->H / 8), g.s + (size_t)M->I * (M->H / M->group),
+                  g.b + (size_t)M->I * (M->H / M->group)};
+}
+static bool qb_gmm(const qwk_moe *M)
+{
+#ifdef QB_NO_GMM
+    return false;
+#else
+    return M->SI == M->I && qwk_gmm16_supported(M->H, M->group, (M->split ? M->gate : M->gate_up).w, qb_up_bank(M).w) &&
+           qwk_gmm16_supported(M->H, M->group, M->sh_gate.w, M->sh_up.w);
+#endif
+}
 
 static QbLayout qb_layout(const qwk_moe *M, int rows)
 {
     QbLayout L;
     size_t o = 0;
+    const bool gmm = qb_gmm(M);
     L.logits = o; o += al((size_t)rows * M->E * 4);
-    L.qx = o;     o += al((size_t)rows * (M->H / 16) * QW_Q16_BYTES);
+    L.qx = o;     o += gmm ? 0 : al((size_t)rows * (M->H / 16) * QW_Q16_BYTES);
     L.tab = o;    o += al((size_t)QB_TAB_INTS * 4);
     L.qact = o;   o += al((size_t)rows * M->K * (M->I / 16) * QW_Q16_BYTES);
     L.qsh = o;    o += al((size_t)rows * (M->SI / 16) * QW_Q16_BYTES);
+    // the matrix-core gate / up: the token rows staged as f16, the pairs by
+    // expert (then the shared expert's rows), a tile per unique expert and
+    // one for the shared expert, the activations in fp32
+    const size_t npk = (size_t)rows * M->K;
+    L.xh = o;     o += gmm ? al((size_t)rows * M->H * 2) : 0;
+    L.xF = o;     o += gmm ? al((size_t)rows * 4) : 0;
+    L.perm = o;   o += gmm ? al((npk + rows) * 4) : 0;
+    L.tiles = o;  o += gmm ? al((1 + 3 * ((size_t)QD_MAXU + 1)) * 4) : 0;
+    L.act = o;    o += gmm ? al((npk + rows) * M->I * 4) : 0;
     L.total = o;
     return L;
 }
@@ -1210,6 +1241,9 @@ struct QbArgs {
     const float *logits;
     int32_t *tab;
     int xstaged;              // the router launch staged the token rows into qx
+    int gmm;                  // gate / up on the matrix cores: emit perm and tiles
+    int32_t *perm, *tiles;
+    const float *act;         // their fp32 activations [pairs + rows][I]
 };
 
 template <int PL>
@@ -1308,7 +1342,48 @@ __global__ __launch_bounds__(QD_MAXT * 64) void k_batch_route(QbArgs b)
         b.tab[QB_TAB_USTART + u] = R.ustart[u];
     }
     for (int p = t; p < npk; p += nthr) b.tab[QB_TAB_UPAIR + p] = R.upair[p];
+    if (b.gmm) {
+        // the grouped product's tile list: unique expert u's pairs, then the
+        // shared expert (expert E) on the token rows, pairs npk + r
+        if (t == 0) {
+            b.tiles[0] = R.U + 1;
+            b.tiles[1 + 3 * R.U] = E;
+            b.tiles[2 + 3 * R.U] = npk;
+            b.tiles[3 + 3 * R.U] = a.rows;
+        }
+        for (int u = t; u < R.U; u += nthr) {
+            b.tiles[1 + 3 * u] = R.uexp[u];
+            b.tiles[2 + 3 * u] = R.ustart[u];
+            b.tiles[3 + 3 * u] = R.ucnt[u];
+        }
+        for (int p = t; p < npk; p += nthr) b.perm[p] = R.upair[p];
+        for (int r = t; r < a.rows; r += nthr) b.perm[npk + r] = npk + r;
+    }
     (void)nwd;
+}
+
+// The matrix-core gate / up's fp32 activations as the q16 vectors the down
+// launch reads: pair p's into qact, the shared expert's (rows npk + t) into
+// qsh.  A thread per (vector, 16-unit).
+__global__ __launch_bounds__(256) void k_batch_act_q16(QbArgs b)
+{
+    const QdArgs &a = b.d;
+    const int I = a.m.I, units = I / 16, npk = a.rows * a.m.K;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (npk + a.rows) * units) return;
+    const int v = i / units, u = i % units;
+    float f[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float4 x = reinterpret_cast<const float4 *>(b.act + (size_t)v * I + 16 * u)[q];
+        f[4 * q] = x.x; f[4 * q + 1] = x.y; f[4 * q + 2] = x.z; f[4 * q + 3] = x.w;
+    }
+    uint4 q3[3];
+    qw_q16_make(f, q3);
+    uint4 *d = v < npk ? a.qact + ((size_t)v * units + u) * 3 : a.qsh + ((size_t)(v - npk) * units + u) * 3;
+    d[0] = q3[0];
+    d[1] = q3[1];
+    d[2] = q3[2];
 }
 
 template <int LPR, int NUL>
@@ -1488,6 +1563,12 @@ extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, flo
     a.qsh = (uint4 *)(S + L.qsh);
     b.logits = (const float *)(S + L.logits);
     b.tab = (int32_t *)(S + L.tab);
+    const qwk_q4 g0 = M->split ? M->gate : M->gate_up, u0 = qb_up_bank(M);
+    const int npk = rows * M->K;
+    b.gmm = qb_gmm(M);
+    b.perm = (int32_t *)(S + L.perm);
+    b.tiles = (int32_t *)(S + L.tiles);
+    b.act = (const float *)(S + L.act);
     const size_t xs_bytes = (size_t)a.tch * vbytes;
     const size_t xa_bytes = ((size_t)(M->SI / 16) + (size_t)M->K * (M->I / 16)) * QW_Q16_BYTES;
     if (a.tch < 1 || xa_bytes > QD_LDS || a.umax > QD_MAXU) return (int)hipErrorInvalidValue;
@@ -1495,19 +1576,33 @@ extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, flo
     float *lg = (float *)(S + L.logits), *gl = (float *)(b.tab + QB_TAB_GATE);
     // (which also stages the token rows as q16 for the gate / up launch)
     b.xstaged = 1;
-    int rc = qwk_dmat_bf16_gate(s, lg, gl, x, M->router, M->sh_gate_w, M->H, M->E, rows, a.qx);
+    int rc = qwk_dmat_bf16_gate(s, lg, gl, x, M->router, M->sh_gate_w, M->H, M->E, rows, b.gmm ? nullptr : a.qx);
     if (rc == (int)hipErrorInvalidValue) {   // a layout the one launch does not take: two order-R launches
-        b.xstaged = 0;
+        b.xstaged = b.gmm;
         rc = qwk_dmat_bf16(s, lg, x, M->router, M->H, M->E, rows);
         if (!rc) rc = qwk_dmat_bf16(s, gl, x, M->sh_gate_w, M->H, 1, rows);
     }
+    if (!rc && b.gmm) rc = qwk_stage16(s, (uint16_t *)(S + L.xh), (float *)(S + L.xF), x, rows, M->H);
     if (rc) return rc;
     const int nrb8 = (a.n_down_rb + 7) / 8 * 8;
+    const qwk_gmm_extra xgu = {M->sh_gate, M->sh_up, M->E, npk};
+    const int nvu = (npk + rows) * (M->I / 16);
 #define QB_GO(L_, N_, D_, P_)                                                                                   \
     if (lpr_h == L_ && nul_h == N_ && nul_d == D_ && pl == P_) {                                              \
         hipLaunchKernelGGL(k_batch_route<P_>, dim3(1), dim3(QD_MAXT * 64), 0, s, b);                          \
-        hipLaunchKernelGGL((k_batch_gu<L_, N_>), dim3(a.n_ex + a.n_sh), dim3(QD_THREADS), xs_bytes, s, b);    \
+        if (b.gmm) {                                                                                          \
+            const int rg = qwk_gmm16(s, (float *)b.act, M->I, (const uint16_t *)(S + L.xh),                   \
+                                     (const float *)(S + L.xF), b.perm, b.tiles, a.umax + 1, g0, u0,           \
+                                     (long)(M->split ? 1 : 2) * M->I * (M->H / 8),                             \
+                                     (long)(M->split ? 1 : 2) * M->I * (M->H / G), M->H, M->I, M->K, 0, G, 1, \
+                                     0, &xgu);                                                                 \
+            if (rg) return rg;                                                                                \
+            hipLaunchKernelGGL(k_batch_act_q16, dim3((nvu + 255) / 256), dim3(256), 0, s, b);                 \
+        } else {                                                                                              \
+            hipLaunchKernelGGL((k_batch_gu<L_, N_>), dim3(a.n_ex + a.n_sh), dim3(QD_THREADS), xs_bytes, s, b);\
+        }                                                                                                     \
         hipLaunchKernelGGL(k_batch_down<D_>, dim3(rows * nrb8), dim3(QD_THREADS), xa_bytes, s, b);            \
+        return (int)hipGetLastError();                                                                        \
     } else
     QD_SHAPES(QB_GO)
 #undef QB_GO

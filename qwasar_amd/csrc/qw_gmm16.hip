@@ -527,6 +527,20 @@ static int g16_cus_per_xcd()
     return cpx;
 }
 
+// Whether qwk_gmm16 takes this inner size, group and these weight banks
+// (as its own checks; the scale / bias block must exist).
+extern "C" int qwk_gmm16_supported(int k, int group, const void *w0, const void *w1)
+{
+    const int kc = k % 256 == 0 ? 256 : 64;
+    if (k < 64 || k % kc || (group != 32 && group != 64 && group != 128) || k % group ||
+        ((uintptr_t)w0 & 15u) || ((uintptr_t)w1 & 15u))
+        return 0;
+    const int groups = k / group;
+    for (int g = 16; g >= 1; g /= 2)
+        if (groups % g == 0 && (g * group) % kc == 0) return 1;
+    return 0;
+}
+
 extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb, const float *aF,
                          const int32_t *perm, const int32_t *tiles, int max_tiles,
                          qwk_q4 m0, qwk_q4 m1, long ew, long eg, int k, int n, int K, int x_by_pair,

@@ -87,6 +87,7 @@ int qwk_stage16(hipStream_t s, uint16_t *h, float *F, const float *x, int rows, 
  * m0 (and with swiglu m1, the up rows) point at expert 0 of the bank; ew/eg
  * are the per-expert strides in words / groups.  With swiglu, n = features
  * and y = silu(W0 A) * (W1 A).  k % 64 == 0 and k % group == 0. */
+int qwk_gmm16_supported(int k, int group, const void *w0, const void *w1);
 int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ah, const float *aF,
               const int32_t *perm, const int32_t *tiles, int max_tiles, qwk_q4 m0, qwk_q4 m1, long ew,
               long eg, int k, int n, int K, int x_by_pair, int group, int swiglu, int dense_rows,
@@ -135,7 +136,7 @@ int qwk_decode_sync_words(void *sync, uint32_t **err, void **words, size_t *nwor
 /* The allocation-free decode entry's device scratch (qw_static.hip): a
  * file-scope device array of this many bytes per GPU, holding the hand-off
  * state and then the staging area. */
-#define QWK_STATIC_SCRATCH_BYTES (320u * 1024u)
+#define QWK_STATIC_SCRATCH_BYTES (512u * 1024u)
 /* Resolves the array's address on the current device (hipGetSymbolAddress)
  * and zeroes it; once per device, at init.  Synchronous. */
 int qwk_static_init(hipStream_t s);

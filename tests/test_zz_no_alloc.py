@@ -42,18 +42,19 @@ def test_noalloc_matches_moe_layer(gpu, cfg, rows):
 def test_noalloc_refuses_oversized_staging(gpu):
     """Staging past the static array is refused with nothing encoded (no
     command is needed to ask); a fitting shape is accepted.  Several tokens
-    take the batch path, whose staging (logits, the q16 token rows, the
-    unique-expert table, the activations) must fit the 249,600 bytes past the
+    take the batch path, whose staging (logits, the unique-expert table, the
+    f16 token rows, the pairs and tiles of the grouped gate / up, its fp32
+    activations and their q16 vectors) must fit the 446,208 bytes past the
     hand-off state."""
     r = gpu.NULL_REF
     q = gpu.qw_q4_ref(r, r, r, 64)
-    # H 4096, K 15, I 512: 313,344 bytes at 8 rows do not fit, 196,608 at 5 do
+    # H 4096, K 15, I 512: 545,024 bytes at 8 rows do not fit, 342,272 at 5 do
     big = gpu.qw_moe_layer(4096, 512, 15, 512, 512, True, True, r, q, q, q, q, q, q, q, r)
     assert gpu.qw_op_moe_layer(None, r, r, r, r, big, 8)
     assert not gpu.qw_op_moe_layer_noalloc(None, r, r, r, r, big, 8)
     assert gpu.qw_op_moe_layer_noalloc(None, r, r, r, r, big, 5)
     assert gpu.qw_op_moe_layer_noalloc(None, r, r, r, r, big, 1)
-    # config 1's shape: 227,328 bytes at 8 rows
+    # config 1's shape: 385,280 bytes at 8 rows
     small = gpu.qw_moe_layer(3072, 512, 10, 512, 512, True, True, r, q, q, q, q, q, q, q, r)
     assert gpu.qw_op_moe_layer_noalloc(None, r, r, r, r, small, 8)
     assert not gpu.qw_op_moe_layer_noalloc(None, r, r, r, r, small, 9)   # past the decode path
