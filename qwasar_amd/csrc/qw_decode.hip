@@ -1576,13 +1576,16 @@ extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, flo
     float *lg = (float *)(S + L.logits), *gl = (float *)(b.tab + QB_TAB_GATE);
     // (which also stages the token rows as q16 for the gate / up launch)
     b.xstaged = 1;
-    int rc = qwk_dmat_bf16_gate(s, lg, gl, x, M->router, M->sh_gate_w, M->H, M->E, rows, b.gmm ? nullptr : a.qx);
+    // (or, for the matrix-core gate / up, as f16 rows with a scale each)
+    int rc = qwk_dmat_bf16_gate(s, lg, gl, x, M->router, M->sh_gate_w, M->H, M->E, rows, b.gmm ? nullptr : a.qx,
+                                b.gmm ? (uint16_t *)(S + L.xh) : nullptr, b.gmm ? (float *)(S + L.xF) : nullptr);
+    bool staged16 = rc == 0;
     if (rc == (int)hipErrorInvalidValue) {   // a layout the one launch does not take: two order-R launches
         b.xstaged = b.gmm;
         rc = qwk_dmat_bf16(s, lg, x, M->router, M->H, M->E, rows);
         if (!rc) rc = qwk_dmat_bf16(s, gl, x, M->sh_gate_w, M->H, 1, rows);
     }
-    if (!rc && b.gmm) rc = qwk_stage16(s, (uint16_t *)(S + L.xh), (float *)(S + L.xF), x, rows, M->H);
+    if (!rc && b.gmm && !staged16) rc = qwk_stage16(s, (uint16_t *)(S + L.xh), (float *)(S + L.xF), x, rows, M->H);
     if (rc) return rc;
     const int nrb8 = (a.n_down_rb + 7) / 8 * 8;
     const qwk_gmm_extra xgu = {M->sh_gate, M->sh_up, M->E, npk};

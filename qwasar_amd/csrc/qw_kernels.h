@@ -27,10 +27,12 @@ int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint16_t *w,
 
 /* The same for up to 8 token rows (k % 64 == 0, k <= 4096, 16-byte aligned),
  * with, when w2 is given, one more output: g[r] = order-R dot of w2 [k] with
- * x row r, in the same launch; and when qx is given, x staged there as q16
- * units ([rows][k / 16][3] uint4, 16-byte aligned). */
+ * x row r, in the same launch; when qx is given, x staged there as q16
+ * units ([rows][k / 16][3] uint4, 16-byte aligned); when hx is given, x
+ * staged there as qwk_stage16 stages it (hx [rows, k] f16, 16-byte aligned,
+ * hF [rows]). */
 int qwk_dmat_bf16_gate(hipStream_t s, float *y, float *g, const float *x, const uint16_t *w,
-                       const uint16_t *w2, int k, int n, int rows, void *qx);
+                       const uint16_t *w2, int k, int n, int rows, void *qx, uint16_t *hx, float *hF);
 
 /* Softmax, top-K, renormalise: idx/w [rows, K]. */
 int qwk_route(hipStream_t s, int32_t *idx, float *w, const float *logits,

@@ -411,10 +411,12 @@ __global__ __launch_bounds__(QW_DF_WAVES * 64) void k_dmat_few(float *__restrict
                                                                const float *__restrict__ x,
                                                                const uint16_t *__restrict__ w,
                                                                const uint16_t *__restrict__ w2, int k, int n,
-                                                               int rows, uint4 *__restrict__ qx)
+                                                               int rows, uint4 *__restrict__ qx,
+                                                               uint16_t *__restrict__ hx, float *__restrict__ hF)
 {
     extern __shared__ float xl[];                    // [rows of this group][nch][QW_DF_PAD]
     __shared__ float part[QW_DF_WAVES][QW_DF_MAXR][64];
+    __shared__ float smax[QW_DF_MAXR][QW_DF_WAVES];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nch = k / 64, o = blockIdx.x * QW_DF_WAVES + wave;
     // blockIdx.y: a group of QW_DF_TPG token rows (a workgroup stages only
@@ -467,6 +469,38 @@ __global__ __launch_bounds__(QW_DF_WAVES * 64) void k_dmat_few(float *__restrict
             d[2] = q[2];
         }
     }
+    if (hx && blockIdx.x == 0) {
+        // the group's rows also leave staged as f16 with one power of two a
+        // row, as k_stage16 stages them (the same bits): each row's largest
+        // magnitude, then h = f16(x 2^sh) in 8-blocks ordered 0,4,1,5,2,6,3,7
+        for (int r = 0; r < rows; r++) {
+            float m = 0.0f;
+            for (int c = threadIdx.x; c < k; c += QW_DF_WAVES * 64)
+                m = fmaxf(m, fabsf(xl[((size_t)r * nch + c / 64) * QW_DF_PAD + c % 64]));
+            m = qw_wave_max(m);
+            if (lane == 0) smax[r][wave] = m;
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < rows * (k / 8); i += QW_DF_WAVES * 64) {
+            const int r = i / (k / 8), b8 = i % (k / 8);
+            float m = smax[r][0];
+#pragma unroll
+            for (int v = 1; v < QW_DF_WAVES; v++) m = fmaxf(m, smax[r][v]);
+            int sh = 0;
+            if (m > 0.0f && m <= 3.40282346638528859812e+38f) {
+                sh = 15 - __builtin_amdgcn_frexp_expf(m);
+                sh = sh < -126 ? -126 : sh > 126 ? 126 : sh;
+            }
+            if (b8 == 0) hF[r0 + r] = __builtin_ldexpf(1.0f, -sh);
+            const float *src = xl + ((size_t)r * nch + (8 * b8) / 64) * QW_DF_PAD + (8 * b8) % 64;
+            _Float16 q[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) q[j] = (_Float16)__builtin_ldexpf(src[j], sh);
+            typedef _Float16 df_h8 __attribute__((ext_vector_type(8)));
+            reinterpret_cast<df_h8 *>(hx + (size_t)(r0 + r) * k)[b8] =
+                df_h8{q[0], q[4], q[1], q[5], q[2], q[6], q[3], q[7]};
+        }
+    }
     if (!has) return;
     if (lane < nch) {
 #pragma unroll
@@ -507,7 +541,7 @@ static bool qw_few_ok(const float *x, const uint16_t *w, int k, int rows)
 }
 
 static int qw_launch_few(hipStream_t s, float *y, float *g, const float *x, const uint16_t *w, const uint16_t *w2,
-                         int k, int n, int rows, uint4 *qx = nullptr)
+                         int k, int n, int rows, uint4 *qx = nullptr, uint16_t *hx = nullptr, float *hF = nullptr)
 {
     const size_t lds = (size_t)min(rows, QW_DF_TPG) * (k / 64) * QW_DF_PAD * sizeof(float);
     static bool attr = false;
@@ -520,16 +554,17 @@ static int qw_launch_few(hipStream_t s, float *y, float *g, const float *x, cons
     }
     const int outs = n + (w2 ? 1 : 0);
     hipLaunchKernelGGL(k_dmat_few, dim3((outs + QW_DF_WAVES - 1) / QW_DF_WAVES, (rows + QW_DF_TPG - 1) / QW_DF_TPG),
-                       dim3(QW_DF_WAVES * 64), lds, s, y, g, x, w, w2, k, n, rows, qx);
+                       dim3(QW_DF_WAVES * 64), lds, s, y, g, x, w, w2, k, n, rows, qx, hx, hF);
     return (int)hipGetLastError();
 }
 
 extern "C" int qwk_dmat_bf16_gate(hipStream_t s, float *y, float *g, const float *x, const uint16_t *w,
-                                  const uint16_t *w2, int k, int n, int rows, void *qx)
+                                  const uint16_t *w2, int k, int n, int rows, void *qx, uint16_t *hx, float *hF)
 {
-    if (n < 1 || !qw_few_ok(x, w, k, rows) || (w2 && ((uintptr_t)w2 % 16) != 0) || ((uintptr_t)qx % 16) != 0)
+    if (n < 1 || !qw_few_ok(x, w, k, rows) || (w2 && ((uintptr_t)w2 % 16) != 0) || ((uintptr_t)qx % 16) != 0 ||
+        ((uintptr_t)hx % 16) != 0 || (hx && (!hF || k % 8)))
         return (int)hipErrorInvalidValue;
-    return qw_launch_few(s, y, g, x, w, w2, k, n, rows, static_cast<uint4 *>(qx));
+    return qw_launch_few(s, y, g, x, w, w2, k, n, rows, static_cast<uint4 *>(qx), hx, hF);
 }
 
 extern "C" int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint16_t *w,
