@@ -31,6 +31,11 @@ int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint16_t *w,
  * units ([rows][k / 16][3] uint4, 16-byte aligned); when hx is given, x
  * staged there as qwk_stage16 stages it (hx [rows, k] f16, 16-byte aligned,
  * hF [rows]). */
+/* y[rows, n] as qwk_dmat_bf16 (order R, n <= 8, k % 64 == 0, k <= 4096,
+ * 16-byte aligned) and, in the same launch, x staged into hx / hF exactly as
+ * qwk_stage16 stages it. */
+int qwk_dmat_rows_stage16(hipStream_t s, float *y, uint16_t *hx, float *hF, const float *x,
+                          const uint16_t *w, int k, int n, int rows);
 int qwk_dmat_bf16_gate(hipStream_t s, float *y, float *g, const float *x, const uint16_t *w,
                        const uint16_t *w2, int k, int n, int rows, void *qx, uint16_t *hx, float *hF);
 

@@ -304,9 +304,15 @@ __global__ __launch_bounds__(256) void k_dmat_mfma(float *__restrict__ y, const 
 // partials meet in LDS and lane o adds output o's left to right.  k % 64 == 0.
 #define QW_DROWS_WAVES 4
 #define QW_DROWS_MAXN 8                    // outputs a row (n < 8 takes this path)
+// STAGE (k <= 64 * 64): the row also leaves staged as f16, as k_stage16
+// stages it (the same bits): from the chunk each lane holds, the row's
+// largest magnitude by a wave maximum, then h = f16(x 2^sh) in 8-blocks
+// ordered 0,4,1,5,2,6,3,7, and F = 2^-sh.
+template <bool STAGE>
 __global__ __launch_bounds__(QW_DROWS_WAVES * 64) void k_dmat_rows(float *__restrict__ y, const float *__restrict__ x,
                                                                   const uint16_t *__restrict__ w, int k, int n,
-                                                                  int rows)
+                                                                  int rows, uint16_t *__restrict__ hx,
+                                                                  float *__restrict__ hF)
 {
     __shared__ float part[QW_DROWS_WAVES][QW_DROWS_MAXN][QW_DMAT_MAXCH];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -314,10 +320,10 @@ __global__ __launch_bounds__(QW_DROWS_WAVES * 64) void k_dmat_rows(float *__rest
     if (r >= rows) return;
     const int nch = k / 64;
     const float *xr = x + (size_t)r * k;
+    float4 xa[16];        // with STAGE (nch <= 64): lane c's chunk, after the loop
     for (int c = lane; c < nch; c += 64) {
         // the row's chunk once, for every output
         const float4 *xv = reinterpret_cast<const float4 *>(xr + c * 64);
-        float4 xa[16];
 #pragma unroll
         for (int q = 0; q < 16; q++) xa[q] = xv[q];
         for (int o = 0; o < n; o++) {
@@ -337,6 +343,35 @@ __global__ __launch_bounds__(QW_DROWS_WAVES * 64) void k_dmat_rows(float *__rest
                 p = __builtin_fmaf(__uint_as_float(ww.w & 0xFFFF0000u), b.w, p);
             }
             part[wave][o][c] = p;
+        }
+    }
+    if (STAGE) {
+        const int c = lane;
+        float m = 0.0f;
+        if (c < nch) {
+#pragma unroll
+            for (int q = 0; q < 16; q++)
+                m = fmaxf(m, fmaxf(fmaxf(fabsf(xa[q].x), fabsf(xa[q].y)), fmaxf(fabsf(xa[q].z), fabsf(xa[q].w))));
+        }
+        m = qw_wave_max(m);
+        int sh = 0;
+        if (m > 0.0f && m <= 3.40282346638528859812e+38f) {
+            sh = 15 - __builtin_amdgcn_frexp_expf(m);
+            sh = sh < -126 ? -126 : sh > 126 ? 126 : sh;
+        }
+        if (c == 0) hF[r] = __builtin_ldexpf(1.0f, -sh);
+        if (c < nch) {
+            typedef _Float16 dr_h8 __attribute__((ext_vector_type(8)));
+            dr_h8 *hr = reinterpret_cast<dr_h8 *>(hx + (size_t)r * k + c * 64);
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                const float4 a = xa[2 * q], b = xa[2 * q + 1];
+                const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                _Float16 h[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) h[j] = (_Float16)__builtin_ldexpf(v[j], sh);
+                hr[q] = dr_h8{h[0], h[4], h[1], h[5], h[2], h[6], h[3], h[7]};
+            }
         }
     }
     // the wave's LDS accesses run in order: lane o reads what the wave wrote
@@ -567,6 +602,17 @@ extern "C" int qwk_dmat_bf16_gate(hipStream_t s, float *y, float *g, const float
     return qw_launch_few(s, y, g, x, w, w2, k, n, rows, static_cast<uint4 *>(qx), hx, hF);
 }
 
+extern "C" int qwk_dmat_rows_stage16(hipStream_t s, float *y, uint16_t *hx, float *hF, const float *x,
+                                     const uint16_t *w, int k, int n, int rows)
+{
+    if (k < 64 || k % 64 || k > 64 * 64 || n < 1 || n > QW_DROWS_MAXN || rows < 1 || !hx || !hF ||
+        ((uintptr_t)w % 16) || ((uintptr_t)x % 16) || ((uintptr_t)hx % 16))
+        return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_dmat_rows<true>, dim3((unsigned)((rows + QW_DROWS_WAVES - 1) / QW_DROWS_WAVES)),
+                       dim3(QW_DROWS_WAVES * 64), 0, s, y, x, w, k, n, rows, hx, hF);
+    return (int)hipGetLastError();
+}
+
 extern "C" int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint16_t *w,
                              int k, int n, int rows)
 {
@@ -577,8 +623,8 @@ extern "C" int qwk_dmat_bf16(hipStream_t s, float *y, const float *x, const uint
         return (int)hipGetLastError();
     }
     if (vec && k % 64 == 0 && n < 8 && rows >= 8) {
-        hipLaunchKernelGGL(k_dmat_rows, dim3((unsigned)((rows + QW_DROWS_WAVES - 1) / QW_DROWS_WAVES)),
-                           dim3(QW_DROWS_WAVES * 64), 0, s, y, x, w, k, n, rows);
+        hipLaunchKernelGGL(k_dmat_rows<false>, dim3((unsigned)((rows + QW_DROWS_WAVES - 1) / QW_DROWS_WAVES)),
+                           dim3(QW_DROWS_WAVES * 64), 0, s, y, x, w, k, n, rows, nullptr, nullptr);
         return (int)hipGetLastError();
     }
     if (vec && n >= 8 && qw_few_ok(x, w, k, rows)) return qw_launch_few(s, y, nullptr, x, w, nullptr, k, n, rows);

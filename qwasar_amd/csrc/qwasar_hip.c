@@ -893,7 +893,11 @@ static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const floa
     const long words = H / 8, groups = H / grp;
     const qwk_gmm_extra xgu = { q4r(&M->sh_gate), q4r(&M->sh_up), E, pairs };
     const qwk_gmm_extra xdn = { q4r(&M->sh_down), q4r(&M->sh_down), E, pairs };
-    int rc = qwk_stage16(s, xh, xF, x, rows, H);
+    /* the token rows staged as f16 by the shared gate's launch (one read of
+     * them for both), or by their own launch where it does not take them */
+    int rc = qwk_dmat_rows_stage16(s, g1, xh, xF, x, dp(M->sh_gate_w), H, 1, rows);
+    const bool gated = rc == 0;
+    if (!gated) rc = qwk_stage16(s, xh, xF, x, rows, H);
     if (!rc) rc = qwk_dmat_bf16(s, logits, x, dp(M->router), H, E, rows);
     if (!rc) rc = qwk_route(s, idx, w, logits, rows, E, K, M->norm ? 1 : 0);
     if (!rc) rc = qwk_moe_group(s, perm, tiles, idx, pairs, E, QW_PF_BM, mt, S + o_gw,
@@ -917,7 +921,7 @@ static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const floa
         if (!rc) rc = qwk_gmm16(s, sh, H, sh16, sF, NULL, NULL, 0, q4r(&M->sh_down), q4r(&M->sh_down),
                                 0, 0, SI, H, 1, 0, grp, 0, rows, NULL);
     }
-    if (!rc) rc = qwk_dmat_bf16(s, g1, x, dp(M->sh_gate_w), H, 1, rows);
+    if (!rc && !gated) rc = qwk_dmat_bf16(s, g1, x, dp(M->sh_gate_w), H, 1, rows);
     if (!rc) rc = qwk_moe_combine(s, out, ey, w, fuse ? ey + (size_t)pairs * H : sh, g1, rows, K, H);
     launched(c, "moe_layer (prefill)", rc);
     return rc == 0;
