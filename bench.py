@@ -163,7 +163,7 @@ def time_prefill(gpu, lb, x, reps):
     return ms, int(counts.max()), int((counts > 0).sum())
 
 
-def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444, read_ahead=False):
+def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444):
     """`nlayers` layers of config 1's shape (weights written
     on the device), joined by the residual bf16 RMS norm; one `rows`-token
     prefill, then `steps` decode steps, each fed a fresh N(0, 1) token."""
@@ -204,7 +204,7 @@ def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444, read_ahead=False):
     c = gpu.qw_cmd_begin()
     for s in range(warmup):
         fresh_h(c, 1, f"dec.warm{s}")
-        st.encode_fused(c, 1, read_ahead)
+        st.encode_fused(c, 1)
     gpu.run(c, "stack decode warm-up")
     gpu.qw_prof_reset()
     gpu.qw_prof_set_enabled(True)
@@ -212,7 +212,7 @@ def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444, read_ahead=False):
     gpu.qw_prof_set_enabled(False)
     for s in range(steps):
         fresh_h(c, 1, f"dec{s}")
-        st.encode_fused(c, 1, read_ahead)
+        st.encode_fused(c, 1)
     gpu.qw_prof_set_enabled(True)
     gpu.qw_cmd_mark(c, b"stack decode region")
     gpu.run(c, "stack decode")
@@ -233,10 +233,9 @@ def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444, read_ahead=False):
                         "ms_per_layer_max": round(float(per_layer.max()), 3),
                         "mfma_util": round(fl / (pf_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
             "decode": {"steps": steps, "us_per_token": round(us_tok, 2), "us_per_token_layer": round(us_tl, 3),
-                       "routed_hbm_frac": round(routed / (us_tl * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                       "next_router_read_ahead": read_ahead},
+                       "routed_hbm_frac": round(routed / (us_tl * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
             "includes": "per layer: the MoE block and the residual bf16 RMS norm (at decode folded into "
-                        "the layer's one launch, qw_op_moe_layer_residual_next); decode steps include writing "
+                        "the layer's one launch, qw_op_moe_layer_residual); decode steps include writing "
                         "the fresh token on the device and the closing residual step"}
 
 
@@ -628,9 +627,6 @@ def main():
     ap.add_argument("--no-config2", action="store_true", help="skip config 2 (batch-8 decode)")
     ap.add_argument("--no-config4", action="store_true", help="skip the 48-layer stack (config 4)")
     ap.add_argument("--config4-only", action="store_true", help="run only the 48-layer stack and print it")
-    ap.add_argument("--read-ahead", action="store_true",
-                    help="config 4 decode reading the next layer's router rows ahead (off: slower since the "
-                         "down loads wait for the experts' stream)")
     ap.add_argument("--no-hc", action="store_true", help="skip the hyper-connection mixer")
     ap.add_argument("--hc-only", action="store_true", help="run only the hyper-connection mixer and print it")
     ap.add_argument("--no-sparse", action="store_true", help="skip QSA and the gated DeltaNet")
@@ -666,7 +662,7 @@ def main():
         print(json.dumps({"sparse": bench_sparse(gpu)}), flush=True)
         return
     if args.config4_only:
-        print(json.dumps({"config4": bench_stack(gpu, 48, 2048, 256, 4, read_ahead=args.read_ahead)}),
+        print(json.dumps({"config4": bench_stack(gpu, 48, 2048, 256, 4)}),
               flush=True)
         return
     if args.decode_only_steps:
@@ -762,7 +758,7 @@ def main():
         out["prefill"] = pf
 
     if not args.no_config4:
-        out["config4"] = bench_stack(gpu, 48, 2048, 256, 4, read_ahead=args.read_ahead)
+        out["config4"] = bench_stack(gpu, 48, 2048, 256, 4)
     if not args.no_hc:
         out["hc_mixer"] = bench_hc(gpu, 200)
     if not args.no_sparse:

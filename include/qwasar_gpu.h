@@ -384,32 +384,26 @@ bool qw_op_moe_layer(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,
  * than h and y_prev.  False (nothing encoded) where qw_op_moe_layer refuses. */
 bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref h, qw_ref y_prev,
                               qw_ref h_out, qw_ref x_out, const qw_moe_layer *M, int32_t rows, float eps);
-/* The same, with the layer that runs next: at decode sizes the launch also
- * reads that layer's router rows and shared gate row (when it has this
- * layer's E and H) once its own router rows are out, so that the next
- * launch finds them in the caches.  No counterpart in the reference: for
- * drivers of a layer stack, which know the next layer.  next may be NULL
- * (then exactly qw_op_moe_layer_residual). */
-bool qw_op_moe_layer_residual_next(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref h, qw_ref y_prev,
-                                   qw_ref h_out, qw_ref x_out, const qw_moe_layer *M, const qw_moe_layer *next,
-                                   int32_t rows, float eps);
 
 /* qw_op_moe_layer's decode path (rows <= 8) with no allocation.  No
  * counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  The launch's staging and hand-off state live in a
- * static device array of 512 KiB per GPU (held until the process ends), whose
+ * static device array of 768 KiB per GPU (held until the process ends), whose
  * address the library resolves at qw_gpu_init; this call makes no
  * allocation of any kind and gives qw_op_moe_layer's bits (the one-launch
  * path for one token, the batch path for 2..8).  False, nothing encoded,
  * where qw_op_moe_layer would not take a decode path (past 8 rows, or shapes
  * the decode kernels do not take), or where the layer's staging at `rows`
- * exceeds what the array holds past its 76 KB hand-off state (446,208
+ * exceeds what the array holds past its 317 KiB hand-off state (462,080
  * bytes: config 1's shape at 8 rows stages 385,280; H 4096 with K 15 at 8
  * rows, 545,024, is refused, at 5 rows, 342,272, taken).
  * Every call on one GPU shares the array and finds it as the last call
- * left it (the hand-off state stays valid between calls; the staging needs
- * no clearing).  Calls whose launches overlap on one GPU -- the library's
+ * left it (the hand-off state stays valid between calls, and qw_gpu_init
+ * zeroes it; the staging needs no clearing).  The outputs go on the
+ * command's written list like any op's (qw_cmd_begin leaves room for 16
+ * buffers; a command already holding 16 others is refused, nothing
+ * encoded).  Calls whose launches overlap on one GPU -- the library's
  * single stream serialises its own -- would race on it.  Hand-off failures are reported as qw_op_moe_layer's
  * are, by qw_cmd_error after qw_cmd_wait. */
 bool qw_op_moe_layer_noalloc(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref x,

@@ -120,9 +120,6 @@ typedef struct {
     const uint16_t *sh_gate_w;       /* bf16 [H] */
 } qwk_moe;
 
-/* Bytes of device scratch the decode path needs for `rows` tokens.  Nothing
- * in it needs to be initialised. */
-size_t qwk_moe_decode_scratch(const qwk_moe *M, int rows);
 /* Bytes of the decode path's hand-off state.  It must be zeroed once before
  * first use (and again after an error); each launch then needs an epoch one
  * greater than the last (never 0; zero the state again before an epoch
@@ -143,7 +140,7 @@ int qwk_decode_sync_words(void *sync, uint32_t **err, void **words, size_t *nwor
 /* The allocation-free decode entry's device scratch (qw_static.hip): a
  * file-scope device array of this many bytes per GPU, holding the hand-off
  * state and then the staging area. */
-#define QWK_STATIC_SCRATCH_BYTES (512u * 1024u)
+#define QWK_STATIC_SCRATCH_BYTES (768u * 1024u)
 /* Resolves the array's address on the current device (hipGetSymbolAddress)
  * and zeroes it; once per device, at init.  Synchronous. */
 int qwk_static_init(hipStream_t s);
@@ -153,8 +150,12 @@ void *qwk_static_scratch(size_t *bytes);
 /* Zeroes `bytes` (a multiple of 16, 16-byte aligned) at p with a fill kernel
  * on s (no memset node, so it may sit in a captured graph). */
 int qwk_zero_fill(hipStream_t s, void *p, size_t bytes);
-/* Non-zero when the decode path takes this layer shape and token count. */
+/* Non-zero when the decode path takes this layer shape and token count: the
+ * one-token launch (qwk_decode1_supported) or the batch path
+ * (qwk_moe_decode_batch_supported, 1..QWK_DECODE_MAX_ROWS tokens). */
 int qwk_moe_decode_supported(const qwk_moe *M, int rows);
+int qwk_decode1_supported(const qwk_moe *M);
+int qwk_moe_decode_batch_supported(const qwk_moe *M, int rows);
 /* The residual step before a layer of a stack: the layer's input is
  * x = rms_norm(bf16(h + y)) (rms_norm(h) when y is NULL), unit weight;
  * h_out receives bf16(h + y) (or h), x_out that x.  h_out must not alias h
@@ -165,22 +166,19 @@ typedef struct {
     uint16_t *h_out;
     float *x_out;
     float eps;
-    /* When not NULL: the router rows (bf16 [E, H]) and shared gate row of
-     * the layer that runs next, read by the router workgroups once their
-     * own rows are out so that the next launch finds them in the caches. */
-    const uint16_t *next_router, *next_gate_w;
 } qwk_resid;
 
-/* Decode (rows <= QWK_DECODE_MAX_ROWS, K <= QWK_DECODE_MAX_K), one launch:
- * out [rows, H], idx/w [rows, K]; the input is x, or, when `res` is not NULL,
- * the residual step's x computed inside the launch.  `ev`, when not NULL,
- * holds 2 events, the launch's start and end, stamped by the dispatch itself. */
+/* Decode of one token in one launch (qwk_decode1_supported layers), K <=
+ * QWK_DECODE_MAX_K: out [H], idx/w [K]; the input is x, or, when `res` is
+ * not NULL, the residual step's x computed inside the launch.  It needs no
+ * scratch beyond the hand-off state `sync` (qwk_moe_decode_sync_bytes) and
+ * LDS.  `ev`, when not NULL, holds 2 events, the launch's start and end,
+ * stamped by the dispatch itself. */
 #define QWK_DECODE_MAX_ROWS 8
 #define QWK_DECODE_MAX_K 15
 int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
-                   const qwk_resid *res, const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes,
-                   void *sync, uint32_t epoch, hipEvent_t *ev);
-/* Decode of 2..QWK_DECODE_MAX_ROWS tokens over the batch's unique experts,
+                   const qwk_resid *res, const qwk_moe *M, void *sync, uint32_t epoch, hipEvent_t *ev);
+/* Decode of 1..QWK_DECODE_MAX_ROWS tokens over the batch's unique experts,
  * in four launches with no cross-workgroup waits (router logits, routing and
  * the unique-expert table, gate/up per unique expert, down and combine per
  * token).  Same shapes as qwk_moe_decode; scratch of

@@ -85,6 +85,10 @@ static struct {
 #define QW_DS_HEAP 0
 #define QW_DS_STATIC 1
 
+/* places in a command's written list from qw_cmd_begin (the list grows past
+ * them for every op but the allocation-free one) */
+#define QW_CMD_FIXED_WRITTEN 16
+
 /* ---- profiling table ---------------------------------------------------- */
 
 #define QW_PROF_MAX 64
@@ -119,6 +123,10 @@ void qw_prof_report(FILE *out, long tokens) {
                 (long long)P[i].count);
 }
 
+/* The hand-off state's size, rounded up to the fill kernel's 16 bytes (and
+ * allocated at that size). */
+static size_t dsync_bytes(void) { return (qwk_moe_decode_sync_bytes() + 15) & ~(size_t)15; }
+
 /* ---- device --------------------------------------------------------------- */
 
 bool qw_gpu_init(char *err, size_t errcap) {
@@ -148,7 +156,10 @@ bool qw_gpu_init(char *err, size_t errcap) {
         size_t sb = 0;
         char *sp = qwk_static_init(G.stream) == 0 ? qwk_static_scratch(&sb) : NULL;
         const size_t hs = (qwk_moe_decode_sync_bytes() + 255) & ~(size_t)255;
-        if (sp && sb > hs) {
+        /* the hand-off state is zeroed on every init: epochs restart at 1,
+         * so words and an error left by an earlier session must not survive */
+        if (sp && sb > hs && qwk_zero_fill(G.stream, sp, dsync_bytes()) == 0 &&
+            hipStreamSynchronize(G.stream) == hipSuccess) {
             G.ds[QW_DS_STATIC].sync = sp;
             G.ds[QW_DS_STATIC].epoch = 0;
             G.static_stage = sp + hs;
@@ -297,6 +308,11 @@ qw_cmd qw_cmd_begin(void) {
     if (!ensure_init()) return NULL;
     qw_cmd c = calloc(1, sizeof *c);
     if (!c) return NULL;
+    /* the written list starts with room for QW_CMD_FIXED_WRITTEN buffers, so
+     * the allocation-free entry can record its outputs without growing it */
+    c->written = malloc(QW_CMD_FIXED_WRITTEN * sizeof *c->written);
+    if (!c->written) { free(c); return NULL; }
+    c->capwritten = QW_CMD_FIXED_WRITTEN;
     c->next = G.live;
     G.live = c;
     if (G.prof) c->last = cmd_event(c, 1);
@@ -333,27 +349,31 @@ static void touch(qw_cmd c, qw_ref r, int writes) {
 
 static void *dp(qw_ref r) { return r.buf ? (char *)r.buf->dev + r.off : NULL; }
 
-/* touch() without the command's written list (which can grow): the buffer's
- * mirror is marked stale, so qw_buf_contents copies it back when the host
- * next asks for it.  For the allocation-free entry. */
-static void touch_fixed(qw_ref r, int writes) {
+/* touch() that never grows the command's written list: a written buffer is
+ * recorded only while the list has room (qw_cmd_begin gives it
+ * QW_CMD_FIXED_WRITTEN places), so qw_cmd_wait copies it back as it does for
+ * every other op.  Returns 0 when the list is full.  For the
+ * allocation-free entry. */
+static int touch_fixed(qw_cmd c, qw_ref r, int writes) {
     qw_buf b = r.buf;
-    if (!b) return;
+    if (!b) return 1;
     if (b->dev_stale) {
         hipMemcpyAsync(b->dev, b->host, b->len, hipMemcpyHostToDevice, G.stream);
         hipStreamSynchronize(G.stream);
         b->dev_stale = 0;
     }
-    if (writes) b->host_stale = 1;
+    if (!writes) return 1;
+    b->host_stale = 1;
+    for (int i = 0; i < c->nwritten; i++) if (c->written[i] == b) return 1;
+    if (c->nwritten >= c->capwritten) return 0;
+    c->written[c->nwritten++] = b;
+    return 1;
 }
 
 
 /* A decode hand-off state: the heap one is allocated on first use; both are
  * zeroed (epochs restarting at 1) at first use, after a launch reported an
  * error and before an epoch would repeat.  Zeroed by a fill kernel. */
-/* The hand-off state's size, rounded up to the fill kernel's 16 bytes (and
- * allocated at that size). */
-static size_t dsync_bytes(void) { return (qwk_moe_decode_sync_bytes() + 15) & ~(size_t)15; }
 
 static int dsync_reset(int k) {
     hipStreamSynchronize(G.stream);
@@ -941,22 +961,26 @@ static void moe_desc(qwk_moe *mp, const qw_moe_layer *M) {
     *mp = m;
 }
 
-/* Decode: one launch over only the selected experts.  Its staging and
- * hand-off state are the backend's heap scratch (k = QW_DS_HEAP) or the
- * static device array (k = QW_DS_STATIC: nothing allocated; the caller has
- * checked that the staging fits). */
-/* Decode scratch: the one-launch path's (one token) or the batch path's. */
+/* Decode over only the selected experts: one launch for one token, the
+ * batch path's launches otherwise.  The hand-off state and the batch path's
+ * staging are the backend's heap scratch (k = QW_DS_HEAP) or the static
+ * device array (k = QW_DS_STATIC: nothing allocated; the caller has checked
+ * that the staging fits). */
+/* Decode scratch: none for the one-launch path (one token; everything it
+ * hands over sits in the hand-off state), else the batch path's. */
+static int decode_one_launch(const qwk_moe *m, int32_t rows) { return rows == 1 && qwk_decode1_supported(m); }
 static size_t decode_need(const qwk_moe *m, int32_t rows) {
-    return rows >= 2 ? qwk_moe_decode_batch_scratch(m, rows) : qwk_moe_decode_scratch(m, rows);
+    return decode_one_launch(m, rows) ? 0 : qwk_moe_decode_batch_scratch(m, rows);
 }
 
 static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float *x,
                        const qwk_resid *res, const qwk_moe *mp, int32_t rows, int k) {
     const qwk_moe m = *mp;
     const size_t need = decode_need(&m, rows);
-    if (rows >= 2) {
-        /* several tokens: the batch path over their unique experts, after the
-         * residual step as its own pass when there is one */
+    if (!decode_one_launch(&m, rows)) {
+        /* several tokens (or a shape the one launch does not take): the
+         * batch path over their unique experts, after the residual step as
+         * its own pass when there is one */
         void *S = k == QW_DS_STATIC ? (void *)G.static_stage : scratch(need);
         const size_t have = k == QW_DS_STATIC ? G.static_stage_len : need;
         if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", need); return false; }
@@ -969,14 +993,11 @@ static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float
         launched(c, k == QW_DS_STATIC ? "moe_layer_noalloc" : "moe_layer (decode batch)", rc);
         return rc == 0;
     }
-    void *S = k == QW_DS_STATIC ? (void *)G.static_stage : scratch(need);
-    const size_t have = k == QW_DS_STATIC ? G.static_stage_len : need;
-    if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", need); return false; }
     if (!G.ds[k].sync && !dsync_reset(k)) {
         cmd_fail(c, hipErrorOutOfMemory, "moe_layer: decode hand-off state");
         return false;
     }
-    /* Flags and tagged logits hold past epochs, so an epoch is not reused
+    /* Tagged words hold past epochs, so an epoch is not reused
      * until the state is zeroed again (0 is "never"). */
     if (G.ds[k].epoch == UINT32_MAX && !dsync_check(k, 1)) {
         cmd_fail(c, hipErrorUnknown, "moe_layer: decode hand-off state");
@@ -985,7 +1006,7 @@ static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float
     const uint32_t epoch = ++G.ds[k].epoch;
     hipEvent_t ev[2] = { NULL, NULL };
     const int per_kernel = k == QW_DS_HEAP && G.prof && (ev[0] = cmd_event(c, 0)) && (ev[1] = cmd_event(c, 0));
-    const int rc = qwk_moe_decode(G.stream, out, idx, w, x, res, &m, rows, S, have, G.ds[k].sync, epoch,
+    const int rc = qwk_moe_decode(G.stream, out, idx, w, x, res, &m, G.ds[k].sync, epoch,
                                   per_kernel ? ev : NULL);
     if (per_kernel) cmd_add_mark(c, "moe decode", ev[0], ev[1]);
     c->ep_hi[k] = epoch;
@@ -1045,19 +1066,31 @@ bool qw_op_moe_layer_noalloc(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref 
                           M->down.w, M->down.scales, M->down.biases, M->sh_gate.w, M->sh_gate.scales,
                           M->sh_gate.biases, M->sh_up.w, M->sh_up.scales, M->sh_up.biases, M->sh_down.w,
                           M->sh_down.scales, M->sh_down.biases };
-    for (size_t i = 0; i < sizeof in / sizeof in[0]; i++) touch_fixed(in[i], 0);
-    touch_fixed(out, 1); touch_fixed(idx, 1); touch_fixed(w, 1);
+    /* the outputs go on the command's written list (room for them is checked
+     * before anything is touched), so qw_cmd_wait refreshes their mirrors */
+    {
+        int room = c->capwritten - c->nwritten;
+        const qw_buf o3[3] = { out.buf, idx.buf, w.buf };
+        for (int j = 0; j < 3; j++) {
+            int have = !o3[j];
+            for (int i = 0; i < c->nwritten && !have; i++) have = c->written[i] == o3[j];
+            for (int i = 0; i < j && !have; i++) have = o3[i] == o3[j];
+            room -= !have;
+        }
+        if (room < 0) {
+            cmd_fail(c, hipErrorInvalidValue, "moe_layer_noalloc: the command's written list is full (%d buffers); "
+                     "wait on the command before encoding more", QW_CMD_FIXED_WRITTEN);
+            fprintf(stderr, "qwasar: %s\n", c->msg);
+            return false;
+        }
+    }
+    for (size_t i = 0; i < sizeof in / sizeof in[0]; i++) touch_fixed(c, in[i], 0);
+    touch_fixed(c, out, 1); touch_fixed(c, idx, 1); touch_fixed(c, w, 1);
     return moe_decode(c, dp(out), dp(idx), dp(w), dp(x), NULL, &m, rows, QW_DS_STATIC);
 }
 
 bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref h, qw_ref y_prev,
                               qw_ref h_out, qw_ref x_out, const qw_moe_layer *M, int32_t rows, float eps) {
-    return qw_op_moe_layer_residual_next(c, out, idx, w, h, y_prev, h_out, x_out, M, NULL, rows, eps);
-}
-
-bool qw_op_moe_layer_residual_next(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref h, qw_ref y_prev,
-                                   qw_ref h_out, qw_ref x_out, const qw_moe_layer *M, const qw_moe_layer *next,
-                                   int32_t rows, float eps) {
     if (!moe_layer_ok(M, rows) || !h.buf || !h_out.buf || !x_out.buf) return false;
     if (h_out.buf == h.buf || (y_prev.buf && h_out.buf == y_prev.buf)) return false;
     if (!c) return true;
@@ -1073,12 +1106,7 @@ bool qw_op_moe_layer_residual_next(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, q
         if (rc != 0) return false;
         return moe_prefill(c, dp(out), dp(idx), dp(w), dp(x_out), M, rows);
     }
-    /* the next layer's router is read ahead only when it has this one's shape */
-    const int ahead = next && next->router.buf && next->sh_gate_w.buf && next->E == M->E && next->H == M->H;
-    if (ahead) { touch(c, next->router, 0); touch(c, next->sh_gate_w, 0); }
-    const qwk_resid res = { dp(h), dp(y_prev), dp(h_out), dp(x_out), eps,
-                            ahead ? (const uint16_t *)dp(next->router) : NULL,
-                            ahead ? (const uint16_t *)dp(next->sh_gate_w) : NULL };
+    const qwk_resid res = { dp(h), dp(y_prev), dp(h_out), dp(x_out), eps };
     return moe_decode(c, dp(out), dp(idx), dp(w), NULL, &res, &m, rows, QW_DS_HEAP);
 }
 

@@ -126,8 +126,6 @@ _sig("qw_moe_layer_free", None, C.POINTER(qw_moe_layer))
 _sig("qw_op_moe_layer", _B, _P, _R, _R, _R, _R, C.POINTER(qw_moe_layer), _I)
 _sig("qw_op_moe_layer_noalloc", _B, _P, _R, _R, _R, _R, C.POINTER(qw_moe_layer), _I)
 _sig("qw_op_moe_layer_residual", _B, _P, _R, _R, _R, _R, _R, _R, _R, C.POINTER(qw_moe_layer), _I, C.c_float)
-_sig("qw_op_moe_layer_residual_next", _B, _P, _R, _R, _R, _R, _R, _R, _R, C.POINTER(qw_moe_layer),
-     C.POINTER(qw_moe_layer), _I, C.c_float)
 _sig("qw_op_rms_norm", None, _P, _R, _R, _R, _I, _I, C.c_float, C.c_float)
 _sig("qw_op_hc_inject_norm", None, _P, _R, _R, _R, _R, _R, _I, _I, _I, C.c_float)
 _sig("qw_op_hc_pre_decode", _B, _P, _R, _R, _R, _R, _R, _R, _R, _R, _R, _R, _R, _R, _I, _I, _I, _I, C.c_float)

@@ -136,24 +136,21 @@ class Stack:
                 raise RuntimeError(f"qw_op_moe_layer refused layer {l} at {rows} rows")
             gpu.qw_op_residual_rms_norm_bf16(c, self.h.ref(), self.x.ref(), self.y.ref(), self.H, rows, EPS)
 
-    def encode_fused(self, c, rows: int, read_ahead: bool = False) -> None:
+    def encode_fused(self, c, rows: int) -> None:
         """The whole stack over h[:rows] with each residual step folded into
-        the next layer's op (qw_op_moe_layer_residual_next; at decode sizes
-        inside its one launch): layer l reads h from one of two buffers and
-        writes the other, y alternates the same way, and a last residual step
+        the next layer's op (qw_op_moe_layer_residual; at decode sizes inside
+        its one launch): layer l reads h from one of two buffers and writes
+        the other, y alternates the same way, and a last residual step
         finishes h, which ends in self.h_final.  Same arithmetic, in the same
-        order, as encode().  With read_ahead each decode launch also reads
-        the next layer's router rows (the last layer: the first's, for the
-        next token), which changes no result."""
+        order, as encode()."""
         hb, yb = (self.h, self.h2), (self.y, self.y2)
         n = len(self.layers)
         for l in range(n):
             y_prev = yb[(l - 1) % 2].ref() if l else gpu.NULL_REF
-            nxt = self.layers[(l + 1) % n].desc if read_ahead else None
-            if not gpu.qw_op_moe_layer_residual_next(c, yb[l % 2].ref(), self.idx.ref(), self.w.ref(),
-                                                     hb[l % 2].ref(), y_prev, hb[(l + 1) % 2].ref(), self.x.ref(),
-                                                     self.layers[l].desc, nxt, rows, EPS):
-                raise RuntimeError(f"qw_op_moe_layer_residual_next refused layer {l} at {rows} rows")
+            if not gpu.qw_op_moe_layer_residual(c, yb[l % 2].ref(), self.idx.ref(), self.w.ref(),
+                                                hb[l % 2].ref(), y_prev, hb[(l + 1) % 2].ref(), self.x.ref(),
+                                                self.layers[l].desc, rows, EPS):
+                raise RuntimeError(f"qw_op_moe_layer_residual refused layer {l} at {rows} rows")
         gpu.qw_op_residual_rms_norm_bf16(c, hb[n % 2].ref(), self.x.ref(), yb[(n - 1) % 2].ref(), self.H, rows, EPS)
         self.h_final = hb[n % 2]
 

@@ -174,9 +174,8 @@ def test_stack_config1_shape_layer_by_layer_and_free_running(gpu):
 
 
 def _fused_equals_unfused(gpu, layers, h0, rows):
-    """The fused stack, with and without the next layer's router read ahead
-    (qw_op_moe_layer_residual_next with and without `next`), gives the
-    unfused stack's bits."""
+    """The fused stack (qw_op_moe_layer_residual: each residual step inside
+    the next layer's op) gives the unfused stack's bits."""
     st = stack.Stack(layers, rows)
     st.h.write(h0)
     c = gpu.qw_cmd_begin()
@@ -184,15 +183,14 @@ def _fused_equals_unfused(gpu, layers, h0, rows):
     gpu.run(c, "unfused stack")
     want_h = st.h.read(np.uint16, (rows, st.H))
     want_x = st.x.read(np.float32, (rows, st.H))
-    for read_ahead in (True, False):
-        st.h.write(h0)
-        c = gpu.qw_cmd_begin()
-        st.encode_fused(c, rows, read_ahead)
-        gpu.run(c, "fused stack")
-        got_h = st.h_final.read(np.uint16, (rows, st.H))
-        got_x = st.x.read(np.float32, (rows, st.H))
-        assert np.array_equal(got_h, want_h), f"fused stack h differs from the unfused one (read ahead {read_ahead})"
-        assert np.array_equal(got_x.view(np.uint32), want_x.view(np.uint32)), f"fused stack x differs ({read_ahead})"
+    st.h.write(h0)
+    c = gpu.qw_cmd_begin()
+    st.encode_fused(c, rows)
+    gpu.run(c, "fused stack")
+    got_h = st.h_final.read(np.uint16, (rows, st.H))
+    got_x = st.x.read(np.float32, (rows, st.H))
+    assert np.array_equal(got_h, want_h), "fused stack h differs from the unfused one"
+    assert np.array_equal(got_x.view(np.uint32), want_x.view(np.uint32)), "fused stack x differs"
     st.free()
 
 

@@ -44,7 +44,7 @@ def test_noalloc_refuses_oversized_staging(gpu):
     command is needed to ask); a fitting shape is accepted.  Several tokens
     take the batch path, whose staging (logits, the unique-expert table, the
     f16 token rows, the pairs and tiles of the grouped gate / up, its fp32
-    activations and their q16 vectors) must fit the 446,208 bytes past the
+    activations and their q16 vectors) must fit the 462,080 bytes past the
     hand-off state."""
     r = gpu.NULL_REF
     q = gpu.qw_q4_ref(r, r, r, 64)
@@ -58,3 +58,44 @@ def test_noalloc_refuses_oversized_staging(gpu):
     small = gpu.qw_moe_layer(3072, 512, 10, 512, 512, True, True, r, q, q, q, q, q, q, q, r)
     assert gpu.qw_op_moe_layer_noalloc(None, r, r, r, r, small, 8)
     assert not gpu.qw_op_moe_layer_noalloc(None, r, r, r, r, small, 9)   # past the decode path
+
+
+def test_noalloc_refreshes_caller_mirrors(gpu):
+    """The outputs' host mirrors are current after qw_cmd_wait without another
+    qw_buf_contents: caller memory wrapped by qw_buf_wrap, and a view taken
+    before the call."""
+    L, _ = synth.make_config(1)
+    lb = gpu.LayerBufs(L)
+    x = synth.make_x(7300, 3, L.H)
+    want = _run(gpu, gpu.qw_op_moe_layer, lb, x)
+    B = gpu.Buf
+    out = np.zeros((3, L.H), np.float32)
+    ob = B(wrap=out)                   # the caller's own array is the mirror
+    ib = B(3 * L.K * 4)
+    iv = ib.view(np.int32, (3, L.K))   # a view kept from before the call
+    wb, xb = B(3 * L.K * 4), B.of(x)
+    c = gpu.qw_cmd_begin()
+    assert gpu.qw_op_moe_layer_noalloc(c, ob.ref(), ib.ref(), wb.ref(), xb.ref(), lb.desc, 3)
+    gpu.run(c, "noalloc into wrapped outputs")
+    assert np.array_equal(ob._keep.view(np.uint32), want[0].view(np.uint32)), "wrapped output not refreshed"
+    assert np.array_equal(iv, want[1]), "a view from before the call is stale"
+    lb.free()
+
+
+def test_noalloc_after_reinit(gpu):
+    """qw_gpu_shutdown then qw_gpu_init zeroes the static hand-off state (the
+    epochs restart at 1), so the calls after re-init give qw_op_moe_layer's
+    bits, not words left by the earlier session."""
+    L, _ = synth.make_config(1)
+    lb = gpu.LayerBufs(L)
+    xs = [synth.make_x(7400 + i, 1, L.H) for i in range(6)]
+    for x in xs:
+        _run(gpu, gpu.qw_op_moe_layer_noalloc, lb, x)
+    gpu.qw_gpu_shutdown()
+    gpu.init()
+    for i, x in enumerate(reversed(xs)):
+        got = _run(gpu, gpu.qw_op_moe_layer_noalloc, lb, x)
+        want = _run(gpu, gpu.qw_op_moe_layer, lb, x)
+        for g, w in zip(got, want):
+            assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), f"call {i} after re-init differs"
+    lb.free()
