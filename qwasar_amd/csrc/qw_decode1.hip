@@ -56,7 +56,14 @@
 // once, and the host reports the error.  A workgroup whose wait gave up still
 // publishes what it computed, so no other wait is left without an end.
 #include <hip/hip_ext.h>
+#include <type_traits>
 
+#ifdef QW_TRACE
+// (the routing helpers' phase hooks, in the same trace: slots 3..9 and 10, 11)
+extern __device__ unsigned long long qx_trace[2048 * 16];
+#define QW_RSTAMP(slot) do { if (threadIdx.x == 0) qx_trace[blockIdx.x * 16 + 1 + (slot)] = wall_clock64(); } while (0)
+#define QW_STAMP(slot) do { if (threadIdx.x == 0) qx_trace[blockIdx.x * 16 + 4 + (slot)] = wall_clock64(); } while (0)
+#endif
 #include "qw_device.h"
 #include "qw_kernels.h"
 
@@ -159,6 +166,7 @@ struct QxArgs {
     int gsb4;                      // a gate/up row's scales copied 2 groups a dword, else one a dword slot
     int lgSW, lgppi, lgngw;        // log2 of SW, of the copies a down row (SW / 2 / pb), of ngw
     int sb16;                      // gate/up scales by one 16-byte load a lane (see the worker)
+    int pre;                       // the shared expert's slices requested before the picks
 };
 
 // A plain load from global memory through a pointer the compiler cannot see
@@ -567,25 +575,26 @@ __host__ __device__ inline QxWL qx_wlayout(int UH, int rows_x, int P, int nux, i
 
 __host__ __device__ constexpr int qx_up64(int n) { return (n + 63) / 64 * 64; }
 
-// The order in which worker j requests its gate/up rows: row q goes to slot
-// (q A + j B) mod nq, A coprime with nq.  Workers that walked their rows in
-// step would request the same memory channels at the same time (measured:
-// 256 workgroups each streaming its own contiguous run move a third less
-// than when their requests are scattered); spread over different strides and
-// starts, the rows a chip requests at once fall on all of them.
-__device__ __forceinline__ int qx_perm_a(int nq)
+// The order in which worker j requests its gate/up rows: the rows past the
+// first n0 (those requested before the picks) go from slot n0 + s to row
+// n0 + (s A + j 5) mod (nq - n0), A coprime with nq - n0.  Workers that walk
+// their rows in step request the same memory channels at the same time
+// (measured: 256 workgroups each streaming its own contiguous run move a
+// third less than when their requests are scattered); spread over different
+// strides and starts, the rows a chip requests at once fall on all of them.
+__device__ __forceinline__ int qx_perm_a(int n)
 {
     const int c[5] = {7, 11, 13, 5, 3};
     for (int i = 0; i < 5; i++) {
-        int x = c[i], y = nq;
+        int x = c[i], y = n;
         while (y) { const int t = x % y; x = y; y = t; }
         if (x == 1) return c[i];
     }
     return 1;
 }
-__device__ __forceinline__ int qx_rot(int q, int j, int nq, int A)
+__device__ __forceinline__ int qx_slot_row(int s, int j, int n0, int nq, int A)
 {
-    return nq > 0 ? (q * A + j * 5) % nq : q;
+    return s < n0 || s >= nq ? s : n0 + ((s - n0) * A + j * 5) % (nq - n0);
 }
 
 // units of XCD x: x, x + 8, ...
@@ -643,85 +652,67 @@ __device__ void qx_worker(const QxArgs &a, int x, int j, uint4 *lds, QxWorkLds &
                 reinterpret_cast<float4 *>(a.xout)[i] = make_float4(v.x * qinv, v.y * qinv, v.z * qinv, v.w * qinv);
             }
     }
-    // the picks of this XCD's gatherer, then the table of this XCD's units
-    if (wave == 0) {
-        uint32_t v[1];
-        qx_poll<1, false, QX_SLEEP_PICKS>(a, a.sync->loc[x].pick, 2 * K + 1, v);
-        // (clamped: after a wait that gave up the words are whatever was read)
-        if (lane < K) S.pick[lane] = (int)min(v[0], (uint32_t)(a.m.E - 1));
-        else if (lane < 2 * K) S.coef[1 + lane - K] = __uint_as_float(v[0]);
-        else if (lane == 2 * K) S.coef[0] = __uint_as_float(v[0]);
-    }
-    __syncthreads();
-    // (an XCD without units still fills entry 0, with a valid unit: its
-    // gate/up waves issue their clamped loads through it and drop them)
-    if ((int)threadIdx.x < max(nux, 1)) S.unit[threadIdx.x] = qx_unit(a, S, min(x + 8 * (int)threadIdx.x, a.NU - 1));
-    __syncthreads();
-    QX_TS(1);
-
-    // ---- requests: this worker's gate/up rows (waves < QX_GUW), their
-    // scales and biases and its down slices (the other waves) ----
-    // gate/up: row q of the worker (q < 2 np_) is pair j + W (q / 2), gate
-    // (q even) or up; wave w's instruction i covers rows (w + QX_GUW i) rpi + slot
+    // ---- requests.  Gate/up: row q of the worker (q < 2 np_) is pair
+    // j + W (q / 2), gate (q even) or up; wave w's instruction i covers rows
+    // (w + QX_GUW i) rpi + slot.  The shared expert needs no routing, so when
+    // this XCD's first unit is one of its slices (x < nus) its rows (the
+    // first nq_sh of this worker's) and their down slices are requested
+    // before the picks are known (pass A), the rest after (pass B) ----
     const int lrg = a.lrg, rpi = 64 / lrg, slot = lane / lrg, lr = lane % lrg;
     const int nq = 2 * np_, words = H / 8, lgSW = a.lgSW;
-    const int pa = qx_perm_a(nq);                          // the request order's stride
+    const int nq_sh = a.pre && x < a.nus ? 2 * (j < a.SW ? (a.SW - 1 - j) / a.W + 1 : 0) : 0;
+    const int pa = qx_perm_a(max(nq - nq_sh, 1));
     uint2 gw[NRI][NUPL];
     int gq[NRI];
-    // The two roles are separate branches joined by a barrier without a fence
-    // (a fence would make every wave wait for all its loads in flight).
-    if (wave < QX_GUW) {
-        // The rows' scales and biases into LDS (row q at slot q gst), then the
-        // rows' words into registers, every load issued (at a clamped, valid
-        // address) before any is used.  With one row an instruction and
-        // 16-byte runs of scales (a.sb16), one 16-byte load a lane brings all
-        // of this wave's rows' scales and biases: lane i takes row i / 16,
-        // biases when (i / 8) % 2, piece i % 8; issued first, so waiting for
-        // it does not wait for the words.  Else the runs are copied into LDS
-        // a dword (or a bf16) a lane, a row an instruction.
-        uint4 sbv = make_uint4(0, 0, 0, 0);
-        const int sbp = groups / 8;                    // 16-byte pieces of a row's scales
-        int sbq = -1;
-        if (a.sb16) {
-            const int ri = lane >> 4, isb = (lane >> 3) & 1, pc = lane & 7;
-            const int q = qx_rot(wave + QX_GUW * ri, j, nq, pa);
-            if (ri < a.nri && wave + QX_GUW * ri < nq && pc < sbp) {
-                const int p = j + a.W * (q >> 1);
-                const QxUnit &U = S.unit[p >> lgSW];
-                const uint16_t *rb = isb ? ((q & 1) ? U.ub : U.gb) : ((q & 1) ? U.us : U.gs);
-                sbv = qx_ldg4(rb + (size_t)(p & (a.SW - 1)) * groups + 8 * pc);
-                sbq = q;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < NRI; i++) {
-            const int q0_ = (wave + QX_GUW * i) * rpi + slot;
-            const int q = q0_ < nq ? qx_rot(q0_, j, nq, pa) : q0_;
-            gq[i] = i < a.nri && q0_ < nq ? q : -1;
-            const int qc = min(q, max(nq - 1, 0));
-            const int p = min(j + a.W * (qc >> 1), max(rows_x - 1, 0));
+    const int sbp = groups / 8;                        // 16-byte pieces of a row's scales
+    // The gate/up waves (< QX_GUW) request rows' words into registers and
+    // the rows' scales and biases into LDS (row q at slot q gst), every load
+    // at a clamped, valid address and none used yet.  With one row an
+    // instruction and 16-byte runs of scales (a.sb16), one 16-byte load a
+    // lane (lane i: the wave's instruction i / 16, biases when (i / 8) % 2,
+    // piece i % 8), issued before the words, so that its store into LDS waits
+    // for it alone; else copies into LDS a dword (or a bf16) a lane, a row an
+    // instruction.  Only instruction 0 of a wave is ever a shared row
+    // (nq_sh <= QX_GUW - 1, one row an instruction).
+    auto sb_load = [&](bool want, uint4 &v, int &vq) {
+        const int ri = lane >> 4, isb = (lane >> 3) & 1, pc = lane & 7;
+        const int qs = wave + QX_GUW * ri, q = qx_slot_row(qs, j, nq_sh, nq, pa);
+        vq = -1;
+        if (want && ri < a.nri && qs < nq && pc < sbp) {
+            const int p = j + a.W * (q >> 1);
             const QxUnit &U = S.unit[p >> lgSW];
-            const uint32_t *rw = ((qc & 1) ? U.uw : U.gw) + (size_t)(p & (a.SW - 1)) * words;
-#pragma unroll
-            for (int n = 0; n < NUPL; n++)
-                gw[i][n] = qx_ldg2(rw + 2 * min(lr + lrg * n, UH - 1));
+            const uint16_t *rb = isb ? ((q & 1) ? U.ub : U.gb) : ((q & 1) ? U.us : U.gs);
+            v = qx_ldg4(rb + (size_t)(p & (a.SW - 1)) * groups + 8 * pc);
+            vq = q;
         }
-        if (a.sb16) {
-            if (sbq >= 0)
-                *reinterpret_cast<uint4 *>(((lane >> 3) & 1 ? gB : gS) + sbq * gst + 4 * (lane & 7)) = sbv;
-        } else {
-#ifndef QX_X_NOSC
-        for (int i = 0; i < a.nri; i++)
+    };
+    auto sb_store = [&](const uint4 &v, int vq) {
+        if (vq >= 0) *reinterpret_cast<uint4 *>(((lane >> 3) & 1 ? gB : gS) + vq * gst + 4 * (lane & 7)) = v;
+    };
+    auto row_load = [&](int i) {
+        const int qs = (wave + QX_GUW * i) * rpi + slot, q = qx_slot_row(qs, j, nq_sh, nq, pa);
+        gq[i] = i < a.nri && qs < nq ? q : -1;
+        const int qc = min(q, max(nq - 1, 0));
+        const int p = min(j + a.W * (qc >> 1), max(rows_x - 1, 0));
+        const QxUnit &U = S.unit[p >> lgSW];
+        const uint32_t *rw = ((qc & 1) ? U.uw : U.gw) + (size_t)(p & (a.SW - 1)) * words;
+#pragma unroll
+        for (int n = 0; n < NUPL; n++)
+            gw[i][n] = qx_ldg2(rw + 2 * min(lr + lrg * n, UH - 1));
+    };
+    auto sc_copy = [&](int i0, int i1) {
+        for (int i = i0; i < i1; i++)
             for (int sl = 0; sl < rpi; sl++) {
-                const int q0_ = (wave + QX_GUW * i) * rpi + sl;
-                if (q0_ >= nq || lane >= gst) continue;
-                const int q = qx_rot(q0_, j, nq, pa);
+                const int qs = (wave + QX_GUW * i) * rpi + sl, q = qx_slot_row(qs, j, nq_sh, nq, pa);
+                if (qs >= nq || lane >= gst) continue;
                 const int p = j + a.W * (q >> 1);
                 const QxUnit &U = S.unit[p >> lgSW];
                 const size_t ro = (size_t)(p & (a.SW - 1)) * groups + (a.gsb4 ? 2 : 1) * lane;
                 const uint16_t *ps = ((q & 1) ? U.us : U.gs) + ro, *pb = ((q & 1) ? U.ub : U.gb) + ro;
-                __attribute__((address_space(3))) void *ds_ = (__attribute__((address_space(3))) void *)(gS + q * gst);
-                __attribute__((address_space(3))) void *db_ = (__attribute__((address_space(3))) void *)(gB + q * gst);
+                __attribute__((address_space(3))) void *ds_ =
+                    (__attribute__((address_space(3))) void *)(gS + q * gst);
+                __attribute__((address_space(3))) void *db_ =
+                    (__attribute__((address_space(3))) void *)(gB + q * gst);
                 if (a.gsb4) {
                     __builtin_amdgcn_global_load_lds(ps, ds_, 4, 0, 0);
                     __builtin_amdgcn_global_load_lds(pb, db_, 4, 0, 0);
@@ -730,8 +721,20 @@ __device__ void qx_worker(const QxArgs &a, int x, int j, uint4 *lds, QxWorkLds &
                     __builtin_amdgcn_global_load_lds(pb, db_, 2, 0, 0);
                 }
             }
-#endif
-        }
+    };
+    // The rest of a gate/up wave's requests, then its dots; instantiated with
+    // and without instruction 0 already requested, so that no register holds
+    // either of two loads (a merge of registers with loads in flight waits
+    // for them).
+    auto gu_rest = [&](auto pre0, auto sb16c) {
+        constexpr bool P0 = decltype(pre0)::value, SB = decltype(sb16c)::value;
+        uint4 sbv;                                 // (no initial value: a write would wait for the load)
+        int sbq = -1;
+        if (SB) sb_load(!P0 || (lane >> 4) > 0, sbv, sbq);
+#pragma unroll
+        for (int i = P0 ? 1 : 0; i < NRI; i++) row_load(i);
+        if (SB) sb_store(sbv, sbq);
+        else sc_copy(P0 ? 1 : 0, a.nri);
         QX_TSW(0, 7);
         // ---- gate/up dots (the first LDS read waits for this wave's loads) ----
 #pragma unroll
@@ -755,49 +758,118 @@ __device__ void qx_worker(const QxArgs &a, int x, int j, uint4 *lds, QxWorkLds &
             if (lr == 0 && gq[i] >= 0) ys[gq[i]] = acc;
             if (i == 0) QX_TSW(0, 8);
         }
-    } else {
-        const int cw = wave - QX_GUW;
-#ifdef QX_DOWN_DELAY
+    };
+    // The copy waves copy the units' down slices straight into LDS
+    // (global_load_lds: no registers held): unit ui's rows j, j + W, ... of
+    // its slice in PB-byte pieces (lane order = LDS order: piece q of the
+    // unit is row q / ppi), then their scales and biases (ngw dword slots a
+    // row: two groups a dword, or one bf16 in a dword's low half).  Pass 0
+    // the shared unit (unit 0, when nq_sh > 0), pass 1 the others.
+    auto issue_cp = [&](int pass) {
         {
-            const unsigned long long t0 = wall_clock64();
-            while (wall_clock64() - t0 < QX_DOWN_DELAY) __builtin_amdgcn_s_sleep(2);
-        }
-#endif
-        // down: unit ui's rows j, j + W, ... of its slice, copied straight into
-        // LDS (global_load_lds: no registers held), in PB-byte pieces (lane
-        // order = LDS order: piece q of the unit is row q / ppi); then their
-        // scales and biases (ngw dword slots a row: two groups a dword, or
-        // one bf16 in a dword's low half)
-        // (each worker starts at a different unit, for the same reason as the
-        // gate/up rows' order)
-        for (int uj = 0; uj < nux; uj++) {
-            const int ui = (uj + j) % nux;
-            const QxUnit &U = S.unit[ui];
-            for (int q0 = 64 * cw; q0 < nr * ppi; q0 += 64 * QX_CPW) {
-                const int q = min(q0 + lane, nr * ppi - 1);
-                const uint8_t *src = reinterpret_cast<const uint8_t *>(U.dw + (size_t)(j + a.W * (q >> lgppi)) * U.dwr) +
-                                     (q & (ppi - 1)) * PB;
-                __attribute__((address_space(3))) void *dst =
-                    (__attribute__((address_space(3))) void *)(dW + ((size_t)ui * ustr + q0) * PB);
-                if (PB == 16) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
-                else __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
-            }
-            for (int q0 = 64 * cw; q0 < nr * ngw; q0 += 64 * QX_CPW) {
-                const int q = min(q0 + lane, nr * ngw - 1);
-                const size_t ro = (size_t)(j + a.W * (q >> lgngw)) * U.dgr + (a.sb4 ? 2 : 1) * (q & (ngw - 1));
-                __attribute__((address_space(3))) void *ds_ =
-                    (__attribute__((address_space(3))) void *)(dS + ui * sstr + q0);
-                __attribute__((address_space(3))) void *db_ =
-                    (__attribute__((address_space(3))) void *)(dB + ui * sstr + q0);
-                if (a.sb4) {
-                    __builtin_amdgcn_global_load_lds(U.ds + ro, ds_, 4, 0, 0);
-                    __builtin_amdgcn_global_load_lds(U.db + ro, db_, 4, 0, 0);
-                } else {
-                    __builtin_amdgcn_global_load_lds(U.ds + ro, ds_, 2, 0, 0);
-                    __builtin_amdgcn_global_load_lds(U.db + ro, db_, 2, 0, 0);
+            const int cw = wave - QX_GUW;
+            // pass 0: unit 0 when it is a shared slice; pass 1: the rest
+            const int u_lo = pass == 0 ? 0 : (nq_sh > 0 ? 1 : 0), u_hi = pass == 0 ? (nq_sh > 0 ? 1 : 0) : nux;
+            for (int uk = u_lo; uk < u_hi; uk++) {
+                // (workers start on different units: spread over channels)
+                const int ui = u_lo + (uk - u_lo + j) % (u_hi - u_lo);
+                const QxUnit &U = S.unit[ui];
+                for (int q0 = 64 * cw; q0 < nr * ppi; q0 += 64 * QX_CPW) {
+                    const int q = min(q0 + lane, nr * ppi - 1);
+                    const uint8_t *src =
+                        reinterpret_cast<const uint8_t *>(U.dw + (size_t)(j + a.W * (q >> lgppi)) * U.dwr) +
+                        (q & (ppi - 1)) * PB;
+                    __attribute__((address_space(3))) void *dst =
+                        (__attribute__((address_space(3))) void *)(dW + ((size_t)ui * ustr + q0) * PB);
+                    if (PB == 16) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+                    else __builtin_amdgcn_global_load_lds(src, dst, 4, 0, 0);
+                }
+                for (int q0 = 64 * cw; q0 < nr * ngw; q0 += 64 * QX_CPW) {
+                    const int q = min(q0 + lane, nr * ngw - 1);
+                    const size_t ro = (size_t)(j + a.W * (q >> lgngw)) * U.dgr + (a.sb4 ? 2 : 1) * (q & (ngw - 1));
+                    __attribute__((address_space(3))) void *ds_ =
+                        (__attribute__((address_space(3))) void *)(dS + ui * sstr + q0);
+                    __attribute__((address_space(3))) void *db_ =
+                        (__attribute__((address_space(3))) void *)(dB + ui * sstr + q0);
+                    if (a.sb4) {
+                        __builtin_amdgcn_global_load_lds(U.ds + ro, ds_, 4, 0, 0);
+                        __builtin_amdgcn_global_load_lds(U.db + ro, db_, 4, 0, 0);
+                    } else {
+                        __builtin_amdgcn_global_load_lds(U.ds + ro, ds_, 2, 0, 0);
+                        __builtin_amdgcn_global_load_lds(U.db + ro, db_, 2, 0, 0);
+                    }
                 }
             }
         }
+    };
+#pragma unroll
+    for (int i = 0; i < NRI; i++) gq[i] = -1;
+
+    // The two roles run as separate branches with matching barriers (without
+    // a fence: a fence would make every wave wait for all its loads in
+    // flight), so that the gate/up waves' first LDS read waits only for their
+    // own loads, not for copies into LDS on some other path.
+    // The gate/up branch, instantiated for each way of bringing the scales
+    // (the copies into LDS of the other way would make the compiler wait for
+    // every load before the dots' first LDS read).
+    auto gu_branch = [&](auto sb16c) {
+        constexpr bool SB = decltype(sb16c)::value;
+        const bool pre0 = wave < nq_sh;            // (instruction 0 is a shared row: rpi = 1)
+        // pass A: the shared unit's table entry (its pointers need no routing), its rows
+        if (nq_sh > 0) {
+            if (threadIdx.x == 0) S.unit[0] = qx_unit(a, S, x);
+            qx_barrier();
+        }
+        if (pre0) {
+            if (SB) {
+                uint4 v;
+                int vq;
+                sb_load((lane >> 4) == 0, v, vq);
+                row_load(0);
+                sb_store(v, vq);
+            } else {
+                row_load(0);
+                sc_copy(0, 1);
+            }
+        }
+        // the picks of this XCD's gatherer, polled by a wave with nothing in
+        // flight (a poll waits for its wave's earlier loads): the last gate/up
+        // wave, whose rows are not the shared unit's (nq_sh <= QX_GUW - 1)
+        if (wave == QX_GUW - 1) {
+            uint32_t v[1];
+            qx_poll<1, false, QX_SLEEP_PICKS>(a, a.sync->loc[x].pick, 2 * K + 1, v);
+            // (clamped: after a wait that gave up the words are whatever was read)
+            if (lane < K) S.pick[lane] = (int)min(v[0], (uint32_t)(a.m.E - 1));
+            else if (lane < 2 * K) S.coef[1 + lane - K] = __uint_as_float(v[0]);
+            else if (lane == 2 * K) S.coef[0] = __uint_as_float(v[0]);
+        }
+        qx_barrier();
+        // the rest of the table (an XCD without units still fills entry 0, with
+        // a valid unit: its gate/up waves issue their clamped loads through it
+        // and drop them), then every unit's combine coefficient
+        if ((int)threadIdx.x < max(nux, 1) && !(threadIdx.x == 0 && nq_sh > 0))
+            S.unit[threadIdx.x] = qx_unit(a, S, min(x + 8 * (int)threadIdx.x, a.NU - 1));
+        qx_barrier();
+        if ((int)threadIdx.x < nux) {
+            const int u = x + 8 * threadIdx.x;
+            S.unit[threadIdx.x].coef = u < a.nus ? S.coef[0] : S.coef[1 + min((u - a.nus) / a.nui, K - 1)];
+        }
+        QX_TS(1);
+        // pass B
+        if (pre0) gu_rest(std::true_type{}, sb16c);
+        else gu_rest(std::false_type{}, sb16c);
+    };
+    if (wave < QX_GUW) {
+        if (a.sb16) gu_branch(std::true_type{});
+        else gu_branch(std::false_type{});
+    } else {
+        if (nq_sh > 0) {
+            qx_barrier();
+            issue_cp(0);
+        }
+        qx_barrier();
+        qx_barrier();
+        issue_cp(1);
         QX_TSW(QX_GUW, 10);
     }
     qx_barrier();          // (B2) every gate/up row result is in LDS (the down copies may be in flight)
@@ -918,7 +990,7 @@ __global__ __launch_bounds__(QX_THREADS, 8) void k_decode1(QxArgs a)
 // ---- host side ------------------------------------------------------------------
 
 struct QxPlan {
-    int nupl, lrg, nri, W, SW, NSU, nus, nui, NU, rpw, pb, sb4, ngw, gsb4, lgSW, lgppi, lgngw, sb16;
+    int nupl, lrg, nri, W, SW, NSU, nus, nui, NU, rpw, pb, sb4, ngw, gsb4, lgSW, lgppi, lgngw, sb16, pre;
 };
 
 // The launch's shape for a layer, or false when the one-token launch does
@@ -974,6 +1046,9 @@ static bool qx_plan(const qwk_moe *M, QxPlan *p)
     // one row an instruction, a row's scales whole 16-byte runs (8 groups),
     // at most 8 runs, and the rows a wave holds in 16 lanes each
     p->sb16 = p->lrg == 64 && (H / G) % 8 == 0 && H / G <= 64 && p->nri <= 4 && p->gsb4;
+    // the shared slices' rows ahead of the picks: at most one a XCD, and no
+    // more rows a worker than leave the last gate/up wave free to poll
+    p->pre = p->nus <= QX_NX && 2 * ((sw + p->W - 1) / p->W) <= QX_GUW - 1 && p->lrg == 64;
     if (qx_wlayout(UH, nux * sw, P, nux, p->rpw, qx_up64(p->rpw * (sw / 2 / p->pb)), p->pb, qx_up64(p->rpw * p->ngw),
                    p->gsb4 ? H / G / 2 : H / G).total > QX_LDS)
         return false;
@@ -1062,6 +1137,7 @@ extern "C" int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w,
     a.lgppi = p.lgppi;
     a.lgngw = p.lgngw;
     a.sb16 = p.sb16;
+    a.pre = p.pre;
     const int grid = a.n_rt + QX_NX + QX_NX * p.W;
     hipEvent_t e0 = ev ? ev[0] : 0, e1 = ev ? ev[1] : 0;
 #define QX_GO(N_, R_)                                                      \

@@ -193,6 +193,21 @@ def test_prefill_shared_expert_grouped(gpu, split):
     lb.free()
 
 
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("si", [128, 256])
+def test_decode_shared_slices_ahead(gpu, split, si):
+    """Slices of 128 features (I = 128) on a 1024-wide layer: the one-token
+    launch requests the shared expert's slices before the picks are known
+    and the routed ones after, its rows first in each worker's order.  One
+    token at a time, every output against the oracle."""
+    L = synth.make_layer(331 + si, H=1024, E=64, K=6, I=128, SI=si, group=64, split=split, tag=f"shahead{si}.")
+    lb = gpu.LayerBufs(L)
+    for t in range(3):
+        x = synth.make_x(340 + t, 1, L.H, name=f"shahead.x{t}")
+        check(run_layer(gpu, lb, x), ref.moe_forward(L, x), DECODE_REL)
+    lb.free()
+
+
 @pytest.mark.parametrize("rows", [1, 3])
 def test_decode_back_to_back(gpu, c1, rows):
     """Sixteen decode launches queued in one command, each on its own tokens
