@@ -59,10 +59,15 @@
 #include <type_traits>
 
 #ifdef QW_TRACE
+// QW_TRACE_MASK: the slots that stamp (each stamp costs its wave time)
+#ifndef QW_TRACE_MASK
+#define QW_TRACE_MASK 0xffff
+#endif
+#define QX_TON(slot) ((((QW_TRACE_MASK) >> (slot)) & 1) != 0)
 // (the routing helpers' phase hooks, in the same trace: slots 3..9 and 10, 11)
 extern __device__ unsigned long long qx_trace[2048 * 16];
-#define QW_RSTAMP(slot) do { if (threadIdx.x == 0) qx_trace[blockIdx.x * 16 + 1 + (slot)] = wall_clock64(); } while (0)
-#define QW_STAMP(slot) do { if (threadIdx.x == 0) qx_trace[blockIdx.x * 16 + 4 + (slot)] = wall_clock64(); } while (0)
+#define QW_RSTAMP(slot) do { if (QX_TON(1 + (slot)) && threadIdx.x == 0) qx_trace[blockIdx.x * 16 + 1 + (slot)] = wall_clock64(); } while (0)
+#define QW_STAMP(slot) do { if (QX_TON(4 + (slot)) && threadIdx.x == 0) qx_trace[blockIdx.x * 16 + 4 + (slot)] = wall_clock64(); } while (0)
 #endif
 #include "qw_device.h"
 #include "qw_kernels.h"
@@ -74,10 +79,10 @@ extern __device__ unsigned long long qx_trace[2048 * 16];
 __device__ unsigned long long qx_trace[2048 * 16];
 // slots 0..14 the phases (thread 0, or the first lane of wave w for
 // QX_TSW); slot 15 where the workgroup ran (HW_REG_XCC_ID)
-#define QX_TS(slot) do { if (threadIdx.x == 0) { qx_trace[blockIdx.x * 16 + (slot)] = wall_clock64(); \
+#define QX_TS(slot) do { if (QX_TON(slot) && threadIdx.x == 0) { qx_trace[blockIdx.x * 16 + (slot)] = wall_clock64(); \
     if ((slot) == 0) qx_trace[blockIdx.x * 16 + 15] = (unsigned)__builtin_amdgcn_s_getreg((31 << 11) | 20) | \
         ((unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 4) << 32); } } while (0)
-#define QX_TSW(w, slot) do { if (threadIdx.x == 64 * (w)) qx_trace[blockIdx.x * 16 + (slot)] = wall_clock64(); } while (0)
+#define QX_TSW(w, slot) do { if (QX_TON(slot) && threadIdx.x == 64 * (w)) qx_trace[blockIdx.x * 16 + (slot)] = wall_clock64(); } while (0)
 extern "C" int qwk_decode_trace_read(unsigned long long *dst, size_t n)
 {
     return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(qx_trace), n * sizeof(unsigned long long));
@@ -114,9 +119,7 @@ extern "C" int qwk_decode_trace_read(unsigned long long *dst, size_t n)
 #define QX_SLEEP_FAR 8
 #define QX_SLEEP_NEAR 1
 // (the picks come a routing's time after the workers start: they poll slower)
-#ifndef QX_SLEEP_PICKS
 #define QX_SLEEP_PICKS 2
-#endif
 // (the XCD that sums the partials polls last, with the weight stream over)
 #define QX_SLEEP_PART 2
 
@@ -451,21 +454,31 @@ __device__ void qx_gather(const QxArgs &a, int x, QxGatherLds &G)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int E = a.m.E, K = a.m.K;
-    float lv = 0.0f;
-    if (wave < QX_PL && 64 * wave < E) {
-        uint32_t v[1];
-        qx_poll<1, true>(a, a.sync->lgt + 64 * wave, E - 64 * wave, v);
-        lv = __uint_as_float(v[0]);
-    } else if (wave == QX_PL) {
-        uint32_t v[1];
-        qx_poll<1, true>(a, a.sync->lgt + E, 1, v);
-        if (lane == 0) G.coef = qw_sigmoid(__uint_as_float(v[0]));
-    }
-    QX_TS(1);
-    // (waves whose slice starts past E hold -inf there: qw_route_block masks e >= E)
     int pi = 0;
     float pw = 0.0f;
-    qw_route_block<QX_PL>(lv, E, K, a.m.norm, wave, lane, &pi, &pw, G.sx, G.vb);
+    // Two passes over the same code: the first on made-up logits while the
+    // router works, which brings the routing code into this CU's instruction
+    // cache (a launch runs it once: cold, every miss a trip to memory); the
+    // second on the real ones.
+#pragma nounroll
+    for (int pass = 0; pass < 2; pass++) {
+        float lv = -0.01f * (float)(lane + 64 * wave);
+        if (pass == 1) {
+            if (wave < QX_PL && 64 * wave < E) {
+                uint32_t v[1];
+                qx_poll<1, true>(a, a.sync->lgt + 64 * wave, E - 64 * wave, v);
+                lv = __uint_as_float(v[0]);
+            } else if (wave == QX_PL) {
+                uint32_t v[1];
+                qx_poll<1, true>(a, a.sync->lgt + E, 1, v);
+                if (lane == 0) G.coef = qw_sigmoid(__uint_as_float(v[0]));
+            }
+            QX_TS(1);
+        }
+        // (waves whose slice starts past E hold -inf there: qw_route_block masks e >= E)
+        qw_route_block<QX_PL>(lv, E, K, a.m.norm, wave, lane, &pi, &pw, G.sx, G.vb);
+        __syncthreads();
+    }
     if (wave == 0) {
         // clamped: after a wait that gave up the logits are whatever was read,
         // and no pick may then address outside the banks
@@ -1007,10 +1020,7 @@ static bool qx_plan(const qwk_moe *M, QxPlan *p)
     p->nupl = UH >= 64 ? UH / 64 : 1;
     if (p->nupl > 4) return false;
     // slice: the widest of 256, 128, 64, 32, 16 features dividing I and SI
-#ifndef QX_SW_MAX
-#define QX_SW_MAX 256
-#endif
-    int sw = QX_SW_MAX;
+    int sw = 256;
     while (sw > 16 && (I % sw || SI % sw)) sw /= 2;
     p->SW = sw;
     p->NSU = sw / 16;

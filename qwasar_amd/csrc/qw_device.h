@@ -336,9 +336,7 @@ __device__ __forceinline__ uint32_t qw_ldu16(const void *base, uint32_t off)
 // expert lane + 64 j (0 past E), the softmax p = v / sum, and the top K by
 // p, descending, ties to the lower expert.  The sum adds a lane's v[j] in j
 // order from 0, then the lane partials by the 64-lane xor tree.
-#ifndef QW_ROUTE_PRIO
 #define QW_ROUTE_PRIO 3
-#endif
 template <int PL>
 __device__ __forceinline__ void qw_route_finish(float (&v)[PL], int E, int K, int norm, int lane,
                                                int *pick_i, float *pick_w, uint32_t *sx)

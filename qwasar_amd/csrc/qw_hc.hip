@@ -19,18 +19,6 @@
 #define QH_THREADS 256
 #define QH_PRE_MAXS 4             // streams a fused decode kernel takes
 
-// Built with -DQH_TRACE, every workgroup stamps the device wall clock
-// (100 MHz) at its phases into qh_trace[block][slot], for timelines.
-#ifdef QH_TRACE
-__device__ unsigned long long qh_trace[2048 * 8];
-#define QH_TS(slot) do { if (threadIdx.x == 0) qh_trace[blockIdx.x * 8 + (slot)] = wall_clock64(); } while (0)
-extern "C" int qh_trace_read(unsigned long long *dst)
-{
-    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(qh_trace), sizeof(qh_trace));
-}
-#else
-#define QH_TS(slot) do { } while (0)
-#endif
 
 __device__ __forceinline__ float qh_sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
 
@@ -328,14 +316,12 @@ __device__ __forceinline__ void qh_inject_norm(float4 *nl, float (*part)[QH_THRE
                 }
         }
     }
-    QH_TS(5);
 #pragma unroll
     for (int s = 0; s < QH_PRE_MAXS; s++) {
         const float v = qw_xor_sum<64>(ss[s]);
         if (lane == 0) part[s][wave] = v;
     }
     __syncthreads();
-    QH_TS(6);
 #pragma unroll
     for (int s = 0; s < QH_PRE_MAXS; s++) {
         float tot = part[s][0];
@@ -698,9 +684,7 @@ extern "C" int qwk_hc_mix_up(hipStream_t s, float *x, const float *d, const floa
 // Nothing waits on a workgroup dispatched after it (the down workgroups come
 // first), and every wait is bounded: on giving up it raises the error word
 // (the launch's epoch, unless set) and the workgroup finishes.
-#ifndef QH_DR
 #define QH_DR 8                   // down rows a workgroup (of one stream; 32 lanes a row)
-#endif
 #define QH_DLPR (QH_THREADS / QH_DR)   // lanes a down row
 #define QH_NSJ 8                  // 32-input segments a down lane holds (H <= 32 * QH_DLPR * QH_NSJ)
 #define QH_MAX_LR 512             // lowrank
@@ -711,9 +695,7 @@ extern "C" int qwk_hc_mix_up(hipStream_t s, float *x, const float *d, const floa
 #define QH_TDONE (QH_TD + QH_PRE_MAXS * QH_MAX_LR)   // (stream-major), then the done copies
 #define QH_TAG_WORDS (QH_TDONE + QH_DREP * QH_DSTRIDE)
 #define QH_SPIN_LIMIT (1 << 16)
-#ifndef QH_SLEEP
 #define QH_SLEEP 1                // s_sleep between polls (units of 64 clocks)
-#endif
 
 
 __device__ __forceinline__ unsigned long long qh_ld(const uint2 *p)
@@ -751,9 +733,7 @@ __device__ bool qh_wait_words(const uint2 *p, int n, uint32_t *err, uint32_t epo
     }
 }
 
-#ifndef QH_UP_RATE
 #define QH_UP_RATE 200.0     // bytes a 100 MHz tick through one CU's L1 (~20 GB/s), for up_delay
-#endif
 
 struct QhArgs {
     float *x, *h4_out, *n4, *d, *inj_out;
@@ -776,10 +756,6 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
     __shared__ float pc[QH_THREADS];
     const int b = blockIdx.x, t = threadIdx.x, H = a.H, S = a.S, HH = S * H, k = a.lowrank;
     const int wave = t >> 6, lane = t & 63;
-    QH_TS(0);
-#ifdef QH_TRACE
-    if (t == 0) qh_trace[blockIdx.x * 8 + 7] = __builtin_readcyclecounter();
-#endif
     if (b < a.nd) {
         const int sd = b % S, r0 = (b / S) * QH_DR, words = HH / 8, nsg = H / 32;
         const int q = t / QH_DLPR, l = t % QH_DLPR, r = r0 + q;
@@ -802,7 +778,6 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
             }
         };
         const float inv = qh_norm1<NI>(nl, part, sd, a.h4, a.out, a.inj, a.wn, H, S, a.eps, weights);
-        QH_TS(1);
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < QH_NSJ; j++) {
@@ -832,7 +807,6 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
         // acknowledgement: a reader checks every partial's tag and re-reads
         // stale ones, so the done words only say when to start reading
         __syncthreads();
-        QH_TS(2);
         if (t < QH_DREP) qh_st(a.tw + QH_TDONE + t * QH_DSTRIDE + b, a.epoch, 0u);
         return;
     }
@@ -844,9 +818,7 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
         uint4 ww[8];
         qh_inject_norm<NI, true>(nl, part, s, a.h4_out, a.n4, a.h4, a.out, a.inj, a.wn, H, S, a.eps, inv,
                                  [&] { qh_inj_load(a.bj, s, HH, ww); });
-        QH_TS(1);
         qh_inj_logit<true>(nl, pc, ww, s, HH, a.inj_out);
-        QH_TS(2);
         return;
     }
     // up
@@ -885,7 +857,6 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
     float *dl = xsl + QH_MAX_LR;                            // [k]
     float *invl = dl + QH_MAX_LR;                           // [S]
     float *mixv = invl + QH_PRE_MAXS;                       // [ow][S]
-    QH_TS(1);
     // one wave polls the down workgroups' done words (its XCD's copy: the
     // polling stays off the words the down workgroups write), then the
     // workgroup reads d's partials and the 1/rms, every tag checked (the
@@ -897,7 +868,6 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
     if (wave == 0 && !qh_wait_words(a.tw + QH_TDONE + (b & (QH_DREP - 1)) * QH_DSTRIDE, a.nd, a.err, a.epoch))
         fail = 1;
     __syncthreads();
-    QH_TS(2);
     if (!fail) {
         for (int spins = 0;; spins++) {
             bool stale = false;
@@ -944,7 +914,6 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
         }
     }
     __syncthreads();
-    QH_TS(3);
     if (u == 0)
         for (int r = t; r < k; r += QH_THREADS) a.d[r] = dl[r];
     float acc = 0.0f;
@@ -966,10 +935,6 @@ __global__ void __launch_bounds__(QH_THREADS) k_hc_decode(QhArgs a)
         for (int q = 0; q < S; q++) mix = mix + mixv[t * S + q];
         a.x[i0 + t] = mix / (float)S;
     }
-    QH_TS(4);
-#ifdef QH_TRACE
-    if (t == 0) qh_trace[blockIdx.x * 8 + 5] = __builtin_readcyclecounter();
-#endif
 }
 
 extern "C" size_t qwk_hc_decode_tag_words(void) { return QH_TAG_WORDS; }

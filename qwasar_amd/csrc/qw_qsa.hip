@@ -240,27 +240,6 @@ __device__ __forceinline__ uint32_t qs_scan(uint32_t v, uint32_t *wt, uint32_t *
     return r;
 }
 
-// Built with -DQS_TRACE, thread 0 of each selection workgroup stamps the
-// device wall clock (100 MHz) at its phases into qs_trace[row][slot].
-#ifdef QS_TRACE
-__device__ unsigned long long qs_trace[64 * 16];
-#define QS_TS(slot) do { if (threadIdx.x == 0 && blockIdx.x < 64) qs_trace[blockIdx.x * 16 + (slot)] = wall_clock64(); } while (0)
-extern "C" int qs_trace_read(unsigned long long *dst)
-{
-    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(qs_trace), sizeof(qs_trace));
-}
-__device__ unsigned long long qa_trace[1024 * 16];
-#define QA_TS(slot) do { if (threadIdx.x == 0 && blockIdx.x < 1024) qa_trace[blockIdx.x * 16 + (slot)] = wall_clock64(); } while (0)
-#define QA_TSV(slot, v) do { if (threadIdx.x == 0 && blockIdx.x < 1024) qa_trace[blockIdx.x * 16 + (slot)] = (v) == 0x12345 ? 0 : wall_clock64(); } while (0)
-extern "C" int qa_trace_read(unsigned long long *dst)
-{
-    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(qa_trace), sizeof(qa_trace));
-}
-#else
-#define QS_TS(slot) do { } while (0)
-#define QA_TS(slot) do { } while (0)
-#define QA_TSV(slot, v) do { } while (0)
-#endif
 
 #define QS_SEL_KREG 8      // keys a thread keeps in registers (up to 8192 blocks)
 
@@ -313,7 +292,6 @@ __global__ void __launch_bounds__(QS_SEL_THREADS) k_qsa_select(uint8_t *__restri
     const int per = (nb + QS_SEL_THREADS - 1) / QS_SEL_THREADS;
     const int lo = min(tid * per, nb), hi = min(lo + per, nb);
     const bool in_regs = per <= QS_SEL_KREG;
-    QS_TS(0);
     // every load of the run issued before the first use (in-range addresses
     // for the lanes past the run, whose keys are then dropped)
     uint32_t kr[QS_SEL_KREG];
@@ -335,17 +313,12 @@ __global__ void __launch_bounds__(QS_SEL_THREADS) k_qsa_select(uint8_t *__restri
 #pragma unroll
         for (int i = 0; i < QS_SEL_KREG; i++) kr[i] = 0u;
     }
-#ifdef QS_TRACE
-    if (threadIdx.x == 0 && blockIdx.x < 64) qs_trace[blockIdx.x * 16 + 12] = kr[0] == 0x12345u ? 0 : wall_clock64();
-#endif
     uint4 *h0 = reinterpret_cast<uint4 *>(&hist[0][0][0]);
     h0[tid] = make_uint4(0u, 0u, 0u, 0u);   // 16 x 256 words: one uint4 a thread
 
     uint32_t S = 0, mn = 0xFFFFFFFFu, mx = 0u;
     QS_RUN(if (k) { S++; mn = min(mn, k); mx = max(mx, k); })
-    QS_TS(13);
     qs_reduce3(S, mn, mx, wt3);
-    QS_TS(1);
     const uint32_t take = min((uint32_t)max(block_topk, 0), S);
     // blocks taken: key > T, then the first `need` blocks whose key equals T
     uint32_t T = 0u, need = 0u;
@@ -357,12 +330,11 @@ __global__ void __launch_bounds__(QS_SEL_THREADS) k_qsa_select(uint8_t *__restri
         // the range's top bit, so even scores that share their leading bits
         // spread over the bins.  A pass whose bin holds exactly the blocks
         // still needed ends the search: the bin's lowest key bounds the take.
-        QS_TS(2);
         const uint32_t range = mx - mn;
         const int nbits = range ? 32 - __builtin_clz(range) : 0;
         uint32_t prefix = 0;
         bool exact = false;
-        int prev = 32, shift = nbits > 8 ? nbits - 8 : 0, cur = 0, pass = 0;
+        int prev = 32, shift = nbits > 8 ? nbits - 8 : 0, cur = 0;
         need = take;
         while (true) {
             const uint32_t bmask = prev - shift >= 32 ? 0xFFFFFFFFu : ((1u << (prev - shift)) - 1u);
@@ -405,7 +377,6 @@ __global__ void __launch_bounds__(QS_SEL_THREADS) k_qsa_select(uint8_t *__restri
             prefix |= sh_bin << shift;
             need = sh_need;
             exact = sh_exact != 0u;
-            QS_TS(3 + min(pass++, 4));
             if (exact || shift == 0) break;
             prev = shift;
             shift = shift > 8 ? shift - 8 : 0;
@@ -446,10 +417,8 @@ __global__ void __launch_bounds__(QS_SEL_THREADS) k_qsa_select(uint8_t *__restri
     } else {
         for (int b = lo; b < hi; b++) mine += sel[b];
     }
-    QS_TS(8);
     const uint32_t first = qs_scan(mine, wt, &sh_total);   // its barriers publish sel
     const uint32_t n_sel = sh_total;
-    QS_TS(9);
     uint32_t *lr = list + (size_t)r * (1 + cap);
     uint32_t at = 1 + first * ratio;
     if (in_regs) {
@@ -467,7 +436,6 @@ __global__ void __launch_bounds__(QS_SEL_THREADS) k_qsa_select(uint8_t *__restri
         for (int t = nb * ratio; t < n_keys; t++) lr[1 + n++] = (uint32_t)t;
         lr[0] = n;
     }
-    QS_TS(10);
     uint8_t *mr = mask + (size_t)r * max_ctx;
     int t0 = 0;
     if (ratio == 4 && (reinterpret_cast<uintptr_t>(mr) & 15) == 0) {
@@ -481,7 +449,6 @@ __global__ void __launch_bounds__(QS_SEL_THREADS) k_qsa_select(uint8_t *__restri
         t0 = n4 * 16;
     }
     for (int t = t0 + tid; t < n_keys; t += QS_SEL_THREADS) mr[t] = t >= nb * ratio ? 1 : sel[t / ratio];
-    QS_TS(11);
 }
 #undef QS_RUN
 
@@ -524,7 +491,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     const int split = blockIdx.x % nsplit, rk = blockIdx.x / nsplit;
     const int row = rk / kv_heads, kvh = rk % kv_heads;
     const uint32_t *lr = list + (size_t)row * (1 + cap);
-    QA_TS(0);
     // the splits divide the list's capacity, so a split knows its range
     // before the list's length arrives: its first pass's entries are
     // requested with the length (entries past the length are not positions
@@ -540,7 +506,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
     };
     const int n_sel = (int)lr[0];
     if (j_lo < j_cap) load_list(j_lo);
-    QA_TSV(1, n_sel);
     const int j_hi = min(j_cap, n_sel);
     const float4 *qp = reinterpret_cast<const float4 *>(q + ((size_t)row * q_heads + (size_t)kvh * G) * QA_D);
     const float sl2 = scale * QA_LOG2E;   // scores in log2 units: weights are 2^(s - max)
@@ -599,7 +564,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
 #pragma unroll
         for (int g = 0; g < G; g++) sg[g] = 0.0f;
         if (valid) {
-            QA_TSV(2, kv[0].x);
 #pragma unroll
             for (int c = 0; c < 4; c++) {
                 const uint32_t w[4] = { kv[c].x, kv[c].y, kv[c].z, kv[c].w };
@@ -621,7 +585,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
                 }
             }
         }
-        QA_TS(3);
         // per head: the wave's maximum over its positions (lane bits 3-5),
         // the online rescale, the weights (into this wave's slice of ps) and
         // their sum in a fixed xor tree
@@ -642,11 +605,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[g][i] *= rs;
         }
-        QA_TS(7);
         // values: lane dims 4l..4l+3 of the wave's positions (their rows
         // were requested with the keys); the weights come back from the
         // wave's own slice of ps (its writes above, in program order)
-        QA_TSV(8, vv[0].x);
 #pragma unroll
         for (int i = 0; i < QA_P / 4; i++) {
             if (i < nj) {
@@ -662,9 +623,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
                 }
             }
         }
-        QA_TSV(9, acc[0][0]);
     }
-    QA_TS(4);
     // the four waves' states meet: the common maximum, each wave's factor,
     // the sums (w0 + w1) + (w2 + w3), and the outputs in the same tree
     // through wbuf and the query array (no longer read)
@@ -710,7 +669,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
             for (int i = 0; i < 4; i++) bufA[g * QA_D + 4 * lane + i] = acc[g][i];
     }
     __syncthreads();
-    QA_TS(5);
     if (wave != 0) return;
     if (nsplit == 1) {
         // the gate rows requested together, before the first is used

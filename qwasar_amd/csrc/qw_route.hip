@@ -439,9 +439,7 @@ __global__ __launch_bounds__(QW_DW_THREADS) void k_dmat_wide(float *__restrict__
 #define QW_DF_WAVES 8
 #define QW_DF_MAXR 8
 #define QW_DF_PAD 68
-#ifndef QW_DF_TPG
 #define QW_DF_TPG 2      // token rows a workgroup
-#endif
 __global__ __launch_bounds__(QW_DF_WAVES * 64) void k_dmat_few(float *__restrict__ y, float *__restrict__ g,
                                                                const float *__restrict__ x,
                                                                const uint16_t *__restrict__ w,
