@@ -29,6 +29,7 @@ the reference's own CPU path restated; see oracle/).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -63,15 +64,27 @@ def decode_bytes(c):
     }
 
 
+PROFILE_JSON = os.path.join(ROOT, "profiles", "k_decode1_config1.json")
+
+
+def _profile_figures():
+    try:
+        with open(PROFILE_JSON) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
+
+
 def measured_traffic(kernel):
     """HBM bytes per dispatch of `kernel` (fetch + write) from the committed
     rocprofv3 counter passes, or None when no summary covers it."""
-    path = os.path.join(ROOT, "profiles", "k_decode_fused_config1_traffic.json")
-    try:
-        with open(path) as f:
-            return json.load(f)["bytes_per_dispatch"].get(kernel)
-    except (OSError, ValueError, KeyError):
-        return None
+    return _profile_figures().get("bytes_per_dispatch", {}).get(kernel)
+
+
+def profiled_kernel_us(kernel):
+    """`kernel`'s average duration in the committed rocprofv3 kernel trace of
+    the headline decode, or None."""
+    return _profile_figures().get("avg_us", {}).get(kernel)
 
 
 def prefill_flops(c, rows):
@@ -108,8 +121,11 @@ def select_cold_pool(gpu, lb, cand_x, K):
     return np.ascontiguousarray(cand_x[chosen]), ids[chosen]
 
 
-def time_decode(gpu, lb, xpool, steps, warmup, profile):
-    """Returns ms for `steps` decode steps, bracketed by HIP events (marks)."""
+def time_decode(gpu, lb, xpool, steps, warmup, mode):
+    """Times `steps` decode steps after `warmup` untimed ones.  mode "region":
+    HIP events at the region's two ends only; "steps": an event after every
+    step as well (per-step durations, for the median); "kernels": events
+    around every kernel launch as well (the decode kernel's own time)."""
     L = lb.L
     B = gpu.Buf
     xb = B.of(xpool)
@@ -123,18 +139,89 @@ def time_decode(gpu, lb, xpool, steps, warmup, profile):
     gpu.qw_prof_set_enabled(True)
     gpu.qw_cmd_free(c)
     c = gpu.qw_cmd_begin()                       # records the region's start event
-    if not profile:
-        gpu.qw_prof_set_enabled(False)           # no per-kernel events inside the region
+    if mode == "steps":
+        gpu.qw_cmd_mark(c, b"decode start")
+    gpu.qw_prof_set_enabled(mode == "kernels")   # per-kernel events only when asked
     for s in range(steps):
         gpu.qw_op_moe_layer(c, ob.ref(), ib.ref(), wb.ref(), xb.ref(((warmup + s) % POOL) * row), lb.desc, 1)
+        if mode == "steps":
+            gpu.qw_prof_set_enabled(True)
+            gpu.qw_cmd_mark(c, b"decode step")
+            gpu.qw_prof_set_enabled(False)
     gpu.qw_prof_set_enabled(True)
     gpu.qw_cmd_mark(c, b"decode region")
     gpu.run(c, "decode")
     gpu.qw_prof_set_enabled(False)
-    res = {"region": gpu.qw_prof_ms(b"decode region", None),
+    res = {"region": gpu.qw_prof_ms(b"decode region", None) if mode != "steps" else None,
            "fused": gpu.qw_prof_ms(b"moe decode", None)}
+    if mode == "steps":
+        buf = (ctypes.c_float * steps)()
+        n = gpu.qw_prof_mark_times(b"decode step", buf, steps)
+        res["per_step"] = np.array(buf[:n], np.float64)
     gpu.qw_prof_reset()
     return res
+
+
+def hbm_ceiling(gpu, lb, reps=12):
+    """The box's measured HBM read ceiling, by the read probe (every load
+    independent, 16 bytes a lane, non-temporal): (a) one 2 GiB stream, past
+    the 256 MB Infinity Cache; (b) ten experts' gate/up/down banks, the
+    decode's routed bytes, read cold: launch r reads experts 10 s .. 10 s + 9
+    for s = r mod (E / 10), so every set was last read E / 10 launches ago
+    (1.35 GB of other experts in between).  Medians over `reps` launches at
+    the best of a few piece sizes (a workgroup a piece)."""
+    L = lb.L
+    B = gpu.Buf
+    out = {}
+    big = B(2 << 30)
+    best = None
+    for blocks in (16384, 65536, 262144):      # piece bytes, one workgroup each
+        ms = (ctypes.c_float * reps)()
+        assert gpu.qw_probe_read((gpu.qw_ref * 1)(big.ref()), (ctypes.c_uint64 * 1)(2 << 30), 1, 1, reps,
+                                 blocks, ms)
+        med = float(np.median(np.array(ms[1:], np.float64)))
+        if best is None or med < best[1]:
+            best = (blocks, med)
+    big.free()
+    out["stream_2gib"] = {"gbs": round((2 << 30) / (best[1] * 1e-3) / 1e9, 1), "ms": round(best[1], 4),
+                          "piece_bytes": best[0]}
+    I, H, G, K = L.I, L.H, L.group, L.K
+    q = lb.q
+    per = []          # (buffer, byte offset, bytes) of one expert, in bank order
+    for e in range(L.E):
+        segs = []
+        if L.split:
+            for nm in ("gate", "up"):
+                segs += [(q[nm].w, e * I * H // 2, I * H // 2), (q[nm].s, e * I * (H // G) * 2, I * (H // G) * 2),
+                         (q[nm].b, e * I * (H // G) * 2, I * (H // G) * 2)]
+        else:
+            nm = "gate_up"
+            segs += [(q[nm].w, e * 2 * I * H // 2, 2 * I * H // 2),
+                     (q[nm].s, e * 2 * I * (H // G) * 2, 2 * I * (H // G) * 2),
+                     (q[nm].b, e * 2 * I * (H // G) * 2, 2 * I * (H // G) * 2)]
+        segs += [(q["down"].w, e * H * I // 2, H * I // 2), (q["down"].s, e * H * (I // G) * 2, H * (I // G) * 2),
+                 (q["down"].b, e * H * (I // G) * 2, H * (I // G) * 2)]
+        per.append(segs)
+    nsets, nseg = L.E // K, K * len(per[0])
+    refs = (gpu.qw_ref * (nsets * nseg))()
+    nbytes = (ctypes.c_uint64 * (nsets * nseg))()
+    for s_ in range(nsets):
+        for k in range(K):
+            for i, (buf, off, n) in enumerate(per[s_ * K + k]):
+                refs[s_ * nseg + k * len(per[0]) + i] = buf.ref(off)
+                nbytes[s_ * nseg + k * len(per[0]) + i] = n
+    set_bytes = sum(n for _, _, n in per[0]) * K
+    best = None
+    r2 = 2 * nsets
+    for blocks in (4096, 8192, 16384, 32768):  # piece bytes, one workgroup each
+        ms = (ctypes.c_float * r2)()
+        assert gpu.qw_probe_read(refs, nbytes, nsets, nseg, r2, blocks, ms)
+        med = float(np.median(np.array(ms[nsets:], np.float64)))    # the second cycle: every set cold
+        if best is None or med < best[1]:
+            best = (blocks, med)
+    out["ten_experts_cold"] = {"bytes": int(set_bytes), "us": round(best[1] * 1e3, 2),
+                               "gbs": round(set_bytes / (best[1] * 1e-3) / 1e9, 1), "piece_bytes": best[0]}
+    return out
 
 
 def time_prefill(gpu, lb, x, reps):
@@ -163,7 +250,7 @@ def time_prefill(gpu, lb, x, reps):
     return ms, int(counts.max()), int((counts > 0).sum())
 
 
-def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444):
+def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444, cpu_seconds=0.0):
     """`nlayers` layers of config 1's shape (weights written
     on the device), joined by the residual bf16 RMS norm; one `rows`-token
     prefill, then `steps` decode steps, each fed a fresh N(0, 1) token."""
@@ -220,6 +307,9 @@ def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444):
     gpu.qw_prof_set_enabled(False)
     gpu.qw_prof_reset()
     wbytes = sum(L.weight_bytes() for L in layers)
+    cpu = None
+    if cpu_seconds > 0:
+        cpu = stack_cpu_sample(layers[0], rows, cpu_seconds, nlayers, seed)
     st.free()
     for L in layers:
         L.free()
@@ -234,9 +324,39 @@ def bench_stack(gpu, nlayers, rows, steps, warmup, seed=4444):
                         "mfma_util": round(fl / (pf_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
             "decode": {"steps": steps, "us_per_token": round(us_tok, 2), "us_per_token_layer": round(us_tl, 3),
                        "routed_hbm_frac": round(routed / (us_tl * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+            "cpu": cpu,
             "includes": "per layer: the MoE block and the residual bf16 RMS norm (at decode folded into "
                         "the layer's one launch, qw_op_moe_layer_residual); decode steps include writing "
                         "the fresh token on the device and the closing residual step"}
+
+
+def stack_cpu_sample(layer, rows, seconds, nlayers, seed):
+    """The oracle on config 4's layer 0 (its weights read back from the
+    device): decode tokens one at a time, then prefill rows 8 at a time, each
+    for about `seconds`, every pass the MoE block and the residual bf16 RMS
+    norm as the stack runs them; per-token-layer time scaled by the stack's
+    `nlayers` layers."""
+    from oracle import ref
+    from qwasar_amd import synth
+    L = layer.host()
+    x = synth.make_x(seed + 17, 64, L.H, name="stack.cpu")
+
+    def one(xs):
+        y, _, _ = ref.moe_forward(L, xs)
+        ref.rms_norm(xs + y)
+
+    res = {}
+    for name, per in (("decode", 1), ("prefill", 8)):
+        n, t0 = 0, time.perf_counter()
+        while (n == 0 or time.perf_counter() - t0 < seconds) and (n + 1) * per <= x.shape[0]:
+            one(x[n * per:(n + 1) * per])
+            n += 1
+        t = (time.perf_counter() - t0) / (n * per)      # seconds a token-layer
+        res[name] = {"tokens_per_s": round(1.0 / (t * nlayers), 3), "us_per_token_layer": round(t * 1e6, 1),
+                     "sample": f"{n * per} tokens through layer 0 ({per} a call), scaled by {nlayers} layers"}
+    res["kind"] = "port"
+    res["cores"] = 1
+    return res
 
 
 def bench_hc(gpu, steps, H=3072, S=4, k=320, G=64, pool=96, prefill_rows=2048, seed=777):
@@ -605,18 +725,6 @@ def cpu_sample(L, x, seconds, rows_per_call):
     return (time.perf_counter() - t0) / n, n
 
 
-def calib_copy(nbytes):
-    """A plain device copy of known size, for scaling rocprofv3's FETCH_SIZE /
-    WRITE_SIZE counters to bytes."""
-    import torch
-    a = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
-    b = torch.empty_like(a)
-    for _ in range(3):
-        b.copy_(a)
-    torch.cuda.synchronize()
-    print(json.dumps({"calib_copy_bytes": nbytes}))
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -628,23 +736,14 @@ def main():
     ap.add_argument("--no-config4", action="store_true", help="skip the 48-layer stack (config 4)")
     ap.add_argument("--config4-only", action="store_true", help="run only the 48-layer stack and print it")
     ap.add_argument("--no-hc", action="store_true", help="skip the hyper-connection mixer")
-    ap.add_argument("--hc-only", action="store_true", help="run only the hyper-connection mixer and print it")
     ap.add_argument("--no-sparse", action="store_true", help="skip QSA and the gated DeltaNet")
-    ap.add_argument("--sparse-only", action="store_true", help="run only QSA and the gated DeltaNet and print them")
+    ap.add_argument("--no-ceiling", action="store_true", help="skip the measured HBM read ceiling")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--calib-copy", type=int, default=0, help="bytes: run only the copy calibration")
-    ap.add_argument("--decode-only-steps", type=int, default=0,
-                    help="profiling aid: only run this many decode steps after setup")
-    ap.add_argument("--prefill-only-rows", type=int, default=0,
-                    help="profiling aid: only time prefill of this many uniform-routed rows")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)
         sys.exit(2)
-    if args.calib_copy:
-        calib_copy(args.calib_copy)
-        return
 
     from qwasar_amd import gpu, synth
     gpu.init()
@@ -655,42 +754,28 @@ def main():
     cand = synth.make_x(seed, 2048, L.H, name="bench.candidates")
     xpool, pool_ids = select_cold_pool(gpu, lb, cand, L.K)
 
-    if args.hc_only:
-        print(json.dumps({"hc_mixer": bench_hc(gpu, 200)}), flush=True)
-        return
-    if args.sparse_only:
-        print(json.dumps({"sparse": bench_sparse(gpu)}), flush=True)
-        return
-    if args.config4_only:
-        print(json.dumps({"config4": bench_stack(gpu, 48, 2048, 256, 4)}),
-              flush=True)
-        return
-    if args.decode_only_steps:
-        time_decode(gpu, lb, xpool, args.decode_only_steps, 0, False)
-        return
-    if args.prefill_only_rows:
-        rows = args.prefill_only_rows
-        x = synth.make_x(seed + rows, rows, L.H, name=f"bench.prefill{rows}")
-        ms, _, _ = time_prefill(gpu, lb, x, reps=5)
-        print(json.dumps({"prefill_rows": rows, "ms": round(ms, 3)}), flush=True)
-        return
-
     nb = decode_bytes(cfg)
-    dec = time_decode(gpu, lb, xpool, args.steps, args.warmup, profile=False)
-    us_tok = dec["region"] * 1000.0 / args.steps
-    # the one decode launch, timed by its own dispatch stamps
-    brk = time_decode(gpu, lb, xpool, args.steps, 0, profile=True)
+    # the K timed steps, HIP events at the region's ends only: the value
+    dec = time_decode(gpu, lb, xpool, args.steps, args.warmup, "region")
+    us_mean = dec["region"] * 1000.0 / args.steps
+    # the same count of steps with an event after each, for their median and
+    # spread (each event adds a gap of its own to its step)
+    per = time_decode(gpu, lb, xpool, args.steps, 0, "steps")["per_step"] * 1000.0
+    # the same steps with events around every launch: the decode kernel's own duration
+    brk = time_decode(gpu, lb, xpool, args.steps, 0, "kernels")
     k_us = brk["fused"] * 1000.0 / args.steps
     roof_gbs = nb["all"] / (k_us * 1e-6) / 1e9
+    prof_us = profiled_kernel_us("k_decode1")
+    ceiling = None if args.no_ceiling else hbm_ceiling(gpu, lb)
 
     out = {
         "metric": "moe_layer_decode_us_per_token",
-        "value": round(us_tok, 3),
+        "value": round(us_mean, 3),
         "unit": "us/token",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(us_tok / 1000.0, 6),
+        "ms_per_step": round(us_mean / 1000.0, 6),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -701,17 +786,26 @@ def main():
                    "group": cfg["group"], "tokens_per_step": 1, "token_pool": POOL,
                    "cold_window": COLD_WINDOW},
         "decode": {
-            "us_per_token": round(us_tok, 3),
+            "us_per_token": round(us_mean, 3),
+            "evented_steps": {"n": int(per.size), "median_us": round(float(np.median(per)), 3),
+                              "p10_us": round(float(np.percentile(per, 10)), 3),
+                              "p90_us": round(float(np.percentile(per, 90)), 3),
+                              "note": "an event after every step; each adds its own gap"},
             "routed_bytes": nb["routed"], "all_bytes": nb["all"],
-            "routed_hbm_gbs": round(nb["routed"] / (us_tok * 1e-6) / 1e9, 1),
-            "routed_hbm_frac": round(nb["routed"] / (us_tok * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "all_hbm_gbs": round(nb["all"] / (us_tok * 1e-6) / 1e9, 1),
+            "routed_hbm_gbs": round(nb["routed"] / (us_mean * 1e-6) / 1e9, 1),
+            "routed_hbm_frac": round(nb["routed"] / (us_mean * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "all_hbm_gbs": round(nb["all"] / (us_mean * 1e-6) / 1e9, 1),
             "kernel_us": round(k_us, 3),
         },
-        "roofline": {"bound": "hbm", "kernel": "k_decode_fused", "achieved": round(roof_gbs, 1),
+        "roofline": {"bound": "hbm", "kernel": "k_decode1", "achieved": round(roof_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(roof_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic("k_decode_fused"),
-                     "algorithmic_bytes": nb["all"]},
+                     "traffic": measured_traffic("k_decode1"),
+                     "algorithmic_bytes": nb["all"],
+                     "kernel_us_live": round(k_us, 3),
+                     "kernel_us_profile": prof_us,
+                     "frac_from_profile": (round(nb["all"] / (prof_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                                           if prof_us else None),
+                     "measured_ceiling": ceiling},
     }
 
     c2, c2_router, c2_x = None, None, None
@@ -732,7 +826,9 @@ def main():
         lb3 = _LB3()
         lb3.L, lb3.desc = L, d3
         for name, rows, lbx, const0 in (("config3_zipf_512", 512, lb3, True),
-                                        ("chunk_2048_uniform", 2048, lb, False)):
+                                        ("chunk_2048_uniform", 2048, lb, False),
+                                        ("chunk_256_uniform", 256, lb, False),
+                                        ("chunk_1024_uniform", 1024, lb, False)):
             x = synth.make_x(seed + rows, rows, L.H, name=f"bench.prefill{rows}", const_col0=const0)
             if rows == 512:
                 x3 = x
@@ -753,12 +849,17 @@ def main():
                 "hbm_frac_of_weight_floor": round(ch["weight_read_floor_ms"] / ch["ms"], 4),
                 "config3_rows": z["rows"], "config3_ms": z["ms"], "config3_tokens_per_s": z["tokens_per_s"],
                 "config3_mfma_util": z["mfma_util"], "config3_hottest_expert_pairs": z["hottest_expert_pairs"],
-                "config3_experts_touched": z["experts_touched"]}
+                "config3_experts_touched": z["experts_touched"],
+                # the grouped layer at the chunk sizes the reference's own grouped-experts
+                # figures are quoted at (256, 1024, 2048 rows; uniform routing)
+                "chunk_sweep": {str(pf[k]["rows"]): {"ms": pf[k]["ms"], "tokens_per_s": pf[k]["tokens_per_s"],
+                                                     "mfma_util": pf[k]["mfma_util"]}
+                                for k in ("chunk_256_uniform", "chunk_1024_uniform", "chunk_2048_uniform")}}
         pf = flat
         out["prefill"] = pf
 
     if not args.no_config4:
-        out["config4"] = bench_stack(gpu, 48, 2048, 256, 4)
+        out["config4"] = bench_stack(gpu, 48, 2048, 256, 4, cpu_seconds=0.0 if args.no_cpu else 3.0)
     if not args.no_hc:
         out["hc_mixer"] = bench_hc(gpu, 200)
     if not args.no_sparse:
@@ -767,7 +868,8 @@ def main():
     if not args.no_cpu:
         # the oracle (scalar C, one thread) on bounded samples of the same
         # workloads: config 1 (the headline's tokens), config 0, config 2 (the
-        # first timed batches) and config 3 (its first tokens)
+        # first timed batches), config 3 (its first tokens) and config 4 (layer
+        # 0 of the stack, scaled by its 48 layers)
         import dataclasses
         s1, n1 = cpu_sample(L, xpool, args.cpu_seconds, 1)
         by = {}
@@ -783,6 +885,8 @@ def main():
             L3 = dataclasses.replace(L, router=r3)
             s3, n3 = cpu_sample(L3, x3, 3.0, 8)
             by["config3"] = {"tokens_per_s": round(8 / s3, 2), "sample": f"the first {8 * n3} of its 512 tokens"}
+        if out.get("config4", {}).get("cpu"):
+            by["config4"] = out["config4"]["cpu"]
         out["cpu_baseline"] = {"value": round(s1 * 1e6, 1), "unit": "us/token", "cores": 1, "kind": "port",
                                "sample": f"{n1} decode tokens of config 1 through oracle/moe_ref.c "
                                          "(scalar C, -O2, one thread), same weights and tokens",

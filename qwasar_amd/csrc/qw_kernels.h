@@ -272,6 +272,12 @@ int qwk_attn_masked(hipStream_t s, float *out, const float *gate, const float *q
                     int head_dim, int max_ctx, float scale, int cap, void *work, size_t work_bytes);
 size_t qwk_attn_masked_work_bytes(int rows, int q_heads, int kv_heads, int cap);
 
+/* Read-bandwidth probe (measurement only): launch r reads set r % nsets of
+ * nseg 16-byte-aligned ranges once, one workgroup a piece of at most
+ * piece_bytes; ms[r] its event-timed duration. */
+int qwk_read_probe(const void *const *ptr, const uint64_t *bytes, int nsets, int nseg, int reps,
+                   uint64_t piece_bytes, float *ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -95,7 +95,14 @@ static struct {
 static struct { const char *label; double ms; int64_t count; } P[QW_PROF_MAX];
 static int NP;
 
+/* every mark's own duration, in completion order, since the last reset (the
+ * first QW_PROF_KEEP): what a median over steps is taken from */
+#define QW_PROF_KEEP 8192
+static struct { const char *label; float ms; } PK[QW_PROF_KEEP];
+static int NPK;
+
 static void prof_add(const char *label, double ms) {
+    if (NPK < QW_PROF_KEEP) { PK[NPK].label = label; PK[NPK].ms = (float)ms; NPK++; }
     for (int i = 0; i < NP; i++)
         if (P[i].label == label || !strcmp(P[i].label, label)) { P[i].ms += ms; P[i].count++; return; }
     if (NP < QW_PROF_MAX) { P[NP].label = label; P[NP].ms = ms; P[NP].count = 1; NP++; }
@@ -103,7 +110,16 @@ static void prof_add(const char *label, double ms) {
 
 bool qw_prof_enabled(void) { return G.prof != 0; }
 void qw_prof_set_enabled(bool on) { G.prof = on ? 1 : 0; }
-void qw_prof_reset(void) { NP = 0; }
+void qw_prof_reset(void) { NP = 0; NPK = 0; }
+
+/* Not in the reference interface: the individual durations of `label`'s
+ * marks since the last reset, oldest first, up to cap; returns how many. */
+int32_t qw_prof_mark_times(const char *label, float *ms, int32_t cap) {
+    int32_t n = 0;
+    for (int i = 0; i < NPK && n < cap; i++)
+        if (PK[i].label == label || !strcmp(PK[i].label, label)) ms[n++] = PK[i].ms;
+    return n;
+}
 
 double qw_prof_ms(const char *label, int64_t *count) {
     for (int i = 0; i < NP; i++)
@@ -1271,4 +1287,30 @@ void qw_op_attn_masked(qw_cmd c, qw_ref out, qw_ref q, qw_ref kcache, qw_ref vca
     const qw_ref none = { 0 };
     qw_op_attn_masked_gated(c, out, none, q, kcache, vcache, list, rows, q_heads, kv_heads, head_dim, max_ctx,
                             base_pos, scale, block_topk, ratio);
+}
+
+/* ---- measurement probe ---------------------------------------------------------
+ * Not part of the reference interface: the HBM read ceiling the kernels are
+ * measured against.  Launch r reads set (r % nsets) of nseg ranges
+ * (segs[s * nseg + i], bytes[...]: 16-byte multiples at 16-byte-aligned
+ * offsets) once, one workgroup a piece of at most piece_bytes, and ms[r] is
+ * its duration.  The bytes' values are not used, so
+ * host mirrors are not consulted.  Returns false on bad arguments or a HIP
+ * error. */
+bool qw_probe_read(const qw_ref *segs, const uint64_t *bytes, int32_t nsets, int32_t nseg, int32_t reps,
+                   uint64_t piece_bytes, float *ms) {
+    if (!G.ready || !segs || !bytes || !ms || nsets < 1 || nseg < 1 || reps < 1) return false;
+    const size_t n = (size_t)nsets * (size_t)nseg;
+    const void **p = (const void **)calloc(n, sizeof(void *));
+    if (!p) return false;
+    bool ok = true;
+    for (size_t i = 0; i < n && ok; i++) {
+        p[i] = dp(segs[i]);
+        ok = p[i] && segs[i].off + bytes[i] <= segs[i].buf->len;
+    }
+    /* (the library's queued work first, so that none of it runs under the probe) */
+    if (ok) ok = hipStreamSynchronize(G.stream) == hipSuccess;
+    if (ok) ok = qwk_read_probe(p, bytes, nsets, nseg, reps, piece_bytes, ms) == 0;
+    free(p);
+    return ok;
 }

@@ -94,6 +94,9 @@ _sig("qw_cmd_mark", None, _P, C.c_char_p)
 _sig("qw_prof_reset", None)
 _sig("qw_prof_set_enabled", None, _B)
 _sig("qw_prof_ms", C.c_double, C.c_char_p, C.POINTER(C.c_int64))
+_sig("qw_prof_mark_times", _I, C.c_char_p, C.POINTER(C.c_float), _I)
+# measurement probe (not a reference entry point): HBM read ceiling
+_sig("qw_probe_read", _B, C.POINTER(qw_ref), C.POINTER(C.c_uint64), _I, _I, _I, C.c_uint64, C.POINTER(C.c_float))
 _sig("qw_debug_decode_handoff_fail", _B)
 
 _sig("qw_op_qmat_q4", None, _P, _R, _R, _R, _R, _R, _I, _I, _I, _I)
