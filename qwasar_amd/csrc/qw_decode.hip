@@ -696,7 +696,7 @@ extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, flo
                                      (const float *)(S + L.xF), b.perm, b.tiles, a.umax + 1, g0, u0,           \
                                      (long)(M->split ? 1 : 2) * M->I * (M->H / 8),                             \
                                      (long)(M->split ? 1 : 2) * M->I * (M->H / G), M->H, M->I, M->K, 0, G, 1, \
-                                     0, &xgu);                                                                 \
+                                     0, &xgu, rows);                                                           \
             if (rg) return rg;                                                                                \
             hipLaunchKernelGGL(k_batch_act_q16, dim3((nvu + 255) / 256), dim3(256), 0, s, b);                 \
         } else {                                                                                              \

@@ -139,21 +139,23 @@ struct Gmm16Args {
     int xe, xpairs;
 };
 
-template <int G, bool SWIGLU, bool DENSE, int KC>
-__global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
+template <int G, bool SWIGLU, bool DENSE, int KC, int BM>
+__global__ __launch_bounds__(G16_THREADS, BM == 64 ? 1 : 2) void k_gmm16(Gmm16Args a)
 {
     constexpr int WPL = KC / 32;                         // words (MFMA k steps) per lane per chunk
     constexpr int KPL = WPL * 8;                         // k a lane covers per chunk
     constexpr int NGL = KPL > G ? KPL / G : 1;           // quantisation groups in that span
     constexpr int AST = KC + 8;                          // halfs per A row in LDS (pad: conflict-free reads)
-    constexpr int AU4 = G16_BM * KC / 8 / G16_THREADS;   // uint4 of A a thread moves per chunk
+    constexpr int AU4 = BM * KC / 8 / G16_THREADS;   // uint4 of A a thread moves per chunk
     static_assert(NGL <= 2 && AU4 >= 1 && (WPL == 2 || WPL == 4 || WPL == 8), "chunk shape");
-    static_assert(G16_BM * (KC + 8) < 65536, "LDS offsets of A fit 16 bits");
+    static_assert(BM * (KC + 8) < 65536, "LDS offsets of A fit 16 bits");
     static_assert(G16_THREADS == G16_BN, "a thread per weight row loads the scale / bias blocks");
-    __shared__ __align__(16) _Float16 As[2][G16_BM][AST];
-    __shared__ __align__(16) uint8_t Sb[2][4 * G16_BN * 16];      // scale / bias blocks (below)
-    __shared__ float Fr[G16_BM];
-    __shared__ int srow[G16_BM], drow[G16_BM];
+    __shared__ __align__(16) _Float16 As[2][BM][AST];
+    // scale / bias blocks (below): 4 regions of 16 bytes a row, 2 for 16-row
+    // tiles (whose blocks the host keeps to at most 8 groups of 16-byte runs)
+    __shared__ __align__(16) uint8_t Sb[2][(BM == 64 ? 4 : 2) * G16_BN * 16];
+    __shared__ float Fr[BM];
+    __shared__ int srow[BM], drow[BM];
 
     // Workgroup b runs on XCD b % 8 (round-robin dispatch).  Each XCD takes a
     // contiguous range of tiles, and with r = b / 8 its workgroups walk
@@ -172,7 +174,7 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     // 4), and those, when twice their number fits again, into the tile's row
     // halves.
     const int bid = blockIdx.x, xcd = bid & 7, r = bid >> 3, ngr = (a.nblk + a.nbw - 1) / a.nbw;
-    const int ntl = DENSE ? (a.rows + G16_BM - 1) / G16_BM : a.tiles[0];
+    const int ntl = DENSE ? (a.rows + BM - 1) / BM : a.tiles[0];
     const int tpx = (ntl + 7) / 8;
     const int items = min(max(ntl - xcd * tpx, 0), tpx) * ngr, full = items - items % a.cpx;
     int tl, nb0, nitems, hc = 0, rh = -1;
@@ -182,7 +184,7 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
         nb0 = (r % ngr) * a.nbw;
         nitems = min(a.nbw, a.nblk - nb0);
     } else if (a.nbw == 1) {
-        const int rem = items - full, cs = 4 * rem <= 2 * a.cpx ? 2 : 1, rs = cs == 2 && 4 * rem <= a.cpx ? 2 : 1;
+        const int rem = items - full, cs = 4 * rem <= 2 * a.cpx ? 2 : 1, rs = BM == 64 && cs == 2 && 4 * rem <= a.cpx ? 2 : 1;
         const int per = cs * rs, it = full + (r - full) / per, pc = (r - full) % per;
         if (it >= items) return;
         tl = it / ngr;
@@ -205,9 +207,9 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     constexpr int NT = decltype(ntc)::value, NH = NT / 2, BNT = NT * 16 * (G16_THREADS / 64);
     int expert, first, len;
     if (DENSE) {
-        first = tile * G16_BM;
+        first = tile * BM;
         expert = 0;
-        len = min(G16_BM, a.rows - first);
+        len = min(BM, a.rows - first);
     } else {
         expert = a.tiles[1 + 3 * tile];
         first = a.tiles[2 + 3 * tile];
@@ -216,7 +218,7 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, ln = lane & 15, kg = lane >> 4;
     const int k = a.k, words = k / 8, groups = k / G, nch = k / KC, T = nitems * nch;
     const int gpb = a.gpb, sbc = gpb * G / KC, nbk = groups / gpb;   // chunks a block, blocks an item
-    if (t < G16_BM) {
+    if (t < BM) {
         int sr = -1, dr = -1;
         if (t < len && (rh < 0 || (t >> 5) == rh)) {
             const int p = DENSE ? first + t : a.perm[first + t];
@@ -232,7 +234,7 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     // Loads are buffer loads: a wave-uniform base (a descriptor in SGPRs) and a
     // 32-bit per-lane offset in place of a 64-bit address.
     //
-    // Activations: a chunk is G16_BM rows of KC halfs, LPR 128-byte lines a
+    // Activations: a chunk is BM rows of KC halfs, LPR 128-byte lines a
     // row.  Load i of thread t takes 16 bytes (t % 8) of line
     // i * (threads / 8) + t / 8, so each load instruction of a wave covers 8
     // whole lines (a cache tag per 128 bytes).  Loads go to valid (clamped)
@@ -364,9 +366,9 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
     // barrier that publishes a block leaves them in flight)
     constexpr int NBL = NT * (WPL == 2 ? 1 : WPL / 4);
 
-    g16_f4 acc[4][NT];
+    g16_f4 acc[BM / 16][NT];
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
+    for (int mt = 0; mt < BM / 16; mt++)
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) acc[mt][nt] = g16_f4{0.f, 0.f, 0.f, 0.f};
     uint32_t lo = 0x64006400u, hi = 0x54005400u;
@@ -398,10 +400,10 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
         __builtin_amdgcn_sched_barrier(0);
         if (bstart) fetch_sb(beta + 1, (beta + 1) & 1);
         __builtin_amdgcn_sched_barrier(0);
-        auto lda = [&](int st, g16_h8 (&o)[4]) {
+        auto lda = [&](int st, g16_h8 (&o)[BM / 16]) {
             const int ah = kg * KPL + 8 * st;
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++) o[mt] = *reinterpret_cast<const g16_h8 *>(&As[q][mt * 16 + ln][ah]);
+            for (int mt = 0; mt < BM / 16; mt++) o[mt] = *reinterpret_cast<const g16_h8 *>(&As[q][mt * 16 + ln][ah]);
         };
         auto dqs = [&](int st, g16_h8 (&o)[NT]) {
             const int g = NGL == 1 ? 0 : st * 8 / G;
@@ -412,7 +414,7 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
                 o[nt] = __builtin_bit_cast(g16_h8, g16_u4{d[0], d[1], d[2], d[3]});
             }
         };
-        g16_h8 af[2][4], bf[2][NT];
+        g16_h8 af[2][BM / 16], bf[2][NT];
         lda(0, af[0]);
         dqs(0, bf[0]);
 #pragma unroll
@@ -423,7 +425,7 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
                 dqs(st + 1, bf[cu ^ 1]);
             }
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++)
+            for (int mt = 0; mt < BM / 16; mt++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
                     acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[cu][mt], bf[cu][nt], acc[mt][nt], 0, 0, 0);
@@ -437,7 +439,7 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16(Gmm16Args a)
         if (c == nch - 1) {
             // the item is done: out, y = F acc, with SWIGLU silu(F g) * (F u)
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++)
+            for (int mt = 0; mt < BM / 16; mt++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     const int m = mt * 16 + 4 * kg + e;
@@ -503,14 +505,28 @@ extern "C" int qwk_stage16(hipStream_t s, uint16_t *hb, float *F, const float *x
     return (int)hipGetLastError();
 }
 
-template <int G, int KC>
-static void g16_launch(hipStream_t s, const Gmm16Args &a, int swiglu, int dense, unsigned grid)
+template <int G, int KC, int BM>
+static void g16_launch_bm(hipStream_t s, const Gmm16Args &a, int swiglu, int dense, unsigned grid)
 {
     const dim3 g(grid), b(G16_THREADS);
-    if (swiglu && dense) hipLaunchKernelGGL((k_gmm16<G, true, true, KC>), g, b, 0, s, a);
-    else if (swiglu) hipLaunchKernelGGL((k_gmm16<G, true, false, KC>), g, b, 0, s, a);
-    else if (dense) hipLaunchKernelGGL((k_gmm16<G, false, true, KC>), g, b, 0, s, a);
-    else hipLaunchKernelGGL((k_gmm16<G, false, false, KC>), g, b, 0, s, a);
+    if (swiglu && dense) hipLaunchKernelGGL((k_gmm16<G, true, true, KC, BM>), g, b, 0, s, a);
+    else if (swiglu) hipLaunchKernelGGL((k_gmm16<G, true, false, KC, BM>), g, b, 0, s, a);
+    else if (dense) hipLaunchKernelGGL((k_gmm16<G, false, true, KC, BM>), g, b, 0, s, a);
+    else hipLaunchKernelGGL((k_gmm16<G, false, false, KC, BM>), g, b, 0, s, a);
+}
+// (16-row tiles: grouped products only, the chunks of 256)
+template <int G, int KC>
+static void g16_launch(hipStream_t s, const Gmm16Args &a, int swiglu, int dense, unsigned grid, int bm)
+{
+    if constexpr (KC == 256) {
+        if (bm == 16 && !dense) {
+            const dim3 g(grid), b(G16_THREADS);
+            if (swiglu) hipLaunchKernelGGL((k_gmm16<G, true, false, KC, 16>), g, b, 0, s, a);
+            else hipLaunchKernelGGL((k_gmm16<G, false, false, KC, 16>), g, b, 0, s, a);
+            return;
+        }
+    }
+    g16_launch_bm<G, KC, 64>(s, a, swiglu, dense, grid);
 }
 
 // CUs an XCD: the device's CUs over its 8 XCDs (of the current device, read
@@ -544,10 +560,13 @@ extern "C" int qwk_gmm16_supported(int k, int group, const void *w0, const void 
 extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb, const float *aF,
                          const int32_t *perm, const int32_t *tiles, int max_tiles,
                          qwk_q4 m0, qwk_q4 m1, long ew, long eg, int k, int n, int K, int x_by_pair,
-                         int group, int swiglu, int dense_rows, const qwk_gmm_extra *xb)
+                         int group, int swiglu, int dense_rows, const qwk_gmm_extra *xb, int tile_rows)
 {
     // chunks of 256 where k allows, else 64
     const int kc = k % 256 == 0 ? 256 : 64;
+    // 16-row tiles (two workgroups a CU) where the caller's tiles hold at most
+    // 16 rows and the shapes allow; else 64
+    int bm = tile_rows <= 16 && dense_rows <= 0 && kc == 256 ? 16 : 64;
     if (k < 64 || k % kc || n < 1 || (group != 32 && group != 64 && group != 128) || k % group ||
         ((uintptr_t)ahb & 15u) || ((uintptr_t)m0.w & 15u) || (swiglu && ((uintptr_t)m1.w & 15u)))
         return (int)hipErrorInvalidValue;
@@ -573,12 +592,16 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
         // the largest scale / bias block (groups) that divides a row's groups
         // and ends on a chunk boundary
         const int groups = k / group;
-        a.gpb = 0;
-        for (int g = 16; g >= 1 && !a.gpb; g /= 2)
-            if (groups % g == 0 && (g * group) % kc == 0) a.gpb = g;
+        for (int pass = 0; pass < 2; pass++) {
+            a.gpb = 0;
+            for (int g = bm == 16 ? 8 : 16; g >= 1 && !a.gpb; g /= 2)
+                if (groups % g == 0 && (g * group) % kc == 0) a.gpb = g;
+            if (a.gpb || bm == 64) break;
+            bm = 64;             // (no block of at most 8 groups ends on a chunk boundary)
+        }
         if (!a.gpb) return (int)hipErrorInvalidValue;
     }
-    const int ntiles = dense ? (dense_rows + G16_BM - 1) / G16_BM : max_tiles;
+    const int ntiles = dense ? (dense_rows + bm - 1) / bm : max_tiles;
     if (ntiles <= 0) return 0;
     // column blocks per workgroup: long streams, but enough workgroups to
     // fill the chip (max_tiles bounds the grouped tile count from above)
@@ -591,22 +614,22 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
         while (a.nblk % nbw) nbw--;
         a.nbw = nbw;
     }
-    a.cpx = g16_cus_per_xcd();
+    a.cpx = g16_cus_per_xcd() * (bm == 16 ? 2 : 1);   // workgroups an XCD holds at once
     // r = b / 8 < ngr * ceil(ntiles / 8) covers every XCD's whole items, and
     // cpx * max(nbw, 4) more the pieces of its last round's (fewer than cpx)
     const int ngr = (a.nblk + a.nbw - 1) / a.nbw;
     const unsigned grid = (unsigned)((ngr * ((ntiles + 7) / 8) + a.cpx * (a.nbw > 4 ? a.nbw : 4)) * 8);
     if (kc == 256) {
         switch (group) {
-        case 32: g16_launch<32, 256>(s, a, swiglu, dense, grid); break;
-        case 64: g16_launch<64, 256>(s, a, swiglu, dense, grid); break;
-        default: g16_launch<128, 256>(s, a, swiglu, dense, grid); break;
+        case 32: g16_launch<32, 256>(s, a, swiglu, dense, grid, bm); break;
+        case 64: g16_launch<64, 256>(s, a, swiglu, dense, grid, bm); break;
+        default: g16_launch<128, 256>(s, a, swiglu, dense, grid, bm); break;
         }
     } else {
         switch (group) {
-        case 32: g16_launch<32, 64>(s, a, swiglu, dense, grid); break;
-        case 64: g16_launch<64, 64>(s, a, swiglu, dense, grid); break;
-        default: g16_launch<128, 64>(s, a, swiglu, dense, grid); break;
+        case 32: g16_launch<32, 64>(s, a, swiglu, dense, grid, bm); break;
+        case 64: g16_launch<64, 64>(s, a, swiglu, dense, grid, bm); break;
+        default: g16_launch<128, 64>(s, a, swiglu, dense, grid, bm); break;
         }
     }
     return (int)hipGetLastError();

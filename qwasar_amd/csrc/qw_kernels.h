@@ -98,7 +98,7 @@ int qwk_gmm16_supported(int k, int group, const void *w0, const void *w1);
 int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ah, const float *aF,
               const int32_t *perm, const int32_t *tiles, int max_tiles, qwk_q4 m0, qwk_q4 m1, long ew,
               long eg, int k, int n, int K, int x_by_pair, int group, int swiglu, int dense_rows,
-              const qwk_gmm_extra *xb);
+              const qwk_gmm_extra *xb, int tile_rows);
 
 /* Elementwise. */
 int qwk_swiglu(hipStream_t s, float *y, const float *gate, const float *up, int64_t n);
