@@ -263,8 +263,11 @@ void qw_op_qsa_pool(qw_cmd c, qw_ref pool, qw_ref ikeys, qw_ref k_norm, qw_ref i
 void qw_op_qsa_scores_pooled(qw_cmd c, qw_ref scores, qw_ref qn, qw_ref pool, int32_t rows,
                              int32_t nq, int32_t d, int32_t ratio, int32_t base_pos, int32_t max_blocks);
 /* Selection: the block_topk best complete blocks (score descending, ties to
- * the lower block; a score of -FLT_MAX or below, or NaN, is never taken) and
- * the incomplete tail are visible.  mask U8 [rows, max_ctx] gets 1/0 for
+ * the lower block; a score of -FLT_MAX or below, or NaN, is never taken, as in
+ * the reference's CPU selection, qwasar_flash_cpu.c:395-402; its Metal kernel,
+ * metal/sparse.metal:965-1030, instead orders every float, NaN above +inf and
+ * -inf lowest, and always takes min(block_topk, blocks)) and the incomplete
+ * tail are visible.  mask U8 [rows, max_ctx] gets 1/0 for
  * positions 0..base_pos + r; list U32 [rows, 1 + qw_qsa_list_cap] the count,
  * then the visible positions ascending.  Up to 65536 blocks a row. */
 static inline int32_t qw_qsa_list_cap(int32_t block_topk, int32_t ratio) {

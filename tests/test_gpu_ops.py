@@ -217,6 +217,14 @@ def test_swiglu_bank(gpu, layout):
         act = np.array([ref.lib().qr_silu(float(v)) for v in g[:pairs * k]], np.float32).reshape(pairs, k) \
             * g[pairs * k:].reshape(pairs, k)
     assert rel_l2(actb.read(np.float32, (pairs, k)), act) < 1e-6
+    # the fused product itself against the oracle: pair p's expert idx[p]
+    # (rows idx[p] n .. + n of the bank) applied to the oracle's activation
+    y2h = y2.read(np.float32, (pairs, n))
+    for pr in range(pairs):
+        e = int(idx[pr])
+        want = ref.qmv_q4(act[pr][None], q.w[e * n:(e + 1) * n], q.s[e * n:(e + 1) * n], q.b[e * n:(e + 1) * n],
+                          k, n, 1, G)[0]
+        assert rel_l2(y2h[pr], want) < 1e-5, f"pair {pr} (expert {e}) against the oracle"
 
 
 @pytest.mark.parametrize("count", [1, 2, 3, 4])
@@ -357,9 +365,9 @@ def test_grouped_experts(gpu, G, by_pair):
     assert big > 10, f"expert 0 should span many tiles, got {big}"
     # spot-check rows against the oracle directly
     sel = np.arange(0, pairs, 97)
-    if by_pair:
-        xs = x[sel]
-        want = np.stack([ref.qmv_q4(xs[i][None], q.w[idx[s] * n:(idx[s] + 1) * n],
-                                    q.s[idx[s] * n:(idx[s] + 1) * n], q.b[idx[s] * n:(idx[s] + 1) * n],
-                                    k, n, 1, G)[0] for i, s in enumerate(sel)])
-        assert rel_l2(yg.read(np.float32, (pairs, n))[sel], want) < 1e-3
+    # (A row of pair p: x[p] by pair, else the token's row x[p // K])
+    xs = x[sel] if by_pair else x[sel // K]
+    want = np.stack([ref.qmv_q4(xs[i][None], q.w[idx[s] * n:(idx[s] + 1) * n],
+                                q.s[idx[s] * n:(idx[s] + 1) * n], q.b[idx[s] * n:(idx[s] + 1) * n],
+                                k, n, 1, G)[0] for i, s in enumerate(sel)])
+    assert rel_l2(yg.read(np.float32, (pairs, n))[sel], want) < 1e-3

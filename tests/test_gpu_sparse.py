@@ -162,6 +162,12 @@ def test_qsa_select_edges(gpu):
     s = np.full((1, 64), -np.finfo(np.float32).max, np.float32)
     s[0, [3, 40]] = [1.0, -1e30]
     check_select(gpu, s, 1, ratio, 255, 8, 256, 64)
+    # +inf is the best score; -inf, -NaN and NaN among the rest stay unselected
+    # when the budget exceeds the selectable blocks
+    s = rnd((1, 64), 7)
+    s[0, [5, 9, 20, 33, 50]] = [np.inf, -np.inf, np.nan, -np.nan, np.inf]
+    check_select(gpu, s, 1, ratio, 255, 62, 256, 64)
+    check_select(gpu, s, 1, ratio, 255, 3, 256, 64)
     # the budget covers every block; no complete block at all
     check_select(gpu, rnd((3, 16), 4), 3, ratio, 9, 8, 64, 16)
     check_select(gpu, rnd((3, 16), 5), 3, ratio, 0, 8, 64, 16)
