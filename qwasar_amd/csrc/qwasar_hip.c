@@ -900,7 +900,12 @@ static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const floa
     const int32_t grp = M->split ? M->gate.group : M->gate_up.group;
     const bool fuse = SI == I && M->sh_gate.group == grp && M->sh_up.group == grp && M->sh_down.group == grp;
     const int32_t xr = fuse ? rows : 0, ntot = pairs + xr;
-    const int32_t mt = tiles_for(pairs, E, QW_PF_BM) + (xr + QW_PF_BM - 1) / QW_PF_BM;
+    /* 16-row tiles (two workgroups a CU) where the experts average under 8
+     * pairs, so that 64-row tiles would be mostly idle rows; else 64 (at 8 to
+     * 12 a Zipf-skewed config 3 measured slower with 16: its hottest expert's
+     * ~500 pairs then read its weights 32 times) */
+    const int32_t bm = (int64_t)pairs < (int64_t)8 * E ? 16 : QW_PF_BM;
+    const int32_t mt = tiles_for(pairs, E, bm) + (xr + bm - 1) / bm;
     const int32_t srows = fuse ? 0 : rows;      /* the unfused shared expert's buffers */
     size_t off = 0;
     const size_t o_xh = off;     off += al256((size_t)rows * H * 2);
@@ -936,20 +941,20 @@ static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const floa
     if (!gated) rc = qwk_stage16(s, xh, xF, x, rows, H);
     if (!rc) rc = qwk_dmat_bf16(s, logits, x, dp(M->router), H, E, rows);
     if (!rc) rc = qwk_route(s, idx, w, logits, rows, E, K, M->norm ? 1 : 0);
-    if (!rc) rc = qwk_moe_group(s, perm, tiles, idx, pairs, E, QW_PF_BM, mt, S + o_gw,
+    if (!rc) rc = qwk_moe_group(s, perm, tiles, idx, pairs, E, bm, mt, S + o_gw,
                                 qwk_moe_group_work_bytes(pairs, E), xr);
     if (M->split) {
         if (!rc) rc = qwk_gmm16(s, act, I, xh, xF, perm, tiles, mt, q4r(&M->gate), q4r(&M->up),
-                                (long)I * words, (long)I * groups, H, I, K, 0, grp, 1, 0, fuse ? &xgu : NULL, 64);
+                                (long)I * words, (long)I * groups, H, I, K, 0, grp, 1, 0, fuse ? &xgu : NULL, bm);
     } else {
         const qwk_q4 g0 = q4r(&M->gate_up);
         const qwk_q4 u0 = { g0.w + (size_t)I * words, g0.s + (size_t)I * groups, g0.b + (size_t)I * groups };
         if (!rc) rc = qwk_gmm16(s, act, I, xh, xF, perm, tiles, mt, g0, u0,
-                                2L * I * words, 2L * I * groups, H, I, K, 0, grp, 1, 0, fuse ? &xgu : NULL, 64);
+                                2L * I * words, 2L * I * groups, H, I, K, 0, grp, 1, 0, fuse ? &xgu : NULL, bm);
     }
     if (!rc) rc = qwk_stage16(s, ah, aF, act, ntot, I);
     if (!rc) rc = qwk_gmm16(s, ey, H, ah, aF, perm, tiles, mt, q4r(&M->down), q4r(&M->down),
-                            (long)H * (I / 8), (long)H * (I / grp), I, H, K, 1, grp, 0, 0, fuse ? &xdn : NULL, 64);
+                            (long)H * (I / 8), (long)H * (I / grp), I, H, K, 1, grp, 0, 0, fuse ? &xdn : NULL, bm);
     if (!fuse) {
         if (!rc) rc = qwk_gmm16(s, sa, SI, xh, xF, NULL, NULL, 0, q4r(&M->sh_gate), q4r(&M->sh_up),
                                 0, 0, H, SI, 1, 0, grp, 1, rows, NULL, 64);
