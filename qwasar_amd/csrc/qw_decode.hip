@@ -463,7 +463,7 @@ __global__ __launch_bounds__(QD_MAXT * 64) void k_batch_route(QbArgs b)
 }
 
 // The matrix-core gate / up's fp32 activations as the q16 vectors the down
-// launch reads: pair p's into qact, the shared expert's (rows npk + t) into
+// launch reads, where the product does not write them itself: pair p's into qact, the shared expert's (rows npk + t) into
 // qsh.  A thread per (vector, 16-unit).
 __global__ __launch_bounds__(256) void k_batch_act_q16(QbArgs b)
 {
@@ -687,6 +687,11 @@ extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, flo
     if (rc) return rc;
     const int nrb8 = (a.n_down_rb + 7) / 8 * 8;
     const qwk_gmm_extra xgu = {M->sh_gate, M->sh_up, M->E, npk};
+    // the activations leave the grouped product directly as the down
+    // launch's q16 vectors where it takes that form (16-row tiles), else as
+    // fp32 for k_batch_act_q16
+    const qwk_gmm_q16out q16o = {a.qact, a.qsh, npk};
+    const bool q16d = b.gmm && qwk_gmm16_q16_supported(M->H, G, rows);
     const int nvu = (npk + rows) * (M->I / 16);
 #define QB_GO(L_, N_, D_, P_)                                                                                   \
     if (lpr_h == L_ && nul_h == N_ && nul_d == D_ && pl == P_) {                                              \
@@ -696,9 +701,9 @@ extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, flo
                                      (const float *)(S + L.xF), b.perm, b.tiles, a.umax + 1, g0, u0,           \
                                      (long)(M->split ? 1 : 2) * M->I * (M->H / 8),                             \
                                      (long)(M->split ? 1 : 2) * M->I * (M->H / G), M->H, M->I, M->K, 0, G, 1, \
-                                     0, &xgu, rows);                                                           \
+                                     0, &xgu, rows, q16d ? &q16o : nullptr);                                  \
             if (rg) return rg;                                                                                \
-            hipLaunchKernelGGL(k_batch_act_q16, dim3((nvu + 255) / 256), dim3(256), 0, s, b);                 \
+            if (!q16d) hipLaunchKernelGGL(k_batch_act_q16, dim3((nvu + 255) / 256), dim3(256), 0, s, b);      \
         } else {                                                                                              \
             hipLaunchKernelGGL((k_batch_gu<L_, N_>), dim3(a.n_ex + a.n_sh), dim3(QD_THREADS), xs_bytes, s, b);\
         }                                                                                                     \

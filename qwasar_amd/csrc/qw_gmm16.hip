@@ -137,11 +137,17 @@ struct Gmm16Args {
     const uint32_t *xw0, *xw1;
     const uint16_t *xs0, *xb0, *xs1, *xb1;
     int xe, xpairs;
+    // with SWIGLU, the activations as q16 units instead of fp32: pair p < qnpk
+    // into qa[p], pair qnpk + r into qs[r] (vectors of n / 16 units)
+    uint4 *qa, *qs;
+    int qnpk;
 };
 
-template <int G, bool SWIGLU, bool DENSE, int KC, int BM>
+
+template <int G, bool SWIGLU, bool DENSE, int KC, int BM, bool Q16 = false>
 __global__ __launch_bounds__(G16_THREADS, BM == 64 ? 1 : 2) void k_gmm16(Gmm16Args a)
 {
+    static_assert(!Q16 || (SWIGLU && !DENSE && BM == 16), "q16 output: grouped SwiGLU, 16-row tiles");
     constexpr int WPL = KC / 32;                         // words (MFMA k steps) per lane per chunk
     constexpr int KPL = WPL * 8;                         // k a lane covers per chunk
     constexpr int NGL = KPL > G ? KPL / G : 1;           // quantisation groups in that span
@@ -156,6 +162,9 @@ __global__ __launch_bounds__(G16_THREADS, BM == 64 ? 1 : 2) void k_gmm16(Gmm16Ar
     __shared__ __align__(16) uint8_t Sb[2][(BM == 64 ? 4 : 2) * G16_BN * 16];
     __shared__ float Fr[BM];
     __shared__ int srow[BM], drow[BM];
+    // with q16 output (16-row tiles, one item a workgroup): the item's
+    // activations, fp32, until the last step is done
+    __shared__ float Lq[Q16 ? BM : 1][Q16 ? G16_BN / 2 : 1];
 
     // Workgroup b runs on XCD b % 8 (round-robin dispatch).  Each XCD takes a
     // contiguous range of tiles, and with r = b / 8 its workgroups walk
@@ -447,7 +456,14 @@ __global__ __launch_bounds__(G16_THREADS, BM == 64 ? 1 : 2) void k_gmm16(Gmm16Ar
                     if (dr >= 0) {
                         const float f = Fr[m];
                         float *yr = a.y + (size_t)dr * a.ldy;
-                        if (SWIGLU) {
+                        if constexpr (Q16) {
+                            // (into LDS: the q16 units are made after the last step)
+#pragma unroll
+                            for (int nt = 0; nt < NH; nt++) {
+                                const int col = colof(item, rowof(nt));
+                                if (col < a.n) Lq[m][col & (G16_BN / 2 - 1)] = qw_silu(f * acc[mt][nt][e]) * (f * acc[mt][nt + NH][e]);
+                            }
+                        } else if (SWIGLU) {
 #pragma unroll
                             for (int nt = 0; nt < NH; nt++) {
                                 const int col = colof(item, rowof(nt));
@@ -488,6 +504,24 @@ __global__ __launch_bounds__(G16_THREADS, BM == 64 ? 1 : 2) void k_gmm16(Gmm16Ar
     fetch_a(1);
     __syncthreads();
     for (int i = 0; i < T; i++) step(i);
+    if constexpr (Q16) {
+        {
+            // the item's q16 units: row m, 16 features from the item's first
+            __syncthreads();
+            const int units = a.n >> 4, c0 = colof(0, 0), upr = (BNT / 2) / 16;
+            for (int q = t; q < BM * upr; q += G16_THREADS) {
+                const int m = q / upr, uu = q % upr, dr = drow[m];
+                const int col = c0 + 16 * uu;
+                if (dr < 0 || col >= a.n) continue;
+                float v[16];
+#pragma unroll
+                for (int z = 0; z < 16; z++) v[z] = Lq[m][(col & (G16_BN / 2 - 1)) + z];
+                uint4 *qv = (dr < a.qnpk ? a.qa + (size_t)dr * units * 3 : a.qs + (size_t)(dr - a.qnpk) * units * 3) +
+                            (size_t)(col >> 4) * 3;
+                qw_q16_stage(v, qv);
+            }
+        }
+    }
     };
     if (half) body(std::integral_constant<int, 2>{});
     else body(std::integral_constant<int, 4>{});
@@ -521,7 +555,8 @@ static void g16_launch(hipStream_t s, const Gmm16Args &a, int swiglu, int dense,
     if constexpr (KC == 256) {
         if (bm == 16 && !dense) {
             const dim3 g(grid), b(G16_THREADS);
-            if (swiglu) hipLaunchKernelGGL((k_gmm16<G, true, false, KC, 16>), g, b, 0, s, a);
+            if (swiglu && a.qa) hipLaunchKernelGGL((k_gmm16<G, true, false, KC, 16, true>), g, b, 0, s, a);
+            else if (swiglu) hipLaunchKernelGGL((k_gmm16<G, true, false, KC, 16>), g, b, 0, s, a);
             else hipLaunchKernelGGL((k_gmm16<G, false, false, KC, 16>), g, b, 0, s, a);
             return;
         }
@@ -557,10 +592,23 @@ extern "C" int qwk_gmm16_supported(int k, int group, const void *w0, const void 
     return 0;
 }
 
+// Whether qwk_gmm16 writes q16 activations for a grouped SwiGLU product of
+// inner size k and this group with tiles of at most tile_rows rows (16-row
+// tiles: chunks of 256, a scale / bias block of at most 8 groups).
+extern "C" int qwk_gmm16_q16_supported(int k, int group, int tile_rows)
+{
+    if (tile_rows > 16 || k % 256 || (group != 32 && group != 64 && group != 128) || k % group) return 0;
+    const int groups = k / group;
+    for (int g = 8; g >= 1; g /= 2)
+        if (groups % g == 0 && (g * group) % 256 == 0) return 1;
+    return 0;
+}
+
 extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb, const float *aF,
                          const int32_t *perm, const int32_t *tiles, int max_tiles,
                          qwk_q4 m0, qwk_q4 m1, long ew, long eg, int k, int n, int K, int x_by_pair,
-                         int group, int swiglu, int dense_rows, const qwk_gmm_extra *xb, int tile_rows)
+                         int group, int swiglu, int dense_rows, const qwk_gmm_extra *xb, int tile_rows,
+                         const qwk_gmm_q16out *q16)
 {
     // chunks of 256 where k allows, else 64
     const int kc = k % 256 == 0 ? 256 : 64;
@@ -572,6 +620,7 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
         return (int)hipErrorInvalidValue;
     const _Float16 *ah = reinterpret_cast<const _Float16 *>(ahb);
     const bool dense = dense_rows > 0;
+    if (q16 && (!swiglu || dense || n % 16 || !q16->qa || !q16->qs || tile_rows > 16)) return (int)hipErrorInvalidValue;
     if (!dense && (!perm || !tiles || K < 1)) return (int)hipErrorInvalidValue;
     Gmm16Args a;
     a.y = y; a.ldy = ldy; a.ah = ah; a.aF = aF; a.perm = perm; a.tiles = tiles;
@@ -587,6 +636,9 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
         a.xw0 = a.xw1 = m0.w; a.xs0 = a.xs1 = m0.s; a.xb0 = a.xb1 = m0.b;
         a.xe = -1; a.xpairs = 0x7FFFFFFF;
     }
+    a.qa = q16 ? static_cast<uint4 *>(q16->qa) : nullptr;
+    a.qs = q16 ? static_cast<uint4 *>(q16->qs) : nullptr;
+    a.qnpk = q16 ? q16->npk : 0;
     a.nblk = swiglu ? (n + G16_BN / 2 - 1) / (G16_BN / 2) : (n + G16_BN - 1) / G16_BN;
     {
         // the largest scale / bias block (groups) that divides a row's groups
@@ -599,7 +651,7 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
             if (a.gpb || bm == 64) break;
             bm = 64;             // (no block of at most 8 groups ends on a chunk boundary)
         }
-        if (!a.gpb) return (int)hipErrorInvalidValue;
+        if (!a.gpb || (q16 && bm != 16)) return (int)hipErrorInvalidValue;
     }
     const int ntiles = dense ? (dense_rows + bm - 1) / bm : max_tiles;
     if (ntiles <= 0) return 0;
@@ -612,7 +664,7 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
         int nbw = per < 1 ? 1 : per > 8 ? 8 : (int)per;
         if (nbw > a.nblk) nbw = a.nblk;
         while (a.nblk % nbw) nbw--;
-        a.nbw = nbw;
+        a.nbw = q16 ? 1 : nbw;        // (q16 output: one item a workgroup, its activations held in LDS)
     }
     a.cpx = g16_cus_per_xcd() * (bm == 16 ? 2 : 1);   // workgroups an XCD holds at once
     // r = b / 8 < ngr * ceil(ntiles / 8) covers every XCD's whole items, and

@@ -94,11 +94,19 @@ int qwk_stage16(hipStream_t s, uint16_t *h, float *F, const float *x, int rows, 
  * m0 (and with swiglu m1, the up rows) point at expert 0 of the bank; ew/eg
  * are the per-expert strides in words / groups.  With swiglu, n = features
  * and y = silu(W0 A) * (W1 A).  k % 64 == 0 and k % group == 0. */
+/* With swiglu (grouped): the activations leave as q16 units (the decode
+ * staging format, [vectors][n / 16][48 bytes]) in place of fp32 y: pair
+ * p < npk into qa's vector p, pair npk + r into qs's vector r. */
+typedef struct {
+    void *qa, *qs;
+    int npk;
+} qwk_gmm_q16out;
+int qwk_gmm16_q16_supported(int k, int group, int tile_rows);
 int qwk_gmm16_supported(int k, int group, const void *w0, const void *w1);
 int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ah, const float *aF,
               const int32_t *perm, const int32_t *tiles, int max_tiles, qwk_q4 m0, qwk_q4 m1, long ew,
               long eg, int k, int n, int K, int x_by_pair, int group, int swiglu, int dense_rows,
-              const qwk_gmm_extra *xb, int tile_rows);
+              const qwk_gmm_extra *xb, int tile_rows, const qwk_gmm_q16out *q16);
 
 /* Elementwise. */
 int qwk_swiglu(hipStream_t s, float *y, const float *gate, const float *up, int64_t n);

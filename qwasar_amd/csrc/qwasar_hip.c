@@ -945,22 +945,22 @@ static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const floa
                                 qwk_moe_group_work_bytes(pairs, E), xr);
     if (M->split) {
         if (!rc) rc = qwk_gmm16(s, act, I, xh, xF, perm, tiles, mt, q4r(&M->gate), q4r(&M->up),
-                                (long)I * words, (long)I * groups, H, I, K, 0, grp, 1, 0, fuse ? &xgu : NULL, bm);
+                                (long)I * words, (long)I * groups, H, I, K, 0, grp, 1, 0, fuse ? &xgu : NULL, bm, NULL);
     } else {
         const qwk_q4 g0 = q4r(&M->gate_up);
         const qwk_q4 u0 = { g0.w + (size_t)I * words, g0.s + (size_t)I * groups, g0.b + (size_t)I * groups };
         if (!rc) rc = qwk_gmm16(s, act, I, xh, xF, perm, tiles, mt, g0, u0,
-                                2L * I * words, 2L * I * groups, H, I, K, 0, grp, 1, 0, fuse ? &xgu : NULL, bm);
+                                2L * I * words, 2L * I * groups, H, I, K, 0, grp, 1, 0, fuse ? &xgu : NULL, bm, NULL);
     }
     if (!rc) rc = qwk_stage16(s, ah, aF, act, ntot, I);
     if (!rc) rc = qwk_gmm16(s, ey, H, ah, aF, perm, tiles, mt, q4r(&M->down), q4r(&M->down),
-                            (long)H * (I / 8), (long)H * (I / grp), I, H, K, 1, grp, 0, 0, fuse ? &xdn : NULL, bm);
+                            (long)H * (I / 8), (long)H * (I / grp), I, H, K, 1, grp, 0, 0, fuse ? &xdn : NULL, bm, NULL);
     if (!fuse) {
         if (!rc) rc = qwk_gmm16(s, sa, SI, xh, xF, NULL, NULL, 0, q4r(&M->sh_gate), q4r(&M->sh_up),
-                                0, 0, H, SI, 1, 0, grp, 1, rows, NULL, 64);
+                                0, 0, H, SI, 1, 0, grp, 1, rows, NULL, 64, NULL);
         if (!rc) rc = qwk_stage16(s, sh16, sF, sa, rows, SI);
         if (!rc) rc = qwk_gmm16(s, sh, H, sh16, sF, NULL, NULL, 0, q4r(&M->sh_down), q4r(&M->sh_down),
-                                0, 0, SI, H, 1, 0, grp, 0, rows, NULL, 64);
+                                0, 0, SI, H, 1, 0, grp, 0, rows, NULL, 64, NULL);
     }
     if (!rc && !gated) rc = qwk_dmat_bf16(s, g1, x, dp(M->sh_gate_w), H, 1, rows);
     if (!rc) rc = qwk_moe_combine(s, out, ey, w, fuse ? ey + (size_t)pairs * H : sh, g1, rows, K, H);
