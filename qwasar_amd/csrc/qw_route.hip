@@ -682,13 +682,18 @@ extern "C" int qwk_route(hipStream_t s, int32_t *idx, float *w, const float *log
 // The pairs are cut into chunks of QW_GROUP_CHUNK, one workgroup each, and
 // within a chunk into eight contiguous runs, one a wave.  Three launches:
 //
-//   count  per (chunk, wave, expert) counts (order-free LDS atomics)
+//   count  per (chunk, expert) counts (order-free LDS atomics)
 //   scan   one workgroup: an exclusive scan over experts and then, within an
-//          expert, over (chunk, wave) gives every (chunk, wave, expert) its
-//          first slot; the tile list follows from the per-expert totals
-//   place  each wave walks its run 64 pairs at a time, ranking a lane among
+//          expert, over the chunks gives every (chunk, expert) its first
+//          slot; the tile list follows from the per-expert totals
+//   place  each workgroup counts its chunk's runs again, per (wave, expert),
+//          and adds them in wave order to its (chunk, expert) slots; each
+//          wave then walks its run 64 pairs at a time, ranking a lane among
 //          the lower lanes that share its expert with ballots over the
-//          expert id's bits, from its (chunk, wave, expert) slots
+//          expert id's bits
+// (The scan reads chunk counts, not (chunk, wave) ones: a single workgroup
+// moving 8x the counts through one CU's L1 took 12.6 of the 26 us at 2048
+// tokens.)
 //
 // The counts live in a work buffer of qwk_moe_group_work_bytes(pairs, E).
 // `extra` rows may follow the pairs as one more expert, E (the prefill's
@@ -724,19 +729,17 @@ __device__ int qw_block_excl_scan(int v, int *tmp, int *total, int nthr)
 __global__ __launch_bounds__(QW_GROUP_THREADS) void k_group_count(int *__restrict__ work,
                                                                   const int *__restrict__ idx, int pairs, int E)
 {
-    __shared__ int cnt[QW_GROUP_WAVES][QWK_GROUP_MAX_E];
-    const int t = threadIdx.x, wave = t / 64, lane = t % 64;
-    for (int i = t; i < QW_GROUP_WAVES * E; i += QW_GROUP_THREADS) cnt[i / E][i % E] = 0;
+    __shared__ int cnt[QWK_GROUP_MAX_E];
+    const int t = threadIdx.x;
+    for (int i = t; i < E; i += QW_GROUP_THREADS) cnt[i] = 0;
     __syncthreads();
-    const int p0 = min(pairs, blockIdx.x * QW_GROUP_CHUNK + wave * QW_GROUP_RUN), p1 = min(pairs, p0 + QW_GROUP_RUN);
-    for (int p = p0 + lane; p < p1; p += 64) atomicAdd(&cnt[wave][idx[p]], 1);
+    const int p0 = min(pairs, blockIdx.x * QW_GROUP_CHUNK), p1 = min(pairs, p0 + QW_GROUP_CHUNK);
+    for (int p = p0 + t; p < p1; p += QW_GROUP_THREADS) atomicAdd(&cnt[idx[p]], 1);
     __syncthreads();
-    int *w = work + (size_t)blockIdx.x * QW_GROUP_WAVES * E;
-    for (int i = t; i < QW_GROUP_WAVES * E; i += QW_GROUP_THREADS) w[i] = cnt[i / E][i % E];
+    int *w = work + (size_t)blockIdx.x * E;
+    for (int i = t; i < E; i += QW_GROUP_THREADS) w[i] = cnt[i];
 }
 
-// Counts to first slots, in place, and the tile list.  Thread t owns experts
-// [t * per_t, (t + 1) * per_t).
 __global__ __launch_bounds__(QW_SCAN_THREADS) void k_group_scan(int *__restrict__ work, int *__restrict__ tiles,
                                                                  int *__restrict__ perm, int pairs, int extra,
                                                                  int nruns, int E, int bm, int max_tiles)
@@ -806,10 +809,24 @@ __global__ __launch_bounds__(QW_GROUP_THREADS) void k_group_place(int *__restric
 {
     __shared__ int cnt[QW_GROUP_WAVES][QWK_GROUP_MAX_E];
     const int t = threadIdx.x, wave = t / 64, lane = t % 64;
-    const int *w = work + (size_t)blockIdx.x * QW_GROUP_WAVES * E;
-    for (int i = t; i < QW_GROUP_WAVES * E; i += QW_GROUP_THREADS) cnt[i / E][i % E] = w[i];
+    for (int i = t; i < QW_GROUP_WAVES * E; i += QW_GROUP_THREADS) cnt[i / E][i % E] = 0;
     __syncthreads();
     const int p0 = min(pairs, blockIdx.x * QW_GROUP_CHUNK + wave * QW_GROUP_RUN), p1 = min(pairs, p0 + QW_GROUP_RUN);
+    for (int p = p0 + lane; p < p1; p += 64) atomicAdd(&cnt[wave][idx[p]], 1);
+    __syncthreads();
+    // (wave, expert) slots: the chunk's slot for the expert plus the counts
+    // of the expert's pairs in the runs of the lower waves
+    const int *w = work + (size_t)blockIdx.x * E;
+    for (int e = t; e < E; e += QW_GROUP_THREADS) {
+        int run = w[e];
+#pragma unroll
+        for (int v = 0; v < QW_GROUP_WAVES; v++) {
+            const int c = cnt[v][e];
+            cnt[v][e] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
     int nbits = 1;
     while ((1 << nbits) < E) nbits++;
     const unsigned long long below = (1ull << lane) - 1ull;
@@ -838,7 +855,7 @@ __global__ __launch_bounds__(QW_GROUP_THREADS) void k_group_place(int *__restric
 extern "C" size_t qwk_moe_group_work_bytes(int pairs, int E)
 {
     const size_t chunks = pairs > 0 ? (size_t)(pairs + QW_GROUP_CHUNK - 1) / QW_GROUP_CHUNK : 1;
-    return chunks * QW_GROUP_WAVES * (size_t)(E > 0 ? E : 1) * sizeof(int);
+    return chunks * (size_t)(E > 0 ? E : 1) * sizeof(int);
 }
 
 extern "C" int qwk_moe_group(hipStream_t s, int32_t *perm, int32_t *tiles, const int32_t *idx,
@@ -852,7 +869,7 @@ extern "C" int qwk_moe_group(hipStream_t s, int32_t *perm, int32_t *tiles, const
     int *wk = static_cast<int *>(work);
     hipLaunchKernelGGL(k_group_count, dim3(chunks), dim3(QW_GROUP_THREADS), 0, s, wk, idx, pairs, E);
     hipLaunchKernelGGL(k_group_scan, dim3(1), dim3(QW_SCAN_THREADS), 0, s, wk, tiles, perm, pairs, extra,
-                       chunks * QW_GROUP_WAVES, E, bm, max_tiles);
+                       chunks, E, bm, max_tiles);
     hipLaunchKernelGGL(k_group_place, dim3(chunks), dim3(QW_GROUP_THREADS), 0, s, perm, wk, idx, pairs, E);
     return (int)hipGetLastError();
 }
