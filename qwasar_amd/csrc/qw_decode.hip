@@ -18,6 +18,9 @@
 // loaded straight into registers next to the weights.
 #include "qw_device.h"
 #include "qw_kernels.h"
+#include "qw_few.h"
+
+#include <algorithm>
 
 #define QD_MAXT QWK_DECODE_MAX_ROWS
 #define QD_MAXU (QWK_DECODE_MAX_ROWS * QWK_DECODE_MAX_K)
@@ -344,10 +347,17 @@ struct QbArgs {
     int gmm;                  // gate / up on the matrix cores: emit perm and tiles
     int32_t *perm, *tiles;
     const float *act;         // their fp32 activations [pairs + rows][I]
+    uint16_t *xh;             // the token rows staged as f16 (matrix-core gate / up)
+    float *xF;                //   and their scales
 };
 
+#define QB_SPIN_LIMIT (1 << 16)
+
+// Every token routed and the batch's tables, by one workgroup of QD_MAXT
+// waves (the logits of token r at logits + r E: global memory, or LDS in
+// the router-and-route launch).
 template <int PL>
-__global__ __launch_bounds__(QD_MAXT * 64) void k_batch_route(QbArgs b)
+__device__ __forceinline__ void qb_route_body(const QbArgs &b, const float *logits)
 {
     __shared__ QdRoute R;
     const QdArgs &a = b.d;
@@ -356,7 +366,7 @@ __global__ __launch_bounds__(QD_MAXT * 64) void k_batch_route(QbArgs b)
     if (wave < a.rows) {
         int pi;
         float pw;
-        qw_route_wave<PL>(b.logits + (size_t)wave * E, E, K, a.m.norm, lane, &pi, &pw, R.rs.sx[wave]);
+        qw_route_wave<PL>(logits + (size_t)wave * E, E, K, a.m.norm, lane, &pi, &pw, R.rs.sx[wave]);
         if (lane < K) {
             R.picks[wave * K + lane] = pi;
             R.pw[wave * K + lane] = pw;
@@ -460,6 +470,65 @@ __global__ __launch_bounds__(QD_MAXT * 64) void k_batch_route(QbArgs b)
         for (int r = t; r < a.rows; r += nthr) b.perm[npk + r] = npk + r;
     }
     (void)nwd;
+}
+
+template <int PL>
+__global__ __launch_bounds__(QD_MAXT * 64) void k_batch_route(QbArgs b)
+{
+    qb_route_body<PL>(b, b.logits);
+}
+
+// The router's logits and the routing in one launch: blocks (x < gridDim.x
+// - 1, y) are k_dmat_few's (the logits leave as tagged words, device scope);
+// the last block, (gridDim.x - 1, gridDim.y - 1), dispatched after every
+// other, polls them into LDS (wave r: token r's E logits, every tag
+// checked, bounded as the one-token launch's waits) and routes.  The grid's
+// other blocks of the last column return at once.
+template <int PL>
+__global__ __launch_bounds__(QD_MAXT * 64) void k_batch_router(QbArgs b, uint2 *ty, uint32_t *err, uint32_t epoch)
+{
+    extern __shared__ float xl[];
+    const QdArgs &a = b.d;
+    const int E = a.m.E, H = a.m.H;
+    if ((int)blockIdx.x < (int)gridDim.x - 1) {
+        qw_few_body<true>(nullptr, reinterpret_cast<float *>(b.tab + QB_TAB_GATE), a.x, a.m.router, a.m.sh_gate_w,
+                          H, E, a.rows, nullptr, b.xh, b.xF, ty, epoch, blockIdx.x, blockIdx.y, xl);
+        return;
+    }
+    if (blockIdx.y != gridDim.y - 1) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float *lg = xl;                                  // [rows][E]
+    if (wave < a.rows) {
+        const uint2 *tw = ty + (size_t)wave * E;
+        for (int spins = 0;; spins++) {
+            unsigned long long q[PL];
+#pragma unroll
+            for (int i = 0; i < PL; i++) {
+                const uint2 *pi = tw + min(lane + 64 * i, E - 1);
+                asm volatile("global_load_dwordx2 %0, %1, off sc1" : "=v"(q[i]) : "v"(pi) : "memory");
+            }
+            uint32_t e;
+            asm volatile("global_load_dword %0, %1, off sc1" : "=v"(e) : "v"(err) : "memory");
+            asm volatile("s_waitcnt vmcnt(0)" : "+v"(e) : : "memory");
+            bool stale = false;
+#pragma unroll
+            for (int i = 0; i < PL; i++) {
+                asm volatile("" : "+v"(q[i]));
+                stale |= lane + 64 * i < E && (uint32_t)q[i] != epoch;
+            }
+            if (__ballot(stale) == 0ull || spins >= QB_SPIN_LIMIT || __ballot(e != 0u) != 0ull) {
+                if (__ballot(stale) != 0ull && lane == 0)
+                    __hip_atomic_store(err, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (int i = 0; i < PL; i++)
+                    if (lane + 64 * i < E) lg[(size_t)wave * E + lane + 64 * i] = __uint_as_float((uint32_t)(q[i] >> 32));
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    __syncthreads();
+    qb_route_body<PL>(b, lg);
 }
 
 // The matrix-core gate / up's fp32 activations as the q16 vectors the down
@@ -632,8 +701,10 @@ extern "C" size_t qwk_moe_decode_batch_scratch(const qwk_moe *M, int rows)
 }
 
 extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
-                                    const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes)
+                                    const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes, void *tags,
+                                    size_t tag_words, uint32_t *err, uint32_t epoch, int *handoff)
 {
+    if (handoff) *handoff = 0;
     const int G = M->group;
     if (rows < 1 || !qwk_moe_decode_batch_supported(M, rows) || !x || ((uintptr_t)x & 15u)) return (int)hipErrorInvalidValue;
     const QbLayout L = qb_layout(M, rows);
@@ -667,23 +738,38 @@ extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, flo
     b.perm = (int32_t *)(S + L.perm);
     b.tiles = (int32_t *)(S + L.tiles);
     b.act = (const float *)(S + L.act);
+    b.xh = (uint16_t *)(S + L.xh);
+    b.xF = (float *)(S + L.xF);
     const size_t xs_bytes = (size_t)a.tch * vbytes;
     const size_t xa_bytes = ((size_t)(M->SI / 16) + (size_t)M->K * (M->I / 16)) * QW_Q16_BYTES;
     if (a.tch < 1 || xa_bytes > QD_LDS || a.umax > QD_MAXU) return (int)hipErrorInvalidValue;
     // the router logits and the shared expert's gate logits, one launch
     float *lg = (float *)(S + L.logits), *gl = (float *)(b.tab + QB_TAB_GATE);
-    // (which also stages the token rows as q16 for the gate / up launch)
+    // The matrix-core gate / up with the hand-off words at hand: the logits,
+    // the f16 staging and the routing in one launch (k_batch_router).
+    const int ygroups = (rows + QW_DF_TPG - 1) / QW_DF_TPG, xblocks = (M->E + 1 + QW_DF_WAVES - 1) / QW_DF_WAVES;
+    const bool fused = b.gmm && tags && err && epoch && (size_t)rows * M->E <= tag_words && M->H % 64 == 0 &&
+                       M->H <= 64 * 64 && rows <= QW_DF_MAXR && ((uintptr_t)M->router & 15u) == 0 &&
+                       ((uintptr_t)M->sh_gate_w & 15u) == 0;
+    int rc = 0;
+    bool staged16 = true;
     b.xstaged = 1;
-    // (or, for the matrix-core gate / up, as f16 rows with a scale each)
-    int rc = qwk_dmat_bf16_gate(s, lg, gl, x, M->router, M->sh_gate_w, M->H, M->E, rows, b.gmm ? nullptr : a.qx,
-                                b.gmm ? (uint16_t *)(S + L.xh) : nullptr, b.gmm ? (float *)(S + L.xF) : nullptr);
-    bool staged16 = rc == 0;
-    if (rc == (int)hipErrorInvalidValue) {   // a layout the one launch does not take: two order-R launches
-        b.xstaged = b.gmm;
-        rc = qwk_dmat_bf16(s, lg, x, M->router, M->H, M->E, rows);
-        if (!rc) rc = qwk_dmat_bf16(s, gl, x, M->sh_gate_w, M->H, 1, rows);
+    if (fused && handoff) *handoff = 1;
+    if (!fused) {
+        // (which also stages the token rows as q16 for the gate / up launch,
+        // or, for the matrix-core gate / up, as f16 rows with a scale each)
+        rc = qwk_dmat_bf16_gate(s, lg, gl, x, M->router, M->sh_gate_w, M->H, M->E, rows, b.gmm ? nullptr : a.qx,
+                                b.gmm ? b.xh : nullptr, b.gmm ? b.xF : nullptr);
+        staged16 = rc == 0;
+        if (rc == (int)hipErrorInvalidValue) {   // a layout the one launch does not take: two order-R launches
+            b.xstaged = b.gmm;
+            rc = qwk_dmat_bf16(s, lg, x, M->router, M->H, M->E, rows);
+            if (!rc) rc = qwk_dmat_bf16(s, gl, x, M->sh_gate_w, M->H, 1, rows);
+        }
+        if (!rc && b.gmm && !staged16) rc = qwk_stage16(s, b.xh, b.xF, x, rows, M->H);
     }
-    if (!rc && b.gmm && !staged16) rc = qwk_stage16(s, (uint16_t *)(S + L.xh), (float *)(S + L.xF), x, rows, M->H);
+    const size_t few_lds = (size_t)min(rows, QW_DF_TPG) * (M->H / 64) * QW_DF_PAD * sizeof(float);
+    const size_t rt_lds = std::max(few_lds, (size_t)rows * M->E * sizeof(float));
     if (rc) return rc;
     const int nrb8 = (a.n_down_rb + 7) / 8 * 8;
     const qwk_gmm_extra xgu = {M->sh_gate, M->sh_up, M->E, npk};
@@ -695,7 +781,11 @@ extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, flo
     const int nvu = (npk + rows) * (M->I / 16);
 #define QB_GO(L_, N_, D_, P_)                                                                                   \
     if (lpr_h == L_ && nul_h == N_ && nul_d == D_ && pl == P_) {                                              \
-        hipLaunchKernelGGL(k_batch_route<P_>, dim3(1), dim3(QD_MAXT * 64), 0, s, b);                          \
+        if (fused)                                                                                            \
+            hipLaunchKernelGGL(k_batch_router<P_>, dim3(xblocks + 1, ygroups), dim3(QD_MAXT * 64), rt_lds, s, b, \
+                               (uint2 *)tags, err, epoch);                                                    \
+        else                                                                                                  \
+            hipLaunchKernelGGL(k_batch_route<P_>, dim3(1), dim3(QD_MAXT * 64), 0, s, b);                      \
         if (b.gmm) {                                                                                          \
             const int rg = qwk_gmm16(s, (float *)b.act, M->I, (const uint16_t *)(S + L.xh),                   \
                                      (const float *)(S + L.xF), b.perm, b.tiles, a.umax + 1, g0, u0,           \

@@ -186,14 +186,20 @@ typedef struct {
 #define QWK_DECODE_MAX_K 15
 int qwk_moe_decode(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
                    const qwk_resid *res, const qwk_moe *M, void *sync, uint32_t epoch, hipEvent_t *ev);
-/* Decode of 1..QWK_DECODE_MAX_ROWS tokens over the batch's unique experts,
- * in four launches with no cross-workgroup waits (router logits, routing and
- * the unique-expert table, gate/up per unique expert, down and combine per
- * token).  Same shapes as qwk_moe_decode; scratch of
- * qwk_moe_decode_batch_scratch bytes, nothing in it initialised. */
+/* Decode of 1..QWK_DECODE_MAX_ROWS tokens over the batch's unique experts:
+ * router logits, routing and the unique-expert table, gate/up per unique
+ * expert, down and combine per token.  With the decode hand-off words (tags,
+ * tag_words of them, the error word and a fresh epoch: from
+ * qwk_decode_sync_words) and the matrix-core gate/up, the logits and the
+ * routing share one launch (its routing workgroup waits for the logits'
+ * tagged words; *handoff = 1); else they are launches of their own
+ * (*handoff = 0).  Same shapes as
+ * qwk_moe_decode; scratch of qwk_moe_decode_batch_scratch bytes, nothing in it
+ * initialised. */
 size_t qwk_moe_decode_batch_scratch(const qwk_moe *M, int rows);
 int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, float *w, const float *x,
-                         const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes);
+                         const qwk_moe *M, int rows, void *scratch, size_t scratch_bytes, void *tags,
+                         size_t tag_words, uint32_t *err, uint32_t epoch, int *handoff);
 
 /* RMS norm of [rows, dim] fp32 rows (dim % 4 == 0), optional bf16 weight:
  * y = x / sqrt(mean(x^2) + eps) * out_scale (* w). */

@@ -1005,12 +1005,26 @@ static bool moe_decode(qw_cmd c, float *out, int32_t *idx, float *w, const float
         void *S = k == QW_DS_STATIC ? (void *)G.static_stage : scratch(need);
         const size_t have = k == QW_DS_STATIC ? G.static_stage_len : need;
         if (!S) { cmd_fail(c, hipErrorOutOfMemory, "moe_layer: scratch of %zu bytes", need); return false; }
+        /* the hand-off words, for the router-and-route launch */
+        uint32_t *err = NULL, epoch = 0;
+        void *words = NULL;
+        size_t nwords = 0;
+        if ((G.ds[k].sync || dsync_reset(k)) && (G.ds[k].epoch != UINT32_MAX || dsync_check(k, 1))) {
+            qwk_decode_sync_words(G.ds[k].sync, &err, &words, &nwords);
+            epoch = G.ds[k].epoch + 1;
+        }
+        int handoff = 0;
         int rc = 0;
         if (res) {
             rc = qwk_resid_rms_bf16(G.stream, res->h, res->h_out, res->x_out, res->y, m.H, rows, res->eps);
             x = res->x_out;
         }
-        if (!rc) rc = qwk_moe_decode_batch(G.stream, out, idx, w, x, &m, rows, S, have);
+        if (!rc) rc = qwk_moe_decode_batch(G.stream, out, idx, w, x, &m, rows, S, have, words, nwords, err, epoch,
+                                           &handoff);
+        if (handoff) {            /* the epoch is taken only by a launch that hands off */
+            G.ds[k].epoch = epoch;
+            c->ep_hi[k] = epoch;
+        }
         launched(c, k == QW_DS_STATIC ? "moe_layer_noalloc" : "moe_layer (decode batch)", rc);
         return rc == 0;
     }

@@ -44,9 +44,14 @@ def _exact(L, x, bufs):
     assert e < 5e-4
 
 
-@pytest.mark.parametrize("rows", [1])
+@pytest.mark.parametrize("rows", [1, 3])
 def test_handoff_give_up_is_reported_and_recovered(gpu, rows):
-    L, _ = synth.make_config(0, rows=rows, seed=4100 + rows)
+    """One token (the one launch) and three (the batch path's router-and-route
+    launch, whose routing workgroup waits for the logits' tagged words)."""
+    if rows == 1:
+        L, _ = synth.make_config(0, rows=rows, seed=4101)
+    else:   # the shared expert as wide as the routed ones: the matrix-core batch path
+        L = synth.make_layer(4103, H=256, E=16, K=4, I=128, SI=128, group=64, tag="handoff3.")
     lb = gpu.LayerBufs(L)
     xs = [synth.make_x(4200 + rows + i, rows, L.H) for i in range(3)]
     # A launches normally; the word is then raised for the next launch, B's.
@@ -66,11 +71,13 @@ def test_handoff_give_up_is_reported_and_recovered(gpu, rows):
     lb.free()
 
 
-def test_batch_decode_has_no_handoff(gpu):
-    """Several tokens take the batch path (separate launches, no waits between
-    workgroups): a raised error word does not touch it, and stays for the next
-    one-token launch, which fails and recovers as above."""
-    L, _ = synth.make_config(0, rows=3, seed=4150)
+def test_batch_decode_without_matrix_core_has_no_handoff(gpu):
+    """A batch whose shared expert is wider than the routed experts runs its
+    gate / up as q16 dots, with the router and the routing as launches of
+    their own (no waits between workgroups): a raised error word does not
+    touch it, and stays for the next one-token launch, which fails and
+    recovers as above."""
+    L = synth.make_layer(4150, H=256, E=32, K=4, I=64, SI=128, group=64, tag="nohandoff.")
     lb = gpu.LayerBufs(L)
     x3, x1 = synth.make_x(4151, 3, L.H), synth.make_x(4152, 1, L.H)
     assert gpu.qw_debug_decode_handoff_fail()
