@@ -527,7 +527,231 @@ __global__ __launch_bounds__(G16_THREADS, BM == 64 ? 1 : 2) void k_gmm16(Gmm16Ar
     else body(std::integral_constant<int, 4>{});
 }
 
+// ---- the batch decode's gate / up: one stream a wave ------------------------------
+//
+// Grouped SwiGLU with tiles of at most 16 rows and q16 output (a decode
+// batch: a tile is one unique expert's pairs, or the shared expert's token
+// rows), where the bytes are the experts' weights, each read once.  The
+// product above moves them in chunk steps its 8 waves take together (the
+// activation chunk through LDS, the scale / bias blocks by DMA, a barrier a
+// chunk), so each of its loads waits behind the others and a workgroup holds
+// about one chunk in flight.  Here:
+//   - a workgroup (8 waves) owns one tile and 128 features; it stages the
+//     tile's rows (all of k) and its 256 weight rows' scales and biases (four
+//     contiguous runs) in LDS once, and from then on its waves never wait
+//     for one another;
+//   - wave w owns features f0 = 16 (8 fb + w) .. f0 + 15: its 16 gate and 16
+//     up rows, a weight tile of 16 each, with the product's lane layout
+//     (lane group kg holds k from kg 64 of each 256-chunk, 8 words);
+//   - a chunk's words load into one slot of a D-slot register ring and are
+//     consumed D chunks later: every wait in the loop is a counted one on the
+//     words of one chunk;
+//   - the 16 features of a row are one q16 unit of the down launch: the wave
+//     makes its rows' units itself.
+// Scales and biases are not loaded a chunk at a time: a 2-byte load a lane
+// touches 16 rows' lines for 32 bytes of use and doubled the requests the
+// weights make (11 of 35 us at config 2's batch).
+// Workgroup b is item b: tile b / nfb, feature block b % nfb (the items of
+// a tile on consecutive XCDs).
+// ring slots: two chunks (one and three measured within a microsecond)
+constexpr int GS_DEPTH = 2;
+// LDS of k_gmm16_stream, for k <= GS_MAXK and k / G <= GS_MAXG: the tile's
+// rows (16 of k + 8 halfs), four scale / bias runs (gate s, gate b, up s,
+// up b: 128 rows of k / G bf16, a run's stride rounded up to whole 1 KB DMA
+// slabs) and the waves' output squares; 153 KB of the CU's 160
+#define GS_MAXK 3072
+#define GS_MAXG 48
+static __host__ __device__ inline int gs_run_stride(int groups) { return (128 * groups * 2 + 1023) / 1024 * 1024; }
+
+template <int G, int D>
+__global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16_stream(Gmm16Args a)
+{
+    constexpr int KC = 256, WPL = 8, KPL = 64, NGL = KPL > G ? KPL / G : 1;
+    static_assert(NGL <= 2, "at most two groups a lane a chunk");
+    __shared__ __align__(16) _Float16 As[16 * (GS_MAXK + 8)];
+    __shared__ __align__(16) uint8_t Sb[4 * 128 * GS_MAXG * 2];
+    __shared__ float Lw[(G16_THREADS / 64) * 16 * 17];
+    __shared__ float Fr[16];
+    __shared__ int srow[16], drow[16];
+    const int k = a.k, AST = k + 8, words = k / 8, groups = k / G, nch = k / KC;
+    const int RS = gs_run_stride(groups);
+    const int nfb = (a.n + 127) / 128, tile = blockIdx.x / nfb, fb = blockIdx.x % nfb;
+    if (tile >= a.tiles[0]) return;
+    const int expert = a.tiles[1 + 3 * tile], first = a.tiles[2 + 3 * tile], len = a.tiles[3 + 3 * tile];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, ln = lane & 15, kg = lane >> 4;
+    // the wave's rows: gate and up of features f0 + ln (row j of the block)
+    const int f0 = fb * 128 + wave * 16, f = min(f0 + ln, a.n - 1), j = wave * 16 + ln;
+    const bool xe = expert == a.xe;
+    const __amdgpu_buffer_rsrc_t rW0 = qw_rsrc(xe ? a.xw0 : a.w0 + (size_t)expert * a.ew),
+                                 rW1 = qw_rsrc(xe ? a.xw1 : a.w1 + (size_t)expert * a.ew);
+    const uint32_t wrow = (uint32_t)(f * words + kg * WPL) * 4;
+    uint32_t wq[D][2][WPL];
+    // chunk c's words (clamped to the last: the same loads every chunk) into
+    // slot z: 4 loads
+    auto fetch = [&](int c, auto zc) {
+        constexpr int z = decltype(zc)::value;
+        c = min(c, nch - 1);
+        const uint32_t wo = wrow + (uint32_t)c * (KC / 8) * 4;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const __amdgpu_buffer_rsrc_t rw = h ? rW1 : rW0;
+            const g16_u4 v0 = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 0));
+            const g16_u4 v1 = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rw, wo + 16, 0, 0));
+            wq[z][h][0] = v0.x; wq[z][h][1] = v0.y; wq[z][h][2] = v0.z; wq[z][h][3] = v0.w;
+            wq[z][h][4] = v1.x; wq[z][h][5] = v1.y; wq[z][h][6] = v1.z; wq[z][h][7] = v1.w;
+        }
+    };
+    // Start-up.  Loads complete in issue order, and every workgroup starts
+    // at once.  The tile's pair order is read first, alone (one barrier);
+    // then each wave issues the tile's rows, the scale / bias runs (DMA into
+    // LDS) and only then the ring's first D slots.
+    if (t < 16) {
+        int sr = -1, dr = -1;
+        if (t < len) {
+            dr = a.perm[first + t];
+            sr = a.x_by_pair ? dr : (dr < a.xpairs ? dr / a.K : dr - a.xpairs);
+        }
+        srow[t] = sr;
+        drow[t] = dr;
+    }
+    __syncthreads();
+    constexpr int AREG = 16 * GS_MAXK / 8 / G16_THREADS;   // uint4 a thread at most
+    const int au = 16 * words;                          // uint4 of the tile
+    g16_u4 ra[AREG];
+    const __amdgpu_buffer_rsrc_t rA = qw_rsrc(a.ah);
+#pragma unroll
+    for (int i = 0; i < AREG; i++) {
+        const int u = t + i * G16_THREADS, row = u / words, cw = u % words;
+        const int sr = u < au ? srow[row] : -1;
+        ra[i] = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(
+                    rA, sr >= 0 ? (uint32_t)((sr * k + cw * 8) * 2) : 0x80000000u, 0, 0));
+    }
+    const int mysr = t < 16 ? srow[t] : -1;
+    const float myF = mysr >= 0 ? a.aF[mysr] : 0.0f;
+    {
+        // run r: rows fb 128 .. of (gate s, gate b, up s, up b), contiguous
+        // in its bank; 1 KB slabs a wave instruction (lane l: bytes 16 l ..)
+        const int rows = min(128, a.n - fb * 128), rbytes = rows * groups * 2, slabs = RS / 1024;
+        const uint32_t off0 = (uint32_t)(fb * 128 * groups * 2);
+        for (int q = wave; q < 4 * slabs; q += G16_THREADS / 64) {
+            const int r = q / slabs, sl = q % slabs, h = r >> 1;
+            const uint16_t *bank = (r & 1) ? (xe ? (h ? a.xb1 : a.xb0) : (h ? a.b1 : a.b0))
+                                           : (xe ? (h ? a.xs1 : a.xs0) : (h ? a.s1 : a.s0));
+            if (!xe) bank += (size_t)expert * a.eg;
+            const int bo = sl * 1024 + lane * 16;
+            __attribute__((address_space(3))) uint8_t *dst =
+                (__attribute__((address_space(3))) uint8_t *)(&Sb[r * RS + sl * 1024]);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(qw_rsrc(bank), dst, 16,
+                                                     bo < rbytes ? off0 + (uint32_t)bo : 0x80000000u, 0, 0, 0);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(0, std::integral_constant<int, 0>{});
+    if constexpr (D > 1) fetch(1, std::integral_constant<int, 1>{});
+    if constexpr (D > 2) fetch(2, std::integral_constant<int, 2>{});
+    if constexpr (D > 3) fetch(3, std::integral_constant<int, 3>{});
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < AREG; i++) {
+        const int u = t + i * G16_THREADS, row = u / words, cw = u % words;
+        if (u < au) *reinterpret_cast<g16_u4 *>(&As[row * AST + cw * 8]) = ra[i];
+    }
+    if (t < 16) Fr[t] = myF;
+    // the runs landed (the ring's 4 D loads after them stay in flight)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * D) : "memory");
+    __syncthreads();
+    if (f0 >= a.n) return;      // (wave-uniform) no features of this wave
+
+    g16_f4 acc[2][2];
+#pragma unroll
+    for (int jj = 0; jj < 2; jj++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) acc[jj][h] = g16_f4{0.f, 0.f, 0.f, 0.f};
+    uint32_t lo = 0x64006400u, hi = 0x54005400u;
+    asm volatile("" : "+v"(lo), "+v"(hi));
+    // scale / bias of the lane's row j, group gl, run r (as bf16 bits; two
+    // groups in one dword where NGL = 2)
+    const uint8_t *sbl = &Sb[j * groups * 2];
+    auto sbat = [&](int r, int gl) -> uint32_t {
+        const uint8_t *p = sbl + r * RS + gl * 2;
+        return NGL == 2 ? *reinterpret_cast<const uint32_t *>(p) : *reinterpret_cast<const uint16_t *>(p);
+    };
+    auto step = [&](int c, auto zc) {
+        constexpr int z = decltype(zc)::value;
+        const int gl = (c * KC + kg * KPL) / G;
+        g16_h2 s2[2][NGL], b2[2][NGL];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t sv = sbat(2 * h, gl), bv = sbat(2 * h + 1, gl);
+#pragma unroll
+            for (int g = 0; g < NGL; g++) {
+                s2[h][g] = g16_bf2h2(sv, g);
+                b2[h][g] = g16_bf2h2(bv, g);
+            }
+        }
+        const _Float16 *ar = &As[ln * AST + c * KC + kg * KPL];
+#pragma unroll
+        for (int st = 0; st < WPL; st++) {
+            const g16_h8 af = *reinterpret_cast<const g16_h8 *>(ar + 8 * st);
+            const int g = NGL == 1 ? 0 : st * 8 / G;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                uint32_t d[4];
+                g16_dq(wq[z][h][st], s2[h][g], b2[h][g], lo, hi, d);
+                const g16_h8 bf = __builtin_bit_cast(g16_h8, g16_u4{d[0], d[1], d[2], d[3]});
+                acc[st & 1][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[st & 1][h], 0, 0, 0);
+            }
+        }
+        fetch(c + D, zc);
+    };
+    int c = 0;
+    for (; c + D <= nch; c += D) {
+        step(c, std::integral_constant<int, 0>{});
+        if constexpr (D > 1) step(c + 1, std::integral_constant<int, 1>{});
+        if constexpr (D > 2) step(c + 2, std::integral_constant<int, 2>{});
+        if constexpr (D > 3) step(c + 3, std::integral_constant<int, 3>{});
+    }
+    if (c < nch) { step(c, std::integral_constant<int, 0>{}); c++; }
+    if constexpr (D > 2) if (c < nch) { step(c, std::integral_constant<int, 1>{}); c++; }
+    if constexpr (D > 3) if (c < nch) { step(c, std::integral_constant<int, 2>{}); c++; }
+    // silu(F g) * (F u) of row 4 kg + e, feature f0 + ln, through the wave's
+    // LDS square; lane m < 16 then makes row m's unit
+    float *sq = Lw + wave * 16 * 17;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int m = 4 * kg + e;
+        const float fr = Fr[m];
+        sq[m * 17 + ln] = qw_silu(fr * (acc[0][0][e] + acc[1][0][e])) * (fr * (acc[0][1][e] + acc[1][1][e]));
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < 16) {
+        const int dr = drow[lane];
+        if (dr >= 0) {
+            float v[16];
+#pragma unroll
+            for (int q = 0; q < 16; q++) v[q] = sq[lane * 17 + q];
+            const int units = a.n >> 4;
+            uint4 *qv = (dr < a.qnpk ? a.qa + (size_t)dr * units * 3 : a.qs + (size_t)(dr - a.qnpk) * units * 3) +
+                        (size_t)(f0 >> 4) * 3;
+            qw_q16_stage(v, qv);
+        }
+    }
+}
+
 // ---- host side ---------------------------------------------------------------------
+
+// k_gmm16_stream's scale / bias runs move by 16-byte DMA: each bank and every
+// expert's start 16-byte aligned
+static bool gs_aligned(const qwk_q4 &m0, const qwk_q4 &m1, const qwk_gmm_extra *xb, long ew, long eg)
+{
+    (void)ew;
+    auto al = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
+    if (!al(m0.s) || !al(m0.b) || !al(m1.s) || !al(m1.b) || (eg * 2) % 16) return false;
+    return !xb || (al(xb->m0.s) && al(xb->m0.b) && al(xb->m1.s) && al(xb->m1.b));
+}
+
 
 extern "C" int qwk_stage16(hipStream_t s, uint16_t *hb, float *F, const float *x, int rows, int k)
 {
@@ -639,6 +863,18 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
     a.qa = q16 ? static_cast<uint4 *>(q16->qa) : nullptr;
     a.qs = q16 ? static_cast<uint4 *>(q16->qs) : nullptr;
     a.qnpk = q16 ? q16->npk : 0;
+    if (q16 && k % 256 == 0 && k <= GS_MAXK && k / group <= GS_MAXG && gs_aligned(m0, m1, xb, ew, eg)) {
+        // the decode batch's shape: one stream a wave
+        const unsigned grid = (unsigned)max_tiles * (unsigned)((n + 127) / 128);
+        if (max_tiles <= 0) return 0;
+        const dim3 b(G16_THREADS);
+        switch (group) {
+        case 32: hipLaunchKernelGGL((k_gmm16_stream<32, GS_DEPTH>), dim3(grid), b, 0, s, a); break;
+        case 64: hipLaunchKernelGGL((k_gmm16_stream<64, GS_DEPTH>), dim3(grid), b, 0, s, a); break;
+        default: hipLaunchKernelGGL((k_gmm16_stream<128, GS_DEPTH>), dim3(grid), b, 0, s, a); break;
+        }
+        return (int)hipGetLastError();
+    }
     a.nblk = swiglu ? (n + G16_BN / 2 - 1) / (G16_BN / 2) : (n + G16_BN - 1) / G16_BN;
     {
         // the largest scale / bias block (groups) that divides a row's groups
