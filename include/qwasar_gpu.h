@@ -392,15 +392,15 @@ bool qw_op_moe_layer_residual(qw_cmd c, qw_ref out, qw_ref idx, qw_ref w, qw_ref
  * counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  The launch's staging and hand-off state live in a
- * static device array of 768 KiB per GPU (held until the process ends), whose
+ * static device array of 2 MiB per GPU (held until the process ends), whose
  * address the library resolves at qw_gpu_init; this call makes no
  * allocation of any kind and gives qw_op_moe_layer's bits (the one-launch
  * path for one token, the batch path for 2..8).  False, nothing encoded,
  * where qw_op_moe_layer would not take a decode path (past 8 rows, or shapes
  * the decode kernels do not take), or where the layer's staging at `rows`
- * exceeds what the array holds past its 317 KiB hand-off state (462,080
- * bytes: config 1's shape at 8 rows stages 385,280; H 4096 with K 15 at 8
- * rows, 545,024, is refused, at 5 rows, 342,272, taken).
+ * exceeds what the array holds past its 317 KiB hand-off state (1,772,800
+ * bytes: config 1's shape at 8 rows stages 1,466,624; H 3072 with K 15 at 8
+ * rows, 2,101,504, is refused, at 6 rows, 1,577,216, taken).
  * Every call on one GPU shares the array and finds it as the last call
  * left it (the hand-off state stays valid between calls, and qw_gpu_init
  * zeroes it; the staging needs no clearing).  The outputs go on the

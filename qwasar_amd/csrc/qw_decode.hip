@@ -296,7 +296,7 @@ extern "C" int qwk_moe_decode_batch_supported(const qwk_moe *M, int rows)
 #define QB_TAB_INTS (1 + 4 * QD_MAXU + QD_MAXT)
 
 struct QbLayout {
-    size_t logits, tab, qx, qact, qsh, xh, xF, perm, tiles, act, total;
+    size_t logits, tab, qx, qact, qsh, xh, xF, perm, tiles, act, ey, total;
 };
 
 // The batch's gate / up runs on the matrix cores (qwk_gmm16, the shared
@@ -314,6 +314,19 @@ static bool qb_gmm(const qwk_moe *M)
 {
     return M->SI == M->I && qwk_gmm16_supported(M->H, M->group, (M->split ? M->gate : M->gate_up).w, qb_up_bank(M).w) &&
            qwk_gmm16_supported(M->H, M->group, M->sh_gate.w, M->sh_up.w);
+}
+
+// ... and both grouped products run as one weight stream a wave
+// (qwk_gmm16_stream: gate / up with fp32 activations, then the down into
+// per-pair rows and the combine) when they take the shapes and banks.
+static bool qb_stream(const qwk_moe *M)
+{
+    if (!qb_gmm(M)) return false;
+    const int G = M->group;
+    const qwk_q4 g0 = M->split ? M->gate : M->gate_up, u0 = qb_up_bank(M);
+    const qwk_gmm_extra xgu = {M->sh_gate, M->sh_up, M->E, 0}, xd = {M->sh_down, M->sh_down, M->E, 0};
+    return qwk_gmm16_stream_supported(M->H, M->I, G, 1, g0, u0, &xgu, (long)(M->split ? 1 : 2) * M->I * (M->H / G)) &&
+           qwk_gmm16_stream_supported(M->I, M->H, G, 0, M->down, M->down, &xd, (long)M->H * (M->I / G));
 }
 
 static QbLayout qb_layout(const qwk_moe *M, int rows)
@@ -335,6 +348,8 @@ static QbLayout qb_layout(const qwk_moe *M, int rows)
     L.perm = o;   o += gmm ? al((npk + rows) * 4) : 0;
     L.tiles = o;  o += gmm ? al((1 + 3 * ((size_t)QD_MAXU + 1)) * 4) : 0;
     L.act = o;    o += gmm ? al((npk + rows) * M->I * 4) : 0;
+    // the streamed down's rows: every pair's, then the shared expert's
+    L.ey = o;     o += qb_stream(M) ? al((npk + rows) * M->H * 4) : 0;
     L.total = o;
     return L;
 }
@@ -772,7 +787,9 @@ extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, flo
     const size_t rt_lds = std::max(few_lds, (size_t)rows * M->E * sizeof(float));
     if (rc) return rc;
     const int nrb8 = (a.n_down_rb + 7) / 8 * 8;
-    const qwk_gmm_extra xgu = {M->sh_gate, M->sh_up, M->E, npk};
+    const qwk_gmm_extra xgu = {M->sh_gate, M->sh_up, M->E, npk}, xd = {M->sh_down, M->sh_down, M->E, npk};
+    const bool stream = qb_stream(M);
+    float *ey = (float *)(S + L.ey);
     // the activations leave the grouped product directly as the down
     // launch's q16 vectors where it takes that form (16-row tiles), else as
     // fp32 for k_batch_act_q16
@@ -786,6 +803,18 @@ extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, flo
                                (uint2 *)tags, err, epoch);                                                    \
         else                                                                                                  \
             hipLaunchKernelGGL(k_batch_route<P_>, dim3(1), dim3(QD_MAXT * 64), 0, s, b);                      \
+        if (stream) {                                                                                         \
+            int rg = qwk_gmm16_stream(s, (float *)b.act, M->I, (const uint16_t *)(S + L.xh),                 \
+                                      (const float *)(S + L.xF), nullptr, b.perm, b.tiles, a.umax + 1, g0, u0, \
+                                      (long)(M->split ? 1 : 2) * M->I * (M->H / 8),                            \
+                                      (long)(M->split ? 1 : 2) * M->I * (M->H / G), M->H, M->I, M->K, 0, G, 1,\
+                                      &xgu, nullptr);                                                         \
+            if (!rg) rg = qwk_gmm16_stream(s, ey, M->H, nullptr, nullptr, b.act, b.perm, b.tiles, a.umax + 1,   \
+                                           M->down, M->down, (long)M->H * (M->I / 8), (long)M->H * (M->I / G), \
+                                           M->I, M->H, M->K, 1, G, 0, &xd, nullptr);                          \
+            if (!rg) rg = qwk_moe_combine(s, out, ey, w, ey + (size_t)npk * M->H, gl, rows, M->K, M->H);      \
+            return rg ? rg : (int)hipGetLastError();                                                          \
+        }                                                                                                     \
         if (b.gmm) {                                                                                          \
             const int rg = qwk_gmm16(s, (float *)b.act, M->I, (const uint16_t *)(S + L.xh),                   \
                                      (const float *)(S + L.xF), b.perm, b.tiles, a.umax + 1, g0, u0,           \

@@ -714,9 +714,20 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16_stream(Gmm16Args a)
     if (c < nch) { step(c, std::integral_constant<int, 0>{}); c++; }
     if constexpr (D > 2) if (c < nch) { step(c, std::integral_constant<int, 1>{}); c++; }
     if constexpr (D > 3) if (c < nch) { step(c, std::integral_constant<int, 2>{}); c++; }
-    // silu(F g) * (F u) of row 4 kg + e, feature f0 + ln, through the wave's
-    // LDS square; lane m < 16 then makes row m's unit
+    // silu(F g) * (F u) of row 4 kg + e, feature f0 + ln: fp32 into y, or
+    // through the wave's LDS square, lane m < 16 then making row m's unit
     float *sq = Lw + wave * 16 * 17;
+    if (!a.qa) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int m = 4 * kg + e, dr = drow[m];
+            const float fr = Fr[m];
+            if (dr >= 0 && f0 + ln < a.n)
+                a.y[(size_t)dr * a.ldy + f0 + ln] =
+                    qw_silu(fr * (acc[0][0][e] + acc[1][0][e])) * (fr * (acc[0][1][e] + acc[1][1][e]));
+        }
+        return;
+    }
 #pragma unroll
     for (int e = 0; e < 4; e++) {
         const int m = 4 * kg + e;
@@ -740,18 +751,196 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16_stream(Gmm16Args a)
     }
 }
 
-// ---- host side ---------------------------------------------------------------------
+// The same for the batch's down product: y[p] = A_p . W^T for every pair p
+// of a tile (its expert's n output rows over k = I inputs), fp32 out, the
+// combine left to the caller.  A workgroup owns one tile and 384 output
+// rows: wave w's weight tiles nt = 0..2 are rows rb0 + 16 (8 nt + w) ..
+// + 15, so the 8 waves read 128 consecutive rows at a time.  k is short
+// (I = 512: two chunks), so the ring holds all of a wave's words at once
+// where it can.  The tile's rows come in as fp32 activations (each row
+// p of A at ax + p k) and are staged in LDS as k_stage16 stages rows: one
+// power of two a row, f16, the 8-blocks in the weight words' order.
+#define GSD_MAXK 1024
+#define GSD_MAXG 16
+#define GSD_NT 3
+#define GSD_RB (GSD_NT * 16 * (G16_THREADS / 64))
+static __host__ __device__ inline int gsd_run_stride(int groups) { return (GSD_RB * groups * 2 + 1023) / 1024 * 1024; }
 
-// k_gmm16_stream's scale / bias runs move by 16-byte DMA: each bank and every
-// expert's start 16-byte aligned
-static bool gs_aligned(const qwk_q4 &m0, const qwk_q4 &m1, const qwk_gmm_extra *xb, long ew, long eg)
+template <int G>
+__global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16_stream_down(Gmm16Args a, const float *ax)
 {
-    (void)ew;
-    auto al = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
-    if (!al(m0.s) || !al(m0.b) || !al(m1.s) || !al(m1.b) || (eg * 2) % 16) return false;
-    return !xb || (al(xb->m0.s) && al(xb->m0.b) && al(xb->m1.s) && al(xb->m1.b));
+    constexpr int KC = 256, WPL = 8, KPL = 64, NGL = KPL > G ? KPL / G : 1, NT = GSD_NT, D = 2;
+    static_assert(NGL <= 2, "at most two groups a lane a chunk");
+    __shared__ __align__(16) _Float16 As[16 * (GSD_MAXK + 8)];
+    __shared__ __align__(16) uint8_t Sb[2 * GSD_RB * GSD_MAXG * 2];
+    __shared__ float Fr[16];
+    __shared__ int srow[16], drow[16];
+    const int k = a.k, AST = k + 8, words = k / 8, groups = k / G, nch = k / KC, RS = gsd_run_stride(groups);
+    const int nrb = (a.n + GSD_RB - 1) / GSD_RB, tile = blockIdx.x / nrb, rb0 = (blockIdx.x % nrb) * GSD_RB;
+    if (tile >= a.tiles[0]) return;
+    const int expert = a.tiles[1 + 3 * tile], first = a.tiles[2 + 3 * tile], len = a.tiles[3 + 3 * tile];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, ln = lane & 15, kg = lane >> 4;
+    const bool xe = expert == a.xe;
+    const __amdgpu_buffer_rsrc_t rW = qw_rsrc(xe ? a.xw0 : a.w0 + (size_t)expert * a.ew);
+    // the pair order first, alone (see k_gmm16_stream)
+    if (t < 16) {
+        int sr = -1, dr = -1;
+        if (t < len) {
+            dr = a.perm[first + t];
+            sr = a.x_by_pair ? dr : (dr < a.xpairs ? dr / a.K : dr - a.xpairs);
+        }
+        srow[t] = sr;
+        drow[t] = dr;
+    }
+    __syncthreads();
+    // the tile's rows: wave w stages rows w and w + 8, lane l the 8-blocks
+    // l, l + 64 (k <= 1024: at most 2 a lane)
+    constexpr int XB = GSD_MAXK / 8 / 64;
+    float4 xv[2][XB][2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int sr = srow[wave + 8 * h];
+#pragma unroll
+        for (int q = 0; q < XB; q++) {
+            const int b8 = lane + 64 * q;
+            const bool ok = sr >= 0 && b8 < words;
+            const float4 *src = reinterpret_cast<const float4 *>(ax + (size_t)(ok ? sr : 0) * k + (ok ? b8 : 0) * 8);
+            xv[h][q][0] = ok ? src[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+            xv[h][q][1] = ok ? src[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    {
+        // the scale and bias runs of the block's rows (contiguous in their
+        // banks), 1 KB slabs a wave instruction
+        const int rows = min(GSD_RB, a.n - rb0), rbytes = rows * groups * 2, slabs = RS / 1024;
+        const uint32_t off0 = (uint32_t)(rb0 * groups * 2);
+        for (int q = wave; q < 2 * slabs; q += G16_THREADS / 64) {
+            const int r = q / slabs, sl = q % slabs;
+            const uint16_t *bank = r ? (xe ? a.xb0 : a.b0 + (size_t)expert * a.eg) : (xe ? a.xs0 : a.s0 + (size_t)expert * a.eg);
+            const int bo = sl * 1024 + lane * 16;
+            __attribute__((address_space(3))) uint8_t *dst =
+                (__attribute__((address_space(3))) uint8_t *)(&Sb[r * RS + sl * 1024]);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(qw_rsrc(bank), dst, 16,
+                                                     bo < rbytes ? off0 + (uint32_t)bo : 0x80000000u, 0, 0, 0);
+        }
+    }
+    // the ring: chunk c's words of the wave's NT rows into slot z, 2 NT loads
+    uint32_t wq[D][NT][WPL];
+    auto rowof = [&](int nt) { return min(rb0 + 16 * (8 * nt + wave) + ln, a.n - 1); };
+    auto fetch = [&](int c, auto zc) {
+        constexpr int z = decltype(zc)::value;
+        c = min(c, nch - 1);
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const uint32_t wo = (uint32_t)(rowof(nt) * words + c * (KC / 8) + kg * WPL) * 4;
+            const g16_u4 v0 = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rW, wo, 0, 0));
+            const g16_u4 v1 = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rW, wo + 16, 0, 0));
+            wq[z][nt][0] = v0.x; wq[z][nt][1] = v0.y; wq[z][nt][2] = v0.z; wq[z][nt][3] = v0.w;
+            wq[z][nt][4] = v1.x; wq[z][nt][5] = v1.y; wq[z][nt][6] = v1.z; wq[z][nt][7] = v1.w;
+        }
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(0, std::integral_constant<int, 0>{});
+    fetch(1, std::integral_constant<int, 1>{});
+    __builtin_amdgcn_sched_barrier(0);
+    // stage: one power of two a row (its largest magnitude into [2^14,
+    // 2^15)), f16, each 8-block in the order 0,4,1,5,2,6,3,7
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int row = wave + 8 * h;
+        float mx = 0.0f;
+#pragma unroll
+        for (int q = 0; q < XB; q++)
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const float4 f = xv[h][q][u];
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w))));
+            }
+        mx = qw_wave_max(mx);
+        int sh = 0;
+        if (mx > 0.0f && mx <= 3.40282346638528859812e+38f) {
+            sh = 15 - __builtin_amdgcn_frexp_expf(mx);
+            sh = sh < -126 ? -126 : sh > 126 ? 126 : sh;
+        }
+        if (lane == 0) Fr[row] = srow[row] >= 0 ? __builtin_ldexpf(1.0f, -sh) : 0.0f;
+#pragma unroll
+        for (int q = 0; q < XB; q++) {
+            const int b8 = lane + 64 * q;
+            if (b8 < words) {
+                const float4 lo4 = xv[h][q][0], hi4 = xv[h][q][1];
+                const float v[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+                _Float16 hq[8];
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++) hq[jj] = (_Float16)__builtin_ldexpf(v[jj], sh);
+                *reinterpret_cast<g16_h8 *>(&As[row * AST + b8 * 8]) =
+                    g16_h8{hq[0], hq[4], hq[1], hq[5], hq[2], hq[6], hq[3], hq[7]};
+            }
+        }
+    }
+    // the runs landed (the ring's 4 NT loads after them stay in flight)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * NT) : "memory");
+    __syncthreads();
+
+    g16_f4 acc[2][NT];
+#pragma unroll
+    for (int jj = 0; jj < 2; jj++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[jj][nt] = g16_f4{0.f, 0.f, 0.f, 0.f};
+    uint32_t lo = 0x64006400u, hi = 0x54005400u;
+    asm volatile("" : "+v"(lo), "+v"(hi));
+    auto sbat = [&](int r, int j, int gl) -> uint32_t {
+        const uint8_t *p = &Sb[r * RS + (j * groups + gl) * 2];
+        return NGL == 2 ? *reinterpret_cast<const uint32_t *>(p) : *reinterpret_cast<const uint16_t *>(p);
+    };
+    auto step = [&](int c, auto zc) {
+        constexpr int z = decltype(zc)::value;
+        const int gl = (c * KC + kg * KPL) / G;
+        g16_h2 s2[NT][NGL], b2[NT][NGL];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int j = 16 * (8 * nt + wave) + ln;
+            const uint32_t sv = sbat(0, j, gl), bv = sbat(1, j, gl);
+#pragma unroll
+            for (int g = 0; g < NGL; g++) {
+                s2[nt][g] = g16_bf2h2(sv, g);
+                b2[nt][g] = g16_bf2h2(bv, g);
+            }
+        }
+        const _Float16 *ar = &As[ln * AST + c * KC + kg * KPL];
+#pragma unroll
+        for (int st = 0; st < WPL; st++) {
+            const g16_h8 af = *reinterpret_cast<const g16_h8 *>(ar + 8 * st);
+            const int g = NGL == 1 ? 0 : st * 8 / G;
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                uint32_t d[4];
+                g16_dq(wq[z][nt][st], s2[nt][g], b2[nt][g], lo, hi, d);
+                const g16_h8 bf = __builtin_bit_cast(g16_h8, g16_u4{d[0], d[1], d[2], d[3]});
+                acc[st & 1][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[st & 1][nt], 0, 0, 0);
+            }
+        }
+        fetch(c + D, zc);
+    };
+    int c = 0;
+    for (; c + 2 <= nch; c += 2) {
+        step(c, std::integral_constant<int, 0>{});
+        step(c + 1, std::integral_constant<int, 1>{});
+    }
+    if (c < nch) step(c, std::integral_constant<int, 0>{});
+    // y[pair of row 4 kg + e][output row] = F acc
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int m = 4 * kg + e, dr = drow[m];
+        const float fr = Fr[m];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int row = rb0 + 16 * (8 * nt + wave) + ln;
+            if (dr >= 0 && row < a.n) a.y[(size_t)dr * a.ldy + row] = fr * (acc[0][nt][e] + acc[1][nt][e]);
+        }
+    }
 }
 
+// ---- host side ---------------------------------------------------------------------
 
 extern "C" int qwk_stage16(hipStream_t s, uint16_t *hb, float *F, const float *x, int rows, int k)
 {
@@ -863,18 +1052,6 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
     a.qa = q16 ? static_cast<uint4 *>(q16->qa) : nullptr;
     a.qs = q16 ? static_cast<uint4 *>(q16->qs) : nullptr;
     a.qnpk = q16 ? q16->npk : 0;
-    if (q16 && k % 256 == 0 && k <= GS_MAXK && k / group <= GS_MAXG && gs_aligned(m0, m1, xb, ew, eg)) {
-        // the decode batch's shape: one stream a wave
-        const unsigned grid = (unsigned)max_tiles * (unsigned)((n + 127) / 128);
-        if (max_tiles <= 0) return 0;
-        const dim3 b(G16_THREADS);
-        switch (group) {
-        case 32: hipLaunchKernelGGL((k_gmm16_stream<32, GS_DEPTH>), dim3(grid), b, 0, s, a); break;
-        case 64: hipLaunchKernelGGL((k_gmm16_stream<64, GS_DEPTH>), dim3(grid), b, 0, s, a); break;
-        default: hipLaunchKernelGGL((k_gmm16_stream<128, GS_DEPTH>), dim3(grid), b, 0, s, a); break;
-        }
-        return (int)hipGetLastError();
-    }
     a.nblk = swiglu ? (n + G16_BN / 2 - 1) / (G16_BN / 2) : (n + G16_BN - 1) / G16_BN;
     {
         // the largest scale / bias block (groups) that divides a row's groups
@@ -918,6 +1095,68 @@ extern "C" int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ahb,
         case 32: g16_launch<32, 64>(s, a, swiglu, dense, grid, bm); break;
         case 64: g16_launch<64, 64>(s, a, swiglu, dense, grid, bm); break;
         default: g16_launch<128, 64>(s, a, swiglu, dense, grid, bm); break;
+        }
+    }
+    return (int)hipGetLastError();
+}
+
+// The decode batch's grouped products as one weight stream a wave: whether
+// the shapes and banks suit them, and the launch.
+extern "C" int qwk_gmm16_stream_supported(int k, int n, int group, int swiglu, qwk_q4 m0, qwk_q4 m1,
+                                          const qwk_gmm_extra *xb, long eg)
+{
+    if (group != 32 && group != 64 && group != 128) return 0;
+    if (k < 256 || k % 256 || n < 16 || n % 16 || (eg * 2) % 16) return 0;
+    if (swiglu ? (k > GS_MAXK || k / group > GS_MAXG) : (k > GSD_MAXK || k / group > GSD_MAXG)) return 0;
+    auto al = [](const void *p) { return p && ((uintptr_t)p & 15u) == 0; };
+    if (!al(m0.w) || !al(m0.s) || !al(m0.b)) return 0;
+    if (swiglu && (!al(m1.w) || !al(m1.s) || !al(m1.b))) return 0;
+    if (xb && (!al(xb->m0.w) || !al(xb->m0.s) || !al(xb->m0.b) ||
+               (swiglu && (!al(xb->m1.w) || !al(xb->m1.s) || !al(xb->m1.b)))))
+        return 0;
+    return 1;
+}
+
+extern "C" int qwk_gmm16_stream(hipStream_t s, float *y, long ldy, const uint16_t *ah, const float *aF,
+                                const float *ax, const int32_t *perm, const int32_t *tiles, int max_tiles,
+                                qwk_q4 m0, qwk_q4 m1, long ew, long eg, int k, int n, int K, int x_by_pair,
+                                int group, int swiglu, const qwk_gmm_extra *xb, const qwk_gmm_q16out *q16)
+{
+    if (!qwk_gmm16_stream_supported(k, n, group, swiglu, m0, m1, xb, eg) || !perm || !tiles || K < 1 ||
+        (swiglu ? (!ah || !aF || ((uintptr_t)ah & 15u) || (!q16 && !y)) : (!ax || ((uintptr_t)ax & 15u) || !y || q16)) ||
+        (q16 && (!q16->qa || !q16->qs)))
+        return (int)hipErrorInvalidValue;
+    if (max_tiles <= 0) return 0;
+    Gmm16Args a{};
+    a.y = y; a.ldy = ldy; a.ah = reinterpret_cast<const _Float16 *>(ah); a.aF = aF; a.perm = perm; a.tiles = tiles;
+    a.w0 = m0.w; a.s0 = m0.s; a.b0 = m0.b;
+    a.w1 = swiglu ? m1.w : m0.w; a.s1 = swiglu ? m1.s : m0.s; a.b1 = swiglu ? m1.b : m0.b;
+    a.ew = ew; a.eg = eg; a.k = k; a.n = n; a.K = K; a.x_by_pair = x_by_pair;
+    if (xb) {
+        a.xw0 = xb->m0.w; a.xs0 = xb->m0.s; a.xb0 = xb->m0.b;
+        a.xw1 = swiglu ? xb->m1.w : xb->m0.w; a.xs1 = swiglu ? xb->m1.s : xb->m0.s; a.xb1 = swiglu ? xb->m1.b : xb->m0.b;
+        a.xe = xb->expert; a.xpairs = xb->pairs;
+    } else {
+        a.xw0 = a.xw1 = m0.w; a.xs0 = a.xs1 = m0.s; a.xb0 = a.xb1 = m0.b;
+        a.xe = -1; a.xpairs = 0x7FFFFFFF;
+    }
+    a.qa = q16 ? static_cast<uint4 *>(q16->qa) : nullptr;
+    a.qs = q16 ? static_cast<uint4 *>(q16->qs) : nullptr;
+    a.qnpk = q16 ? q16->npk : 0;
+    const dim3 b(G16_THREADS);
+    if (swiglu) {
+        const dim3 grid((unsigned)max_tiles * (unsigned)((n + 127) / 128));
+        switch (group) {
+        case 32: hipLaunchKernelGGL((k_gmm16_stream<32, GS_DEPTH>), grid, b, 0, s, a); break;
+        case 64: hipLaunchKernelGGL((k_gmm16_stream<64, GS_DEPTH>), grid, b, 0, s, a); break;
+        default: hipLaunchKernelGGL((k_gmm16_stream<128, GS_DEPTH>), grid, b, 0, s, a); break;
+        }
+    } else {
+        const dim3 grid((unsigned)max_tiles * (unsigned)((n + GSD_RB - 1) / GSD_RB));
+        switch (group) {
+        case 32: hipLaunchKernelGGL(k_gmm16_stream_down<32>, grid, b, 0, s, a, ax); break;
+        case 64: hipLaunchKernelGGL(k_gmm16_stream_down<64>, grid, b, 0, s, a, ax); break;
+        default: hipLaunchKernelGGL(k_gmm16_stream_down<128>, grid, b, 0, s, a, ax); break;
         }
     }
     return (int)hipGetLastError();

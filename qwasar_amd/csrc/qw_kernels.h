@@ -102,6 +102,19 @@ typedef struct {
     int npk;
 } qwk_gmm_q16out;
 int qwk_gmm16_q16_supported(int k, int group, int tile_rows);
+/* The decode batch's grouped products (tiles of at most 16 rows, each tile
+ * one expert's pairs, the extra bank's tile the shared expert's rows), one
+ * weight stream a wave.  swiglu: the staged f16 rows ah / aF against gate
+ * (m0) and up (m1), out as q16 units (q16) or fp32 y[p][n]; else the down:
+ * the fp32 rows ax (row p at ax + p k) against m0, fp32 y[p][n].  Needs
+ * k % 256 == 0 (k <= 3072 and k / group <= 48 with swiglu, else k <= 1024
+ * and k / group <= 16), n % 16 == 0 and 16-byte aligned banks. */
+int qwk_gmm16_stream_supported(int k, int n, int group, int swiglu, qwk_q4 m0, qwk_q4 m1,
+                               const qwk_gmm_extra *xb, long eg);
+int qwk_gmm16_stream(hipStream_t s, float *y, long ldy, const uint16_t *ah, const float *aF,
+                     const float *ax, const int32_t *perm, const int32_t *tiles, int max_tiles,
+                     qwk_q4 m0, qwk_q4 m1, long ew, long eg, int k, int n, int K, int x_by_pair,
+                     int group, int swiglu, const qwk_gmm_extra *xb, const qwk_gmm_q16out *q16);
 int qwk_gmm16_supported(int k, int group, const void *w0, const void *w1);
 int qwk_gmm16(hipStream_t s, float *y, long ldy, const uint16_t *ah, const float *aF,
               const int32_t *perm, const int32_t *tiles, int max_tiles, qwk_q4 m0, qwk_q4 m1, long ew,
@@ -148,7 +161,7 @@ int qwk_decode_sync_words(void *sync, uint32_t **err, void **words, size_t *nwor
 /* The allocation-free decode entry's device scratch (qw_static.hip): a
  * file-scope device array of this many bytes per GPU, holding the hand-off
  * state and then the staging area. */
-#define QWK_STATIC_SCRATCH_BYTES (768u * 1024u)
+#define QWK_STATIC_SCRATCH_BYTES (2048u * 1024u)
 /* Resolves the array's address on the current device (hipGetSymbolAddress)
  * and zeroes it; once per device, at init.  Synchronous. */
 int qwk_static_init(hipStream_t s);

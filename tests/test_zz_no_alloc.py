@@ -43,21 +43,24 @@ def test_noalloc_refuses_oversized_staging(gpu):
     """Staging past the static array is refused with nothing encoded (no
     command is needed to ask); a fitting shape is accepted.  Several tokens
     take the batch path, whose staging (logits, the unique-expert table, the
-    f16 token rows, the pairs and tiles of the grouped gate / up, its fp32
-    activations and their q16 vectors) must fit the 462,080 bytes past the
-    hand-off state."""
+    f16 token rows, the pairs and tiles of the grouped products, their fp32
+    activations and, where the products stream, every pair's down row) must
+    fit the 1,772,800 bytes past the hand-off state.  The banks are one small
+    aligned buffer: only the shapes and the alignment are looked at."""
     r = gpu.NULL_REF
-    q = gpu.qw_q4_ref(r, r, r, 64)
-    # H 4096, K 15, I 512: 545,024 bytes at 8 rows do not fit, 342,272 at 5 do
-    big = gpu.qw_moe_layer(4096, 512, 15, 512, 512, True, True, r, q, q, q, q, q, q, q, r)
+    buf = gpu.Buf(4096)
+    q = gpu.qw_q4_ref(buf.ref(), buf.ref(), buf.ref(), 64)
+    # H 3072, K 15, I 512: 2,101,504 bytes at 8 rows do not fit, 1,577,216 at 6 do
+    big = gpu.qw_moe_layer(3072, 512, 15, 512, 512, True, True, buf.ref(), q, q, q, q, q, q, q, buf.ref())
     assert gpu.qw_op_moe_layer(None, r, r, r, r, big, 8)
     assert not gpu.qw_op_moe_layer_noalloc(None, r, r, r, r, big, 8)
-    assert gpu.qw_op_moe_layer_noalloc(None, r, r, r, r, big, 5)
+    assert gpu.qw_op_moe_layer_noalloc(None, r, r, r, r, big, 6)
     assert gpu.qw_op_moe_layer_noalloc(None, r, r, r, r, big, 1)
-    # config 1's shape: 385,280 bytes at 8 rows
-    small = gpu.qw_moe_layer(3072, 512, 10, 512, 512, True, True, r, q, q, q, q, q, q, q, r)
+    # config 1's shape: 1,466,624 bytes at 8 rows
+    small = gpu.qw_moe_layer(3072, 512, 10, 512, 512, True, True, buf.ref(), q, q, q, q, q, q, q, buf.ref())
     assert gpu.qw_op_moe_layer_noalloc(None, r, r, r, r, small, 8)
     assert not gpu.qw_op_moe_layer_noalloc(None, r, r, r, r, small, 9)   # past the decode path
+    buf.free()
 
 
 def test_noalloc_refreshes_caller_mirrors(gpu):
