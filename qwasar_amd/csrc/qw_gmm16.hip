@@ -720,10 +720,10 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16_stream(Gmm16Args a)
     if (!a.qa) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int m = 4 * kg + e, dr = drow[m];
+            const int m = 4 * kg + e;
             const float fr = Fr[m];
-            if (dr >= 0 && f0 + ln < a.n)
-                a.y[(size_t)dr * a.ldy + f0 + ln] =
+            if (m < len && f0 + ln < a.n)
+                a.y[(size_t)(first + m) * a.ldy + f0 + ln] =
                     qw_silu(fr * (acc[0][0][e] + acc[1][0][e])) * (fr * (acc[0][1][e] + acc[1][1][e]));
         }
         return;
@@ -752,29 +752,35 @@ __global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16_stream(Gmm16Args a)
 }
 
 // The same for the batch's down product: y[p] = A_p . W^T for every pair p
-// of a tile (its expert's n output rows over k = I inputs), fp32 out, the
-// combine left to the caller.  A workgroup owns one tile and 384 output
-// rows: wave w's weight tiles nt = 0..2 are rows rb0 + 16 (8 nt + w) ..
-// + 15, so the 8 waves read 128 consecutive rows at a time.  k is short
-// (I = 512: two chunks), so the ring holds all of a wave's words at once
-// where it can.  The tile's rows come in as fp32 activations (each row
-// p of A at ax + p k) and are staged in LDS as k_stage16 stages rows: one
+// of a tile (its expert's n output rows over k = I inputs), fp32 out by
+// pair, the combine left to the caller.  A workgroup owns one tile and
+// GSD_RB output rows; wave w walks its GSD_NB blocks of 16 rows, block bi
+// being rows rb0 + 16 (8 bi + w) .. + 15 (the 8 waves read 128 consecutive
+// rows at a time), a chunk of k a step, with a GSD_D-step register ring, so
+// that a wave dequantises and multiplies one block while the next ones'
+// words are in flight.  (With every word requested at once the dequant ran
+// as a tail after the last words landed: 18 us against 12.7 us of reads.)
+// The tile's rows come in as fp32 activations in slot order (row s of ax:
+// the pair at perm[s]) and are staged in LDS as k_stage16 stages rows: one
 // power of two a row, f16, the 8-blocks in the weight words' order.
 #define GSD_MAXK 1024
 #define GSD_MAXG 16
-#define GSD_NT 3
-#define GSD_RB (GSD_NT * 16 * (G16_THREADS / 64))
+#define GSD_NB 6
+#define GSD_D 4
+#define GSD_RB (GSD_NB * 16 * (G16_THREADS / 64))
+#define GSD_DMA ((2 * GSD_RB * GSD_MAXG * 2 / 1024 + G16_THREADS / 64 - 1) / (G16_THREADS / 64))
 static __host__ __device__ inline int gsd_run_stride(int groups) { return (GSD_RB * groups * 2 + 1023) / 1024 * 1024; }
 
 template <int G>
-__global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16_stream_down(Gmm16Args a, const float *ax)
+__global__ __launch_bounds__(G16_THREADS, 1) void k_gmm16_stream_down(Gmm16Args a, const float *ax)
 {
-    constexpr int KC = 256, WPL = 8, KPL = 64, NGL = KPL > G ? KPL / G : 1, NT = GSD_NT, D = 2;
+    constexpr int KC = 256, WPL = 8, KPL = 64, NGL = KPL > G ? KPL / G : 1, D = GSD_D;
     static_assert(NGL <= 2, "at most two groups a lane a chunk");
     __shared__ __align__(16) _Float16 As[16 * (GSD_MAXK + 8)];
     __shared__ __align__(16) uint8_t Sb[2 * GSD_RB * GSD_MAXG * 2];
+    __shared__ __align__(16) uint8_t Sd[1024];
     __shared__ float Fr[16];
-    __shared__ int srow[16], drow[16];
+    __shared__ int drow[16];
     const int k = a.k, AST = k + 8, words = k / 8, groups = k / G, nch = k / KC, RS = gsd_run_stride(groups);
     const int nrb = (a.n + GSD_RB - 1) / GSD_RB, tile = blockIdx.x / nrb, rb0 = (blockIdx.x % nrb) * GSD_RB;
     if (tile >= a.tiles[0]) return;
@@ -782,66 +788,62 @@ __global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16_stream_down(Gmm16Args 
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, ln = lane & 15, kg = lane >> 4;
     const bool xe = expert == a.xe;
     const __amdgpu_buffer_rsrc_t rW = qw_rsrc(xe ? a.xw0 : a.w0 + (size_t)expert * a.ew);
-    // the pair order first, alone (see k_gmm16_stream)
-    if (t < 16) {
-        int sr = -1, dr = -1;
-        if (t < len) {
-            dr = a.perm[first + t];
-            sr = a.x_by_pair ? dr : (dr < a.xpairs ? dr / a.K : dr - a.xpairs);
-        }
-        srow[t] = sr;
-        drow[t] = dr;
-    }
-    __syncthreads();
-    // the tile's rows: wave w stages rows w and w + 8, lane l the 8-blocks
-    // l, l + 64 (k <= 1024: at most 2 a lane)
+    const int T = GSD_NB * nch;                       // steps: block bi = s / nch, chunk s % nch
+    // Start-up.  The tile's rows are its slots first .. first + len - 1 of
+    // ax, so they need no pair order: they are requested first, then the
+    // slots' pair ids (wanted only at the end), the scale and bias runs
+    // (GSD_DMA 1 KB slabs a wave, a fixed count: the lanes of a slab past
+    // the runs read nothing and land in a spare KB) and last the ring's
+    // first D steps.  Staging waits for the rows alone.
     constexpr int XB = GSD_MAXK / 8 / 64;
     float4 xv[2][XB][2];
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-        const int sr = srow[wave + 8 * h];
+        const int m = wave + 8 * h;
 #pragma unroll
         for (int q = 0; q < XB; q++) {
             const int b8 = lane + 64 * q;
-            const bool ok = sr >= 0 && b8 < words;
-            const float4 *src = reinterpret_cast<const float4 *>(ax + (size_t)(ok ? sr : 0) * k + (ok ? b8 : 0) * 8);
+            const bool ok = m < len && b8 < words;
+            const float4 *src = reinterpret_cast<const float4 *>(ax + (size_t)(ok ? first + m : 0) * k + (ok ? b8 : 0) * 8);
             xv[h][q][0] = ok ? src[0] : make_float4(0.f, 0.f, 0.f, 0.f);
             xv[h][q][1] = ok ? src[1] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
+    const int mydr = t < 16 && t < len ? a.perm[first + t] : -1;
     {
-        // the scale and bias runs of the block's rows (contiguous in their
-        // banks), 1 KB slabs a wave instruction
+        // the runs of the block's rows (contiguous in their banks): slab q
+        // of 2 slabs is run q / slabs, its KB q % slabs
         const int rows = min(GSD_RB, a.n - rb0), rbytes = rows * groups * 2, slabs = RS / 1024;
         const uint32_t off0 = (uint32_t)(rb0 * groups * 2);
-        for (int q = wave; q < 2 * slabs; q += G16_THREADS / 64) {
-            const int r = q / slabs, sl = q % slabs;
+#pragma unroll
+        for (int i = 0; i < GSD_DMA; i++) {
+            const int q = wave + 8 * i, r = q / slabs, sl = q % slabs, bo = sl * 1024 + lane * 16;
+            const bool in = q < 2 * slabs;
             const uint16_t *bank = r ? (xe ? a.xb0 : a.b0 + (size_t)expert * a.eg) : (xe ? a.xs0 : a.s0 + (size_t)expert * a.eg);
-            const int bo = sl * 1024 + lane * 16;
             __attribute__((address_space(3))) uint8_t *dst =
-                (__attribute__((address_space(3))) uint8_t *)(&Sb[r * RS + sl * 1024]);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(qw_rsrc(bank), dst, 16,
-                                                     bo < rbytes ? off0 + (uint32_t)bo : 0x80000000u, 0, 0, 0);
+                (__attribute__((address_space(3))) uint8_t *)(in ? &Sb[r * RS + sl * 1024] : &Sd[0]);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(qw_rsrc(in ? bank : a.s0), dst, 16,
+                                                     in && bo < rbytes ? off0 + (uint32_t)bo : 0x80000000u, 0, 0, 0);
         }
     }
-    // the ring: chunk c's words of the wave's NT rows into slot z, 2 NT loads
-    uint32_t wq[D][NT][WPL];
-    auto rowof = [&](int nt) { return min(rb0 + 16 * (8 * nt + wave) + ln, a.n - 1); };
-    auto fetch = [&](int c, auto zc) {
+    // the ring: step s's words (block s / nch, chunk s % nch) into slot z, 2 loads
+    uint32_t wq[D][WPL];
+    auto rowof = [&](int bi) { return min(rb0 + 16 * (8 * bi + wave) + ln, a.n - 1); };
+    auto fetch = [&](int st, auto zc) {
         constexpr int z = decltype(zc)::value;
-        c = min(c, nch - 1);
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const uint32_t wo = (uint32_t)(rowof(nt) * words + c * (KC / 8) + kg * WPL) * 4;
-            const g16_u4 v0 = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rW, wo, 0, 0));
-            const g16_u4 v1 = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rW, wo + 16, 0, 0));
-            wq[z][nt][0] = v0.x; wq[z][nt][1] = v0.y; wq[z][nt][2] = v0.z; wq[z][nt][3] = v0.w;
-            wq[z][nt][4] = v1.x; wq[z][nt][5] = v1.y; wq[z][nt][6] = v1.z; wq[z][nt][7] = v1.w;
-        }
+        st = min(st, T - 1);
+        const int bi = st / nch, c = st % nch;
+        const uint32_t wo = (uint32_t)(rowof(bi) * words + c * (KC / 8) + kg * WPL) * 4;
+        const g16_u4 v0 = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rW, wo, 0, 0));
+        const g16_u4 v1 = __builtin_bit_cast(g16_u4, __builtin_amdgcn_raw_buffer_load_b128(rW, wo + 16, 0, 0));
+        wq[z][0] = v0.x; wq[z][1] = v0.y; wq[z][2] = v0.z; wq[z][3] = v0.w;
+        wq[z][4] = v1.x; wq[z][5] = v1.y; wq[z][6] = v1.z; wq[z][7] = v1.w;
     };
     __builtin_amdgcn_sched_barrier(0);
     fetch(0, std::integral_constant<int, 0>{});
     fetch(1, std::integral_constant<int, 1>{});
+    fetch(2, std::integral_constant<int, 2>{});
+    fetch(3, std::integral_constant<int, 3>{});
     __builtin_amdgcn_sched_barrier(0);
     // stage: one power of two a row (its largest magnitude into [2^14,
     // 2^15)), f16, each 8-block in the order 0,4,1,5,2,6,3,7
@@ -862,7 +864,7 @@ __global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16_stream_down(Gmm16Args 
             sh = 15 - __builtin_amdgcn_frexp_expf(mx);
             sh = sh < -126 ? -126 : sh > 126 ? 126 : sh;
         }
-        if (lane == 0) Fr[row] = srow[row] >= 0 ? __builtin_ldexpf(1.0f, -sh) : 0.0f;
+        if (lane == 0) Fr[row] = row < len ? __builtin_ldexpf(1.0f, -sh) : 0.0f;
 #pragma unroll
         for (int q = 0; q < XB; q++) {
             const int b8 = lane + 64 * q;
@@ -877,67 +879,68 @@ __global__ __launch_bounds__(G16_THREADS, 2) void k_gmm16_stream_down(Gmm16Args 
             }
         }
     }
-    // the runs landed (the ring's 4 NT loads after them stay in flight)
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * NT) : "memory");
+    if (t < 16) drow[t] = mydr;
+    // the runs landed (the ring's 2 D loads after them stay in flight)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * D) : "memory");
     __syncthreads();
 
-    g16_f4 acc[2][NT];
-#pragma unroll
-    for (int jj = 0; jj < 2; jj++)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) acc[jj][nt] = g16_f4{0.f, 0.f, 0.f, 0.f};
+    g16_f4 acc[2];
+    acc[0] = g16_f4{0.f, 0.f, 0.f, 0.f};
+    acc[1] = g16_f4{0.f, 0.f, 0.f, 0.f};
     uint32_t lo = 0x64006400u, hi = 0x54005400u;
     asm volatile("" : "+v"(lo), "+v"(hi));
-    auto sbat = [&](int r, int j, int gl) -> uint32_t {
-        const uint8_t *p = &Sb[r * RS + (j * groups + gl) * 2];
-        return NGL == 2 ? *reinterpret_cast<const uint32_t *>(p) : *reinterpret_cast<const uint16_t *>(p);
-    };
-    auto step = [&](int c, auto zc) {
+    int dr4[4];
+    float fr4[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        dr4[e] = drow[4 * kg + e];
+        fr4[e] = Fr[4 * kg + e];
+    }
+    auto step = [&](int st, auto zc) {
         constexpr int z = decltype(zc)::value;
+        const int bi = st / nch, c = st % nch, j = 16 * (8 * bi + wave) + ln;
         const int gl = (c * KC + kg * KPL) / G;
-        g16_h2 s2[NT][NGL], b2[NT][NGL];
+        const uint8_t *sp = &Sb[(j * groups + gl) * 2];
+        const uint32_t sv = NGL == 2 ? *reinterpret_cast<const uint32_t *>(sp) : *reinterpret_cast<const uint16_t *>(sp);
+        const uint32_t bv = NGL == 2 ? *reinterpret_cast<const uint32_t *>(sp + RS) : *reinterpret_cast<const uint16_t *>(sp + RS);
+        g16_h2 s2[NGL], b2[NGL];
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const int j = 16 * (8 * nt + wave) + ln;
-            const uint32_t sv = sbat(0, j, gl), bv = sbat(1, j, gl);
-#pragma unroll
-            for (int g = 0; g < NGL; g++) {
-                s2[nt][g] = g16_bf2h2(sv, g);
-                b2[nt][g] = g16_bf2h2(bv, g);
-            }
+        for (int g = 0; g < NGL; g++) {
+            s2[g] = g16_bf2h2(sv, g);
+            b2[g] = g16_bf2h2(bv, g);
         }
         const _Float16 *ar = &As[ln * AST + c * KC + kg * KPL];
 #pragma unroll
-        for (int st = 0; st < WPL; st++) {
-            const g16_h8 af = *reinterpret_cast<const g16_h8 *>(ar + 8 * st);
-            const int g = NGL == 1 ? 0 : st * 8 / G;
+        for (int s8 = 0; s8 < WPL; s8++) {
+            const g16_h8 af = *reinterpret_cast<const g16_h8 *>(ar + 8 * s8);
+            const int g = NGL == 1 ? 0 : s8 * 8 / G;
+            uint32_t d[4];
+            g16_dq(wq[z][s8], s2[g], b2[g], lo, hi, d);
+            const g16_h8 bf = __builtin_bit_cast(g16_h8, g16_u4{d[0], d[1], d[2], d[3]});
+            acc[s8 & 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[s8 & 1], 0, 0, 0);
+        }
+        fetch(st + D, zc);
+        if (c == nch - 1) {
+            // block bi done: y[pair of row 4 kg + e][its output row] = F acc
+            const int row = rb0 + 16 * (8 * bi + wave) + ln;
 #pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                uint32_t d[4];
-                g16_dq(wq[z][nt][st], s2[nt][g], b2[nt][g], lo, hi, d);
-                const g16_h8 bf = __builtin_bit_cast(g16_h8, g16_u4{d[0], d[1], d[2], d[3]});
-                acc[st & 1][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[st & 1][nt], 0, 0, 0);
+            for (int e = 0; e < 4; e++) {
+                if (dr4[e] >= 0 && row < a.n) a.y[(size_t)dr4[e] * a.ldy + row] = fr4[e] * (acc[0][e] + acc[1][e]);
             }
+            acc[0] = g16_f4{0.f, 0.f, 0.f, 0.f};
+            acc[1] = g16_f4{0.f, 0.f, 0.f, 0.f};
         }
-        fetch(c + D, zc);
     };
-    int c = 0;
-    for (; c + 2 <= nch; c += 2) {
-        step(c, std::integral_constant<int, 0>{});
-        step(c + 1, std::integral_constant<int, 1>{});
+    int st = 0;
+    for (; st + D <= T; st += D) {
+        step(st, std::integral_constant<int, 0>{});
+        step(st + 1, std::integral_constant<int, 1>{});
+        step(st + 2, std::integral_constant<int, 2>{});
+        step(st + 3, std::integral_constant<int, 3>{});
     }
-    if (c < nch) step(c, std::integral_constant<int, 0>{});
-    // y[pair of row 4 kg + e][output row] = F acc
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const int m = 4 * kg + e, dr = drow[m];
-        const float fr = Fr[m];
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const int row = rb0 + 16 * (8 * nt + wave) + ln;
-            if (dr >= 0 && row < a.n) a.y[(size_t)dr * a.ldy + row] = fr * (acc[0][nt][e] + acc[1][nt][e]);
-        }
-    }
+    if (st < T) { step(st, std::integral_constant<int, 0>{}); st++; }
+    if (st < T) { step(st, std::integral_constant<int, 1>{}); st++; }
+    if (st < T) { step(st, std::integral_constant<int, 2>{}); st++; }
 }
 
 // ---- host side ---------------------------------------------------------------------

@@ -105,8 +105,9 @@ int qwk_gmm16_q16_supported(int k, int group, int tile_rows);
 /* The decode batch's grouped products (tiles of at most 16 rows, each tile
  * one expert's pairs, the extra bank's tile the shared expert's rows), one
  * weight stream a wave.  swiglu: the staged f16 rows ah / aF against gate
- * (m0) and up (m1), out as q16 units (q16) or fp32 y[p][n]; else the down:
- * the fp32 rows ax (row p at ax + p k) against m0, fp32 y[p][n].  Needs
+ * (m0) and up (m1), out as q16 units (q16, by pair) or fp32 rows in slot
+ * order (y row s: the pair at perm[s]); else the down: the fp32 rows ax in
+ * that slot order against m0, out fp32 by pair, y[p][n].  Needs
  * k % 256 == 0 (k <= 3072 and k / group <= 48 with swiglu, else k <= 1024
  * and k / group <= 16), n % 16 == 0 and 16-byte aligned banks. */
 int qwk_gmm16_stream_supported(int k, int n, int group, int swiglu, qwk_q4 m0, qwk_q4 m1,
