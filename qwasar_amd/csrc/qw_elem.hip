@@ -40,19 +40,22 @@ __global__ void k_moe_combine(float *__restrict__ out, const float *__restrict__
     if (i >= H) return;
     const size_t row = (size_t)r * H;
     if (V4) {
+        // every load in flight together: the shared row's, then every
+        // slot's, unconditional (a slot past the last reads the last
+        // again), since a guarded load becomes a branch that waits for the
+        // loads before it; the shared term is used only after
+        const float4 shv = sh ? *reinterpret_cast<const float4 *>(sh + row + i) : make_float4(0.f, 0.f, 0.f, 0.f);
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (sh) {
-            const float gs = qw_sigmoid(g[r]);
-            const float4 v = *reinterpret_cast<const float4 *>(sh + row + i);
-            acc = make_float4(v.x * gs, v.y * gs, v.z * gs, v.w * gs);
-        }
-        // every slot's loads in flight together
         float4 yv[16];
         for (int k0 = 0; k0 < K; k0 += 16) {
             const int kn = min(16, K - k0);
 #pragma unroll
             for (int k = 0; k < 16; k++)
-                if (k < kn) yv[k] = *reinterpret_cast<const float4 *>(y + ((size_t)r * K + k0 + k) * H + i);
+                yv[k] = *reinterpret_cast<const float4 *>(y + ((size_t)r * K + k0 + min(k, kn - 1)) * H + i);
+            if (k0 == 0 && sh) {
+                const float gs = qw_sigmoid(g[r]);
+                acc = make_float4(shv.x * gs, shv.y * gs, shv.z * gs, shv.w * gs);
+            }
 #pragma unroll
             for (int k = 0; k < 16; k++)
                 if (k < kn) {
