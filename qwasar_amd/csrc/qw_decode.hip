@@ -493,24 +493,28 @@ __global__ __launch_bounds__(QD_MAXT * 64) void k_batch_route(QbArgs b)
     qb_route_body<PL>(b, b.logits);
 }
 
-// The router's logits and the routing in one launch: blocks (x < gridDim.x
-// - 1, y) are k_dmat_few's (the logits leave as tagged words, device scope);
-// the last block, (gridDim.x - 1, gridDim.y - 1), dispatched after every
-// other, polls them into LDS (wave r: token r's E logits, every tag
-// checked, bounded as the one-token launch's waits) and routes.  The grid's
-// other blocks of the last column return at once.
+// The router's logits and the routing in one launch: blocks (x < nxb, y)
+// are k_dmat_few's (the logits leave as tagged words, device scope); the
+// last block, (gridDim.x - 1, gridDim.y - 1), dispatched after every other,
+// polls them into LDS (wave r: token r's E logits, every tag checked,
+// bounded as the one-token launch's waits) and routes.  The grid's other
+// blocks past column nxb return at once.
 template <int PL>
 __global__ __launch_bounds__(QD_MAXT * 64) void k_batch_router(QbArgs b, uint2 *ty, uint32_t *err, uint32_t epoch)
 {
     extern __shared__ float xl[];
     const QdArgs &a = b.d;
     const int E = a.m.E, H = a.m.H;
-    if ((int)blockIdx.x < (int)gridDim.x - 1) {
+    // columns past the logits' (the grid is a multiple of 8 wide, so that
+    // column bx sits on XCD bx mod 8 for every group of token rows and its
+    // router rows are read from memory once, then from that XCD's L2)
+    const int nxb = (E + 1 + QW_DF_WAVES - 1) / QW_DF_WAVES;
+    if ((int)blockIdx.x < nxb) {
         qw_few_body<true>(nullptr, reinterpret_cast<float *>(b.tab + QB_TAB_GATE), a.x, a.m.router, a.m.sh_gate_w,
                           H, E, a.rows, nullptr, b.xh, b.xF, ty, epoch, blockIdx.x, blockIdx.y, xl);
         return;
     }
-    if (blockIdx.y != gridDim.y - 1) return;
+    if (blockIdx.y != gridDim.y - 1 || blockIdx.x != gridDim.x - 1) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     float *lg = xl;                                  // [rows][E]
     if (wave < a.rows) {
@@ -799,7 +803,7 @@ extern "C" int qwk_moe_decode_batch(hipStream_t s, float *out, int32_t *idx, flo
 #define QB_GO(L_, N_, D_, P_)                                                                                   \
     if (lpr_h == L_ && nul_h == N_ && nul_d == D_ && pl == P_) {                                              \
         if (fused)                                                                                            \
-            hipLaunchKernelGGL(k_batch_router<P_>, dim3(xblocks + 1, ygroups), dim3(QD_MAXT * 64), rt_lds, s, b, \
+            hipLaunchKernelGGL(k_batch_router<P_>, dim3((xblocks + 8) / 8 * 8, ygroups), dim3(QD_MAXT * 64), rt_lds, s, b,\
                                (uint2 *)tags, err, epoch);                                                    \
         else                                                                                                  \
             hipLaunchKernelGGL(k_batch_route<P_>, dim3(1), dim3(QD_MAXT * 64), 0, s, b);                      \

@@ -943,7 +943,23 @@ static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const floa
     if (!rc) rc = qwk_route(s, idx, w, logits, rows, E, K, M->norm ? 1 : 0);
     if (!rc) rc = qwk_moe_group(s, perm, tiles, idx, pairs, E, bm, mt, S + o_gw,
                                 qwk_moe_group_work_bytes(pairs, E), xr);
-    if (M->split) {
+    /* 16-row tiles: the grouped products as one weight stream a wave where
+     * they take the shapes (the down stages the activations itself) */
+    const qwk_q4 gb = M->split ? q4r(&M->gate) : q4r(&M->gate_up);
+    const qwk_q4 ub = M->split ? q4r(&M->up) : (qwk_q4){ gb.w + (size_t)I * words, gb.s + (size_t)I * groups,
+                                                        gb.b + (size_t)I * groups };
+    const long gew = (M->split ? 1L : 2L) * I * words, geg = (M->split ? 1L : 2L) * I * groups;
+    const bool stream = bm == 16 &&
+        qwk_gmm16_stream_supported(H, I, grp, 1, gb, ub, fuse ? &xgu : NULL, geg) &&
+        qwk_gmm16_stream_supported(I, H, grp, 0, q4r(&M->down), q4r(&M->down), fuse ? &xdn : NULL,
+                                   (long)H * (I / grp));
+    if (stream) {
+        if (!rc) rc = qwk_gmm16_stream(s, act, I, xh, xF, NULL, perm, tiles, mt, gb, ub, gew, geg, H, I, K, 0, grp, 1,
+                                       fuse ? &xgu : NULL, NULL);
+        if (!rc) rc = qwk_gmm16_stream(s, ey, H, NULL, NULL, act, perm, tiles, mt, q4r(&M->down), q4r(&M->down),
+                                       (long)H * (I / 8), (long)H * (I / grp), I, H, K, 1, grp, 0,
+                                       fuse ? &xdn : NULL, NULL);
+    } else if (M->split) {
         if (!rc) rc = qwk_gmm16(s, act, I, xh, xF, perm, tiles, mt, q4r(&M->gate), q4r(&M->up),
                                 (long)I * words, (long)I * groups, H, I, K, 0, grp, 1, 0, fuse ? &xgu : NULL, bm, NULL);
     } else {
@@ -952,9 +968,12 @@ static bool moe_prefill(qw_cmd c, float *out, int32_t *idx, float *w, const floa
         if (!rc) rc = qwk_gmm16(s, act, I, xh, xF, perm, tiles, mt, g0, u0,
                                 2L * I * words, 2L * I * groups, H, I, K, 0, grp, 1, 0, fuse ? &xgu : NULL, bm, NULL);
     }
-    if (!rc) rc = qwk_stage16(s, ah, aF, act, ntot, I);
-    if (!rc) rc = qwk_gmm16(s, ey, H, ah, aF, perm, tiles, mt, q4r(&M->down), q4r(&M->down),
-                            (long)H * (I / 8), (long)H * (I / grp), I, H, K, 1, grp, 0, 0, fuse ? &xdn : NULL, bm, NULL);
+    if (!stream) {
+        if (!rc) rc = qwk_stage16(s, ah, aF, act, ntot, I);
+        if (!rc) rc = qwk_gmm16(s, ey, H, ah, aF, perm, tiles, mt, q4r(&M->down), q4r(&M->down),
+                                (long)H * (I / 8), (long)H * (I / grp), I, H, K, 1, grp, 0, 0, fuse ? &xdn : NULL, bm,
+                                NULL);
+    }
     if (!fuse) {
         if (!rc) rc = qwk_gmm16(s, sa, SI, xh, xF, NULL, NULL, 0, q4r(&M->sh_gate), q4r(&M->sh_up),
                                 0, 0, H, SI, 1, 0, grp, 1, rows, NULL, 64, NULL);
