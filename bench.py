@@ -121,15 +121,26 @@ def select_cold_pool(gpu, lb, cand_x, K):
     return np.ascontiguousarray(cand_x[chosen]), ids[chosen]
 
 
+LEAD_ROWS = 2048          # one lead launch: the router's product over 2048 rows (~90 us)
+
+
 def time_decode(gpu, lb, xpool, steps, warmup, mode):
     """Times `steps` decode steps after `warmup` untimed ones.  mode "region":
     HIP events at the region's two ends only; "steps": an event after every
     step as well (per-step durations, for the median); "kernels": events
-    around every kernel launch as well (the decode kernel's own time)."""
+    around every kernel launch as well (the decode kernel's own time).
+
+    The region opens behind a lead of device work (router-shaped products,
+    ~30 us of it per step to come, over a scratch row block: no expert byte
+    is touched), so the host queues every step while the device is busy and
+    the region holds the steps back to back.  Without it the region also
+    holds whatever time the host takes to issue a step beyond the step's
+    device time (on one box ~26 us a step against a 20 us kernel)."""
     L = lb.L
     B = gpu.Buf
     xb = B.of(xpool)
     ob, ib, wb = B(L.H * 4), B(L.K * 4), B(L.K * 4)
+    lx, ly = B(LEAD_ROWS * L.H * 4), B(LEAD_ROWS * L.E * 4)
     row = L.H * 4
     c = gpu.qw_cmd_begin()
     for s in range(warmup):
@@ -138,7 +149,10 @@ def time_decode(gpu, lb, xpool, steps, warmup, mode):
     gpu.qw_prof_reset()
     gpu.qw_prof_set_enabled(True)
     gpu.qw_cmd_free(c)
-    c = gpu.qw_cmd_begin()                       # records the region's start event
+    c = gpu.qw_cmd_begin()
+    for _ in range(max(4, (steps * 30 + 89) // 90)):
+        gpu.qw_op_dmat_bf16(c, ly.ref(), lx.ref(), lb.router.ref(), L.H, L.E, LEAD_ROWS)
+    gpu.qw_cmd_mark(c, b"decode lead")           # the region opens here, on the device
     if mode == "steps":
         gpu.qw_cmd_mark(c, b"decode start")
     gpu.qw_prof_set_enabled(mode == "kernels")   # per-kernel events only when asked
@@ -159,6 +173,8 @@ def time_decode(gpu, lb, xpool, steps, warmup, mode):
         n = gpu.qw_prof_mark_times(b"decode step", buf, steps)
         res["per_step"] = np.array(buf[:n], np.float64)
     gpu.qw_prof_reset()
+    for t in (xb, ob, ib, wb, lx, ly):
+        t.free()
     return res
 
 

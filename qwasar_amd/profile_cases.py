@@ -3,7 +3,7 @@ counter passes kept as summaries beside the benchmark).  Each case sets up
 what bench.py sets up for it and runs only that, so a profile holds nothing
 else of note:
 
-    python3 -m qwasar_amd.profile_cases decode STEPS     config 1 decode, STEPS tokens (cold pool)
+    python3 -m qwasar_amd.profile_cases decode STEPS     config 1 decode, STEPS tokens (cold pool) after 20 warm-up
     python3 -m qwasar_amd.profile_cases prefill ROWS     one layer's prefill of ROWS uniform-routed rows, 5 passes
     python3 -m qwasar_amd.profile_cases config2 STEPS    config 2 (batch-8 decode), STEPS steps
     python3 -m qwasar_amd.profile_cases config4          the 48-layer stack (prefill 2048 rows, 256 decode steps)
@@ -75,7 +75,7 @@ def main(argv) -> None:
     if case == "decode":
         cand = synth.make_x(seed, 2048, L.H, name="bench.candidates")
         xpool, _ = bench.select_cold_pool(gpu, lb, cand, L.K)
-        r = bench.time_decode(gpu, lb, xpool, arg or 200, 0, "region")
+        r = bench.time_decode(gpu, lb, xpool, arg or 200, 20, "region")   # (as bench.py: warm-up steps first)
         print(json.dumps({"decode_steps": arg or 200, "us_per_token": round(r["region"] * 1e3 / (arg or 200), 3)}),
               flush=True)
         return
