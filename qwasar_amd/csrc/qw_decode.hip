@@ -502,6 +502,7 @@ __global__ __launch_bounds__(QD_MAXT * 64) void k_batch_route(QbArgs b)
 template <int PL>
 __global__ __launch_bounds__(QD_MAXT * 64) void k_batch_router(QbArgs b, uint2 *ty, uint32_t *err, uint32_t epoch)
 {
+    static_assert(QD_MAXT == QW_DF_WAVES, "the logits' body takes the launch's waves, one an output");
     extern __shared__ float xl[];
     const QdArgs &a = b.d;
     const int E = a.m.E, H = a.m.H;

@@ -15,7 +15,7 @@
 #define QW_DF_WAVES 8
 #define QW_DF_MAXR 8
 #define QW_DF_PAD 68
-#define QW_DF_TPG 2      // token rows a workgroup
+#define QW_DF_TPG 2      // token rows a workgroup (3: the same; 4: +2 us a config-2 step)
 // The body of one workgroup (bx, by) of k_dmat_few's grid, xl its dynamic
 // LDS.  TAGGED: the logits leave as tagged words {epoch, value} in ty (device
 // scope, past this XCD's L2) for a reader in the same launch, in place of y.
