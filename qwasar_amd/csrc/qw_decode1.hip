@@ -380,12 +380,12 @@ __device__ void qx_router(const QxArgs &a, int b, float *lds, float *qpart)
     const bool row = wave < QX_RT_ROWS && o <= E;
     float *xl = lds, *part = lds + 64 * QX_XPAD + wave * 64;
     uint32_t *wl = reinterpret_cast<uint32_t *>(lds + 64 * QX_XPAD + QX_WAVES * 64) + wave * 64 * QX_WPAD;
-    // (with RES the row scale comes first: held across its barrier the row's
-    // registers go to scratch)
-    float qinv = 1.0f;
-    if constexpr (RES) qinv = qx_norm(a, qpart, 0);
     // waves < QX_RT_ROWS load their rows (a wave past E loads the gate row and
-    // drops it) and pass them through LDS; the others stage the token
+    // drops it) and pass them through LDS; the others stage the token.  With
+    // RES the token's row scale comes from waves QX_RT_ROWS .. QX_RT_ROWS + 3
+    // while the rows are in flight, and the router waves meet its barrier with
+    // their rows already in LDS (no registers held across it)
+    float qinv = 1.0f;
     if (wave < QX_RT_ROWS) {
         const uint16_t *wr = o < E ? a.m.router + (size_t)o * H : a.m.sh_gate_w;
         uint4 v[8];
@@ -398,7 +398,9 @@ __device__ void qx_router(const QxArgs &a, int b, float *lds, float *qpart)
             const int i = lane + 64 * r;
             *reinterpret_cast<uint4 *>(wl + (i / 8) * QX_WPAD + (i % 8) * 4) = v[r];
         }
-    } else {
+    }
+    if constexpr (RES) qinv = qx_norm(a, qpart, 64 * QX_RT_ROWS);
+    if (wave >= QX_RT_ROWS) {
         for (int i = threadIdx.x - 64 * QX_RT_ROWS; i < H / 4; i += QX_THREADS - 64 * QX_RT_ROWS)
             *reinterpret_cast<float4 *>(xl + (i / 16) * QX_XPAD + (i % 16) * 4) = qx_x4<RES>(a, qinv, i);
     }
