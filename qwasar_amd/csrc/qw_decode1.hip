@@ -338,6 +338,7 @@ __device__ __forceinline__ float4 qx_x4(const QxArgs &a, float qinv, int i4)
 // 1 / sqrt(mean(v^2) + eps) of the row, by the 256 threads t0 .. t0 + 255 as
 // k_resid_rms_bf16's threads 0..255 (the whole workgroup calls it; it holds
 // a barrier)
+template <bool FENCE = true>
 __device__ __forceinline__ float qx_norm(const QxArgs &a, float *qpart, int t0)
 {
     const int tid = (int)threadIdx.x - t0, g = tid >> 6;
@@ -353,7 +354,8 @@ __device__ __forceinline__ float qx_norm(const QxArgs &a, float *qpart, int t0)
         }
     ss = qw_xor_sum<64>(ss);
     if ((tid & 63) == 0 && tid >= 0 && g < 4) qpart[g] = ss;
-    __syncthreads();
+    if constexpr (FENCE) __syncthreads();
+    else qx_barrier();           // (loads in flight stay in flight)
     float sum = qpart[0];
     sum = sum + qpart[1];
     sum = sum + qpart[2];
@@ -645,28 +647,35 @@ __device__ void qx_worker(const QxArgs &a, int x, int j, uint4 *lds, QxWorkLds &
     uint4 *xq = reinterpret_cast<uint4 *>(lb + L.xq);
     float *fp = reinterpret_cast<float *>(lb + L.fp);          // [8][nr]
 
-    // the token, staged as q16 units
-    float qinv = 1.0f;
-    if constexpr (RES) qinv = qx_norm(a, S.qpart, 0);
-    for (int u = threadIdx.x; u < UH; u += QX_THREADS) {
-        float v[16];
+    // the token, staged as q16 units (every thread calls it: it holds a
+    // barrier).  With RES it waits on the token's row scale (a read of the
+    // row, a barrier, a second read), so it runs while the picks are awaited,
+    // after the first requests (its barrier fence-free: they stay in flight);
+    // else first.
+    auto stage_token = [&]() {
+        float qinv = 1.0f;
+        if constexpr (RES) qinv = qx_norm<false>(a, S.qpart, 0);
+        for (int u = threadIdx.x; u < UH; u += QX_THREADS) {
+            float v[16];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const float4 f = qx_x4<RES>(a, qinv, 4 * u + q);
-            v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
-        }
-        qw_q16_stage(v, xs + 3 * u);
-    }
-    if constexpr (RES) {
-        if (x == 0 && j == 0)
-            for (int i = threadIdx.x; i < H / 4; i += QX_THREADS) {
-                const float4 v = qx_v4(a, i);
-                reinterpret_cast<uint2 *>(a.hout)[i] =
-                    make_uint2((__float_as_uint(v.x) >> 16) | (__float_as_uint(v.y) & 0xFFFF0000u),
-                               (__float_as_uint(v.z) >> 16) | (__float_as_uint(v.w) & 0xFFFF0000u));
-                reinterpret_cast<float4 *>(a.xout)[i] = make_float4(v.x * qinv, v.y * qinv, v.z * qinv, v.w * qinv);
+            for (int q = 0; q < 4; q++) {
+                const float4 f = qx_x4<RES>(a, qinv, 4 * u + q);
+                v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
             }
-    }
+            qw_q16_stage(v, xs + 3 * u);
+        }
+        if constexpr (RES) {
+            if (x == 0 && j == 0)
+                for (int i = threadIdx.x; i < H / 4; i += QX_THREADS) {
+                    const float4 v = qx_v4(a, i);
+                    reinterpret_cast<uint2 *>(a.hout)[i] =
+                        make_uint2((__float_as_uint(v.x) >> 16) | (__float_as_uint(v.y) & 0xFFFF0000u),
+                                   (__float_as_uint(v.z) >> 16) | (__float_as_uint(v.w) & 0xFFFF0000u));
+                    reinterpret_cast<float4 *>(a.xout)[i] = make_float4(v.x * qinv, v.y * qinv, v.z * qinv, v.w * qinv);
+                }
+        }
+    };
+    if constexpr (!RES) stage_token();
     // ---- requests.  Gate/up: row q of the worker (q < 2 np_) is pair
     // j + W (q / 2), gate (q even) or up; wave w's instruction i covers rows
     // (w + QX_GUW i) rpi + slot.  The shared expert needs no routing, so when
@@ -847,6 +856,7 @@ __device__ void qx_worker(const QxArgs &a, int x, int j, uint4 *lds, QxWorkLds &
                 sc_copy(0, 1);
             }
         }
+        if constexpr (RES) stage_token();
         // the picks of this XCD's gatherer, polled by a wave with nothing in
         // flight (a poll waits for its wave's earlier loads): the last gate/up
         // wave, whose rows are not the shared unit's (nq_sh <= QX_GUW - 1)
@@ -882,6 +892,7 @@ __device__ void qx_worker(const QxArgs &a, int x, int j, uint4 *lds, QxWorkLds &
             qx_barrier();
             issue_cp(0);
         }
+        if constexpr (RES) stage_token();
         qx_barrier();
         qx_barrier();
         issue_cp(1);
