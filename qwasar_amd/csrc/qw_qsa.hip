@@ -587,20 +587,24 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))
         }
         // per head: the wave's maximum over its positions (lane bits 3-5),
         // the online rescale, the weights (into this wave's slice of ps) and
-        // their sum in a fixed xor tree
+        // their sum in a fixed tree.  The 8 lanes of a position hold one
+        // value, so the xor steps 8, 16, 32 are a row mirror (it pairs
+        // position 2r with 2r + 1, as xor 8 does) and the row sums read from
+        // lanes 0, 16, 32, 48, added (0 + 16) + (32 + 48) as xor 16 then 32
+        // add them: the same bits, in the VALU (a shuffle goes through LDS)
 #pragma unroll
         for (int g = 0; g < G; g++) {
             const float sc = qw_xor_sum<8>(sg[g]);
             float cm = valid ? sc : -FLT_MAX;
-#pragma unroll
-            for (int o = 8; o < 64; o <<= 1) cm = fmaxf(cm, __shfl_xor(cm, o, 64));
+            cm = fmaxf(cm, qw_dpp<QW_DPP_MIRROR>(cm));
+            cm = fmaxf(fmaxf(qw_lane(cm, 0), qw_lane(cm, 16)), fmaxf(qw_lane(cm, 32), qw_lane(cm, 48)));
             const float mn = fmaxf(m[g], cm);
             const float rs = qa_exp2(m[g] - mn);
             m[g] = mn;
             float e = valid ? qa_exp2(sc - mn) : 0.0f;
             if (kp == 0) ps[g][jj] = e;
-#pragma unroll
-            for (int o = 8; o < 64; o <<= 1) e += __shfl_xor(e, o, 64);
+            e = e + qw_dpp<QW_DPP_MIRROR>(e);
+            e = (qw_lane(e, 0) + qw_lane(e, 16)) + (qw_lane(e, 32) + qw_lane(e, 48));
             l[g] = l[g] * rs + e;
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[g][i] *= rs;
