@@ -134,6 +134,20 @@ def test_config2_decode_batch8_shared_experts(gpu, c1):
     lb.free()
 
 
+@pytest.mark.parametrize("group", [32, 128])
+@pytest.mark.parametrize("rows", [3, 8, 64])
+def test_streamed_products_group_sizes(gpu, group, rows):
+    """The streamed grouped products (the batch decode at 3 and 8 rows; the
+    prefill's 16-row tiles at 64 rows, 4 pairs an expert on average) at the
+    group sizes besides 64: two groups in a lane's 64 inputs of a chunk (32)
+    and half a group (128), in the gate/up and in the down."""
+    L = synth.make_layer(4600 + group, H=512, E=64, K=4, I=256, SI=256, group=group, tag=f"sg{group}.")
+    lb = gpu.LayerBufs(L)
+    x = synth.make_x(4700 + rows, rows, L.H)
+    check(run_layer(gpu, lb, x), ref.moe_forward(L, x), DECODE_REL if rows <= 8 else 1e-3)
+    lb.free()
+
+
 def test_config3_prefill_sample(gpu):
     """512-token prefill with Zipf-skewed routing: every token's routing
     bit-exact; outputs of a sample of tokens against the oracle."""
