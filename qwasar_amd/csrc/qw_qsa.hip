@@ -140,21 +140,14 @@ __device__ __forceinline__ void qs_score_rows(float *__restrict__ scores, const 
     }
 }
 
+// Phase 1: the workgroup's QS_BLK block keys into LDS, row stride D + 4, dims
+// past d and blocks from nb_hi on zero.
 template <int D, bool POOLED>
-__global__ void __launch_bounds__(QS_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) k_qsa_scores(float *__restrict__ scores, const float *__restrict__ qn,
-                                                           const float *__restrict__ src,
-                                                           const uint16_t *__restrict__ kw,
-                                                           const float *__restrict__ inv_freq, int rows, int nq,
-                                                           int d, int ratio, int base_pos, int max_blocks, float eps)
+__device__ __forceinline__ void qs_keys_to_lds(float *kl, const float *__restrict__ src, const uint16_t *__restrict__ kw,
+                                               const float *__restrict__ inv_freq, int b0, int nb_hi, int d,
+                                               int ratio, float eps)
 {
-    extern __shared__ float4 qs_lds[];
-    float *kl = reinterpret_cast<float *>(qs_lds);            // [QS_BLK][D + 4]
-    float *part = kl + QS_BLK * (D + 4);                       // [4][QS_BLK]
-    float *ql = part + 4 * QS_BLK;                             // [nq][D]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int b0 = blockIdx.x * QS_BLK, r0 = blockIdx.y * QS_ROWS;
-    const int nb_hi = (base_pos + min(r0 + QS_ROWS, rows)) / ratio;   // blocks any row of the tile sees
-    if (nb_hi <= b0) return;                                   // uniform
     if (POOLED) {
         for (int i = tid; i < QS_BLK * (D / 4); i += QS_THREADS) {
             const int bl = i / (D / 4), j = 4 * (i % (D / 4));
@@ -177,8 +170,117 @@ __global__ void __launch_bounds__(QS_THREADS) __attribute__((amdgpu_waves_per_eu
             for (int m = 0; m < D / 64; m++) kl[bl * (D + 4) + lane + 64 * m] = kn[m];
         }
     }
+}
+
+template <int D, bool POOLED>
+__global__ void __launch_bounds__(QS_THREADS) __attribute__((amdgpu_waves_per_eu(1, 2))) k_qsa_scores(float *__restrict__ scores, const float *__restrict__ qn,
+                                                           const float *__restrict__ src,
+                                                           const uint16_t *__restrict__ kw,
+                                                           const float *__restrict__ inv_freq, int rows, int nq,
+                                                           int d, int ratio, int base_pos, int max_blocks, float eps)
+{
+    extern __shared__ float4 qs_lds[];
+    float *kl = reinterpret_cast<float *>(qs_lds);            // [QS_BLK][D + 4]
+    float *part = kl + QS_BLK * (D + 4);                       // [4][QS_BLK]
+    float *ql = part + 4 * QS_BLK;                             // [nq][D]
+    const int b0 = blockIdx.x * QS_BLK, r0 = blockIdx.y * QS_ROWS;
+    const int nb_hi = (base_pos + min(r0 + QS_ROWS, rows)) / ratio;   // blocks any row of the tile sees
+    if (nb_hi <= b0) return;                                   // uniform
+    qs_keys_to_lds<D, POOLED>(kl, src, kw, inv_freq, b0, nb_hi, d, ratio, eps);
     __syncthreads();
     qs_score_rows<D>(scores, qn, kl, ql, part, b0, r0, rows, nq, d, ratio, base_pos, max_blocks);
+}
+
+// The same scores on the fp32 matrix cores (nq <= 16, D <= 128, many rows).
+// v_mfma_f32_16x16x1_4b_f32 adds a 16x16 outer product to its accumulator in
+// each of four blocks, one rounding per element: element (i, j) of a block
+// takes fmaf(a_i, b_j, c), so D of them in dim order are phase 2's chain
+// (from 0, dims ascending), bit for bit.  Lane l feeds B column l % 16 of
+// block l / 16 with its own block's key -- block b0 + l, held in registers
+// for the whole tile -- and A row l % 16 of every block with one query row's
+// head hd(l % 16), hd(i) = 4 (i % 4) + i / 4 (heads past nq zero: a zero dot,
+// never summed).  Accumulator e of lane l is then block column 16 (e / 4) +
+// l % 16 against A row 4 (l / 16) + e % 4, head l / 16 + 4 (e % 4): the lanes
+// of group g = l / 16 hold heads g, g + 4, g + 8, g + 12 in e order, the
+// heads phase 2's wave g sums, in its order.  Two xor shuffles (16, then 32)
+// form (p0 + p1) + (p2 + p3) (each pair's sum the same bits whichever lane
+// adds it), and lane l writes block b0 + l.  A workgroup scores its 64 blocks
+// against QM_ROWS rows, eight at a time: the eight rows' heads are staged in
+// LDS (over the block keys, once those are in registers), each wave runs two
+// rows' chains interleaved.
+#define QM_ROWS 32
+#define QM_GROUP 8                                 // rows staged at once: 2 a wave
+template <int D, bool POOLED>
+__global__ void __launch_bounds__(QS_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) k_qsa_scores_mx(
+    float *__restrict__ scores, const float *__restrict__ qn, const float *__restrict__ src,
+    const uint16_t *__restrict__ kw, const float *__restrict__ inv_freq, int rows, int nq, int d, int ratio,
+    int base_pos, int max_blocks, float eps)
+{
+    typedef float f16v __attribute__((ext_vector_type(4 * 4)));
+    constexpr int QST = 16 * (D + 4);                          // floats a staged row
+    __shared__ float4 lds4[(QM_GROUP * QST > QS_BLK * (D + 4) ? QM_GROUP * QST : QS_BLK * (D + 4)) / 4];
+    float *lds = reinterpret_cast<float *>(lds4);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int b0 = blockIdx.x * QS_BLK, r0 = blockIdx.y * QM_ROWS;
+    const int rend = min(r0 + QM_ROWS, rows);
+    const int nb_hi = (base_pos + rend) / ratio;
+    if (nb_hi <= b0) return;                                   // uniform
+    qs_keys_to_lds<D, POOLED>(lds, src, kw, inv_freq, b0, nb_hi, d, ratio, eps);
+    __syncthreads();
+    float kr[D];
+#pragma unroll
+    for (int i = 0; i < D; i += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(lds + lane * (D + 4) + i);
+        kr[i] = v.x; kr[i + 1] = v.y; kr[i + 2] = v.z; kr[i + 3] = v.w;
+    }
+    const float rs = sqrtf((float)d);
+    const int g = lane >> 4;
+    const float *qa = lds + (2 * wave) * QST + (lane & 15) * (D + 4), *qb = qa + QST;
+    for (int g0 = r0; g0 < rend; g0 += QM_GROUP) {
+        const int gl = min(g0 + QM_GROUP, rend);
+        if ((base_pos + gl) / ratio <= b0) continue;           // uniform: no row of the group sees these blocks
+        __syncthreads();                                       // the keys are in registers / the last group is done
+        // stage: A row i of staged row t holds head hd(i) (4 x 4 transpose: its own inverse)
+        for (int q = tid; q < QM_GROUP * 16 * (D / 4); q += QS_THREADS) {
+            const int t = q / (16 * (D / 4)), i = (q / (D / 4)) % 16, j = 4 * (q % (D / 4));
+            const int h = 4 * (i % 4) + i / 4, r = g0 + t;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (r < gl && h < nq && j < d) v = *reinterpret_cast<const float4 *>(qn + ((size_t)r * nq + h) * d + j);
+            *reinterpret_cast<float4 *>(lds + t * QST + i * (D + 4) + j) = v;
+        }
+        __syncthreads();
+        f16v acc0 = {}, acc1 = {};
+#pragma unroll
+        for (int k = 0; k < D; k += 4) {
+            const float4 a0 = *reinterpret_cast<const float4 *>(qa + k), a1 = *reinterpret_cast<const float4 *>(qb + k);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x1f32(a0.x, kr[k], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x1f32(a1.x, kr[k], acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x1f32(a0.y, kr[k + 1], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x1f32(a1.y, kr[k + 1], acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x1f32(a0.z, kr[k + 2], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x1f32(a1.z, kr[k + 2], acc1, 0, 0, 0);
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x1f32(a0.w, kr[k + 3], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x1f32(a1.w, kr[k + 3], acc1, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int r = g0 + 2 * wave + u;
+            const f16v &acc = u ? acc1 : acc0;
+            float mine = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                float p = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+                    if (acc[4 * c + t] > 0.0f) p += acc[4 * c + t];
+                const float x = p + __shfl_xor(p, 16, 64);
+                const float sc = x + __shfl_xor(x, 32, 64);
+                if (c == g) mine = sc;
+            }
+            const int b = b0 + lane;
+            if (r < gl && b < (base_pos + r + 1) / ratio) scores[(size_t)r * max_blocks + b] = mine / rs;
+        }
+    }
 }
 
 template <int M>
@@ -768,6 +870,8 @@ __global__ void __launch_bounds__(256) k_attn_merge(float *__restrict__ out, con
 
 // ---- launchers ----------------------------------------------------------------------
 
+#define QS_MX_MIN_ROWS 16                  // rows from which the scores take the matrix cores
+
 static bool qs_shape_ok(int d, int rotary_dim) { return rotary_dim == QS_ROTARY && d >= 64 && d % 32 == 0 && d <= 256; }
 
 template <bool POOLED>
@@ -779,6 +883,16 @@ static int qs_launch_scores(hipStream_t s, float *scores, const float *qn, const
     if (blocks == 0) return 0;
     const dim3 grid((blocks + QS_BLK - 1) / QS_BLK, (rows + QS_ROWS - 1) / QS_ROWS);
     const int D = d <= 64 ? 64 : d <= 128 ? 128 : d <= 192 ? 192 : 256;
+    if (rows >= QS_MX_MIN_ROWS && nq <= 16 && D <= 128) {
+        const dim3 gm((blocks + QS_BLK - 1) / QS_BLK, (rows + QM_ROWS - 1) / QM_ROWS);
+        if (D == 64)
+            hipLaunchKernelGGL((k_qsa_scores_mx<64, POOLED>), gm, dim3(QS_THREADS), 0, s, scores, qn, src, kw, inv_freq,
+                               rows, nq, d, ratio, base_pos, max_blocks, eps);
+        else
+            hipLaunchKernelGGL((k_qsa_scores_mx<128, POOLED>), gm, dim3(QS_THREADS), 0, s, scores, qn, src, kw, inv_freq,
+                               rows, nq, d, ratio, base_pos, max_blocks, eps);
+        return (int)hipGetLastError();
+    }
     const size_t lds = ((size_t)QS_BLK * (D + 4) + 4 * QS_BLK + (size_t)nq * D) * sizeof(float);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
 #define QS_GO(DD) hipLaunchKernelGGL((k_qsa_scores<DD, POOLED>), grid, dim3(QS_THREADS), lds, s, scores, qn, src, kw, \

@@ -100,6 +100,31 @@ def test_qsa_scores_and_pooled(gpu, rows, base, max_ctx, d):
 
 # ---- selection -------------------------------------------------------------------
 
+@pytest.mark.parametrize("nq,d,base,rows", [(16, 128, 4000, 48), (12, 96, 130, 40), (16, 64, 0, 33)])
+@pytest.mark.parametrize("pooled", [False, True])
+def test_qsa_scores_matrix_cores_match_rowwise(gpu, nq, d, base, rows, pooled):
+    """From 16 rows on (nq <= 16, d <= 128) the scores run on the fp32 matrix
+    cores; one row at a time they take the per-thread fma chains.  Both are
+    the same chain of fmas per head, so every score agrees bit for bit:
+    rows that straddle block boundaries, a ragged last row group, fewer heads
+    than the instruction's rows and a head size under 128."""
+    ratio = int(FX["ratio"])
+    mb = (base + rows) // ratio + 3
+    kw = FX["k_norm"] if d == 128 else synth.to_bf16(1.0 + 0.1 * rnd(d, d + nq))
+    qn, ik, inv = rnd((rows, nq, d), 61 + d), rnd((mb * ratio, d), 62 + d), rope_inv()
+    got, _ = gpu_scores(gpu, qn, ik, kw, inv, rows, nq, d, ratio, base, mb, pooled=pooled)
+    assert rows >= 16
+    for r in range(rows):
+        one, _ = gpu_scores(gpu, qn[r:r + 1], ik, kw, inv, 1, nq, d, ratio, base + r, mb, pooled=pooled)
+        nb = (base + r + 1) // ratio
+        assert same_bits(got[r, :nb], one[0, :nb]), f"row {r}"
+        assert np.isnan(got[r, nb:]).all(), f"row {r}: entries past the row's complete blocks are left alone"
+    want = sparse.qsa_scores(qn, ik, kw, inv, rows, nq, d, ratio, base, 64, mb, EPS)
+    for r in range(rows):
+        nb = (base + r + 1) // ratio
+        assert np.all(np.abs(got[r, :nb] - want[r, :nb]) <= 1e-5 * (1 + np.abs(want[r, :nb]))), f"row {r}"
+
+
 def gpu_select(gpu, scores, rows, ratio, base, topk, max_ctx, max_blocks):
     B = gpu.Buf
     cap = gpu.qw_qsa_list_cap(topk, ratio)
