@@ -31,6 +31,17 @@ __device__ __forceinline__ float qg_softplus(float x) { return x > 20.0f ? x : l
 
 // ---- causal conv ------------------------------------------------------------
 
+// Output t of a channel depends only on the inputs t - KS + 1 .. t (the
+// carried window standing in for t < 0), never on an earlier output, so the
+// launch runs over (channel, run of QG_CONV_T steps) in parallel: a thread
+// a channel of one run, its window loaded once, each step one fma chain over
+// the taps oldest first (from 0) and silu.  Snapshot t (t < n_snap) is the
+// window after step t: inputs t - KS + 2 .. t.  The thread of a channel's
+// first run is the only one that reads the carried window, and it also writes
+// the window after the last step (the last KS - 1 inputs, older ones from the
+// window it read), so the window is updated in place without a race between
+// workgroups.
+#define QG_CONV_T 16
 template <int KS>
 __global__ void __launch_bounds__(256) k_conv1d_causal_silu(float *__restrict__ y, const float *__restrict__ x,
                                                             float *__restrict__ state, const uint16_t *__restrict__ w,
@@ -39,28 +50,46 @@ __global__ void __launch_bounds__(256) k_conv1d_causal_silu(float *__restrict__ 
 {
     const int ch = blockIdx.x * 256 + threadIdx.x;
     if (ch >= channels) return;
-    float taps[KS], win[KS];
+    const int t0 = blockIdx.y * QG_CONV_T, t1 = min(t0 + QG_CONV_T, rows);
+    float taps[KS], win[KS + QG_CONV_T], old[KS - 1];
 #pragma unroll
     for (int j = 0; j < KS; j++) taps[j] = qw_bf16(w[(size_t)ch * KS + j]);
+    // win[i] = input t0 - (KS - 1) + i
+    if (t0 == 0) {
 #pragma unroll
-    for (int j = 0; j < KS - 1; j++) win[j] = state[(size_t)j * channels + ch];
-    float nx = rows > 0 ? x[ch] : 0.0f;
-    for (int t = 0; t < rows; t++) {
-        win[KS - 1] = nx;
-        if (t + 1 < rows) nx = x[(size_t)(t + 1) * channels + ch];
-        float acc = 0.0f;
+        for (int j = 0; j < KS - 1; j++) win[j] = old[j] = state[(size_t)j * channels + ch];
+    } else {
 #pragma unroll
-        for (int j = 0; j < KS; j++) acc = __builtin_fmaf(win[j], taps[j], acc);
-        y[(size_t)t * channels + ch] = acc / (1.0f + expf(-acc));
-#pragma unroll
-        for (int j = 0; j < KS - 1; j++) win[j] = win[j + 1];
-        if (t < n_snap) {
-#pragma unroll
-            for (int j = 0; j < KS - 1; j++) snap[(size_t)t * snap_stride + (size_t)j * channels + ch] = win[j];
-        }
+        for (int j = 0; j < KS - 1; j++) win[j] = x[(size_t)(t0 - (KS - 1) + j) * channels + ch];
     }
 #pragma unroll
-    for (int j = 0; j < KS - 1; j++) state[(size_t)j * channels + ch] = win[j];
+    for (int u = 0; u < QG_CONV_T; u++) win[KS - 1 + u] = t0 + u < t1 ? x[(size_t)(t0 + u) * channels + ch] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < QG_CONV_T; u++) {
+        const int t = t0 + u;
+        if (t < t1) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KS; j++) acc = __builtin_fmaf(win[u + j], taps[j], acc);
+            y[(size_t)t * channels + ch] = acc / (1.0f + expf(-acc));
+            if (t < n_snap) {
+#pragma unroll
+                for (int j = 0; j < KS - 1; j++) snap[(size_t)t * snap_stride + (size_t)j * channels + ch] = win[u + 1 + j];
+            }
+        }
+    }
+    if (t0 == 0) {
+        // the window after the last step: inputs rows - KS + 1 .. rows - 1
+#pragma unroll
+        for (int j = 0; j < KS - 1; j++) {
+            const int t = rows - (KS - 1) + j;
+            float v = 0.0f;
+#pragma unroll
+            for (int m = 0; m < KS - 1; m++)
+                if (m == KS - 1 + t) v = old[m];                       // rows < KS - 1: from the window read
+            state[(size_t)j * channels + ch] = t >= 0 ? x[(size_t)t * channels + ch] : v;
+        }
+    }
 }
 
 // ---- gates ------------------------------------------------------------------
@@ -240,7 +269,8 @@ extern "C" int qwk_conv1d_causal_silu(hipStream_t s, float *y, const float *x, f
     if (ksize != 4 || channels < 1 || rows < 0 || n_snap < 0 || (n_snap > 0 && (!snap || snap_stride < 3 * channels)))
         return hipErrorInvalidValue;
     if (rows == 0) return 0;
-    hipLaunchKernelGGL(k_conv1d_causal_silu<4>, dim3((channels + 255) / 256), dim3(256), 0, s, y, x, state, w,
+    hipLaunchKernelGGL(k_conv1d_causal_silu<4>, dim3((channels + 255) / 256, (rows + QG_CONV_T - 1) / QG_CONV_T),
+                       dim3(256), 0, s, y, x, state, w,
                        channels, rows, snap, n_snap, snap_stride);
     return (int)hipGetLastError();
 }

@@ -255,21 +255,51 @@ def test_attn_masked_split_merge(gpu, rows, qh, kvh, base):
 
 # ---- gated DeltaNet ----------------------------------------------------------------
 
-@pytest.mark.parametrize("channels,rows", [(1024, 1), (1024, 7), (10240, 3)])
-def test_conv1d_causal_silu(gpu, channels, rows):
+@pytest.mark.parametrize("channels,rows,n_snap", [(1024, 1, 1), (1024, 7, 7), (10240, 3, 3), (1024, 2, 2),
+                                                 (320, 40, 40), (1000, 53, 20), (256, 17, 0)])
+def test_conv1d_causal_silu(gpu, channels, rows, n_snap):
+    """Steps run in parallel runs of 16: a run's window comes from the
+    inputs before it, the first run's from the carried window (fewer rows
+    than the window among the cases), snapshots for the first n_snap rows."""
     w = np.ascontiguousarray(FX["conv1d"]) if channels == 1024 else synth.to_bf16(0.3 * rnd((channels, 4), 9))
     x, st = rnd((rows, channels), 81), rnd((3, channels), 82)
     B = gpu.Buf
     xb, sb, wb, yb = B.of(x), B.of(st), B.of(w), B(rows * channels * 4)
-    nb = B((rows) * 3 * channels * 4)
+    nb = B(max(n_snap, 1) * 3 * channels * 4)
     c = gpu.qw_cmd_begin()
-    gpu.qw_op_conv1d_causal_silu(c, yb.ref(), xb.ref(), sb.ref(), wb.ref(), channels, rows, 4, nb.ref(), rows,
-                                 3 * channels)
+    gpu.qw_op_conv1d_causal_silu(c, yb.ref(), xb.ref(), sb.ref(), wb.ref(), channels, rows, 4,
+                                 nb.ref() if n_snap else gpu.NULL_REF, n_snap, 3 * channels)
     gpu.run(c, "conv1d")
-    y, s1, snap = sparse.conv1d_causal_silu(x, st, w, channels, rows, 4, n_snap=rows)
+    y, s1, snap = sparse.conv1d_causal_silu(x, st, w, channels, rows, 4, n_snap=n_snap)
     assert np.allclose(yb.read(np.float32, (rows, channels)), y, rtol=2e-6, atol=1e-7)
     assert same_bits(sb.read(np.float32, (3, channels)), s1), "the window is a copy of inputs"
-    assert same_bits(nb.read(np.float32, (rows, 3, channels)), snap)
+    if n_snap:
+        assert same_bits(nb.read(np.float32, (n_snap, 3, channels)), snap[:n_snap])
+
+
+def test_conv1d_prefill_equals_split_calls(gpu):
+    """One 2048-row call at the model's 10240 channels against the same rows
+    in three calls (1000, 1, 1047) carrying the window: the same bits."""
+    channels, rows = 10240, 2048
+    w = synth.to_bf16(0.3 * rnd((channels, 4), 19))
+    x, st = rnd((rows, channels), 83), rnd((3, channels), 84)
+    B = gpu.Buf
+    xb, wb, yb, y2 = B.of(x), B.of(w), B(rows * channels * 4), B(rows * channels * 4)
+    s_one, s_split = B.of(st), B.of(st)
+    c = gpu.qw_cmd_begin()
+    gpu.qw_op_conv1d_causal_silu(c, yb.ref(), xb.ref(), s_one.ref(), wb.ref(), channels, rows, 4, gpu.NULL_REF, 0, 0)
+    t = 0
+    for n in (1000, 1, 1047):
+        off = t * channels * 4
+        gpu.qw_op_conv1d_causal_silu(c, y2.ref(off), xb.ref(off), s_split.ref(), wb.ref(), channels, n, 4,
+                                     gpu.NULL_REF, 0, 0)
+        t += n
+    gpu.run(c, "conv1d split")
+    assert same_bits(yb.read(np.float32, (rows, channels)), y2.read(np.float32, (rows, channels)))
+    assert same_bits(s_one.read(np.float32, (3, channels)), s_split.read(np.float32, (3, channels)))
+    assert same_bits(s_one.read(np.float32, (3, channels)), x[-3:])
+    yo = sparse.conv1d_causal_silu(x[:64], st, w, channels, 64, 4)[0]
+    assert np.allclose(yb.read(np.float32, (rows, channels))[:64], yo, rtol=2e-6, atol=1e-7)
 
 
 def test_gdn_gates(gpu):
