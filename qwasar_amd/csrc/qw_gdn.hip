@@ -11,19 +11,21 @@
 //                         step) the conv too, for the channels it reads
 //
 // The recurrence is serial in time but independent across the rows of each
-// head's [dv, dk] state.  A wave owns two value rows: each half-wave one
-// row, each lane four consecutive key columns held in registers for the
-// whole call, so the state crosses HBM once per call, not once per step.  A
-// workgroup (four waves) owns eight rows of one head; the timesteps' q, k,
-// v and gates are staged 16 at a time into LDS, which the eight rows share,
-// so the serial loop reads only LDS.  Both dot products of a step reduce over
-// the half-wave with the fixed xor tree (four DPP steps and one swizzle).
+// head's [dv, dk] state.  A wave owns four value rows: each 16-lane row of
+// the wave one state row, each lane eight consecutive key columns held in
+// registers for the whole call, so the state crosses HBM once per call, not
+// once per step.  A workgroup (four waves) owns sixteen rows of one head; the
+// timesteps' q, k, v and gates are staged 16 at a time into LDS, which the
+// sixteen rows share (with PREP, q and k already scaled by their norms), so
+// the serial loop reads only LDS.  Each dot product of a step is two fma
+// chains of four columns in a lane, their sum, then the fixed xor tree over
+// the 16 lanes (four DPP steps inside the row, no cross-row traffic).
 #include "qw_device.h"
 #include "qw_kernels.h"
 
 #define QG_DK 128
 #define QG_DV 128
-#define QG_ROWS_PER_WG 8
+#define QG_ROWS_PER_WG 16
 #define QG_CHUNK 16
 #define QG_THREADS 256
 
@@ -170,15 +172,46 @@ __global__ void __launch_bounds__(QG_THREADS) k_gated_delta(float *__restrict__ 
     const int groups = QG_DV / QG_ROWS_PER_WG;
     const int h = blockIdx.x / groups, r0 = (blockIdx.x % groups) * QG_ROWS_PER_WG;
     const int hx = h / (hv / hk);
-    const int rl = 2 * wave + (lane >> 5);        // row within the workgroup
+    const int rl = 4 * wave + (lane >> 4);        // row within the workgroup
     const int row = r0 + rl;
-    const int c4 = lane & 31;                      // float4 column index
+    const int c8 = lane & 15;                      // columns 8 c8 .. 8 c8 + 7
 
-    float4 *sp = reinterpret_cast<float4 *>(state + ((size_t)h * QG_DV + row) * QG_DK) + c4;
-    float4 st = *sp;
+    float4 *sp = reinterpret_cast<float4 *>(state + ((size_t)h * QG_DV + row) * QG_DK) + 2 * c8;
+    float4 st = sp[0], su = sp[1];
     const float A = PREP ? qw_bf16(pp.A_log[h]) : 0.0f;
     const float dt = PREP ? qw_bf16(pp.dt_bias[h]) : 0.0f;
     const size_t qstride = (size_t)hk * QG_DK, vstride = (size_t)hv * QG_DV;
+
+    // Without CONV a chunk's q, k, v and gate inputs are fetched into
+    // registers one chunk ahead, so their loads run under the previous
+    // chunk's steps: thread tid holds float4s tid and tid + 256 of the
+    // chunk's [16][32] q and k, value (tid / 16, tid % 16) and, for tid in
+    // [128, 144), step tid - 128's gate inputs.
+    static_assert(QG_CHUNK * (QG_DK / 4) == 2 * QG_THREADS && QG_CHUNK * QG_ROWS_PER_WG == QG_THREADS,
+                  "one chunk's staging is two float4s of q and of k and one value a thread");
+    float4 fq0 = {}, fq1 = {}, fk0 = {}, fk1 = {};
+    float fv = 0.0f, fa = 0.0f, fb = 0.0f;
+    auto fetch = [&](int c) __attribute__((always_inline)) {
+        const int nn = min(QG_CHUNK, rows - c);
+        const int t0 = tid / (QG_DK / 4), t1 = t0 + QG_THREADS / (QG_DK / 4), cc = tid % (QG_DK / 4);
+        const size_t o0 = (size_t)(c + t0) * qstride + (size_t)hx * QG_DK, o1 = o0 + (size_t)(t1 - t0) * qstride;
+        if (t0 < nn) {
+            fq0 = reinterpret_cast<const float4 *>(q + o0)[cc];
+            fk0 = reinterpret_cast<const float4 *>(k + o0)[cc];
+        }
+        if (t1 < nn) {
+            fq1 = reinterpret_cast<const float4 *>(q + o1)[cc];
+            fk1 = reinterpret_cast<const float4 *>(k + o1)[cc];
+        }
+        if (tid / QG_ROWS_PER_WG < nn)
+            fv = v[(size_t)(c + tid / QG_ROWS_PER_WG) * vstride + (size_t)h * QG_DV + r0 + tid % QG_ROWS_PER_WG];
+        if (tid >= 128 && tid < 128 + nn) {
+            const size_t gi = (size_t)(c + tid - 128) * hv + h;
+            fa = PREP ? pp.a[gi] : g[gi];
+            fb = PREP ? pp.b[gi] : beta[gi];
+        }
+    };
+    if (!CONV) fetch(0);
 
     for (int c0 = 0; c0 < rows; c0 += QG_CHUNK) {
         const int n = min(QG_CHUNK, rows - c0);
@@ -190,75 +223,116 @@ __global__ void __launch_bounds__(QG_THREADS) k_gated_delta(float *__restrict__ 
             if (tid < QG_DK) fq[tid] = qg_conv1(cv, hx * QG_DK + tid, own_qk);
             else if (tid < 2 * QG_DK) fk[tid - QG_DK] = qg_conv1(cv, kd + hx * QG_DK + tid - QG_DK, own_qk);
             if (tid < QG_ROWS_PER_WG) sv[0][tid] = qg_conv1(cv, 2 * kd + h * QG_DV + r0 + tid, true);
+            if (tid >= 128 && tid < 128 + n) {
+                const size_t gi = (size_t)(c0 + tid - 128) * hv + h;
+                qg_gates(pp.a[gi], pp.b[gi], A, dt, sg[tid - 128][0], sg[tid - 128][1]);
+            }
         } else {
-            for (int i = tid; i < n * (QG_DK / 4); i += QG_THREADS) {
-                const int t = i / (QG_DK / 4), c = i % (QG_DK / 4);
-                const size_t off = (size_t)(c0 + t) * qstride + (size_t)hx * QG_DK;
-                sq[t][c] = reinterpret_cast<const float4 *>(q + off)[c];
-                sk[t][c] = reinterpret_cast<const float4 *>(k + off)[c];
+            const int t0 = tid / (QG_DK / 4), t1 = t0 + QG_THREADS / (QG_DK / 4), cc = tid % (QG_DK / 4);
+            sq[t0][cc] = fq0;
+            sk[t0][cc] = fk0;
+            sq[t1][cc] = fq1;
+            sk[t1][cc] = fk1;
+            sv[tid / QG_ROWS_PER_WG][tid % QG_ROWS_PER_WG] = fv;
+            if (tid >= 128 && tid < 128 + n) {
+                if (PREP) qg_gates(fa, fb, A, dt, sg[tid - 128][0], sg[tid - 128][1]);
+                else {
+                    sg[tid - 128][0] = fa;
+                    sg[tid - 128][1] = fb;
+                }
             }
-            if (tid < n * QG_ROWS_PER_WG) {
-                const int t = tid / QG_ROWS_PER_WG, j = tid % QG_ROWS_PER_WG;
-                sv[t][j] = v[(size_t)(c0 + t) * vstride + (size_t)h * QG_DV + r0 + j];
-            }
-        }
-        if (tid >= 128 && tid < 128 + n) {
-            const int t = tid - 128;
-            const size_t gi = (size_t)(c0 + t) * hv + h;
-            if (PREP) {
-                qg_gates(pp.a[gi], pp.b[gi], A, dt, sg[t][0], sg[t][1]);
-            } else {
-                sg[t][0] = g[gi];
-                sg[t][1] = beta[gi];
-            }
+            if (c0 + QG_CHUNK < rows) fetch(c0 + QG_CHUNK);
         }
         if (PREP) {
             __syncthreads();
             // the l2 norms of the chunk's q and k vectors: a wave per (step,
-            // vector), each lane two of the 128 values, then the wave's xor tree
-            for (int p = wave; p < 2 * n; p += QG_THREADS / 64) {
-                const int t = p >> 1, isk = p & 1;
-                const float *src = reinterpret_cast<const float *>(isk ? &sk[t][0] : &sq[t][0]);
-                const float a0 = src[lane], a1 = src[lane + 64];
+            // vector), each lane two of the 128 values, then the wave's xor
+            // tree; in a whole chunk a wave's eight vectors are loaded first
+            // and their trees run side by side
+            auto norm = [&](int p, float a0, float a1) __attribute__((always_inline)) {
                 float ss = __builtin_fmaf(a0, a0, 0.0f);
                 ss = __builtin_fmaf(a1, a1, ss);
                 ss = qw_xor_sum<64>(ss);
                 if (lane == 0)
-                    sn[t][isk] = 1.0f / sqrtf(ss / (float)QG_DK + pp.l2eps) * (isk ? pp.k_scale : pp.q_scale);
+                    sn[p >> 1][p & 1] = 1.0f / sqrtf(ss / (float)QG_DK + pp.l2eps) * ((p & 1) ? pp.k_scale : pp.q_scale);
+            };
+            auto vec = [&](int p) __attribute__((always_inline)) {
+                return reinterpret_cast<const float *>((p & 1) ? &sk[p >> 1][0] : &sq[p >> 1][0]);
+            };
+            if (n == QG_CHUNK) {
+                static_assert(2 * QG_CHUNK == 8 * (QG_THREADS / 64), "eight vectors a wave");
+                float a0[8], a1[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    a0[j] = vec(wave + 4 * j)[lane];
+                    a1[j] = vec(wave + 4 * j)[lane + 64];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) norm(wave + 4 * j, a0[j], a1[j]);
+            } else {
+                for (int p = wave; p < 2 * n; p += QG_THREADS / 64) norm(p, vec(p)[lane], vec(p)[lane + 64]);
+            }
+            __syncthreads();
+            for (int i = tid; i < n * (QG_DK / 4); i += QG_THREADS) {
+                const int t = i / (QG_DK / 4), c = i % (QG_DK / 4);
+                const float iq = sn[t][0], ik = sn[t][1];
+                float4 a = sq[t][c], b = sk[t][c];
+                a.x *= iq; a.y *= iq; a.z *= iq; a.w *= iq;
+                b.x *= ik; b.y *= ik; b.z *= ik; b.w *= ik;
+                sq[t][c] = a;
+                sk[t][c] = b;
             }
         }
         __syncthreads();
-        for (int t = 0; t < n; t++) {
-            float4 qv = sq[t][c4], kv4 = sk[t][c4];
-            if (PREP) {
-                const float iq = sn[t][0], ik = sn[t][1];
-                qv.x *= iq; qv.y *= iq; qv.z *= iq; qv.w *= iq;
-                kv4.x *= ik; kv4.y *= ik; kv4.z *= ik; kv4.w *= ik;
-            }
+        // a step; whole chunks unrolled, so that a step's output dot and
+        // the next step's LDS reads overlap the state's serial chain
+        auto step = [&](int t) __attribute__((always_inline)) {
+            const float4 q0 = sq[t][2 * c8], q1 = sq[t][2 * c8 + 1], k0 = sk[t][2 * c8], k1 = sk[t][2 * c8 + 1];
             const float gt = sg[t][0], bt = sg[t][1];
             st.x *= gt; st.y *= gt; st.z *= gt; st.w *= gt;
-            float kv = st.x * kv4.x;
-            kv = __builtin_fmaf(st.y, kv4.y, kv);
-            kv = __builtin_fmaf(st.z, kv4.z, kv);
-            kv = __builtin_fmaf(st.w, kv4.w, kv);
-            kv = qw_xor_sum<32>(kv);
+            su.x *= gt; su.y *= gt; su.z *= gt; su.w *= gt;
+            float ka = st.x * k0.x, kb = su.x * k1.x;
+            ka = __builtin_fmaf(st.y, k0.y, ka);
+            kb = __builtin_fmaf(su.y, k1.y, kb);
+            ka = __builtin_fmaf(st.z, k0.z, ka);
+            kb = __builtin_fmaf(su.z, k1.z, kb);
+            ka = __builtin_fmaf(st.w, k0.w, ka);
+            kb = __builtin_fmaf(su.w, k1.w, kb);
+            const float kv = qw_xor_sum<16>(ka + kb);
             const float delta = (sv[t][rl] - kv) * bt;
-            st.x = __builtin_fmaf(kv4.x, delta, st.x);
-            st.y = __builtin_fmaf(kv4.y, delta, st.y);
-            st.z = __builtin_fmaf(kv4.z, delta, st.z);
-            st.w = __builtin_fmaf(kv4.w, delta, st.w);
-            float o = st.x * qv.x;
-            o = __builtin_fmaf(st.y, qv.y, o);
-            o = __builtin_fmaf(st.z, qv.z, o);
-            o = __builtin_fmaf(st.w, qv.w, o);
-            o = qw_xor_sum<32>(o);
+            st.x = __builtin_fmaf(k0.x, delta, st.x);
+            st.y = __builtin_fmaf(k0.y, delta, st.y);
+            st.z = __builtin_fmaf(k0.z, delta, st.z);
+            st.w = __builtin_fmaf(k0.w, delta, st.w);
+            su.x = __builtin_fmaf(k1.x, delta, su.x);
+            su.y = __builtin_fmaf(k1.y, delta, su.y);
+            su.z = __builtin_fmaf(k1.z, delta, su.z);
+            su.w = __builtin_fmaf(k1.w, delta, su.w);
+            float oa = st.x * q0.x, ob = su.x * q1.x;
+            oa = __builtin_fmaf(st.y, q0.y, oa);
+            ob = __builtin_fmaf(su.y, q1.y, ob);
+            oa = __builtin_fmaf(st.z, q0.z, oa);
+            ob = __builtin_fmaf(su.z, q1.z, ob);
+            oa = __builtin_fmaf(st.w, q0.w, oa);
+            ob = __builtin_fmaf(su.w, q1.w, ob);
+            const float o = qw_xor_sum<16>(oa + ob);
             const int tt = c0 + t;
-            if (c4 == 0) y[(size_t)tt * vstride + (size_t)h * QG_DV + row] = o;
-            if (tt < n_snap)
-                reinterpret_cast<float4 *>(snap + (size_t)tt * snap_stride + ((size_t)h * QG_DV + row) * QG_DK)[c4] = st;
+            if (c8 == 0) y[(size_t)tt * vstride + (size_t)h * QG_DV + row] = o;
+            if (tt < n_snap) {
+                float4 *sn4 = reinterpret_cast<float4 *>(snap + (size_t)tt * snap_stride + ((size_t)h * QG_DV + row) * QG_DK) + 2 * c8;
+                sn4[0] = st;
+                sn4[1] = su;
+            }
+        };
+        if (n == QG_CHUNK) {
+#pragma unroll
+            for (int t = 0; t < QG_CHUNK; t++) step(t);
+        } else {
+            for (int t = 0; t < n; t++) step(t);
         }
     }
-    *sp = st;
+    sp[0] = st;
+    sp[1] = su;
 }
 
 // ---- launchers ----------------------------------------------------------------
