@@ -27,6 +27,7 @@
 #define QG_DV 128
 #define QG_ROWS_PER_WG 16
 #define QG_CHUNK 16
+#define QG_PRE_MIN_ROWS 64      // prepared calls from this many steps on take k_gdn_pre
 #define QG_THREADS 256
 
 __device__ __forceinline__ float qg_softplus(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
@@ -119,7 +120,45 @@ struct qg_prep {
     const float *a, *b;
     const uint16_t *A_log, *dt_bias;
     float l2eps, q_scale, k_scale;
+    // from k_gdn_pre (or null): each step's q and k norm factors
+    // [rows][hk][2] and gates (g, beta) [rows][hv][2]
+    const float *nrm, *gb;
 };
+
+// The l2 norm factor of one 128-value q or k vector, by a whole wave: lane
+// l squares values l and l + 64 (an fma chain from 0), then the wave's xor
+// tree.  Every lane gets the factor.
+__device__ __forceinline__ float qg_norm(float a0, float a1, float l2eps, float scale)
+{
+    float ss = __builtin_fmaf(a0, a0, 0.0f);
+    ss = __builtin_fmaf(a1, a1, ss);
+    ss = qw_xor_sum<64>(ss);
+    return 1.0f / sqrtf(ss / (float)QG_DK + l2eps) * scale;
+}
+
+// A long prepared call's norms and gates ahead of the recurrence, in
+// parallel over every step: the first nvw / 4 workgroups a wave a vector
+// (vector w: step w / (2 hk), key head (w / 2) % hk, k if w is odd), the
+// rest a thread a (step, value head) gate; the recurrence's own functions,
+// so the same bits as computed inside it.
+__global__ void __launch_bounds__(256) k_gdn_pre(qg_prep pp, const float *__restrict__ q, const float *__restrict__ k,
+                                                 int hk, int hv, int rows)
+{
+    const int nvw = rows * hk * 2, nbv = (nvw + 3) / 4;
+    float *nrm = const_cast<float *>(pp.nrm), *gb = const_cast<float *>(pp.gb);
+    if ((int)blockIdx.x < nbv) {
+        const int w = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+        if (w >= nvw) return;
+        const float *src = ((w & 1) ? k : q) + (size_t)(w >> 1) * QG_DK;
+        const float f = qg_norm(src[lane], src[lane + 64], pp.l2eps, (w & 1) ? pp.k_scale : pp.q_scale);
+        if (lane == 0) nrm[w] = f;
+    } else {
+        const int i = (blockIdx.x - nbv) * 256 + threadIdx.x;
+        if (i >= rows * hv) return;
+        const int h = i % hv;
+        qg_gates(pp.a[i], pp.b[i], qw_bf16(pp.A_log[h]), qw_bf16(pp.dt_bias[h]), gb[2 * i], gb[2 * i + 1]);
+    }
+}
 
 // The fused decode step's conv: the mixed channels before the conv, the
 // window in and out (distinct buffers), the taps.
@@ -190,7 +229,8 @@ __global__ void __launch_bounds__(QG_THREADS) k_gated_delta(float *__restrict__ 
     static_assert(QG_CHUNK * (QG_DK / 4) == 2 * QG_THREADS && QG_CHUNK * QG_ROWS_PER_WG == QG_THREADS,
                   "one chunk's staging is two float4s of q and of k and one value a thread");
     float4 fq0 = {}, fq1 = {}, fk0 = {}, fk1 = {};
-    float fv = 0.0f, fa = 0.0f, fb = 0.0f;
+    float fv = 0.0f, fa = 0.0f, fb = 0.0f, fn = 0.0f;
+    const bool pre = PREP && !CONV && pp.nrm;
     auto fetch = [&](int c) __attribute__((always_inline)) {
         const int nn = min(QG_CHUNK, rows - c);
         const int t0 = tid / (QG_DK / 4), t1 = t0 + QG_THREADS / (QG_DK / 4), cc = tid % (QG_DK / 4);
@@ -207,9 +247,11 @@ __global__ void __launch_bounds__(QG_THREADS) k_gated_delta(float *__restrict__ 
             fv = v[(size_t)(c + tid / QG_ROWS_PER_WG) * vstride + (size_t)h * QG_DV + r0 + tid % QG_ROWS_PER_WG];
         if (tid >= 128 && tid < 128 + nn) {
             const size_t gi = (size_t)(c + tid - 128) * hv + h;
-            fa = PREP ? pp.a[gi] : g[gi];
-            fb = PREP ? pp.b[gi] : beta[gi];
+            fa = pre ? pp.gb[2 * gi] : PREP ? pp.a[gi] : g[gi];
+            fb = pre ? pp.gb[2 * gi + 1] : PREP ? pp.b[gi] : beta[gi];
         }
+        if (pre && tid >= 160 && tid < 160 + 2 * nn)
+            fn = pp.nrm[((size_t)(c + (tid - 160) / 2) * hk + hx) * 2 + (tid & 1)];
     };
     if (!CONV) fetch(0);
 
@@ -235,12 +277,13 @@ __global__ void __launch_bounds__(QG_THREADS) k_gated_delta(float *__restrict__ 
             sk[t1][cc] = fk1;
             sv[tid / QG_ROWS_PER_WG][tid % QG_ROWS_PER_WG] = fv;
             if (tid >= 128 && tid < 128 + n) {
-                if (PREP) qg_gates(fa, fb, A, dt, sg[tid - 128][0], sg[tid - 128][1]);
+                if (PREP && !pre) qg_gates(fa, fb, A, dt, sg[tid - 128][0], sg[tid - 128][1]);
                 else {
                     sg[tid - 128][0] = fa;
                     sg[tid - 128][1] = fb;
                 }
             }
+            if (pre && tid >= 160 && tid < 160 + 2 * n) sn[(tid - 160) / 2][tid & 1] = fn;
             if (c0 + QG_CHUNK < rows) fetch(c0 + QG_CHUNK);
         }
         if (PREP) {
@@ -250,16 +293,15 @@ __global__ void __launch_bounds__(QG_THREADS) k_gated_delta(float *__restrict__ 
             // tree; in a whole chunk a wave's eight vectors are loaded first
             // and their trees run side by side
             auto norm = [&](int p, float a0, float a1) __attribute__((always_inline)) {
-                float ss = __builtin_fmaf(a0, a0, 0.0f);
-                ss = __builtin_fmaf(a1, a1, ss);
-                ss = qw_xor_sum<64>(ss);
-                if (lane == 0)
-                    sn[p >> 1][p & 1] = 1.0f / sqrtf(ss / (float)QG_DK + pp.l2eps) * ((p & 1) ? pp.k_scale : pp.q_scale);
+                const float f = qg_norm(a0, a1, pp.l2eps, (p & 1) ? pp.k_scale : pp.q_scale);
+                if (lane == 0) sn[p >> 1][p & 1] = f;
             };
             auto vec = [&](int p) __attribute__((always_inline)) {
                 return reinterpret_cast<const float *>((p & 1) ? &sk[p >> 1][0] : &sq[p >> 1][0]);
             };
-            if (n == QG_CHUNK) {
+            if (pre) {
+                // the factors came with the chunk
+            } else if (n == QG_CHUNK) {
                 static_assert(2 * QG_CHUNK == 8 * (QG_THREADS / 64), "eight vectors a wave");
                 float a0[8], a1[8];
 #pragma unroll
@@ -356,7 +398,8 @@ extern "C" int qwk_gdn_decode(hipStream_t s, float *y, const float *x, const flo
     if (dk != QG_DK || dv != QG_DV || hk < 1 || hv < 1 || hv % hk || !prep || !x || !win || !wout || !w)
         return hipErrorInvalidValue;
     const int channels = 2 * hk * dk + hv * dv;
-    const qg_prep pp = { prep->a, prep->b, prep->A_log, prep->dt_bias, prep->l2eps, prep->q_scale, prep->k_scale };
+    const qg_prep pp = { prep->a, prep->b, prep->A_log, prep->dt_bias, prep->l2eps, prep->q_scale, prep->k_scale,
+                         nullptr, nullptr };
     const qg_conv cv = { x, win, wout, w, channels };
     hipLaunchKernelGGL((k_gated_delta<true, true>), dim3(hv * (QG_DV / QG_ROWS_PER_WG)), dim3(QG_THREADS), 0, s, y,
                        nullptr, nullptr, nullptr, nullptr, nullptr, state, hk, hv, 1, nullptr, 0, 0, pp, cv);
@@ -373,9 +416,16 @@ extern "C" int qwk_gdn_gates(hipStream_t s, float *g, float *beta, const float *
     return (int)hipGetLastError();
 }
 
+extern "C" size_t qwk_gated_delta_work(int hk, int hv, int rows, int prep)
+{
+    if (!prep || rows < QG_PRE_MIN_ROWS || hk < 1 || hv < 1) return 0;
+    return ((size_t)rows * hk * 2 + (size_t)rows * hv * 2) * sizeof(float);
+}
+
 extern "C" int qwk_gated_delta(hipStream_t s, float *y, const float *q, const float *k, const float *v,
                                const float *g, const float *beta, float *state, int hk, int hv, int dk, int dv,
-                               int rows, float *snap, int n_snap, int snap_stride, const qwk_gdn_prep *prep)
+                               int rows, float *snap, int n_snap, int snap_stride, const qwk_gdn_prep *prep,
+                               void *work)
 {
     if (dk != QG_DK || dv != QG_DV || hk < 1 || hv < 1 || hv % hk || rows < 0 || n_snap < 0 ||
         (n_snap > 0 && (!snap || snap_stride < hv * dv * dk || snap_stride % 4)))
@@ -383,7 +433,14 @@ extern "C" int qwk_gated_delta(hipStream_t s, float *y, const float *q, const fl
     if (rows == 0) return 0;
     const dim3 grid(hv * (QG_DV / QG_ROWS_PER_WG));
     if (prep) {
-        const qg_prep pp = { prep->a, prep->b, prep->A_log, prep->dt_bias, prep->l2eps, prep->q_scale, prep->k_scale };
+        qg_prep pp = { prep->a, prep->b, prep->A_log, prep->dt_bias, prep->l2eps, prep->q_scale, prep->k_scale,
+                       nullptr, nullptr };
+        if (work && qwk_gated_delta_work(hk, hv, rows, 1) > 0) {
+            pp.nrm = static_cast<float *>(work);
+            pp.gb = pp.nrm + (size_t)rows * hk * 2;
+            const int nbv = (rows * hk * 2 + 3) / 4, nbg = (rows * hv + 255) / 256;
+            hipLaunchKernelGGL(k_gdn_pre, dim3(nbv + nbg), dim3(256), 0, s, pp, q, k, hk, hv, rows);
+        }
         hipLaunchKernelGGL(k_gated_delta<true>, grid, dim3(QG_THREADS), 0, s, y, q, k, v, nullptr, nullptr, state,
                            hk, hv, rows, snap, n_snap, snap_stride, pp);
     } else {

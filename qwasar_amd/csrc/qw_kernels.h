@@ -268,10 +268,14 @@ int qwk_conv1d_causal_silu(hipStream_t s, float *y, const float *x, float *state
                            int channels, int rows, int ksize, float *snap, int n_snap, int snap_stride);
 int qwk_gdn_gates(hipStream_t s, float *g, float *beta, const float *a, const float *b,
                   const uint16_t *A_log, const uint16_t *dt_bias, int hv, int rows);
-/* prep NULL: q, k normed and g, beta given; else g and beta are unused. */
+/* prep NULL: q, k normed and g, beta given; else g and beta are unused.
+ * work: qwk_gated_delta_work() bytes of device memory (NULL when that is 0):
+ * a long prepared call computes its norms and gates there first, in
+ * parallel, instead of a chunk at a time inside the recurrence. */
+size_t qwk_gated_delta_work(int hk, int hv, int rows, int prep);
 int qwk_gated_delta(hipStream_t s, float *y, const float *q, const float *k, const float *v,
                     const float *g, const float *beta, float *state, int hk, int hv, int dk, int dv,
-                    int rows, float *snap, int n_snap, int snap_stride, const qwk_gdn_prep *prep);
+                    int rows, float *snap, int n_snap, int snap_stride, const qwk_gdn_prep *prep, void *work);
 /* One decode step: the conv over x [2 hk dk + hv dv] (window win in, wout
  * out: distinct buffers, [3, channels] oldest first), then the prepared delta
  * rule on its q, k and v channels; the bits of qwk_conv1d_causal_silu then

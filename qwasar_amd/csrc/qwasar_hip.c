@@ -1206,9 +1206,12 @@ static void gated_delta(qw_cmd c, qw_ref y, qw_ref q, qw_ref k, qw_ref v, qw_ref
     } else {
         touch(c, g, 0); touch(c, beta, 0);
     }
+    const size_t wb = qwk_gated_delta_work(hk, hv, rows, prep != NULL);
+    void *work = wb ? scratch(wb) : NULL;
+    if (wb && !work) { cmd_fail(c, hipErrorOutOfMemory, "gated_delta: scratch of %zu bytes", wb); return; }
     launched(c, prep ? "gated_delta_prep" : "gated_delta",
              qwk_gated_delta(G.stream, dp(y), dp(q), dp(k), dp(v), dp(g), dp(beta), dp(state), hk, hv, dk, dv, rows,
-                             n_snap > 0 ? dp(snap) : NULL, n_snap, snap_stride, prep ? &pp : NULL));
+                             n_snap > 0 ? dp(snap) : NULL, n_snap, snap_stride, prep ? &pp : NULL, work));
 }
 
 void qw_op_gated_delta(qw_cmd c, qw_ref y, qw_ref q, qw_ref k, qw_ref v, qw_ref g, qw_ref beta, qw_ref state,

@@ -412,7 +412,7 @@ def test_gdn_decode_one_launch(gpu, hk, hv):
             t.free()
 
 
-@pytest.mark.parametrize("hk,hv,rows", [(2, 4, 3), (16, 48, 20)])
+@pytest.mark.parametrize("hk,hv,rows", [(2, 4, 3), (16, 48, 20), (16, 48, 150)])
 def test_gated_delta_prep(gpu, hk, hv, rows):
     """Norms and gates inside the recurrence, against the oracle's prep and
     against the GPU's own composition of rms_norm, gates and the recurrence
@@ -444,6 +444,39 @@ def test_gated_delta_prep(gpu, hk, hv, rows):
     wy, ws, _ = sparse.gated_delta_prep(q, k, v, a, b, Al, dt, eps, qs, ks, s0, hk, hv, dk, dv, rows)
     assert rel_l2(y2, wy) < 5e-6 and rel_l2(s2, ws) < 5e-6, (rel_l2(y2, wy), rel_l2(s2, ws))
     assert rel_l2(y2, y1) < 5e-6 and rel_l2(s2, s1) < 5e-6
+
+
+def test_gated_delta_prep_long_equals_short_calls(gpu):
+    """From 64 steps on a prepared call computes every step's norms and
+    gates first, in parallel; shorter calls compute them a chunk at a time
+    inside the recurrence.  150 steps in one call against 60 + 60 + 30
+    carrying the state: the same bits in y and the state."""
+    hk, hv, dk, rows = 16, 48, 128, 150
+    q, k, v = rnd((rows, hk, dk), 141), rnd((rows, hk, dk), 142), rnd((rows, hv, dk), 143)
+    a, b = rnd((rows, hv), 144, -4, 4), rnd((rows, hv), 145, -4, 4)
+    s0 = rnd((hv, dk, dk), 146) * np.float32(0.05)
+    Al = np.ascontiguousarray(np.resize(FX["A_log"], hv))
+    dt = np.ascontiguousarray(np.resize(FX["dt_bias"], hv))
+    eps, qs, ks = 1e-6 / dk, 1.0 / dk, 1.0 / np.sqrt(dk)
+    B = gpu.Buf
+    qb, kb, vb, ab, bb, Ab, db = B.of(q), B.of(k), B.of(v), B.of(a), B.of(b), B.of(Al), B.of(dt)
+    s1b, s2b = B.of(s0), B.of(s0)
+    y1b, y2b = B(rows * hv * dk * 4), B(rows * hv * dk * 4)
+    c = gpu.qw_cmd_begin()
+    prep = gpu.qw_gdn_prep(ab.ref(), bb.ref(), Ab.ref(), db.ref(), eps, qs, ks)
+    gpu.qw_op_gated_delta_prep(c, y1b.ref(), qb.ref(), kb.ref(), vb.ref(), prep, s1b.ref(), hk, hv, dk, dk, rows,
+                               gpu.NULL_REF, 0, 0)
+    t = 0
+    for n in (60, 60, 30):
+        pn = gpu.qw_gdn_prep(ab.ref(t * hv * 4), bb.ref(t * hv * 4), Ab.ref(), db.ref(), eps, qs, ks)
+        gpu.qw_op_gated_delta_prep(c, y2b.ref(t * hv * dk * 4), qb.ref(t * hk * dk * 4), kb.ref(t * hk * dk * 4),
+                                   vb.ref(t * hv * dk * 4), pn, s2b.ref(), hk, hv, dk, dk, n, gpu.NULL_REF, 0, 0)
+        t += n
+    gpu.run(c, "gated delta prep, long and short calls")
+    assert same_bits(y1b.read(np.float32, (rows, hv, dk)), y2b.read(np.float32, (rows, hv, dk)))
+    assert same_bits(s1b.read(np.float32, (hv, dk, dk)), s2b.read(np.float32, (hv, dk, dk)))
+    wy, ws, _ = sparse.gated_delta_prep(q, k, v, a, b, Al, dt, eps, qs, ks, s0, hk, hv, dk, dk, rows)
+    assert rel_l2(y1b.read(np.float32, (rows, hv, dk)), wy) < 5e-6
 
 
 def test_rms_norm_gated_sigmoid(gpu):
