@@ -479,17 +479,23 @@ __device__ void qx_gather(const QxArgs &a, int x, QxGatherLds &G)
             }
             QX_TS(1);
         }
+        // The ids leave as soon as they are final (the workers' weight
+        // streams wait on them); the weights and the shared gate, which only
+        // the down dots use, follow once renormalised.  Ids are clamped:
+        // after a wait that gave up the logits are whatever was read, and no
+        // pick may then address outside the banks.
+        QxLocal &L = a.sync->loc[x];
+        auto put_ids = [&](int id) {
+            if (pass == 1 && lane < K) qx_put_near(L.pick + lane, a.epoch, (uint32_t)min(max(id, 0), E - 1));
+        };
         // (waves whose slice starts past E hold -inf there: qw_route_block masks e >= E)
-        qw_route_block<QX_PL>(lv, E, K, a.m.norm, wave, lane, &pi, &pw, G.sx, G.vb);
+        qw_route_block<QX_PL>(lv, E, K, a.m.norm, wave, lane, &pi, &pw, G.sx, G.vb, put_ids);
         __syncthreads();
     }
     if (wave == 0) {
-        // clamped: after a wait that gave up the logits are whatever was read,
-        // and no pick may then address outside the banks
         pi = min(max(pi, 0), E - 1);
         QxLocal &L = a.sync->loc[x];
         if (lane < K) {
-            qx_put_near(L.pick + lane, a.epoch, (uint32_t)pi);
             qx_put_near(L.pick + K + lane, a.epoch, __float_as_uint(pw));
         } else if (lane == K) {
             qx_put_near(L.pick + 2 * K, a.epoch, __float_as_uint(G.coef));
@@ -862,23 +868,18 @@ __device__ void qx_worker(const QxArgs &a, int x, int j, uint4 *lds, QxWorkLds &
         // wave, whose rows are not the shared unit's (nq_sh <= QX_GUW - 1)
         if (wave == QX_GUW - 1) {
             uint32_t v[1];
-            qx_poll<1, false, QX_SLEEP_PICKS>(a, a.sync->loc[x].pick, 2 * K + 1, v);
+            qx_poll<1, false, QX_SLEEP_PICKS>(a, a.sync->loc[x].pick, K, v);
             // (clamped: after a wait that gave up the words are whatever was read)
             if (lane < K) S.pick[lane] = (int)min(v[0], (uint32_t)(a.m.E - 1));
-            else if (lane < 2 * K) S.coef[1 + lane - K] = __uint_as_float(v[0]);
-            else if (lane == 2 * K) S.coef[0] = __uint_as_float(v[0]);
         }
         qx_barrier();
         // the rest of the table (an XCD without units still fills entry 0, with
         // a valid unit: its gate/up waves issue their clamped loads through it
-        // and drop them), then every unit's combine coefficient
+        // and drop them); the units' combine coefficients are set after
+        // the gate/up, once the weights have come
         if ((int)threadIdx.x < max(nux, 1) && !(threadIdx.x == 0 && nq_sh > 0))
             S.unit[threadIdx.x] = qx_unit(a, S, min(x + 8 * (int)threadIdx.x, a.NU - 1));
-        qx_barrier();
-        if ((int)threadIdx.x < nux) {
-            const int u = x + 8 * threadIdx.x;
-            S.unit[threadIdx.x].coef = u < a.nus ? S.coef[0] : S.coef[1 + min((u - a.nus) / a.nui, K - 1)];
-        }
+        qx_barrier();      // the table is in LDS before pass B reads it
         QX_TS(1);
         // pass B
         if (pre0) gu_rest(std::true_type{}, sb16c);
@@ -903,7 +904,14 @@ __device__ void qx_worker(const QxArgs &a, int x, int j, uint4 *lds, QxWorkLds &
     for (int t = threadIdx.x; t < np_; t += QX_THREADS)
         qx_put_near(a.sync->loc[x].act + j + a.W * t, a.epoch, __float_as_uint(qw_silu(ys[2 * t]) * ys[2 * t + 1]));
 
-    // ---- the XCD's activations, as q16 units ----
+    // ---- the picks' weights and the shared gate (published after the ids),
+    // then the XCD's activations, as q16 units ----
+    if (wave == QX_WAVES - 1) {
+        uint32_t v[1];
+        qx_poll<1, false>(a, a.sync->loc[x].pick + K, K + 1, v);
+        if (lane < K) S.coef[1 + lane] = __uint_as_float(v[0]);
+        else if (lane == K) S.coef[0] = __uint_as_float(v[0]);
+    }
     {
         const uint2 *src = a.sync->loc[x].act;
         for (int c0 = 64 * wave; c0 < rows_x; c0 += 64 * QX_WAVES) {
@@ -913,6 +921,10 @@ __device__ void qx_worker(const QxArgs &a, int x, int j, uint4 *lds, QxWorkLds &
         }
     }
     qx_barrier();
+    if ((int)threadIdx.x < nux) {
+        const int u = x + 8 * threadIdx.x;
+        S.unit[threadIdx.x].coef = u < a.nus ? S.coef[0] : S.coef[1 + min((u - a.nus) / a.nui, K - 1)];
+    }
     QX_TS(4);
     for (int u = threadIdx.x; u < rows_x / 16; u += QX_THREADS) qw_q16_stage(af + 16 * u, xq + 3 * u);
     QX_TS(11);

@@ -337,9 +337,15 @@ __device__ __forceinline__ uint32_t qw_ldu16(const void *base, uint32_t off)
 // p, descending, ties to the lower expert.  The sum adds a lane's v[j] in j
 // order from 0, then the lane partials by the 64-lane xor tree.
 #define QW_ROUTE_PRIO 3
-template <int PL>
+// on_ids(id) is called by the whole wave once the picks' experts are final
+// (lane n < K: pick n) and before their weights are computed, so a caller
+// can hand the ids on while the renormalisation runs.
+struct QwNoIds {
+    __device__ __forceinline__ void operator()(int) const {}
+};
+template <int PL, class OnIds = QwNoIds>
 __device__ __forceinline__ void qw_route_finish(float (&v)[PL], int E, int K, int norm, int lane,
-                                               int *pick_i, float *pick_w, uint32_t *sx)
+                                               int *pick_i, float *pick_w, uint32_t *sx, OnIds on_ids = OnIds{})
 {
     // One wave's chain of dependent steps, on a SIMD it shares with the
     // other waves of its CU's workgroups: issued ahead of them while it runs
@@ -417,25 +423,36 @@ __device__ __forceinline__ void qw_route_finish(float (&v)[PL], int E, int K, in
             __builtin_amdgcn_wave_barrier();
             const uint64_t mk = lane < C ? keys[lane] : 0;
             QW_RSTAMP(6);
-            // each lane's rank among the C keys, the keys broadcast from
-            // their lanes (C is wave-uniform; keys are distinct)
-            const uint32_t mlo = (uint32_t)mk, mhi = (uint32_t)(mk >> 32);
+            // each lane's rank among the C keys (C is wave-uniform; keys are
+            // distinct), the keys read four at a time as LDS broadcasts, all
+            // four requested before the first is compared (slots past C
+            // hold stale words inside sx and are masked)
             int rank = 0;
-            for (int q = 0; q < C; q++) {
-                const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)mlo, q);
-                const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)mhi, q);
-                rank += (hi > mhi) | ((hi == mhi) & (lo > mlo));
+            for (int q = 0; q < C; q += 4) {
+                uint64_t kq[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) kq[i] = keys[q + i];
+#pragma unroll
+                for (int i = 0; i < 4; i++) rank += (q + i < C) & (kq[i] > mk);
             }
             QW_RSTAMP(7);
             if (lane < C && rank < K) picks[rank] = mk;
             __builtin_amdgcn_wave_barrier();
-            // the renormalising sum adds the picks in pick order, each
-            // broadcast from its lane
             const uint64_t pk = lane < K ? picks[lane] : 0;
+            *pick_i = lane < K ? 0xFFFF - (int)(uint32_t)pk : 0;
+            on_ids(*pick_i);
+            // the renormalising sum adds the picks in pick order, read back
+            // as LDS broadcasts
             const float mw = __uint_as_float((uint32_t)(pk >> 32));
             float wsum = 0.0f;
-            for (int n = 0; n < K; n++) wsum = wsum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mw), n));
-            *pick_i = lane < K ? 0xFFFF - (int)(uint32_t)pk : 0;
+            for (int n = 0; n < K; n += 4) {
+                float pw[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) pw[i] = __uint_as_float((uint32_t)(picks[min(n + i, K - 1)] >> 32));
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (n + i < K) wsum = wsum + pw[i];
+            }
             *pick_w = norm ? mw / wsum : mw;
             QW_RSTAMP(8);
             if (QW_ROUTE_PRIO > 0) __builtin_amdgcn_s_setprio(0);
@@ -501,6 +518,7 @@ __device__ __forceinline__ void qw_route_finish(float (&v)[PL], int E, int K, in
         }
     }
     *pick_i = mine_i;
+    on_ids(mine_i);
     *pick_w = norm ? mine_w / wsum : mine_w;
     if (QW_ROUTE_PRIO > 0) __builtin_amdgcn_s_setprio(0);
 }
@@ -550,9 +568,9 @@ __device__ __forceinline__ void qw_route_wave(const float *__restrict__ l, int E
 // exponentials of its slice, and wave 0 sums and selects exactly as
 // qw_route_wave does, so the picks and weights are the same bits.  The results
 // land in wave 0's lanes (lane n < K: pick n).
-template <int PL>
+template <int PL, class OnIds = QwNoIds>
 __device__ __forceinline__ void qw_route_block(float x, int E, int K, int norm, int wave, int lane, int *pick_i,
-                                               float *pick_w, uint32_t *sx, float *vb)
+                                               float *pick_w, uint32_t *sx, float *vb, OnIds on_ids = OnIds{})
 {
     float *wm = vb + QWK_ROUTE_MAX_E;
     const int e = lane + 64 * wave;
@@ -576,6 +594,6 @@ __device__ __forceinline__ void qw_route_block(float x, int E, int K, int norm, 
         float v[PL];
 #pragma unroll
         for (int j = 0; j < PL; j++) v[j] = vb[lane + 64 * j];
-        qw_route_finish<PL>(v, E, K, norm, lane, pick_i, pick_w, sx);
+        qw_route_finish<PL>(v, E, K, norm, lane, pick_i, pick_w, sx, on_ids);
     }
 }
