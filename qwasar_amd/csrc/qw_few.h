@@ -15,7 +15,7 @@
 #define QW_DF_WAVES 8
 #define QW_DF_MAXR 8
 #define QW_DF_PAD 68
-#define QW_DF_TPG 2      // token rows a workgroup (3: the same; 4: +2 us a config-2 step)
+#define QW_DF_TPG 2      // token rows a workgroup (1 or 3: the same; 4: +2 us a config-2 step)
 // The body of one workgroup (bx, by) of k_dmat_few's grid, xl its dynamic
 // LDS.  TAGGED: the logits leave as tagged words {epoch, value} in ty (device
 // scope, past this XCD's L2) for a reader in the same launch, in place of y.
@@ -62,6 +62,46 @@ __device__ __forceinline__ void qw_few_body(float *__restrict__ y, float *__rest
         }
     }
     __syncthreads();
+    // the logits first: a reader in the same launch waits for them, and the
+    // staged rows below are read by the next launch only
+    if (has && lane < nch) {
+#pragma unroll
+        for (int r = 0; r < QW_DF_MAXR; r++) {
+            if (r < rows) {
+                const float4 *xv = reinterpret_cast<const float4 *>(xl + ((size_t)r * nch + lane) * QW_DF_PAD);
+                float p = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const uint4 ww = wv[q];
+                    const float4 a = xv[2 * q], b = xv[2 * q + 1];
+                    p = __builtin_fmaf(__uint_as_float(ww.x << 16), a.x, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.x & 0xFFFF0000u), a.y, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.y << 16), a.z, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.y & 0xFFFF0000u), a.w, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.z << 16), b.x, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.z & 0xFFFF0000u), b.y, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.w << 16), b.z, p);
+                    p = __builtin_fmaf(__uint_as_float(ww.w & 0xFFFF0000u), b.w, p);
+                }
+                part[wave][r][lane] = p;
+            }
+        }
+    }
+    // a wave's LDS accesses run in order: lane r reads what the wave wrote
+    if (has && lane < rows) {
+        float tot = part[wave][lane][0];
+        for (int c = 1; c < nch; c++) tot = tot + part[wave][lane][c];
+        if (o < n) {
+            if constexpr (TAGGED)
+                __hip_atomic_store(reinterpret_cast<unsigned long long *>(ty + (size_t)(r0 + lane) * n + o),
+                                   (unsigned long long)epoch | ((unsigned long long)__float_as_uint(tot) << 32),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else
+                y[(size_t)(r0 + lane) * n + o] = tot;
+        } else {
+            g[r0 + lane] = tot;
+        }
+    }
     if (qx && bx == 0) {
         // the group's rows also leave as q16 units (16 values, 3 uint4 each),
         // for a launch that reads them after this one
@@ -110,45 +150,6 @@ __device__ __forceinline__ void qw_few_body(float *__restrict__ y, float *__rest
             typedef _Float16 df_h8 __attribute__((ext_vector_type(8)));
             reinterpret_cast<df_h8 *>(hx + (size_t)(r0 + r) * k)[b8] =
                 df_h8{q[0], q[4], q[1], q[5], q[2], q[6], q[3], q[7]};
-        }
-    }
-    if (!has) return;
-    if (lane < nch) {
-#pragma unroll
-        for (int r = 0; r < QW_DF_MAXR; r++) {
-            if (r < rows) {
-                const float4 *xv = reinterpret_cast<const float4 *>(xl + ((size_t)r * nch + lane) * QW_DF_PAD);
-                float p = 0.0f;
-#pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    const uint4 ww = wv[q];
-                    const float4 a = xv[2 * q], b = xv[2 * q + 1];
-                    p = __builtin_fmaf(__uint_as_float(ww.x << 16), a.x, p);
-                    p = __builtin_fmaf(__uint_as_float(ww.x & 0xFFFF0000u), a.y, p);
-                    p = __builtin_fmaf(__uint_as_float(ww.y << 16), a.z, p);
-                    p = __builtin_fmaf(__uint_as_float(ww.y & 0xFFFF0000u), a.w, p);
-                    p = __builtin_fmaf(__uint_as_float(ww.z << 16), b.x, p);
-                    p = __builtin_fmaf(__uint_as_float(ww.z & 0xFFFF0000u), b.y, p);
-                    p = __builtin_fmaf(__uint_as_float(ww.w << 16), b.z, p);
-                    p = __builtin_fmaf(__uint_as_float(ww.w & 0xFFFF0000u), b.w, p);
-                }
-                part[wave][r][lane] = p;
-            }
-        }
-    }
-    // a wave's LDS accesses run in order: lane r reads what the wave wrote
-    if (lane < rows) {
-        float tot = part[wave][lane][0];
-        for (int c = 1; c < nch; c++) tot = tot + part[wave][lane][c];
-        if (o < n) {
-            if constexpr (TAGGED)
-                __hip_atomic_store(reinterpret_cast<unsigned long long *>(ty + (size_t)(r0 + lane) * n + o),
-                                   (unsigned long long)epoch | ((unsigned long long)__float_as_uint(tot) << 32),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else
-                y[(size_t)(r0 + lane) * n + o] = tot;
-        } else {
-            g[r0 + lane] = tot;
         }
     }
 }
