@@ -45,21 +45,29 @@ __global__ void k_moe_combine(float *__restrict__ out, const float *__restrict__
         // again), since a guarded load becomes a branch that waits for the
         // loads before it; the shared term is used only after
         const float4 shv = sh ? *reinterpret_cast<const float4 *>(sh + row + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        // the gate logit and the slots' weights (uniform: scalar loads) with
+        // the rows, not one wait each inside the sum
+        const float gl = sh ? g[r] : 0.0f;
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
         float4 yv[16];
+        float wv[16];
         for (int k0 = 0; k0 < K; k0 += 16) {
             const int kn = min(16, K - k0);
 #pragma unroll
+            for (int k = 0; k < 16; k++) wv[k] = w[(size_t)r * K + k0 + min(k, kn - 1)];
+#pragma unroll
             for (int k = 0; k < 16; k++)
                 yv[k] = *reinterpret_cast<const float4 *>(y + ((size_t)r * K + k0 + min(k, kn - 1)) * H + i);
+#pragma unroll
+            for (int k = 0; k < 16; k++) asm volatile("" ::"s"(wv[k]));   // (requested with the rows, not in the sum)
             if (k0 == 0 && sh) {
-                const float gs = qw_sigmoid(g[r]);
+                const float gs = qw_sigmoid(gl);
                 acc = make_float4(shv.x * gs, shv.y * gs, shv.z * gs, shv.w * gs);
             }
 #pragma unroll
             for (int k = 0; k < 16; k++)
                 if (k < kn) {
-                    const float wk = w[(size_t)r * K + k0 + k];
+                    const float wk = wv[k];
                     acc.x = __builtin_fmaf(wk, yv[k].x, acc.x);
                     acc.y = __builtin_fmaf(wk, yv[k].y, acc.y);
                     acc.z = __builtin_fmaf(wk, yv[k].z, acc.z);
