@@ -219,14 +219,9 @@ __device__ __forceinline__ void qd_glu_block(const qwk_q4 gm, const qwk_q4 um, i
 // ---- the batch's routing table -----------------------------------------------------
 
 struct QdRoute {
-    int U;
     int picks[QD_MAXU];
-    float pw[QD_MAXU];
-    int uexp[QD_MAXU];
-    int ucnt[QD_MAXU];
-    int ustart[QD_MAXU];
-    int upair[QD_MAXU];       // pairs grouped by unique expert, ascending pair index
-    int mark[QWK_ROUTE_MAX_E];// after routing: the unique-expert slot of each selected expert
+    int ustart[QD_MAXU];      // unique expert u's first slot in the pair order
+    int mark[QWK_ROUTE_MAX_E];// the unique-expert slot of each selected expert
     struct alignas(16) {
         uint32_t sx[QD_MAXT][QW_ROUTE_SX];  // selection scratch of routing wave w (w < rows <= QD_MAXT)
     } rs;
@@ -375,18 +370,24 @@ template <int PL>
 __device__ __forceinline__ void qb_route_body(const QbArgs &b, const float *logits)
 {
     __shared__ QdRoute R;
+    // per token a bitmask of its picks; per 64-expert chunk its unique
+    // experts and pairs
+    __shared__ uint32_t tmask[QD_MAXT][QWK_ROUTE_MAX_E / 32];
+    __shared__ int ctu[QWK_ROUTE_MAX_E / 64], ctp[QWK_ROUTE_MAX_E / 64];
     const QdArgs &a = b.d;
     const int t = threadIdx.x, nthr = blockDim.x, wave = t >> 6, lane = t & 63;
     const int E = a.m.E, K = a.m.K, H = a.m.H;
+    for (int i = t; i < QD_MAXT * (QWK_ROUTE_MAX_E / 32); i += nthr) (&tmask[0][0])[i] = 0u;
+    __syncthreads();
     if (wave < a.rows) {
         int pi;
         float pw;
         qw_route_wave<PL>(logits + (size_t)wave * E, E, K, a.m.norm, lane, &pi, &pw, R.rs.sx[wave]);
         if (lane < K) {
             R.picks[wave * K + lane] = pi;
-            R.pw[wave * K + lane] = pw;
             a.idx[wave * K + lane] = pi;
             a.w[wave * K + lane] = pw;
+            atomicOr(&tmask[wave][pi >> 5], 1u << (pi & 31));
         }
     }
     // the token rows as q16 units for the gate / up launch (unless the
@@ -407,84 +408,80 @@ __device__ __forceinline__ void qb_route_body(const QbArgs &b, const float *logi
     }
     __syncthreads();
     // The union of the picks, ascending, with each expert's pairs in
-    // ascending order, in parallel steps: per token a bitmask of its picks;
-    // the marked experts compacted by ballots; counts by LDS atomics; the
-    // starts by one wave's scan; a pair's place in its expert's run is the
-    // number of earlier tokens that picked the same expert (a token's picks
-    // are distinct, so pairs of one expert are ordered by token).
-    __shared__ uint32_t tmask[QD_MAXT][QWK_ROUTE_MAX_E / 32];
-    __shared__ int cnt[QWK_ROUTE_MAX_E];
-    const int npk = a.rows * K, nwd = (E + 31) / 32;
-    for (int i = t; i < QD_MAXT * (QWK_ROUTE_MAX_E / 32); i += nthr) (&tmask[0][0])[i] = 0u;
-    for (int e = t; e < E; e += nthr) { R.mark[e] = 0; cnt[e] = 0; }
-    __syncthreads();
-    for (int p = t; p < npk; p += nthr) {
-        const int e = R.picks[p];
-        R.mark[e] = 1;
-        atomicOr(&tmask[p / K][e >> 5], 1u << (e & 31));
-        atomicAdd(&cnt[e], 1);
-    }
-    __syncthreads();
-    if (wave == 0) {
-        int base = 0;
-        for (int e0 = 0; e0 < E; e0 += 64) {
-            const int e = e0 + lane;
-            const bool on = e < E && R.mark[e];
-            const unsigned long long bal = __ballot(on);
-            if (on) {
-                const int u = base + __popcll(bal & ((1ull << lane) - 1ull));
-                R.uexp[u] = e;
-                R.mark[e] = u;              // from here on: the expert's slot
-            }
-            base += __popcll(bal);
-        }
-        // starts: lane l scans slots 2l and 2l + 1 (U <= QD_MAXU <= 128)
-        const int u0 = 2 * lane, u1 = 2 * lane + 1;
-        const int c0 = u0 < base ? cnt[R.uexp[u0]] : 0, c1 = u1 < base ? cnt[R.uexp[u1]] : 0;
-        int incl = c0 + c1;
+    // ascending order: a wave a 64-expert chunk (its count of pairs from the
+    // token masks, its unique experts by ballot, the pairs' running count by
+    // an in-wave scan); the chunks' totals meet in LDS; a pair's place in its
+    // expert's run is the number of earlier tokens that picked the same
+    // expert (a token's picks are distinct, so pairs of one expert are
+    // ordered by token).
+    const int npk = a.rows * K, nchk = (E + 63) / 64;
+    constexpr int CW = QWK_ROUTE_MAX_E / 64 / QD_MAXT;       // chunks a wave
+    int cnt[CW], incl[CW];
+    unsigned long long bal[CW];
+#pragma unroll
+    for (int c = 0; c < CW; c++) {
+        const int ch = wave + QD_MAXT * c, e = 64 * ch + lane;
+        int n = 0;
+        if (ch < nchk && e < E)
+            for (int r = 0; r < a.rows; r++) n += (tmask[r][e >> 5] >> (e & 31)) & 1;
+        bal[c] = __ballot(n > 0);
+        int in = n;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o, 64);
-            if (lane >= o) incl += y;
+            const int y = __shfl_up(in, o, 64);
+            if (lane >= o) in += y;
         }
-        const int excl = incl - c0 - c1;
-        if (u0 < base) { R.ucnt[u0] = c0; R.ustart[u0] = excl; }
-        if (u1 < base) { R.ucnt[u1] = c1; R.ustart[u1] = excl + c0; }
-        if (lane == 0) R.U = base;
+        cnt[c] = n;
+        incl[c] = in;
+        if (ch < nchk && lane == 63) {
+            ctu[ch] = __popcll(bal[c]);
+            ctp[ch] = in;
+        }
     }
+    __syncthreads();
+    int U = 0;
+    for (int ch = 0; ch < nchk; ch++) U += ctu[ch];
+    const unsigned long long below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int c = 0; c < CW; c++) {
+        const int ch = wave + QD_MAXT * c, e = 64 * ch + lane;
+        if (ch >= nchk || cnt[c] == 0) continue;
+        int ub = 0, pb = 0;
+        for (int q = 0; q < ch; q++) { ub += ctu[q]; pb += ctp[q]; }
+        const int u = ub + (int)__popcll(bal[c] & below), st = pb + incl[c] - cnt[c];
+        R.mark[e] = u;
+        R.ustart[u] = st;
+        b.tab[QB_TAB_UEXP + u] = e;
+        b.tab[QB_TAB_UCNT + u] = cnt[c];
+        b.tab[QB_TAB_USTART + u] = st;
+        if (b.gmm) {
+            // the grouped product's tile list: unique expert u's pairs
+            b.tiles[1 + 3 * u] = e;
+            b.tiles[2 + 3 * u] = st;
+            b.tiles[3 + 3 * u] = cnt[c];
+        }
+    }
+    if (t == 0) {
+        b.tab[QB_TAB_U] = U;
+        if (b.gmm) {
+            // then the shared expert (expert E) on the token rows, pairs npk + r
+            b.tiles[0] = U + 1;
+            b.tiles[1 + 3 * U] = E;
+            b.tiles[2 + 3 * U] = npk;
+            b.tiles[3 + 3 * U] = a.rows;
+        }
+    }
+    if (b.gmm)
+        for (int r = t; r < a.rows; r += nthr) b.perm[npk + r] = npk + r;
     __syncthreads();
     for (int p = t; p < npk; p += nthr) {
         const int e = R.picks[p], tk = p / K;
         int rank = 0;
         for (int q = 0; q < tk; q++) rank += (tmask[q][e >> 5] >> (e & 31)) & 1u;
-        R.upair[R.ustart[R.mark[e]] + rank] = p;
+        const int dst = R.ustart[R.mark[e]] + rank;
+        b.tab[QB_TAB_UPAIR + dst] = p;
+        if (b.gmm) b.perm[dst] = p;
     }
-    __syncthreads();
-    if (t == 0) b.tab[QB_TAB_U] = R.U;
-    for (int u = t; u < R.U; u += nthr) {
-        b.tab[QB_TAB_UEXP + u] = R.uexp[u];
-        b.tab[QB_TAB_UCNT + u] = R.ucnt[u];
-        b.tab[QB_TAB_USTART + u] = R.ustart[u];
-    }
-    for (int p = t; p < npk; p += nthr) b.tab[QB_TAB_UPAIR + p] = R.upair[p];
-    if (b.gmm) {
-        // the grouped product's tile list: unique expert u's pairs, then the
-        // shared expert (expert E) on the token rows, pairs npk + r
-        if (t == 0) {
-            b.tiles[0] = R.U + 1;
-            b.tiles[1 + 3 * R.U] = E;
-            b.tiles[2 + 3 * R.U] = npk;
-            b.tiles[3 + 3 * R.U] = a.rows;
-        }
-        for (int u = t; u < R.U; u += nthr) {
-            b.tiles[1 + 3 * u] = R.uexp[u];
-            b.tiles[2 + 3 * u] = R.ustart[u];
-            b.tiles[3 + 3 * u] = R.ucnt[u];
-        }
-        for (int p = t; p < npk; p += nthr) b.perm[p] = R.upair[p];
-        for (int r = t; r < a.rows; r += nthr) b.perm[npk + r] = npk + r;
-    }
-    (void)nwd;
 }
 
 template <int PL>
