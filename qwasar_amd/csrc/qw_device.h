@@ -405,8 +405,10 @@ __device__ __forceinline__ void qw_route_finish(float (&v)[PL], int E, int K, in
         }
         const int tau = (int)pref;
         QW_RSTAMP(5);
-        // survivors to keys[0 .. C) in slot order (a position past 63 goes
-        // to the sink keys[64]; C > 64 takes the tournament below)
+        // survivors to keys[0 .. C) in slot order, stored by the surviving
+        // lanes only (a position past 63 goes to the sink keys[64]; C > 64
+        // takes the tournament below).  Every lane storing, the others into
+        // the sink, made each slot's store one address for most of the wave.
         uint64_t *keys = reinterpret_cast<uint64_t *>(sx);  // [66]: 64 is a sink
         uint64_t *picks = keys + 66;                         // [QWK_ROUTE_MAX_K]
         const unsigned long long below = (1ull << lane) - 1ull;
@@ -415,8 +417,9 @@ __device__ __forceinline__ void qw_route_finish(float (&v)[PL], int E, int K, in
         for (int j = 0; j < PL; j++) {
             const bool on = lane + 64 * j < E && pb[j] >= tau;
             const unsigned long long sm = __ballot(on);
-            const int pos = on ? min(C + (int)__popcll(sm & below), 64) : 64;
-            keys[pos] = ((uint64_t)(uint32_t)pb[j] << 32) | (uint32_t)(0xFFFF - (lane + 64 * j));
+            if (on)
+                keys[min(C + (int)__popcll(sm & below), 64)] =
+                    ((uint64_t)(uint32_t)pb[j] << 32) | (uint32_t)(0xFFFF - (lane + 64 * j));
             C += __popcll(sm);
         }
         if (C <= 64) {
