@@ -116,12 +116,15 @@ extern "C" int qwk_decode_trace_read(unsigned long long *dst, size_t n)
 #define QX_SPIN_LIMIT (1 << 16)
 // sleep between polls, in s_sleep units of 64 clocks: the far polls (device
 // scope) share the memory side with the weight stream, the near ones (L2) not
+// (near polls with no sleep, and the partial sums' far polls too, measured
+// 0.25 us a token faster than 1 and 2: 20.27 -> 20.02 over six alternating
+// runs; a sleep of 6 for the partials' polls measured slower)
 #define QX_SLEEP_FAR 8
-#define QX_SLEEP_NEAR 1
+#define QX_SLEEP_NEAR 0
 // (the picks come a routing's time after the workers start: they poll slower)
 #define QX_SLEEP_PICKS 2
 // (the XCD that sums the partials polls last, with the weight stream over)
-#define QX_SLEEP_PART 2
+#define QX_SLEEP_PART 0
 
 static_assert(QX_PICK_WORDS >= 2 * QWK_DECODE_MAX_K + 1, "picks record");
 static_assert(QX_PL * 64 >= 512, "routing lanes");
